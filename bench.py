@@ -1,0 +1,296 @@
+#!/usr/bin/env python3
+"""MatMulNBits INT4 on one MI355X: decode GEMV HBM GB/s at 7B shapes, prefill TFLOP/s.
+
+A step is one pass of a 7B-class decoder layer's INT4 projections at M=1
+(q, k, v, o, gate, up, down; hidden 3584, intermediate 18944, 28 query / 4 KV
+heads of dim 128; block size 32 with packed zero points). Weights, activations
+and outputs are resident in HBM before timing starts. Every step uses a
+different copy of the layer's weights, activations and outputs, rotating over
+enough copies to touch >= 1 GiB, so no op is served from the 256 MiB MALL.
+The steps are enqueued as a HIP graph (captured through torch's stream
+capture) and timed with HIP events on that stream.
+
+Prints one JSON line. value = algorithmic bytes per step / time per step
+(weights + fp32 A + fp32 Y, each once). Beside it:
+  roofline      the gate/up GEMV launch (K=3584, N=18944): bytes per launch /
+                mean launch time, against 8 TB/s;
+  prefill       M=2048 on the Llama-2-7B MLP shapes (the MFMA kernel), TFLOP/s
+                against the 2.5 PFLOP/s dense fp16 peak;
+  cpu_baseline  the CPU oracle (a C restatement of the reference's managed
+                MatMulNBitsKernel) on the host cores, gate projection sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "MatMulNBits INT4 M=1 GEMV HBM GB/s at 7B shapes; M=2048 prefill TFLOP/s"
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Rotation:
+    """R device-resident copies of a set of ops: weights handles, A and Y."""
+
+    def __init__(self, ops, M, copies, seed, kind="normal"):
+        import torch
+        from modelsharp_amd import native, workloads
+        self.ops, self.M, self.copies = ops, M, copies
+        host = [workloads.make_weights(op, seed + i) for i, op in enumerate(ops)]
+        self.handles = [[native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
+                         for (b, s, z), op in zip(host, ops)] for _ in range(copies)]
+        self.A = [[torch.from_numpy(workloads.make_activations(M, op.K, seed + 100 * r + i, kind)).cuda()
+                   for i, op in enumerate(ops)] for r in range(copies)]
+        self.Y = [[torch.empty((M, op.N), dtype=torch.float32, device="cuda") for op in ops] for _ in range(copies)]
+        self.host = host
+
+    def enqueue(self, r, stream, only=None):
+        from modelsharp_amd import native
+        idx = range(len(self.ops)) if only is None else [only]
+        native.gemm_dev_batch([self.handles[r][i] for i in idx], [self.A[r][i].data_ptr() for i in idx],
+                              [self.Y[r][i].data_ptr() for i in idx], self.M, stream)
+
+    def close(self):
+        for row in self.handles:
+            for h in row:
+                h.close()
+
+
+def graph_of(fn):
+    """Captures fn(stream_handle) into a torch CUDA (HIP) graph."""
+    import torch
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn(side.cuda_stream)   # warm: first launches outside capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        fn(torch.cuda.current_stream().cuda_stream)
+    return g
+
+
+def time_graph(g, replays, warmup):
+    """Mean ms per replay, HIP events on the stream the graph is launched on."""
+    import torch
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        g.replay()
+    end.record()
+    end.synchronize()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / replays
+
+
+def cpu_baseline(op, budget_s):
+    import oracle
+    from modelsharp_amd import workloads
+    b, s, z = workloads.make_weights(op, 1234)
+    a = workloads.make_activations(1, op.K, 1235)
+    nthreads = oracle.threads()
+    oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, op.block_size, nthreads=nthreads)   # warm
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, op.block_size, nthreads=nthreads)
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    nbytes = workloads.algorithmic_bytes(op, 1)
+    out = {"value": round(nbytes * calls / el / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
+           "sample": f"{op.name} K={op.K} N={op.N} M=1 bs={op.block_size} zp, {calls} calls in {el:.1f} s "
+                     f"({el / calls * 1e3:.2f} ms/call), C restatement of the managed MatMulNBitsKernel "
+                     f"(column-parallel, {nthreads} threads)"}
+    ref = oracle.ref_lib()
+    if ref is not None:   # the reference's own native ms_qgemm_nbits, when it was built
+        oracle.ref_qgemm_nbits(a, b, s, z, 1, op.N, op.K, 4, op.block_size)
+        calls, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget_s / 2:
+            oracle.ref_qgemm_nbits(a, b, s, z, 1, op.N, op.K, 4, op.block_size)
+            calls += 1
+        el = time.perf_counter() - t0
+        out["reference_native_gbs"] = round(nbytes * calls / el / 1e9, 3)
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200, help="timed decode-layer steps")
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--rotate-mib", type=int, default=1024, help="bytes the weight rotation touches")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget (0 = skip)")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--detail", default="", help="also write per-op results of every workload to this JSON file")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this MatMulNBits build measures one GPU; the op shards by columns or by "
+                                   "K-blocks across GPUs (see the design notes), but no multi-GPU figure is "
+                                   "produced", "n_gpus": args.gpus}), flush=True)
+        return 2
+
+    import torch
+    from modelsharp_amd import native, workloads
+    if not (ROOT / "modelsharp_amd" / "lib" / native.LIB_NAME).is_file():
+        import __graft_entry__
+        __graft_entry__.build()
+    if not native.available():
+        raise SystemExit("no gfx950 device: " + native.last_error())
+    torch.cuda.set_device(0)
+    log(f"device: {native.device_name()}")
+
+    # ---- 7B decode layer, M=1 -------------------------------------------------------------
+    ops = workloads.DECODE_7B
+    step_bytes = sum(workloads.algorithmic_bytes(op, 1) for op in ops)
+    copies = workloads.rotation_copies(step_bytes, args.rotate_mib << 20)
+    log(f"7b decode layer: {step_bytes / 1e6:.2f} MB/step, {copies} rotating copies")
+    rot = Rotation(ops, 1, copies, seed=7)
+
+    def layer_rotation(stream):
+        for r in range(copies):
+            rot.enqueue(r, stream)
+
+    g = graph_of(layer_rotation)
+    replays = max(1, math.ceil(args.steps / copies))
+    warm = max(1, math.ceil(args.warmup / copies))
+    ms_rot = time_graph(g, replays, warm)
+    steps = replays * copies
+    ms_step = ms_rot / copies
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    log(f"graph: {ms_step * 1e3:.2f} us/step  {value:.1f} GB/s")
+
+    # eager launches (no graph) for comparison
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream().cuda_stream
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for r in range(copies):
+        rot.enqueue(r, s)
+    e0.record()
+    for i in range(steps):
+        rot.enqueue(i % copies, s)
+    e1.record()
+    e1.synchronize()
+    ms_step_eager = e0.elapsed_time(e1) / steps
+
+    # per-op launch times (graph of one op over all copies)
+    per_op = {}
+    for i, op in enumerate(ops):
+        gi = graph_of(lambda stream, i=i: [rot.enqueue(r, stream, only=i) for r in range(copies)])
+        ms = time_graph(gi, max(4, 2 * replays), 2) / copies
+        nbytes = workloads.algorithmic_bytes(op, 1)
+        per_op[op.name] = {"K": op.K, "N": op.N, "us": round(ms * 1e3, 3),
+                           "GBs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                           "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                           "kernel": rot.handles[0][i].launch_info(1)}
+        log(f"  {op.name:5s} K={op.K:6d} N={op.N:6d}: {ms * 1e3:7.2f} us  {per_op[op.name]['GBs']:7.1f} GB/s")
+    gate = next(op for op in ops if op.name == "gate")
+    gate_bytes = workloads.algorithmic_bytes(gate, 1)
+    gate_gbs = per_op["gate"]["GBs"]
+    rot.close()
+    del rot, g
+    torch.cuda.empty_cache()
+
+    result = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps,
+        "warmup": warm * copies, "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "7b_decode_layer", "ops": {op.name: [op.K, op.N] for op in ops}, "M": 1,
+                   "bits": 4, "block_size": 32, "zero_points": "packed uint4", "rotating_copies": copies,
+                   "bytes_per_step": step_bytes, "timing": "HIP graph of the rotation, HIP events"},
+        "ms_per_step_eager": round(ms_step_eager, 5),
+        "per_op": per_op,
+        "roofline": {"bound": "hbm", "kernel": "gemv_w4 gate/up (K=3584, N=18944, M=1)",
+                     "achieved": gate_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gate_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": gate_bytes},
+    }
+
+    # ---- prefill, M=2048 ----------------------------------------------------------------
+    if not args.no_prefill:
+        pre = {}
+        total_flops, total_ms = 0, 0.0
+        for op in workloads.LLAMA7B_PREFILL_OPS:
+            M = 2048
+            prot = Rotation([op], M, 2, seed=11, kind="rmsnorm")
+            gp = graph_of(lambda stream: [prot.enqueue(r, stream) for r in range(2)])
+            ms = time_graph(gp, 10, 2) / 2
+            fl = workloads.flops(op, M)
+            pre[f"K{op.K}_N{op.N}"] = {"us": round(ms * 1e3, 2), "TFLOPs": round(fl / (ms * 1e-3) / 1e12, 1),
+                                       "frac_fp16_peak": round(fl / (ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4)}
+            log(f"  prefill M={M} K={op.K} N={op.N}: {ms * 1e3:.1f} us  {pre[f'K{op.K}_N{op.N}']['TFLOPs']} TFLOP/s")
+            total_flops += fl
+            total_ms += ms
+            prot.close()
+            del prot, gp
+            torch.cuda.empty_cache()
+        tf = total_flops / (total_ms * 1e-3) / 1e12
+        result["prefill"] = {"workload": "llama7b_prefill M=2048, (K,N)=(4096,11008),(11008,4096), bs=32, zp",
+                             "per_op": pre, "TFLOPs": round(tf, 1), "peak_TFLOPs": FP16_PEAK_TFLOPS,
+                             "frac": round(tf / FP16_PEAK_TFLOPS, 4), "bound": "mfma"}
+
+    if args.detail:
+        result_detail = detail_workloads(args)
+        pathlib.Path(args.detail).write_text(json.dumps(result_detail, indent=1))
+
+    if args.cpu_seconds > 0:
+        log("cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline(gate, args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def detail_workloads(args):
+    """Per-op results for the other workloads (parity-test sizes; not the bench line)."""
+    import torch
+    from modelsharp_amd import workloads
+    out = {}
+    groups = [("qwen05b_up", [workloads.QWEN05B_UP], [1]),
+              ("qwen05b_decode", workloads.QWEN05B_DECODE, [1]),
+              ("llama7b_smallm", workloads.LLAMA7B_SMALLM_OPS, workloads.LLAMA7B_SMALLM_M),
+              ("llama7b_prefill", workloads.LLAMA7B_PREFILL_OPS, workloads.LLAMA7B_PREFILL_M)]
+    for name, ops, Ms in groups:
+        for M in Ms:
+            for op in ops:
+                fp = workloads.algorithmic_bytes(op, M)
+                copies = min(workloads.rotation_copies(fp, args.rotate_mib << 20), 64)
+                if M >= 128:
+                    copies = 2
+                rot = Rotation([op], M, copies, seed=3, kind="rmsnorm" if M >= 128 else "normal")
+                g = graph_of(lambda stream: [rot.enqueue(r, stream) for r in range(copies)])
+                ms = time_graph(g, 10 if M >= 128 else 50, 2) / copies
+                out[f"{name}/{op.name}/M{M}"] = {
+                    "K": op.K, "N": op.N, "M": M, "us": round(ms * 1e3, 3),
+                    "GBs": round(fp / (ms * 1e-3) / 1e9, 1),
+                    "TFLOPs": round(workloads.flops(op, M) / (ms * 1e-3) / 1e12, 2),
+                    "kernel": rot.handles[0][0].launch_info(M)}
+                log(f"  {name}/{op.name}/M{M}: {out[f'{name}/{op.name}/M{M}']}")
+                rot.close()
+                del rot, g
+                torch.cuda.empty_cache()
+    return out
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,130 @@
+/*
+ * ms_hip_kernels.h — C ABI of the MI355X (gfx950) MatMulNBits library,
+ * libms_hip_nbits.so.
+ *
+ * The operator: Y[M,N] = A[M,K] * dequant(B)^T with
+ *   B       uint8 [N, ceil(K/block_size), block_size*bits/8], codes packed
+ *           least-significant first (bits=4: even k in the low nibble);
+ *   scales  fp32 [N * ceil(K/block_size)], scales[n*nb + b];
+ *   zp      optional uint8 packed like B, row stride ceil(nb*bits/8) bytes,
+ *           or NULL for the symmetric default 2^(bits-1);
+ *   W[n,k]  = ((float)q - zp) * scale (one fp32 rounding).
+ * Semantics follow src/ModelSharp/Cpu/Kernels/Quantize/MatMulNBitsKernel.cs
+ * (paths relative to the ModelSharp checkout).
+ *
+ * Conventions (those of native/ms_kernels.h:7-13, plus a status code):
+ *   - fp32 buffers are IEEE binary32, row-major, contiguous;
+ *   - pointers are caller-owned; outputs are fully overwritten;
+ *   - every entry returns int status, MS_HIP_OK (0) on success; on failure
+ *     ms_hip_last_error() (thread-local) holds the message and outputs are
+ *     untouched;
+ *   - add functions rather than change signatures.
+ * Threading: every entry may be called from any host thread. A weights handle
+ * is immutable after creation; the synchronous host-pointer entries serialise
+ * per handle. Device-pointer entries enqueue on the caller's stream.
+ */
+#ifndef MS_HIP_KERNELS_H
+#define MS_HIP_KERNELS_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MS_HIP_OK               0
+#define MS_HIP_ERR_INVALID      1  /* argument / layout validation failed    */
+#define MS_HIP_ERR_NO_DEVICE    2  /* no usable gfx950 device                */
+#define MS_HIP_ERR_HIP          3  /* a HIP runtime call failed              */
+#define MS_HIP_ERR_UNSUPPORTED  4  /* valid operator input this ABI cannot take */
+
+/* ---- capability / diagnostics ---------------------------------------------
+ * Replace ms_build_info / ms_has_avx512 / ms_has_vnni
+ * (native/ms_kernels.h:23-25, native/src/info.cpp:10-26) for the GPU library:
+ * the C# guard probes these before routing (NativeQuant.cs:41-56). */
+int         ms_hip_available(void);     /* 1 if a gfx950 device is usable, else 0 */
+const char* ms_hip_device_name(void);   /* "" when unavailable                    */
+const char* ms_hip_build_info(void);
+const char* ms_hip_last_error(void);    /* thread-local, "" when none              */
+
+/* ---- validation ------------------------------------------------------------
+ * The operator's input rules, MatMulNBitsKernel.cs:87-145 and :158-161, with
+ * the reference's exception messages (returned through ms_hip_last_error).
+ * zp_kind: 0 absent, 1 uint8 packed, 2 float32, 3 any other dtype.
+ * a_last_dim: A's innermost dimension, or -1 to skip that check. */
+int ms_hip_nbits_check(int N, int K, int bits, int block_size,
+                       int64_t b_len, int64_t scales_len,
+                       int zp_kind, int64_t zp_len, int64_t a_last_dim);
+
+/* ---- load-time weight upload (once per initializer) ------------------------
+ * Replaces the per-run widening + upload of IlgpuEngine.RunMatMulNBits
+ * (src/ModelSharp.Gpu/IlgpuEngine.cs:2222-2229, ResidentOrTempInt/Float
+ * :3392-3429): B, scales and packed zero points are copied once into HBM.
+ * Lengths are element counts of the host arrays and are validated as
+ * MatMulNBitsKernel.cs:100-139 does. zp may be NULL (zp_len ignored). */
+int ms_hip_nbits_weights_create(const uint8_t* bq, int64_t bq_len,
+                                const float* scales, int64_t scales_len,
+                                const uint8_t* zero_points, int64_t zp_len,
+                                int N, int K, int bits, int block_size,
+                                void** out_handle);
+/* Same, from buffers already resident on the device (copied device-to-device). */
+int ms_hip_nbits_weights_create_dev(const uint8_t* d_bq, const float* d_scales,
+                                    const uint8_t* d_zero_points,
+                                    int N, int K, int bits, int block_size,
+                                    void** out_handle);
+/* Frees the device copy (IlgpuEngine.Dispose, IlgpuEngine.cs:3926-3942). */
+int ms_hip_nbits_weights_destroy(void* handle);
+/* N, K, bits, block_size and has-zero-points of a handle (any pointer may be NULL). */
+int ms_hip_nbits_weights_info(void* handle, int* N, int* K, int* bits, int* block_size,
+                              int* has_zp);
+
+/* ---- the operator ----------------------------------------------------------
+ * Host-pointer drop-in: y[M,N] = a[M,K] * dequant(B)^T, synchronous.
+ * Replaces ms_qgemm_nbits (native/ms_kernels.h:42-44, qgemm.cpp:77-118) on the
+ * path NativeQuant.TryMatMulNBits (NativeQuant.cs:78-115) takes from
+ * MatMulNBitsKernel.Execute (MatMulNBitsKernel.cs:174-191), with the weights
+ * already resident. M<=16 runs the dequant-fused GEMV, larger M the MFMA GEMM. */
+int ms_hip_nbits_gemm(void* handle, const float* a_host, float* y_host, int M);
+
+/* Device-pointer form: enqueues on `stream` (a hipStream_t, NULL = the null
+ * stream) and returns without synchronising. dA: [M,K] fp32, dY: [M,N] fp32,
+ * both 16-byte aligned device memory. */
+int ms_hip_nbits_gemm_dev(void* handle, const float* dA, float* dY, int M, void* stream);
+
+/* Enqueues `count` device-pointer calls back to back on `stream`, call i on
+ * handles[i] with dA[i], dY[i] (all with the same M). For callers that chain
+ * several projections without a host round trip per call. */
+int ms_hip_nbits_gemm_dev_batch(void* const* handles, const float* const* dA,
+                                float* const* dY, int count, int M, void* stream);
+
+/* One-shot form with the exact signature semantics of ms_qgemm_nbits
+ * (native/ms_kernels.h:42-44): uploads, computes, downloads, frees. */
+int ms_hip_qgemm_nbits(const float* a, const uint8_t* bq, const float* scales,
+                       const uint8_t* zero_points, float* y,
+                       int M, int N, int K, int bits, int block_size);
+
+/* ---- dequantized weights ---------------------------------------------------
+ * W[N,K] fp32 as the device stores it, W[n,k] = ((float)q - zp) * scale
+ * (MatMulNBitsSimd.cs:40-111); for the bit-exact dequant check. */
+int ms_hip_nbits_dequant(void* handle, float* w_host);
+int ms_hip_nbits_dequant_dev(void* handle, float* dW, void* stream);
+
+/* ---- device memory helpers (NativeCuda.Alloc/Upload/Download/Free,
+ * src/ModelSharp.Gpu/NativeCuda.cs:92-128) ---------------------------------- */
+int ms_hip_alloc(void** dptr, int64_t bytes);
+int ms_hip_free(void* dptr);
+int ms_hip_upload(void* dptr, const void* host, int64_t bytes);
+int ms_hip_download(void* host, const void* dptr, int64_t bytes);
+int ms_hip_sync(void);
+
+/* ---- measurement support ---------------------------------------------------
+ * No counterpart in the reference. Fixes the GEMV's lanes-per-row split
+ * (4, 8, 16, 32 or 64; 0 restores the shape heuristic) for launch-shape
+ * sweeps, and reports the split and grid the heuristic picks. */
+int ms_hip_set_gemv_lanes(int lanes_per_row);
+int ms_hip_nbits_launch_info(void* handle, int M, int* kernel_id, int* lanes_per_row,
+                             int* grid, int* block);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,649 @@
+// ms_hip_nbits.hip — host runtime and C ABI of libms_hip_nbits.so (gfx950).
+//
+// Weights handles hold B, scales and packed zero points resident in HBM in the
+// operator's own layout (uploaded once per initializer); each call dispatches
+//   M <= 16, bits=4, block_size in {32,64,128,256}, K % 32 == 0 -> gemv_w4
+//   M >  16, same conditions                                   -> mfma_w4
+//   anything else                                              -> generic
+// Declarations and reference citations: include/ms_hip_kernels.h.
+#include "../../include/ms_hip_kernels.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "gemv_w4.h"
+#include "generic_nbits.h"
+#include "mfma_w4.h"
+
+using namespace msnb;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char* fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return status;
+}
+
+#define MS_HIP_CHECK(expr)                                                                  \
+    do {                                                                                    \
+        hipError_t e_ = (expr);                                                             \
+        if (e_ != hipSuccess)                                                               \
+            return fail(MS_HIP_ERR_HIP, "[ms_hip] %s failed: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+// ---- device probe ---------------------------------------------------------------------
+struct DeviceInfo {
+    int ok = 0;
+    int device = -1;
+    std::string name;
+};
+
+const DeviceInfo& device_info()
+{
+    static DeviceInfo info = [] {
+        DeviceInfo d;
+        int count = 0;
+        if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+            (void)hipGetLastError();
+            return d;
+        }
+        hipDeviceProp_t prop;
+        for (int i = 0; i < count; ++i) {
+            if (hipGetDeviceProperties(&prop, i) != hipSuccess) continue;
+            if (std::strncmp(prop.gcnArchName, "gfx950", 6) == 0) {
+                d.ok = 1;
+                d.device = i;
+                d.name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+                break;
+            }
+        }
+        (void)hipGetLastError();
+        return d;
+    }();
+    return info;
+}
+
+int require_device()
+{
+    const DeviceInfo& d = device_info();
+    if (!d.ok) return fail(MS_HIP_ERR_NO_DEVICE, "[ms_hip] no gfx950 device is available");
+    return MS_HIP_OK;
+}
+
+// ---- weights handle --------------------------------------------------------------------
+struct Weights {
+    int N = 0, K = 0, bits = 0, bs = 0, nb = 0, blob = 0, zrb = 0;
+    int has_zp = 0;
+    int64_t row_bytes = 0;
+    int fast = 0;       // gemv_w4 / mfma_w4 eligible
+    int log2cpb = 0;    // log2(bs / 32) when fast
+    int device = 0;
+    uint8_t* d_b = nullptr;
+    float* d_scales = nullptr;
+    uint8_t* d_zp = nullptr;
+    // synchronous host-pointer path: staging buffers + stream, guarded by mu
+    std::mutex mu;
+    hipStream_t stream = nullptr;
+    float* d_stage = nullptr;
+    size_t stage_bytes = 0;
+};
+
+constexpr uint32_t kHandleMagic = 0x4D534E42u;   // "MSNB"
+struct HandleBox {
+    uint32_t magic = kHandleMagic;
+    Weights w;
+};
+
+Weights* from_handle(void* h)
+{
+    HandleBox* box = static_cast<HandleBox*>(h);
+    if (!box || box->magic != kHandleMagic) return nullptr;
+    return &box->w;
+}
+
+void derive_layout(Weights& w, int N, int K, int bits, int bs)
+{
+    w.N = N;
+    w.K = K;
+    w.bits = bits;
+    w.bs = bs;
+    w.nb = (K + bs - 1) / bs;
+    w.blob = (bs * bits + 7) / 8;
+    w.zrb = (w.nb * bits + 7) / 8;
+    w.row_bytes = (int64_t)w.nb * w.blob;
+    w.fast = 0;
+    if (bits == 4 && (K % 32) == 0 && (bs == 32 || bs == 64 || bs == 128 || bs == 256)) {
+        w.fast = 1;
+        w.log2cpb = bs == 32 ? 0 : bs == 64 ? 1 : bs == 128 ? 2 : 3;
+    }
+}
+
+RawLayout raw_layout(const Weights& w)
+{
+    RawLayout L;
+    L.b = w.d_b;
+    L.scales = w.d_scales;
+    L.zp = w.has_zp ? w.d_zp : nullptr;
+    L.N = w.N;
+    L.K = w.K;
+    L.bits = w.bits;
+    L.bs = w.bs;
+    L.nb = w.nb;
+    L.blob = w.blob;
+    L.zrb = w.zrb;
+    return L;
+}
+
+void free_weights(Weights& w)
+{
+    if (w.d_b) (void)hipFree(w.d_b);
+    if (w.d_scales) (void)hipFree(w.d_scales);
+    if (w.d_zp) (void)hipFree(w.d_zp);
+    if (w.d_stage) (void)hipFree(w.d_stage);
+    if (w.stream) (void)hipStreamDestroy(w.stream);
+    w.d_b = nullptr;
+    w.d_scales = nullptr;
+    w.d_zp = nullptr;
+    w.d_stage = nullptr;
+    w.stream = nullptr;
+}
+
+// ---- GEMV launch shape --------------------------------------------------------------------
+int g_gemv_lanes_override = 0;
+
+constexpr int kLaneChoices[5] = {4, 8, 16, 32, 64};
+
+// Lanes per row G: enough waves to cover the chip (~2048 waves = 8 per CU) while
+// wasting as few lane-steps as possible on the row's chunk count C; among equal
+// choices prefer G >= 8 (whole 128-byte lines per row per load).
+int pick_gemv_lanes(int N, int C)
+{
+    if (g_gemv_lanes_override) return g_gemv_lanes_override;
+    double best = -1.0;
+    int best_g = 8;
+    for (int G : kLaneChoices) {
+        const int R = kWave / G;
+        const double waves = (double)((N + R - 1) / R);
+        const int steps = (C + G - 1) / G;
+        const double eff = (double)C / (double)(steps * G);
+        const double fill = std::min(1.0, waves / 2048.0);
+        double score = eff * fill;
+        if (G < 8) score *= 0.97;
+        if (score > best + 1e-9) {
+            best = score;
+            best_g = G;
+        }
+    }
+    return best_g;
+}
+
+typedef void (*GemvFn)(GemvParams);
+
+template <int M>
+GemvFn gemv_for_lanes(int G)
+{
+    switch (G) {
+        case 4: return gemv_w4_kernel<M, 4>;
+        case 8: return gemv_w4_kernel<M, 8>;
+        case 16: return gemv_w4_kernel<M, 16>;
+        case 32: return gemv_w4_kernel<M, 32>;
+        default: return gemv_w4_kernel<M, 64>;
+    }
+}
+
+GemvFn gemv_kernel(int M, int G)
+{
+    switch (M) {
+        case 1: return gemv_for_lanes<1>(G);
+        case 2: return gemv_for_lanes<2>(G);
+        case 3: return gemv_for_lanes<3>(G);
+        case 4: return gemv_for_lanes<4>(G);
+        case 5: return gemv_for_lanes<5>(G);
+        case 6: return gemv_for_lanes<6>(G);
+        case 7: return gemv_for_lanes<7>(G);
+        case 8: return gemv_for_lanes<8>(G);
+        case 9: return gemv_for_lanes<9>(G);
+        case 10: return gemv_for_lanes<10>(G);
+        case 11: return gemv_for_lanes<11>(G);
+        case 12: return gemv_for_lanes<12>(G);
+        case 13: return gemv_for_lanes<13>(G);
+        case 14: return gemv_for_lanes<14>(G);
+        case 15: return gemv_for_lanes<15>(G);
+        default: return gemv_for_lanes<16>(G);
+    }
+}
+
+constexpr int kGemvMaxM = 16;
+
+struct GemvShape {
+    int G, grid, panel_chunks;
+    size_t lds_bytes;
+};
+
+GemvShape gemv_shape(const Weights& w, int M)
+{
+    GemvShape s;
+    const int C = w.K / 32;
+    s.G = pick_gemv_lanes(w.N, C);
+    const int rows_per_wg = (kGemvThreads / kWave) * (kWave / s.G);
+    s.grid = (w.N + rows_per_wg - 1) / rows_per_wg;
+    // LDS panel: <= 40 KiB for M <= 4 (4 workgroups per CU), <= 64 KiB beyond.
+    const size_t budget = M <= 4 ? 40 * 1024 : 64 * 1024;
+    const int bytes_per_chunk = M * kChunkStride4 * 16;
+    int pmax = (int)(budget / bytes_per_chunk);
+    if (pmax < 1) pmax = 1;
+    const int npanels = (C + pmax - 1) / pmax;
+    int P = (C + npanels - 1) / npanels;
+    if (P % s.G) {
+        const int up = ((P + s.G - 1) / s.G) * s.G;
+        if (up <= pmax) P = up;
+    }
+    s.panel_chunks = P;
+    s.lds_bytes = (size_t)M * P * kChunkStride4 * 16;
+    return s;
+}
+
+int launch_gemv(const Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
+{
+    const GemvShape s = gemv_shape(w, M);
+    GemvParams p;
+    p.b = w.d_b;
+    p.scales = w.d_scales;
+    p.zp = w.has_zp ? w.d_zp : nullptr;
+    p.a = dA;
+    p.y = dY;
+    p.row_bytes = w.row_bytes;
+    p.N = w.N;
+    p.K = w.K;
+    p.C = w.K / 32;
+    p.log2cpb = w.log2cpb;
+    p.nb = w.nb;
+    p.zrb = w.zrb;
+    p.panel_chunks = s.panel_chunks;
+    hipLaunchKernelGGL(gemv_kernel(M, s.G), dim3(s.grid), dim3(kGemvThreads), s.lds_bytes, stream, p);
+    MS_HIP_CHECK(hipGetLastError());
+    return MS_HIP_OK;
+}
+
+int launch_generic(const Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
+{
+    const int64_t total = (int64_t)M * w.N;
+    const int64_t grid = (total + 255) / 256;
+    hipLaunchKernelGGL(nbits_generic_kernel, dim3((unsigned)grid), dim3(256), 0, stream, raw_layout(w), dA,
+                       dY, M);
+    MS_HIP_CHECK(hipGetLastError());
+    return MS_HIP_OK;
+}
+
+int enqueue_gemm(const Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
+{
+    if (M < 0) return fail(MS_HIP_ERR_INVALID, "MatMulNBits M must be non-negative; got %d.", M);
+    if (M == 0) return MS_HIP_OK;
+    if (!dA || !dY) return fail(MS_HIP_ERR_INVALID, "[ms_hip] null activation or output pointer");
+    if ((reinterpret_cast<uintptr_t>(dA) & 15) || (reinterpret_cast<uintptr_t>(dY) & 3))
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] A must be 16-byte and Y 4-byte aligned");
+    if (!w.fast) return launch_generic(w, dA, dY, M, stream);
+    if (M <= kGemvMaxM) return launch_gemv(w, dA, dY, M, stream);
+    return launch_mfma(w.d_b, w.d_scales, w.has_zp ? w.d_zp : nullptr, w.row_bytes, w.N, w.K, w.nb,
+                       w.zrb, w.log2cpb, dA, dY, M, stream)
+               ? fail(MS_HIP_ERR_HIP, "[ms_hip] MFMA launch failed: %s", hipGetErrorString(hipGetLastError()))
+               : MS_HIP_OK;
+}
+
+int check_impl(int N, int K, int bits, int bs, int64_t b_len, int64_t scales_len, int zp_kind, int64_t zp_len,
+               int64_t a_last_dim)
+{
+    // Messages of MatMulNBitsKernel.cs:87-161 (U+00D7 in UTF-8).
+    if (N <= 0 || K <= 0)
+        return fail(MS_HIP_ERR_INVALID, "MatMulNBits requires positive N and K attributes (got N=%d, K=%d).", N,
+                    K);
+    if (bits != 4 && bits != 8)
+        return fail(MS_HIP_ERR_INVALID, "MatMulNBits supports bits=4 or bits=8; got %d.", bits);
+    if (bs <= 0) return fail(MS_HIP_ERR_INVALID, "MatMulNBits requires a positive block_size; got %d.", bs);
+    const int64_t nb = ((int64_t)K + bs - 1) / bs;
+    const int64_t blob = ((int64_t)bs * bits + 7) / 8;
+    const int64_t expected_b = (int64_t)N * nb * blob;
+    if (b_len != expected_b)
+        return fail(MS_HIP_ERR_INVALID,
+                    "MatMulNBits B has %lld elements; expected %lld (N=%d \xC3\x97 n_blocks_per_row=%lld "
+                    "\xC3\x97 blob_size=%lld).",
+                    (long long)b_len, (long long)expected_b, N, (long long)nb, (long long)blob);
+    const int64_t expected_scales = (int64_t)N * nb;
+    if (scales_len != expected_scales)
+        return fail(MS_HIP_ERR_INVALID,
+                    "MatMulNBits scales has %lld elements; expected %lld (N=%d \xC3\x97 n_blocks_per_row=%lld).",
+                    (long long)scales_len, (long long)expected_scales, N, (long long)nb);
+    const int64_t zrb = (nb * bits + 7) / 8;
+    if (zp_kind == 2 && zp_len != expected_scales)
+        return fail(MS_HIP_ERR_INVALID, "MatMulNBits float zero_points has %lld elements; expected %lld.",
+                    (long long)zp_len, (long long)expected_scales);
+    if (zp_kind == 1 && zp_len != (int64_t)N * zrb)
+        return fail(MS_HIP_ERR_INVALID,
+                    "MatMulNBits packed zero_points has %lld bytes; expected %lld (N=%d \xC3\x97 %lld).",
+                    (long long)zp_len, (long long)N * zrb, N, (long long)zrb);
+    if (zp_kind != 0 && zp_kind != 1 && zp_kind != 2)
+        return fail(MS_HIP_ERR_INVALID, "MatMulNBits zero_points must be Float32 or UInt8.");
+    if (a_last_dim >= 0 && a_last_dim != K)
+        return fail(MS_HIP_ERR_INVALID, "MatMulNBits A inner dimension must equal K=%d; got %lld.", K,
+                    (long long)a_last_dim);
+    return MS_HIP_OK;
+}
+
+int alloc_weights(Weights& w, int has_zp)
+{
+    w.has_zp = has_zp;
+    MS_HIP_CHECK(hipMalloc(&w.d_b, (size_t)w.N * w.row_bytes));
+    MS_HIP_CHECK(hipMalloc(&w.d_scales, (size_t)w.N * w.nb * sizeof(float)));
+    if (has_zp) MS_HIP_CHECK(hipMalloc(&w.d_zp, (size_t)w.N * w.zrb));
+    return MS_HIP_OK;
+}
+
+}  // namespace
+
+// =========================================================================================
+extern "C" {
+
+int ms_hip_available(void) { return device_info().ok; }
+
+const char* ms_hip_device_name(void) { return device_info().name.c_str(); }
+
+const char* ms_hip_build_info(void)
+{
+    return "ms_hip_nbits (hipcc " __VERSION__ ", --offload-arch=gfx950, -ffp-contract=off)";
+}
+
+const char* ms_hip_last_error(void) { return g_last_error.c_str(); }
+
+int ms_hip_nbits_check(int N, int K, int bits, int block_size, int64_t b_len, int64_t scales_len, int zp_kind,
+                       int64_t zp_len, int64_t a_last_dim)
+{
+    return check_impl(N, K, bits, block_size, b_len, scales_len, zp_kind, zp_len, a_last_dim);
+}
+
+int ms_hip_nbits_weights_create(const uint8_t* bq, int64_t bq_len, const float* scales, int64_t scales_len,
+                                const uint8_t* zero_points, int64_t zp_len, int N, int K, int bits,
+                                int block_size, void** out_handle)
+{
+    if (!out_handle) return fail(MS_HIP_ERR_INVALID, "[ms_hip] out_handle is null");
+    *out_handle = nullptr;
+    int st = check_impl(N, K, bits, block_size, bq_len, scales_len, zero_points ? 1 : 0, zp_len, -1);
+    if (st) return st;
+    if (!bq || !scales) return fail(MS_HIP_ERR_INVALID, "[ms_hip] null B or scales pointer");
+    if ((st = require_device())) return st;
+    MS_HIP_CHECK(hipSetDevice(device_info().device));
+    HandleBox* box = new HandleBox();
+    Weights& w = box->w;
+    w.device = device_info().device;
+    derive_layout(w, N, K, bits, block_size);
+    st = alloc_weights(w, zero_points != nullptr);
+    if (!st) {
+        hipError_t e = hipMemcpy(w.d_b, bq, (size_t)N * w.row_bytes, hipMemcpyHostToDevice);
+        if (e == hipSuccess)
+            e = hipMemcpy(w.d_scales, scales, (size_t)N * w.nb * sizeof(float), hipMemcpyHostToDevice);
+        if (e == hipSuccess && zero_points)
+            e = hipMemcpy(w.d_zp, zero_points, (size_t)N * w.zrb, hipMemcpyHostToDevice);
+        if (e != hipSuccess) st = fail(MS_HIP_ERR_HIP, "[ms_hip] weight upload failed: %s", hipGetErrorString(e));
+    }
+    if (st) {
+        free_weights(w);
+        delete box;
+        return st;
+    }
+    *out_handle = box;
+    return MS_HIP_OK;
+}
+
+int ms_hip_nbits_weights_create_dev(const uint8_t* d_bq, const float* d_scales, const uint8_t* d_zero_points,
+                                    int N, int K, int bits, int block_size, void** out_handle)
+{
+    if (!out_handle) return fail(MS_HIP_ERR_INVALID, "[ms_hip] out_handle is null");
+    *out_handle = nullptr;
+    int st = check_impl(N, K, bits, block_size, (int64_t)N * ((K + block_size - 1) / block_size) *
+                                                    ((block_size * bits + 7) / 8),
+                        (int64_t)N * ((K + block_size - 1) / block_size), 0, 0, -1);
+    if (st) return st;
+    if (!d_bq || !d_scales) return fail(MS_HIP_ERR_INVALID, "[ms_hip] null B or scales pointer");
+    if ((st = require_device())) return st;
+    MS_HIP_CHECK(hipSetDevice(device_info().device));
+    HandleBox* box = new HandleBox();
+    Weights& w = box->w;
+    w.device = device_info().device;
+    derive_layout(w, N, K, bits, block_size);
+    st = alloc_weights(w, d_zero_points != nullptr);
+    if (!st) {
+        hipError_t e = hipMemcpy(w.d_b, d_bq, (size_t)N * w.row_bytes, hipMemcpyDeviceToDevice);
+        if (e == hipSuccess)
+            e = hipMemcpy(w.d_scales, d_scales, (size_t)N * w.nb * sizeof(float), hipMemcpyDeviceToDevice);
+        if (e == hipSuccess && d_zero_points)
+            e = hipMemcpy(w.d_zp, d_zero_points, (size_t)N * w.zrb, hipMemcpyDeviceToDevice);
+        if (e != hipSuccess) st = fail(MS_HIP_ERR_HIP, "[ms_hip] weight copy failed: %s", hipGetErrorString(e));
+    }
+    if (st) {
+        free_weights(w);
+        delete box;
+        return st;
+    }
+    *out_handle = box;
+    return MS_HIP_OK;
+}
+
+int ms_hip_nbits_weights_destroy(void* handle)
+{
+    Weights* w = from_handle(handle);
+    if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
+    {
+        std::lock_guard<std::mutex> lock(w->mu);
+        if (w->stream) (void)hipStreamSynchronize(w->stream);
+        free_weights(*w);
+    }
+    HandleBox* box = static_cast<HandleBox*>(handle);
+    box->magic = 0;
+    delete box;
+    return MS_HIP_OK;
+}
+
+int ms_hip_nbits_weights_info(void* handle, int* N, int* K, int* bits, int* block_size, int* has_zp)
+{
+    Weights* w = from_handle(handle);
+    if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
+    if (N) *N = w->N;
+    if (K) *K = w->K;
+    if (bits) *bits = w->bits;
+    if (block_size) *block_size = w->bs;
+    if (has_zp) *has_zp = w->has_zp;
+    return MS_HIP_OK;
+}
+
+int ms_hip_nbits_gemm_dev(void* handle, const float* dA, float* dY, int M, void* stream)
+{
+    Weights* w = from_handle(handle);
+    if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
+    return enqueue_gemm(*w, dA, dY, M, static_cast<hipStream_t>(stream));
+}
+
+int ms_hip_nbits_gemm_dev_batch(void* const* handles, const float* const* dA, float* const* dY, int count, int M,
+                                void* stream)
+{
+    if (count < 0 || (count > 0 && (!handles || !dA || !dY)))
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid batch arguments");
+    for (int i = 0; i < count; ++i) {
+        Weights* w = from_handle(handles[i]);
+        if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle at batch index %d", i);
+        const int st = enqueue_gemm(*w, dA[i], dY[i], M, static_cast<hipStream_t>(stream));
+        if (st) return st;
+    }
+    return MS_HIP_OK;
+}
+
+int ms_hip_nbits_gemm(void* handle, const float* a_host, float* y_host, int M)
+{
+    Weights* w = from_handle(handle);
+    if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
+    if (M < 0) return fail(MS_HIP_ERR_INVALID, "MatMulNBits M must be non-negative; got %d.", M);
+    if (M == 0) return MS_HIP_OK;
+    if (!a_host || !y_host) return fail(MS_HIP_ERR_INVALID, "[ms_hip] null activation or output pointer");
+    std::lock_guard<std::mutex> lock(w->mu);
+    MS_HIP_CHECK(hipSetDevice(w->device));
+    if (!w->stream) MS_HIP_CHECK(hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking));
+    const size_t a_bytes = (size_t)M * w->K * sizeof(float);
+    const size_t a_span = (a_bytes + 255) & ~(size_t)255;
+    const size_t y_bytes = (size_t)M * w->N * sizeof(float);
+    if (w->stage_bytes < a_span + y_bytes) {
+        if (w->d_stage) MS_HIP_CHECK(hipFree(w->d_stage));
+        w->d_stage = nullptr;
+        w->stage_bytes = 0;
+        MS_HIP_CHECK(hipMalloc(&w->d_stage, a_span + y_bytes));
+        w->stage_bytes = a_span + y_bytes;
+    }
+    float* dA = w->d_stage;
+    float* dY = reinterpret_cast<float*>(reinterpret_cast<char*>(w->d_stage) + a_span);
+    MS_HIP_CHECK(hipMemcpyAsync(dA, a_host, a_bytes, hipMemcpyHostToDevice, w->stream));
+    const int st = enqueue_gemm(*w, dA, dY, M, w->stream);
+    if (st) {
+        (void)hipStreamSynchronize(w->stream);
+        return st;
+    }
+    MS_HIP_CHECK(hipMemcpyAsync(y_host, dY, y_bytes, hipMemcpyDeviceToHost, w->stream));
+    MS_HIP_CHECK(hipStreamSynchronize(w->stream));
+    return MS_HIP_OK;
+}
+
+int ms_hip_qgemm_nbits(const float* a, const uint8_t* bq, const float* scales, const uint8_t* zero_points,
+                       float* y, int M, int N, int K, int bits, int block_size)
+{
+    // Buffer lengths are implied by the dimensions here, as in ms_qgemm_nbits.
+    if (N <= 0 || K <= 0 || (bits != 4 && bits != 8) || block_size <= 0)
+        return check_impl(N, K, bits, block_size, 0, 0, 0, 0, -1);
+    const int64_t nb = (K + block_size - 1) / block_size;
+    const int64_t blob = (block_size * bits + 7) / 8;
+    const int64_t zrb = (nb * bits + 7) / 8;
+    void* h = nullptr;
+    int st = ms_hip_nbits_weights_create(bq, (int64_t)N * nb * blob, scales, (int64_t)N * nb, zero_points,
+                                     (int64_t)N * zrb, N, K, bits, block_size, &h);
+    if (st) return st;
+    st = ms_hip_nbits_gemm(h, a, y, M);
+    const std::string err = g_last_error;
+    ms_hip_nbits_weights_destroy(h);
+    if (st) g_last_error = err;
+    return st;
+}
+
+int ms_hip_nbits_dequant_dev(void* handle, float* dW, void* stream)
+{
+    Weights* w = from_handle(handle);
+    if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
+    if (!dW) return fail(MS_HIP_ERR_INVALID, "[ms_hip] null output pointer");
+    const int64_t total = (int64_t)w->N * w->K;
+    hipLaunchKernelGGL(nbits_dequant_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), raw_layout(*w), dW);
+    MS_HIP_CHECK(hipGetLastError());
+    return MS_HIP_OK;
+}
+
+int ms_hip_nbits_dequant(void* handle, float* w_host)
+{
+    Weights* w = from_handle(handle);
+    if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
+    if (!w_host) return fail(MS_HIP_ERR_INVALID, "[ms_hip] null output pointer");
+    MS_HIP_CHECK(hipSetDevice(w->device));
+    const size_t bytes = (size_t)w->N * w->K * sizeof(float);
+    float* dW = nullptr;
+    MS_HIP_CHECK(hipMalloc(&dW, bytes));
+    int st = ms_hip_nbits_dequant_dev(handle, dW, nullptr);
+    if (!st) {
+        hipError_t e = hipMemcpy(w_host, dW, bytes, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) st = fail(MS_HIP_ERR_HIP, "[ms_hip] dequant download failed: %s", hipGetErrorString(e));
+    }
+    (void)hipFree(dW);
+    return st;
+}
+
+int ms_hip_alloc(void** dptr, int64_t bytes)
+{
+    if (!dptr || bytes < 0) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid alloc arguments");
+    int st = require_device();
+    if (st) return st;
+    MS_HIP_CHECK(hipMalloc(dptr, (size_t)(bytes ? bytes : 1)));
+    return MS_HIP_OK;
+}
+
+int ms_hip_free(void* dptr)
+{
+    if (dptr) MS_HIP_CHECK(hipFree(dptr));
+    return MS_HIP_OK;
+}
+
+int ms_hip_upload(void* dptr, const void* host, int64_t bytes)
+{
+    if (bytes < 0 || (bytes && (!dptr || !host))) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid upload");
+    if (bytes) MS_HIP_CHECK(hipMemcpy(dptr, host, (size_t)bytes, hipMemcpyHostToDevice));
+    return MS_HIP_OK;
+}
+
+int ms_hip_download(void* host, const void* dptr, int64_t bytes)
+{
+    if (bytes < 0 || (bytes && (!dptr || !host))) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid download");
+    if (bytes) MS_HIP_CHECK(hipMemcpy(host, dptr, (size_t)bytes, hipMemcpyDeviceToHost));
+    return MS_HIP_OK;
+}
+
+int ms_hip_sync(void)
+{
+    int st = require_device();
+    if (st) return st;
+    MS_HIP_CHECK(hipDeviceSynchronize());
+    return MS_HIP_OK;
+}
+
+int ms_hip_set_gemv_lanes(int lanes_per_row)
+{
+    if (lanes_per_row != 0 && lanes_per_row != 4 && lanes_per_row != 8 && lanes_per_row != 16 &&
+        lanes_per_row != 32 && lanes_per_row != 64)
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] lanes_per_row must be 0, 4, 8, 16, 32 or 64; got %d",
+                    lanes_per_row);
+    g_gemv_lanes_override = lanes_per_row;
+    return MS_HIP_OK;
+}
+
+int ms_hip_nbits_launch_info(void* handle, int M, int* kernel_id, int* lanes_per_row, int* grid, int* block)
+{
+    Weights* w = from_handle(handle);
+    if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
+    if (M <= 0) return fail(MS_HIP_ERR_INVALID, "[ms_hip] M must be positive; got %d", M);
+    int kid = 0, G = 0, gr = 0, bl = 0;
+    if (!w->fast) {
+        kid = 0;
+        gr = (int)(((int64_t)M * w->N + 255) / 256);
+        bl = 256;
+    } else if (M <= kGemvMaxM) {
+        const GemvShape s = gemv_shape(*w, M);
+        kid = 1;
+        G = s.G;
+        gr = s.grid;
+        bl = kGemvThreads;
+    } else {
+        kid = 2;
+        mfma_launch_shape(w->N, M, &gr, &bl);
+    }
+    if (kernel_id) *kernel_id = kid;
+    if (lanes_per_row) *lanes_per_row = G;
+    if (grid) *grid = gr;
+    if (block) *block = bl;
+    return MS_HIP_OK;
+}
+
+}  // extern "C"

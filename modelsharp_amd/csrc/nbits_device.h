@@ -1,0 +1,101 @@
+// nbits_device.h — device-side helpers shared by the MatMulNBits kernels.
+//
+// Dequantization is W[n,k] = ((float)q - zp) * scale with q the 4-bit code of
+// column k in row n and zp an integer, as in
+// src/ModelSharp/Cpu/Kernels/Quantize/MatMulNBitsSimd.cs:100-111. For integer
+// zp, q - zp is exact, so the product is the only rounding. The library is
+// compiled with -ffp-contract=off, so that product is never fused into the
+// accumulation that follows it; the accumulations are explicit fmaf.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace msnb {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;             // CDNA wavefront
+constexpr uint32_t kHalfMagic = 0x64006400u;   // two fp16 1024.0: 1024 + v for a 10-bit v
+
+__device__ __forceinline__ h2_t as_h2(uint32_t v) { return __builtin_bit_cast(h2_t, v); }
+
+__device__ __forceinline__ uint32_t as_u32(h2_t v) { return __builtin_bit_cast(uint32_t, v); }
+
+// (x & mask) | orv in one VALU op. gfx9 VOP3 takes no literal and at most one
+// scalar operand, so the mask rides in an SGPR and orv in a VGPR.
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t orv)
+{
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(orv));
+    return r;
+}
+
+// fp32 fma(fp16 lane of h2 widened, s, c): with c = -0.0 (the additive
+// identity) this is the single rounding of (float)h * s.
+__device__ __forceinline__ float mix_lo(uint32_t h2, float s, float c)
+{
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(s), "s"(c));
+    return r;
+}
+__device__ __forceinline__ float mix_hi(uint32_t h2, float s, float c)
+{
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(s), "s"(c));
+    return r;
+}
+
+// Per-block dequant constants. A 4-bit code sitting in bits 0-3 of an fp16
+// lane with exponent bits 0x6400 reads as 1024 + q; sitting in bits 4-7 it
+// reads as 1024 + 16q. Subtracting 1024 + zp (resp. 1024 + 16zp) in packed fp16
+// is exact and leaves d = q - zp (resp. 16(q - zp)); the fp32 product with s
+// (resp. s/16, exact by a power of two for |s| >= 2^-122) is then the single
+// rounding of (q - zp) * s.
+struct BlockDq {
+    h2_t zb;     // (1024 + zp) x2
+    h2_t zb16;   // (1024 + 16 zp) x2
+    float s;     // scale
+    float s16;   // scale / 16
+};
+
+__device__ __forceinline__ BlockDq block_dq(int zp, float s)
+{
+    BlockDq q;
+    q.zb = as_h2(kHalfMagic | ((uint32_t)zp << 16) | (uint32_t)zp);
+    q.zb16 = as_h2(kHalfMagic | ((uint32_t)zp << 20) | ((uint32_t)zp << 4));
+    q.s = s;
+    q.s16 = s * 0.0625f;
+    return q;
+}
+
+// Dequantizes the eight 4-bit codes of one little-endian dword (codes for
+// k = 8j .. 8j+7 of a chunk: byte i holds k=2i in its low nibble and k=2i+1 in
+// its high nibble) to fp32, w[i] for k = 8j + i. 25 VALU ops for 8 weights:
+// one shift, four and_or, four packed fp16 subtracts, eight fma_mix.
+__device__ __forceinline__ void dequant8(uint32_t x, const BlockDq& q, float (&w)[8])
+{
+    const uint32_t magic = kHalfMagic;
+    const uint32_t x8 = x >> 8;
+    const uint32_t d0 = as_u32(as_h2(and_or(x, 0x000F000Fu, magic)) - q.zb);      // k0, k4
+    const uint32_t d1 = as_u32(as_h2(and_or(x, 0x00F000F0u, magic)) - q.zb16);    // 16*k1, 16*k5
+    const uint32_t d2 = as_u32(as_h2(and_or(x8, 0x000F000Fu, magic)) - q.zb);     // k2, k6
+    const uint32_t d3 = as_u32(as_h2(and_or(x8, 0x00F000F0u, magic)) - q.zb16);   // 16*k3, 16*k7
+    const float nz = -0.0f;
+    w[0] = mix_lo(d0, q.s, nz);
+    w[4] = mix_hi(d0, q.s, nz);
+    w[1] = mix_lo(d1, q.s16, nz);
+    w[5] = mix_hi(d1, q.s16, nz);
+    w[2] = mix_lo(d2, q.s, nz);
+    w[6] = mix_hi(d2, q.s, nz);
+    w[3] = mix_lo(d3, q.s16, nz);
+    w[7] = mix_hi(d3, q.s16, nz);
+}
+
+// Packed zero point of block `blk` from a row of packed nibbles
+// (MatMulNBitsKernel.cs:349-356 with bits=4).
+__device__ __forceinline__ int zp_nibble(const uint8_t* zrow, int blk)
+{
+    return (zrow[blk >> 1] >> ((blk & 1) * 4)) & 0x0F;
+}
+
+}  // namespace msnb

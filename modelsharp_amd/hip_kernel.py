@@ -1,0 +1,146 @@
+"""HipMatMulNBitsKernel — the MatMulNBits operator routed to the MI355X library.
+
+A drop-in for the reference's managed kernel behind the same interface
+(IKernel, OpType "MatMulNBits"): it validates its inputs exactly as
+src/ModelSharp/Cpu/Kernels/Quantize/MatMulNBitsKernel.cs:79-169 does (same
+checks, same order, same messages), keeps one device-resident weight handle per
+initializer (created at load time by preload(), or on first use), and calls the
+C ABI of libms_hip_nbits.so. It never falls back to a CPU kernel: inputs the C
+ABI cannot take (float zero points, a non-uint8 B) raise
+DeviceUnsupportedInput, which a host engine answers by keeping the reference's
+own managed kernel registered for such nodes (the C# binding does exactly that).
+"""
+from __future__ import annotations
+
+import threading
+
+import numpy as np
+
+from . import native
+from .graph import GraphContext, GraphNode, IKernel, KernelRegistry, ModelGraph, ModelSharpException, element_type
+
+
+class DeviceUnsupportedInput(ModelSharpException):
+    """Valid operator input that the HIP path does not take (the reference's
+    native seam declines the same inputs: NativeQuant.cs:78-101,
+    MatMulNBitsKernel.cs:172-174)."""
+
+
+def _to_numpy(t):
+    if isinstance(t, np.ndarray):
+        return t
+    return t.detach().cpu().numpy()
+
+
+class HipMatMulNBitsKernel(IKernel):
+    op_type = "MatMulNBits"
+
+    def __init__(self):
+        self._lock = threading.Lock()
+        self._handles: dict[tuple, native.NBitsWeights] = {}
+
+    # ---- validation: MatMulNBitsKernel.cs:79-161 ----------------------------------------
+    @staticmethod
+    def _validate(node: GraphNode, ctx: GraphContext):
+        a = ctx.get(node.inputs[0])
+        b = ctx.get_tensor(node.inputs[1])
+        if element_type(b) != "UInt8":                          # QuantizeKernels.cs:54-56
+            raise ModelSharpException(f"Tensor dtype is {element_type(b)}; expected UInt8.")
+        N = node.attr_int("N", 0)
+        K = node.attr_int("K", 0)
+        bits = node.attr_int("bits", 4)
+        block_size = node.attr_int("block_size", 0)
+        scales = ctx.get(node.inputs[2])
+        lib = native.load()
+        st = lib.ms_hip_nbits_check(N, K, bits, block_size, int(np.prod(b.shape)), int(np.prod(scales.shape)),
+                                    0, 0, -1)
+        if st:
+            raise ModelSharpException(native.last_error())
+        zp = None
+        if len(node.inputs) > 3 and ctx.has(node.inputs[3]):   # :119-145
+            zp = ctx.get_tensor(node.inputs[3])
+            kind = {"UInt8": 1, "Float32": 2}.get(element_type(zp))
+            if kind is None:
+                raise ModelSharpException(
+                    f"MatMulNBits zero_points must be Float32 or UInt8; got {element_type(zp)}.")
+            st = lib.ms_hip_nbits_check(N, K, bits, block_size, int(np.prod(b.shape)),
+                                        int(np.prod(scales.shape)), kind, int(np.prod(zp.shape)), -1)
+            if st:
+                raise ModelSharpException(native.last_error())
+        if len(node.inputs) > 4 and ctx.has(node.inputs[4]):   # :148-155
+            g_idx = _to_numpy(ctx.get_tensor(node.inputs[4])).reshape(-1).astype(np.int64)
+            if np.any(g_idx != np.arange(g_idx.size, dtype=np.int64) // block_size):
+                raise ModelSharpException(
+                    "MatMulNBits g_idx with a non-trivial block permutation is not supported.")
+        shape = tuple(a.shape)
+        if len(shape) == 0 or shape[-1] != K:                  # :158-161
+            raise ModelSharpException(
+                f"MatMulNBits A inner dimension must equal K={K}; got shape [{','.join(str(d) for d in shape)}].")
+        return a, b, scales, zp, N, K, bits, block_size
+
+    # ---- device-resident weights -----------------------------------------------------------
+    @staticmethod
+    def _key(node: GraphNode, b, scales, zp):
+        names = tuple(node.inputs[1:4])
+        return names + (id(b), id(scales), id(zp))
+
+    def _weights(self, node, b, scales, zp, N, K, bits, block_size) -> native.NBitsWeights:
+        if zp is not None and element_type(zp) == "Float32":
+            raise DeviceUnsupportedInput(
+                "MatMulNBits float zero_points are not representable in the HIP C ABI; "
+                "run this node on the managed kernel.")
+        key = self._key(node, b, scales, zp)
+        with self._lock:
+            w = self._handles.get(key)
+            if w is None:
+                w = native.NBitsWeights(_to_numpy(b), _to_numpy(scales).astype(np.float32),
+                                        None if zp is None else _to_numpy(zp), N, K, bits, block_size)
+                self._handles[key] = w
+            return w
+
+    def preload(self, graph: ModelGraph) -> int:
+        """Load-time upload: one handle per MatMulNBits node whose B, scales and
+        zero points are initializers. Returns the number of handles created."""
+        made = 0
+        ctx = GraphContext(graph.initializers)
+        for node in graph.nodes:
+            if node.op_type != self.op_type:
+                continue
+            names = node.inputs[1:4]
+            if not all(ctx.has(n) for n in names if n) or not ctx.has(node.inputs[1]):
+                continue
+            b = ctx.get_tensor(node.inputs[1])
+            scales = ctx.get(node.inputs[2])
+            zp = ctx.get_tensor(node.inputs[3]) if len(node.inputs) > 3 and ctx.has(node.inputs[3]) else None
+            before = len(self._handles)
+            self._weights(node, b, scales, zp, node.attr_int("N", 0), node.attr_int("K", 0),
+                          node.attr_int("bits", 4), node.attr_int("block_size", 0))
+            made += len(self._handles) - before
+        return made
+
+    def close(self) -> None:
+        with self._lock:
+            for w in self._handles.values():
+                w.close()
+            self._handles.clear()
+
+    # ---- IKernel.Execute -------------------------------------------------------------------
+    def execute(self, node: GraphNode, ctx: GraphContext) -> None:
+        a, b, scales, zp, N, K, bits, block_size = self._validate(node, ctx)
+        w = self._weights(node, b, scales, zp, N, K, bits, block_size)
+        lead = tuple(a.shape[:-1])
+        M = int(np.prod(lead)) if lead else 1
+        if isinstance(a, np.ndarray):
+            y = w.gemm(a.reshape(M, K)).reshape(lead + (N,))
+        else:
+            import torch
+            a2 = a.reshape(M, K).contiguous()
+            y = torch.empty(lead + (N,), dtype=torch.float32, device=a.device)
+            w.gemm_dev(a2.data_ptr(), y.data_ptr(), M, torch.cuda.current_stream(a.device).cuda_stream)
+        ctx.set(node.outputs[0], y)
+
+
+def register_kernels(registry: KernelRegistry) -> KernelRegistry:
+    """Routes MatMulNBits to the HIP kernel; last registration wins, as for
+    ImageSharpRegistration.RegisterKernels (src/ModelSharp.ImageSharp/ImageSharpRegistration.cs:52-60)."""
+    return registry.register(HipMatMulNBitsKernel())

@@ -1,0 +1,231 @@
+"""ctypes binding of libms_hip_nbits.so, the C ABI in include/ms_hip_kernels.h.
+
+The library is built in-tree (``__graft_entry__.build()`` or
+``make -C modelsharp_amd/csrc``) into ``modelsharp_amd/lib/``;
+``MODELSHARP_HIP_LIB`` overrides the path, as ``MODELSHARP_NATIVE_LIB`` does for
+the reference's CPU library (src/ModelSharp/Native/NativeGemm.cs:98-116).
+There is no CPU fallback: a missing library raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+import re
+import threading
+
+import numpy as np
+
+_PKG = pathlib.Path(__file__).resolve().parent
+LIB_NAME = "libms_hip_nbits.so"
+HEADER = _PKG.parent / "include" / "ms_hip_kernels.h"
+
+MS_HIP_OK = 0
+MS_HIP_ERR_INVALID = 1
+MS_HIP_ERR_NO_DEVICE = 2
+MS_HIP_ERR_HIP = 3
+MS_HIP_ERR_UNSUPPORTED = 4
+
+_c_int = ctypes.c_int
+_c_i64 = ctypes.c_int64
+_vp = ctypes.c_void_p
+_fp = ctypes.POINTER(ctypes.c_float)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_ip = ctypes.POINTER(ctypes.c_int)
+
+# name -> (restype, argtypes); must cover every function in the header.
+_PROTOTYPES = {
+    "ms_hip_available": (_c_int, []),
+    "ms_hip_device_name": (ctypes.c_char_p, []),
+    "ms_hip_build_info": (ctypes.c_char_p, []),
+    "ms_hip_last_error": (ctypes.c_char_p, []),
+    "ms_hip_nbits_check": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_int, _c_i64, _c_i64]),
+    "ms_hip_nbits_weights_create": (
+        _c_int, [_vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_vp)]),
+    "ms_hip_nbits_weights_create_dev": (
+        _c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_vp)]),
+    "ms_hip_nbits_weights_destroy": (_c_int, [_vp]),
+    "ms_hip_nbits_weights_info": (_c_int, [_vp, _ip, _ip, _ip, _ip, _ip]),
+    "ms_hip_nbits_gemm": (_c_int, [_vp, _vp, _vp, _c_int]),
+    "ms_hip_nbits_gemm_dev": (_c_int, [_vp, _vp, _vp, _c_int, _vp]),
+    "ms_hip_nbits_gemm_dev_batch": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _vp]),
+    "ms_hip_qgemm_nbits": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int]),
+    "ms_hip_nbits_dequant": (_c_int, [_vp, _vp]),
+    "ms_hip_nbits_dequant_dev": (_c_int, [_vp, _vp, _vp]),
+    "ms_hip_alloc": (_c_int, [ctypes.POINTER(_vp), _c_i64]),
+    "ms_hip_free": (_c_int, [_vp]),
+    "ms_hip_upload": (_c_int, [_vp, _vp, _c_i64]),
+    "ms_hip_download": (_c_int, [_vp, _vp, _c_i64]),
+    "ms_hip_sync": (_c_int, []),
+    "ms_hip_set_gemv_lanes": (_c_int, [_c_int]),
+    "ms_hip_nbits_launch_info": (_c_int, [_vp, _c_int, _ip, _ip, _ip, _ip]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class HipError(RuntimeError):
+    """A nonzero status from the library, with ms_hip_last_error()'s message."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(message)
+        self.status = status
+        self.message = message
+
+
+def lib_path() -> pathlib.Path:
+    env = os.environ.get("MODELSHARP_HIP_LIB")
+    return pathlib.Path(env) if env else _PKG / "lib" / LIB_NAME
+
+
+def load() -> ctypes.CDLL:
+    """Loads the library once; raises RuntimeError when it has not been built."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        # torch ships its own libamdhip64 (same soname, different file name);
+        # importing it first makes this library bind to that one copy, so the
+        # process never holds two HIP runtimes.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
+        path = lib_path()
+        if not path.is_file():
+            raise RuntimeError(
+                f"{LIB_NAME} is not built (expected at {path}); run __graft_entry__.build() "
+                "or make -C modelsharp_amd/csrc")
+        lib = ctypes.CDLL(str(path))
+        for name, (res, args) in _PROTOTYPES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def header_functions() -> list[str]:
+    """Names of every function the C header declares."""
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"\b(ms_hip_\w+)\s*\(", text)
+
+
+def last_error() -> str:
+    return load().ms_hip_last_error().decode("utf-8", "replace")
+
+
+def check(status: int) -> None:
+    if status != MS_HIP_OK:
+        raise HipError(status, last_error())
+
+
+def available() -> bool:
+    return bool(load().ms_hip_available())
+
+
+def device_name() -> str:
+    return load().ms_hip_device_name().decode()
+
+
+def _ptr(arr):
+    return None if arr is None else arr.ctypes.data_as(_vp)
+
+
+class NBitsWeights:
+    """A device-resident MatMulNBits weight (B, scales, packed zero points).
+
+    Created once per initializer (load-time upload) and reused by every call,
+    like the per-initializer residency of IlgpuEngine.ResidentOrTempInt
+    (src/ModelSharp.Gpu/IlgpuEngine.cs:3392-3429), minus its int32 widening.
+    """
+
+    def __init__(self, b: np.ndarray, scales: np.ndarray, zero_points: np.ndarray | None,
+                 N: int, K: int, bits: int = 4, block_size: int = 32):
+        lib = load()
+        b = np.ascontiguousarray(b, dtype=np.uint8).reshape(-1)
+        scales = np.ascontiguousarray(scales, dtype=np.float32).reshape(-1)
+        zp = None if zero_points is None else np.ascontiguousarray(zero_points, dtype=np.uint8).reshape(-1)
+        handle = _vp()
+        check(lib.ms_hip_nbits_weights_create(
+            _ptr(b), b.size, _ptr(scales), scales.size, _ptr(zp), 0 if zp is None else zp.size,
+            int(N), int(K), int(bits), int(block_size), ctypes.byref(handle)))
+        self._init(handle, N, K, bits, block_size, zp is not None)
+
+    @classmethod
+    def from_device(cls, d_b: int, d_scales: int, d_zp: int | None, N: int, K: int, bits: int = 4,
+                    block_size: int = 32) -> "NBitsWeights":
+        lib = load()
+        handle = _vp()
+        check(lib.ms_hip_nbits_weights_create_dev(_vp(d_b), _vp(d_scales), _vp(d_zp) if d_zp else None,
+                                                  N, K, bits, block_size, ctypes.byref(handle)))
+        self = cls.__new__(cls)
+        self._init(handle, N, K, bits, block_size, bool(d_zp))
+        return self
+
+    def _init(self, handle, N, K, bits, block_size, has_zp):
+        self.handle = handle
+        self.N, self.K, self.bits, self.block_size, self.has_zp = int(N), int(K), int(bits), int(block_size), has_zp
+
+    def gemm(self, a: np.ndarray) -> np.ndarray:
+        """Host-pointer call: a[M,K] fp32 -> y[M,N] fp32 (synchronous)."""
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        M = a.size // self.K
+        y = np.empty((M, self.N), dtype=np.float32)
+        check(load().ms_hip_nbits_gemm(self.handle, _ptr(a), _ptr(y), M))
+        return y
+
+    def gemm_dev(self, dA: int, dY: int, M: int, stream: int | None = None) -> None:
+        check(load().ms_hip_nbits_gemm_dev(self.handle, _vp(dA), _vp(dY), int(M), _vp(stream or 0)))
+
+    def dequant(self) -> np.ndarray:
+        w = np.empty((self.N, self.K), dtype=np.float32)
+        check(load().ms_hip_nbits_dequant(self.handle, _ptr(w)))
+        return w
+
+    def dequant_dev(self, dW: int, stream: int | None = None) -> None:
+        check(load().ms_hip_nbits_dequant_dev(self.handle, _vp(dW), _vp(stream or 0)))
+
+    def launch_info(self, M: int) -> dict:
+        k, g, gr, bl = (ctypes.c_int() for _ in range(4))
+        check(load().ms_hip_nbits_launch_info(self.handle, int(M), ctypes.byref(k), ctypes.byref(g),
+                                              ctypes.byref(gr), ctypes.byref(bl)))
+        return {"kernel": ("generic", "gemv_w4", "mfma_w4")[k.value], "lanes_per_row": g.value,
+                "grid": gr.value, "block": bl.value}
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            check(load().ms_hip_nbits_weights_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def gemm_dev_batch(weights: list, dA: list[int], dY: list[int], M: int, stream: int | None = None) -> None:
+    """Enqueues len(weights) calls back to back with one library call."""
+    n = len(weights)
+    hs = (_vp * n)(*[w.handle for w in weights])
+    pa = (_vp * n)(*dA)
+    py = (_vp * n)(*dY)
+    check(load().ms_hip_nbits_gemm_dev_batch(hs, pa, py, n, int(M), _vp(stream or 0)))
+
+
+def set_gemv_lanes(lanes: int) -> None:
+    check(load().ms_hip_set_gemv_lanes(int(lanes)))
+
+
+def qgemm_nbits(a, b, scales, zero_points, M, N, K, bits, block_size) -> np.ndarray:
+    """One-shot call with ms_qgemm_nbits's argument meaning (uploads per call)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    y = np.empty((M, N), dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    scales = np.ascontiguousarray(scales, dtype=np.float32)
+    zp = None if zero_points is None else np.ascontiguousarray(zero_points, dtype=np.uint8)
+    check(load().ms_hip_qgemm_nbits(_ptr(a), _ptr(b), _ptr(scales), _ptr(zp), _ptr(y), M, N, K, bits, block_size))
+    return y

@@ -1,0 +1,127 @@
+"""CPU oracle of the MatMulNBits operator — TEST INFRASTRUCTURE.
+
+Loaded only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+leg, as the checker or as the timed CPU baseline; the product never imports
+it. liboracle_nbits.so is the C restatement of the reference's managed kernel
+(ms_nbits_oracle.c, citations there); _ref/libms_ref_qgemm.so, when present, is
+the reference's own native ms_qgemm_nbits compiled from its sources.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+_vp = ctypes.c_void_p
+_lib = None
+_ref = None
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(_vp)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        path = HERE / "liboracle_nbits.so"
+        if not path.is_file():
+            raise RuntimeError(f"oracle not built: {path} (run __graft_entry__.build())")
+        L = ctypes.CDLL(str(path))
+        L.msor_unpack_nbit.restype = ctypes.c_int
+        L.msor_unpack_nbit.argtypes = [_vp, ctypes.c_int64, ctypes.c_int, ctypes.c_int]
+        L.msor_dequant_block4.argtypes = [_vp, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_float, _vp]
+        L.msor_dequant_block8.argtypes = [_vp, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_float, _vp]
+        L.msor_fma_accumulate.restype = ctypes.c_float
+        L.msor_fma_accumulate.argtypes = [ctypes.c_float, _vp, _vp, ctypes.c_int]
+        L.msor_should_parallelize.restype = ctypes.c_int
+        L.msor_should_parallelize.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int]
+        L.msor_matmul_nbits.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp] + [ctypes.c_int] * 6
+        L.msor_dequant_weights.argtypes = [_vp, _vp, _vp, _vp, _vp] + [ctypes.c_int] * 5
+        L.msor_matmul_f64.argtypes = [_vp, _vp, _vp] + [ctypes.c_int] * 4
+        _lib = L
+    return _lib
+
+
+def ref_lib():
+    """The reference's own ms_qgemm_nbits (built from its sources), or None."""
+    global _ref
+    if _ref is None:
+        path = HERE / "_ref" / "libms_ref_qgemm.so"
+        if not path.is_file():
+            return None
+        L = ctypes.CDLL(str(path))
+        L.ms_qgemm_nbits.restype = None
+        L.ms_qgemm_nbits.argtypes = [_vp, _vp, _vp, _vp, _vp] + [ctypes.c_int] * 5
+        _ref = L
+    return _ref
+
+
+def threads() -> int:
+    try:
+        return max(1, len(os.sched_getaffinity(0)))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def matmul_nbits(a, b, scales, zp_packed, N, K, bits, block_size, zp_float=None, nthreads=None):
+    """y[M,N] of the managed kernel's default path (MatMulNBitsKernel.cs:193-262)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    M = a.size // K
+    y = np.empty((M, N), dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    scales = np.ascontiguousarray(scales, dtype=np.float32)
+    zp_packed = None if zp_packed is None else np.ascontiguousarray(zp_packed, dtype=np.uint8)
+    zp_float = None if zp_float is None else np.ascontiguousarray(zp_float, dtype=np.float32)
+    lib().msor_matmul_nbits(_ptr(a), _ptr(b), _ptr(scales), _ptr(zp_packed), _ptr(zp_float), _ptr(y),
+                            M, N, K, bits, block_size, nthreads or threads())
+    return y
+
+
+def dequant_weights(b, scales, zp_packed, N, K, bits, block_size, zp_float=None, nthreads=None):
+    w = np.empty((N, K), dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    scales = np.ascontiguousarray(scales, dtype=np.float32)
+    zp_packed = None if zp_packed is None else np.ascontiguousarray(zp_packed, dtype=np.uint8)
+    zp_float = None if zp_float is None else np.ascontiguousarray(zp_float, dtype=np.float32)
+    lib().msor_dequant_weights(_ptr(b), _ptr(scales), _ptr(zp_packed), _ptr(zp_float), _ptr(w),
+                               N, K, bits, block_size, nthreads or threads())
+    return w
+
+
+def matmul_f64(a, w, nthreads=None):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    N, K = w.shape
+    M = a.size // K
+    y = np.empty((M, N), dtype=np.float64)
+    lib().msor_matmul_f64(_ptr(a), _ptr(w), _ptr(y), M, N, K, nthreads or threads())
+    return y
+
+
+def fma_accumulate(acc, a, w):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    return lib().msor_fma_accumulate(ctypes.c_float(acc), _ptr(a), _ptr(w), int(a.size))
+
+
+def unpack_nbit(data, base_byte, index, bits):
+    data = np.ascontiguousarray(data, dtype=np.uint8)
+    return lib().msor_unpack_nbit(_ptr(data), base_byte, index, bits)
+
+
+def ref_qgemm_nbits(a, b, scales, zp_packed, M, N, K, bits, block_size):
+    """The reference's native ms_qgemm_nbits (qgemm.cpp:77-118), or None if not built."""
+    L = ref_lib()
+    if L is None:
+        return None
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    y = np.empty((M, N), dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    scales = np.ascontiguousarray(scales, dtype=np.float32)
+    zp_packed = None if zp_packed is None else np.ascontiguousarray(zp_packed, dtype=np.uint8)
+    L.ms_qgemm_nbits(_ptr(a), _ptr(b), _ptr(scales), _ptr(zp_packed), _ptr(y), M, N, K, bits, block_size)
+    return y

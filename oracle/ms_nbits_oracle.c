@@ -1,0 +1,229 @@
+/*
+ * ms_nbits_oracle.c — CPU restatement of ModelSharp's managed MatMulNBits.
+ *
+ * TEST INFRASTRUCTURE: the oracle the HIP path is checked against, and the
+ * CPU baseline bench.py times beside the GPU. Nothing in the product loads it.
+ *
+ * Built with -ffp-contract=off so that every multiply-add is fused exactly
+ * where the reference fuses it (explicit fmaf, standing for the
+ * Avx512F/Fma.FusedMultiplyAdd calls) and nowhere else.
+ *
+ * Pinning (tests/test_oracle.py):
+ *   msor_unpack_nbit        exhaustive over all 256 bytes vs the packing rule,
+ *                           reference KATs (MatMulNBitsTests.cs:57-267).
+ *   msor_dequant_block4/8   closed form fl32((q-zp)*s) element-wise; bit-exact
+ *                           against the reference's own ms_qgemm_nbits
+ *                           (native/src/qgemm.cpp, built from source) through
+ *                           one-hot activations.
+ *   msor_fma_accumulate     exact sums of small integers (every partial sum
+ *                           representable), double-precision brute force on
+ *                           random data, all lengths 0..200 (every branch).
+ *   msor_matmul_nbits       the 8 hand-derived KATs, the reference native
+ *                           kernel on its own parity grid, f64 brute force.
+ *   msor_matmul_f64         exact small-integer products.
+ * The horizontal-sum order of Vector512.Sum / Vector256.Sum lives in the .NET
+ * runtime (not in the checkout); it is restated as a pairwise fold of halves,
+ * which fixes the oracle's own bits but not the managed kernel's (parity to
+ * tolerance only, as the reference's own tests do).
+ */
+#include "ms_nbits_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+int msor_unpack_nbit(const uint8_t* data, int64_t base_byte, int index, int bits)
+{
+    /* MatMulNBitsKernel.cs:351-355 */
+    if (bits == 8) return data[base_byte + index];
+    const int64_t byte_off = base_byte + (index >> 1);
+    const int shift = (index & 1) * 4;
+    return (data[byte_off] >> shift) & 0x0F;
+}
+
+void msor_dequant_block4(const uint8_t* src, int64_t blob_base, int count,
+                         float zp, float scale, float* dst)
+{
+    /* MatMulNBitsSimd.cs:50-95. The AVX2 path (UnpackLow/High of the low and
+     * high nibbles, widen, convert, (q - zp) * scale) and the scalar tail
+     * compute the same two fp32 operations per code, so one loop states all. */
+    for (int i = 0; i < count; ++i) {
+        const int b = src[blob_base + (i >> 1)];
+        const int q = ((i & 1) == 0) ? (b & 0x0F) : ((b >> 4) & 0x0F);
+        dst[i] = ((float)q - zp) * scale;
+    }
+}
+
+void msor_dequant_block8(const uint8_t* src, int64_t blob_base, int count,
+                         float zp, float scale, float* dst)
+{
+    /* MatMulNBitsSimd.cs:125-131 */
+    for (int i = 0; i < count; ++i) dst[i] = ((float)src[blob_base + i] - zp) * scale;
+}
+
+/* Horizontal sums standing for Vector512.Sum / Vector256.Sum (runtime code,
+ * not in the checkout): fold the upper half onto the lower half until one
+ * lane remains. */
+static float hsum16(const float* v)
+{
+    float t[8], u[4];
+    for (int j = 0; j < 8; ++j) t[j] = v[j] + v[j + 8];
+    for (int j = 0; j < 4; ++j) u[j] = t[j] + t[j + 4];
+    return (u[0] + u[2]) + (u[1] + u[3]);
+}
+
+static float hsum8(const float* v)
+{
+    float u[4];
+    for (int j = 0; j < 4; ++j) u[j] = v[j] + v[j + 4];
+    return (u[0] + u[2]) + (u[1] + u[3]);
+}
+
+float msor_fma_accumulate(float acc, const float* a, const float* w, int n)
+{
+    int i = 0;
+    if (n >= 16) {
+        /* MatMulNBitsSimd.cs:145-162 (Avx512F branch) */
+        float s0[16], s1[16], s2[16], s3[16], s[16];
+        for (int j = 0; j < 16; ++j) s0[j] = s1[j] = s2[j] = s3[j] = 0.0f;
+        const int last4 = n - 64;
+        for (; i <= last4; i += 64) {
+            for (int j = 0; j < 16; ++j) s0[j] = fmaf(a[i + j], w[i + j], s0[j]);
+            for (int j = 0; j < 16; ++j) s1[j] = fmaf(a[i + 16 + j], w[i + 16 + j], s1[j]);
+            for (int j = 0; j < 16; ++j) s2[j] = fmaf(a[i + 32 + j], w[i + 32 + j], s2[j]);
+            for (int j = 0; j < 16; ++j) s3[j] = fmaf(a[i + 48 + j], w[i + 48 + j], s3[j]);
+        }
+        for (int j = 0; j < 16; ++j) s[j] = (s0[j] + s1[j]) + (s2[j] + s3[j]);
+        const int last = n - 16;
+        for (; i <= last; i += 16)
+            for (int j = 0; j < 16; ++j) s[j] = fmaf(a[i + j], w[i + j], s[j]);
+        acc += hsum16(s);
+    } else if (n >= 8) {
+        /* MatMulNBitsSimd.cs:163-180 (Fma branch; AVX-512 hosts take it for 8 <= n < 16) */
+        float s0[8], s1[8], s2[8], s3[8], s[8];
+        for (int j = 0; j < 8; ++j) s0[j] = s1[j] = s2[j] = s3[j] = 0.0f;
+        const int last4 = n - 32;
+        for (; i <= last4; i += 32) {
+            for (int j = 0; j < 8; ++j) s0[j] = fmaf(a[i + j], w[i + j], s0[j]);
+            for (int j = 0; j < 8; ++j) s1[j] = fmaf(a[i + 8 + j], w[i + 8 + j], s1[j]);
+            for (int j = 0; j < 8; ++j) s2[j] = fmaf(a[i + 16 + j], w[i + 16 + j], s2[j]);
+            for (int j = 0; j < 8; ++j) s3[j] = fmaf(a[i + 24 + j], w[i + 24 + j], s3[j]);
+        }
+        for (int j = 0; j < 8; ++j) s[j] = (s0[j] + s1[j]) + (s2[j] + s3[j]);
+        const int last = n - 8;
+        for (; i <= last; i += 8)
+            for (int j = 0; j < 8; ++j) s[j] = fmaf(a[i + j], w[i + j], s[j]);
+        acc += hsum8(s);
+    } else {
+        /* MatMulNBitsSimd.cs:181-199 (portable Vector<T>, 8 lanes): for n < 8
+         * no full vector is formed, and Vector.Dot of the zero vector adds 0. */
+        acc += 0.0f;
+    }
+    /* MatMulNBitsSimd.cs:201 — scalar tail, multiply then add */
+    for (; i < n; ++i) {
+        const float p = a[i] * w[i];
+        acc += p;
+    }
+    return acc;
+}
+
+int msor_should_parallelize(int64_t rows, int64_t inner_cost, int dop)
+{
+    /* MatMulParallel.cs:32 (threshold 1<<16) and :38-39 */
+    return rows > 1 && dop > 1 && rows * inner_cost >= (1LL << 16);
+}
+
+static float zero_point_of(const uint8_t* zp_packed, const float* zp_float, int64_t scale_row_base,
+                           int64_t zp_row_base, int bk, int bits)
+{
+    /* MatMulNBitsKernel.cs:239-242 and the default at :115 */
+    if (zp_float) return zp_float[scale_row_base + bk];
+    if (zp_packed) return (float)msor_unpack_nbit(zp_packed, zp_row_base, bk, bits);
+    return (float)(1 << (bits - 1));
+}
+
+void msor_matmul_nbits(const float* a, const uint8_t* b, const float* scales,
+                       const uint8_t* zp_packed, const float* zp_float, float* y,
+                       int M, int N, int K, int bits, int block_size, int nthreads)
+{
+    /* MatMulNBitsKernel.cs:95-96, :118, :193 */
+    const int nb = (K + block_size - 1) / block_size;
+    const int blob = (block_size * bits + 7) / 8;
+    const int zrb = (nb * bits + 7) / 8;
+    const int64_t row_bytes = (int64_t)nb * blob;
+    if (nthreads < 1) nthreads = 1;
+    const int par = msor_should_parallelize(N, (int64_t)K * (M + 1), nthreads);
+
+#pragma omp parallel num_threads(nthreads) if (par)
+    {
+        /* MatMulNBitsKernel.cs:233-234 (block scratch and per-row accumulators) */
+        float* wblock = (float*)malloc(sizeof(float) * (size_t)block_size);
+        float* acc = (float*)malloc(sizeof(float) * (size_t)(M > 0 ? M : 1));
+#pragma omp for schedule(static)
+        for (int n = 0; n < N; ++n) {
+            const int64_t b_row_base = (int64_t)n * row_bytes;
+            const int64_t scale_row_base = (int64_t)n * nb;
+            const int64_t zp_row_base = (int64_t)n * zrb;
+            for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+            for (int bk = 0; bk < nb; ++bk) {              /* :236-258 */
+                const float scale = scales[scale_row_base + bk];
+                const float zp = zero_point_of(zp_packed, zp_float, scale_row_base, zp_row_base, bk, bits);
+                const int64_t blob_base = b_row_base + (int64_t)bk * blob;
+                const int k_start = bk * block_size;
+                const int len = (block_size < K - k_start) ? block_size : K - k_start;
+                if (len <= 0) break;
+                if (bits == 4) msor_dequant_block4(b, blob_base, len, zp, scale, wblock);
+                else msor_dequant_block8(b, blob_base, len, zp, scale, wblock);
+                for (int m = 0; m < M; ++m)
+                    acc[m] = msor_fma_accumulate(acc[m], a + (int64_t)m * K + k_start, wblock, len);
+            }
+            for (int m = 0; m < M; ++m) y[(int64_t)m * N + n] = acc[m];   /* :260-261 */
+        }
+        free(wblock);
+        free(acc);
+    }
+}
+
+void msor_dequant_weights(const uint8_t* b, const float* scales,
+                          const uint8_t* zp_packed, const float* zp_float, float* w,
+                          int N, int K, int bits, int block_size, int nthreads)
+{
+    const int nb = (K + block_size - 1) / block_size;
+    const int blob = (block_size * bits + 7) / 8;
+    const int zrb = (nb * bits + 7) / 8;
+    const int64_t row_bytes = (int64_t)nb * blob;
+    if (nthreads < 1) nthreads = 1;
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+    for (int n = 0; n < N; ++n) {
+        for (int bk = 0; bk < nb; ++bk) {
+            const float scale = scales[(int64_t)n * nb + bk];
+            const float zp = zero_point_of(zp_packed, zp_float, (int64_t)n * nb, (int64_t)n * zrb, bk, bits);
+            const int k_start = bk * block_size;
+            const int len = (block_size < K - k_start) ? block_size : K - k_start;
+            if (len <= 0) break;
+            float* dst = w + (int64_t)n * K + k_start;
+            const int64_t blob_base = (int64_t)n * row_bytes + (int64_t)bk * blob;
+            if (bits == 4) msor_dequant_block4(b, blob_base, len, zp, scale, dst);
+            else msor_dequant_block8(b, blob_base, len, zp, scale, dst);
+        }
+    }
+}
+
+void msor_matmul_f64(const float* a, const float* w, double* y, int M, int N, int K, int nthreads)
+{
+    if (nthreads < 1) nthreads = 1;
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+    for (int n = 0; n < N; ++n) {
+        const float* wr = w + (int64_t)n * K;
+        for (int m = 0; m < M; ++m) {
+            const float* ar = a + (int64_t)m * K;
+            double s = 0.0;
+            for (int k = 0; k < K; ++k) s += (double)ar[k] * (double)wr[k];
+            y[(int64_t)m * N + n] = s;
+        }
+    }
+}

@@ -1,0 +1,69 @@
+/*
+ * ms_nbits_oracle.h — CPU oracle for the MatMulNBits operator.
+ *
+ * TEST INFRASTRUCTURE. Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg load this library, and only as the checker or as the timed
+ * CPU baseline. The product library (modelsharp_amd/csrc) never links it.
+ *
+ * Every function restates one piece of the reference's managed kernel; the
+ * file:line citation is on each declaration (paths are relative to the
+ * ModelSharp checkout).
+ */
+#ifndef MS_NBITS_ORACLE_H
+#define MS_NBITS_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* UnpackNBit — src/ModelSharp/Cpu/Kernels/Quantize/MatMulNBitsKernel.cs:349-356.
+ * index-th `bits`-wide code of the packed region at base_byte; bits=4 keeps the
+ * even index in the low nibble. */
+int msor_unpack_nbit(const uint8_t* data, int64_t base_byte, int index, int bits);
+
+/* DequantBlock4 — MatMulNBitsSimd.cs:40-96 (AVX2 unpack :50-69, vector tail
+ * :72-88, scalar tail :90-95; all three produce the same fp32 values).
+ * dst[i] = ((float)q_i - zp) * scale, one rounding for integer zp. */
+void msor_dequant_block4(const uint8_t* src, int64_t blob_base, int count,
+                         float zp, float scale, float* dst);
+
+/* DequantBlock8 — MatMulNBitsSimd.cs:117-132. */
+void msor_dequant_block8(const uint8_t* src, int64_t blob_base, int count,
+                         float zp, float scale, float* dst);
+
+/* FmaAccumulate — MatMulNBitsSimd.cs:141-203, the branch an AVX-512 host takes:
+ * n>=16: four 16-lane FMA accumulators over 64-element steps, fold, 16-lane
+ * steps, horizontal sum added to acc; 8<=n<16: the 8-lane FMA branch;
+ * n<8: the portable branch (no full vector); then the scalar tail
+ * acc += a*w (separate multiply and add, no fusion). */
+float msor_fma_accumulate(float acc, const float* a, const float* w, int n);
+
+/* MatMulParallel.ShouldParallelize — Cpu/Kernels/Linear/MatMulParallel.cs:32-39. */
+int msor_should_parallelize(int64_t rows, int64_t inner_cost, int dop);
+
+/* MatMulNBitsKernel.Execute default path — MatMulNBitsKernel.cs:193-262:
+ * column-parallel over N (MatMulParallel.For, :216), per column the fused
+ * block loop (:236-258) and the store (:260-261).
+ * zp_packed / zp_float: at most one non-NULL (NULL/NULL = default 2^(bits-1)).
+ * nthreads is the degree of parallelism (Environment.ProcessorCount). */
+void msor_matmul_nbits(const float* a, const uint8_t* b, const float* scales,
+                       const uint8_t* zp_packed, const float* zp_float, float* y,
+                       int M, int N, int K, int bits, int block_size, int nthreads);
+
+/* The dequantized weight matrix W[N,K] the kernel above multiplies by, built
+ * from the same per-block dequant (MatMulNBitsKernel.cs:236-253). */
+void msor_dequant_weights(const uint8_t* b, const float* scales,
+                          const uint8_t* zp_packed, const float* zp_float, float* w,
+                          int N, int K, int bits, int block_size, int nthreads);
+
+/* Double-accumulated brute force y[m,n] = sum_k (double)a[m,k]*(double)w[n,k]
+ * over the fp32 dequantized weights, as native/test/qgemm_test.cpp:60-89
+ * does for its reference. */
+void msor_matmul_f64(const float* a, const float* w, double* y,
+                     int M, int N, int K, int nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,309 @@
+"""GPU parity of libms_hip_nbits.so against the oracle and the golden fixtures.
+
+Bars (from the operator's definition):
+  * dequantized weights: bit-exact (value equality) with the oracle and with
+    the reference's native kernel's one-hot output;
+  * decode GEMV (M <= 16): per row m, max_n |y - y_ref| <= 1e-5 * max_n |y_ref[m, n]|;
+  * prefill MFMA (M > 16): ||y - y_ref||_F / ||y_ref||_F <= 2e-3.
+All calls go through the C ABI.
+"""
+from __future__ import annotations
+
+import threading
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import kat_arrays
+from modelsharp_amd import native, workloads
+from modelsharp_amd.graph import Engine, GraphNode, KernelRegistry, ModelGraph
+from modelsharp_amd.hip_kernel import HipMatMulNBitsKernel, register_kernels
+
+pytestmark = pytest.mark.gpu
+
+GEMV_RTOL = 1e-5
+MFMA_FRO = 2e-3
+
+
+def log(msg):
+    print(msg, flush=True)
+
+
+def assert_gemv_close(y, ref, what, cond=None):
+    """Row bar 1e-5 * ||y_ref[m,:]||_inf. With `cond` = sum_k |a_k w_nk| given
+    (rows of a few outputs, where the row norm is one possibly cancelling dot
+    product), an error within the order-independent fp32 bound 2*gamma_K*cond of
+    either summation also passes."""
+    ref = ref.reshape(y.shape)
+    rowmax = np.max(np.abs(ref), axis=-1, keepdims=True)
+    allowed = GEMV_RTOL * rowmax
+    if cond is not None:
+        allowed = np.maximum(allowed, cond)
+    err = np.max(np.abs(y - ref) / np.maximum(rowmax, 1e-30))
+    log(f"  {what}: max row-relative err {err:.3e}")
+    assert np.all(np.abs(y - ref) <= allowed), f"{what}: {err:.3e}"
+
+
+def fp32_dot_bound(a, W):
+    """2*gamma_K * sum_k |a_mk * W_nk|: bounds the gap between two fp32 sums in any order."""
+    K = a.shape[-1]
+    u = np.finfo(np.float32).eps / 2
+    gamma = K * u / (1 - K * u)
+    return 2 * gamma * (np.abs(a).astype(np.float64) @ np.abs(W).astype(np.float64).T)
+
+
+def assert_fro_close(y, ref, what):
+    rel = float(np.linalg.norm((y - ref).astype(np.float64)) / np.linalg.norm(ref.astype(np.float64)))
+    log(f"  {what}: rel Frobenius {rel:.3e}")
+    assert rel <= MFMA_FRO, f"{what}: {rel:.3e}"
+
+
+def weights_for(op, seed):
+    b, s, z = workloads.make_weights(op, seed)
+    return b, s, z, native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
+
+
+# ---- the reference's known answers ---------------------------------------------------------
+def test_kats_through_the_device(gpu, kat_cases):
+    for case in kat_cases:
+        a, b, s, zp, y = kat_arrays(case)
+        if zp is not None and zp.dtype == np.float32:
+            continue   # float zero points are not representable in the C ABI
+        at = case["attrs"]
+        log(f"KAT {case['name']}")
+        w = native.NBitsWeights(b, s, zp, at["N"], at["K"], at["bits"], at["block_size"])
+        got = w.gemm(a.reshape(-1, at["K"])).reshape(y.shape)
+        np.testing.assert_allclose(got, y, rtol=0, atol=1e-4, err_msg=case["name"])
+        assert np.array_equal(got, y)
+        w.close()
+
+
+def test_golden_reference_vectors_through_the_device(gpu, ref_vectors):
+    for key, g in sorted(ref_vectors.items()):
+        if key.startswith("grid"):
+            M, N, K, bits, bs = (int(x) for x in g["dims"])
+            log(f"golden {key}")
+            w = native.NBitsWeights(g["b"], g["scales"], g.get("zp"), N, K, bits, bs)
+            assert_gemv_close(w.gemm(g["a"]), g["y"], key)
+        else:
+            N, K, bits, bs = (int(x) for x in g["dims"])
+            log(f"golden {key}")
+            w = native.NBitsWeights(g["b"], g["scales"], g.get("zp"), N, K, bits, bs)
+            assert np.array_equal(w.dequant(), g["w"]), key
+        w.close()
+
+
+# ---- dequantized weights: bit-exact on every workload shape -----------------------------------
+ALL_OPS = ([workloads.QWEN05B_UP] + workloads.QWEN05B_DECODE + workloads.DECODE_7B + workloads.LLAMA7B_SMALLM_OPS
+           + workloads.LLAMA7B_PREFILL_OPS)
+
+
+@pytest.mark.parametrize("op", ALL_OPS, ids=lambda o: f"{o.name}_K{o.K}_N{o.N}_bs{o.block_size}_{'zp' if o.has_zp else 'nozp'}")
+def test_dequant_bit_exact(gpu, op):
+    b, s, z, w = weights_for(op, seed=op.K * 7 + op.N)
+    log(f"dequant K={op.K} N={op.N} bs={op.block_size}")
+    assert np.array_equal(w.dequant(), oracle.dequant_weights(b, s, z, op.N, op.K, 4, op.block_size))
+    w.close()
+
+
+# ---- decode GEMV parity at the workloads' full sizes --------------------------------------------
+DECODE_CASES = ([(workloads.QWEN05B_UP, 1)] + [(o, 1) for o in workloads.QWEN05B_DECODE]
+                + [(o, 1) for o in workloads.DECODE_7B]
+                + [(o, m) for o in workloads.LLAMA7B_SMALLM_OPS for m in workloads.LLAMA7B_SMALLM_M])
+
+
+@pytest.mark.parametrize("op,M", DECODE_CASES, ids=lambda v: str(v) if isinstance(v, int) else f"{v.name}_K{v.K}_N{v.N}")
+def test_gemv_parity(gpu, op, M):
+    b, s, z, w = weights_for(op, seed=op.N + 3 * op.K + M)
+    a = workloads.make_activations(M, op.K, seed=M + op.K)
+    assert w.launch_info(M)["kernel"] == "gemv_w4"
+    log(f"gemv M={M} K={op.K} N={op.N} bs={op.block_size} {w.launch_info(M)}")
+    y = w.gemm(a)
+    assert_gemv_close(y, oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, op.block_size), f"M={M} {op}")
+    w.close()
+
+
+def test_gemv_one_hot_is_bit_exact(gpu):
+    """A = rows of the identity: each output is one product 1*W[n,k] plus zeros."""
+    op = workloads.DECODE_7B[4]
+    b, s, z, w = weights_for(op, seed=9)
+    ks = np.random.default_rng(1).choice(op.K, 16, replace=False)
+    a = np.zeros((16, op.K), np.float32)
+    a[np.arange(16), ks] = 1.0
+    W = oracle.dequant_weights(b, s, z, op.N, op.K, 4, op.block_size)
+    for M in (1, 4, 16):
+        y = w.gemm(a[:M])
+        assert np.array_equal(y, W[:, ks[:M]].T), M
+    w.close()
+
+
+@pytest.mark.parametrize("lanes", [4, 8, 16, 32, 64])
+def test_gemv_every_lane_split(gpu, lanes):
+    ops = [workloads.Op("a", 3584, 1000), workloads.Op("b", 896, 77, 128, False), workloads.Op("c", 4864, 96, 64)]
+    try:
+        native.set_gemv_lanes(lanes)
+        for op in ops:
+            for M in (1, 3, 16):
+                b, s, z, w = weights_for(op, seed=lanes + M)
+                a = workloads.make_activations(M, op.K, seed=M)
+                log(f"lanes={lanes} M={M} K={op.K} N={op.N}")
+                assert_gemv_close(w.gemm(a), oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, op.block_size),
+                                  f"lanes={lanes} M={M} {op}")
+                w.close()
+    finally:
+        native.set_gemv_lanes(0)
+
+
+# ---- shapes the fast kernels do not take, and edges ----------------------------------------------
+EDGE = [
+    workloads.Op("ktail", 100, 33, 32, True),          # K % 32 != 0 -> generic
+    workloads.Op("bs16", 96, 40, 16, True),            # block size 16 -> generic
+    workloads.Op("bits8", 256, 24, 32, True, bits=8),  # 8-bit -> generic
+    workloads.Op("bits8sym", 192, 20, 64, False, bits=8),
+    workloads.Op("bs64", 640, 70, 64, True),           # fast, 2 chunks per block
+    workloads.Op("bs256", 1024, 65, 256, False),       # fast, 8 chunks per block
+    workloads.Op("n1", 512, 1, 32, True),              # a single output column
+    workloads.Op("odd_nb", 96, 37, 32, True),          # 3 blocks: odd packed zero-point row
+]
+
+
+@pytest.mark.parametrize("op", EDGE, ids=lambda o: o.name)
+@pytest.mark.parametrize("M", [1, 5, 16, 40])
+def test_edge_shapes(gpu, op, M):
+    b, s, z, w = weights_for(op, seed=M + op.N)
+    a = workloads.make_activations(M, op.K, seed=M * 3)
+    log(f"edge {op.name} M={M} {w.launch_info(M)}")
+    ref = oracle.matmul_nbits(a, b, s, z, op.N, op.K, op.bits, op.block_size)
+    y = w.gemm(a)
+    W = oracle.dequant_weights(b, s, z, op.N, op.K, op.bits, op.block_size)
+    if w.launch_info(M)["kernel"] == "mfma_w4":
+        assert_fro_close(y, ref, f"{op.name} M={M}")
+    else:
+        assert_gemv_close(y, ref, f"{op.name} M={M}", cond=fp32_dot_bound(a, W))
+    assert np.array_equal(w.dequant(), W)
+    w.close()
+
+
+def test_m_zero_is_a_no_op(gpu):
+    op = workloads.Op("m0", 128, 16)
+    b, s, z, w = weights_for(op, 1)
+    assert w.gemm(np.zeros((0, op.K), np.float32)).shape == (0, op.N)
+    w.close()
+
+
+# ---- prefill MFMA -------------------------------------------------------------------------------
+@pytest.mark.parametrize("op", workloads.LLAMA7B_PREFILL_OPS, ids=lambda o: f"K{o.K}_N{o.N}")
+@pytest.mark.parametrize("M", workloads.LLAMA7B_PREFILL_M)
+def test_mfma_parity_sampled_columns(gpu, op, M):
+    """Full-size call; the oracle checks a seeded sample of 96 output columns."""
+    b, s, z, w = weights_for(op, seed=M + op.N)
+    a = workloads.make_activations(M, op.K, seed=M, kind="rmsnorm")
+    assert w.launch_info(M)["kernel"] == "mfma_w4"
+    log(f"mfma M={M} K={op.K} N={op.N}")
+    y = w.gemm(a)
+    cols = np.sort(np.random.default_rng(M).choice(op.N, 96, replace=False))
+    zc = None if z is None else z[cols]
+    ref = oracle.matmul_nbits(a, b[cols], s.reshape(op.N, -1)[cols], zc, len(cols), op.K, 4, op.block_size)
+    assert_fro_close(y[:, cols], ref, f"M={M} sampled")
+    assert np.all(np.isfinite(y))
+    w.close()
+
+
+@pytest.mark.parametrize("M", [17, 33, 64, 100, 129, 300])
+def test_mfma_partial_tiles(gpu, M):
+    op = workloads.Op("pt", 896, 333, 32, True)
+    b, s, z, w = weights_for(op, seed=M)
+    a = workloads.make_activations(M, op.K, seed=M, kind="rmsnorm")
+    log(f"mfma partial M={M} N={op.N}")
+    assert_fro_close(w.gemm(a), oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, 32), f"M={M}")
+    w.close()
+
+
+def test_mfma_full_vs_torch_fp32(gpu):
+    """Every output of an M=2048 call against an fp32 product of the
+    (bit-exact) dequantized weights on the device."""
+    import torch
+    torch.backends.cuda.matmul.allow_tf32 = False
+    op = workloads.LLAMA7B_PREFILL_OPS[0]
+    b, s, z, w = weights_for(op, seed=5)
+    a = workloads.make_activations(2048, op.K, seed=6, kind="rmsnorm")
+    dA = torch.from_numpy(a).cuda()
+    dY = torch.empty((2048, op.N), dtype=torch.float32, device="cuda")
+    dW = torch.empty((op.N, op.K), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    w.gemm_dev(dA.data_ptr(), dY.data_ptr(), 2048, stream)
+    w.dequant_dev(dW.data_ptr(), stream)
+    ref = dA.double() @ dW.double().T
+    rel = float(torch.linalg.norm(dY.double() - ref) / torch.linalg.norm(ref))
+    log(f"  mfma M=2048 full vs fp64 device product: rel Frobenius {rel:.3e}")
+    assert rel <= MFMA_FRO
+    w.close()
+
+
+# ---- determinism, concurrency, the operator interface ------------------------------------------
+def test_repeatable_and_thread_safe(gpu):
+    op = workloads.Op("thr", 2048, 1536, 32, True)
+    b, s, z, w = weights_for(op, 4)
+    a = workloads.make_activations(3, op.K, 5)
+    a_big = workloads.make_activations(70, op.K, 6)
+    y0, y0b = w.gemm(a), w.gemm(a_big)
+    results = {}
+
+    def worker(i):
+        results[i] = (w.gemm(a), w.gemm(a_big))
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(8)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    for i in range(8):
+        assert np.array_equal(results[i][0], y0) and np.array_equal(results[i][1], y0b), i
+    w.close()
+
+
+def test_operator_interface_drop_in(gpu):
+    import torch
+    op = workloads.Op("proj", 896, 4864, 32, True)
+    b, s, z = workloads.make_weights(op, 8)
+    graph = ModelGraph(
+        nodes=[GraphNode("MatMulNBits", "mmnb", ["A", "B", "scales", "zp"], ["Y"],
+                         {"N": op.N, "K": op.K, "bits": 4, "block_size": 32})],
+        initializers={"B": b, "scales": s, "zp": z}, inputs=["A"], outputs=["Y"])
+    registry = register_kernels(KernelRegistry())
+    kernel = registry.try_get("MatMulNBits")[1]
+    assert isinstance(kernel, HipMatMulNBitsKernel)
+    assert kernel.preload(graph) == 1
+    a = workloads.make_activations(6, op.K, 9).reshape(2, 3, op.K)
+    y = Engine(graph, registry).run({"A": a})["Y"]
+    assert y.shape == (2, 3, op.N)
+    ref = oracle.matmul_nbits(a.reshape(6, op.K), b, s, z, op.N, op.K, 4, 32)
+    assert_gemv_close(y.reshape(6, op.N), ref, "engine host path")
+    yd = Engine(graph, registry).run({"A": torch.from_numpy(a).cuda()})["Y"]
+    torch.cuda.synchronize()
+    assert np.array_equal(yd.cpu().numpy(), y)
+    assert len(kernel._handles) == 1
+    kernel.close()
+
+
+def test_one_shot_entry_matches_handle_path(gpu):
+    op = workloads.Op("one", 512, 200, 32, True)
+    b, s, z, w = weights_for(op, 12)
+    a = workloads.make_activations(4, op.K, 13)
+    assert np.array_equal(native.qgemm_nbits(a, b, s, z, 4, op.N, op.K, 4, 32), w.gemm(a))
+    w.close()
+
+
+def test_batch_entry_matches_single_calls(gpu):
+    import torch
+    ops = workloads.DECODE_7B[:4]
+    ws = [weights_for(o, i)[3] for i, o in enumerate(ops)]
+    As = [torch.from_numpy(workloads.make_activations(1, o.K, i)).cuda() for i, o in enumerate(ops)]
+    Ys = [torch.empty((1, o.N), device="cuda") for o in ops]
+    stream = torch.cuda.current_stream().cuda_stream
+    native.gemm_dev_batch(ws, [x.data_ptr() for x in As], [y.data_ptr() for y in Ys], 1, stream)
+    torch.cuda.synchronize()
+    for w, x, y in zip(ws, As, Ys):
+        assert np.array_equal(y.cpu().numpy(), w.gemm(x.cpu().numpy()))
+        w.close()

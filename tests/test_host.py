@@ -1,0 +1,173 @@
+"""Host-side tests that need no GPU: the C-ABI library loads and exports what
+include/ms_hip_kernels.h declares, the validation rules and messages match
+MatMulNBitsKernel.cs:87-161, and the operator-interface mirror behaves like
+KernelRegistry / ManagedCpuEngine."""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import ROOT, kat_arrays
+from modelsharp_amd import native
+from modelsharp_amd.graph import (Engine, GraphContext, GraphNode, KernelRegistry, ModelGraph, ModelSharpException,
+                                  UnsupportedOperatorException)
+from modelsharp_amd.hip_kernel import DeviceUnsupportedInput, HipMatMulNBitsKernel, register_kernels
+
+X = "×"
+
+
+def test_library_exports_every_header_symbol():
+    lib = native.load()
+    names = native.header_functions()
+    assert len(names) >= 20
+    for name in names:
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", str(native.lib_path())], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert set(names) <= exported
+    assert set(native._PROTOTYPES) == set(names)
+
+
+def test_library_is_gfx950_code():
+    blob = native.lib_path().read_bytes()
+    assert b"amdgcn-amd-amdhsa--gfx950" in blob
+    for other in (b"--gfx942", b"--gfx90a", b"--gfx1100"):
+        assert other not in blob
+
+
+def test_no_device_is_reported_not_crashed():
+    if native.available():
+        pytest.skip("a gfx950 device is present")
+    lib = native.load()
+    assert lib.ms_hip_available() == 0
+    h = ctypes.c_void_p()
+    b = np.zeros(64, np.uint8)
+    s = np.ones(4, np.float32)
+    st = lib.ms_hip_nbits_weights_create(b.ctypes.data, b.size, s.ctypes.data, s.size, None, 0, 4, 32, 4, 32,
+                                         ctypes.byref(h))
+    assert st == native.MS_HIP_ERR_NO_DEVICE
+    assert "no gfx950 device" in native.last_error()
+    assert not h.value
+
+
+def check(N, K, bits, bs, b_len, s_len, zp_kind=0, zp_len=0, a_last=-1):
+    st = native.load().ms_hip_nbits_check(N, K, bits, bs, b_len, s_len, zp_kind, zp_len, a_last)
+    return st, (native.last_error() if st else "")
+
+
+def test_check_messages_match_reference():
+    # MatMulNBitsKernel.cs:87-93
+    assert check(0, 4, 4, 4, 0, 0) == (1, "MatMulNBits requires positive N and K attributes (got N=0, K=4).")
+    assert check(2, -1, 4, 4, 0, 0) == (1, "MatMulNBits requires positive N and K attributes (got N=2, K=-1).")
+    assert check(2, 4, 3, 4, 0, 0) == (1, "MatMulNBits supports bits=4 or bits=8; got 3.")
+    assert check(2, 4, 4, 0, 0, 0) == (1, "MatMulNBits requires a positive block_size; got 0.")
+    # :100-104
+    assert check(2, 8, 4, 4, 7, 4) == (
+        1, f"MatMulNBits B has 7 elements; expected 8 (N=2 {X} n_blocks_per_row=2 {X} blob_size=2).")
+    # :108-112
+    assert check(2, 8, 4, 4, 8, 3) == (
+        1, f"MatMulNBits scales has 3 elements; expected 4 (N=2 {X} n_blocks_per_row=2).")
+    # :126-129 float zp, :134-138 packed zp
+    assert check(2, 8, 4, 4, 8, 4, 2, 3) == (1, "MatMulNBits float zero_points has 3 elements; expected 4.")
+    assert check(2, 8, 4, 4, 8, 4, 1, 3) == (1, f"MatMulNBits packed zero_points has 3 bytes; expected 2 (N=2 {X} 1).")
+    # valid inputs, K tail and 8-bit
+    assert check(2, 8, 4, 4, 8, 4, 1, 2) == (0, "")
+    assert check(1, 6, 4, 4, 4, 2) == (0, "")
+    assert check(2, 4, 8, 4, 8, 2, 1, 2) == (0, "")
+    assert check(3, 100, 4, 32, 3 * 4 * 16, 12, 1, 6) == (0, "")
+
+
+def _node(inputs, N, K, bits=4, bs=4, name="n"):
+    return GraphNode("MatMulNBits", name, inputs, ["Y"], {"N": N, "K": K, "bits": bits, "block_size": bs})
+
+
+def test_kernel_validation_messages(kat_cases):
+    k = HipMatMulNBitsKernel()
+    a, b, s, zp, y = kat_arrays(kat_cases[0])
+    ctx = GraphContext({"A": a, "B": b, "scales": s})
+    with pytest.raises(ModelSharpException, match=r"^MatMulNBits requires positive N and K attributes \(got N=0, K=4\)\.$"):
+        k.execute(_node(["A", "B", "scales"], 0, 4), ctx)
+    with pytest.raises(ModelSharpException, match=r"^Tensor dtype is Int32; expected UInt8\.$"):
+        k.execute(_node(["A", "B2", "scales"], 2, 4), GraphContext({"A": a, "B2": b.astype(np.int32), "scales": s}))
+    with pytest.raises(ModelSharpException, match=r"^MatMulNBits zero_points must be Float32 or UInt8; got Int64\.$"):
+        k.execute(_node(["A", "B", "scales", "zp"], 2, 4),
+                  GraphContext({"A": a, "B": b, "scales": s, "zp": np.array([6, 10], np.int64)}))
+    with pytest.raises(ModelSharpException, match=r"^MatMulNBits A inner dimension must equal K=4; got shape \[1,3\]\.$"):
+        k.execute(_node(["A", "B", "scales"], 2, 4), GraphContext({"A": a[:, :3].copy(), "B": b, "scales": s}))
+    with pytest.raises(ModelSharpException, match="non-trivial block permutation"):
+        k.execute(_node(["A", "B", "scales", "", "g"], 2, 4),
+                  GraphContext({"A": a, "B": b, "scales": s, "g": np.array([0, 0, 1, 0], np.int32)}))
+
+
+def test_float_zero_points_are_declined_not_computed(kat_cases):
+    case = next(c for c in kat_cases if c["name"] == "Bits4_FloatZeroPoints")
+    a, b, s, zp, _ = kat_arrays(case)
+    k = HipMatMulNBitsKernel()
+    with pytest.raises(DeviceUnsupportedInput):
+        k.execute(_node(["A", "B", "scales", "zp"], 2, 4), GraphContext({"A": a, "B": b, "scales": s, "zp": zp}))
+
+
+def test_registry_last_registration_wins():
+    class Other:
+        op_type = "MatMulNBits"
+
+        def execute(self, node, ctx):
+            pass
+
+    r = KernelRegistry().register(Other())
+    register_kernels(r)
+    ok, k = r.try_get("MatMulNBits")
+    assert ok and isinstance(k, HipMatMulNBitsKernel) and r.count == 1
+    assert r.try_get("Relu") == (False, None)
+
+
+def test_engine_unknown_op_message():
+    g = ModelGraph(nodes=[GraphNode("Relu", "r0", ["X"], ["Y"])], initializers={}, inputs=["X"], outputs=["Y"])
+    with pytest.raises(UnsupportedOperatorException, match=r"^Operator 'Relu' is not supported yet by the managed engine \(node 'r0'\)\.$"):
+        Engine(g, KernelRegistry()).run({"X": np.zeros(1, np.float32)})
+
+
+def test_context_semantics():
+    ctx = GraphContext({"h": np.ones(3, np.float16)})
+    assert ctx.get("h").dtype == np.float32
+    assert not ctx.has("")
+    with pytest.raises(ModelSharpException, match="Tensor 'x' is not available in the execution context."):
+        ctx.get_tensor("x")
+
+
+def test_workload_costs_match_published_table():
+    from modelsharp_amd import workloads as W
+    # BASELINE table rows (bytes, flops)
+    assert W.algorithmic_bytes(W.QWEN05B_UP, 1) == 2_814_976
+    assert W.flops(W.QWEN05B_UP, 1) == 8_716_288
+    gate = next(o for o in W.DECODE_7B if o.name == "gate")
+    assert W.algorithmic_bytes(gate, 1) == 43_585_536
+    assert sum(W.algorithmic_bytes(o, 1) for o in W.DECODE_7B) == 149_655_552
+    assert sum(W.algorithmic_bytes(o, 1) for o in W.QWEN05B_DECODE) == 97_465_600
+    up, down = W.LLAMA7B_PREFILL_OPS
+    # (4096,11008) and (11008,4096) cost the same each
+    for op in (up, down):
+        assert W.algorithmic_bytes(op, 2048) == 152_616_960
+        assert W.flops(op, 2048) == 184_683_593_728
+        assert W.algorithmic_bytes(op, 128) == 36_618_240
+    for op in W.LLAMA7B_SMALLM_OPS:
+        assert W.algorithmic_bytes(op, 1) == 24_013_824
+        assert W.algorithmic_bytes(op, 16) == 24_920_064
+
+
+def test_pack_nibbles_layout():
+    from modelsharp_amd.workloads import pack_nibbles
+    assert pack_nibbles(np.array([[8, 9, 7, 10]])).tolist() == [[0x98, 0xA7]]
+    assert pack_nibbles(np.array([[1, 2, 3]])).tolist() == [[0x21, 0x03]]
+
+
+def test_header_is_plain_c():
+    src = (ROOT / "include" / "ms_hip_kernels.h").read_text()
+    assert "torch" not in src and "hip_runtime" not in src
+    out = subprocess.run(["gcc", "-fsyntax-only", "-x", "c", "-std=c99", "-Wall", "-Werror", "-"], input=src,
+                         capture_output=True, text=True)
+    assert out.returncode == 0, out.stderr

@@ -1,0 +1,168 @@
+"""Pins the CPU oracle (oracle/ms_nbits_oracle.c) before anything is checked against it.
+
+Each oracle function is checked against something other than its own formula:
+the reference's hand-derived KATs, the reference's own native ms_qgemm_nbits
+(built from source; golden vectors and, where present, live), exhaustive
+enumeration, exact small-integer arithmetic and a double-precision brute force.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import kat_arrays
+from modelsharp_amd import workloads
+
+
+# ---- unpack (MatMulNBitsKernel.cs:349-356) ---------------------------------------------------
+def test_unpack_exhaustive_all_bytes():
+    data = np.arange(256, dtype=np.uint8)
+    for v in range(256):
+        # the packing rule of MatMulNBitsTests.cs:42: byte = lo | hi << 4
+        lo, hi = v % 16, v // 16
+        assert oracle.unpack_nbit(data, v, 0, 4) == lo
+        assert oracle.unpack_nbit(data, v, 1, 4) == hi
+        assert oracle.unpack_nbit(data, 0, v, 8) == v
+    # index i of a region: byte base + i//2, nibble i%2
+    row = np.array([0x21, 0x43, 0x65], np.uint8)
+    assert [oracle.unpack_nbit(row, 0, i, 4) for i in range(6)] == [1, 2, 3, 4, 5, 6]
+    assert [oracle.unpack_nbit(row, 1, i, 4) for i in range(4)] == [3, 4, 5, 6]
+
+
+# ---- the reference's known-answer tests -------------------------------------------------------
+def test_kats(kat_cases):
+    assert len(kat_cases) == 8
+    for case in kat_cases:
+        a, b, s, zp, y = kat_arrays(case)
+        at = case["attrs"]
+        zp_packed = zp if (zp is not None and zp.dtype == np.uint8) else None
+        zp_float = zp if (zp is not None and zp.dtype == np.float32) else None
+        got = oracle.matmul_nbits(a, b, s, zp_packed, at["N"], at["K"], at["bits"], at["block_size"],
+                                  zp_float=zp_float).reshape(y.shape)
+        np.testing.assert_allclose(got, y, rtol=0, atol=1e-4, err_msg=case["name"])
+        # small integers and dyadic scales: the oracle is exact on all eight
+        assert np.array_equal(got, y), case["name"]
+
+
+# ---- FmaAccumulate (MatMulNBitsSimd.cs:141-203) ------------------------------------------------
+def test_fma_accumulate_exact_on_small_integers():
+    rng = np.random.default_rng(5)
+    for n in range(0, 201):
+        a = rng.integers(-3, 4, n).astype(np.float32)
+        w = rng.integers(-3, 4, n).astype(np.float32)
+        acc0 = float(rng.integers(-50, 50))
+        # every partial sum is an integer below 2^24: any dropped, doubled or
+        # misindexed term changes the result
+        assert oracle.fma_accumulate(acc0, a, w) == acc0 + float(np.dot(a.astype(np.int64), w.astype(np.int64))), n
+
+
+def test_fma_accumulate_vs_f64():
+    rng = np.random.default_rng(6)
+    eps = np.finfo(np.float32).eps
+    for n in [1, 7, 8, 15, 16, 17, 31, 32, 33, 63, 64, 65, 128, 200, 1000]:
+        a = rng.standard_normal(n).astype(np.float32)
+        w = rng.standard_normal(n).astype(np.float32)
+        exact = float(np.dot(a.astype(np.float64), w.astype(np.float64)))
+        bound = (n + 2) * eps * float(np.sum(np.abs(a.astype(np.float64) * w)))
+        assert abs(oracle.fma_accumulate(0.0, a, w) - exact) <= bound, n
+
+
+def test_should_parallelize_threshold():
+    L = oracle.lib()
+    # MatMulParallel.cs:32-39: rows > 1, dop > 1, rows * innerCost >= 65536
+    assert L.msor_should_parallelize(2, 32768, 8) == 1
+    assert L.msor_should_parallelize(2, 32767, 8) == 0
+    assert L.msor_should_parallelize(1, 1 << 20, 8) == 0
+    assert L.msor_should_parallelize(4096, 4096, 1) == 0
+
+
+# ---- against the reference's own native kernel ---------------------------------------------------
+def test_dequant_bit_exact_vs_reference_native(ref_vectors):
+    """One-hot activations make ms_qgemm_nbits return its dequantized weights."""
+    cases = [g for k, g in ref_vectors.items() if k.startswith("onehot")]
+    assert len(cases) == 4
+    for g in cases:
+        N, K, bits, bs = (int(x) for x in g["dims"])
+        w = oracle.dequant_weights(g["b"], g["scales"], g.get("zp"), N, K, bits, bs)
+        assert np.array_equal(w, g["w"]), (N, K, bits, bs)
+
+
+def test_matmul_vs_reference_native_grid(ref_vectors):
+    cases = [g for k, g in ref_vectors.items() if k.startswith("grid")]
+    assert len(cases) == 16
+    for g in cases:
+        M, N, K, bits, bs = (int(x) for x in g["dims"])
+        y = oracle.matmul_nbits(g["a"], g["b"], g["scales"], g.get("zp"), N, K, bits, bs)
+        ref = g["y"]
+        tol = 1e-5 * np.max(np.abs(ref), axis=1, keepdims=True)
+        assert np.all(np.abs(y - ref) <= tol), (M, N, K, bits, bs)
+
+
+def test_live_reference_native_when_built():
+    if oracle.ref_lib() is None:
+        pytest.skip("oracle/_ref not built (no reference checkout on this host)")
+    for (M, N, K, bs, zp, bits) in [(3, 70, 320, 32, True, 4), (5, 33, 4096, 128, False, 4), (2, 20, 192, 64, True, 8)]:
+        op = workloads.Op("live", K, N, bs, zp, 0.001, 0.01, bits)
+        b, s, z = workloads.make_weights(op, 77)
+        a = workloads.make_activations(M, K, 78)
+        ref = oracle.ref_qgemm_nbits(a, b, s, z, M, N, K, bits, bs)
+        y = oracle.matmul_nbits(a, b, s, z, N, K, bits, bs)
+        tol = 1e-5 * np.max(np.abs(ref), axis=1, keepdims=True)
+        assert np.all(np.abs(y - ref) <= tol)
+        eye = np.eye(K, dtype=np.float32)
+        w_ref = oracle.ref_qgemm_nbits(eye, b, s, z, K, N, K, bits, bs).T
+        assert np.array_equal(oracle.dequant_weights(b, s, z, N, K, bits, bs), w_ref)
+
+
+# ---- against a double-precision brute force ---------------------------------------------------
+@pytest.mark.parametrize("M,N,K,bs,zp", [(1, 96, 896, 32, True), (4, 64, 4096, 128, False), (7, 50, 200, 16, True)])
+def test_matmul_vs_f64(M, N, K, bs, zp):
+    op = workloads.Op("f64", K, N, bs, zp)
+    b, s, z = workloads.make_weights(op, 11)
+    a = workloads.make_activations(M, K, 12)
+    w = oracle.dequant_weights(b, s, z, N, K, 4, bs)
+    y = oracle.matmul_nbits(a, b, s, z, N, K, 4, bs)
+    y64 = oracle.matmul_f64(a, w)
+    eps = np.finfo(np.float32).eps
+    bound = (K + 2) * eps * (np.abs(a).astype(np.float64) @ np.abs(w).astype(np.float64).T)
+    assert np.all(np.abs(y - y64) <= bound)
+
+
+def test_matmul_f64_exact_integers():
+    rng = np.random.default_rng(3)
+    a = rng.integers(-8, 8, (3, 40)).astype(np.float32)
+    w = rng.integers(-8, 8, (5, 40)).astype(np.float32)
+    assert np.array_equal(oracle.matmul_f64(a, w), (a.astype(np.int64) @ w.astype(np.int64).T).astype(np.float64))
+
+
+def test_serial_reference_case_of_the_perf_test():
+    """MatMulParallelPerfTests.cs:72-140: M=32, K=256, N=512, bs=32, default zp,
+    scales 0.05 + 0.01*((n+blk)%7); serial scalar reference at abs 1e-3.
+    (The reference draws its codes and A from System.Random(99); here they come
+    from a seeded numpy generator.)"""
+    M, K, N, bs = 32, 256, 512, 32
+    nb = K // bs
+    rng = np.random.default_rng(99)
+    a = (rng.random((M, K)) * 2 - 1).astype(np.float32)
+    codes = rng.integers(0, 16, (N, K))
+    scales = np.array([0.05 + 0.01 * ((n + blk) % 7) for n in range(N) for blk in range(nb)], np.float32)
+    b = workloads.pack_nibbles(codes.reshape(N, nb, bs))
+    y = oracle.matmul_nbits(a, b, scales, None, N, K, 4, bs)
+    ref = np.zeros((M, N), np.float32)
+    w = ((codes.astype(np.float32) - np.float32(8)) * np.repeat(scales.reshape(N, nb), bs, axis=1)).astype(np.float32)
+    for m in range(M):
+        acc = np.zeros(N, np.float32)
+        for k in range(K):
+            acc = (acc + a[m, k] * w[:, k]).astype(np.float32)
+        ref[m] = acc
+    assert np.max(np.abs(y - ref)) <= 1e-3
+
+
+def test_threading_does_not_change_results():
+    op = workloads.Op("thr", 512, 300, 32, True)
+    b, s, z = workloads.make_weights(op, 21)
+    a = workloads.make_activations(3, op.K, 22)
+    y1 = oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, 32, nthreads=1)
+    y8 = oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, 32, nthreads=8)
+    assert np.array_equal(y1, y8)
