@@ -99,6 +99,21 @@ def time_graph(g, replays, warmup):
     return start.elapsed_time(end) / replays
 
 
+TRAFFIC_PROFILE = "profiles/gemv_w4_gate_7b_hbm_traffic.json"
+
+
+def measured_traffic(launch):
+    """HBM bytes per gate/up launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes (scaled by a plain copy's counters), used only when that
+    profile was taken on the kernel configuration this run launches."""
+    path = ROOT / TRAFFIC_PROFILE
+    if not path.is_file():
+        return None
+    prof = json.loads(path.read_text())
+    same = all(prof.get(k) == launch.get(k) for k in ("kernel", "lanes_per_row", "grid", "block"))
+    return prof["traffic_bytes"] if same else None
+
+
 def cpu_baseline(op, budget_s):
     import oracle
     from modelsharp_amd import workloads
@@ -139,6 +154,10 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget (0 = skip)")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--detail", default="", help="also write per-op results of every workload to this JSON file")
+    ap.add_argument("--op", default="", help="profiling mode: launch only this 7B decode op (q,k,v,o,gate,up,down), "
+                                             "eagerly over the rotation, then a plain copy of --copy-mib; no JSON line")
+    ap.add_argument("--calls", type=int, default=64, help="launches in --op mode")
+    ap.add_argument("--copy-mib", type=int, default=256, help="size of the calibration copy in --op mode")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -157,6 +176,8 @@ def main() -> int:
         raise SystemExit("no gfx950 device: " + native.last_error())
     torch.cuda.set_device(0)
     log(f"device: {native.device_name()}")
+    if args.op:
+        return profile_op(args)
 
     # ---- 7B decode layer, M=1 -------------------------------------------------------------
     ops = workloads.DECODE_7B
@@ -205,6 +226,7 @@ def main() -> int:
     gate = next(op for op in ops if op.name == "gate")
     gate_bytes = workloads.algorithmic_bytes(gate, 1)
     gate_gbs = per_op["gate"]["GBs"]
+    traffic = measured_traffic(per_op["gate"]["kernel"])
     rot.close()
     del rot, g
     torch.cuda.empty_cache()
@@ -220,7 +242,8 @@ def main() -> int:
         "per_op": per_op,
         "roofline": {"bound": "hbm", "kernel": "gemv_w4 gate/up (K=3584, N=18944, M=1)",
                      "achieved": gate_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gate_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gate_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": TRAFFIC_PROFILE if traffic else None,
                      "algorithmic_bytes_per_launch": gate_bytes},
     }
 
@@ -258,6 +281,32 @@ def main() -> int:
         result["cpu_baseline"] = None
 
     print(json.dumps(result), flush=True)
+    return 0
+
+
+def profile_op(args) -> int:
+    """Eager launches of one decode op over the rotation (for per-dispatch
+    hardware counters), then a device-to-device copy of known size whose
+    counters calibrate the byte counts."""
+    import torch
+    from modelsharp_amd import workloads
+    op = next(o for o in workloads.DECODE_7B if o.name == args.op)
+    fp = workloads.algorithmic_bytes(op, 1)
+    copies = workloads.rotation_copies(fp, args.rotate_mib << 20)
+    rot = Rotation([op], 1, copies, seed=7)
+    stream = torch.cuda.current_stream().cuda_stream
+    for i in range(args.calls):
+        rot.enqueue(i % copies, stream)
+    torch.cuda.synchronize()
+    log(f"{args.calls} launches of {op.name} (K={op.K}, N={op.N}, {fp} algorithmic bytes each), "
+        f"{copies} rotating copies")
+    src = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"4 copies of {args.copy_mib << 20} bytes (read {args.copy_mib << 20}, write {args.copy_mib << 20} each)")
+    rot.close()
     return 0
 
 

@@ -5,16 +5,27 @@
 //     n; the G lanes of a row split that row's K into 32-code chunks (one
 //     16-byte load each) taken round-robin, so one wave-wide load reads R
 //     contiguous segments of G*16 bytes of packed B in the reference layout
-//     B[n][K/2] (G >= 8 makes every segment a whole 128-byte line).
-//   * The activation slice A[0..M)[panel] is staged once per workgroup in LDS
-//     (a chunk is 32 floats padded to 36 so the G distinct chunk addresses of
-//     one wave-wide read fall on different banks); lanes with the same chunk
-//     index read the same address (broadcast).
-//   * Per chunk: one dwordx4 load of codes, one scale, one zero-point nibble;
-//     32 exact dequants W = (q - zp) * s (nbits_device.h), then M fp32 FMAs
-//     per dequantized weight. The dequant is shared by all M rows.
+//     B[n][K/2]. Codes, scales and zero points are read with buffer loads
+//     (32-bit offsets off one scalar resource each).
+//   * The activation slice A[0..M)[panel] is staged once per workgroup in LDS:
+//     a chunk is 32 activations, pre-scaled as below, plus their plain sum in a
+//     ninth float4 (which also pads the chunk stride so that the G distinct
+//     chunk addresses of one wave-wide read fall on different banks). Lanes
+//     with the same chunk index read the same address.
+//   * Weight loads are software-pipelined in two ping-pong batches of U chunks:
+//     one batch is in flight while the other is reduced. The first batch is
+//     issued before A is staged, so the two latencies overlap.
 //   * End: the G partial sums of a row are combined with a butterfly over the
-//     G lanes (fixed order: deterministic), lane 0 of the row stores Y.
+//     G lanes (fixed order: deterministic); lane 0 of the row stores Y.
+// Arithmetic per chunk (32 codes q_k, zero point zp, scale s):
+//   A code in the low mantissa bits of an fp16 lane is the exact subnormal
+//   q * 2^-24 (code bits 0-3) or 16q * 2^-24 (bits 4-7). With the activations
+//   staged times 2^24 (even k) and 2^20 (odd k) — exact powers of two — one
+//   v_fma_mix_f32 adds exactly a_k * q_k. Per row m,
+//       blk = sum_k a_k q_k - zp * sum_k a_k,   acc += s * blk,
+//   i.e. sum_k a_k (q_k - zp) s: the dot product with the dequantized weights
+//   W = (q - zp) s, folded per block. The code masks (5 ops per 8 codes) are
+//   shared by the M rows; each row costs one fma per code plus two per chunk.
 // HBM traffic is the algorithmic minimum: every byte of B, scales and zero
 // points is read once; A is read once per workgroup (L2-resident).
 #pragma once
@@ -28,7 +39,7 @@ struct GemvParams {
     const uint8_t* zp;       // [N][zrb] packed nibbles, or nullptr (zp = 8)
     const float* a;          // [M][K]
     float* y;                // [M][N]
-    int64_t row_bytes;       // nb * block_size / 2
+    int row_bytes;           // nb * block_size / 2
     int N, K;
     int C;                   // K / 32 chunks per row
     int log2cpb;             // log2(block_size / 32)
@@ -37,13 +48,34 @@ struct GemvParams {
 };
 
 constexpr int kGemvThreads = 256;
-constexpr int kChunkStride4 = 9;   // float4 per staged chunk (8 + 1 pad)
+constexpr int kChunkStride4 = 9;   // float4 per staged chunk: 8 activations + (sum, 0, 0, 0)
+constexpr int kGemvU = 4;          // chunks per lane per pipeline batch
+// acc + sum of a_k q_k over the 8 codes of one dword, a0 = a'[k0..k3],
+// a1 = a'[k4..k7] staged pre-scaled.
+__device__ __forceinline__ float qdot8(const uint32_t (&p)[4], const float4& a0, const float4& a1, float acc)
+{
+    acc = mix_lo_acc(p[0], a0.x, acc);
+    acc = mix_lo_acc(p[1], a0.y, acc);
+    acc = mix_lo_acc(p[2], a0.z, acc);
+    acc = mix_lo_acc(p[3], a0.w, acc);
+    acc = mix_hi_acc(p[0], a1.x, acc);
+    acc = mix_hi_acc(p[1], a1.y, acc);
+    acc = mix_hi_acc(p[2], a1.z, acc);
+    acc = mix_hi_acc(p[3], a1.w, acc);
+    return acc;
+}
+
+struct ChunkBatch {
+    u32x4_t q[kGemvU];
+    float s[kGemvU];
+    int z[kGemvU];    // zero-point byte (both nibbles); the block's nibble is picked at use
+};
 
 template <int M, int G>
 __global__ __launch_bounds__(kGemvThreads) void gemv_w4_kernel(GemvParams p)
 {
     constexpr int R = kWave / G;   // rows per wave
-    constexpr int U = 4;           // chunks per lane in flight
+    constexpr int U = kGemvU;
     extern __shared__ float4 lds_a4[];   // [M][panel_chunks][kChunkStride4]
 
     const int lane = threadIdx.x & (kWave - 1);
@@ -54,9 +86,13 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_w4_kernel(GemvParams p)
     const bool row_ok = n < p.N;
     const int nl = row_ok ? n : p.N - 1;   // clamped row for loads
 
-    const uint8_t* brow = p.b + (int64_t)nl * p.row_bytes;
-    const float* srow = p.scales + (int64_t)nl * p.nb;
-    const uint8_t* zrow = p.zp ? p.zp + (int64_t)nl * p.zrb : nullptr;
+    const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(p.b, p.N * p.row_bytes);
+    const __amdgpu_buffer_rsrc_t rsc = buffer_rsrc(p.scales, p.N * p.nb * 4);
+    const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(p.zp ? (const void*)p.zp : (const void*)p.scales,
+                                                  p.zp ? p.N * p.zrb : 0);
+    const int boff = nl * p.row_bytes;
+    const int soff = nl * p.nb * 4;
+    const int zoff = nl * p.zrb;
 
     float acc[M];
 #pragma unroll
@@ -65,60 +101,72 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_w4_kernel(GemvParams p)
     const int P = p.panel_chunks;
     for (int c0 = 0; c0 < p.C; c0 += P) {
         const int pc = min(P, p.C - c0);
-        // ---- stage A[:, c0*32 .. (c0+pc)*32) into LDS --------------------------------
+        // ---- this lane's chunks of the panel: cc = g + G*k, k < nk -----------------------
+        const int nk = g < pc ? (pc - g + G - 1) / G : 0;
+        auto load = [&](ChunkBatch& bt, int k0) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int k = k0 + u;
+                const int c = c0 + (k < nk ? g + G * k : 0);
+                const int blk = c >> p.log2cpb;
+                bt.q[u] = __builtin_amdgcn_raw_buffer_load_b128(rb, boff + c * 16, 0, 0);
+                bt.s[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc, soff + blk * 4, 0, 0));
+                bt.z[u] = p.zp ? (int)__builtin_amdgcn_raw_buffer_load_b8(rz, zoff + (blk >> 1), 0, 0) : 0x88;
+            }
+        };
+        ChunkBatch b0, b1;
+        load(b0, 0);
+
+        // ---- stage A[:, c0*32 .. (c0+pc)*32): one thread per (row, chunk) ----------------
         __syncthreads();
-        const int per_row = pc * 8;   // float4 per A row in this panel
-        for (int idx = threadIdx.x; idx < M * per_row; idx += kGemvThreads) {
-            const int m = idx / per_row;
-            const int rem = idx - m * per_row;
-            const int cc = rem >> 3;
-            const int q4 = rem & 7;
-            const float4 v = *reinterpret_cast<const float4*>(
-                p.a + (int64_t)m * p.K + (int64_t)(c0 + cc) * 32 + q4 * 4);
-            lds_a4[(m * P + cc) * kChunkStride4 + q4] = v;
+        for (int idx = threadIdx.x; idx < M * pc; idx += kGemvThreads) {
+            const int m = idx / pc;
+            const int cc = idx - m * pc;
+            const float4* src = reinterpret_cast<const float4*>(p.a + (int64_t)m * p.K + (int64_t)(c0 + cc) * 32);
+            float4* dst = &lds_a4[(m * P + cc) * kChunkStride4];
+            float sum = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float4 v = src[j];
+                sum += v.x;
+                sum += v.y;
+                sum += v.z;
+                sum += v.w;
+                dst[j] = float4{v.x * kTwo24, v.y * kTwo20, v.z * kTwo24, v.w * kTwo20};
+            }
+            dst[8] = float4{sum, 0.0f, 0.0f, 0.0f};
         }
         __syncthreads();
 
-        // ---- stream this row's chunks of the panel, U at a time ------------------------
-        for (int base = 0; base < pc; base += G * U) {
-            uint4 q[U];
-            float s[U];
-            int z[U];
+        auto reduce = [&](const ChunkBatch& bt, int k0) {
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const int cc = base + u * G + g;
-                const int c = c0 + (cc < pc ? cc : 0);
-                const int blk = c >> p.log2cpb;
-                q[u] = *reinterpret_cast<const uint4*>(brow + (int64_t)c * 16);
-                s[u] = srow[blk];
-                z[u] = zrow ? zp_nibble(zrow, blk) : 8;
-            }
+                if (k0 + u < nk) {
+                    const int cc = g + G * (k0 + u);
+                    const int blk = (c0 + cc) >> p.log2cpb;
+                    const float zpf = (float)((bt.z[u] >> ((blk & 1) * 4)) & 0x0F);
+                    const uint32_t qd[4] = {bt.q[u].x, bt.q[u].y, bt.q[u].z, bt.q[u].w};
+                    uint32_t pr[4][4];
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int cc = base + u * G + g;
-                if (cc < pc) {
-                    const BlockDq dq = block_dq(z[u], s[u]);
-                    const uint32_t qd[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+                    for (int j = 0; j < 4; ++j) code_pairs(qd[j], pr[j]);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        float w[8];
-                        dequant8(qd[j], dq, w);
+                    for (int m = 0; m < M; ++m) {
+                        const float4* arow = &lds_a4[(m * P + cc) * kChunkStride4];
+                        float blkacc = 0.0f;
 #pragma unroll
-                        for (int m = 0; m < M; ++m) {
-                            const float4 a0 = lds_a4[(m * P + cc) * kChunkStride4 + 2 * j];
-                            const float4 a1 = lds_a4[(m * P + cc) * kChunkStride4 + 2 * j + 1];
-                            acc[m] = __builtin_fmaf(a0.x, w[0], acc[m]);
-                            acc[m] = __builtin_fmaf(a0.y, w[1], acc[m]);
-                            acc[m] = __builtin_fmaf(a0.z, w[2], acc[m]);
-                            acc[m] = __builtin_fmaf(a0.w, w[3], acc[m]);
-                            acc[m] = __builtin_fmaf(a1.x, w[4], acc[m]);
-                            acc[m] = __builtin_fmaf(a1.y, w[5], acc[m]);
-                            acc[m] = __builtin_fmaf(a1.z, w[6], acc[m]);
-                            acc[m] = __builtin_fmaf(a1.w, w[7], acc[m]);
-                        }
+                        for (int j = 0; j < 4; ++j) blkacc = qdot8(pr[j], arow[2 * j], arow[2 * j + 1], blkacc);
+                        blkacc = __builtin_fmaf(-zpf, arow[8].x, blkacc);
+                        acc[m] = __builtin_fmaf(bt.s[u], blkacc, acc[m]);
                     }
                 }
             }
+        };
+        for (int k0 = 0; k0 < nk; k0 += 2 * U) {
+            if (k0 + U < nk) load(b1, k0 + U);
+            reduce(b0, k0);
+            if (k0 + U >= nk) break;
+            if (k0 + 2 * U < nk) load(b0, k0 + 2 * U);
+            reduce(b1, k0 + U);
         }
     }
 

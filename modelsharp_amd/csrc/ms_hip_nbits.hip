@@ -2,8 +2,10 @@
 //
 // Weights handles hold B, scales and packed zero points resident in HBM in the
 // operator's own layout (uploaded once per initializer); each call dispatches
-//   M <= 16, bits=4, block_size in {32,64,128,256}, K % 32 == 0 -> gemv_w4
-//   M >  16, same conditions                                   -> mfma_w4
+//   M == 1, bits=4, block_size in {32,64,128,256}, K % 32 == 0,
+//           K >= 1536                                            -> gemv_w4_m1
+//   M <= 16, same conditions                                    -> gemv_w4
+//   M >  16, same conditions                                    -> mfma_w4
 //   anything else                                              -> generic
 // Declarations and reference citations: include/ms_hip_kernels.h.
 #include "../../include/ms_hip_kernels.h"
@@ -11,6 +13,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <climits>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -18,6 +21,7 @@
 #include <string>
 
 #include "gemv_w4.h"
+#include "gemv_w4_m1.h"
 #include "generic_nbits.h"
 #include "mfma_w4.h"
 
@@ -126,7 +130,9 @@ void derive_layout(Weights& w, int N, int K, int bits, int bs)
     w.zrb = (w.nb * bits + 7) / 8;
     w.row_bytes = (int64_t)w.nb * w.blob;
     w.fast = 0;
-    if (bits == 4 && (K % 32) == 0 && (bs == 32 || bs == 64 || bs == 128 || bs == 256)) {
+    // The fast kernels address B, scales and zero points with 32-bit buffer offsets.
+    const bool fits = (int64_t)N * w.row_bytes <= INT32_MAX && (int64_t)N * w.nb * 4 <= INT32_MAX;
+    if (bits == 4 && fits && (K % 32) == 0 && (bs == 32 || bs == 64 || bs == 128 || bs == 256)) {
         w.fast = 1;
         w.log2cpb = bs == 32 ? 0 : bs == 64 ? 1 : bs == 128 ? 2 : 3;
     }
@@ -163,27 +169,35 @@ void free_weights(Weights& w)
 }
 
 // ---- GEMV launch shape --------------------------------------------------------------------
-int g_gemv_lanes_override = 0;
+// Tuning knobs (ms_hip_set_tuning); 0 = the shape heuristics below.
+int g_gemv_lanes_override = 0;   // knob 0: gemv_w4 lanes per row
+int g_m1_enable = 0;             // knob 1: 1 use gemv_w4_m1 for M == 1, 0 never (default: gemv_w4 measures faster)
+int g_m1_rows = 0;               // knob 2: gemv_w4_m1 rows per step (1, 2, 4, 8)
+int g_m1_steps = 0;              // knob 3: gemv_w4_m1 row steps per wave
+int g_m1_slices = 0;             // knob 4: gemv_w4_m1 K slices (1..8)
 
 constexpr int kLaneChoices[5] = {4, 8, 16, 32, 64};
 
-// Lanes per row G: enough waves to cover the chip (~2048 waves = 8 per CU) while
-// wasting as few lane-steps as possible on the row's chunk count C; among equal
-// choices prefer G >= 8 (whole 128-byte lines per row per load).
+// Lanes per row G (measured on MI355X over the decode workloads): score =
+// lane efficiency on the row's C chunks x wave fill (>= 1024 waves) x a
+// preference for 16-32 lanes (whole 256-512 B segments per row per load) x a
+// penalty when a lane owns fewer than 3 chunks (per-wave costs not amortised);
+// ties go to the larger G.
 int pick_gemv_lanes(int N, int C)
 {
     if (g_gemv_lanes_override) return g_gemv_lanes_override;
     double best = -1.0;
-    int best_g = 8;
+    int best_g = 16;
     for (int G : kLaneChoices) {
         const int R = kWave / G;
         const double waves = (double)((N + R - 1) / R);
         const int steps = (C + G - 1) / G;
         const double eff = (double)C / (double)(steps * G);
-        const double fill = std::min(1.0, waves / 2048.0);
-        double score = eff * fill;
-        if (G < 8) score *= 0.97;
-        if (score > best + 1e-9) {
+        const double fill = std::min(1.0, waves / 1024.0);
+        const double pref = G == 4 ? 0.80 : G == 8 ? 0.93 : G == 64 ? 0.95 : 1.0;
+        const double per_lane = (double)C / G < 3.0 ? 0.85 : 1.0;
+        const double score = eff * fill * pref * per_lane;
+        if (score >= best - 1e-9) {
             best = score;
             best_g = G;
         }
@@ -257,8 +271,97 @@ GemvShape gemv_shape(const Weights& w, int M)
     return s;
 }
 
+struct M1Shape {
+    int ok = 0;
+    int yt, T, kw, rs, steps, grid, block;
+    size_t lds;
+};
+
+// gemv_w4_m1: K slices so every lane owns at most 2 chunks with the fewest idle
+// lane-chunks; ~2560 waves in flight (10 per CU) across row steps.
+M1Shape m1_shape(const Weights& w)
+{
+    M1Shape s;
+    const int C = w.K / 32;
+    if (!g_m1_enable || C < 48) return s;
+    int best_kw = 0, best_T = 0;
+    double best_eff = -1.0;
+    for (int kw = 1; kw <= 8; ++kw) {
+        if (g_m1_slices && kw != g_m1_slices) continue;
+        const int cs = (C + kw - 1) / kw;
+        const int T = (cs + kWave - 1) / kWave;
+        if (T > 2) continue;
+        const double eff = (double)C / (double)(kw * kWave * T);
+        if (eff > best_eff + 1e-9) {
+            best_eff = eff;
+            best_kw = kw;
+            best_T = T;
+        }
+    }
+    if (!best_kw) return s;
+    s.kw = best_kw;
+    s.T = best_T;
+    s.rs = std::max(1, 4 / s.kw);
+    s.yt = g_m1_rows ? g_m1_rows : (w.N >= 8192 ? 4 : 2);
+    if (s.T == 2 && s.yt > 4) s.yt = 4;
+    s.steps = g_m1_steps ? g_m1_steps
+                         : std::max(1, (int)std::lround((double)s.kw * w.N / (s.yt * 2560.0)));
+    const int rows_per_block = s.rs * s.yt * s.steps;
+    s.grid = (w.N + rows_per_block - 1) / rows_per_block;
+    s.block = kWave * s.kw * s.rs;
+    s.lds = s.kw > 1 ? (size_t)rows_per_block * s.kw * sizeof(float) : 0;
+    s.ok = s.block <= 512 && s.lds <= 64 * 1024;
+    return s;
+}
+
+typedef void (*GemvM1Fn)(GemvM1Params);
+
+GemvM1Fn gemv_m1_kernel(int yt, int T)
+{
+    if (T == 1) {
+        switch (yt) {
+            case 1: return gemv_w4_m1_kernel<1, 1>;
+            case 2: return gemv_w4_m1_kernel<2, 1>;
+            case 8: return gemv_w4_m1_kernel<8, 1>;
+            default: return gemv_w4_m1_kernel<4, 1>;
+        }
+    }
+    switch (yt) {
+        case 1: return gemv_w4_m1_kernel<1, 2>;
+        case 2: return gemv_w4_m1_kernel<2, 2>;
+        default: return gemv_w4_m1_kernel<4, 2>;   // 8 rows x 2 chunks exceeds the VGPR file
+    }
+}
+
+int launch_gemv_m1(const Weights& w, const M1Shape& s, const float* dA, float* dY, hipStream_t stream)
+{
+    GemvM1Params p;
+    p.b = w.d_b;
+    p.scales = w.d_scales;
+    p.zp = w.has_zp ? w.d_zp : nullptr;
+    p.a = dA;
+    p.y = dY;
+    p.row_bytes = w.row_bytes;
+    p.N = w.N;
+    p.K = w.K;
+    p.C = w.K / 32;
+    p.log2cpb = w.log2cpb;
+    p.nb = w.nb;
+    p.zrb = w.zrb;
+    p.kw = s.kw;
+    p.rs = s.rs;
+    p.steps = s.steps;
+    hipLaunchKernelGGL(gemv_m1_kernel(s.yt, s.T), dim3(s.grid), dim3(s.block), s.lds, stream, p);
+    MS_HIP_CHECK(hipGetLastError());
+    return MS_HIP_OK;
+}
+
 int launch_gemv(const Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
 {
+    if (M == 1) {
+        const M1Shape s1 = m1_shape(w);
+        if (s1.ok) return launch_gemv_m1(w, s1, dA, dY, stream);
+    }
     const GemvShape s = gemv_shape(w, M);
     GemvParams p;
     p.b = w.d_b;
@@ -266,7 +369,7 @@ int launch_gemv(const Weights& w, const float* dA, float* dY, int M, hipStream_t
     p.zp = w.has_zp ? w.d_zp : nullptr;
     p.a = dA;
     p.y = dY;
-    p.row_bytes = w.row_bytes;
+    p.row_bytes = (int)w.row_bytes;
     p.N = w.N;
     p.K = w.K;
     p.C = w.K / 32;
@@ -619,6 +722,28 @@ int ms_hip_set_gemv_lanes(int lanes_per_row)
     return MS_HIP_OK;
 }
 
+int ms_hip_set_tuning(int knob, int value)
+{
+    switch (knob) {
+        case 0: return ms_hip_set_gemv_lanes(value);
+        case 1: g_m1_enable = value ? 1 : 0; return MS_HIP_OK;
+        case 2:
+            if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8) break;
+            g_m1_rows = value;
+            return MS_HIP_OK;
+        case 3:
+            if (value < 0 || value > 64) break;
+            g_m1_steps = value;
+            return MS_HIP_OK;
+        case 4:
+            if (value < 0 || value > 8) break;
+            g_m1_slices = value;
+            return MS_HIP_OK;
+        default: break;
+    }
+    return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid tuning knob %d = %d", knob, value);
+}
+
 int ms_hip_nbits_launch_info(void* handle, int M, int* kernel_id, int* lanes_per_row, int* grid, int* block)
 {
     Weights* w = from_handle(handle);
@@ -629,6 +754,12 @@ int ms_hip_nbits_launch_info(void* handle, int M, int* kernel_id, int* lanes_per
         kid = 0;
         gr = (int)(((int64_t)M * w->N + 255) / 256);
         bl = 256;
+    } else if (M == 1 && m1_shape(*w).ok) {
+        const M1Shape s = m1_shape(*w);
+        kid = 3;
+        G = kWave;
+        gr = s.grid;
+        bl = s.block;
     } else if (M <= kGemvMaxM) {
         const GemvShape s = gemv_shape(*w, M);
         kid = 1;

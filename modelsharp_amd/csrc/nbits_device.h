@@ -91,6 +91,81 @@ __device__ __forceinline__ void dequant8(uint32_t x, const BlockDq& q, float (&w
     w[7] = mix_hi(d3, q.s16, nz);
 }
 
+// acc + (float)h * a for the low / high fp16 lane of h2: an fp32 fma of the
+// widened half (exact) — selected as one v_fma_mix_f32. Written in C++, not
+// asm, so the scheduler can hoist the activation loads feeding it.
+__device__ __forceinline__ float fmac_lo(uint32_t h2, float a, float acc)
+{
+    return __builtin_fmaf((float)as_h2(h2).x, a, acc);
+}
+__device__ __forceinline__ float fmac_hi(uint32_t h2, float a, float acc)
+{
+    return __builtin_fmaf((float)as_h2(h2).y, a, acc);
+}
+
+// The exact differences of one dword of codes as four fp16 pairs:
+// d[0] = (k0, k4), d[1] = 16*(k1, k5), d[2] = (k2, k6), d[3] = 16*(k3, k7),
+// each k standing for q_k - zp. 9 VALU ops.
+__device__ __forceinline__ void diffs8(uint32_t x, h2_t zb, h2_t zb16, uint32_t (&d)[4])
+{
+    const uint32_t magic = kHalfMagic;
+    const uint32_t x8 = x >> 8;
+    d[0] = as_u32(as_h2(and_or(x, 0x000F000Fu, magic)) - zb);
+    d[1] = as_u32(as_h2(and_or(x, 0x00F000F0u, magic)) - zb16);
+    d[2] = as_u32(as_h2(and_or(x8, 0x000F000Fu, magic)) - zb);
+    d[3] = as_u32(as_h2(and_or(x8, 0x00F000F0u, magic)) - zb16);
+}
+
+// acc + sum_i (q_i - zp) * a_i over the 8 codes whose diffs8() are d, with the
+// activations a0 = a[k0..k3], a1 = a[k4..k7] staged with the odd k pre-divided
+// by 16 (exact: a power of two), which cancels the 16 in d[1], d[3]. Every
+// product is exact inside the fma; one rounding per accumulation.
+__device__ __forceinline__ float dot8(const uint32_t (&d)[4], const float4& a0, const float4& a1, float acc)
+{
+    acc = fmac_lo(d[0], a0.x, acc);
+    acc = fmac_lo(d[1], a0.y, acc);
+    acc = fmac_lo(d[2], a0.z, acc);
+    acc = fmac_lo(d[3], a0.w, acc);
+    acc = fmac_hi(d[0], a1.x, acc);
+    acc = fmac_hi(d[1], a1.y, acc);
+    acc = fmac_hi(d[2], a1.z, acc);
+    acc = fmac_hi(d[3], a1.w, acc);
+    return acc;
+}
+
+// ---- shared by the GEMV kernels ---------------------------------------------------
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+constexpr uint32_t kBufferWord3 = 0x00020000u;   // raw buffer resource, gfx9 data format
+constexpr float kTwo24 = 16777216.0f;            // 2^24
+constexpr float kTwo20 = 1048576.0f;             // 2^20
+
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, (int)kBufferWord3);
+}
+
+// acc + a * (fp16 lane widened) — one v_fma_mix_f32.
+__device__ __forceinline__ float mix_lo_acc(uint32_t h2, float a, float acc)
+{
+    return __builtin_fmaf((float)as_h2(h2).x, a, acc);
+}
+__device__ __forceinline__ float mix_hi_acc(uint32_t h2, float a, float acc)
+{
+    return __builtin_fmaf((float)as_h2(h2).y, a, acc);
+}
+
+// The four masked code pairs of dword x: p[0] = (k0, k4) and p[2] = (k2, k6) as
+// q * 2^-24, p[1] = (k1, k5) and p[3] = (k3, k7) as 16 q * 2^-24.
+__device__ __forceinline__ void code_pairs(uint32_t x, uint32_t (&p)[4])
+{
+    const uint32_t x8 = x >> 8;
+    p[0] = x & 0x000F000Fu;
+    p[1] = x & 0x00F000F0u;
+    p[2] = x8 & 0x000F000Fu;
+    p[3] = x8 & 0x00F000F0u;
+}
+
 // Packed zero point of block `blk` from a row of packed nibbles
 // (MatMulNBitsKernel.cs:349-356 with bits=4).
 __device__ __forceinline__ int zp_nibble(const uint8_t* zrow, int blk)

@@ -58,6 +58,7 @@ _PROTOTYPES = {
     "ms_hip_download": (_c_int, [_vp, _vp, _c_i64]),
     "ms_hip_sync": (_c_int, []),
     "ms_hip_set_gemv_lanes": (_c_int, [_c_int]),
+    "ms_hip_set_tuning": (_c_int, [_c_int, _c_int]),
     "ms_hip_nbits_launch_info": (_c_int, [_vp, _c_int, _ip, _ip, _ip, _ip]),
 }
 
@@ -192,7 +193,7 @@ class NBitsWeights:
         k, g, gr, bl = (ctypes.c_int() for _ in range(4))
         check(load().ms_hip_nbits_launch_info(self.handle, int(M), ctypes.byref(k), ctypes.byref(g),
                                               ctypes.byref(gr), ctypes.byref(bl)))
-        return {"kernel": ("generic", "gemv_w4", "mfma_w4")[k.value], "lanes_per_row": g.value,
+        return {"kernel": ("generic", "gemv_w4", "mfma_w4", "gemv_w4_m1")[k.value], "lanes_per_row": g.value,
                 "grid": gr.value, "block": bl.value}
 
     def close(self) -> None:
@@ -218,6 +219,11 @@ def gemm_dev_batch(weights: list, dA: list[int], dY: list[int], M: int, stream: 
 
 def set_gemv_lanes(lanes: int) -> None:
     check(load().ms_hip_set_gemv_lanes(int(lanes)))
+
+
+def set_tuning(knob: int, value: int) -> None:
+    """Launch-shape knobs for sweeps (include/ms_hip_kernels.h); 0 restores the heuristic."""
+    check(load().ms_hip_set_tuning(int(knob), int(value)))
 
 
 def qgemm_nbits(a, b, scales, zero_points, M, N, K, bits, block_size) -> np.ndarray:
