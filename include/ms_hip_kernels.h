@@ -118,13 +118,14 @@ int ms_hip_sync(void);
 
 /* ---- measurement support ---------------------------------------------------
  * No counterpart in the reference; for launch-shape sweeps. Process-wide.
- * ms_hip_set_gemv_lanes: lanes per weight row of the M<=16 GEMV (4, 8, 16,
- *   32 or 64; 0 restores the shape heuristic) — the same as knob 0 below.
+ * ms_hip_set_gemv_lanes: lanes per weight row of the gemv_w4_panel kernel
+ *   (16, 32 or 64; 0 restores the shape heuristic) — the same as knob 0 below.
  * ms_hip_set_tuning knobs (value 0 restores the heuristic):
- *   0 GEMV lanes per row, 1 use the M=1 GEMV (1) or not (0, default), 2 M=1 rows per
- *   step (1,2,4,8), 3 M=1 row steps per wave, 4 M=1 K slices (1..8).
+ *   0 gemv_w4_panel lanes per row;
+ *   1 gemv_w4 launch configuration: c+1 forces configuration c of the library's
+ *     table (used only where it fits the shape), -1 forces gemv_w4_panel.
  * ms_hip_nbits_launch_info reports what a call with M rows would launch:
- *   kernel_id 0 generic, 1 gemv_w4, 2 mfma_w4, 3 gemv_w4_m1. */
+ *   kernel_id 0 generic, 1 gemv_w4, 2 mfma_w4, 3 gemv_w4_panel. */
 int ms_hip_set_gemv_lanes(int lanes_per_row);
 int ms_hip_set_tuning(int knob, int value);
 int ms_hip_nbits_launch_info(void* handle, int M, int* kernel_id, int* lanes_per_row,

@@ -2,10 +2,10 @@
 //
 // Weights handles hold B, scales and packed zero points resident in HBM in the
 // operator's own layout (uploaded once per initializer); each call dispatches
-//   M == 1, bits=4, block_size in {32,64,128,256}, K % 32 == 0,
-//           K >= 1536                                            -> gemv_w4_m1
-//   M <= 16, same conditions                                    -> gemv_w4
-//   M >  16, same conditions                                    -> mfma_w4
+//   bits=4, block_size in {32,64,128,256}, K % 32 == 0 ("fast" layouts):
+//     M <= 4, block_size 32 or 128, M*K/32 <= 1024              -> gemv_w4
+//     M <= 16 otherwise                                         -> gemv_w4_panel
+//     M >  16                                                   -> mfma_w4
 //   anything else                                              -> generic
 // Declarations and reference citations: include/ms_hip_kernels.h.
 #include "../../include/ms_hip_kernels.h"
@@ -13,6 +13,10 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
+#include <atomic>
+#include <cmath>
+#include <utility>
 #include <climits>
 #include <cstdarg>
 #include <cstdio>
@@ -21,7 +25,7 @@
 #include <string>
 
 #include "gemv_w4.h"
-#include "gemv_w4_m1.h"
+#include "gemv_w4_panel.h"
 #include "generic_nbits.h"
 #include "mfma_w4.h"
 
@@ -170,33 +174,128 @@ void free_weights(Weights& w)
 
 // ---- GEMV launch shape --------------------------------------------------------------------
 // Tuning knobs (ms_hip_set_tuning); 0 = the shape heuristics below.
-int g_gemv_lanes_override = 0;   // knob 0: gemv_w4 lanes per row
-int g_m1_enable = 0;             // knob 1: 1 use gemv_w4_m1 for M == 1, 0 never (default: gemv_w4 measures faster)
-int g_m1_rows = 0;               // knob 2: gemv_w4_m1 rows per step (1, 2, 4, 8)
-int g_m1_steps = 0;              // knob 3: gemv_w4_m1 row steps per wave
-int g_m1_slices = 0;             // knob 4: gemv_w4_m1 K slices (1..8)
+int g_panel_lanes_override = 0;  // knob 0: gemv_w4_panel lanes per row
+int g_gemv_config = 0;           // knob 1: c+1 forces kGemvConfigs[c], -1 forces gemv_w4_panel
 
-constexpr int kLaneChoices[5] = {4, 8, 16, 32, 64};
-
-// Lanes per row G (measured on MI355X over the decode workloads): score =
-// lane efficiency on the row's C chunks x wave fill (>= 1024 waves) x a
-// preference for 16-32 lanes (whole 256-512 B segments per row per load) x a
-// penalty when a lane owns fewer than 3 chunks (per-wave costs not amortised);
-// ties go to the larger G.
-int pick_gemv_lanes(int N, int C)
+// gemv_w4 instantiations: [M-1][L slot][config], L slot 0 = block size 32, 1 = block size 128.
+typedef void (*GemvFn)(GemvParams);
+template <int M, int L, size_t I>
+constexpr GemvFn gemv_fn_at()
 {
-    if (g_gemv_lanes_override) return g_gemv_lanes_override;
+    constexpr GemvConfig c = kGemvConfigs[I];
+    return gemv_w4_kernel<M, c.G, c.KW, c.U, L, c.waves>;
+}
+template <int M, int L, size_t... I>
+constexpr std::array<GemvFn, sizeof...(I)> gemv_row(std::index_sequence<I...>)
+{
+    return {gemv_fn_at<M, L, I>()...};
+}
+template <int M, int L>
+constexpr std::array<GemvFn, kNumGemvConfigs> gemv_row()
+{
+    return gemv_row<M, L>(std::make_index_sequence<kNumGemvConfigs>{});
+}
+const std::array<GemvFn, kNumGemvConfigs> kGemvTable[kGemvMaxM][2] = {
+    {gemv_row<1, 0>(), gemv_row<1, 2>()},
+    {gemv_row<2, 0>(), gemv_row<2, 2>()},
+    {gemv_row<3, 0>(), gemv_row<3, 2>()},
+    {gemv_row<4, 0>(), gemv_row<4, 2>()},
+};
+std::atomic<bool> g_gemv_lds_raised[kGemvMaxM][2][kNumGemvConfigs];
+
+int l_slot(const Weights& w) { return w.log2cpb == 0 ? 0 : w.log2cpb == 2 ? 1 : -1; }
+
+// gemv_w4 takes M <= 4, block size 32 or 128, and A panels that one thread per
+// chunk stages in LDS (M * C <= 64 * waves).
+bool gemv_config_fits(const Weights& w, int M, const GemvConfig& c)
+{
+    return M <= kGemvMaxM && l_slot(w) >= 0 && M * (w.K / 32) <= 64 * c.waves;
+}
+
+// Config choice (measured on MI355X over the decode workloads): score = lane
+// efficiency on the row's C chunks x wave fill (>= 2048 waves) x CU balance of
+// the grid x a small penalty when a lane has a single step; ties go to the
+// lower index.
+int pick_gemv_config(const Weights& w, int M)
+{
+    if (g_gemv_config < 0) return -1;
+    if (g_gemv_config > 0) {
+        const int ci = g_gemv_config - 1;
+        return gemv_config_fits(w, M, kGemvConfigs[ci]) ? ci : -1;
+    }
+    const int C = w.K / 32;
+    int best = -1;
+    double best_score = 0.0;
+    for (int ci = 0; ci < kNumGemvConfigs; ++ci) {
+        const GemvConfig& c = kGemvConfigs[ci];
+        if (!gemv_config_fits(w, M, c)) continue;
+        const int rows = (kWave / c.G) * (c.waves / c.KW);
+        const int grid = (w.N + rows - 1) / rows;
+        const int span = c.G * c.KW;
+        const int steps = (C + span - 1) / span;
+        const double eff = (double)C / ((double)steps * span);
+        const double fill = std::min(1.0, (double)grid * c.waves / 2048.0);
+        const double rounds = std::ceil(grid / 256.0);
+        const double bal = grid >= 256 ? grid / (256.0 * rounds) : grid / 256.0;
+        const double pref = steps >= 2 ? 1.0 : 0.9;
+        const double score = eff * fill * bal * pref;
+        if (score > best_score + 1e-9) {
+            best_score = score;
+            best = ci;
+        }
+    }
+    return best;
+}
+
+int launch_gemv_w4(const Weights& w, int ci, const float* dA, float* dY, int M, hipStream_t stream)
+{
+    const GemvConfig& c = kGemvConfigs[ci];
+    const int ls = l_slot(w);
+    GemvFn fn = kGemvTable[M - 1][ls][ci];
+    const int rows = (kWave / c.G) * (c.waves / c.KW);
+    const int grid = (w.N + rows - 1) / rows;
+    const size_t lds = (size_t)M * (w.K / 32) * kChunkStride4 * 16;
+    if (lds > 64 * 1024 && !g_gemv_lds_raised[M - 1][ls][ci].load()) {
+        MS_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        g_gemv_lds_raised[M - 1][ls][ci].store(true);
+    }
+    GemvParams p;
+    p.b = w.d_b;
+    p.scales = w.d_scales;
+    p.zp = w.has_zp ? w.d_zp : nullptr;
+    p.a = dA;
+    p.y = dY;
+    p.row_bytes = (int)w.row_bytes;
+    p.N = w.N;
+    p.K = w.K;
+    p.C = w.K / 32;
+    p.nb = w.nb;
+    p.zrb = w.zrb;
+    hipLaunchKernelGGL(fn, dim3(grid), dim3(c.waves * kWave), lds, stream, p);
+    MS_HIP_CHECK(hipGetLastError());
+    return MS_HIP_OK;
+}
+
+// ---- gemv_w4_panel: M <= 16, any fast block size, A staged in LDS panels ---------------
+constexpr int kPanelMaxM = 16;
+constexpr int kPanelLanes[3] = {16, 32, 64};
+
+// Lanes per row G: lane efficiency on the row's C chunks x wave fill (>= 1024
+// waves) x a penalty when a lane owns fewer than 3 chunks; ties go to the larger G.
+int pick_panel_lanes(int N, int C)
+{
+    if (g_panel_lanes_override) return g_panel_lanes_override;
     double best = -1.0;
     int best_g = 16;
-    for (int G : kLaneChoices) {
+    for (int G : kPanelLanes) {
         const int R = kWave / G;
         const double waves = (double)((N + R - 1) / R);
         const int steps = (C + G - 1) / G;
         const double eff = (double)C / (double)(steps * G);
         const double fill = std::min(1.0, waves / 1024.0);
-        const double pref = G == 4 ? 0.80 : G == 8 ? 0.93 : G == 64 ? 0.95 : 1.0;
         const double per_lane = (double)C / G < 3.0 ? 0.85 : 1.0;
-        const double score = eff * fill * pref * per_lane;
+        const double score = eff * fill * per_lane;
         if (score >= best - 1e-9) {
             best = score;
             best_g = G;
@@ -205,55 +304,50 @@ int pick_gemv_lanes(int N, int C)
     return best_g;
 }
 
-typedef void (*GemvFn)(GemvParams);
-
+typedef void (*PanelFn)(GemvPanelParams);
 template <int M>
-GemvFn gemv_for_lanes(int G)
+PanelFn panel_for_lanes(int G)
 {
     switch (G) {
-        case 4: return gemv_w4_kernel<M, 4>;
-        case 8: return gemv_w4_kernel<M, 8>;
-        case 16: return gemv_w4_kernel<M, 16>;
-        case 32: return gemv_w4_kernel<M, 32>;
-        default: return gemv_w4_kernel<M, 64>;
+        case 16: return gemv_w4_panel_kernel<M, 16>;
+        case 32: return gemv_w4_panel_kernel<M, 32>;
+        default: return gemv_w4_panel_kernel<M, 64>;
     }
 }
 
-GemvFn gemv_kernel(int M, int G)
+PanelFn panel_kernel(int M, int G)
 {
     switch (M) {
-        case 1: return gemv_for_lanes<1>(G);
-        case 2: return gemv_for_lanes<2>(G);
-        case 3: return gemv_for_lanes<3>(G);
-        case 4: return gemv_for_lanes<4>(G);
-        case 5: return gemv_for_lanes<5>(G);
-        case 6: return gemv_for_lanes<6>(G);
-        case 7: return gemv_for_lanes<7>(G);
-        case 8: return gemv_for_lanes<8>(G);
-        case 9: return gemv_for_lanes<9>(G);
-        case 10: return gemv_for_lanes<10>(G);
-        case 11: return gemv_for_lanes<11>(G);
-        case 12: return gemv_for_lanes<12>(G);
-        case 13: return gemv_for_lanes<13>(G);
-        case 14: return gemv_for_lanes<14>(G);
-        case 15: return gemv_for_lanes<15>(G);
-        default: return gemv_for_lanes<16>(G);
+        case 1: return panel_for_lanes<1>(G);
+        case 2: return panel_for_lanes<2>(G);
+        case 3: return panel_for_lanes<3>(G);
+        case 4: return panel_for_lanes<4>(G);
+        case 5: return panel_for_lanes<5>(G);
+        case 6: return panel_for_lanes<6>(G);
+        case 7: return panel_for_lanes<7>(G);
+        case 8: return panel_for_lanes<8>(G);
+        case 9: return panel_for_lanes<9>(G);
+        case 10: return panel_for_lanes<10>(G);
+        case 11: return panel_for_lanes<11>(G);
+        case 12: return panel_for_lanes<12>(G);
+        case 13: return panel_for_lanes<13>(G);
+        case 14: return panel_for_lanes<14>(G);
+        case 15: return panel_for_lanes<15>(G);
+        default: return panel_for_lanes<16>(G);
     }
 }
 
-constexpr int kGemvMaxM = 16;
-
-struct GemvShape {
+struct PanelShape {
     int G, grid, panel_chunks;
     size_t lds_bytes;
 };
 
-GemvShape gemv_shape(const Weights& w, int M)
+PanelShape panel_shape(const Weights& w, int M)
 {
-    GemvShape s;
+    PanelShape s;
     const int C = w.K / 32;
-    s.G = pick_gemv_lanes(w.N, C);
-    const int rows_per_wg = (kGemvThreads / kWave) * (kWave / s.G);
+    s.G = pick_panel_lanes(w.N, C);
+    const int rows_per_wg = (kPanelThreads / kWave) * (kWave / s.G);
     s.grid = (w.N + rows_per_wg - 1) / rows_per_wg;
     // LDS panel: <= 40 KiB for M <= 4 (4 workgroups per CU), <= 64 KiB beyond.
     const size_t budget = M <= 4 ? 40 * 1024 : 64 * 1024;
@@ -271,99 +365,10 @@ GemvShape gemv_shape(const Weights& w, int M)
     return s;
 }
 
-struct M1Shape {
-    int ok = 0;
-    int yt, T, kw, rs, steps, grid, block;
-    size_t lds;
-};
-
-// gemv_w4_m1: K slices so every lane owns at most 2 chunks with the fewest idle
-// lane-chunks; ~2560 waves in flight (10 per CU) across row steps.
-M1Shape m1_shape(const Weights& w)
+int launch_panel(const Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
 {
-    M1Shape s;
-    const int C = w.K / 32;
-    if (!g_m1_enable || C < 48) return s;
-    int best_kw = 0, best_T = 0;
-    double best_eff = -1.0;
-    for (int kw = 1; kw <= 8; ++kw) {
-        if (g_m1_slices && kw != g_m1_slices) continue;
-        const int cs = (C + kw - 1) / kw;
-        const int T = (cs + kWave - 1) / kWave;
-        if (T > 2) continue;
-        const double eff = (double)C / (double)(kw * kWave * T);
-        if (eff > best_eff + 1e-9) {
-            best_eff = eff;
-            best_kw = kw;
-            best_T = T;
-        }
-    }
-    if (!best_kw) return s;
-    s.kw = best_kw;
-    s.T = best_T;
-    s.rs = std::max(1, 4 / s.kw);
-    s.yt = g_m1_rows ? g_m1_rows : (w.N >= 8192 ? 4 : 2);
-    if (s.T == 2 && s.yt > 4) s.yt = 4;
-    s.steps = g_m1_steps ? g_m1_steps
-                         : std::max(1, (int)std::lround((double)s.kw * w.N / (s.yt * 2560.0)));
-    const int rows_per_block = s.rs * s.yt * s.steps;
-    s.grid = (w.N + rows_per_block - 1) / rows_per_block;
-    s.block = kWave * s.kw * s.rs;
-    s.lds = s.kw > 1 ? (size_t)rows_per_block * s.kw * sizeof(float) : 0;
-    s.ok = s.block <= 512 && s.lds <= 64 * 1024;
-    return s;
-}
-
-typedef void (*GemvM1Fn)(GemvM1Params);
-
-GemvM1Fn gemv_m1_kernel(int yt, int T)
-{
-    if (T == 1) {
-        switch (yt) {
-            case 1: return gemv_w4_m1_kernel<1, 1>;
-            case 2: return gemv_w4_m1_kernel<2, 1>;
-            case 8: return gemv_w4_m1_kernel<8, 1>;
-            default: return gemv_w4_m1_kernel<4, 1>;
-        }
-    }
-    switch (yt) {
-        case 1: return gemv_w4_m1_kernel<1, 2>;
-        case 2: return gemv_w4_m1_kernel<2, 2>;
-        default: return gemv_w4_m1_kernel<4, 2>;   // 8 rows x 2 chunks exceeds the VGPR file
-    }
-}
-
-int launch_gemv_m1(const Weights& w, const M1Shape& s, const float* dA, float* dY, hipStream_t stream)
-{
-    GemvM1Params p;
-    p.b = w.d_b;
-    p.scales = w.d_scales;
-    p.zp = w.has_zp ? w.d_zp : nullptr;
-    p.a = dA;
-    p.y = dY;
-    p.row_bytes = w.row_bytes;
-    p.N = w.N;
-    p.K = w.K;
-    p.C = w.K / 32;
-    p.log2cpb = w.log2cpb;
-    p.nb = w.nb;
-    p.zrb = w.zrb;
-    p.kw = s.kw;
-    p.rs = s.rs;
-    p.steps = s.steps;
-    hipLaunchKernelGGL(gemv_m1_kernel(s.yt, s.T), dim3(s.grid), dim3(s.block), s.lds, stream, p);
-    MS_HIP_CHECK(hipGetLastError());
-    return MS_HIP_OK;
-}
-
-int launch_gemv(const Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
-{
-    if (M == 1) {
-        const M1Shape s1 = m1_shape(w);
-        if (s1.ok) return launch_gemv_m1(w, s1, dA, dY, stream);
-    }
-    const GemvShape s = gemv_shape(w, M);
-    GemvParams p;
+    const PanelShape s = panel_shape(w, M);
+    GemvPanelParams p;
     p.b = w.d_b;
     p.scales = w.d_scales;
     p.zp = w.has_zp ? w.d_zp : nullptr;
@@ -377,9 +382,16 @@ int launch_gemv(const Weights& w, const float* dA, float* dY, int M, hipStream_t
     p.nb = w.nb;
     p.zrb = w.zrb;
     p.panel_chunks = s.panel_chunks;
-    hipLaunchKernelGGL(gemv_kernel(M, s.G), dim3(s.grid), dim3(kGemvThreads), s.lds_bytes, stream, p);
+    hipLaunchKernelGGL(panel_kernel(M, s.G), dim3(s.grid), dim3(kPanelThreads), s.lds_bytes, stream, p);
     MS_HIP_CHECK(hipGetLastError());
     return MS_HIP_OK;
+}
+
+int launch_gemv(const Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
+{
+    const int ci = pick_gemv_config(w, M);
+    if (ci >= 0) return launch_gemv_w4(w, ci, dA, dY, M, stream);
+    return launch_panel(w, dA, dY, M, stream);
 }
 
 int launch_generic(const Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
@@ -400,7 +412,7 @@ int enqueue_gemm(const Weights& w, const float* dA, float* dY, int M, hipStream_
     if ((reinterpret_cast<uintptr_t>(dA) & 15) || (reinterpret_cast<uintptr_t>(dY) & 3))
         return fail(MS_HIP_ERR_INVALID, "[ms_hip] A must be 16-byte and Y 4-byte aligned");
     if (!w.fast) return launch_generic(w, dA, dY, M, stream);
-    if (M <= kGemvMaxM) return launch_gemv(w, dA, dY, M, stream);
+    if (M <= kPanelMaxM) return launch_gemv(w, dA, dY, M, stream);
     return launch_mfma(w.d_b, w.d_scales, w.has_zp ? w.d_zp : nullptr, w.row_bytes, w.N, w.K, w.nb,
                        w.zrb, w.log2cpb, dA, dY, M, stream)
                ? fail(MS_HIP_ERR_HIP, "[ms_hip] MFMA launch failed: %s", hipGetErrorString(hipGetLastError()))
@@ -714,11 +726,9 @@ int ms_hip_sync(void)
 
 int ms_hip_set_gemv_lanes(int lanes_per_row)
 {
-    if (lanes_per_row != 0 && lanes_per_row != 4 && lanes_per_row != 8 && lanes_per_row != 16 &&
-        lanes_per_row != 32 && lanes_per_row != 64)
-        return fail(MS_HIP_ERR_INVALID, "[ms_hip] lanes_per_row must be 0, 4, 8, 16, 32 or 64; got %d",
-                    lanes_per_row);
-    g_gemv_lanes_override = lanes_per_row;
+    if (lanes_per_row != 0 && lanes_per_row != 16 && lanes_per_row != 32 && lanes_per_row != 64)
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] lanes_per_row must be 0, 16, 32 or 64; got %d", lanes_per_row);
+    g_panel_lanes_override = lanes_per_row;
     return MS_HIP_OK;
 }
 
@@ -726,18 +736,9 @@ int ms_hip_set_tuning(int knob, int value)
 {
     switch (knob) {
         case 0: return ms_hip_set_gemv_lanes(value);
-        case 1: g_m1_enable = value ? 1 : 0; return MS_HIP_OK;
-        case 2:
-            if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8) break;
-            g_m1_rows = value;
-            return MS_HIP_OK;
-        case 3:
-            if (value < 0 || value > 64) break;
-            g_m1_steps = value;
-            return MS_HIP_OK;
-        case 4:
-            if (value < 0 || value > 8) break;
-            g_m1_slices = value;
+        case 1:
+            if (value < -1 || value > kNumGemvConfigs) break;
+            g_gemv_config = value;
             return MS_HIP_OK;
         default: break;
     }
@@ -754,18 +755,22 @@ int ms_hip_nbits_launch_info(void* handle, int M, int* kernel_id, int* lanes_per
         kid = 0;
         gr = (int)(((int64_t)M * w->N + 255) / 256);
         bl = 256;
-    } else if (M == 1 && m1_shape(*w).ok) {
-        const M1Shape s = m1_shape(*w);
-        kid = 3;
-        G = kWave;
-        gr = s.grid;
-        bl = s.block;
-    } else if (M <= kGemvMaxM) {
-        const GemvShape s = gemv_shape(*w, M);
-        kid = 1;
-        G = s.G;
-        gr = s.grid;
-        bl = kGemvThreads;
+    } else if (M <= kPanelMaxM) {
+        const int ci = pick_gemv_config(*w, M);
+        if (ci >= 0) {
+            const GemvConfig& c = kGemvConfigs[ci];
+            const int rows = (kWave / c.G) * (c.waves / c.KW);
+            kid = 1;
+            G = c.G;
+            gr = (w->N + rows - 1) / rows;
+            bl = c.waves * kWave;
+        } else {
+            const PanelShape s = panel_shape(*w, M);
+            kid = 3;
+            G = s.G;
+            gr = s.grid;
+            bl = kPanelThreads;
+        }
     } else {
         kid = 2;
         mfma_launch_shape(w->N, M, &gr, &bl);

@@ -135,6 +135,13 @@ __device__ __forceinline__ float dot8(const uint32_t (&d)[4], const float4& a0, 
 
 // ---- shared by the GEMV kernels ---------------------------------------------------
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+// A staged activation chunk in LDS: 32 activations pre-scaled (even k by 2^24, odd
+// k by 2^20) in 8 float4, then (sum of the 32 unscaled activations, 0, 0, 0). The
+// ninth float4 also pads the chunk stride off a power of two (fewer bank conflicts).
+constexpr int kChunkStride4 = 9;
+// A buffer offset beyond every resource the kernels build: a load from it returns
+// zero and makes no memory request.
+constexpr int kOOB = 0x7ffffff0;
 constexpr uint32_t kBufferWord3 = 0x00020000u;   // raw buffer resource, gfx9 data format
 constexpr float kTwo24 = 16777216.0f;            // 2^24
 constexpr float kTwo20 = 1048576.0f;             // 2^20
@@ -171,6 +178,22 @@ __device__ __forceinline__ void code_pairs(uint32_t x, uint32_t (&p)[4])
 __device__ __forceinline__ int zp_nibble(const uint8_t* zrow, int blk)
 {
     return (zrow[blk >> 1] >> ((blk & 1) * 4)) & 0x0F;
+}
+
+// acc + sum of a_k q_k over the 8 codes of one dword whose code_pairs() are p,
+// with a0 = a'[k0..k3], a1 = a'[k4..k7] staged pre-scaled. Every product is exact
+// inside its fma; one rounding per accumulation.
+__device__ __forceinline__ float qdot8(const uint32_t (&p)[4], const float4& a0, const float4& a1, float acc)
+{
+    acc = mix_lo_acc(p[0], a0.x, acc);
+    acc = mix_lo_acc(p[1], a0.y, acc);
+    acc = mix_lo_acc(p[2], a0.z, acc);
+    acc = mix_lo_acc(p[3], a0.w, acc);
+    acc = mix_hi_acc(p[0], a1.x, acc);
+    acc = mix_hi_acc(p[1], a1.y, acc);
+    acc = mix_hi_acc(p[2], a1.z, acc);
+    acc = mix_hi_acc(p[3], a1.w, acc);
+    return acc;
 }
 
 }  // namespace msnb

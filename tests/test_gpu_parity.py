@@ -117,7 +117,7 @@ DECODE_CASES = ([(workloads.QWEN05B_UP, 1)] + [(o, 1) for o in workloads.QWEN05B
 def test_gemv_parity(gpu, op, M):
     b, s, z, w = weights_for(op, seed=op.N + 3 * op.K + M)
     a = workloads.make_activations(M, op.K, seed=M + op.K)
-    assert w.launch_info(M)["kernel"] in ("gemv_w4", "gemv_w4_m1")
+    assert w.launch_info(M)["kernel"] in ("gemv_w4", "gemv_w4_panel")
     log(f"gemv M={M} K={op.K} N={op.N} bs={op.block_size} {w.launch_info(M)}")
     y = w.gemm(a)
     assert_gemv_close(y, oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, op.block_size), f"M={M} {op}")
@@ -138,65 +138,67 @@ def test_gemv_one_hot_is_bit_exact(gpu):
     w.close()
 
 
-@pytest.mark.parametrize("lanes", [4, 8, 16, 32, 64])
-def test_gemv_every_lane_split(gpu, lanes):
+def gemv_config_count():
+    """Number of gemv_w4 launch configurations (knob 1 accepts 1..count)."""
+    n = 0
+    while True:
+        try:
+            native.set_tuning(1, n + 1)
+        except native.HipError:
+            native.set_tuning(1, 0)
+            return n
+        n += 1
+
+
+GEMV_SHAPES = [workloads.Op("a", 3584, 1000), workloads.Op("b", 896, 77, 128, False), workloads.Op("c", 4864, 96),
+               workloads.Op("d", 1536, 65, 128, True), workloads.Op("e", 11008, 129, 32, True),
+               workloads.Op("f", 320, 300, 32, False)]
+
+
+def test_gemv_every_launch_config(gpu):
+    """Every gemv_w4 configuration (where it fits) and the panel kernel at every lane
+    split, M = 1..4, block sizes 32 and 128, with and without zero points, K not a
+    multiple of the step, N not a multiple of the workgroup's rows."""
+    count = gemv_config_count()
+    assert count >= 8
+    try:
+        for cfg in list(range(1, count + 1)) + [-1]:
+            native.set_tuning(1, cfg)
+            for lanes in ([16, 32, 64] if cfg == -1 else [0]):
+                native.set_gemv_lanes(lanes)
+                for op in GEMV_SHAPES:
+                    for M in (1, 2, 3, 4):
+                        b, s, z, w = weights_for(op, seed=(cfg + 2) * 31 + M)
+                        a = workloads.make_activations(M, op.K, seed=M + cfg + 2)
+                        info = w.launch_info(M)
+                        if cfg == -1:
+                            assert info["kernel"] == "gemv_w4_panel"
+                        log(f"cfg={cfg} lanes={lanes} M={M} K={op.K} N={op.N} {info}")
+                        assert_gemv_close(w.gemm(a), oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, op.block_size),
+                                          f"cfg={cfg} M={M} {op}")
+                        w.close()
+    finally:
+        native.set_tuning(1, 0)
+        native.set_gemv_lanes(0)
+
+
+@pytest.mark.parametrize("lanes", [16, 32, 64])
+def test_gemv_panel_every_lane_split(gpu, lanes):
+    """The panel kernel for M = 5..16 (its own range) at every lane split."""
     ops = [workloads.Op("a", 3584, 1000), workloads.Op("b", 896, 77, 128, False), workloads.Op("c", 4864, 96, 64)]
     try:
         native.set_gemv_lanes(lanes)
         for op in ops:
-            for M in (1, 3, 16):
+            for M in (5, 11, 16):
                 b, s, z, w = weights_for(op, seed=lanes + M)
                 a = workloads.make_activations(M, op.K, seed=M)
-                log(f"lanes={lanes} M={M} K={op.K} N={op.N}")
+                assert w.launch_info(M)["kernel"] == "gemv_w4_panel"
+                log(f"panel lanes={lanes} M={M} K={op.K} N={op.N}")
                 assert_gemv_close(w.gemm(a), oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, op.block_size),
                                   f"lanes={lanes} M={M} {op}")
                 w.close()
     finally:
         native.set_gemv_lanes(0)
-
-
-M1_OPS = [workloads.Op("m1a", 3584, 1000), workloads.Op("m1b", 18944, 300), workloads.Op("m1c", 4096, 777, 128, False),
-          workloads.Op("m1d", 1536, 65, 64, True), workloads.Op("m1e", 11008, 129, 32, True)]
-
-
-@pytest.mark.parametrize("rows,steps,slices", [(0, 0, 0), (1, 1, 1), (2, 3, 0), (4, 1, 2), (4, 5, 0), (8, 2, 0),
-                                               (1, 0, 8), (4, 2, 3), (2, 1, 5)])
-def test_gemv_m1_every_launch_shape(gpu, rows, steps, slices):
-    try:
-        native.set_tuning(1, 1)
-        native.set_tuning(2, rows)
-        native.set_tuning(3, steps)
-        native.set_tuning(4, slices)
-        for op in M1_OPS:
-            b, s, z, w = weights_for(op, seed=rows * 100 + steps * 10 + slices)
-            a = workloads.make_activations(1, op.K, seed=op.K)
-            info = w.launch_info(1)
-            log(f"m1 rows={rows} steps={steps} slices={slices} K={op.K} N={op.N} {info}")
-            ref = oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, op.block_size)
-            assert_gemv_close(w.gemm(a), ref, f"m1 {op.name}")
-            w.close()
-    finally:
-        for knob in (2, 3, 4):
-            native.set_tuning(knob, 0)
-        native.set_tuning(1, 0)
-
-
-def test_gemv_m1_switch(gpu):
-    op = workloads.DECODE_7B[4]
-    b, s, z, w = weights_for(op, seed=2)
-    a = workloads.make_activations(1, op.K, seed=3)
-    ref = oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, op.block_size)
-    assert w.launch_info(1)["kernel"] == "gemv_w4"
-    y2 = w.gemm(a)
-    try:
-        native.set_tuning(1, 1)
-        assert w.launch_info(1)["kernel"] == "gemv_w4_m1"
-        y1 = w.gemm(a)
-    finally:
-        native.set_tuning(1, 0)
-    assert_gemv_close(y1, ref, "m1 kernel")
-    assert_gemv_close(y2, ref, "lds kernel")
-    w.close()
 
 
 # ---- shapes the fast kernels do not take, and edges ----------------------------------------------
