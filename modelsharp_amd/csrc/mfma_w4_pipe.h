@@ -1,0 +1,286 @@
+// mfma_w4_pipe.h — INT4 MatMulNBits prefill GEMM on the CDNA4 matrix cores with a
+// buffer->LDS load pipeline (M > 16, block size 32, K a multiple of 128).
+//
+// Y[M,N] = A[M,K] * W[N,K]^T, W = (q - zp) * s dequantized in-kernel.
+//
+// Two launches per call:
+//   a_to_f16_kernel  A (fp32) -> fp16 workspace, each 8-k group stored in the
+//                    order (k0,k4),(k1,k5),(k2,k6),(k3,k7) — the order in which the
+//                    weight dequant below produces its codes, so both MFMA
+//                    operands carry the same permutation of k (a dot product does
+//                    not depend on the order of its terms).
+//   mfma_w4_pipe_kernel
+//     * A 256x256 output tile per workgroup: 4 waves in a 2x2 layout, each wave
+//       128x128 as 4x4 v_mfma_f32_32x32x16_f16 fragments accumulating in AGPRs.
+//       A step is 32 k (one block of 32 codes per weight row).
+//     * Every global load of the main loop is a buffer->LDS load
+//       (buffer_load_dword{,x4} ... lds) issued from inline asm, so no vector
+//       register waits on memory and the compiler inserts no conservative
+//       s_waitcnt for them; each wait is an explicit vmcnt count that follows
+//       from the issue order below (which is why the loop is unrolled by 4).
+//         - A: 4 LDS stages of one step (256 rows x 64 B, 16-byte chunks XOR-
+//           swizzled per row against bank conflicts), issued 3 steps ahead;
+//         - weights: per group of 4 steps, 64 B of codes, 16 B of scales and
+//           2 zero-point bytes per row (two groups double-buffered), so a row's
+//           codes for 4 steps are one contiguous 64-byte request.
+//     * Dequant: each lane owns one weight row of the tile (the rows its own wave
+//       loaded, so only a wave-local wait is needed). It turns 32 codes into fp16
+//       with packed-half math — the code in the mantissa of 1024.0 minus
+//       (1024 + zp) is exactly q - zp, times the block scale rounded to fp16 —
+//       and writes them to a double-buffered fp16 weight tile. The raw codes of
+//       step s+2 are read into registers during step s, so the dequant of step
+//       s+1 interleaves with the MFMAs of step s.
+//     * One barrier per step. Tile order is XCD-aware (workgroup b runs on XCD
+//       b % 8; each XCD walks an m-major range of tiles, sharing A panels in L2).
+// Numerics: A rounded once to fp16; W = fl16((q - zp) * fl16(s)); products exact,
+// sums fp32. Requires |A| < 65504 (fp16 range) and fp16-normal scales for the
+// 2^-11 relative bound; the library routes other inputs to mfma_w4.
+#pragma once
+#include "mfma_w4.h"
+
+namespace msnb {
+
+struct PipeParams {
+    const uint8_t* b;
+    const float* scales;
+    const uint8_t* zp;       // nullptr: zp = 8
+    const _Float16* a16;     // [M][K] fp16, permuted within 8-k groups
+    float* y;                // [M][N]
+    int row_bytes, M, N, K, C, nb, zrb;
+    int tiles_m, tiles_n;
+};
+
+constexpr int kPipeBM = 256, kPipeBN = 256;
+constexpr int kPipeLdsBytes = 4 * kPipeBM * 64 + 2 * (kPipeBN * 64 + kPipeBN * 16 + kPipeBN * 8) + 2 * kPipeBN * 64;
+// Base offset of a row beyond the matrix: above every buffer the kernel reads
+// (the host checks each is smaller), so loads from it return zero.
+constexpr int kPipeFar = 0x40000000;
+
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi)
+{
+    return __builtin_bit_cast(uint32_t, h2_t{(_Float16)lo, (_Float16)hi});
+}
+
+// fp32 -> fp16, 8 values per thread, in the permuted order above.
+__global__ __launch_bounds__(256) void a_to_f16_kernel(const float* __restrict__ a, uint32_t* __restrict__ o, int64_t n8)
+{
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n8; i += (int64_t)gridDim.x * blockDim.x) {
+        const float4 lo = reinterpret_cast<const float4*>(a)[2 * i];
+        const float4 hi = reinterpret_cast<const float4*>(a)[2 * i + 1];
+        reinterpret_cast<u32x4_t*>(o)[i] =
+            u32x4_t{pack_h2(lo.x, hi.x), pack_h2(lo.y, hi.y), pack_h2(lo.z, hi.z), pack_h2(lo.w, hi.w)};
+    }
+}
+
+// fp16 weights of one dword of codes in the order (k0,k4),(k1,k5),(k2,k6),(k3,k7).
+__device__ __forceinline__ void dequant8_f16(uint32_t x, h2_t zb, h2_t s2, uint32_t (&o)[4])
+{
+    const uint32_t m = kHalfMagic;
+    o[0] = as_u32((as_h2(and_or(x, 0x000F000Fu, m)) - zb) * s2);
+    o[1] = as_u32((as_h2(and_or(x >> 4, 0x000F000Fu, m)) - zb) * s2);
+    o[2] = as_u32((as_h2(and_or(x >> 8, 0x000F000Fu, m)) - zb) * s2);
+    o[3] = as_u32((as_h2(and_or(x >> 12, 0x000F000Fu, m)) - zb) * s2);
+}
+
+typedef __attribute__((address_space(3))) uint8_t lds_byte_t;
+__device__ __forceinline__ uint32_t lds_address(const void* p) { return (uint32_t)(uintptr_t)(lds_byte_t*)p; }
+
+// buffer -> LDS loads: lane i's bytes land at LDS m0 + 16*i (x4) or m0 + 4*i (dword, ubyte).
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, int voff, int soff, uint32_t m0v)
+{
+    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0v) : "memory");
+}
+__device__ __forceinline__ void lds_load1(__amdgpu_buffer_rsrc_t r, int voff, int soff, uint32_t m0v)
+{
+    asm volatile("buffer_load_ubyte %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0v) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// 16-byte chunk slot of k-chunk j in row r: conflict-free for 8- and 16-row passes.
+__device__ __forceinline__ int pipe_slot(int r, int j) { return j ^ (((r >> 2) & 3) ^ (r & 2)); }
+
+__global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
+{
+    constexpr int BM = kPipeBM, BN = kPipeBN, FM = 4, FN = 4;
+    constexpr int A_ST = BM * 64;                               // one step of A
+    constexpr int CG = BN * 64, SG = BN * 16, ZG = BN * 8;      // one group: codes, scales, zp
+    constexpr int OFF_A = 0, OFF_C = OFF_A + 4 * A_ST, OFF_S = OFF_C + 2 * CG, OFF_Z = OFF_S + 2 * SG,
+                  OFF_B = OFF_Z + 2 * ZG;
+    constexpr int B16_SZ = BN * 64;
+    extern __shared__ __attribute__((aligned(16))) uint8_t pipe_lds[];
+    uint8_t* const lds = pipe_lds;
+    const uint32_t lbase = lds_address(lds);
+
+    const int tiles = p.tiles_m * p.tiles_n;
+    const int tile = xcd_tile(blockIdx.x, tiles);
+    if (tile >= tiles) return;
+    const int m0 = (tile / p.tiles_n) * BM, n0 = (tile % p.tiles_n) * BN;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int wm = wave & 1, wn = wave >> 1;
+
+    const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(p.a16, p.M * p.K * 2);
+    const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(p.b, p.N * p.row_bytes);
+    const __amdgpu_buffer_rsrc_t rsc = buffer_rsrc(p.scales, p.N * p.nb * 4);
+    const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(p.zp ? (const void*)p.zp : (const void*)p.scales,
+                                                  p.zp ? p.N * p.zrb : 0);
+    // Loop-invariant per-lane offsets; the step advance rides in the scalar soffset.
+    int avo[4], cvo[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int r = wave * 64 + 16 * q + (lane >> 2);
+        const int m = m0 + r;
+        avo[q] = m < p.M ? m * p.K * 2 + pipe_slot(r, lane & 3) * 16 : kPipeFar;
+        const int n = n0 + r;
+        cvo[q] = n < p.N ? n * p.row_bytes + (lane & 3) * 16 : kPipeFar;
+    }
+    const int brow = wave * 64 + lane;   // the weight row this lane loads scales for and dequantizes
+    const int bn = n0 + brow;
+    const int svo = bn < p.N ? bn * p.nb * 4 : kPipeFar;
+    const int zvo = bn < p.N ? bn * p.zrb : kPipeFar;
+    const int last = p.C - 1;
+
+    auto issue_a = [&](int t, int st) {   // step t -> stage st (clamped: a prefetch past the end re-reads)
+        const int tc = min(t, last);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            lds_load16(ra, avo[q], tc * 64, lbase + OFF_A + st * A_ST + (wave * 64 + 16 * q) * 64);
+    };
+    auto issue_b = [&](int g, int buf) {  // steps 4g .. 4g+3 -> buffer buf
+        const int gc = min(g, last >> 2);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            lds_load16(rb, cvo[q], gc * 64, lbase + OFF_C + buf * CG + (wave * 64 + 16 * q) * 64);
+        lds_load16(rsc, svo, gc * 16, lbase + OFF_S + buf * SG + wave * 64 * 16);
+        lds_load1(rz, zvo, gc * 2, lbase + OFF_Z + buf * ZG + wave * 64 * 4);
+        lds_load1(rz, zvo, gc * 2 + 1, lbase + OFF_Z + buf * ZG + BN * 4 + wave * 64 * 4);
+    };
+    struct Raw {
+        u32x4_t q;
+        float s;
+        uint32_t zb;
+    };
+    auto read_raw = [&](int t) {
+        Raw r;
+        const int buf = (t >> 2) & 1, ph = t & 3;
+        r.q = *reinterpret_cast<const u32x4_t*>(lds + OFF_C + buf * CG + brow * 64 + ph * 16);
+        r.s = *reinterpret_cast<const float*>(lds + OFF_S + buf * SG + brow * 16 + ph * 4);
+        r.zb = *reinterpret_cast<const uint32_t*>(lds + OFF_Z + buf * ZG + (ph >> 1) * BN * 4 + brow * 4);
+        return r;
+    };
+    auto dequant = [&](const Raw& raw, int t) {
+        const int zp = p.zp ? (int)((raw.zb >> ((t & 1) * 4)) & 0x0F) : 8;
+        const h2_t zb = as_h2(kHalfMagic | ((uint32_t)zp << 16) | (uint32_t)zp);
+        const _Float16 sh = (_Float16)raw.s;
+        const h2_t s2 = h2_t{sh, sh};
+        uint8_t* dst = lds + OFF_B + (t & 1) * B16_SZ + brow * 64;
+        const uint32_t qd[4] = {raw.q.x, raw.q.y, raw.q.z, raw.q.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t o[4];
+            dequant8_f16(qd[j], zb, s2, o);
+            *reinterpret_cast<u32x4_t*>(dst + pipe_slot(brow, j) * 16) = u32x4_t{o[0], o[1], o[2], o[3]};
+        }
+    };
+
+    floatx16_t acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = floatx16_t{};
+    }
+    const int lr = lane & 31, lh = lane >> 5;
+    auto mma = [&](int st, int bbuf) {
+        const uint8_t* As = lds + OFF_A + st * A_ST;
+        const uint8_t* Bs = lds + OFF_B + bbuf * B16_SZ;
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+            const int j = 2 * sub + lh;
+            half8_t af[FM], bf[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const int r = wm * 128 + 32 * i + lr;
+                af[i] = *reinterpret_cast<const half8_t*>(As + r * 64 + pipe_slot(r, j) * 16);
+            }
+#pragma unroll
+            for (int i = 0; i < FN; ++i) {
+                const int r = wn * 128 + 32 * i + lr;
+                bf[i] = *reinterpret_cast<const half8_t*>(Bs + r * 64 + pipe_slot(r, j) * 16);
+            }
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+#pragma unroll
+                for (int jn = 0; jn < FN; ++jn)
+                    acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[jn], acc[i][jn], 0, 0, 0);
+            }
+        }
+    };
+
+    // Issue order per wave, and the vmcnt each wait needs (loads issued after the
+    // one waited for): prologue B(0) A(0) A(1) A(2); step 4g+p issues A(4g+p+3),
+    // and at p = 0 also B(g+1) [7 loads]; A(s) is 4 loads.
+    issue_b(0, 0);
+    issue_a(0, 0);
+    issue_a(1, 1);
+    issue_a(2, 2);
+    wait_vmcnt<8>();                     // B(0), A(0)
+    Raw raw = read_raw(0);
+    dequant(raw, 0);
+    raw = read_raw(1);
+    lds_barrier();
+    for (int t = 0; t < p.C; t += 4) {
+        wait_vmcnt<4>();                 // A(t+1): after it A(t+2)
+        Raw rn = read_raw(t + 2);
+        mma(0, 0);
+        dequant(raw, t + 1);
+        raw = rn;
+        issue_a(t + 3, 3);
+        issue_b((t >> 2) + 1, ((t >> 2) + 1) & 1);
+        lds_barrier();
+        wait_vmcnt<11>();                // A(t+2): after it A(t+3), B(g+1)
+        rn = read_raw(t + 3);
+        mma(1, 1);
+        dequant(raw, t + 2);
+        raw = rn;
+        issue_a(t + 4, 0);
+        lds_barrier();
+        wait_vmcnt<4>();                 // B(g+1) (raw of t+4), A(t+3): after B(g+1) A(t+4)
+        rn = read_raw(t + 4);
+        mma(2, 0);
+        dequant(raw, t + 3);
+        raw = rn;
+        issue_a(t + 5, 1);
+        lds_barrier();
+        wait_vmcnt<4>();                 // A(t+4): after it A(t+5)
+        rn = read_raw(t + 5);
+        mma(3, 1);
+        dequant(raw, t + 4);
+        raw = rn;
+        issue_a(t + 6, 2);
+        lds_barrier();
+    }
+    wait_vmcnt<0>();
+
+    // acc[i][j][v] is Y[row][col], col = lane % 32, row = 8*(v/4) + 4*(lane/32) + v%4.
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const int mrow0 = m0 + wm * 128 + 32 * i + 4 * lh;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int col = n0 + wn * 128 + 32 * j + lr;
+            if (col < p.N) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int row = mrow0 + 8 * (v >> 2) + (v & 3);
+                    if (row < p.M) p.y[(int64_t)row * p.N + col] = acc[i][j][v];
+                }
+            }
+        }
+    }
+}
+
+}  // namespace msnb

@@ -5,7 +5,8 @@
 //   bits=4, block_size in {32,64,128,256}, K % 32 == 0 ("fast" layouts):
 //     M <= 4, block_size 32 or 128, M*K/32 <= 1024              -> gemv_w4
 //     M <= 16 otherwise                                         -> gemv_w4_panel
-//     M >  16                                                   -> mfma_w4
+//     M >  16, block_size 32, K % 128 == 0, fp16-safe scales  -> a_to_f16 + mfma_w4_pipe
+//     M >  16 otherwise                                         -> mfma_w4
 //   anything else                                              -> generic
 // Declarations and reference citations: include/ms_hip_kernels.h.
 #include "../../include/ms_hip_kernels.h"
@@ -28,6 +29,7 @@
 #include "gemv_w4_panel.h"
 #include "generic_nbits.h"
 #include "mfma_w4.h"
+#include "mfma_w4_pipe.h"
 
 using namespace msnb;
 
@@ -108,6 +110,11 @@ struct Weights {
     hipStream_t stream = nullptr;
     float* d_stage = nullptr;
     size_t stage_bytes = 0;
+    // prefill pipeline: scales fp16-safe (checked at load), fp16 activation workspace
+    int pipe_scales_ok = 0;
+    std::mutex ws_mu;
+    uint32_t* d_a16 = nullptr;
+    size_t a16_bytes = 0;
 };
 
 constexpr uint32_t kHandleMagic = 0x4D534E42u;   // "MSNB"
@@ -164,18 +171,63 @@ void free_weights(Weights& w)
     if (w.d_scales) (void)hipFree(w.d_scales);
     if (w.d_zp) (void)hipFree(w.d_zp);
     if (w.d_stage) (void)hipFree(w.d_stage);
+    if (w.d_a16) (void)hipFree(w.d_a16);
     if (w.stream) (void)hipStreamDestroy(w.stream);
     w.d_b = nullptr;
     w.d_scales = nullptr;
     w.d_zp = nullptr;
     w.d_stage = nullptr;
+    w.d_a16 = nullptr;
+    w.a16_bytes = 0;
     w.stream = nullptr;
+}
+
+// Smallest nonzero and largest |scale| bit patterns (positive floats order as integers).
+__global__ __launch_bounds__(256) void scale_range_kernel(const float* __restrict__ s, int64_t n, unsigned* out)
+{
+    unsigned lo = 0xFFFFFFFFu, hi = 0u;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const unsigned b = __builtin_bit_cast(unsigned, s[i]) & 0x7FFFFFFFu;
+        if (b) {
+            lo = min(lo, b);
+            hi = max(hi, b);
+        }
+    }
+    atomicMin(&out[0], lo);
+    atomicMax(&out[1], hi);
+}
+
+// The pipelined prefill rounds scales to fp16 and forms (q - zp) * s in fp16: every
+// nonzero |s| must be an fp16 normal (>= 2^-14) and 15 |s| must stay below 65504.
+int check_pipe_scales(Weights& w)
+{
+    w.pipe_scales_ok = 0;
+    if (!w.fast || w.log2cpb != 0) return MS_HIP_OK;
+    unsigned* d = nullptr;
+    MS_HIP_CHECK(hipMalloc(&d, 2 * sizeof(unsigned)));
+    const unsigned init[2] = {0xFFFFFFFFu, 0u};
+    hipError_t e = hipMemcpy(d, init, sizeof init, hipMemcpyHostToDevice);
+    const int64_t n = (int64_t)w.N * w.nb;
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(scale_range_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 1024)), dim3(256), 0,
+                           nullptr, w.d_scales, n, d);
+        e = hipGetLastError();
+    }
+    unsigned r[2] = {0u, 0u};
+    if (e == hipSuccess) e = hipMemcpy(r, d, sizeof r, hipMemcpyDeviceToHost);
+    (void)hipFree(d);
+    if (e != hipSuccess) return fail(MS_HIP_ERR_HIP, "[ms_hip] scale range check failed: %s", hipGetErrorString(e));
+    const unsigned kMinNormal16 = 0x38800000u;   // 2^-14
+    const unsigned kMaxScale = 0x45886000u;      // 4364.0: 15 * s < 65504
+    w.pipe_scales_ok = (r[0] == 0xFFFFFFFFu) || (r[0] >= kMinNormal16 && r[1] <= kMaxScale);
+    return MS_HIP_OK;
 }
 
 // ---- GEMV launch shape --------------------------------------------------------------------
 // Tuning knobs (ms_hip_set_tuning); 0 = the shape heuristics below.
 int g_panel_lanes_override = 0;  // knob 0: gemv_w4_panel lanes per row
 int g_gemv_config = 0;           // knob 1: c+1 forces kGemvConfigs[c], -1 forces gemv_w4_panel
+int g_pipe_off = 0;              // knob 2: 1 routes every prefill call to mfma_w4
 
 // gemv_w4 instantiations: [M-1][L slot][config], L slot 0 = block size 32, 1 = block size 128.
 typedef void (*GemvFn)(GemvParams);
@@ -404,7 +456,72 @@ int launch_generic(const Weights& w, const float* dA, float* dY, int M, hipStrea
     return MS_HIP_OK;
 }
 
-int enqueue_gemm(const Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
+// The pipelined prefill takes M > 16, block size 32, K a multiple of 128, fp16-safe
+// scales, and buffers below kPipeFar (its out-of-range row offset).
+bool pipe_eligible(const Weights& w, int M)
+{
+    return !g_pipe_off && w.fast && M > kPanelMaxM && w.log2cpb == 0 && (w.K % 128) == 0 && w.pipe_scales_ok &&
+           (int64_t)w.N * w.row_bytes < kPipeFar && (int64_t)M * w.K * 2 < kPipeFar &&
+           (int64_t)w.N * w.nb * 4 < kPipeFar;
+}
+
+// Returns 1 when the pipelined prefill was launched, 0 when the caller should use
+// mfma_w4 (the workspace would have to grow while the stream is being captured),
+// or a negative value on a launch error (last error set).
+int launch_pipe(Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
+{
+    const size_t need = (size_t)M * w.K * 2;
+    uint32_t* ws = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(w.ws_mu);
+        if (w.a16_bytes < need) {
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+                (void)hipGetLastError();
+                return 0;
+            }
+            if (w.d_a16) {
+                if (hipStreamSynchronize(stream) != hipSuccess || hipFree(w.d_a16) != hipSuccess) return -1;
+            }
+            w.d_a16 = nullptr;
+            w.a16_bytes = 0;
+            if (hipMalloc(&w.d_a16, need) != hipSuccess) return -1;
+            w.a16_bytes = need;
+        }
+        ws = w.d_a16;
+    }
+    static std::atomic<bool> lds_raised{false};
+    if (!lds_raised.load()) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(mfma_w4_pipe_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, kPipeLdsBytes) != hipSuccess)
+            return -1;
+        lds_raised.store(true);
+    }
+    const int64_t n8 = (int64_t)M * w.K / 8;
+    hipLaunchKernelGGL(a_to_f16_kernel, dim3((unsigned)std::min<int64_t>((n8 + 255) / 256, 4096)), dim3(256), 0,
+                       stream, dA, ws, n8);
+    PipeParams p;
+    p.b = w.d_b;
+    p.scales = w.d_scales;
+    p.zp = w.has_zp ? w.d_zp : nullptr;
+    p.a16 = reinterpret_cast<const _Float16*>(ws);
+    p.y = dY;
+    p.row_bytes = (int)w.row_bytes;
+    p.M = M;
+    p.N = w.N;
+    p.K = w.K;
+    p.C = w.K / 32;
+    p.nb = w.nb;
+    p.zrb = w.zrb;
+    p.tiles_m = (M + kPipeBM - 1) / kPipeBM;
+    p.tiles_n = (w.N + kPipeBN - 1) / kPipeBN;
+    const int tiles = p.tiles_m * p.tiles_n;
+    hipLaunchKernelGGL(mfma_w4_pipe_kernel, dim3(((tiles + kXcds - 1) / kXcds) * kXcds), dim3(256), kPipeLdsBytes,
+                       stream, p);
+    return hipGetLastError() == hipSuccess ? 1 : -1;
+}
+
+int enqueue_gemm(Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
 {
     if (M < 0) return fail(MS_HIP_ERR_INVALID, "MatMulNBits M must be non-negative; got %d.", M);
     if (M == 0) return MS_HIP_OK;
@@ -413,6 +530,11 @@ int enqueue_gemm(const Weights& w, const float* dA, float* dY, int M, hipStream_
         return fail(MS_HIP_ERR_INVALID, "[ms_hip] A must be 16-byte and Y 4-byte aligned");
     if (!w.fast) return launch_generic(w, dA, dY, M, stream);
     if (M <= kPanelMaxM) return launch_gemv(w, dA, dY, M, stream);
+    if (pipe_eligible(w, M)) {
+        const int r = launch_pipe(w, dA, dY, M, stream);
+        if (r < 0) return fail(MS_HIP_ERR_HIP, "[ms_hip] prefill launch failed: %s", hipGetErrorString(hipGetLastError()));
+        if (r > 0) return MS_HIP_OK;
+    }
     return launch_mfma(w.d_b, w.d_scales, w.has_zp ? w.d_zp : nullptr, w.row_bytes, w.N, w.K, w.nb,
                        w.zrb, w.log2cpb, dA, dY, M, stream)
                ? fail(MS_HIP_ERR_HIP, "[ms_hip] MFMA launch failed: %s", hipGetErrorString(hipGetLastError()))
@@ -512,6 +634,7 @@ int ms_hip_nbits_weights_create(const uint8_t* bq, int64_t bq_len, const float* 
         if (e == hipSuccess && zero_points)
             e = hipMemcpy(w.d_zp, zero_points, (size_t)N * w.zrb, hipMemcpyHostToDevice);
         if (e != hipSuccess) st = fail(MS_HIP_ERR_HIP, "[ms_hip] weight upload failed: %s", hipGetErrorString(e));
+        if (!st) st = check_pipe_scales(w);
     }
     if (st) {
         free_weights(w);
@@ -546,6 +669,7 @@ int ms_hip_nbits_weights_create_dev(const uint8_t* d_bq, const float* d_scales, 
         if (e == hipSuccess && d_zero_points)
             e = hipMemcpy(w.d_zp, d_zero_points, (size_t)N * w.zrb, hipMemcpyDeviceToDevice);
         if (e != hipSuccess) st = fail(MS_HIP_ERR_HIP, "[ms_hip] weight copy failed: %s", hipGetErrorString(e));
+        if (!st) st = check_pipe_scales(w);
     }
     if (st) {
         free_weights(w);
@@ -740,6 +864,10 @@ int ms_hip_set_tuning(int knob, int value)
             if (value < -1 || value > kNumGemvConfigs) break;
             g_gemv_config = value;
             return MS_HIP_OK;
+        case 2:
+            if (value != 0 && value != 1) break;
+            g_pipe_off = value;
+            return MS_HIP_OK;
         default: break;
     }
     return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid tuning knob %d = %d", knob, value);
@@ -771,6 +899,11 @@ int ms_hip_nbits_launch_info(void* handle, int M, int* kernel_id, int* lanes_per
             gr = s.grid;
             bl = kPanelThreads;
         }
+    } else if (pipe_eligible(*w, M)) {
+        kid = 4;
+        const int tiles = ((M + kPipeBM - 1) / kPipeBM) * ((w->N + kPipeBN - 1) / kPipeBN);
+        gr = ((tiles + kXcds - 1) / kXcds) * kXcds;
+        bl = 256;
     } else {
         kid = 2;
         mfma_launch_shape(w->N, M, &gr, &bl);

@@ -193,7 +193,7 @@ class NBitsWeights:
         k, g, gr, bl = (ctypes.c_int() for _ in range(4))
         check(load().ms_hip_nbits_launch_info(self.handle, int(M), ctypes.byref(k), ctypes.byref(g),
                                               ctypes.byref(gr), ctypes.byref(bl)))
-        return {"kernel": ("generic", "gemv_w4", "mfma_w4", "gemv_w4_panel")[k.value], "lanes_per_row": g.value,
+        return {"kernel": ("generic", "gemv_w4", "mfma_w4", "gemv_w4_panel", "mfma_w4_pipe")[k.value], "lanes_per_row": g.value,
                 "grid": gr.value, "block": bl.value}
 
     def close(self) -> None:

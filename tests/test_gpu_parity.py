@@ -223,7 +223,7 @@ def test_edge_shapes(gpu, op, M):
     ref = oracle.matmul_nbits(a, b, s, z, op.N, op.K, op.bits, op.block_size)
     y = w.gemm(a)
     W = oracle.dequant_weights(b, s, z, op.N, op.K, op.bits, op.block_size)
-    if w.launch_info(M)["kernel"] == "mfma_w4":
+    if w.launch_info(M)["kernel"] in ("mfma_w4", "mfma_w4_pipe"):
         assert_fro_close(y, ref, f"{op.name} M={M}")
     else:
         assert_gemv_close(y, ref, f"{op.name} M={M}", cond=fp32_dot_bound(a, W))
@@ -245,7 +245,7 @@ def test_mfma_parity_sampled_columns(gpu, op, M):
     """Full-size call; the oracle checks a seeded sample of 96 output columns."""
     b, s, z, w = weights_for(op, seed=M + op.N)
     a = workloads.make_activations(M, op.K, seed=M, kind="rmsnorm")
-    assert w.launch_info(M)["kernel"] == "mfma_w4"
+    assert w.launch_info(M)["kernel"] == "mfma_w4_pipe"
     log(f"mfma M={M} K={op.K} N={op.N}")
     y = w.gemm(a)
     cols = np.sort(np.random.default_rng(M).choice(op.N, 96, replace=False))
@@ -258,11 +258,71 @@ def test_mfma_parity_sampled_columns(gpu, op, M):
 
 @pytest.mark.parametrize("M", [17, 33, 64, 100, 129, 300])
 def test_mfma_partial_tiles(gpu, M):
+    """Both prefill kernels on tiles cut by M and N (N=333 is not a multiple of 256)."""
     op = workloads.Op("pt", 896, 333, 32, True)
     b, s, z, w = weights_for(op, seed=M)
     a = workloads.make_activations(M, op.K, seed=M, kind="rmsnorm")
-    log(f"mfma partial M={M} N={op.N}")
-    assert_fro_close(w.gemm(a), oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, 32), f"M={M}")
+    ref = oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, 32)
+    assert w.launch_info(M)["kernel"] == "mfma_w4_pipe"
+    log(f"mfma partial M={M} N={op.N} {w.launch_info(M)}")
+    assert_fro_close(w.gemm(a), ref, f"pipe M={M}")
+    try:
+        native.set_tuning(2, 1)
+        assert w.launch_info(M)["kernel"] == "mfma_w4"
+        assert_fro_close(w.gemm(a), ref, f"mfma_w4 M={M}")
+    finally:
+        native.set_tuning(2, 0)
+    w.close()
+
+
+@pytest.mark.parametrize("op,kernel", [
+    (workloads.Op("bs128", 1024, 300, 128, False), "mfma_w4"),    # block size 128
+    (workloads.Op("k96", 96, 200, 32, True), "mfma_w4"),          # K not a multiple of 128
+    (workloads.Op("k640", 640, 260, 32, False), "mfma_w4_pipe"),  # no zero points
+], ids=lambda v: v.name if hasattr(v, "name") else v)
+def test_prefill_kernel_choice(gpu, op, kernel):
+    b, s, z, w = weights_for(op, seed=op.K)
+    a = workloads.make_activations(70, op.K, seed=3, kind="rmsnorm")
+    assert w.launch_info(70)["kernel"] == kernel
+    log(f"prefill {op.name} {w.launch_info(70)}")
+    assert_fro_close(w.gemm(a), oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, op.block_size), op.name)
+    w.close()
+
+
+def test_prefill_scale_range_fallback(gpu):
+    """Scales outside the fp16-normal range send the call to mfma_w4 (fp32 dequant)."""
+    op = workloads.Op("tiny", 512, 96, 32, True)
+    b, s, z = workloads.make_weights(op, 4)
+    s = s.copy()
+    s[::7] = 3e-6          # below 2^-14
+    w = native.NBitsWeights(b, s, z, op.N, op.K, 4, 32)
+    a = workloads.make_activations(40, op.K, seed=5, kind="rmsnorm")
+    assert w.launch_info(40)["kernel"] == "mfma_w4"
+    assert_fro_close(w.gemm(a), oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, 32), "tiny scales")
+    w.close()
+
+
+def test_prefill_captured_before_eager_call(gpu):
+    """A prefill call captured in a graph before any eager call (no activation
+    workspace yet) runs the workspace-free kernel; every replay matches."""
+    import torch
+    op = workloads.Op("cap", 1024, 512, 32, True)
+    b, s, z, w = weights_for(op, seed=6)
+    a = workloads.make_activations(96, op.K, seed=7, kind="rmsnorm")
+    ref = oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, 32)
+    dA = torch.from_numpy(a).cuda()
+    dY = torch.zeros((96, op.N), dtype=torch.float32, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        w.gemm_dev(dA.data_ptr(), dY.data_ptr(), 96, torch.cuda.current_stream().cuda_stream)
+    for i in range(3):
+        dY.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert_fro_close(dY.cpu().numpy(), ref, f"replay {i}")
+    eager = w.gemm(a)           # grows the workspace, takes the pipelined kernel
+    assert_fro_close(eager, ref, "eager")
     w.close()
 
 
