@@ -102,15 +102,27 @@ def time_graph(g, replays, warmup):
 TRAFFIC_PROFILE = "profiles/gemv_w4_gate_7b_hbm_traffic.json"
 
 
+def kernel_source_digest() -> str:
+    """sha256 over the device sources, so a profile is used only for the code it measured."""
+    import hashlib
+    h = hashlib.sha256()
+    for f in sorted((ROOT / "modelsharp_amd" / "csrc").glob("*")):
+        if f.suffix in (".h", ".hip"):
+            h.update(f.name.encode())
+            h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
 def measured_traffic(launch):
     """HBM bytes per gate/up launch from the committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE passes (scaled by a plain copy's counters), used only when that
-    profile was taken on the kernel configuration this run launches."""
+    profile was taken on the same kernel sources and launch configuration."""
     path = ROOT / TRAFFIC_PROFILE
     if not path.is_file():
         return None
     prof = json.loads(path.read_text())
-    same = all(prof.get(k) == launch.get(k) for k in ("kernel", "lanes_per_row", "grid", "block"))
+    same = prof.get("source_digest") == kernel_source_digest() and \
+        all(prof.get(k) == launch.get(k) for k in ("kernel", "lanes_per_row", "grid", "block"))
     return prof["traffic_bytes"] if same else None
 
 
@@ -154,8 +166,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget (0 = skip)")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--detail", default="", help="also write per-op results of every workload to this JSON file")
-    ap.add_argument("--op", default="", help="profiling mode: launch only this 7B decode op (q,k,v,o,gate,up,down), "
-                                             "eagerly over the rotation, then a plain copy of --copy-mib; no JSON line")
+    ap.add_argument("--op", default="", help="profiling mode: launch only this 7B decode op (q,k,v,o,gate,up,down) "
+                                             "or prefill_up / prefill_down (M=2048), eagerly over the rotation, then a "
+                                             "plain copy of --copy-mib; no JSON line")
     ap.add_argument("--calls", type=int, default=64, help="launches in --op mode")
     ap.add_argument("--copy-mib", type=int, default=256, help="size of the calibration copy in --op mode")
     args = ap.parse_args()
@@ -290,16 +303,22 @@ def profile_op(args) -> int:
     counters calibrate the byte counts."""
     import torch
     from modelsharp_amd import workloads
-    op = next(o for o in workloads.DECODE_7B if o.name == args.op)
-    fp = workloads.algorithmic_bytes(op, 1)
-    copies = workloads.rotation_copies(fp, args.rotate_mib << 20)
-    rot = Rotation([op], 1, copies, seed=7)
+    if args.op.startswith("prefill_"):
+        op = next(o for o in workloads.LLAMA7B_PREFILL_OPS if o.name == args.op[len("prefill_"):])
+        M, copies, kind = 2048, 2, "rmsnorm"
+    else:
+        op = next(o for o in workloads.DECODE_7B if o.name == args.op)
+        M, kind = 1, "normal"
+        copies = workloads.rotation_copies(workloads.algorithmic_bytes(op, 1), args.rotate_mib << 20)
+    fp = workloads.algorithmic_bytes(op, M)
+    rot = Rotation([op], M, copies, seed=7, kind=kind)
     stream = torch.cuda.current_stream().cuda_stream
     for i in range(args.calls):
         rot.enqueue(i % copies, stream)
     torch.cuda.synchronize()
-    log(f"{args.calls} launches of {op.name} (K={op.K}, N={op.N}, {fp} algorithmic bytes each), "
-        f"{copies} rotating copies")
+    log(f"{args.calls} launches of {op.name} (M={M}, K={op.K}, N={op.N}, {fp} algorithmic bytes, "
+        f"{workloads.flops(op, M)} flops each), {copies} rotating copies; launch {rot.handles[0][0].launch_info(M)}; "
+        f"kernel sources {kernel_source_digest()}")
     src = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(4):
