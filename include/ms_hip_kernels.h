@@ -88,8 +88,10 @@ int ms_hip_nbits_gemm(void* handle, const float* a_host, float* y_host, int M);
 /* Device-pointer form: enqueues on `stream` (a hipStream_t, NULL = the null
  * stream) and returns without synchronising. dA: [M,K] fp32, dY: [M,N] fp32,
  * both 16-byte aligned device memory. Prefill calls (M > 16) stage A as fp16 in
- * a workspace owned by the handle (grown on demand, never while `stream` is being
- * captured: a call under capture that would need a larger one takes the
+ * a workspace owned by the handle, and launches with few output tiles split K over
+ * two workgroups per tile that meet through the handle's per-tile counters and
+ * partial-sum slots. These buffers grow on demand, never while `stream` is being
+ * captured (a call under capture that would need larger ones takes the
  * workspace-free MFMA kernel instead), so prefill calls on one handle from
  * different streams must not overlap. */
 int ms_hip_nbits_gemm_dev(void* handle, const float* dA, float* dY, int M, void* stream);
@@ -128,7 +130,8 @@ int ms_hip_sync(void);
  *   0 gemv_w4_panel lanes per row;
  *   1 gemv_w4 launch configuration: c+1 forces configuration c of the library's
  *     table (used only where it fits the shape), -1 forces gemv_w4_panel;
- *   2 1 routes every M > 16 call to mfma_w4 (the pipelined prefill off).
+ *   2 1 routes every M > 16 call to mfma_w4 (the pipelined prefill off);
+ *   3 1 or 2 forces the pipelined prefill's K split (2 needs K >= 256).
  * ms_hip_nbits_launch_info reports what a call with M rows would launch:
  *   kernel_id 0 generic, 1 gemv_w4, 2 mfma_w4, 3 gemv_w4_panel, 4 mfma_w4_pipe. */
 int ms_hip_set_gemv_lanes(int lanes_per_row);

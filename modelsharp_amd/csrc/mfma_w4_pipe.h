@@ -1,5 +1,6 @@
 // mfma_w4_pipe.h — INT4 MatMulNBits prefill GEMM on the CDNA4 matrix cores with a
-// buffer->LDS load pipeline (M > 16, block size 32, K a multiple of 128).
+// buffer->LDS load pipeline (M > 16, block size 32, K a multiple of 128), optionally
+// with each tile's K range split over two workgroups.
 //
 // Y[M,N] = A[M,K] * W[N,K]^T, W = (q - zp) * s dequantized in-kernel.
 //
@@ -32,6 +33,11 @@
 //       s+1 interleaves with the MFMAs of step s.
 //     * One barrier per step. Tile order is XCD-aware (workgroup b runs on XCD
 //       b % 8; each XCD walks an m-major range of tiles, sharing A panels in L2).
+//     * Split K (ksplit = 2, for launches with too few tiles to fill the CUs): the
+//       two halves of a tile (whole groups of 4 steps each) are neighbouring work
+//       items; the first to finish stores its partial sums into Y and raises a
+//       flag, the second stores its own into a workspace slot and then adds the
+//       slot into Y (deterministic: fp32 a + b == b + a).
 // Numerics: A rounded once to fp16; W = fl16((q - zp) * fl16(s)); products exact,
 // sums fp32. Requires |A| < 65504 (fp16 range) and fp16-normal scales for the
 // 2^-11 relative bound; the library routes other inputs to mfma_w4.
@@ -48,6 +54,9 @@ struct PipeParams {
     float* y;                // [M][N]
     int row_bytes, M, N, K, C, nb, zrb;
     int tiles_m, tiles_n;
+    int ksplit;              // 1, or 2: each tile's K range is split over two workgroups
+    int* sync;               // ksplit 2: [tiles][2] arrival counter and ready flag, all zero
+    float* part;             // ksplit 2: [tiles][kPipeBM * kPipeBN] partial sums
 };
 
 constexpr int kPipeBM = 256, kPipeBN = 256;
@@ -117,8 +126,13 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
     const uint32_t lbase = lds_address(lds);
 
     const int tiles = p.tiles_m * p.tiles_n;
-    const int tile = xcd_tile(blockIdx.x, tiles);
-    if (tile >= tiles) return;
+    // The two K halves of a tile are neighbouring work items, so they land on the same XCD.
+    const int item = xcd_tile(blockIdx.x, tiles * p.ksplit);
+    if (item >= tiles * p.ksplit) return;
+    const int tile = item / p.ksplit, kpart = item - tile * p.ksplit;
+    // Steps [c0, c0 + nsteps) of this work item; both halves are whole groups of 4 steps.
+    const int groups = p.C >> 2, g0 = kpart * (groups >> 1);
+    const int c0 = 4 * g0, nsteps = 4 * (p.ksplit == 1 ? groups : kpart == 0 ? (groups >> 1) : groups - g0);
     const int m0 = (tile / p.tiles_n) * BM, n0 = (tile % p.tiles_n) * BN;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int wm = wave & 1, wn = wave >> 1;
@@ -134,15 +148,15 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
     for (int q = 0; q < 4; ++q) {
         const int r = wave * 64 + 16 * q + (lane >> 2);
         const int m = m0 + r;
-        avo[q] = m < p.M ? m * p.K * 2 + pipe_slot(r, lane & 3) * 16 : kPipeFar;
+        avo[q] = m < p.M ? m * p.K * 2 + c0 * 64 + pipe_slot(r, lane & 3) * 16 : kPipeFar;
         const int n = n0 + r;
-        cvo[q] = n < p.N ? n * p.row_bytes + (lane & 3) * 16 : kPipeFar;
+        cvo[q] = n < p.N ? n * p.row_bytes + c0 * 16 + (lane & 3) * 16 : kPipeFar;
     }
     const int brow = wave * 64 + lane;   // the weight row this lane loads scales for and dequantizes
     const int bn = n0 + brow;
-    const int svo = bn < p.N ? bn * p.nb * 4 : kPipeFar;
-    const int zvo = bn < p.N ? bn * p.zrb : kPipeFar;
-    const int last = p.C - 1;
+    const int svo = bn < p.N ? bn * p.nb * 4 + c0 * 4 : kPipeFar;
+    const int zvo = bn < p.N ? bn * p.zrb + c0 / 2 : kPipeFar;
+    const int last = nsteps - 1;
 
     auto issue_a = [&](int t, int st) {   // step t -> stage st (clamped: a prefetch past the end re-reads)
         const int tc = min(t, last);
@@ -232,7 +246,7 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
     dequant(raw, 0);
     raw = read_raw(1);
     lds_barrier();
-    for (int t = 0; t < p.C; t += 4) {
+    for (int t = 0; t < nsteps; t += 4) {
         wait_vmcnt<4>();                 // A(t+1): after it A(t+2)
         Raw rn = read_raw(t + 2);
         mma(0, 0);
@@ -266,20 +280,89 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
     wait_vmcnt<0>();
 
     // acc[i][j][v] is Y[row][col], col = lane % 32, row = 8*(v/4) + 4*(lane/32) + v%4.
+    // Stores go through a buffer resource with an offset that has bit 30 set outside the
+    // valid rows/columns (every destination is smaller than 2^30 bytes, checked by the
+    // host): such stores are dropped, so the epilogue has no branches. The destination
+    // is runtime data: the tile (rb, cb) of an ld-wide matrix with rl x cl valid entries.
+    auto store_tile = [&](__amdgpu_buffer_rsrc_t rd, int ld, int rb, int cb, int rl, int cl) {
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-        const int mrow0 = m0 + wm * 128 + 32 * i + 4 * lh;
+        for (int i = 0; i < FM; ++i) {
+            const int row0 = wm * 128 + 32 * i + 4 * lh;
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const int col = n0 + wn * 128 + 32 * j + lr;
-            if (col < p.N) {
+            for (int j = 0; j < FN; ++j) {
+                const int col = wn * 128 + 32 * j + lr;
+                const uint32_t base = ((uint32_t)(rb + row0) * (uint32_t)ld + (uint32_t)(cb + col)) * 4u;
+                const int cfree = cl - 1 - col;
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
-                    const int row = mrow0 + 8 * (v >> 2) + (v & 3);
-                    if (row < p.M) p.y[(int64_t)row * p.N + col] = acc[i][j][v];
+                    const int rv = 8 * (v >> 2) + (v & 3);
+                    const uint32_t outside = (uint32_t)(((rl - 1 - row0 - rv) | cfree) >> 31);   // all ones outside
+                    const int off = (int)((base + (uint32_t)(rv * 4) * (uint32_t)ld) | (outside & (uint32_t)kPipeFar));
+                    const float x = acc[i][j][v];   // bit_cast of a vector element would read element 0
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x), rd, off, 0, 0);
                 }
             }
         }
+    };
+    const __amdgpu_buffer_rsrc_t ry = buffer_rsrc(p.y, p.M * p.N * 4);
+    const int rl = p.M - m0, cl = p.N - n0;   // valid rows / columns of this tile
+    if (p.ksplit == 1) {
+        store_tile(ry, p.N, m0, n0, rl, cl);
+        return;
+    }
+    // Two halves: the first to arrive stores its partial sums into Y, the second into
+    // its tile's slot of the partials workspace; once the first has raised the tile's
+    // flag the second adds the slot into Y. Y = p0 + p1 either way (fp32 addition
+    // commutes), so the result does not depend on the arrival order. The second waits
+    // only for a workgroup that has already arrived (and is therefore running), so the
+    // wait ends.
+    __shared__ int arrival;
+    int* const cnt = p.sync + 2 * tile;
+    if (threadIdx.x == 0) arrival = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const bool second = arrival != 0;
+    float* const slot = p.part + (int64_t)tile * (BM * BN);
+    const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(slot, BM * BN * 4);
+    if (!second) {
+        store_tile(ry, p.N, m0, n0, rl, cl);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        __syncthreads();
+        if (threadIdx.x == 0) __hip_atomic_store(cnt + 1, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    store_tile(rs, BN, 0, 0, rl, cl);
+    if (threadIdx.x == 0) {
+        // Bounded: the first half is running and needs no other workgroup to finish, so
+        // the flag comes within microseconds; the bound only keeps a misuse (two launches
+        // on one handle overlapping) from hanging the device.
+        for (int spin = 0; spin < (1 << 22); ++spin) {
+            if (__hip_atomic_load(cnt + 1, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
+            __builtin_amdgcn_s_sleep(2);
+        }
+        // Both halves are past their use of the pair: leave it zero for the next launch.
+        __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(cnt + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();   // also orders this workgroup's slot stores before its slot loads
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // Y[m0 + r][n0 + c] += slot[r][c]: thread t takes columns c = t, one row per pass.
+    const int c = threadIdx.x;
+    const uint32_t cfar = (uint32_t)((cl - 1 - c) >> 31) & (uint32_t)kPipeFar;
+    for (int r0 = 0; r0 < BM; r0 += 16) {
+        float yv[16], sv[16];
+        int yo[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int r = r0 + u;
+            const uint32_t far = cfar | ((uint32_t)((rl - 1 - r) >> 31) & (uint32_t)kPipeFar);
+            yo[u] = (int)((((uint32_t)(m0 + r) * (uint32_t)p.N + (uint32_t)(n0 + c)) * 4u) | far);
+            sv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                  rs, (int)(((uint32_t)(r * BN + c) * 4u) | far), 0, 0));
+            yv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ry, yo[u], 0, 0));
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, yv[u] + sv[u]), ry, yo[u], 0, 0);
     }
 }
 

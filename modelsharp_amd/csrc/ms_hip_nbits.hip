@@ -115,6 +115,9 @@ struct Weights {
     std::mutex ws_mu;
     uint32_t* d_a16 = nullptr;
     size_t a16_bytes = 0;
+    int* d_sync = nullptr;      // split-K arrival counters and flags, zero between launches
+    float* d_part = nullptr;    // split-K partial sums, kPipeBM x kPipeBN floats per tile
+    int sync_tiles = 0;         // tiles covered by d_sync and d_part
 };
 
 constexpr uint32_t kHandleMagic = 0x4D534E42u;   // "MSNB"
@@ -172,6 +175,8 @@ void free_weights(Weights& w)
     if (w.d_zp) (void)hipFree(w.d_zp);
     if (w.d_stage) (void)hipFree(w.d_stage);
     if (w.d_a16) (void)hipFree(w.d_a16);
+    if (w.d_sync) (void)hipFree(w.d_sync);
+    if (w.d_part) (void)hipFree(w.d_part);
     if (w.stream) (void)hipStreamDestroy(w.stream);
     w.d_b = nullptr;
     w.d_scales = nullptr;
@@ -179,6 +184,9 @@ void free_weights(Weights& w)
     w.d_stage = nullptr;
     w.d_a16 = nullptr;
     w.a16_bytes = 0;
+    w.d_sync = nullptr;
+    w.d_part = nullptr;
+    w.sync_tiles = 0;
     w.stream = nullptr;
 }
 
@@ -228,6 +236,7 @@ int check_pipe_scales(Weights& w)
 int g_panel_lanes_override = 0;  // knob 0: gemv_w4_panel lanes per row
 int g_gemv_config = 0;           // knob 1: c+1 forces kGemvConfigs[c], -1 forces gemv_w4_panel
 int g_pipe_off = 0;              // knob 2: 1 routes every prefill call to mfma_w4
+int g_pipe_ksplit = 0;           // knob 3: 1 or 2 forces the prefill K split (where K allows 2)
 
 // gemv_w4 instantiations: [M-1][L slot][config], L slot 0 = block size 32, 1 = block size 128.
 typedef void (*GemvFn)(GemvParams);
@@ -457,12 +466,39 @@ int launch_generic(const Weights& w, const float* dA, float* dY, int M, hipStrea
 }
 
 // The pipelined prefill takes M > 16, block size 32, K a multiple of 128, fp16-safe
-// scales, and buffers below kPipeFar (its out-of-range row offset).
+// scales, and buffers (Y included) below kPipeFar (its out-of-range offset).
 bool pipe_eligible(const Weights& w, int M)
 {
     return !g_pipe_off && w.fast && M > kPanelMaxM && w.log2cpb == 0 && (w.K % 128) == 0 && w.pipe_scales_ok &&
            (int64_t)w.N * w.row_bytes < kPipeFar && (int64_t)M * w.K * 2 < kPipeFar &&
-           (int64_t)w.N * w.nb * 4 < kPipeFar;
+           (int64_t)w.N * w.nb * 4 < kPipeFar && (int64_t)M * w.N * 4 < kPipeFar;
+}
+
+// Compute units of the current device (the launch heuristics' notion of "filled").
+int device_cus()
+{
+    static std::atomic<int> cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int v = cached[dev].load();
+    if (v == 0) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cached[dev].store(v);
+    }
+    return v;
+}
+
+// K split of the pipelined prefill: 2 when the tiles fill at most half of the compute
+// units (measured: at 128 tiles on 256 CUs the split takes K=11008 from 328 to 268 us;
+// at 344 tiles splitting to 688 items is slower than 1.34 rounds of whole tiles). It
+// needs two groups of 4 steps (K >= 256).
+int pipe_ksplit(const Weights& w, int M)
+{
+    const int groups = w.K / 128;
+    if (groups < 2) return 1;
+    if (g_pipe_ksplit) return g_pipe_ksplit;
+    const int64_t tiles = (int64_t)((M + kPipeBM - 1) / kPipeBM) * ((w.N + kPipeBN - 1) / kPipeBN);
+    return 2 * tiles <= device_cus() ? 2 : 1;
 }
 
 // Returns 1 when the pipelined prefill was launched, 0 when the caller should use
@@ -471,24 +507,47 @@ bool pipe_eligible(const Weights& w, int M)
 int launch_pipe(Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
 {
     const size_t need = (size_t)M * w.K * 2;
+    const int tiles_m = (M + kPipeBM - 1) / kPipeBM, tiles_n = (w.N + kPipeBN - 1) / kPipeBN;
+    const int tiles = tiles_m * tiles_n;
+    const int ksplit = pipe_ksplit(w, M);
     uint32_t* ws = nullptr;
+    int* sync = nullptr;
+    float* part = nullptr;
     {
         std::lock_guard<std::mutex> lock(w.ws_mu);
-        if (w.a16_bytes < need) {
+        const bool grow_ws = w.a16_bytes < need, grow_sync = ksplit > 1 && w.sync_tiles < tiles;
+        if (grow_ws || grow_sync) {
             hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
             if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
                 (void)hipGetLastError();
                 return 0;
             }
-            if (w.d_a16) {
-                if (hipStreamSynchronize(stream) != hipSuccess || hipFree(w.d_a16) != hipSuccess) return -1;
-            }
+            if (hipStreamSynchronize(stream) != hipSuccess) return -1;
+        }
+        if (grow_ws) {
+            if (w.d_a16 && hipFree(w.d_a16) != hipSuccess) return -1;
             w.d_a16 = nullptr;
             w.a16_bytes = 0;
             if (hipMalloc(&w.d_a16, need) != hipSuccess) return -1;
             w.a16_bytes = need;
         }
+        if (grow_sync) {
+            // The pairs are zeroed once here; every split launch leaves its pairs zero again.
+            if (w.d_sync && hipFree(w.d_sync) != hipSuccess) return -1;
+            if (w.d_part && hipFree(w.d_part) != hipSuccess) return -1;
+            w.d_sync = nullptr;
+            w.d_part = nullptr;
+            w.sync_tiles = 0;
+            if (hipMalloc(&w.d_sync, (size_t)tiles * 2 * sizeof(int)) != hipSuccess) return -1;
+            // On the launch stream: a null-stream memset is not ordered before work on a
+            // non-blocking stream. (Never reached under capture: checked above.)
+            if (hipMemsetAsync(w.d_sync, 0, (size_t)tiles * 2 * sizeof(int), stream) != hipSuccess) return -1;
+            if (hipMalloc(&w.d_part, (size_t)tiles * kPipeBM * kPipeBN * sizeof(float)) != hipSuccess) return -1;
+            w.sync_tiles = tiles;
+        }
         ws = w.d_a16;
+        sync = w.d_sync;
+        part = w.d_part;
     }
     static std::atomic<bool> lds_raised{false};
     if (!lds_raised.load()) {
@@ -513,10 +572,13 @@ int launch_pipe(Weights& w, const float* dA, float* dY, int M, hipStream_t strea
     p.C = w.K / 32;
     p.nb = w.nb;
     p.zrb = w.zrb;
-    p.tiles_m = (M + kPipeBM - 1) / kPipeBM;
-    p.tiles_n = (w.N + kPipeBN - 1) / kPipeBN;
-    const int tiles = p.tiles_m * p.tiles_n;
-    hipLaunchKernelGGL(mfma_w4_pipe_kernel, dim3(((tiles + kXcds - 1) / kXcds) * kXcds), dim3(256), kPipeLdsBytes,
+    p.tiles_m = tiles_m;
+    p.tiles_n = tiles_n;
+    p.ksplit = ksplit;
+    p.sync = sync;
+    p.part = part;
+    const int items = tiles * ksplit;
+    hipLaunchKernelGGL(mfma_w4_pipe_kernel, dim3(((items + kXcds - 1) / kXcds) * kXcds), dim3(256), kPipeLdsBytes,
                        stream, p);
     return hipGetLastError() == hipSuccess ? 1 : -1;
 }
@@ -868,6 +930,10 @@ int ms_hip_set_tuning(int knob, int value)
             if (value != 0 && value != 1) break;
             g_pipe_off = value;
             return MS_HIP_OK;
+        case 3:
+            if (value < 0 || value > 2) break;
+            g_pipe_ksplit = value;
+            return MS_HIP_OK;
         default: break;
     }
     return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid tuning knob %d = %d", knob, value);
@@ -901,8 +967,8 @@ int ms_hip_nbits_launch_info(void* handle, int M, int* kernel_id, int* lanes_per
         }
     } else if (pipe_eligible(*w, M)) {
         kid = 4;
-        const int tiles = ((M + kPipeBM - 1) / kPipeBM) * ((w->N + kPipeBN - 1) / kPipeBN);
-        gr = ((tiles + kXcds - 1) / kXcds) * kXcds;
+        const int items = ((M + kPipeBM - 1) / kPipeBM) * ((w->N + kPipeBN - 1) / kPipeBN) * pipe_ksplit(*w, M);
+        gr = ((items + kXcds - 1) / kXcds) * kXcds;
         bl = 256;
     } else {
         kid = 2;

@@ -256,22 +256,57 @@ def test_mfma_parity_sampled_columns(gpu, op, M):
     w.close()
 
 
+def pipe_items(M, N, ksplit):
+    """Workgroups the pipelined prefill launches: 256x256 tiles times the K split, in whole XCD rounds."""
+    items = -(-M // 256) * -(-N // 256) * ksplit
+    return -(-items // 8) * 8
+
+
 @pytest.mark.parametrize("M", [17, 33, 64, 100, 129, 300])
 def test_mfma_partial_tiles(gpu, M):
-    """Both prefill kernels on tiles cut by M and N (N=333 is not a multiple of 256)."""
+    """Both prefill kernels, and the pipelined one with and without the K split, on
+    tiles cut by M and N (N=333 is not a multiple of 256; K=896 is 7 groups of 4
+    steps, so the two K halves are unequal: 3 and 4 groups)."""
     op = workloads.Op("pt", 896, 333, 32, True)
     b, s, z, w = weights_for(op, seed=M)
     a = workloads.make_activations(M, op.K, seed=M, kind="rmsnorm")
     ref = oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, 32)
-    assert w.launch_info(M)["kernel"] == "mfma_w4_pipe"
-    log(f"mfma partial M={M} N={op.N} {w.launch_info(M)}")
-    assert_fro_close(w.gemm(a), ref, f"pipe M={M}")
     try:
+        for ks in (1, 2):
+            native.set_tuning(3, ks)
+            info = w.launch_info(M)
+            assert info["kernel"] == "mfma_w4_pipe" and info["grid"] == pipe_items(M, op.N, ks)
+            log(f"mfma partial M={M} N={op.N} ksplit={ks} {info}")
+            assert_fro_close(w.gemm(a), ref, f"pipe ksplit={ks} M={M}")
+        native.set_tuning(3, 0)
         native.set_tuning(2, 1)
         assert w.launch_info(M)["kernel"] == "mfma_w4"
         assert_fro_close(w.gemm(a), ref, f"mfma_w4 M={M}")
     finally:
         native.set_tuning(2, 0)
+        native.set_tuning(3, 0)
+    w.close()
+
+
+def test_prefill_split_k_deterministic(gpu):
+    """The K-split prefill (two workgroups per tile, combined by arrival order) gives
+    bit-identical results on every call, and matches the unsplit launch to the bar."""
+    op = workloads.Op("sk", 4096, 1000, 32, True)
+    b, s, z, w = weights_for(op, seed=21)
+    a = workloads.make_activations(300, op.K, seed=22, kind="rmsnorm")
+    ref = oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, 32)
+    assert w.launch_info(300)["grid"] == pipe_items(300, op.N, 2)   # 8 tiles: split by default
+    y0 = w.gemm(a)
+    assert_fro_close(y0, ref, "split")
+    for i in range(4):
+        assert np.array_equal(w.gemm(a), y0), i
+    try:
+        native.set_tuning(3, 1)
+        y1 = w.gemm(a)
+    finally:
+        native.set_tuning(3, 0)
+    assert_fro_close(y1, ref, "unsplit")
+    assert_fro_close(y0, y1, "split vs unsplit")
     w.close()
 
 
@@ -323,6 +358,20 @@ def test_prefill_captured_before_eager_call(gpu):
         assert_fro_close(dY.cpu().numpy(), ref, f"replay {i}")
     eager = w.gemm(a)           # grows the workspace, takes the pipelined kernel
     assert_fro_close(eager, ref, "eager")
+    # Captured again now that the workspace exists: the pipelined kernel with its
+    # K split (4 tiles) runs in the graph; its arrival counters reset themselves,
+    # so every replay equals the eager call bit for bit.
+    assert w.launch_info(96)["grid"] == pipe_items(96, op.N, 2)
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2):
+        w.gemm_dev(dA.data_ptr(), dY.data_ptr(), 96, torch.cuda.current_stream().cuda_stream)
+    for i in range(3):
+        dY.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g2.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(dY.cpu().numpy(), eager), f"split replay {i}"
+        assert np.array_equal(w.gemm(a), eager), f"eager after replay {i}"
     w.close()
 
 
