@@ -15,22 +15,25 @@
 //       128x128 as 4x4 v_mfma_f32_32x32x16_f16 fragments accumulating in AGPRs.
 //       A step is 32 k (one block of 32 codes per weight row).
 //     * Every global load of the main loop is a buffer->LDS load
-//       (buffer_load_dword{,x4} ... lds) issued from inline asm, so no vector
+//       (buffer_load_{ushort,dwordx4} ... lds) issued from inline asm, so no vector
 //       register waits on memory and the compiler inserts no conservative
 //       s_waitcnt for them; each wait is an explicit vmcnt count that follows
 //       from the issue order below (which is why the loop is unrolled by 4).
 //         - A: 4 LDS stages of one step (256 rows x 64 B, 16-byte chunks XOR-
 //           swizzled per row against bank conflicts), issued 3 steps ahead;
 //         - weights: per group of 4 steps, 64 B of codes, 16 B of scales and
-//           2 zero-point bytes per row (two groups double-buffered), so a row's
-//           codes for 4 steps are one contiguous 64-byte request.
+//           2 zero-point bytes per row, in three buffers, issued two groups
+//           ahead, so a row's codes for 4 steps are one contiguous 64-byte request.
 //     * Dequant: each lane owns one weight row of the tile (the rows its own wave
 //       loaded, so only a wave-local wait is needed). It turns 32 codes into fp16
 //       with packed-half math — the code in the mantissa of 1024.0 minus
 //       (1024 + zp) is exactly q - zp, times the block scale rounded to fp16 —
-//       and writes them to a double-buffered fp16 weight tile. The raw codes of
-//       step s+2 are read into registers during step s, so the dequant of step
-//       s+1 interleaves with the MFMAs of step s.
+//       and writes them to a double-buffered fp16 weight tile.
+//     * Software pipeline inside a step: the MFMA operands of each half step are
+//       read from LDS under the MFMAs of the other half, and the dequant's VALU
+//       work and LDS traffic are interleaved one by one with the MFMAs
+//       (sched_group_barrier), since a wave keeps about 5 VALU instructions in
+//       the shadow of one 32-cycle MFMA.
 //     * One barrier per step. Tile order is XCD-aware (workgroup b runs on XCD
 //       b % 8; each XCD walks an m-major range of tiles, sharing A panels in L2).
 //     * Split K (ksplit = 2, for launches with too few tiles to fill the CUs): the
@@ -43,6 +46,7 @@
 // 2^-11 relative bound; the library routes other inputs to mfma_w4.
 #pragma once
 #include "mfma_w4.h"
+#include <type_traits>
 
 namespace msnb {
 
@@ -60,7 +64,7 @@ struct PipeParams {
 };
 
 constexpr int kPipeBM = 256, kPipeBN = 256;
-constexpr int kPipeLdsBytes = 4 * kPipeBM * 64 + 2 * (kPipeBN * 64 + kPipeBN * 16 + kPipeBN * 8) + 2 * kPipeBN * 64;
+constexpr int kPipeLdsBytes = 4 * kPipeBM * 64 + 3 * (kPipeBN * 64 + kPipeBN * 16 + kPipeBN * 4) + 2 * kPipeBN * 64;
 // Base offset of a row beyond the matrix: above every buffer the kernel reads
 // (the host checks each is smaller), so loads from it return zero.
 constexpr int kPipeFar = 0x40000000;
@@ -94,14 +98,14 @@ __device__ __forceinline__ void dequant8_f16(uint32_t x, h2_t zb, h2_t s2, uint3
 typedef __attribute__((address_space(3))) uint8_t lds_byte_t;
 __device__ __forceinline__ uint32_t lds_address(const void* p) { return (uint32_t)(uintptr_t)(lds_byte_t*)p; }
 
-// buffer -> LDS loads: lane i's bytes land at LDS m0 + 16*i (x4) or m0 + 4*i (dword, ubyte).
+// buffer -> LDS loads: lane i's bytes land at LDS m0 + 16*i (x4) or m0 + 4*i (ushort).
 __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, int voff, int soff, uint32_t m0v)
 {
     asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0v) : "memory");
 }
-__device__ __forceinline__ void lds_load1(__amdgpu_buffer_rsrc_t r, int voff, int soff, uint32_t m0v)
+__device__ __forceinline__ void lds_load2(__amdgpu_buffer_rsrc_t r, int voff, int soff, uint32_t m0v)
 {
-    asm volatile("buffer_load_ubyte %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0v) : "memory");
+    asm volatile("buffer_load_ushort %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0v) : "memory");
 }
 template <int N>
 __device__ __forceinline__ void wait_vmcnt()
@@ -117,9 +121,9 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
 {
     constexpr int BM = kPipeBM, BN = kPipeBN, FM = 4, FN = 4;
     constexpr int A_ST = BM * 64;                               // one step of A
-    constexpr int CG = BN * 64, SG = BN * 16, ZG = BN * 8;      // one group: codes, scales, zp
-    constexpr int OFF_A = 0, OFF_C = OFF_A + 4 * A_ST, OFF_S = OFF_C + 2 * CG, OFF_Z = OFF_S + 2 * SG,
-                  OFF_B = OFF_Z + 2 * ZG;
+    constexpr int CG = BN * 64, SG = BN * 16, ZG = BN * 4;      // one group: codes, scales, zp
+    constexpr int OFF_A = 0, OFF_C = OFF_A + 4 * A_ST, OFF_S = OFF_C + 3 * CG, OFF_Z = OFF_S + 3 * SG,
+                  OFF_B = OFF_Z + 3 * ZG;
     constexpr int B16_SZ = BN * 64;
     extern __shared__ __attribute__((aligned(16))) uint8_t pipe_lds[];
     uint8_t* const lds = pipe_lds;
@@ -170,24 +174,23 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
         for (int q = 0; q < 4; ++q)
             lds_load16(rb, cvo[q], gc * 64, lbase + OFF_C + buf * CG + (wave * 64 + 16 * q) * 64);
         lds_load16(rsc, svo, gc * 16, lbase + OFF_S + buf * SG + wave * 64 * 16);
-        lds_load1(rz, zvo, gc * 2, lbase + OFF_Z + buf * ZG + wave * 64 * 4);
-        lds_load1(rz, zvo, gc * 2 + 1, lbase + OFF_Z + buf * ZG + BN * 4 + wave * 64 * 4);
+        lds_load2(rz, zvo, gc * 2, lbase + OFF_Z + buf * ZG + wave * 64 * 4);
     };
     struct Raw {
         u32x4_t q;
         float s;
         uint32_t zb;
     };
-    auto read_raw = [&](int t) {
+    auto read_raw = [&](int t, int buf) {
         Raw r;
-        const int buf = (t >> 2) & 1, ph = t & 3;
+        const int ph = t & 3;
         r.q = *reinterpret_cast<const u32x4_t*>(lds + OFF_C + buf * CG + brow * 64 + ph * 16);
         r.s = *reinterpret_cast<const float*>(lds + OFF_S + buf * SG + brow * 16 + ph * 4);
-        r.zb = *reinterpret_cast<const uint32_t*>(lds + OFF_Z + buf * ZG + (ph >> 1) * BN * 4 + brow * 4);
+        r.zb = *reinterpret_cast<const uint32_t*>(lds + OFF_Z + buf * ZG + brow * 4);
         return r;
     };
     auto dequant = [&](const Raw& raw, int t) {
-        const int zp = p.zp ? (int)((raw.zb >> ((t & 1) * 4)) & 0x0F) : 8;
+        const int zp = p.zp ? (int)((raw.zb >> ((t & 3) * 4)) & 0x0F) : 8;
         const h2_t zb = as_h2(kHalfMagic | ((uint32_t)zp << 16) | (uint32_t)zp);
         const _Float16 sh = (_Float16)raw.s;
         const h2_t s2 = h2_t{sh, sh};
@@ -208,74 +211,108 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
         for (int j = 0; j < FN; ++j) acc[i][j] = floatx16_t{};
     }
     const int lr = lane & 31, lh = lane >> 5;
-    auto mma = [&](int st, int bbuf) {
+    // MFMA operands of one half step (16 k): 4 A and 4 B fragments.
+    struct Ops {
+        half8_t a[FM], b[FN];
+    };
+    auto load_ops = [&](int st, int bbuf, int sub, Ops& o) {
         const uint8_t* As = lds + OFF_A + st * A_ST;
         const uint8_t* Bs = lds + OFF_B + bbuf * B16_SZ;
+        const int j = 2 * sub + lh;
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
-            const int j = 2 * sub + lh;
-            half8_t af[FM], bf[FN];
+        for (int i = 0; i < FM; ++i) {
+            const int r = wm * 128 + 32 * i + lr;
+            o.a[i] = *reinterpret_cast<const half8_t*>(As + r * 64 + pipe_slot(r, j) * 16);
+        }
 #pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                const int r = wm * 128 + 32 * i + lr;
-                af[i] = *reinterpret_cast<const half8_t*>(As + r * 64 + pipe_slot(r, j) * 16);
-            }
+        for (int i = 0; i < FN; ++i) {
+            const int r = wn * 128 + 32 * i + lr;
+            o.b[i] = *reinterpret_cast<const half8_t*>(Bs + r * 64 + pipe_slot(r, j) * 16);
+        }
+    };
+    auto mfma_ops = [&](const Ops& o) {
 #pragma unroll
-            for (int i = 0; i < FN; ++i) {
-                const int r = wn * 128 + 32 * i + lr;
-                bf[i] = *reinterpret_cast<const half8_t*>(Bs + r * 64 + pipe_slot(r, j) * 16);
-            }
+        for (int i = 0; i < FM; ++i) {
 #pragma unroll
-            for (int i = 0; i < FM; ++i) {
-#pragma unroll
-                for (int jn = 0; jn < FN; ++jn)
-                    acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[jn], acc[i][jn], 0, 0, 0);
-            }
+            for (int jn = 0; jn < FN; ++jn)
+                acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(o.a[i], o.b[jn], acc[i][jn], 0, 0, 0);
         }
     };
 
-    // Issue order per wave, and the vmcnt each wait needs (loads issued after the
-    // one waited for): prologue B(0) A(0) A(1) A(2); step 4g+p issues A(4g+p+3),
-    // and at p = 0 also B(g+1) [7 loads]; A(s) is 4 loads.
+    // Step t (A stage t % 4, fp16 weight tile t & 1), with R0 holding the operands of its
+    // first half (k 0-15):
+    //   first half:  read R1 (k 16-31) and the raw weights of step t+2; MFMAs on R0,
+    //                interleaved with the dequant of step t+1 into tile (t+1) & 1;
+    //                wait for A(t+1); barrier;
+    //   second half: read R0 of step t+1; MFMAs on R1, interleaved with the issue of
+    //                A(t+3) and, at t % 4 == 0, of weight group t/4 + 2.
+    // So every LDS read runs under MFMAs that do not depend on it. Weight group g lives
+    // in raw buffer g % 3 and is issued two groups (8 steps) ahead. Issue order per
+    // wave: B(0) B(1) A(0) A(1) A(2), then per step A(t+3) [4 loads] and, at t % 4 == 0,
+    // B(t/4+2) [6 loads]; each wait counts the loads issued after the one waited for
+    // (the weight group read at step t+1 was issued before A(t+1)).
+    Ops R0, R1;
     issue_b(0, 0);
+    issue_b(1, 1);
     issue_a(0, 0);
     issue_a(1, 1);
     issue_a(2, 2);
-    wait_vmcnt<8>();                     // B(0), A(0)
-    Raw raw = read_raw(0);
+    wait_vmcnt<8>();                     // B(0), B(1), A(0): then A(1), A(2)
+    Raw raw = read_raw(0, 0);
     dequant(raw, 0);
-    raw = read_raw(1);
+    raw = read_raw(1, 0);
     lds_barrier();
-    for (int t = 0; t < nsteps; t += 4) {
-        wait_vmcnt<4>();                 // A(t+1): after it A(t+2)
-        Raw rn = read_raw(t + 2);
-        mma(0, 0);
+    load_ops(0, 0, 0, R0);
+    auto step = [&](int t, auto phase, auto wait, int rbuf, int nbuf) {
+        constexpr int ph = decltype(phase)::value;
+        __builtin_amdgcn_sched_barrier(0);
+        load_ops(ph, ph & 1, 1, R1);
+        Raw rn = read_raw(t + 2, rbuf);
+        mfma_ops(R0);
         dequant(raw, t + 1);
+        // 16 MFMAs, each followed by one LDS operation (the 11 reads, then the dequant's 4
+        // writes) and a share of the dequant's VALU work: about 5 VALU instructions fit
+        // in the shadow of one 32-cycle MFMA.
+#pragma unroll
+        for (int g = 0; g < 11; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_barrier(0);
         raw = rn;
-        issue_a(t + 3, 3);
-        issue_b((t >> 2) + 1, ((t >> 2) + 1) & 1);
+        wait_vmcnt<decltype(wait)::value>();
         lds_barrier();
-        wait_vmcnt<11>();                // A(t+2): after it A(t+3), B(g+1)
-        rn = read_raw(t + 3);
-        mma(1, 1);
-        dequant(raw, t + 2);
-        raw = rn;
-        issue_a(t + 4, 0);
-        lds_barrier();
-        wait_vmcnt<4>();                 // B(g+1) (raw of t+4), A(t+3): after B(g+1) A(t+4)
-        rn = read_raw(t + 4);
-        mma(2, 0);
-        dequant(raw, t + 3);
-        raw = rn;
-        issue_a(t + 5, 1);
-        lds_barrier();
-        wait_vmcnt<4>();                 // A(t+4): after it A(t+5)
-        rn = read_raw(t + 5);
-        mma(3, 1);
-        dequant(raw, t + 4);
-        raw = rn;
-        issue_a(t + 6, 2);
-        lds_barrier();
+        load_ops((ph + 1) & 3, (ph + 1) & 1, 0, R0);
+        mfma_ops(R1);
+        issue_a(t + 3, (ph + 3) & 3);
+        if constexpr (ph == 0) issue_b((t >> 2) + 2, nbuf);
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    using std::integral_constant;
+    int b0 = 0, b1 = 1, b2 = 2;           // raw buffers of groups g, g+1, g+2
+    for (int t = 0; t < nsteps; t += 4) {
+        step(t, integral_constant<int, 0>{}, integral_constant<int, 4>{}, b0, b2);       // A(t+1): then A(t+2)
+        step(t + 1, integral_constant<int, 1>{}, integral_constant<int, 10>{}, b0, b2);  // A(t+2): then A(t+3), B(g+2)
+        step(t + 2, integral_constant<int, 2>{}, integral_constant<int, 10>{}, b1, b2);  // A(t+3): then B(g+2), A(t+4)
+        step(t + 3, integral_constant<int, 3>{}, integral_constant<int, 4>{}, b1, b2);   // A(t+4): then A(t+5)
+        const int bt = b0;
+        b0 = b1;
+        b1 = b2;
+        b2 = bt;
     }
     wait_vmcnt<0>();
 
