@@ -33,6 +33,9 @@ ROOT = pathlib.Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 METRIC = "MatMulNBits INT4 M=1 GEMV HBM GB/s at 7B shapes; M=2048 prefill TFLOP/s"
+# Projections of the 7B decode layer that read the same input, by index into DECODE_7B;
+# a batch call runs each group as one launch.
+GROUPS = {"qkv": [0, 1, 2], "gate_up": [4, 5]}
 HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
 
@@ -44,21 +47,26 @@ def log(msg: str) -> None:
 class Rotation:
     """R device-resident copies of a set of ops: weights handles, A and Y."""
 
-    def __init__(self, ops, M, copies, seed, kind="normal"):
+    def __init__(self, ops, M, copies, seed, kind="normal", share=None):
+        """share[i] = the op whose activation buffer op i reads (default: its own), as the
+        projections of one input share it in a decoder layer."""
         import torch
         from modelsharp_amd import native, workloads
         self.ops, self.M, self.copies = ops, M, copies
+        share = list(range(len(ops))) if share is None else share
         host = [workloads.make_weights(op, seed + i) for i, op in enumerate(ops)]
         self.handles = [[native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
                          for (b, s, z), op in zip(host, ops)] for _ in range(copies)]
-        self.A = [[torch.from_numpy(workloads.make_activations(M, op.K, seed + 100 * r + i, kind)).cuda()
-                   for i, op in enumerate(ops)] for r in range(copies)]
+        own = [{i: torch.from_numpy(workloads.make_activations(M, ops[i].K, seed + 100 * r + i, kind)).cuda()
+                for i in set(share)} for r in range(copies)]
+        self.A = [[own[r][share[i]] for i in range(len(ops))] for r in range(copies)]
         self.Y = [[torch.empty((M, op.N), dtype=torch.float32, device="cuda") for op in ops] for _ in range(copies)]
         self.host = host
 
     def enqueue(self, r, stream, only=None):
+        """One batch call over copy r's ops (or the op index / list of indices `only`)."""
         from modelsharp_amd import native
-        idx = range(len(self.ops)) if only is None else [only]
+        idx = range(len(self.ops)) if only is None else ([only] if isinstance(only, int) else list(only))
         native.gemm_dev_batch([self.handles[r][i] for i in idx], [self.A[r][i].data_ptr() for i in idx],
                               [self.Y[r][i].data_ptr() for i in idx], self.M, stream)
 
@@ -99,7 +107,7 @@ def time_graph(g, replays, warmup):
     return start.elapsed_time(end) / replays
 
 
-TRAFFIC_PROFILE = "profiles/gemv_w4_gate_7b_hbm_traffic.json"
+TRAFFIC_PROFILE = "profiles/gemv_w4_gate_up_7b_hbm_traffic.json"
 
 
 def kernel_source_digest() -> str:
@@ -114,7 +122,7 @@ def kernel_source_digest() -> str:
 
 
 def measured_traffic(launch):
-    """HBM bytes per gate/up launch from the committed rocprofv3 FETCH_SIZE /
+    """HBM bytes per gate+up launch from the committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE passes (scaled by a plain copy's counters), used only when that
     profile was taken on the same kernel sources and launch configuration."""
     path = ROOT / TRAFFIC_PROFILE
@@ -166,9 +174,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget (0 = skip)")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--detail", default="", help="also write per-op results of every workload to this JSON file")
-    ap.add_argument("--op", default="", help="profiling mode: launch only this 7B decode op (q,k,v,o,gate,up,down) "
-                                             "or prefill_up / prefill_down (M=2048), eagerly over the rotation, then a "
-                                             "plain copy of --copy-mib; no JSON line")
+    ap.add_argument("--op", default="", help="profiling mode: launch only this 7B decode op (q,k,v,o,gate,up,down), "
+                                             "a grouped launch (qkv, gate_up) or prefill_up / prefill_down (M=2048), "
+                                             "eagerly over the rotation, then a plain copy of --copy-mib; no JSON line")
     ap.add_argument("--calls", type=int, default=64, help="launches in --op mode")
     ap.add_argument("--copy-mib", type=int, default=256, help="size of the calibration copy in --op mode")
     args = ap.parse_args()
@@ -197,7 +205,7 @@ def main() -> int:
     step_bytes = sum(workloads.algorithmic_bytes(op, 1) for op in ops)
     copies = workloads.rotation_copies(step_bytes, args.rotate_mib << 20)
     log(f"7b decode layer: {step_bytes / 1e6:.2f} MB/step, {copies} rotating copies")
-    rot = Rotation(ops, 1, copies, seed=7)
+    rot = Rotation(ops, 1, copies, seed=7, share=workloads.DECODE_7B_SHARE)
 
     def layer_rotation(stream):
         for r in range(copies):
@@ -211,6 +219,12 @@ def main() -> int:
     ms_step = ms_rot / copies
     value = step_bytes / (ms_step * 1e-3) / 1e9
     log(f"graph: {ms_step * 1e3:.2f} us/step  {value:.1f} GB/s")
+
+    # the same step with every op in a launch of its own (no grouping of shared inputs)
+    gu = graph_of(lambda stream: [rot.enqueue(r, stream, only=i) for r in range(copies) for i in range(len(ops))])
+    ms_step_ungrouped = time_graph(gu, replays, warm) / copies
+    log(f"ungrouped: {ms_step_ungrouped * 1e3:.2f} us/step  {step_bytes / (ms_step_ungrouped * 1e-3) / 1e9:.1f} GB/s")
+    del gu
 
     # eager launches (no graph) for comparison
     torch.cuda.synchronize()
@@ -236,10 +250,21 @@ def main() -> int:
                            "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                            "kernel": rot.handles[0][i].launch_info(1)}
         log(f"  {op.name:5s} K={op.K:6d} N={op.N:6d}: {ms * 1e3:7.2f} us  {per_op[op.name]['GBs']:7.1f} GB/s")
-    gate = next(op for op in ops if op.name == "gate")
-    gate_bytes = workloads.algorithmic_bytes(gate, 1)
-    gate_gbs = per_op["gate"]["GBs"]
-    traffic = measured_traffic(per_op["gate"]["kernel"])
+    # grouped launches as the step runs them (projections of one input in one launch)
+    groups = {}
+    for gname, idx in GROUPS.items():
+        gg = graph_of(lambda stream, idx=idx: [rot.enqueue(r, stream, only=idx) for r in range(copies)])
+        ms = time_graph(gg, max(4, 2 * replays), 2) / copies
+        nbytes = workloads.algorithmic_bytes_group([ops[i] for i in idx], 1)
+        info = native.batch_launch_info([rot.handles[0][i] for i in idx], [rot.A[0][i].data_ptr() for i in idx], 1)
+        groups[gname] = {"ops": [ops[i].name for i in idx], "us": round(ms * 1e3, 3),
+                         "bytes": nbytes, "GBs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                         "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "kernel": info}
+        log(f"  {gname:8s} one launch ({info['calls']} ops): {ms * 1e3:7.2f} us  {groups[gname]['GBs']:7.1f} GB/s")
+        del gg
+    dom = groups["gate_up"]
+    gate = next(op for op in ops if op.name == "gate")   # the CPU baseline's sample
+    traffic = measured_traffic(dom["kernel"])
     rot.close()
     del rot, g
     torch.cuda.empty_cache()
@@ -252,12 +277,14 @@ def main() -> int:
                    "bits": 4, "block_size": 32, "zero_points": "packed uint4", "rotating_copies": copies,
                    "bytes_per_step": step_bytes, "timing": "HIP graph of the rotation, HIP events"},
         "ms_per_step_eager": round(ms_step_eager, 5),
+        "ms_per_step_ungrouped": round(ms_step_ungrouped, 5),
         "per_op": per_op,
-        "roofline": {"bound": "hbm", "kernel": "gemv_w4 gate/up (K=3584, N=18944, M=1)",
-                     "achieved": gate_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gate_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+        "groups": groups,
+        "roofline": {"bound": "hbm", "kernel": "gemv_w4, gate+up in one launch (K=3584, 2 x N=18944, M=1)",
+                     "achieved": dom["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom["GBs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_source": TRAFFIC_PROFILE if traffic else None,
-                     "algorithmic_bytes_per_launch": gate_bytes},
+                     "algorithmic_bytes_per_launch": dom["bytes"]},
     }
 
     # ---- prefill, M=2048 ----------------------------------------------------------------
@@ -303,22 +330,26 @@ def profile_op(args) -> int:
     counters calibrate the byte counts."""
     import torch
     from modelsharp_amd import workloads
+    from modelsharp_amd import native
     if args.op.startswith("prefill_"):
-        op = next(o for o in workloads.LLAMA7B_PREFILL_OPS if o.name == args.op[len("prefill_"):])
+        ops = [next(o for o in workloads.LLAMA7B_PREFILL_OPS if o.name == args.op[len("prefill_"):])]
         M, copies, kind = 2048, 2, "rmsnorm"
     else:
-        op = next(o for o in workloads.DECODE_7B if o.name == args.op)
+        ops = ([workloads.DECODE_7B[i] for i in GROUPS[args.op]] if args.op in GROUPS else
+               [next(o for o in workloads.DECODE_7B if o.name == args.op)])
         M, kind = 1, "normal"
-        copies = workloads.rotation_copies(workloads.algorithmic_bytes(op, 1), args.rotate_mib << 20)
-    fp = workloads.algorithmic_bytes(op, M)
-    rot = Rotation([op], M, copies, seed=7, kind=kind)
+    fp = workloads.algorithmic_bytes_group(ops, M)
+    if M == 1:
+        copies = workloads.rotation_copies(fp, args.rotate_mib << 20)
+    rot = Rotation(ops, M, copies, seed=7, kind=kind, share=[0] * len(ops))
     stream = torch.cuda.current_stream().cuda_stream
     for i in range(args.calls):
         rot.enqueue(i % copies, stream)
     torch.cuda.synchronize()
-    log(f"{args.calls} launches of {op.name} (M={M}, K={op.K}, N={op.N}, {fp} algorithmic bytes, "
-        f"{workloads.flops(op, M)} flops each), {copies} rotating copies; launch {rot.handles[0][0].launch_info(M)}; "
-        f"kernel sources {kernel_source_digest()}")
+    launch = native.batch_launch_info(rot.handles[0], [a.data_ptr() for a in rot.A[0]], M)
+    log(f"{args.calls} launches of {args.op} (M={M}, K={ops[0].K}, N={'+'.join(str(o.N) for o in ops)}, "
+        f"{fp} algorithmic bytes, {sum(workloads.flops(o, M) for o in ops)} flops each), {copies} rotating copies; "
+        f"launch {launch}; kernel sources {kernel_source_digest()}")
     src = torch.empty(args.copy_mib << 20, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(4):

@@ -98,7 +98,11 @@ int ms_hip_nbits_gemm_dev(void* handle, const float* dA, float* dY, int M, void*
 
 /* Enqueues `count` device-pointer calls back to back on `stream`, call i on
  * handles[i] with dA[i], dY[i] (all with the same M). For callers that chain
- * several projections without a host round trip per call. */
+ * several projections without a host round trip per call. Consecutive decode
+ * calls (M <= 4) on the same dA pointer whose weights share K and block size (the
+ * projections of one input: q/k/v, gate/up) run as one grouped launch of up to
+ * four matrices; results are those of the same calls made one by one, to the
+ * decode tolerance. */
 int ms_hip_nbits_gemm_dev_batch(void* const* handles, const float* const* dA,
                                 float* const* dY, int count, int M, void* stream);
 
@@ -134,6 +138,11 @@ int ms_hip_sync(void);
  *   3 1 or 2 forces the pipelined prefill's K split (2 needs K >= 256).
  * ms_hip_nbits_launch_info reports what a call with M rows would launch:
  *   kernel_id 0 generic, 1 gemv_w4, 2 mfma_w4, 3 gemv_w4_panel, 4 mfma_w4_pipe. */
+/* ms_hip_nbits_batch_launch_info: what the first launch of a batch call with these
+ * handles and activations would be: `calls` = how many of the leading calls it
+ * serves, then as ms_hip_nbits_launch_info. */
+int ms_hip_nbits_batch_launch_info(void* const* handles, const float* const* dA, int count, int M,
+                                   int* calls, int* kernel_id, int* lanes_per_row, int* grid, int* block);
 int ms_hip_set_gemv_lanes(int lanes_per_row);
 int ms_hip_set_tuning(int knob, int value);
 int ms_hip_nbits_launch_info(void* handle, int M, int* kernel_id, int* lanes_per_row,

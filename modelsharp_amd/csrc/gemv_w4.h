@@ -1,4 +1,5 @@
-// gemv_w4.h — dequant-fused INT4 GEMV for 1 <= M <= 4 (the decode path).
+// gemv_w4.h — dequant-fused INT4 GEMV for 1 <= M <= 4 (the decode path), for one
+// weight matrix or a group of up to four that share the activations.
 //
 // Work mapping (wave64-first):
 //   * A workgroup of WAVES waves owns ROWS = (64/G) * (WAVES/KW) consecutive output
@@ -36,24 +37,43 @@
 
 namespace msnb {
 
-struct GemvParams {
+// One launch serves up to kGemvMaxOps weight matrices that share the activations A
+// and K (the projections of one input: q/k/v, gate/up); op i owns workgroups
+// [first, next op's first).
+constexpr int kGemvMaxOps = 4;
+struct GemvOp {
     const uint8_t* b;        // [N][row_bytes] packed codes (reference layout)
     const float* scales;     // [N][nb]
     const uint8_t* zp;       // [N][zrb] packed nibbles, or nullptr (zp = 8)
-    const float* a;          // [M][K]
     float* y;                // [M][N]
+    int N;
+    int first;               // first workgroup of this op
+};
+struct GemvParams {
+    GemvOp op[kGemvMaxOps];
+    int nops;
+    const float* a;          // [M][K]
     int row_bytes;           // nb * block_size / 2
-    int N, K;
+    int K;
     int C;                   // K / 32 chunks per row
     int nb, zrb;
 };
 
-template <int M, int G, int KW, int U, int L, int WAVES>
+// Uniform choice among the op table's entries (selects on a wave-uniform index, so the
+// table stays in the kernel arguments).
+template <typename T>
+__device__ __forceinline__ T op_field(int oi, T v0, T v1, T v2, T v3)
+{
+    return oi == 0 ? v0 : oi == 1 ? v1 : oi == 2 ? v2 : v3;
+}
+
+template <int M, int G, int KW, int U, int L, int WAVES, int RL>
 __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
 {
     constexpr int R = kWave / G;
     constexpr int WR = WAVES / KW;
-    constexpr int ROWS = R * WR;
+    constexpr int ROWS0 = R * WR;      // rows of one layer; a lane owns RL rows, ROWS0 apart
+    constexpr int ROWS = RL * ROWS0;
     constexpr int SPAN = G * KW;
     constexpr int BSPAN = SPAN >> L;   // blocks per step
     static_assert((BSPAN << L) == SPAN && (BSPAN & 1) == 0, "a step covers an even number of whole blocks");
@@ -66,17 +86,25 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
     const int g = lane % G, r = lane / G;
     const int wk = wave % KW, wr = wave / KW;
     const int rl = wr * R + r;
-    const int n = blockIdx.x * ROWS + rl;
+    const int bid = blockIdx.x;
+    const int oi = (p.nops > 1 && bid >= p.op[1].first) + (p.nops > 2 && bid >= p.op[2].first) +
+                   (p.nops > 3 && bid >= p.op[3].first);
+    const uint8_t* const ob = op_field(oi, p.op[0].b, p.op[1].b, p.op[2].b, p.op[3].b);
+    const float* const osc = op_field(oi, p.op[0].scales, p.op[1].scales, p.op[2].scales, p.op[3].scales);
+    const uint8_t* const ozp = op_field(oi, p.op[0].zp, p.op[1].zp, p.op[2].zp, p.op[3].zp);
+    float* const oy = op_field(oi, p.op[0].y, p.op[1].y, p.op[2].y, p.op[3].y);
+    const int N = op_field(oi, p.op[0].N, p.op[1].N, p.op[2].N, p.op[3].N);
+    const int first = op_field(oi, p.op[0].first, p.op[1].first, p.op[2].first, p.op[3].first);
+    const int n0 = (bid - first) * ROWS + rl;         // row j of this lane: n0 + j * ROWS0
     const int C = p.C;
     const int nsteps = (C + SPAN - 1) / SPAN;
     const int lofs = wk * G + g;                       // chunk offset within a step
-    const int nvalid = (lofs < C && n < p.N) ? (C - lofs + SPAN - 1) / SPAN : 0;
+    const int nvalid = (lofs < C && n0 < N) ? (C - lofs + SPAN - 1) / SPAN : 0;
 
     const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(p.a, M * p.K * 4);
-    const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(p.b, p.N * p.row_bytes);
-    const __amdgpu_buffer_rsrc_t rsc = buffer_rsrc(p.scales, p.N * p.nb * 4);
-    const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(p.zp ? (const void*)p.zp : (const void*)p.scales,
-                                                  p.zp ? p.N * p.zrb : 0);
+    const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(ob, N * p.row_bytes);
+    const __amdgpu_buffer_rsrc_t rsc = buffer_rsrc(osc, N * p.nb * 4);
+    const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(ozp ? (const void*)ozp : (const void*)osc, ozp ? N * p.zrb : 0);
 
     // ---- 1. activation chunks: first in the load queue -------------------------------
     const int na = M * C;
@@ -90,25 +118,34 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- 2. weight stream: two batches of U steps in flight ---------------------------
-    const int nl = n < p.N ? n : p.N - 1;
-    const int bbase = nl * p.row_bytes + lofs * 16;
-    const int sbase = nl * p.nb * 4 + (lofs >> L) * 4;
-    const int zbase = nl * p.zrb + ((lofs >> L) >> 1);
+    // A row past N (the last workgroup's) streams row N-1 again; its sums are not stored.
+    int bbase[RL], sbase[RL], zbase[RL];
+#pragma unroll
+    for (int j = 0; j < RL; ++j) {
+        const int nj = n0 + j * ROWS0;
+        const int nl = nj < N ? nj : N - 1;
+        bbase[j] = nl * p.row_bytes + lofs * 16;
+        sbase[j] = nl * p.nb * 4 + (lofs >> L) * 4;
+        zbase[j] = nl * p.zrb + ((lofs >> L) >> 1);
+    }
     const int zshift = ((lofs >> L) & 1) * 4;
     struct Batch {
-        u32x4_t q[U];
-        float s[U];
-        uint32_t z[U];
+        u32x4_t q[RL][U];
+        float s[RL][U];
+        uint32_t z[RL][U];
     };
     auto load = [&](Batch& bt, int k0) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int k = k0 + u;
             const bool ok = k < nvalid;
-            bt.q[u] = __builtin_amdgcn_raw_buffer_load_b128(rb, ok ? bbase + k * (SPAN * 16) : kOOB, 0, 0);
-            bt.s[u] = __builtin_bit_cast(
-                float, __builtin_amdgcn_raw_buffer_load_b32(rsc, ok ? sbase + k * (BSPAN * 4) : kOOB, 0, 0));
-            bt.z[u] = __builtin_amdgcn_raw_buffer_load_b8(rz, ok ? zbase + k * (BSPAN / 2) : kOOB, 0, 0);
+#pragma unroll
+            for (int j = 0; j < RL; ++j) {
+                bt.q[j][u] = __builtin_amdgcn_raw_buffer_load_b128(rb, ok ? bbase[j] + k * (SPAN * 16) : kOOB, 0, 0);
+                bt.s[j][u] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_raw_buffer_load_b32(rsc, ok ? sbase[j] + k * (BSPAN * 4) : kOOB, 0, 0));
+                bt.z[j][u] = __builtin_amdgcn_raw_buffer_load_b8(rz, ok ? zbase[j] + k * (BSPAN / 2) : kOOB, 0, 0);
+            }
         }
     };
     Batch bA, bB;
@@ -133,37 +170,54 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
     }
     __syncthreads();
 
-    float acc[M];
+    float acc[RL][M];
 #pragma unroll
-    for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+    for (int j = 0; j < RL; ++j) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[j][m] = 0.0f;
+    }
     auto reduce = [&](const Batch& bt, int k0) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int k = k0 + u;
             if (k < nvalid) {
                 const int c = k * SPAN + lofs;
-                const float zpf = p.zp ? (float)((bt.z[u] >> zshift) & 0x0F) : 8.0f;
-                const uint32_t qd[4] = {bt.q[u].x, bt.q[u].y, bt.q[u].z, bt.q[u].w};
-                uint32_t pr[4][4];
+                uint32_t pr[RL][4][4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) code_pairs(qd[j], pr[j]);
+                for (int j = 0; j < RL; ++j) {
+                    const uint32_t qd[4] = {bt.q[j][u].x, bt.q[j][u].y, bt.q[j][u].z, bt.q[j][u].w};
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) code_pairs(qd[d], pr[j][d]);
+                }
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
+                    // With RL > 1 one read of the activation chunk serves the lane's RL rows
+                    // (held in registers); with RL = 1 it streams from LDS (fewer VGPRs).
                     const float4* arow = &lds_a4[(m * C + c) * kChunkStride4];
-                    float blkacc;
-                    if constexpr (M <= 2) {
-                        float t0 = qdot8(pr[0], arow[0], arow[1], 0.0f);
-                        float t1 = qdot8(pr[1], arow[2], arow[3], 0.0f);
-                        t0 = qdot8(pr[2], arow[4], arow[5], t0);
-                        t1 = qdot8(pr[3], arow[6], arow[7], t1);
-                        blkacc = t0 + t1;
-                    } else {
-                        blkacc = 0.0f;
+                    float4 areg[RL > 1 ? 9 : 1];
+                    if constexpr (RL > 1) {
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) blkacc = qdot8(pr[j], arow[2 * j], arow[2 * j + 1], blkacc);
+                        for (int i = 0; i < 9; ++i) areg[i] = arow[i];
                     }
-                    blkacc = __builtin_fmaf(-zpf, arow[8].x, blkacc);
-                    acc[m] = __builtin_fmaf(bt.s[u], blkacc, acc[m]);
+                    const float4* a = RL > 1 ? areg : arow;
+#pragma unroll
+                    for (int j = 0; j < RL; ++j) {
+                        float blkacc;
+                        if constexpr (M <= 2) {
+                            float t0 = qdot8(pr[j][0], a[0], a[1], 0.0f);
+                            float t1 = qdot8(pr[j][1], a[2], a[3], 0.0f);
+                            t0 = qdot8(pr[j][2], a[4], a[5], t0);
+                            t1 = qdot8(pr[j][3], a[6], a[7], t1);
+                            blkacc = t0 + t1;
+                        } else {
+                            blkacc = 0.0f;
+#pragma unroll
+                            for (int d = 0; d < 4; ++d) blkacc = qdot8(pr[j][d], a[2 * d], a[2 * d + 1], blkacc);
+                        }
+                        const float zpf = ozp ? (float)((bt.z[j][u] >> zshift) & 0x0F) : 8.0f;
+                        blkacc = __builtin_fmaf(-zpf, a[8].x, blkacc);
+                        acc[j][m] = __builtin_fmaf(bt.s[j][u], blkacc, acc[j][m]);
+                    }
                 }
             }
         }
@@ -180,37 +234,54 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
 #pragma unroll
     for (int off = G / 2; off > 0; off >>= 1) {
 #pragma unroll
-        for (int m = 0; m < M; ++m) acc[m] += __shfl_xor(acc[m], off, kWave);
+        for (int j = 0; j < RL; ++j) {
+#pragma unroll
+            for (int m = 0; m < M; ++m) acc[j][m] += __shfl_xor(acc[j][m], off, kWave);
+        }
     }
     if constexpr (KW > 1) {
         if (g == 0) {
 #pragma unroll
-            for (int m = 0; m < M; ++m) red[wk][rl][m] = acc[m];
+            for (int j = 0; j < RL; ++j) {
+#pragma unroll
+                for (int m = 0; m < M; ++m) red[wk][j * ROWS0 + rl][m] = acc[j][m];
+            }
         }
         __syncthreads();
         if (wk == 0 && g == 0) {
 #pragma unroll
-            for (int m = 0; m < M; ++m) {
-                float s = red[0][rl][m];
+            for (int j = 0; j < RL; ++j) {
 #pragma unroll
-                for (int j = 1; j < KW; ++j) s += red[j][rl][m];
-                acc[m] = s;
+                for (int m = 0; m < M; ++m) {
+                    float s = red[0][j * ROWS0 + rl][m];
+#pragma unroll
+                    for (int w = 1; w < KW; ++w) s += red[w][j * ROWS0 + rl][m];
+                    acc[j][m] = s;
+                }
             }
         }
     }
-    if (wk == 0 && g == 0 && n < p.N) {
+    if (wk == 0 && g == 0) {
 #pragma unroll
-        for (int m = 0; m < M; ++m) p.y[(int64_t)m * p.N + n] = acc[m];
+        for (int j = 0; j < RL; ++j) {
+            const int nj = n0 + j * ROWS0;
+            if (nj < N) {
+#pragma unroll
+                for (int m = 0; m < M; ++m) oy[(int64_t)m * N + nj] = acc[j][m];
+            }
+        }
     }
 }
 
 // Launch configurations of gemv_w4_kernel (one instantiation each per M and L).
 struct GemvConfig {
-    int waves, G, KW, U;
+    int waves, G, KW, U, RL;
 };
 constexpr GemvConfig kGemvConfigs[] = {
-    {4, 16, 1, 2},  {4, 16, 1, 4},  {4, 32, 1, 4},  {4, 64, 1, 2},  {4, 16, 4, 2},  {4, 32, 2, 2},
-    {8, 32, 1, 4},  {8, 16, 2, 4},  {8, 16, 4, 2},  {16, 16, 4, 2}, {16, 32, 2, 2}, {16, 32, 4, 2},
+    {4, 16, 1, 2, 1},  {4, 16, 1, 4, 1},  {4, 32, 1, 4, 1},  {4, 64, 1, 2, 1},  {4, 16, 4, 2, 1},
+    {4, 32, 2, 2, 1},  {8, 32, 1, 4, 1},  {8, 16, 2, 4, 1},  {8, 16, 4, 2, 1},  {16, 16, 4, 2, 1},
+    {16, 32, 2, 2, 1}, {4, 16, 1, 2, 2},  {4, 16, 1, 4, 2},  {4, 32, 1, 2, 2},  {4, 64, 1, 2, 2},
+    {8, 16, 2, 2, 2},
 };
 constexpr int kNumGemvConfigs = sizeof(kGemvConfigs) / sizeof(kGemvConfigs[0]);
 constexpr int kGemvMaxM = 4;

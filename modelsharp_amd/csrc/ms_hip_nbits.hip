@@ -244,7 +244,7 @@ template <int M, int L, size_t I>
 constexpr GemvFn gemv_fn_at()
 {
     constexpr GemvConfig c = kGemvConfigs[I];
-    return gemv_w4_kernel<M, c.G, c.KW, c.U, L, c.waves>;
+    return gemv_w4_kernel<M, c.G, c.KW, c.U, L, c.waves, c.RL>;
 }
 template <int M, int L, size_t... I>
 constexpr std::array<GemvFn, sizeof...(I)> gemv_row(std::index_sequence<I...>)
@@ -264,6 +264,9 @@ const std::array<GemvFn, kNumGemvConfigs> kGemvTable[kGemvMaxM][2] = {
 };
 std::atomic<bool> g_gemv_lds_raised[kGemvMaxM][2][kNumGemvConfigs];
 
+// Output rows of one gemv_w4 workgroup.
+constexpr int gemv_rows(const GemvConfig& c) { return (kWave / c.G) * (c.waves / c.KW) * c.RL; }
+
 int l_slot(const Weights& w) { return w.log2cpb == 0 ? 0 : w.log2cpb == 2 ? 1 : -1; }
 
 // gemv_w4 takes M <= 4, block size 32 or 128, and A panels that one thread per
@@ -273,69 +276,119 @@ bool gemv_config_fits(const Weights& w, int M, const GemvConfig& c)
     return M <= kGemvMaxM && l_slot(w) >= 0 && M * (w.K / 32) <= 64 * c.waves;
 }
 
-// Config choice (measured on MI355X over the decode workloads): score = lane
-// efficiency on the row's C chunks x wave fill (>= 2048 waves) x CU balance of
-// the grid x a small penalty when a lane has a single step; ties go to the
-// lower index.
-int pick_gemv_config(const Weights& w, int M)
+// Config choice: the first config of a preference list that fits the shape and gives
+// every lane at least 2 steps. The lists come from sweeping every config over the
+// 7B and Qwen2.5-0.5B decode launches on MI355X (M = 1, 2, 4; single matrices and
+// groups of one input's projections): for M <= 2, two rows per lane at 16 lanes per
+// row win from 16K rows up, 64 lanes per row with two rows per lane around 4-16K rows,
+// 32 lanes per row below; for M = 3-4 the 8-wave configs. N is the launch's total
+// rows (summed over a group). Indices are into kGemvConfigs.
+int pick_gemv_config(const Weights& w, int M, int N)
 {
     if (g_gemv_config < 0) return -1;
     if (g_gemv_config > 0) {
         const int ci = g_gemv_config - 1;
         return gemv_config_fits(w, M, kGemvConfigs[ci]) ? ci : -1;
     }
+    static constexpr int kLargeM2[] = {11, 0, 13, 6};   // M <= 2, N >= 16384
+    static constexpr int kMidM2[] = {14, 11, 2};        // M <= 2, N >= 4096
+    static constexpr int kSmallM2[] = {13, 6, 8};       // M <= 2, N >= 2048
+    static constexpr int kTinyM2[] = {3, 14, 8};        // M <= 2
+    static constexpr int kLargeM4[] = {7, 6, 0};        // M <= 4, N >= 16384
+    static constexpr int kMidM4[] = {15, 7, 8};         // M <= 4, N >= 4096
+    static constexpr int kSmallM4[] = {6, 8, 0};        // M <= 4
+    static constexpr int kWide[] = {9, 10};             // panels that need 16 waves to stage
     const int C = w.K / 32;
-    int best = -1;
-    double best_score = 0.0;
-    for (int ci = 0; ci < kNumGemvConfigs; ++ci) {
+    auto usable = [&](int ci) {
         const GemvConfig& c = kGemvConfigs[ci];
-        if (!gemv_config_fits(w, M, c)) continue;
-        const int rows = (kWave / c.G) * (c.waves / c.KW);
-        const int grid = (w.N + rows - 1) / rows;
-        const int span = c.G * c.KW;
-        const int steps = (C + span - 1) / span;
-        const double eff = (double)C / ((double)steps * span);
-        const double fill = std::min(1.0, (double)grid * c.waves / 2048.0);
-        const double rounds = std::ceil(grid / 256.0);
-        const double bal = grid >= 256 ? grid / (256.0 * rounds) : grid / 256.0;
-        const double pref = steps >= 2 ? 1.0 : 0.9;
-        const double score = eff * fill * bal * pref;
-        if (score > best_score + 1e-9) {
-            best_score = score;
-            best = ci;
-        }
+        return gemv_config_fits(w, M, c) && C > c.G * c.KW;   // >= 2 steps per lane
+    };
+    auto first_of = [&](const int* list, int len) {
+        for (int i = 0; i < len; ++i)
+            if (usable(list[i])) return list[i];
+        return -1;
+    };
+    int ci;
+    if (M <= 2)
+        ci = N >= 16384 ? first_of(kLargeM2, 4) : N >= 4096 ? first_of(kMidM2, 3)
+           : N >= 2048  ? first_of(kSmallM2, 3) : first_of(kTinyM2, 3);
+    else
+        ci = N >= 16384 ? first_of(kLargeM4, 3) : N >= 4096 ? first_of(kMidM4, 3) : first_of(kSmallM4, 3);
+    if (ci < 0) ci = first_of(kWide, 2);
+    if (ci < 0) {   // short rows (a lane gets a single step): any config that fits
+        for (int i = 0; i < kNumGemvConfigs && ci < 0; ++i)
+            if (gemv_config_fits(w, M, kGemvConfigs[i])) ci = i;
     }
-    return best;
+    return ci;
 }
 
-int launch_gemv_w4(const Weights& w, int ci, const float* dA, float* dY, int M, hipStream_t stream)
+// One gemv_w4 launch over `n` weight matrices (1 <= n <= kGemvMaxOps) that share A,
+// K and the block size: member i's rows take workgroups after member i-1's.
+struct GemvMember {
+    const Weights* w;
+    float* dY;
+};
+
+int launch_gemv_group(const GemvMember* mem, int n, const float* dA, int M, int ci, hipStream_t stream)
 {
+    const Weights& w0 = *mem[0].w;
     const GemvConfig& c = kGemvConfigs[ci];
-    const int ls = l_slot(w);
+    const int ls = l_slot(w0);
     GemvFn fn = kGemvTable[M - 1][ls][ci];
-    const int rows = (kWave / c.G) * (c.waves / c.KW);
-    const int grid = (w.N + rows - 1) / rows;
-    const size_t lds = (size_t)M * (w.K / 32) * kChunkStride4 * 16;
+    const int rows = gemv_rows(c);
+    const size_t lds = (size_t)M * (w0.K / 32) * kChunkStride4 * 16;
     if (lds > 64 * 1024 && !g_gemv_lds_raised[M - 1][ls][ci].load()) {
         MS_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         g_gemv_lds_raised[M - 1][ls][ci].store(true);
     }
     GemvParams p;
-    p.b = w.d_b;
-    p.scales = w.d_scales;
-    p.zp = w.has_zp ? w.d_zp : nullptr;
+    int first = 0;
+    for (int i = 0; i < kGemvMaxOps; ++i) {
+        const GemvMember& m = mem[std::min(i, n - 1)];   // unused entries repeat the last member
+        p.op[i].b = m.w->d_b;
+        p.op[i].scales = m.w->d_scales;
+        p.op[i].zp = m.w->has_zp ? m.w->d_zp : nullptr;
+        p.op[i].y = m.dY;
+        p.op[i].N = m.w->N;
+        p.op[i].first = first;
+        if (i < n) first += (m.w->N + rows - 1) / rows;
+    }
+    p.nops = n;
     p.a = dA;
-    p.y = dY;
-    p.row_bytes = (int)w.row_bytes;
-    p.N = w.N;
-    p.K = w.K;
-    p.C = w.K / 32;
-    p.nb = w.nb;
-    p.zrb = w.zrb;
-    hipLaunchKernelGGL(fn, dim3(grid), dim3(c.waves * kWave), lds, stream, p);
+    p.row_bytes = (int)w0.row_bytes;
+    p.K = w0.K;
+    p.C = w0.K / 32;
+    p.nb = w0.nb;
+    p.zrb = w0.zrb;
+    hipLaunchKernelGGL(fn, dim3(first), dim3(c.waves * kWave), lds, stream, p);
     MS_HIP_CHECK(hipGetLastError());
     return MS_HIP_OK;
+}
+
+// Members that one gemv_w4 launch can serve together: same device, 4-bit fast layout,
+// K and block size (hence row_bytes, nb and zrb).
+bool gemv_groupable(const Weights& a, const Weights& b)
+{
+    return a.device == b.device && a.fast && b.fast && a.bits == 4 && b.bits == 4 && a.K == b.K &&
+           a.log2cpb == b.log2cpb && l_slot(a) >= 0;
+}
+
+// How many of the calls starting at handles[0] one launch serves: consecutive calls on
+// the same activations (the projections of one input) that gemv_w4 can group, up to
+// kGemvMaxOps; 1 when the first call launches alone. *ci receives the group's config.
+int batch_group(void* const* handles, const float* const* dA, int count, int M, int* ci)
+{
+    const Weights* w = from_handle(handles[0]);
+    if (M <= 0 || M > kGemvMaxM || !dA[0] || (reinterpret_cast<uintptr_t>(dA[0]) & 15)) return 1;
+    int n = 1, ntot = w->N;
+    while (n < count && n < kGemvMaxOps && dA[n] == dA[0] && gemv_groupable(*w, *from_handle(handles[n]))) {
+        ntot += from_handle(handles[n])->N;
+        ++n;
+    }
+    if (n == 1) return 1;
+    *ci = pick_gemv_config(*w, M, ntot);
+    return *ci >= 0 ? n : 1;
 }
 
 // ---- gemv_w4_panel: M <= 16, any fast block size, A staged in LDS panels ---------------
@@ -450,8 +503,11 @@ int launch_panel(const Weights& w, const float* dA, float* dY, int M, hipStream_
 
 int launch_gemv(const Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
 {
-    const int ci = pick_gemv_config(w, M);
-    if (ci >= 0) return launch_gemv_w4(w, ci, dA, dY, M, stream);
+    const int ci = pick_gemv_config(w, M, w.N);
+    if (ci >= 0) {
+        const GemvMember m{&w, dY};
+        return launch_gemv_group(&m, 1, dA, M, ci, stream);
+    }
     return launch_panel(w, dA, dY, M, stream);
 }
 
@@ -781,12 +837,49 @@ int ms_hip_nbits_gemm_dev_batch(void* const* handles, const float* const* dA, fl
 {
     if (count < 0 || (count > 0 && (!handles || !dA || !dY)))
         return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid batch arguments");
-    for (int i = 0; i < count; ++i) {
-        Weights* w = from_handle(handles[i]);
-        if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle at batch index %d", i);
-        const int st = enqueue_gemm(*w, dA[i], dY[i], M, static_cast<hipStream_t>(stream));
-        if (st) return st;
+    for (int i = 0; i < count; ++i)
+        if (!from_handle(handles[i])) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle at batch index %d", i);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    for (int i = 0; i < count;) {
+        int ci = -1;
+        const int n = batch_group(handles + i, dA + i, count - i, M, &ci);
+        if (n > 1) {
+            GemvMember mem[kGemvMaxOps];
+            for (int j = 0; j < n; ++j) {
+                if (!dY[i + j] || (reinterpret_cast<uintptr_t>(dY[i + j]) & 3))
+                    return fail(MS_HIP_ERR_INVALID, "[ms_hip] null or misaligned output at batch index %d", i + j);
+                mem[j] = GemvMember{from_handle(handles[i + j]), dY[i + j]};
+            }
+            const int st = launch_gemv_group(mem, n, dA[i], M, ci, s);
+            if (st) return st;
+        } else {
+            const int st = enqueue_gemm(*from_handle(handles[i]), dA[i], dY[i], M, s);
+            if (st) return st;
+        }
+        i += n;
     }
+    return MS_HIP_OK;
+}
+
+int ms_hip_nbits_batch_launch_info(void* const* handles, const float* const* dA, int count, int M, int* calls,
+                                   int* kernel_id, int* lanes_per_row, int* grid, int* block)
+{
+    if (count <= 0 || !handles || !dA) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid batch arguments");
+    for (int i = 0; i < count; ++i)
+        if (!from_handle(handles[i])) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle at batch index %d", i);
+    if (M <= 0) return fail(MS_HIP_ERR_INVALID, "[ms_hip] M must be positive; got %d", M);
+    int ci = -1;
+    const int n = batch_group(handles, dA, count, M, &ci);
+    if (calls) *calls = n;
+    if (n == 1) return ms_hip_nbits_launch_info(handles[0], M, kernel_id, lanes_per_row, grid, block);
+    const GemvConfig& c = kGemvConfigs[ci];
+    const int rows = gemv_rows(c);
+    int gr = 0;
+    for (int j = 0; j < n; ++j) gr += (from_handle(handles[j])->N + rows - 1) / rows;
+    if (kernel_id) *kernel_id = 1;
+    if (lanes_per_row) *lanes_per_row = c.G;
+    if (grid) *grid = gr;
+    if (block) *block = c.waves * kWave;
     return MS_HIP_OK;
 }
 
@@ -950,10 +1043,10 @@ int ms_hip_nbits_launch_info(void* handle, int M, int* kernel_id, int* lanes_per
         gr = (int)(((int64_t)M * w->N + 255) / 256);
         bl = 256;
     } else if (M <= kPanelMaxM) {
-        const int ci = pick_gemv_config(*w, M);
+        const int ci = pick_gemv_config(*w, M, w->N);
         if (ci >= 0) {
             const GemvConfig& c = kGemvConfigs[ci];
-            const int rows = (kWave / c.G) * (c.waves / c.KW);
+            const int rows = gemv_rows(c);
             kid = 1;
             G = c.G;
             gr = (w->N + rows - 1) / rows;

@@ -18,6 +18,8 @@ import numpy as np
 
 _PKG = pathlib.Path(__file__).resolve().parent
 LIB_NAME = "libms_hip_nbits.so"
+# Kernel ids of ms_hip_nbits_launch_info.
+KERNEL_NAMES = ("generic", "gemv_w4", "mfma_w4", "gemv_w4_panel", "mfma_w4_pipe")
 HEADER = _PKG.parent / "include" / "ms_hip_kernels.h"
 
 MS_HIP_OK = 0
@@ -60,6 +62,7 @@ _PROTOTYPES = {
     "ms_hip_set_gemv_lanes": (_c_int, [_c_int]),
     "ms_hip_set_tuning": (_c_int, [_c_int, _c_int]),
     "ms_hip_nbits_launch_info": (_c_int, [_vp, _c_int, _ip, _ip, _ip, _ip]),
+    "ms_hip_nbits_batch_launch_info": (_c_int, [_vp, _vp, _c_int, _c_int, _ip, _ip, _ip, _ip, _ip]),
 }
 
 _lock = threading.Lock()
@@ -193,8 +196,7 @@ class NBitsWeights:
         k, g, gr, bl = (ctypes.c_int() for _ in range(4))
         check(load().ms_hip_nbits_launch_info(self.handle, int(M), ctypes.byref(k), ctypes.byref(g),
                                               ctypes.byref(gr), ctypes.byref(bl)))
-        return {"kernel": ("generic", "gemv_w4", "mfma_w4", "gemv_w4_panel", "mfma_w4_pipe")[k.value], "lanes_per_row": g.value,
-                "grid": gr.value, "block": bl.value}
+        return {"kernel": KERNEL_NAMES[k.value], "lanes_per_row": g.value, "grid": gr.value, "block": bl.value}
 
     def close(self) -> None:
         if getattr(self, "handle", None):
@@ -215,6 +217,19 @@ def gemm_dev_batch(weights: list, dA: list[int], dY: list[int], M: int, stream: 
     pa = (_vp * n)(*dA)
     py = (_vp * n)(*dY)
     check(load().ms_hip_nbits_gemm_dev_batch(hs, pa, py, n, int(M), _vp(stream or 0)))
+
+
+def batch_launch_info(weights: list, dA: list[int], M: int) -> dict:
+    """The first launch a gemm_dev_batch call with these weights and activations makes:
+    how many leading calls it serves, and the launch shape as NBitsWeights.launch_info."""
+    n = len(weights)
+    hs = (_vp * n)(*[w.handle for w in weights])
+    pa = (_vp * n)(*dA)
+    c, k, g, gr, bl = (ctypes.c_int() for _ in range(5))
+    check(load().ms_hip_nbits_batch_launch_info(hs, pa, n, int(M), ctypes.byref(c), ctypes.byref(k), ctypes.byref(g),
+                                                 ctypes.byref(gr), ctypes.byref(bl)))
+    return {"calls": c.value, "kernel": KERNEL_NAMES[k.value], "lanes_per_row": g.value, "grid": gr.value,
+            "block": bl.value}
 
 
 def set_gemv_lanes(lanes: int) -> None:

@@ -59,6 +59,9 @@ QWEN05B_DECODE = [_qwen("q", 896, 896), _qwen("k", 896, 128), _qwen("v", 896, 12
                   _qwen("lm_head", 896, 151936)]
 DECODE_7B = [_7b("q", 3584, 3584), _7b("k", 3584, 512), _7b("v", 3584, 512), _7b("o", 3584, 3584),
              _7b("gate", 3584, 18944), _7b("up", 3584, 18944), _7b("down", 18944, 3584)]
+# Activation buffer each DECODE_7B projection reads in a decoder layer: q/k/v share the
+# attention input, gate/up the MLP input.
+DECODE_7B_SHARE = [0, 0, 0, 3, 4, 4, 6]
 LLAMA7B_SMALLM_OPS = [Op("up", 4096, 11008, 128, False), Op("down", 11008, 4096, 128, False)]
 LLAMA7B_SMALLM_M = [1, 2, 4, 8, 16]
 LLAMA7B_PREFILL_OPS = [_7b("up", 4096, 11008), _7b("down", 11008, 4096)]
@@ -73,6 +76,12 @@ def weight_bytes(op: Op) -> int:
 def algorithmic_bytes(op: Op, M: int) -> int:
     """Bytes one call must move: weights once, A (fp32) once, Y (fp32) once."""
     return weight_bytes(op) + M * op.K * 4 + M * op.N * 4
+
+
+def algorithmic_bytes_group(ops: list, M: int) -> int:
+    """Bytes one grouped launch over ops that share their activations must move: each
+    op's weights and Y once, the shared A once."""
+    return sum(algorithmic_bytes(op, M) for op in ops) - (len(ops) - 1) * M * ops[0].K * 4
 
 
 def flops(op: Op, M: int) -> int:

@@ -450,6 +450,60 @@ def test_one_shot_entry_matches_handle_path(gpu):
     w.close()
 
 
+@pytest.mark.parametrize("M", [1, 2, 4])
+def test_batch_shared_activations_grouped(gpu, M):
+    """The decode layer as an engine issues it: q/k/v on one input and gate/up on
+    another go through one grouped gemv_w4 launch each; every output against the oracle."""
+    import torch
+    ops = workloads.DECODE_7B            # q, k, v, o, gate, up, down
+    share = workloads.DECODE_7B_SHARE   # activation buffer each call reads
+    host = [weights_for(o, 40 + i) for i, o in enumerate(ops)]
+    acts = {j: workloads.make_activations(M, ops[j].K, 50 + j) for j in set(share)}
+    dA = {j: torch.from_numpy(a).cuda() for j, a in acts.items()}
+    Ys = [torch.full((M, o.N), float("nan"), device="cuda") for o in ops]
+    ptrs = [dA[share[i]].data_ptr() for i in range(len(ops))]
+    info = native.batch_launch_info([h[3] for h in host], ptrs, M)
+    assert info["calls"] == 3 and info["kernel"] == "gemv_w4", info          # q, k, v in one launch
+    assert native.batch_launch_info([h[3] for h in host[3:]], ptrs[3:], M)["calls"] == 1   # o alone
+    assert native.batch_launch_info([h[3] for h in host[4:]], ptrs[4:], M)["calls"] == 2   # gate, up
+    native.gemm_dev_batch([h[3] for h in host], ptrs, [y.data_ptr() for y in Ys], M,
+                          torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    for i, (o, (b, s, z, w)) in enumerate(zip(ops, host)):
+        a = acts[share[i]]
+        log(f"grouped {o.name} M={M}")
+        assert_gemv_close(Ys[i].cpu().numpy(), oracle.matmul_nbits(a, b, s, z, o.N, o.K, 4, o.block_size),
+                          f"grouped {o.name} M={M}")
+        w.close()
+
+
+def test_batch_group_every_launch_config(gpu):
+    """Ragged groups under every gemv_w4 configuration: 5 calls on one input (split
+    4 + 1), members with and without zero points, N not a multiple of any row count."""
+    import torch
+    K, M = 896, 2
+    ops = [workloads.Op(f"g{i}", K, n, 32, zp) for i, (n, zp) in
+           enumerate([(300, True), (77, False), (1000, True), (5, True), (129, False)])]
+    host = [weights_for(o, 60 + i) for i, o in enumerate(ops)]
+    a = workloads.make_activations(M, K, 61)
+    dA = torch.from_numpy(a).cuda()
+    refs = [oracle.matmul_nbits(a, b, s, z, o.N, K, 4, 32) for o, (b, s, z, _) in zip(ops, host)]
+    stream = torch.cuda.current_stream().cuda_stream
+    try:
+        for cfg in range(1, gemv_config_count() + 1):
+            native.set_tuning(1, cfg)
+            Ys = [torch.full((M, o.N), float("nan"), device="cuda") for o in ops]
+            native.gemm_dev_batch([h[3] for h in host], [dA.data_ptr()] * len(ops), [y.data_ptr() for y in Ys],
+                                  M, stream)
+            torch.cuda.synchronize()
+            for o, y, ref in zip(ops, Ys, refs):
+                assert_gemv_close(y.cpu().numpy(), ref, f"cfg {cfg} {o.name}")
+    finally:
+        native.set_tuning(1, 0)
+    for h in host:
+        h[3].close()
+
+
 def test_batch_entry_matches_single_calls(gpu):
     import torch
     ops = workloads.DECODE_7B[:4]
