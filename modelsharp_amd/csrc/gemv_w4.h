@@ -182,40 +182,44 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
             const int k = k0 + u;
             if (k < nvalid) {
                 const int c = k * SPAN + lofs;
-                uint32_t pr[RL][4][4];
+                // Walk the chunk one code dword (8 codes, two float4 of activations) at a time:
+                // each LDS read of activations serves the lane's RL rows, and only one dword's
+                // code pairs per row are live. For M <= 2 even and odd dwords feed two partial
+                // sums (shorter dependency chains); otherwise one chain in dword order.
+                constexpr int NP = M <= 2 ? 2 : 1;
+                float t[RL][M][NP];
 #pragma unroll
                 for (int j = 0; j < RL; ++j) {
-                    const uint32_t qd[4] = {bt.q[j][u].x, bt.q[j][u].y, bt.q[j][u].z, bt.q[j][u].w};
 #pragma unroll
-                    for (int d = 0; d < 4; ++d) code_pairs(qd[d], pr[j][d]);
+                    for (int m = 0; m < M; ++m) {
+#pragma unroll
+                        for (int q = 0; q < NP; ++q) t[j][m][q] = 0.0f;
+                    }
+                }
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    uint32_t pr[RL][4];
+#pragma unroll
+                    for (int j = 0; j < RL; ++j) {
+                        const uint32_t qd = d == 0 ? bt.q[j][u].x : d == 1 ? bt.q[j][u].y : d == 2 ? bt.q[j][u].z : bt.q[j][u].w;
+                        code_pairs(qd, pr[j]);
+                    }
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        const float4* arow = &lds_a4[(m * C + c) * kChunkStride4];
+                        const float4 a0 = arow[2 * d], a1 = arow[2 * d + 1];
+#pragma unroll
+                        for (int j = 0; j < RL; ++j) t[j][m][d % NP] = qdot8(pr[j], a0, a1, t[j][m][d % NP]);
+                    }
                 }
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
-                    // With RL > 1 one read of the activation chunk serves the lane's RL rows
-                    // (held in registers); with RL = 1 it streams from LDS (fewer VGPRs).
-                    const float4* arow = &lds_a4[(m * C + c) * kChunkStride4];
-                    float4 areg[RL > 1 ? 9 : 1];
-                    if constexpr (RL > 1) {
-#pragma unroll
-                        for (int i = 0; i < 9; ++i) areg[i] = arow[i];
-                    }
-                    const float4* a = RL > 1 ? areg : arow;
+                    const float asum = lds_a4[(m * C + c) * kChunkStride4 + 8].x;
 #pragma unroll
                     for (int j = 0; j < RL; ++j) {
-                        float blkacc;
-                        if constexpr (M <= 2) {
-                            float t0 = qdot8(pr[j][0], a[0], a[1], 0.0f);
-                            float t1 = qdot8(pr[j][1], a[2], a[3], 0.0f);
-                            t0 = qdot8(pr[j][2], a[4], a[5], t0);
-                            t1 = qdot8(pr[j][3], a[6], a[7], t1);
-                            blkacc = t0 + t1;
-                        } else {
-                            blkacc = 0.0f;
-#pragma unroll
-                            for (int d = 0; d < 4; ++d) blkacc = qdot8(pr[j][d], a[2 * d], a[2 * d + 1], blkacc);
-                        }
+                        float blkacc = NP == 2 ? t[j][m][0] + t[j][m][NP - 1] : t[j][m][0];
                         const float zpf = ozp ? (float)((bt.z[j][u] >> zshift) & 0x0F) : 8.0f;
-                        blkacc = __builtin_fmaf(-zpf, a[8].x, blkacc);
+                        blkacc = __builtin_fmaf(-zpf, asum, blkacc);
                         acc[j][m] = __builtin_fmaf(bt.s[j][u], blkacc, acc[j][m]);
                     }
                 }
@@ -281,7 +285,7 @@ constexpr GemvConfig kGemvConfigs[] = {
     {4, 16, 1, 2, 1},  {4, 16, 1, 4, 1},  {4, 32, 1, 4, 1},  {4, 64, 1, 2, 1},  {4, 16, 4, 2, 1},
     {4, 32, 2, 2, 1},  {8, 32, 1, 4, 1},  {8, 16, 2, 4, 1},  {8, 16, 4, 2, 1},  {16, 16, 4, 2, 1},
     {16, 32, 2, 2, 1}, {4, 16, 1, 2, 2},  {4, 16, 1, 4, 2},  {4, 32, 1, 2, 2},  {4, 64, 1, 2, 2},
-    {8, 16, 2, 2, 2},
+    {8, 16, 2, 2, 2},  {4, 16, 1, 1, 2},
 };
 constexpr int kNumGemvConfigs = sizeof(kGemvConfigs) / sizeof(kGemvConfigs[0]);
 constexpr int kGemvMaxM = 4;
