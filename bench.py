@@ -264,6 +264,22 @@ def main() -> int:
         del gg
     dom = groups["gate_up"]
     gate = next(op for op in ops if op.name == "gate")   # the CPU baseline's sample
+
+    # host-pointer entry (ms_hip_nbits_gemm): H2D of A, the kernel, D2H of Y, synchronous,
+    # pageable host buffers; rotating over the weight copies. Reported, never `value`.
+    gi = ops.index(gate)
+    a_host = workloads.make_activations(1, gate.K, 99)
+    for r in range(copies):
+        rot.handles[r][gi].gemm(a_host)
+    calls = max(copies, 8 * copies)
+    t0 = time.perf_counter()
+    for c in range(calls):
+        rot.handles[c % copies][gi].gemm(a_host)
+    host_us = (time.perf_counter() - t0) / calls * 1e6
+    host = {"op": "gate", "K": gate.K, "N": gate.N, "M": 1, "us_per_call": round(host_us, 2),
+            "GBs": round(workloads.algorithmic_bytes(gate, 1) / (host_us * 1e-6) / 1e9, 1),
+            "path": "ms_hip_nbits_gemm: H2D A + kernel + D2H Y, synchronous, pageable host buffers"}
+    log(f"  host-pointer gate call: {host_us:.2f} us ({host['GBs']} GB/s, PCIe copies included)")
     traffic = measured_traffic(dom["kernel"])
     rot.close()
     del rot, g
@@ -280,6 +296,7 @@ def main() -> int:
         "ms_per_step_ungrouped": round(ms_step_ungrouped, 5),
         "per_op": per_op,
         "groups": groups,
+        "host_pointer": host,
         "roofline": {"bound": "hbm", "kernel": "gemv_w4, gate+up in one launch (K=3584, 2 x N=18944, M=1)",
                      "achieved": dom["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["GBs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
@@ -388,6 +405,22 @@ def detail_workloads(args):
                 rot.close()
                 del rot, g
                 torch.cuda.empty_cache()
+    # Qwen2.5-0.5B decode token: the 8 projections in one batch call with the inputs shared
+    # as in the model (q/k/v one input, gate/up another), against the sum of single launches.
+    ops = workloads.QWEN05B_DECODE
+    fp = sum(workloads.algorithmic_bytes(op, 1) for op in ops)
+    copies = min(workloads.rotation_copies(fp, args.rotate_mib << 20), 64)
+    rot = Rotation(ops, 1, copies, seed=3, share=workloads.QWEN05B_DECODE_SHARE)
+    g = graph_of(lambda stream: [rot.enqueue(r, stream) for r in range(copies)])
+    ms = time_graph(g, 50, 2) / copies
+    single = sum(v["us"] for k, v in out.items() if k.startswith("qwen05b_decode/"))
+    out["qwen05b_decode/per_token"] = {"bytes": fp, "us_grouped": round(ms * 1e3, 3),
+                                       "GBs_grouped": round(fp / (ms * 1e-3) / 1e9, 1),
+                                       "us_sum_of_single_launches": round(single, 3)}
+    log(f"  qwen05b_decode/per_token: {out['qwen05b_decode/per_token']}")
+    rot.close()
+    del rot, g
+    torch.cuda.empty_cache()
     return out
 
 

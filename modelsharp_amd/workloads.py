@@ -57,6 +57,9 @@ QWEN05B_UP = _qwen("up", 896, 4864)
 QWEN05B_DECODE = [_qwen("q", 896, 896), _qwen("k", 896, 128), _qwen("v", 896, 128), _qwen("o", 896, 896),
                   _qwen("gate", 896, 4864), _qwen("up", 896, 4864), _qwen("down", 4864, 896),
                   _qwen("lm_head", 896, 151936)]
+# Activation buffer each QWEN05B_DECODE projection reads in the model: q/k/v share the
+# attention input, gate/up the MLP input; o, down and lm_head read their own.
+QWEN05B_DECODE_SHARE = [0, 0, 0, 3, 4, 4, 6, 7]
 DECODE_7B = [_7b("q", 3584, 3584), _7b("k", 3584, 512), _7b("v", 3584, 512), _7b("o", 3584, 3584),
              _7b("gate", 3584, 18944), _7b("up", 3584, 18944), _7b("down", 18944, 3584)]
 # Activation buffer each DECODE_7B projection reads in a decoder layer: q/k/v share the
