@@ -82,7 +82,8 @@ int ms_hip_nbits_weights_info(void* handle, int* N, int* K, int* bits, int* bloc
  * Replaces ms_qgemm_nbits (native/ms_kernels.h:42-44, qgemm.cpp:77-118) on the
  * path NativeQuant.TryMatMulNBits (NativeQuant.cs:78-115) takes from
  * MatMulNBitsKernel.Execute (MatMulNBitsKernel.cs:174-191), with the weights
- * already resident. M<=16 runs the dequant-fused GEMV, larger M the MFMA GEMM. */
+ * already resident. M<=16 runs the dequant-fused GEMV (block size 128 and
+ * 4 <= M <= 16: its matrix-core form at the same accuracy), larger M the MFMA GEMM. */
 int ms_hip_nbits_gemm(void* handle, const float* a_host, float* y_host, int M);
 
 /* Device-pointer form: enqueues on `stream` (a hipStream_t, NULL = the null
@@ -90,9 +91,10 @@ int ms_hip_nbits_gemm(void* handle, const float* a_host, float* y_host, int M);
  * both 16-byte aligned device memory. Prefill calls (M > 16) stage A as fp16 in
  * a workspace owned by the handle, and launches with few output tiles split K over
  * two workgroups per tile that meet through the handle's per-tile counters and
- * partial-sum slots. These buffers grow on demand, never while `stream` is being
- * captured (a call under capture that would need larger ones takes the
- * workspace-free MFMA kernel instead), so prefill calls on one handle from
+ * partial-sum slots; the small-M matrix-core kernel splits K over several
+ * workgroups per 128-row tile the same way. These buffers grow on demand, never
+ * while `stream` is being captured (a call under capture that would need larger
+ * ones takes a workspace-free kernel instead), so such calls on one handle from
  * different streams must not overlap. */
 int ms_hip_nbits_gemm_dev(void* handle, const float* dA, float* dY, int M, void* stream);
 
@@ -135,9 +137,14 @@ int ms_hip_sync(void);
  *   1 gemv_w4 launch configuration: c+1 forces configuration c of the library's
  *     table (used only where it fits the shape), -1 forces gemv_w4_panel;
  *   2 1 routes every M > 16 call to mfma_w4 (the pipelined prefill off);
- *   3 1 or 2 forces the pipelined prefill's K split (2 needs K >= 256).
+ *   3 1 or 2 forces the pipelined prefill's K split (2 needs K >= 256);
+ *   4 1 keeps M <= 16 off the small-M matrix-core kernel, 2 sends every eligible
+ *     M (1 and 2 included) to it;
+ *   5 workgroups per row tile of the small-M matrix-core kernel (1..64, clamped to
+ *     [ceil(K / 512), K / 128]).
  * ms_hip_nbits_launch_info reports what a call with M rows would launch:
- *   kernel_id 0 generic, 1 gemv_w4, 2 mfma_w4, 3 gemv_w4_panel, 4 mfma_w4_pipe. */
+ *   kernel_id 0 generic, 1 gemv_w4, 2 mfma_w4, 3 gemv_w4_panel, 4 mfma_w4_pipe,
+ *   5 skinny_w4. */
 /* ms_hip_nbits_batch_launch_info: what the first launch of a batch call with these
  * handles and activations would be: `calls` = how many of the leading calls it
  * serves, then as ms_hip_nbits_launch_info. */

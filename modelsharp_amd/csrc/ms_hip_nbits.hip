@@ -30,6 +30,7 @@
 #include "generic_nbits.h"
 #include "mfma_w4.h"
 #include "mfma_w4_pipe.h"
+#include "skinny_w4.h"
 
 using namespace msnb;
 
@@ -118,6 +119,11 @@ struct Weights {
     int* d_sync = nullptr;      // split-K arrival counters and flags, zero between launches
     float* d_part = nullptr;    // split-K partial sums, kPipeBM x kPipeBN floats per tile
     int sync_tiles = 0;         // tiles covered by d_sync and d_part
+    // small-M matrix-core GEMV: A as hi/lo fp16 + block exponents, K-split slots, counters
+    uint8_t* d_sk = nullptr;    // skinny_w4 slots: [row tiles][workgroups per tile][16 x 128 floats]
+    size_t sk_bytes = 0;
+    int* d_sk_sync = nullptr;   // per row tile, zero between launches
+    int sk_blocks = 0;
 };
 
 constexpr uint32_t kHandleMagic = 0x4D534E42u;   // "MSNB"
@@ -177,6 +183,8 @@ void free_weights(Weights& w)
     if (w.d_a16) (void)hipFree(w.d_a16);
     if (w.d_sync) (void)hipFree(w.d_sync);
     if (w.d_part) (void)hipFree(w.d_part);
+    if (w.d_sk) (void)hipFree(w.d_sk);
+    if (w.d_sk_sync) (void)hipFree(w.d_sk_sync);
     if (w.stream) (void)hipStreamDestroy(w.stream);
     w.d_b = nullptr;
     w.d_scales = nullptr;
@@ -187,6 +195,10 @@ void free_weights(Weights& w)
     w.d_sync = nullptr;
     w.d_part = nullptr;
     w.sync_tiles = 0;
+    w.d_sk = nullptr;
+    w.sk_bytes = 0;
+    w.d_sk_sync = nullptr;
+    w.sk_blocks = 0;
     w.stream = nullptr;
 }
 
@@ -237,6 +249,8 @@ int g_panel_lanes_override = 0;  // knob 0: gemv_w4_panel lanes per row
 int g_gemv_config = 0;           // knob 1: c+1 forces kGemvConfigs[c], -1 forces gemv_w4_panel
 int g_pipe_off = 0;              // knob 2: 1 routes every prefill call to mfma_w4
 int g_pipe_ksplit = 0;           // knob 3: 1 or 2 forces the prefill K split (where K allows 2)
+int g_skinny = 0;                // knob 4: 1 keeps M <= 16 off skinny_w4, 2 sends every eligible M to it
+int g_skinny_ksw = 0;            // knob 5: workgroups per skinny_w4 row block (0: heuristic)
 
 // gemv_w4 instantiations: [M-1][L slot][config], L slot 0 = block size 32, 1 = block size 128.
 typedef void (*GemvFn)(GemvParams);
@@ -379,10 +393,14 @@ bool gemv_groupable(const Weights& a, const Weights& b)
 // How many of the calls starting at handles[0] one launch serves: consecutive calls on
 // the same activations (the projections of one input) that gemv_w4 can group, up to
 // kGemvMaxOps; 1 when the first call launches alone. *ci receives the group's config.
+bool skinny_eligible(const Weights& w, int M);
+int skinny_ksw(const Weights& w);
+
 int batch_group(void* const* handles, const float* const* dA, int count, int M, int* ci)
 {
     const Weights* w = from_handle(handles[0]);
     if (M <= 0 || M > kGemvMaxM || !dA[0] || (reinterpret_cast<uintptr_t>(dA[0]) & 15)) return 1;
+    if (skinny_eligible(*w, M)) return 1;   // the matrix-core small-M path launches per matrix
     int n = 1, ntot = w->N;
     while (n < count && n < kGemvMaxOps && dA[n] == dA[0] && gemv_groupable(*w, *from_handle(handles[n]))) {
         ntot += from_handle(handles[n])->N;
@@ -641,6 +659,94 @@ int launch_pipe(Weights& w, const float* dA, float* dY, int M, hipStream_t strea
     return hipGetLastError() == hipSuccess ? 1 : -1;
 }
 
+// ---- skinny_w4: M <= 16 on the matrix cores at fp32-level accuracy (block size 128) ----
+
+// The small-M matrix-core path takes block size 128 (a block is one group of four MFMA
+// steps), K a multiple of 128, and 4 <= M <= 16: at M <= 2 gemv_w4 is faster (measured
+// on the 7B MLP shapes), unless knob 4 says otherwise.
+constexpr int kSkinnyMinM = 4;
+bool skinny_eligible(const Weights& w, int M)
+{
+    if (g_skinny == 1 || !w.fast || w.log2cpb != 2 || (w.K % 128) != 0 || M < 1 || M > kSkinnyMT) return false;
+    if ((int64_t)kSkinnyMT * w.K * 4 >= INT32_MAX) return false;
+    return g_skinny == 2 || M >= kSkinnyMinM;
+}
+
+// Workgroups per row tile: each takes at most kSkinnyNB blocks and at least one; beyond
+// that minimum, more only while the grid has fewer than two workgroups per CU (every
+// extra split adds a slot to write and to sum).
+int skinny_ksw(const Weights& w)
+{
+    const int tiles = (w.N + kSkinnyRows - 1) / kSkinnyRows;
+    const int G = w.K / 128;
+    const int kmin = (G + kSkinnyNB - 1) / kSkinnyNB;
+    int ksw = kmin;
+    if (g_skinny_ksw > 0) {
+        ksw = g_skinny_ksw;
+    } else {
+        while (ksw < G && (int64_t)tiles * ksw < 2 * device_cus()) ++ksw;
+    }
+    return std::max(kmin, std::min(ksw, G));
+}
+
+// Returns 1 when launched, 0 when the caller should take gemv_w4 / gemv_w4_panel (the
+// workspace would have to grow under capture), negative on a launch error.
+int launch_skinny(Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
+{
+    const int tiles = (w.N + kSkinnyRows - 1) / kSkinnyRows;
+    const int ksw = skinny_ksw(w);
+    const size_t need = ksw > 1 ? (size_t)tiles * ksw * kSkinnySlot * sizeof(float) : 0;
+    uint8_t* ws = nullptr;
+    int* sync = nullptr;
+    if (ksw > 1) {
+        std::lock_guard<std::mutex> lock(w.ws_mu);
+        const bool grow = w.sk_bytes < need, grow_sync = w.sk_blocks < tiles;
+        if (grow || grow_sync) {
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+                (void)hipGetLastError();
+                return 0;
+            }
+            if (hipStreamSynchronize(stream) != hipSuccess) return -1;
+        }
+        if (grow) {
+            if (w.d_sk && hipFree(w.d_sk) != hipSuccess) return -1;
+            w.d_sk = nullptr;
+            w.sk_bytes = 0;
+            if (hipMalloc(&w.d_sk, need) != hipSuccess) return -1;
+            w.sk_bytes = need;
+        }
+        if (grow_sync) {
+            if (w.d_sk_sync && hipFree(w.d_sk_sync) != hipSuccess) return -1;
+            w.d_sk_sync = nullptr;
+            w.sk_blocks = 0;
+            if (hipMalloc(&w.d_sk_sync, (size_t)tiles * sizeof(int)) != hipSuccess) return -1;
+            // On the launch stream (never reached under capture: checked above).
+            if (hipMemsetAsync(w.d_sk_sync, 0, (size_t)tiles * sizeof(int), stream) != hipSuccess) return -1;
+            w.sk_blocks = tiles;
+        }
+        ws = w.d_sk;
+        sync = w.d_sk_sync;
+    }
+    SkinnyParams p;
+    p.b = w.d_b;
+    p.scales = w.d_scales;
+    p.zp = w.has_zp ? w.d_zp : nullptr;
+    p.a = dA;
+    p.y = dY;
+    p.slots = reinterpret_cast<float*>(ws);
+    p.sync = sync;
+    p.row_bytes = (int)w.row_bytes;
+    p.M = M;
+    p.N = w.N;
+    p.K = w.K;
+    p.nb = w.nb;
+    p.zrb = w.zrb;
+    p.ksw = ksw;
+    hipLaunchKernelGGL(skinny_w4_kernel, dim3(tiles * ksw), dim3(256), 0, stream, p);
+    return hipGetLastError() == hipSuccess ? 1 : -1;
+}
+
 int enqueue_gemm(Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
 {
     if (M < 0) return fail(MS_HIP_ERR_INVALID, "MatMulNBits M must be non-negative; got %d.", M);
@@ -649,7 +755,14 @@ int enqueue_gemm(Weights& w, const float* dA, float* dY, int M, hipStream_t stre
     if ((reinterpret_cast<uintptr_t>(dA) & 15) || (reinterpret_cast<uintptr_t>(dY) & 3))
         return fail(MS_HIP_ERR_INVALID, "[ms_hip] A must be 16-byte and Y 4-byte aligned");
     if (!w.fast) return launch_generic(w, dA, dY, M, stream);
-    if (M <= kPanelMaxM) return launch_gemv(w, dA, dY, M, stream);
+    if (M <= kPanelMaxM) {
+        if (skinny_eligible(w, M)) {
+            const int r = launch_skinny(w, dA, dY, M, stream);
+            if (r < 0) return fail(MS_HIP_ERR_HIP, "[ms_hip] small-M launch failed: %s", hipGetErrorString(hipGetLastError()));
+            if (r > 0) return MS_HIP_OK;
+        }
+        return launch_gemv(w, dA, dY, M, stream);
+    }
     if (pipe_eligible(w, M)) {
         const int r = launch_pipe(w, dA, dY, M, stream);
         if (r < 0) return fail(MS_HIP_ERR_HIP, "[ms_hip] prefill launch failed: %s", hipGetErrorString(hipGetLastError()));
@@ -1029,6 +1142,14 @@ int ms_hip_set_tuning(int knob, int value)
             if (value < 0 || value > 2) break;
             g_pipe_ksplit = value;
             return MS_HIP_OK;
+        case 4:
+            if (value < 0 || value > 2) break;
+            g_skinny = value;
+            return MS_HIP_OK;
+        case 5:
+            if (value < 0 || value > 64) break;
+            g_skinny_ksw = value;
+            return MS_HIP_OK;
         default: break;
     }
     return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid tuning knob %d = %d", knob, value);
@@ -1043,6 +1164,10 @@ int ms_hip_nbits_launch_info(void* handle, int M, int* kernel_id, int* lanes_per
     if (!w->fast) {
         kid = 0;
         gr = (int)(((int64_t)M * w->N + 255) / 256);
+        bl = 256;
+    } else if (M <= kPanelMaxM && skinny_eligible(*w, M)) {
+        kid = 5;
+        gr = ((w->N + kSkinnyRows - 1) / kSkinnyRows) * skinny_ksw(*w);
         bl = 256;
     } else if (M <= kPanelMaxM) {
         const int ci = pick_gemv_config(*w, M, w->N);

@@ -152,6 +152,23 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, (int)kBufferWord3);
 }
 
+// Cross-workgroup hand-off through data written and read with agent-scope atomic
+// stores / loads (those write and read through the caches, so the data needs no L2
+// write-back or invalidate). These two only order: the release form waits until every
+// earlier vector memory operation of the wave has completed, the acquire form keeps
+// later loads behind the atomic it follows. (An agent-scope fence would also write back
+// or invalidate the XCD's whole L2, which costs microseconds per workgroup.)
+__device__ __forceinline__ void wait_vmem_order_only_release()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xF << 8));   // vmcnt(0) expcnt(7) lgkmcnt(15)
+}
+__device__ __forceinline__ void wait_vmem_order_only_acquire()
+{
+    __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xF << 8));
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
 // acc + a * (fp16 lane widened) — one v_fma_mix_f32.
 __device__ __forceinline__ float mix_lo_acc(uint32_t h2, float a, float acc)
 {

@@ -1,0 +1,285 @@
+// skinny_w4.h — small-M INT4 GEMV on the matrix cores at fp32-level accuracy
+// (M <= 16, block size 128, K a multiple of 128).
+//
+// Y[M,N] = A[M,K] * W^T with W = (q - zp) * s. Per weight row n and block b (128 k):
+//     Y[m][n] += s[n][b] * sum_{k in b} A[m][k] * (q[n][k] - zp[n][b]).
+// The inner sums run on v_mfma_f32_16x16x32_f16 without losing fp32 accuracy:
+//   * q - zp is a small integer, exact in fp16 (the 0x6400 magic and one packed
+//     subtract, as in the prefill kernel's dequant, without the scale);
+//   * A is split per row m and block b into A = 2^e * (hi + lo), hi = fp16(A 2^-e),
+//     lo = fp16(A 2^-e - hi), with e chosen so the block's max |A| 2^-e lies in
+//     [2^14, 2^15). Every product hi (q - zp) and lo (q - zp) is exact in fp32, and
+//     hi + lo carries A to about 2^-22 of the block's max;
+//   * the block sums (fp32, accumulated by the MFMAs) are multiplied by 2^e (exact) and
+//     by s, and added to the running sum in fp32.
+// So the arithmetic is the GEMV's (exact products, fp32 sums, the scale applied per
+// block); only the activations' last bits below 2^-22 of the block max are dropped.
+//
+// Work mapping. A workgroup (4 waves) owns kSkinnyRows weight rows and a range of at
+// most kSkinnyNB blocks; each wave owns 16 * kSkinnyNF of the rows. The workgroup
+//   1. issues its activation loads, then every weight load of every wave (all blocks in
+//      flight at once: a block costs a wave 6 * kSkinnyNF registers, the activations
+//      live in LDS);
+//   2. converts the activations of its K range to hi / lo / 2^e straight into LDS, in
+//      the MFMA operand order, while the weights are in flight;
+//   3. per block and fragment: lane (n = lane % 16, s = lane / 16) holds the 16-byte
+//      chunk s of its row's 64-byte block and feeds dword j of it to MFMA step j
+//      (j = 0..3): step j covers k = 32 s + 8 j + [0, 8) for s = 0..3, so the four
+//      steps cover the block, and the activations in LDS are laid out to match (lane
+//      (m, s) of step j reads 16 contiguous bytes, a whole step 1 KB);
+//   4. `ksw` workgroups split a row tile's blocks and meet through per-workgroup slots
+//      (rows m < M only), the last to arrive summing the slots in index order
+//      (deterministic; the arrival counters reset themselves).
+// The activation permutation within an 8-k group is k0,k4,k1,k5,k2,k6,k3,k7: the order
+// in which the dequant produces fp16 pairs from one dword of packed nibbles.
+#pragma once
+#include "nbits_device.h"
+#include "mfma_w4.h"
+
+namespace msnb {
+
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kSkinnyMT = 16;                            // MFMA rows: M padded to 16
+constexpr int kSkinnyNF = 2;                             // 16-row MFMA fragments per wave
+constexpr int kSkinnyRows = 4 * 16 * kSkinnyNF;          // weight rows per workgroup
+constexpr int kSkinnyNB = 4;                             // blocks per workgroup, at most
+constexpr int kSkinnyStepBytes = 1024;                   // one MFMA step's activations (hi or lo)
+constexpr int kSkinnyBlockBytes = 4 * 2 * kSkinnyStepBytes;   // one block: 4 steps x (hi, lo)
+constexpr int kSkinnySlot = kSkinnyMT * kSkinnyRows;     // floats per workgroup slot
+// Buffer cache policy sc1 (device scope): stores write through to where every XCD
+// reads, loads do not return another XCD's stale copy.
+constexpr int kDeviceCoherent = 16;
+
+struct SkinnyParams {
+    const uint8_t* b;          // [N][row_bytes]
+    const float* scales;       // [N][nb]
+    const uint8_t* zp;         // [N][zrb] or nullptr (zp = 8)
+    const float* a;            // [M][K]
+    float* y;                  // [M][N]
+    float* slots;              // [row tiles][ksw][kSkinnySlot] (ksw > 1)
+    int* sync;                 // [row tiles] arrival counters, zero between launches (ksw > 1)
+    int row_bytes, M, N, K, nb, zrb;
+    int ksw;                   // workgroups per row tile: ksw * kSkinnyNB >= K / 128, ksw <= K / 128
+};
+
+__global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
+{
+    constexpr int NF = kSkinnyNF, NB = kSkinnyNB;
+    __shared__ __attribute__((aligned(16))) uint32_t lds_a[NB * kSkinnyBlockBytes / 4];
+    __shared__ __attribute__((aligned(16))) float lds_e[NB * kSkinnyMT];
+
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int ln = lane & 15, ls = lane >> 4;
+    const int rt = blockIdx.x / p.ksw, kw = blockIdx.x - rt * p.ksw;
+    const int G = p.K >> 7;
+    const int g0 = (int)((int64_t)kw * G / p.ksw), g1 = (int)((int64_t)(kw + 1) * G / p.ksw);
+    const int cnt = g1 - g0;                                  // 1 .. NB blocks
+    const int n0 = rt * kSkinnyRows + wave * 16 * NF;         // this wave's first row
+
+    const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(p.a, p.M * p.K * 4);
+    const __amdgpu_buffer_rsrc_t rb_ = buffer_rsrc(p.b, p.N * p.row_bytes);
+    const __amdgpu_buffer_rsrc_t rsc = buffer_rsrc(p.scales, p.N * p.nb * 4);
+    const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(p.zp ? (const void*)p.zp : (const void*)p.scales,
+                                                  p.zp ? p.N * p.zrb : 0);
+
+    // ---- 1. loads: activations first (they are consumed first), then the weights ----
+    // Activation pass i: row m = 8 (i & 1) + hh of block lg = i >> 1, where hh = tid / 32
+    // is the half-wave and lane q = tid % 32 takes k = 4 q .. 4 q + 3 of the block. Rows
+    // m >= M and blocks past the range read zeros.
+    const int hh = tid >> 5, q = tid & 31;
+    float4 av[2 * NB];
+#pragma unroll
+    for (int i = 0; i < 2 * NB; ++i) {
+        const int m = 8 * (i & 1) + hh, lg = i >> 1;
+        const bool ok = m < p.M && lg < cnt;
+        av[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               ra, ok ? (m * p.K + (g0 + lg) * 128 + 4 * q) * 4 : kOOB, 0, 0));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    int cbase[NF], sbase[NF], zbase[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        const int n = n0 + 16 * f + ln;
+        const bool in = n < p.N;
+        cbase[f] = in ? n * p.row_bytes + ls * 16 : kOOB;
+        sbase[f] = in ? n * p.nb * 4 : kOOB;
+        zbase[f] = in ? n * p.zrb : kOOB;
+    }
+    // One load group per block, issued in block order, so computing block lg waits only
+    // for its own group (the scheduling barriers keep the groups apart). The zero-point
+    // bytes stay bytes: a widened copy could be moved by the compiler ahead of its group.
+    u32x4_t c[NB][NF];
+    float sc[NB][NF];
+    uint8_t zq[NB][NF];
+#pragma unroll
+    for (int lg = 0; lg < NB; ++lg) {
+        const int g = g0 + lg;
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            const bool ok = lg < cnt && cbase[f] != kOOB;
+            c[lg][f] = __builtin_amdgcn_raw_buffer_load_b128(rb_, ok ? cbase[f] + g * 64 : kOOB, 0, 0);
+            sc[lg][f] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc, ok ? sbase[f] + g * 4 : kOOB, 0, 0));
+            zq[lg][f] = __builtin_amdgcn_raw_buffer_load_b8(rz, ok ? zbase[f] + (g >> 1) : kOOB, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ---- 2. activations -> LDS: hi / lo fp16 in the MFMA operand order, 2^e per row/block ----
+    // LDS layout: block lg, step j, part (0 hi, 1 lo): 1 KB of 64 16-byte chunks, chunk
+    // (s, m) at (16 s + m) * 16 holding k = 32 s + 8 j + (0,4,1,5,2,6,3,7). Quad q has
+    // s = q / 8, j = (q / 2) % 4, and is the first (q even) or second (q odd) value of
+    // each pair in the chunk; the even quad of a pair writes the hi chunk, the odd one
+    // the lo chunk, each after swapping the other part with its neighbour.
+#pragma unroll
+    for (int i = 0; i < 2 * NB; ++i) {
+        const int m = 8 * (i & 1) + hh, lg = i >> 1;
+        const float4 v = av[i];
+        float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+        // 2^-e brings the block max into [2^14, 2^15): e = exponent(mx) - 14 (0 for an
+        // all-zero block); e <= 113 for every finite mx, so 2^-e stays a normal float.
+        int e = 0;
+        if (mx > 0.0f) e = ((int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xFF) - 127) - 14;
+        e = e < -126 ? -126 : e > 126 ? 126 : e;
+        const float up = __builtin_bit_cast(float, (uint32_t)(127 + e) << 23);     // 2^e
+        const float down = __builtin_bit_cast(float, (uint32_t)(127 - e) << 23);   // 2^-e
+        const float x[4] = {v.x * down, v.y * down, v.z * down, v.w * down};
+        uint32_t hp[2], lp[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const _Float16 h0 = (_Float16)x[2 * t], h1 = (_Float16)x[2 * t + 1];
+            const _Float16 l0 = (_Float16)(x[2 * t] - (float)h0), l1 = (_Float16)(x[2 * t + 1] - (float)h1);
+            hp[t] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+            lp[t] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+        }
+        const int odd = q & 1;
+        uint32_t first[2], second[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const uint32_t got = __shfl_xor(odd ? hp[t] : lp[t], 1, kWave);   // the neighbour's other part
+            first[t] = odd ? got : hp[t];       // the even quad's value of the written part
+            second[t] = odd ? lp[t] : got;      // the odd quad's value
+        }
+        u32x4_t out;
+        out.x = (first[0] & 0xFFFFu) | (second[0] << 16);
+        out.y = (first[0] >> 16) | (second[0] & 0xFFFF0000u);
+        out.z = (first[1] & 0xFFFFu) | (second[1] << 16);
+        out.w = (first[1] >> 16) | (second[1] & 0xFFFF0000u);
+        const int s = q >> 3, j = (q >> 1) & 3;
+        const int at = (((lg * 4 + j) * 2 + odd) * kSkinnyStepBytes + (s * 16 + m) * 16) / 4;
+        *reinterpret_cast<u32x4_t*>(&lds_a[at]) = out;
+        if (q == 0) lds_e[lg * kSkinnyMT + m] = up;
+    }
+    __syncthreads();
+
+    // ---- 3. blocks ----
+    floatx4_t acc[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) acc[f] = floatx4_t{};
+    const uint32_t zdef = p.zp ? 0u : 8u;    // without zero points the zp loads read zeros
+#pragma unroll
+    for (int lg = 0; lg < NB; ++lg) {
+        if (lg >= cnt) break;
+        floatx4_t th[NF], tl[NF];
+        uint32_t zb[NF];
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            th[f] = floatx4_t{};
+            tl[f] = floatx4_t{};
+            const uint32_t zp = (((uint32_t)zq[lg][f] >> (((g0 + lg) & 1) * 4)) & 0x0F) + zdef;
+            zb[f] = kHalfMagic | (zp << 16) | zp;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const half8_t ah = *reinterpret_cast<const half8_t*>(&lds_a[((lg * 4 + j) * 2) * 256 + lane * 4]);
+            const half8_t al = *reinterpret_cast<const half8_t*>(&lds_a[((lg * 4 + j) * 2 + 1) * 256 + lane * 4]);
+#pragma unroll
+            for (int f = 0; f < NF; ++f) {
+                const uint32_t x = j == 0 ? c[lg][f].x : j == 1 ? c[lg][f].y : j == 2 ? c[lg][f].z : c[lg][f].w;
+                const h2_t z2 = as_h2(zb[f]);
+                const uint32_t o0 = as_u32(as_h2(and_or(x, 0x000F000Fu, kHalfMagic)) - z2);
+                const uint32_t o1 = as_u32(as_h2(and_or(x >> 4, 0x000F000Fu, kHalfMagic)) - z2);
+                const uint32_t o2 = as_u32(as_h2(and_or(x >> 8, 0x000F000Fu, kHalfMagic)) - z2);
+                const uint32_t o3 = as_u32(as_h2(and_or(x >> 12, 0x000F000Fu, kHalfMagic)) - z2);
+                const half8_t bq = __builtin_bit_cast(half8_t, u32x4_t{o0, o1, o2, o3});
+                th[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq, th[f], 0, 0, 0);
+                tl[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq, tl[f], 0, 0, 0);
+            }
+        }
+        // th / tl[f][v]: block sums for activation row m = 4 ls + v and weight row
+        // n0 + 16 f + ln; times 2^e[m] (exact) and s[n], into the running sum.
+        const float4 e4 = *reinterpret_cast<const float4*>(&lds_e[lg * kSkinnyMT + 4 * ls]);
+        const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[f][v] = __builtin_fmaf((th[f][v] + tl[f][v]) * ev[v], sc[lg][f], acc[f][v]);
+        }
+    }
+
+    // ---- 4. output ----
+    if (p.ksw == 1) {
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            const int n = n0 + 16 * f + ln;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int m = 4 * ls + v;
+                if (m < p.M && n < p.N) p.y[(int64_t)m * p.N + n] = acc[f][v];
+            }
+        }
+        return;
+    }
+    // Slots [m][kSkinnyRows] (rows m < M), written through to device scope and read
+    // back by the last arriver with device-coherent loads: the hand-off needs no L2
+    // write-back or invalidate, only the order (every slot store has completed before
+    // the barrier that precedes the arrival; the last arriver's loads follow its count).
+    const __amdgpu_buffer_rsrc_t rsl = buffer_rsrc(p.slots, (int)gridDim.x * kSkinnySlot * 4);
+    const int own = (rt * p.ksw + kw) * kSkinnySlot;
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        const int col = wave * 16 * NF + 16 * f + ln;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int m = 4 * ls + v;
+            const float val = acc[f][v];   // a scalar first: a bit cast of a vector element reads element 0
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, val), rsl,
+                                                  m < p.M ? (own + m * kSkinnyRows + col) * 4 : kOOB, 0,
+                                                  kDeviceCoherent);
+        }
+    }
+    wait_vmem_order_only_release();
+    __syncthreads();
+    __shared__ int arrival;
+    if (tid == 0) arrival = __hip_atomic_fetch_add(p.sync + rt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (arrival != p.ksw - 1) return;
+    wait_vmem_order_only_acquire();
+    if (tid == 0) __hip_atomic_store(p.sync + rt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int first = rt * p.ksw * kSkinnySlot;
+#pragma unroll
+    for (int i = 0; i < kSkinnySlot / (4 * 256); ++i) {
+        const int e = 4 * (tid + 256 * i), m = e / kSkinnyRows, col = e - m * kSkinnyRows;
+        if (m >= p.M) break;
+        float4 tot = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int w = 0; w < p.ksw; ++w) {
+            const float4 sl = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                             rsl, (first + w * kSkinnySlot + e) * 4, 0, kDeviceCoherent));
+            tot.x += sl.x;
+            tot.y += sl.y;
+            tot.z += sl.z;
+            tot.w += sl.w;
+        }
+        const float tv[4] = {tot.x, tot.y, tot.z, tot.w};
+        const int nb0 = rt * kSkinnyRows + col;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            if (nb0 + t < p.N) p.y[(int64_t)m * p.N + nb0 + t] = tv[t];
+        }
+    }
+}
+
+}  // namespace msnb

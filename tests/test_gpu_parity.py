@@ -117,10 +117,82 @@ DECODE_CASES = ([(workloads.QWEN05B_UP, 1)] + [(o, 1) for o in workloads.QWEN05B
 def test_gemv_parity(gpu, op, M):
     b, s, z, w = weights_for(op, seed=op.N + 3 * op.K + M)
     a = workloads.make_activations(M, op.K, seed=M + op.K)
-    assert w.launch_info(M)["kernel"] in ("gemv_w4", "gemv_w4_panel")
+    assert w.launch_info(M)["kernel"] in ("gemv_w4", "gemv_w4_panel", "skinny_w4")
     log(f"gemv M={M} K={op.K} N={op.N} bs={op.block_size} {w.launch_info(M)}")
     y = w.gemm(a)
     assert_gemv_close(y, oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, op.block_size), f"M={M} {op}")
+    w.close()
+
+
+# (K, knob 5): K=640 is 5 blocks, split 5 ways by default (one block per workgroup) or
+# 2 ways (2 and 3 blocks); K=512 in one workgroup per row tile (no slots, direct stores).
+SKINNY_SPLITS = [(640, 0), (640, 2), (512, 1)]
+
+
+@pytest.mark.parametrize("K,ksw", SKINNY_SPLITS, ids=lambda v: str(v))
+@pytest.mark.parametrize("zp", [False, True], ids=["nozp", "zp"])
+def test_skinny_every_m_dynamic_range(gpu, zp, K, ksw):
+    """The small-M matrix-core path (block size 128) for every M in 1..16 (M = 1 forced),
+    on a ragged shape (N=333 is no multiple of the 128-row tiles), with activations spanning
+    1e-4..1e5 across rows and blocks and a lone outlier: the per-block power-of-two split of
+    A keeps the GEMV bar, whatever the number of workgroups per row tile. Two calls agree
+    bit for bit."""
+    op = workloads.Op("sk", K, 333, 128, zp)
+    b, s, z, w = weights_for(op, seed=70 + zp)
+    rng = np.random.default_rng(71)
+    try:
+        native.set_tuning(4, 2)
+        native.set_tuning(5, ksw)
+        for M in range(1, 17):
+            a = workloads.make_activations(M, op.K, seed=72 + M)
+            a *= (10.0 ** rng.uniform(-4, 5, size=(M, 1))).astype(np.float32)        # per-row magnitude
+            a[:, 128:256] *= np.float32(1e-3)                                         # one quiet block
+            a[M // 2, 300] = np.float32(3e6)                                          # one outlier
+            info = w.launch_info(M)
+            assert info["kernel"] == "skinny_w4", info
+            y = w.gemm(a)
+            assert_gemv_close(y, oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, 128), f"skinny M={M} zp={zp} K={K}")
+            assert np.array_equal(w.gemm(a), y), M
+    finally:
+        native.set_tuning(4, 0)
+        native.set_tuning(5, 0)
+    w.close()
+
+
+def test_skinny_captured_before_and_after_eager_call(gpu):
+    """Captured before any eager call (no workspace yet) the small-M call takes gemv_w4;
+    captured afterwards it runs the matrix-core path, whose slot counters reset
+    themselves: every replay equals the eager call bit for bit."""
+    import torch
+    op = workloads.Op("skc", 4096, 1000, 128, False)
+    b, s, z, w = weights_for(op, seed=73)
+    M = 8
+    a = workloads.make_activations(M, op.K, seed=74)
+    ref = oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, 128)
+    dA = torch.from_numpy(a).cuda()
+    dY = torch.zeros((M, op.N), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        w.gemm_dev(dA.data_ptr(), dY.data_ptr(), M, torch.cuda.current_stream().cuda_stream)
+    for i in range(2):
+        dY.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert_gemv_close(dY.cpu().numpy(), ref, f"pre-eager replay {i}")
+    eager = w.gemm(a)
+    assert w.launch_info(M)["kernel"] == "skinny_w4"
+    assert_gemv_close(eager, ref, "eager")
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2):
+        w.gemm_dev(dA.data_ptr(), dY.data_ptr(), M, torch.cuda.current_stream().cuda_stream)
+    for i in range(3):
+        dY.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g2.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(dY.cpu().numpy(), eager), f"replay {i}"
     w.close()
 
 
