@@ -84,17 +84,18 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
                                                   p.zp ? p.N * p.zrb : 0);
 
     // ---- 1. loads: activations first (they are consumed first), then the weights ----
-    // Activation pass i: row m = 8 (i & 1) + hh of block lg = i >> 1, where hh = tid / 32
-    // is the half-wave and lane q = tid % 32 takes k = 4 q .. 4 q + 3 of the block. Rows
-    // m >= M and blocks past the range read zeros.
-    const int hh = tid >> 5, q = tid & 31;
-    float4 av[2 * NB];
+    // Activation pass i: row m = 4 i + gi / 4 and block lg = gi % 4 of the range, where
+    // gi = tid / 16 is a 16-lane group and lane pl = tid % 16 takes k = 8 pl .. 8 pl + 7
+    // of the block (two 16-byte loads). Only rows m < M and blocks lg < cnt are read.
+    const int gi = tid >> 4, pl = tid & 15;
+    u32x4_t av[4][2];
 #pragma unroll
-    for (int i = 0; i < 2 * NB; ++i) {
-        const int m = 8 * (i & 1) + hh, lg = i >> 1;
+    for (int i = 0; i < 4; ++i) {
+        const int m = 4 * i + (gi >> 2), lg = gi & 3;
         const bool ok = m < p.M && lg < cnt;
-        av[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                               ra, ok ? (m * p.K + (g0 + lg) * 128 + 4 * q) * 4 : kOOB, 0, 0));
+        const int off = (m * p.K + (g0 + lg) * 128 + 8 * pl) * 4;
+        av[i][0] = __builtin_amdgcn_raw_buffer_load_b128(ra, ok ? off : kOOB, 0, 0);
+        av[i][1] = __builtin_amdgcn_raw_buffer_load_b128(ra, ok ? off + 16 : kOOB, 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -127,51 +128,51 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
     }
 
     // ---- 2. activations -> LDS: hi / lo fp16 in the MFMA operand order, 2^e per row/block ----
-    // LDS layout: block lg, step j, part (0 hi, 1 lo): 1 KB of 64 16-byte chunks, chunk
-    // (s, m) at (16 s + m) * 16 holding k = 32 s + 8 j + (0,4,1,5,2,6,3,7). Quad q has
-    // s = q / 8, j = (q / 2) % 4, and is the first (q even) or second (q odd) value of
-    // each pair in the chunk; the even quad of a pair writes the hi chunk, the odd one
-    // the lo chunk, each after swapping the other part with its neighbour.
+    // LDS layout: block lg, step j, part (0 hi, 1 lo): 1 KB of 64 16-byte chunks; the
+    // chunk of (s, m), holding k = 32 s + 8 j + (0,4,1,5,2,6,3,7), sits at position
+    // 16 s + (m ^ c) with c = 8 (s & 1) + 2 j + part. The swizzle keeps both sides free
+    // of bank conflicts: a 16-lane group converting one row writes 16 different
+    // positions (per part), and an MFMA step's 64 lanes read 64 different ones.
+    // Rows m >= M hold zeros (their MFMA rows then add nothing) and 2^e = 0.
 #pragma unroll
-    for (int i = 0; i < 2 * NB; ++i) {
-        const int m = 8 * (i & 1) + hh, lg = i >> 1;
-        const float4 v = av[i];
-        float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    for (int u = 0; u < NB * kSkinnyBlockBytes / (16 * 256); ++u) {
+        const int gc = tid + 256 * u, step = gc >> 6, pc = gc & 63, s = pc >> 4;
+        const int m = (pc & 15) ^ (((s & 1) << 3) | (((step >> 1) & 3) << 1) | (step & 1));
+        if (m >= p.M) *reinterpret_cast<u32x4_t*>(&lds_a[gc * 4]) = u32x4_t{0u, 0u, 0u, 0u};
+    }
+    if (tid < NB * kSkinnyMT && (tid & 15) >= p.M) lds_e[tid] = 0.0f;
 #pragma unroll
-        for (int off = 16; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
-        // 2^-e brings the block max into [2^14, 2^15): e = exponent(mx) - 14 (0 for an
-        // all-zero block); e <= 113 for every finite mx, so 2^-e stays a normal float.
-        int e = 0;
-        if (mx > 0.0f) e = ((int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xFF) - 127) - 14;
-        e = e < -126 ? -126 : e > 126 ? 126 : e;
-        const float up = __builtin_bit_cast(float, (uint32_t)(127 + e) << 23);     // 2^e
-        const float down = __builtin_bit_cast(float, (uint32_t)(127 - e) << 23);   // 2^-e
-        const float x[4] = {v.x * down, v.y * down, v.z * down, v.w * down};
-        uint32_t hp[2], lp[2];
+    for (int i = 0; i < 4; ++i) {
+        if (4 * i >= p.M) break;
+        const int m = 4 * i + (gi >> 2), lg = gi & 3;
+        const float4 v0 = __builtin_bit_cast(float4, av[i][0]), v1 = __builtin_bit_cast(float4, av[i][1]);
+        const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        float mx = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const _Float16 h0 = (_Float16)x[2 * t], h1 = (_Float16)x[2 * t + 1];
-            const _Float16 l0 = (_Float16)(x[2 * t] - (float)h0), l1 = (_Float16)(x[2 * t + 1] - (float)h1);
-            hp[t] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-            lp[t] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+        for (int r = 0; r < 8; ++r) mx = fmaxf(mx, fabsf(v[r]));
+#pragma unroll
+        for (int off = 8; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+        // mx in [2^(E-1), 2^E) with E = frexp exponent; 2^-e with e = E - 15 brings it
+        // into [2^14, 2^15) (an all-zero block gets e = -15 and stays zero).
+        const int e = __builtin_amdgcn_frexp_expf(mx) - 15;
+        if (m < p.M && lg < cnt) {
+            uint32_t hw[4], lw[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                // the pair (k = 8 pl + t, 8 pl + 4 + t): chunk order k0,k4,k1,k5,...
+                const float x0 = __builtin_amdgcn_ldexpf(v[t], -e), x1 = __builtin_amdgcn_ldexpf(v[t + 4], -e);
+                const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+                const _Float16 l0 = (_Float16)(x0 - (float)h0), l1 = (_Float16)(x1 - (float)h1);
+                hw[t] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+                lw[t] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+            }
+            const int s = pl >> 2, j = pl & 3, c = ((s & 1) << 3) | (j << 1);
+            const int base = (lg * 4 + j) * 2 * kSkinnyStepBytes + s * 256;
+            *reinterpret_cast<u32x4_t*>(&lds_a[(base + (m ^ c) * 16) / 4]) = u32x4_t{hw[0], hw[1], hw[2], hw[3]};
+            *reinterpret_cast<u32x4_t*>(&lds_a[(base + kSkinnyStepBytes + (m ^ (c | 1)) * 16) / 4]) =
+                u32x4_t{lw[0], lw[1], lw[2], lw[3]};
+            if (pl == 0) lds_e[lg * kSkinnyMT + m] = __builtin_amdgcn_ldexpf(1.0f, e);
         }
-        const int odd = q & 1;
-        uint32_t first[2], second[2];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const uint32_t got = __shfl_xor(odd ? hp[t] : lp[t], 1, kWave);   // the neighbour's other part
-            first[t] = odd ? got : hp[t];       // the even quad's value of the written part
-            second[t] = odd ? lp[t] : got;      // the odd quad's value
-        }
-        u32x4_t out;
-        out.x = (first[0] & 0xFFFFu) | (second[0] << 16);
-        out.y = (first[0] >> 16) | (second[0] & 0xFFFF0000u);
-        out.z = (first[1] & 0xFFFFu) | (second[1] << 16);
-        out.w = (first[1] >> 16) | (second[1] & 0xFFFF0000u);
-        const int s = q >> 3, j = (q >> 1) & 3;
-        const int at = (((lg * 4 + j) * 2 + odd) * kSkinnyStepBytes + (s * 16 + m) * 16) / 4;
-        *reinterpret_cast<u32x4_t*>(&lds_a[at]) = out;
-        if (q == 0) lds_e[lg * kSkinnyMT + m] = up;
     }
     __syncthreads();
 
@@ -180,6 +181,14 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
 #pragma unroll
     for (int f = 0; f < NF; ++f) acc[f] = floatx4_t{};
     const uint32_t zdef = p.zp ? 0u : 8u;    // without zero points the zp loads read zeros
+    // This lane's chunk (s = ls, m = ln) of each step j and part, within a block's 8 KB.
+    int aoff[4][2];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int pt = 0; pt < 2; ++pt)
+            aoff[j][pt] = (j * 2 + pt) * kSkinnyStepBytes + ls * 256 + (ln ^ (((ls & 1) << 3) | (j << 1) | pt)) * 16;
+    }
 #pragma unroll
     for (int lg = 0; lg < NB; ++lg) {
         if (lg >= cnt) break;
@@ -194,8 +203,8 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const half8_t ah = *reinterpret_cast<const half8_t*>(&lds_a[((lg * 4 + j) * 2) * 256 + lane * 4]);
-            const half8_t al = *reinterpret_cast<const half8_t*>(&lds_a[((lg * 4 + j) * 2 + 1) * 256 + lane * 4]);
+            const half8_t ah = *reinterpret_cast<const half8_t*>(&lds_a[(lg * kSkinnyBlockBytes + aoff[j][0]) / 4]);
+            const half8_t al = *reinterpret_cast<const half8_t*>(&lds_a[(lg * kSkinnyBlockBytes + aoff[j][1]) / 4]);
 #pragma unroll
             for (int f = 0; f < NF; ++f) {
                 const uint32_t x = j == 0 ? c[lg][f].x : j == 1 ? c[lg][f].y : j == 2 ? c[lg][f].z : c[lg][f].w;
@@ -259,19 +268,32 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
     if (arrival != p.ksw - 1) return;
     wait_vmem_order_only_acquire();
     if (tid == 0) __hip_atomic_store(p.sync + rt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // The slots are loaded kBatch at a time, all in flight together, then added in index
+    // order (slots past ksw load as zeros): one device round trip per batch instead of
+    // one per slot.
+    constexpr int kBatch = 16;
     const int first = rt * p.ksw * kSkinnySlot;
 #pragma unroll
     for (int i = 0; i < kSkinnySlot / (4 * 256); ++i) {
         const int e = 4 * (tid + 256 * i), m = e / kSkinnyRows, col = e - m * kSkinnyRows;
         if (m >= p.M) break;
         float4 tot = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int w = 0; w < p.ksw; ++w) {
-            const float4 sl = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                             rsl, (first + w * kSkinnySlot + e) * 4, 0, kDeviceCoherent));
-            tot.x += sl.x;
-            tot.y += sl.y;
-            tot.z += sl.z;
-            tot.w += sl.w;
+        for (int w0 = 0; w0 < p.ksw; w0 += kBatch) {
+            u32x4_t sl[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const int w = w0 + u;
+                sl[u] = __builtin_amdgcn_raw_buffer_load_b128(rsl, w < p.ksw ? (first + w * kSkinnySlot + e) * 4 : kOOB,
+                                                              0, kDeviceCoherent);
+            }
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const float4 v = __builtin_bit_cast(float4, sl[u]);
+                tot.x += v.x;
+                tot.y += v.y;
+                tot.z += v.z;
+                tot.w += v.w;
+            }
         }
         const float tv[4] = {tot.x, tot.y, tot.z, tot.w};
         const int nb0 = rt * kSkinnyRows + col;
