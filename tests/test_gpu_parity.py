@@ -230,10 +230,12 @@ GEMV_SHAPES = [workloads.Op("a", 3584, 1000), workloads.Op("b", 896, 77, 128, Fa
 def test_gemv_every_launch_config(gpu):
     """Every gemv_w4 configuration (where it fits) and the panel kernel at every lane
     split, M = 1..4, block sizes 32 and 128, with and without zero points, K not a
-    multiple of the step, N not a multiple of the workgroup's rows."""
+    multiple of the step, N not a multiple of the workgroup's rows. (The small-M
+    matrix-core path, which would take block size 128 at M = 4, is switched off.)"""
     count = gemv_config_count()
     assert count >= 8
     try:
+        native.set_tuning(4, 1)
         for cfg in list(range(1, count + 1)) + [-1]:
             native.set_tuning(1, cfg)
             for lanes in ([16, 32, 64] if cfg == -1 else [0]):
@@ -251,14 +253,17 @@ def test_gemv_every_launch_config(gpu):
                         w.close()
     finally:
         native.set_tuning(1, 0)
+        native.set_tuning(4, 0)
         native.set_gemv_lanes(0)
 
 
 @pytest.mark.parametrize("lanes", [16, 32, 64])
 def test_gemv_panel_every_lane_split(gpu, lanes):
-    """The panel kernel for M = 5..16 (its own range) at every lane split."""
+    """The panel kernel for M = 5..16 (its own range) at every lane split (the small-M
+    matrix-core path, which would take the block-size-128 shape, switched off)."""
     ops = [workloads.Op("a", 3584, 1000), workloads.Op("b", 896, 77, 128, False), workloads.Op("c", 4864, 96, 64)]
     try:
+        native.set_tuning(4, 1)
         native.set_gemv_lanes(lanes)
         for op in ops:
             for M in (5, 11, 16):
@@ -270,6 +275,7 @@ def test_gemv_panel_every_lane_split(gpu, lanes):
                                   f"lanes={lanes} M={M} {op}")
                 w.close()
     finally:
+        native.set_tuning(4, 0)
         native.set_gemv_lanes(0)
 
 
