@@ -141,10 +141,13 @@ int ms_hip_sync(void);
  *   4 1 keeps M <= 16 off the small-M matrix-core kernel, 2 sends every eligible
  *     M (1 and 2 included) to it;
  *   5 workgroups per row tile of the small-M matrix-core kernel (1..64, clamped to
- *     [ceil(K / 512), K / 128]).
+ *     [ceil(K / 512), K / 128]);
+ *   6 1 keeps M > 16 off the register-operand prefill kernel, 2 sends every eligible
+ *     M > 16 to it;
+ *   7 its K split (workgroups per 128 x 256 tile, 1..64, clamped to K / 128).
  * ms_hip_nbits_launch_info reports what a call with M rows would launch:
  *   kernel_id 0 generic, 1 gemv_w4, 2 mfma_w4, 3 gemv_w4_panel, 4 mfma_w4_pipe,
- *   5 skinny_w4. */
+ *   5 skinny_w4, 6 mfma_w4_rb. */
 /* ms_hip_nbits_batch_launch_info: what the first launch of a batch call with these
  * handles and activations would be: `calls` = how many of the leading calls it
  * serves, then as ms_hip_nbits_launch_info. */

@@ -1,0 +1,281 @@
+// mfma_w4_rb.h — INT4 MatMulNBits prefill GEMM with the weights dequantized straight
+// into MFMA operand registers (M > 16, block sizes 32..., K a multiple of 128).
+//
+// Y[M,N] = A[M,K] * W[N,K]^T, W = fl16((q - zp) * fl16(s)), A the fp16 copy made by
+// a_to_f16_kernel (each 8-k group in the order k0,k4,k1,k5,k2,k6,k3,k7, the order in
+// which one dword of packed codes dequantizes).
+//
+// A workgroup (4 waves) computes a 128 x 256 tile of Y over a range of 128-k blocks:
+//   * wave w owns weight rows n0 + 64 w .. + 63 (4 fragments of 16) and all 128 rows of
+//     A (8 fragments of 16): 32 v_mfma_f32_16x16x32_f16 per 32-k step, 128 fp32
+//     accumulators per lane in AGPRs (one wave per SIMD). Every dequantized weight feeds
+//     128 rows of A, so the dequant's VALU work (15 instructions per dword of 8 codes) is
+//     about half the MFMA time. (Two waves per SIMD at 64 x 64 each, which both
+//     dequantize the same rows, measured slower: their dequant alone matches the MFMA
+//     time.)
+//   * weights never touch LDS: lane (n = lane % 16, s = lane / 16) loads the 16-byte chunk
+//     s of its row's 64-byte block of codes (plus the chunk's scale and zero point) into a
+//     ring of registers three blocks deep, and dword j of the chunk becomes the B operand
+//     of step j (k = 32 s + 8 j + [0, 8));
+//   * A goes through LDS, double-buffered, one block (128 rows x 128 k, 32 KB) per buffer,
+//     laid out so that the A operand of (step j, fragment f) is 1 KB read by the 64 lanes
+//     in order (no bank conflicts). The next block's A is loaded into registers while the
+//     current block computes, written to the other buffer at the start of the next block;
+//     one barrier per block.
+//   * K split (ksw > 1, for launches with too few tiles to fill the CUs): workgroup kw of
+//     a tile writes its partial sums to slice kw of a [ksw][M][N] workspace with plain
+//     stores, and rb_reduce_kernel adds the slices in index order into Y afterwards
+//     (deterministic; the kernel boundary orders the two launches).
+// Rows past M and columns past N read zeros (out-of-range buffer offsets) and are not
+// stored.
+#pragma once
+#include "mfma_w4_pipe.h"
+
+namespace msnb {
+
+constexpr int kRbBM = 128, kRbBN = 256;
+constexpr int kRbRing = 3;                     // weight blocks in registers
+constexpr int kRbBufBytes = kRbBM * 128 * 2;   // one block of fp16 A
+
+struct RbParams {
+    const uint8_t* b;          // [N][row_bytes]
+    const float* scales;       // [N][nb]
+    const uint8_t* zp;         // [N][zrb] or nullptr (zp = 8)
+    const _Float16* a16;       // [M][K] fp16, permuted within 8-k groups
+    float* out;                // Y [M][N] (ksw 1) or the workspace: ksw slices of `slice` floats
+    int64_t slice;             // M * N rounded up to a multiple of 4 (16-byte aligned slices)
+    int row_bytes, M, N, K, nb, zrb, log2bs;
+    int tiles_m, tiles_n, ksw;
+};
+
+__global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
+{
+    constexpr int MF = kRbBM / 16, NF = 4;
+    __shared__ __attribute__((aligned(16))) uint8_t lds_a[2 * kRbBufBytes];
+
+    const int items = p.tiles_m * p.tiles_n * p.ksw;
+    // Consecutive items share (m tile, K range), so an XCD's range reuses its A in L2.
+    const int item = xcd_tile(blockIdx.x, items);
+    if (item >= items) return;
+    const int nt = item % p.tiles_n, rest = item / p.tiles_n;
+    const int kw = rest % p.ksw, mt = rest / p.ksw;
+    const int G = p.K >> 7;
+    const int g0 = (int)((int64_t)kw * G / p.ksw), cnt = (int)((int64_t)(kw + 1) * G / p.ksw) - g0;
+    const int m0 = mt * kRbBM, n0 = nt * kRbBN;
+
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int ln = lane & 15, ls = lane >> 4;
+
+    const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(p.a16, p.M * p.K * 2);
+    const __amdgpu_buffer_rsrc_t rb_ = buffer_rsrc(p.b, p.N * p.row_bytes);
+    const __amdgpu_buffer_rsrc_t rsc = buffer_rsrc(p.scales, p.N * p.nb * 4);
+    const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(p.zp ? (const void*)p.zp : (const void*)p.scales,
+                                                  p.zp ? p.N * p.zrb : 0);
+
+    // ---- A staging: thread t moves chunks q = t + 256 u (u = 0..7) of a block; chunk q is
+    // (step j = q >> 9, fragment f = (q >> 6) & 7, s = (q >> 4) & 3, row r = q & 15) and
+    // holds A[m0 + 16 f + r][128 g + 32 s + 8 j ...] (16 bytes). ----
+    int aoff[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int q = tid + 256 * u;
+        const int j = q >> 9, f = (q >> 6) & 7, s = (q >> 4) & 3, r = q & 15;
+        const int m = m0 + 16 * f + r;
+        aoff[u] = m < p.M ? (m * p.K + 32 * s + 8 * j) * 2 : kOOB;
+    }
+    u32x4_t areg[8];
+    auto load_a = [&](int i) {   // block g0 + i -> registers (zeros past the range)
+        const bool ok = i < cnt;
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            areg[u] = __builtin_amdgcn_raw_buffer_load_b128(ra, ok && aoff[u] != kOOB ? aoff[u] + (g0 + i) * 256 : kOOB, 0, 0);
+    };
+    auto store_a = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            *reinterpret_cast<u32x4_t*>(&lds_a[buf * kRbBufBytes + (tid + 256 * u) * 16]) = areg[u];
+    };
+
+    // ---- weights: lane (ln, ls) of fragment f is row n0 + 64 wave + 16 f + ln ----
+    int cb[NF], sb[NF], zb[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        const int n = n0 + 64 * wave + 16 * f + ln;
+        const bool in = n < p.N;
+        cb[f] = in ? n * p.row_bytes + ls * 16 : kOOB;
+        sb[f] = in ? n * p.nb * 4 : kOOB;
+        zb[f] = in ? n * p.zrb : kOOB;
+    }
+    struct WBlk {
+        u32x4_t c[NF];
+        float s[NF];
+        uint8_t z[NF];   // a byte, so the compiler cannot hoist a widening ahead of the block's wait
+    };
+    WBlk w[kRbRing];
+    auto load_w = [&](WBlk& wb, int i) {
+        const bool ok = i < cnt;
+        const int blk = ((g0 + i) * 128 + 32 * ls) >> p.log2bs;   // the quantization block of this chunk
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            const bool okf = ok && cb[f] != kOOB;
+            wb.c[f] = __builtin_amdgcn_raw_buffer_load_b128(rb_, okf ? cb[f] + (g0 + i) * 64 : kOOB, 0, 0);
+            wb.s[f] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc, okf ? sb[f] + blk * 4 : kOOB, 0, 0));
+            wb.z[f] = __builtin_amdgcn_raw_buffer_load_b8(rz, okf ? zb[f] + (blk >> 1) : kOOB, 0, 0);
+        }
+    };
+
+    floatx4_t acc[MF][NF];
+#pragma unroll
+    for (int f = 0; f < MF; ++f) {
+#pragma unroll
+        for (int e = 0; e < NF; ++e) acc[f][e] = floatx4_t{};
+    }
+    const uint32_t zdef = p.zp ? 0u : 8u;
+
+    // Per-block dequant constants of ring slot wb (block g0 + i): (1024 + zp) and fl16(s),
+    // both twice, per fragment.
+    auto prep = [&](const WBlk& wb, int i, uint32_t (&zz)[NF], h2_t (&s2)[NF]) {
+        const int blk = ((g0 + i) * 128 + 32 * ls) >> p.log2bs;
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            const uint32_t zp = (((uint32_t)wb.z[f] >> ((blk & 1) * 4)) & 0x0F) + zdef;
+            zz[f] = kHalfMagic | (zp << 16) | zp;
+            const _Float16 sh = (_Float16)wb.s[f];
+            s2[f] = h2_t{sh, sh};
+        }
+    };
+    // A operand of (step j, fragment mf): 1 KB, lane-ordered.
+    auto read_a1 = [&](int buf, int j, int mf) {
+        return *reinterpret_cast<const half8_t*>(&lds_a[buf * kRbBufBytes + ((j * MF + mf) * 64 + lane) * 16]);
+    };
+    // B operands of step j, fragment f only.
+    auto deq1 = [&](const WBlk& wb, int j, int f, uint32_t zzf, h2_t s2f) {
+        const uint32_t x = j == 0 ? wb.c[f].x : j == 1 ? wb.c[f].y : j == 2 ? wb.c[f].z : wb.c[f].w;
+        uint32_t o[4];
+        dequant8_f16(x, as_h2(zzf), s2f, o);
+        return __builtin_bit_cast(half8_t, u32x4_t{o[0], o[1], o[2], o[3]});
+    };
+
+    // ---- prologue, in the steady state's issue order: A(0) W(0) W(1) | A(1) W(2) ----
+    load_a(0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(w[0], 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(w[1], 1);
+    __builtin_amdgcn_sched_barrier(0);
+    store_a(0);
+    load_a(1);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(w[2], 2);
+    __builtin_amdgcn_sched_barrier(0);
+    half8_t bq0[NF];   // B operands of step 0 of the next block, prepared under the last step's MFMAs
+    {
+        uint32_t zz[NF];
+        h2_t s2[NF];
+        prep(w[0], 0, zz, s2);
+#pragma unroll
+        for (int f = 0; f < NF; ++f) bq0[f] = deq1(w[0], 0, f, zz[f], s2[f]);
+    }
+    __syncthreads();
+
+    // ---- main loop, unrolled by the ring depth so each ring slot is a register set ----
+    // Block i: (A(i+1) registers -> LDS; issue A(i+2)); 32 groups (step j, fragment mf) of
+    // 4 MFMAs; the A operand of group t + 2 is read under the MFMAs of group t (a 3-entry
+    // window), and the B operands of step j + 1 are dequantized one fragment per group
+    // under the first 4 groups of step j (the last step prepares step 0 of block i+1 from
+    // the next ring slot); then W(i+3) goes into the slot just used; barrier. At the top of
+    // block i the outstanding loads are A(i+1) then W(i+2), so the A store waits for A(i+1)
+    // alone.
+    auto body = [&](int i, WBlk& wb, const WBlk& wbn) {
+        const int buf = i & 1;
+        half8_t aw[3];
+        aw[0] = read_a1(buf, 0, 0);
+        aw[1] = read_a1(buf, 0, 1);
+        if (i + 1 < cnt) store_a((i + 1) & 1);
+        load_a(i + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        uint32_t zz[NF], zzn[NF];
+        h2_t s2[NF], s2n[NF];
+        prep(wb, i, zz, s2);
+        prep(wbn, i + 1, zzn, s2n);
+        half8_t bq[NF], bqn[NF];
+#pragma unroll
+        for (int f = 0; f < NF; ++f) bq[f] = bq0[f];
+#pragma unroll
+        for (int t = 0; t < 4 * MF; ++t) {
+            const int j = t / MF, mf = t % MF;
+            if (t + 2 < 4 * MF) aw[(t + 2) % 3] = read_a1(buf, (t + 2) / MF, (t + 2) % MF);
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+                acc[mf][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[t % 3], bq[f], acc[mf][f], 0, 0, 0);
+            if (mf < NF) bqn[mf] = j < 3 ? deq1(wb, j + 1, mf, zz[mf], s2[mf]) : deq1(wbn, 0, mf, zzn[mf], s2n[mf]);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (t + 2 < 4 * MF) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+#pragma unroll
+            for (int u = 0; u < 3; ++u) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+            }
+            if (mf == MF - 1) {
+#pragma unroll
+                for (int f = 0; f < NF; ++f) bq[f] = bqn[f];
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int f = 0; f < NF; ++f) bq0[f] = bq[f];
+        load_w(wb, i + kRbRing);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+    };
+    for (int i = 0; i < cnt; i += kRbRing) {
+        body(i, w[0], w[1]);
+        if (i + 1 >= cnt) break;
+        body(i + 1, w[1], w[2]);
+        if (i + 2 >= cnt) break;
+        body(i + 2, w[2], w[0]);
+    }
+
+    // ---- epilogue: acc[mf][f][v] is out[m0 + 16 mf + 4 ls + v][n0 + 64 wave + 16 f + ln] ----
+    float* const out = p.out + (p.ksw > 1 ? kw * p.slice : 0);
+    const __amdgpu_buffer_rsrc_t ro = buffer_rsrc(out, p.M * p.N * 4);
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        const int n = n0 + 64 * wave + 16 * f + ln;
+#pragma unroll
+        for (int mf = 0; mf < MF; ++mf) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int m = m0 + 16 * mf + 4 * ls + v;
+                const float x = acc[mf][f][v];   // a scalar first: a bit cast of a vector element reads element 0
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x), ro,
+                                                      m < p.M && n < p.N ? (m * p.N + n) * 4 : kOOB, 0, 0);
+            }
+        }
+    }
+}
+
+// y[e] = sum over kw of slice kw at e, in kw order, for e < n; the slices are
+// slice4 float4 groups apart (16-byte aligned), y only 4-byte aligned.
+__global__ __launch_bounds__(256) void rb_reduce_kernel(const float4* __restrict__ part, float* __restrict__ y,
+                                                        int64_t n, int64_t slice4, int ksw)
+{
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < slice4; i += (int64_t)gridDim.x * blockDim.x) {
+        float4 t = part[i];
+        for (int w = 1; w < ksw; ++w) {
+            const float4 v = part[(int64_t)w * slice4 + i];
+            t.x += v.x;
+            t.y += v.y;
+            t.z += v.z;
+            t.w += v.w;
+        }
+        const float tv[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            if (4 * i + c < n) y[4 * i + c] = tv[c];
+        }
+    }
+}
+
+}  // namespace msnb

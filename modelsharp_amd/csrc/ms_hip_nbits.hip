@@ -30,6 +30,7 @@
 #include "generic_nbits.h"
 #include "mfma_w4.h"
 #include "mfma_w4_pipe.h"
+#include "mfma_w4_rb.h"
 #include "skinny_w4.h"
 
 using namespace msnb;
@@ -119,7 +120,9 @@ struct Weights {
     int* d_sync = nullptr;      // split-K arrival counters and flags, zero between launches
     float* d_part = nullptr;    // split-K partial sums, kPipeBM x kPipeBN floats per tile
     int sync_tiles = 0;         // tiles covered by d_sync and d_part
-    // small-M matrix-core GEMV: A as hi/lo fp16 + block exponents, K-split slots, counters
+    float* d_rbpart = nullptr;  // mfma_w4_rb K-split partial sums [ksw][M][N]
+    size_t rbpart_bytes = 0;
+    // small-M matrix-core GEMV: K-split slots and counters
     uint8_t* d_sk = nullptr;    // skinny_w4 slots: [row tiles][workgroups per tile][16 x 128 floats]
     size_t sk_bytes = 0;
     int* d_sk_sync = nullptr;   // per row tile, zero between launches
@@ -183,6 +186,7 @@ void free_weights(Weights& w)
     if (w.d_a16) (void)hipFree(w.d_a16);
     if (w.d_sync) (void)hipFree(w.d_sync);
     if (w.d_part) (void)hipFree(w.d_part);
+    if (w.d_rbpart) (void)hipFree(w.d_rbpart);
     if (w.d_sk) (void)hipFree(w.d_sk);
     if (w.d_sk_sync) (void)hipFree(w.d_sk_sync);
     if (w.stream) (void)hipStreamDestroy(w.stream);
@@ -195,6 +199,8 @@ void free_weights(Weights& w)
     w.d_sync = nullptr;
     w.d_part = nullptr;
     w.sync_tiles = 0;
+    w.d_rbpart = nullptr;
+    w.rbpart_bytes = 0;
     w.d_sk = nullptr;
     w.sk_bytes = 0;
     w.d_sk_sync = nullptr;
@@ -222,7 +228,7 @@ __global__ __launch_bounds__(256) void scale_range_kernel(const float* __restric
 int check_pipe_scales(Weights& w)
 {
     w.pipe_scales_ok = 0;
-    if (!w.fast || w.log2cpb != 0) return MS_HIP_OK;
+    if (!w.fast) return MS_HIP_OK;
     unsigned* d = nullptr;
     MS_HIP_CHECK(hipMalloc(&d, 2 * sizeof(unsigned)));
     const unsigned init[2] = {0xFFFFFFFFu, 0u};
@@ -251,6 +257,8 @@ int g_pipe_off = 0;              // knob 2: 1 routes every prefill call to mfma_
 int g_pipe_ksplit = 0;           // knob 3: 1 or 2 forces the prefill K split (where K allows 2)
 int g_skinny = 0;                // knob 4: 1 keeps M <= 16 off skinny_w4, 2 sends every eligible M to it
 int g_skinny_ksw = 0;            // knob 5: workgroups per skinny_w4 row block (0: heuristic)
+int g_rb = 0;                    // knob 6: 1 keeps M > 16 off mfma_w4_rb, 2 sends every eligible M to it
+int g_rb_ksw = 0;                // knob 7: mfma_w4_rb K split (0: heuristic)
 
 // gemv_w4 instantiations: [M-1][L slot][config], L slot 0 = block size 32, 1 = block size 128.
 typedef void (*GemvFn)(GemvParams);
@@ -747,6 +755,127 @@ int launch_skinny(Weights& w, const float* dA, float* dY, int M, hipStream_t str
     return hipGetLastError() == hipSuccess ? 1 : -1;
 }
 
+// ---- mfma_w4_rb: prefill with the weights dequantized into MFMA operand registers ----
+// Any power-of-two block size >= 32, K a multiple of 128, fp16-safe scales (as the
+// pipelined kernel: W = fl16((q - zp) * fl16(s))), every buffer below the out-of-range
+// offset the kernel uses for padding rows.
+bool rb_eligible(const Weights& w, int M)
+{
+    return g_rb != 1 && w.fast && M > kPanelMaxM && (w.K % 128) == 0 && w.pipe_scales_ok &&
+           (int64_t)w.N * w.row_bytes < kOOB && (int64_t)M * w.K * 2 < kOOB && (int64_t)w.N * w.nb * 4 < kOOB &&
+           (int64_t)M * w.N * 4 < kOOB;
+}
+
+// K split: the number of workgroups per 128 x 256 tile. A split runs in rounds of one
+// workgroup per CU and pays a reduce pass over ksw + 1 copies of Y (written and read),
+// so the pick minimises rounds x (blocks per workgroup) x t_block + reduce bytes / HBM
+// rate, with t_block the measured time of one 128-k block of a workgroup (about 3.5 us:
+// K=11008 unsplit at M=2048 takes 301 us for 86 blocks). On the 7B MLP shapes this
+// picks the fastest measured split (M=128: 4 and 16; M=512, K=11008: 4).
+int rb_ksw(const Weights& w, int M)
+{
+    const int G = w.K / 128;
+    const int64_t tiles = (int64_t)((M + kRbBM - 1) / kRbBM) * ((w.N + kRbBN - 1) / kRbBN);
+    if (g_rb_ksw > 0) return std::max(1, std::min(g_rb_ksw, G));
+    const int cus = device_cus();
+    const double t_block = 3.5e-6, hbm = 4.0e12, t_launch = 2e-6;
+    const double ybytes = (double)M * w.N * 4;
+    int pick = 1;
+    double best = 1e30;
+    for (int k = 1; k <= std::min(G, 32); ++k) {
+        const double rounds = (double)((tiles * k + cus - 1) / cus);
+        const double t = rounds * std::ceil((double)G / k) * t_block + (k > 1 ? (2.0 * k + 1) * ybytes / hbm + t_launch : 0.0);
+        if (t < best * 0.97) {
+            best = t;
+            pick = k;
+        }
+    }
+    return pick;
+}
+
+// Which prefill kernel: mfma_w4_rb where the pipelined kernel does not apply (block
+// sizes other than 32), and where the pipelined launch would fill less than half of the
+// CUs: measured on the 7B MLP shapes, 128 x 256 tiles with a wide K split beat it there
+// (M=128: 49 / 45 us against 78 / 143 us; M=512, K=11008: 103 against 154 us), while
+// with more tiles the pipelined kernel is faster (M=512, K=4096: 100 against 118 us;
+// M=2048: 262 against 320-355 us).
+bool use_rb(const Weights& w, int M)
+{
+    if (!rb_eligible(w, M)) return false;
+    if (g_rb == 2 || !pipe_eligible(w, M)) return true;
+    const int64_t items = (int64_t)((M + kPipeBM - 1) / kPipeBM) * ((w.N + kPipeBN - 1) / kPipeBN) * pipe_ksplit(w, M);
+    return 2 * items < device_cus();
+}
+
+// Returns 1 when launched, 0 when the caller should take another kernel (the workspace
+// would have to grow under capture), negative on a launch error.
+int launch_rb(Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
+{
+    const int tiles_m = (M + kRbBM - 1) / kRbBM, tiles_n = (w.N + kRbBN - 1) / kRbBN;
+    const int ksw = rb_ksw(w, M);
+    const size_t need_a = (size_t)M * w.K * 2;
+    const int64_t slice = ((int64_t)M * w.N + 3) / 4 * 4;   // floats per K-split slice, 16-byte multiple
+    const size_t need_p = ksw > 1 ? (size_t)ksw * slice * sizeof(float) : 0;
+    uint32_t* ws = nullptr;
+    float* part = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(w.ws_mu);
+        const bool grow_a = w.a16_bytes < need_a, grow_p = w.rbpart_bytes < need_p;
+        if (grow_a || grow_p) {
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+                (void)hipGetLastError();
+                return 0;
+            }
+            if (hipStreamSynchronize(stream) != hipSuccess) return -1;
+        }
+        if (grow_a) {
+            if (w.d_a16 && hipFree(w.d_a16) != hipSuccess) return -1;
+            w.d_a16 = nullptr;
+            w.a16_bytes = 0;
+            if (hipMalloc(&w.d_a16, need_a) != hipSuccess) return -1;
+            w.a16_bytes = need_a;
+        }
+        if (grow_p) {
+            if (w.d_rbpart && hipFree(w.d_rbpart) != hipSuccess) return -1;
+            w.d_rbpart = nullptr;
+            w.rbpart_bytes = 0;
+            if (hipMalloc(&w.d_rbpart, need_p) != hipSuccess) return -1;
+            w.rbpart_bytes = need_p;
+        }
+        ws = w.d_a16;
+        part = w.d_rbpart;
+    }
+    const int64_t n8 = (int64_t)M * w.K / 8;
+    hipLaunchKernelGGL(a_to_f16_kernel, dim3((unsigned)std::min<int64_t>((n8 + 255) / 256, 4096)), dim3(256), 0,
+                       stream, dA, ws, n8);
+    RbParams p;
+    p.b = w.d_b;
+    p.scales = w.d_scales;
+    p.zp = w.has_zp ? w.d_zp : nullptr;
+    p.a16 = reinterpret_cast<const _Float16*>(ws);
+    p.out = ksw > 1 ? part : dY;
+    p.slice = slice;
+    p.row_bytes = (int)w.row_bytes;
+    p.M = M;
+    p.N = w.N;
+    p.K = w.K;
+    p.nb = w.nb;
+    p.zrb = w.zrb;
+    p.log2bs = w.log2cpb + 5;
+    p.tiles_m = tiles_m;
+    p.tiles_n = tiles_n;
+    p.ksw = ksw;
+    const int items = tiles_m * tiles_n * ksw;
+    hipLaunchKernelGGL(mfma_w4_rb_kernel, dim3(((items + kXcds - 1) / kXcds) * kXcds), dim3(256), 0, stream, p);
+    if (ksw > 1) {
+        const int64_t slice4 = slice / 4;
+        hipLaunchKernelGGL(rb_reduce_kernel, dim3((unsigned)std::min<int64_t>((slice4 + 255) / 256, 8192)), dim3(256),
+                           0, stream, reinterpret_cast<const float4*>(part), dY, (int64_t)M * w.N, slice4, ksw);
+    }
+    return hipGetLastError() == hipSuccess ? 1 : -1;
+}
+
 int enqueue_gemm(Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
 {
     if (M < 0) return fail(MS_HIP_ERR_INVALID, "MatMulNBits M must be non-negative; got %d.", M);
@@ -762,6 +891,11 @@ int enqueue_gemm(Weights& w, const float* dA, float* dY, int M, hipStream_t stre
             if (r > 0) return MS_HIP_OK;
         }
         return launch_gemv(w, dA, dY, M, stream);
+    }
+    if (use_rb(w, M)) {
+        const int r = launch_rb(w, dA, dY, M, stream);
+        if (r < 0) return fail(MS_HIP_ERR_HIP, "[ms_hip] prefill launch failed: %s", hipGetErrorString(hipGetLastError()));
+        if (r > 0) return MS_HIP_OK;
     }
     if (pipe_eligible(w, M)) {
         const int r = launch_pipe(w, dA, dY, M, stream);
@@ -1150,6 +1284,14 @@ int ms_hip_set_tuning(int knob, int value)
             if (value < 0 || value > 64) break;
             g_skinny_ksw = value;
             return MS_HIP_OK;
+        case 6:
+            if (value < 0 || value > 2) break;
+            g_rb = value;
+            return MS_HIP_OK;
+        case 7:
+            if (value < 0 || value > 64) break;
+            g_rb_ksw = value;
+            return MS_HIP_OK;
         default: break;
     }
     return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid tuning knob %d = %d", knob, value);
@@ -1185,6 +1327,11 @@ int ms_hip_nbits_launch_info(void* handle, int M, int* kernel_id, int* lanes_per
             gr = s.grid;
             bl = kPanelThreads;
         }
+    } else if (use_rb(*w, M)) {
+        kid = 6;
+        gr = ((M + kRbBM - 1) / kRbBM) * ((w->N + kRbBN - 1) / kRbBN) * rb_ksw(*w, M);
+        gr = ((gr + kXcds - 1) / kXcds) * kXcds;
+        bl = 256;
     } else if (pipe_eligible(*w, M)) {
         kid = 4;
         const int items = ((M + kPipeBM - 1) / kPipeBM) * ((w->N + kPipeBN - 1) / kPipeBN) * pipe_ksplit(*w, M);

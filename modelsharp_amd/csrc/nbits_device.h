@@ -135,6 +135,7 @@ __device__ __forceinline__ float dot8(const uint32_t (&d)[4], const float4& a0, 
 
 // ---- shared by the GEMV kernels ---------------------------------------------------
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
 // A staged activation chunk in LDS: 32 activations pre-scaled (even k by 2^24, odd
 // k by 2^20) in 8 float4, then (sum of the 32 unscaled activations, 0, 0, 0). The
 // ninth float4 also pads the chunk stride off a power of two (fewer bank conflicts).

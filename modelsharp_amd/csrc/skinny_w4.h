@@ -38,8 +38,6 @@
 
 namespace msnb {
 
-typedef float floatx4_t __attribute__((ext_vector_type(4)));
-
 constexpr int kSkinnyMT = 16;                            // MFMA rows: M padded to 16
 constexpr int kSkinnyNF = 2;                             // 16-row MFMA fragments per wave
 constexpr int kSkinnyRows = 4 * 16 * kSkinnyNF;          // weight rows per workgroup

@@ -301,7 +301,7 @@ def test_edge_shapes(gpu, op, M):
     ref = oracle.matmul_nbits(a, b, s, z, op.N, op.K, op.bits, op.block_size)
     y = w.gemm(a)
     W = oracle.dequant_weights(b, s, z, op.N, op.K, op.bits, op.block_size)
-    if w.launch_info(M)["kernel"] in ("mfma_w4", "mfma_w4_pipe"):
+    if w.launch_info(M)["kernel"] in ("mfma_w4", "mfma_w4_pipe", "mfma_w4_rb"):
         assert_fro_close(y, ref, f"{op.name} M={M}")
     else:
         assert_gemv_close(y, ref, f"{op.name} M={M}", cond=fp32_dot_bound(a, W))
@@ -320,10 +320,12 @@ def test_m_zero_is_a_no_op(gpu):
 @pytest.mark.parametrize("op", workloads.LLAMA7B_PREFILL_OPS, ids=lambda o: f"K{o.K}_N{o.N}")
 @pytest.mark.parametrize("M", workloads.LLAMA7B_PREFILL_M)
 def test_mfma_parity_sampled_columns(gpu, op, M):
-    """Full-size call; the oracle checks a seeded sample of 96 output columns."""
+    """Full-size call with the library's own kernel choice (mfma_w4_rb where the pipelined
+    kernel's tiles would fill less than half of the CUs); the oracle checks a seeded
+    sample of 96 output columns."""
     b, s, z, w = weights_for(op, seed=M + op.N)
     a = workloads.make_activations(M, op.K, seed=M, kind="rmsnorm")
-    assert w.launch_info(M)["kernel"] == "mfma_w4_pipe"
+    assert w.launch_info(M)["kernel"] == ("mfma_w4_pipe" if M >= 512 and (M > 512 or op.N > 4096) else "mfma_w4_rb")
     log(f"mfma M={M} K={op.K} N={op.N}")
     y = w.gemm(a)
     cols = np.sort(np.random.default_rng(M).choice(op.N, 96, replace=False))
@@ -344,12 +346,14 @@ def pipe_items(M, N, ksplit):
 def test_mfma_partial_tiles(gpu, M):
     """Both prefill kernels, and the pipelined one with and without the K split, on
     tiles cut by M and N (N=333 is not a multiple of 256; K=896 is 7 groups of 4
-    steps, so the two K halves are unequal: 3 and 4 groups)."""
+    steps, so the two K halves are unequal: 3 and 4 groups). mfma_w4_rb, which these
+    small launches would take, is switched off."""
     op = workloads.Op("pt", 896, 333, 32, True)
     b, s, z, w = weights_for(op, seed=M)
     a = workloads.make_activations(M, op.K, seed=M, kind="rmsnorm")
     ref = oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, 32)
     try:
+        native.set_tuning(6, 1)
         for ks in (1, 2):
             native.set_tuning(3, ks)
             info = w.launch_info(M)
@@ -363,35 +367,93 @@ def test_mfma_partial_tiles(gpu, M):
     finally:
         native.set_tuning(2, 0)
         native.set_tuning(3, 0)
+        native.set_tuning(6, 0)
     w.close()
 
 
 def test_prefill_split_k_deterministic(gpu):
-    """The K-split prefill (two workgroups per tile, combined by arrival order) gives
-    bit-identical results on every call, and matches the unsplit launch to the bar."""
+    """The pipelined prefill's K split (two workgroups per tile, combined by arrival
+    order) gives bit-identical results on every call, and matches the unsplit launch to
+    the bar (mfma_w4_rb, which this launch would take, switched off)."""
     op = workloads.Op("sk", 4096, 1000, 32, True)
     b, s, z, w = weights_for(op, seed=21)
     a = workloads.make_activations(300, op.K, seed=22, kind="rmsnorm")
     ref = oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, 32)
-    assert w.launch_info(300)["grid"] == pipe_items(300, op.N, 2)   # 8 tiles: split by default
-    y0 = w.gemm(a)
-    assert_fro_close(y0, ref, "split")
-    for i in range(4):
-        assert np.array_equal(w.gemm(a), y0), i
     try:
+        native.set_tuning(6, 1)
+        assert w.launch_info(300)["grid"] == pipe_items(300, op.N, 2)   # 8 tiles: split by default
+        y0 = w.gemm(a)
+        assert_fro_close(y0, ref, "split")
+        for i in range(4):
+            assert np.array_equal(w.gemm(a), y0), i
         native.set_tuning(3, 1)
         y1 = w.gemm(a)
     finally:
         native.set_tuning(3, 0)
+        native.set_tuning(6, 0)
     assert_fro_close(y1, ref, "unsplit")
     assert_fro_close(y0, y1, "split vs unsplit")
     w.close()
 
 
+# ---- prefill with the weights dequantized into MFMA operand registers (mfma_w4_rb) -------------
+RB_SHAPES = [workloads.Op("rb32", 896, 333, 32, True),      # 7 blocks of 128 k; N not a multiple of 256
+             workloads.Op("rb64", 640, 200, 64, True),      # 2 chunks per quantization block
+             workloads.Op("rb128", 1024, 300, 128, False)]  # 4 chunks per block, no zero points
+
+
+@pytest.mark.parametrize("op", RB_SHAPES, ids=lambda o: o.name)
+@pytest.mark.parametrize("M", [17, 100, 129, 300])
+def test_rb_partial_tiles_and_splits(gpu, op, M):
+    """mfma_w4_rb on tiles cut by M and N, block sizes 32/64/128, with and without zero
+    points, unsplit and with K split 2, 3 and 7 ways (unequal ranges, reduce launch)."""
+    b, s, z, w = weights_for(op, seed=M + op.K)
+    a = workloads.make_activations(M, op.K, seed=M, kind="rmsnorm")
+    ref = oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, op.block_size)
+    G = op.K // 128
+    try:
+        native.set_tuning(6, 2)
+        for ks in sorted({1, 2, 3, G}):
+            native.set_tuning(7, ks)
+            info = w.launch_info(M)
+            items = -(-M // 128) * -(-op.N // 256) * min(ks, G)
+            assert info["kernel"] == "mfma_w4_rb" and info["grid"] == -(-items // 8) * 8, info
+            log(f"rb {op.name} M={M} ksw={ks} {info}")
+            y = w.gemm(a)
+            assert_fro_close(y, ref, f"rb {op.name} M={M} ksw={ks}")
+            assert np.array_equal(w.gemm(a), y), ks
+    finally:
+        native.set_tuning(6, 0)
+        native.set_tuning(7, 0)
+    w.close()
+
+
+@pytest.mark.parametrize("op", workloads.LLAMA7B_PREFILL_OPS, ids=lambda o: f"K{o.K}_N{o.N}")
+@pytest.mark.parametrize("M", workloads.LLAMA7B_PREFILL_M)
+def test_rb_parity_sampled_columns(gpu, op, M):
+    """mfma_w4_rb at the full prefill sizes (its own K split); the oracle checks 96 columns."""
+    b, s, z, w = weights_for(op, seed=M + op.N)
+    a = workloads.make_activations(M, op.K, seed=M, kind="rmsnorm")
+    try:
+        native.set_tuning(6, 2)
+        info = w.launch_info(M)
+        assert info["kernel"] == "mfma_w4_rb", info
+        log(f"rb M={M} K={op.K} N={op.N} {info}")
+        y = w.gemm(a)
+    finally:
+        native.set_tuning(6, 0)
+    cols = np.sort(np.random.default_rng(M).choice(op.N, 96, replace=False))
+    zc = None if z is None else z[cols]
+    ref = oracle.matmul_nbits(a, b[cols], s.reshape(op.N, -1)[cols], zc, len(cols), op.K, 4, op.block_size)
+    assert_fro_close(y[:, cols], ref, f"rb M={M} sampled")
+    assert np.all(np.isfinite(y))
+    w.close()
+
+
 @pytest.mark.parametrize("op,kernel", [
-    (workloads.Op("bs128", 1024, 300, 128, False), "mfma_w4"),    # block size 128
-    (workloads.Op("k96", 96, 200, 32, True), "mfma_w4"),          # K not a multiple of 128
-    (workloads.Op("k640", 640, 260, 32, False), "mfma_w4_pipe"),  # no zero points
+    (workloads.Op("bs128", 1024, 300, 128, False), "mfma_w4_rb"),  # block size 128
+    (workloads.Op("k96", 96, 200, 32, True), "mfma_w4"),           # K not a multiple of 128
+    (workloads.Op("k640", 640, 260, 32, False), "mfma_w4_rb"),     # no zero points, few tiles
 ], ids=lambda v: v.name if hasattr(v, "name") else v)
 def test_prefill_kernel_choice(gpu, op, kernel):
     b, s, z, w = weights_for(op, seed=op.K)
@@ -425,24 +487,52 @@ def test_prefill_captured_before_eager_call(gpu):
     ref = oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, 32)
     dA = torch.from_numpy(a).cuda()
     dY = torch.zeros((96, op.N), dtype=torch.float32, device="cuda")
+    native.set_tuning(6, 1)   # the pipelined kernel (this small launch would take mfma_w4_rb)
+    try:
+        _captured_before_and_after_eager(w, a, ref, dA, dY, split_grid=pipe_items(96, op.N, 2))
+    finally:
+        native.set_tuning(6, 0)
+    w.close()
+
+
+def test_rb_captured_before_and_after_eager_call(gpu):
+    """mfma_w4_rb under capture: before any eager call (no workspace) the call takes the
+    workspace-free kernel; afterwards the graph holds the conversion, the K-split kernel
+    and the reduce launch, and every replay equals the eager call bit for bit."""
+    import torch
+    op = workloads.Op("capr", 1024, 512, 32, True)
+    b, s, z, w = weights_for(op, seed=8)
+    a = workloads.make_activations(96, op.K, seed=9, kind="rmsnorm")
+    ref = oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, 32)
+    dA = torch.from_numpy(a).cuda()
+    dY = torch.zeros((96, op.N), dtype=torch.float32, device="cuda")
+    info = w.launch_info(96)
+    assert info["kernel"] == "mfma_w4_rb" and info["grid"] > 8, info    # split K
+    _captured_before_and_after_eager(w, a, ref, dA, dY, split_grid=info["grid"])
+    w.close()
+
+
+def _captured_before_and_after_eager(w, a, ref, dA, dY, split_grid):
+    import torch
+    M = a.shape[0]
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        w.gemm_dev(dA.data_ptr(), dY.data_ptr(), 96, torch.cuda.current_stream().cuda_stream)
+        w.gemm_dev(dA.data_ptr(), dY.data_ptr(), M, torch.cuda.current_stream().cuda_stream)
     for i in range(3):
         dY.fill_(float("nan"))
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
         assert_fro_close(dY.cpu().numpy(), ref, f"replay {i}")
-    eager = w.gemm(a)           # grows the workspace, takes the pipelined kernel
+    eager = w.gemm(a)           # grows the workspace
     assert_fro_close(eager, ref, "eager")
-    # Captured again now that the workspace exists: the pipelined kernel with its
-    # K split (4 tiles) runs in the graph; its arrival counters reset themselves,
-    # so every replay equals the eager call bit for bit.
-    assert w.launch_info(96)["grid"] == pipe_items(96, op.N, 2)
+    # Captured again now that the workspace exists: the K-split kernel runs in the graph
+    # (no memset recorded; counters or slices are rewritten every launch), so every
+    # replay equals the eager call bit for bit.
+    assert w.launch_info(M)["grid"] == split_grid
     g2 = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g2):
-        w.gemm_dev(dA.data_ptr(), dY.data_ptr(), 96, torch.cuda.current_stream().cuda_stream)
+        w.gemm_dev(dA.data_ptr(), dY.data_ptr(), M, torch.cuda.current_stream().cuda_stream)
     for i in range(3):
         dY.fill_(float("nan"))
         torch.cuda.synchronize()
@@ -450,7 +540,7 @@ def test_prefill_captured_before_eager_call(gpu):
         torch.cuda.synchronize()
         assert np.array_equal(dY.cpu().numpy(), eager), f"split replay {i}"
         assert np.array_equal(w.gemm(a), eager), f"eager after replay {i}"
-    w.close()
+
 
 
 def test_mfma_full_vs_torch_fp32(gpu):
