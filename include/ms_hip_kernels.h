@@ -83,7 +83,7 @@ int ms_hip_nbits_weights_info(void* handle, int* N, int* K, int* bits, int* bloc
  * path NativeQuant.TryMatMulNBits (NativeQuant.cs:78-115) takes from
  * MatMulNBitsKernel.Execute (MatMulNBitsKernel.cs:174-191), with the weights
  * already resident. M<=16 runs the dequant-fused GEMV (block size 128 and
- * 4 <= M <= 16: its matrix-core form at the same accuracy), larger M the MFMA GEMM. */
+ * 3 <= M <= 16: its matrix-core form at the same accuracy), larger M the MFMA GEMM. */
 int ms_hip_nbits_gemm(void* handle, const float* a_host, float* y_host, int M);
 
 /* Device-pointer form: enqueues on `stream` (a hipStream_t, NULL = the null

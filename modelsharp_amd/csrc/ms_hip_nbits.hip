@@ -670,9 +670,10 @@ int launch_pipe(Weights& w, const float* dA, float* dY, int M, hipStream_t strea
 // ---- skinny_w4: M <= 16 on the matrix cores at fp32-level accuracy (block size 128) ----
 
 // The small-M matrix-core path takes block size 128 (a block is one group of four MFMA
-// steps), K a multiple of 128, and 4 <= M <= 16: at M <= 2 gemv_w4 is faster (measured
-// on the 7B MLP shapes), unless knob 4 says otherwise.
-constexpr int kSkinnyMinM = 4;
+// steps), K a multiple of 128, and 3 <= M <= 16: at M <= 2 gemv_w4 is faster (measured
+// on the 7B MLP shapes: M=2 13.2 / 12.5 us against 15.4 / 16.7 us; M=3 20.4 / 24.2 us
+// against 15.8 / 17.3 us), unless knob 4 says otherwise.
+constexpr int kSkinnyMinM = 3;
 bool skinny_eligible(const Weights& w, int M)
 {
     if (g_skinny == 1 || !w.fast || w.log2cpb != 2 || (w.K % 128) != 0 || M < 1 || M > kSkinnyMT) return false;
