@@ -323,9 +323,27 @@ def main() -> int:
             del prot, gp
             torch.cuda.empty_cache()
         tf = total_flops / (total_ms * 1e-3) / 1e12
+        # The other prefill sizes of the workload (reported, not aggregated): each op with
+        # the kernel the library picks for it.
+        smaller = {}
+        for M in (128, 512):
+            for op in workloads.LLAMA7B_PREFILL_OPS:
+                prot = Rotation([op], M, 2, seed=11, kind="rmsnorm")
+                gp = graph_of(lambda stream: [prot.enqueue(r, stream) for r in range(2)])
+                ms = time_graph(gp, 10, 2) / 2
+                fl = workloads.flops(op, M)
+                smaller[f"M{M}_K{op.K}_N{op.N}"] = {
+                    "us": round(ms * 1e3, 2), "TFLOPs": round(fl / (ms * 1e-3) / 1e12, 1),
+                    "frac_fp16_peak": round(fl / (ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4),
+                    "kernel": prot.handles[0][0].launch_info(M)["kernel"]}
+                log(f"  prefill M={M} K={op.K} N={op.N}: {ms * 1e3:.1f} us ({smaller[f'M{M}_K{op.K}_N{op.N}']['kernel']})")
+                prot.close()
+                del prot, gp
+                torch.cuda.empty_cache()
         result["prefill"] = {"workload": "llama7b_prefill M=2048, (K,N)=(4096,11008),(11008,4096), bs=32, zp",
                              "per_op": pre, "TFLOPs": round(tf, 1), "peak_TFLOPs": FP16_PEAK_TFLOPS,
-                             "frac": round(tf / FP16_PEAK_TFLOPS, 4), "bound": "mfma"}
+                             "frac": round(tf / FP16_PEAK_TFLOPS, 4), "bound": "mfma",
+                             "smaller_m": smaller}
 
     if args.detail:
         result_detail = detail_workloads(args)

@@ -38,7 +38,7 @@
 //       b % 8; each XCD walks an m-major range of tiles, sharing A panels in L2).
 //     * Split K (ksplit = 2, for launches with too few tiles to fill the CUs): the
 //       two halves of a tile (whole groups of 4 steps each) are neighbouring work
-//       items; the first to finish stores its partial sums into Y and raises a
+//       items; the first to finish writes its partial sums through to Y and raises a
 //       flag, the second stores its own into a workspace slot and then adds the
 //       slot into Y (deterministic: fp32 a + b == b + a).
 // Numerics: A rounded once to fp16; W = fl16((q - zp) * fl16(s)); products exact,
@@ -321,7 +321,7 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
     // valid rows/columns (every destination is smaller than 2^30 bytes, checked by the
     // host): such stores are dropped, so the epilogue has no branches. The destination
     // is runtime data: the tile (rb, cb) of an ld-wide matrix with rl x cl valid entries.
-    auto store_tile = [&](__amdgpu_buffer_rsrc_t rd, int ld, int rb, int cb, int rl, int cl) {
+    auto store_tile = [&](__amdgpu_buffer_rsrc_t rd, int ld, int rb, int cb, int rl, int cl, auto cpol) {
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
             const int row0 = wm * 128 + 32 * i + 4 * lh;
@@ -336,15 +336,17 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
                     const uint32_t outside = (uint32_t)(((rl - 1 - row0 - rv) | cfree) >> 31);   // all ones outside
                     const int off = (int)((base + (uint32_t)(rv * 4) * (uint32_t)ld) | (outside & (uint32_t)kPipeFar));
                     const float x = acc[i][j][v];   // bit_cast of a vector element would read element 0
-                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x), rd, off, 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x), rd, off, 0, decltype(cpol)::value);
                 }
             }
         }
     };
     const __amdgpu_buffer_rsrc_t ry = buffer_rsrc(p.y, p.M * p.N * 4);
     const int rl = p.M - m0, cl = p.N - n0;   // valid rows / columns of this tile
+    using plain_store = std::integral_constant<int, 0>;
+    using coherent_store = std::integral_constant<int, kDeviceCoherent>;
     if (p.ksplit == 1) {
-        store_tile(ry, p.N, m0, n0, rl, cl);
+        store_tile(ry, p.N, m0, n0, rl, cl, plain_store{});
         return;
     }
     // Two halves: the first to arrive stores its partial sums into Y, the second into
@@ -352,7 +354,11 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
     // flag the second adds the slot into Y. Y = p0 + p1 either way (fp32 addition
     // commutes), so the result does not depend on the arrival order. The second waits
     // only for a workgroup that has already arrived (and is therefore running), so the
-    // wait ends.
+    // wait ends. The hand-off uses no agent-scope fence (on gfx950 those write back or
+    // invalidate the XCD's whole L2, and an acquiring spin would invalidate it on every
+    // poll): the first half writes Y through to device scope (sc1) and raises the flag
+    // only after those stores have completed; the second polls the flag and reads Y with
+    // device-coherent loads.
     __shared__ int arrival;
     int* const cnt = p.sync + 2 * tile;
     if (threadIdx.x == 0) arrival = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -361,19 +367,19 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
     float* const slot = p.part + (int64_t)tile * (BM * BN);
     const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(slot, BM * BN * 4);
     if (!second) {
-        store_tile(ry, p.N, m0, n0, rl, cl);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        store_tile(ry, p.N, m0, n0, rl, cl, coherent_store{});
+        wait_vmem_order_only_release();
         __syncthreads();
-        if (threadIdx.x == 0) __hip_atomic_store(cnt + 1, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0) __hip_atomic_store(cnt + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
-    store_tile(rs, BN, 0, 0, rl, cl);
+    store_tile(rs, BN, 0, 0, rl, cl, plain_store{});
     if (threadIdx.x == 0) {
         // Bounded: the first half is running and needs no other workgroup to finish, so
         // the flag comes within microseconds; the bound only keeps a misuse (two launches
         // on one handle overlapping) from hanging the device.
         for (int spin = 0; spin < (1 << 22); ++spin) {
-            if (__hip_atomic_load(cnt + 1, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
+            if (__hip_atomic_load(cnt + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
             __builtin_amdgcn_s_sleep(2);
         }
         // Both halves are past their use of the pair: leave it zero for the next launch.
@@ -381,7 +387,7 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
         __hip_atomic_store(cnt + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();   // also orders this workgroup's slot stores before its slot loads
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    wait_vmem_order_only_acquire();
     // Y[m0 + r][n0 + c] += slot[r][c]: thread t takes columns c = t, one row per pass.
     const int c = threadIdx.x;
     const uint32_t cfar = (uint32_t)((cl - 1 - c) >> 31) & (uint32_t)kPipeFar;
@@ -395,7 +401,7 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
             yo[u] = (int)((((uint32_t)(m0 + r) * (uint32_t)p.N + (uint32_t)(n0 + c)) * 4u) | far);
             sv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                                   rs, (int)(((uint32_t)(r * BN + c) * 4u) | far), 0, 0));
-            yv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ry, yo[u], 0, 0));
+            yv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ry, yo[u], 0, kDeviceCoherent));
         }
 #pragma unroll
         for (int u = 0; u < 16; ++u)

@@ -153,6 +153,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, (int)kBufferWord3);
 }
 
+// Buffer cache policy sc1 (device scope): stores write through to where every XCD
+// reads, loads do not return another XCD's stale copy.
+constexpr int kDeviceCoherent = 16;
+
 // Cross-workgroup hand-off through data written and read with agent-scope atomic
 // stores / loads (those write and read through the caches, so the data needs no L2
 // write-back or invalidate). These two only order: the release form waits until every

@@ -45,9 +45,6 @@ constexpr int kSkinnyNB = 4;                             // blocks per workgroup
 constexpr int kSkinnyStepBytes = 1024;                   // one MFMA step's activations (hi or lo)
 constexpr int kSkinnyBlockBytes = 4 * 2 * kSkinnyStepBytes;   // one block: 4 steps x (hi, lo)
 constexpr int kSkinnySlot = kSkinnyMT * kSkinnyRows;     // floats per workgroup slot
-// Buffer cache policy sc1 (device scope): stores write through to where every XCD
-// reads, loads do not return another XCD's stale copy.
-constexpr int kDeviceCoherent = 16;
 
 struct SkinnyParams {
     const uint8_t* b;          // [N][row_bytes]
