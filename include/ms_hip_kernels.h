@@ -137,7 +137,8 @@ int ms_hip_sync(void);
  *   1 gemv_w4 launch configuration: c+1 forces configuration c of the library's
  *     table (used only where it fits the shape), -1 forces gemv_w4_panel;
  *   2 1 routes every M > 16 call to mfma_w4 (the pipelined prefill off);
- *   3 1 or 2 forces the pipelined prefill's K split (2 needs K >= 256);
+ *   3 the pipelined prefill's K split: 1 no tile split, 2 every tile split in two,
+ *     3 the second half of the tiles split (needs K >= 256);
  *   4 1 keeps M <= 16 off the small-M matrix-core kernel, 2 sends every eligible
  *     M (1 and 2 included) to it;
  *   5 workgroups per row tile of the small-M matrix-core kernel (1..64, clamped to

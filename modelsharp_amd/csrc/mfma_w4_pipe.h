@@ -36,11 +36,12 @@
 //       the shadow of one 32-cycle MFMA.
 //     * One barrier per step. Tile order is XCD-aware (workgroup b runs on XCD
 //       b % 8; each XCD walks an m-major range of tiles, sharing A panels in L2).
-//     * Split K (ksplit = 2, for launches with too few tiles to fill the CUs): the
-//       two halves of a tile (whole groups of 4 steps each) are neighbouring work
-//       items; the first to finish writes its partial sums through to Y and raises a
-//       flag, the second stores its own into a workspace slot and then adds the
-//       slot into Y (deterministic: fp32 a + b == b + a).
+//     * Split K (for launches with too few tiles to fill the CUs, or for the tiles of
+//       a last, partly filled round): the two halves of a split tile (whole groups
+//       of 4 steps each) are neighbouring work items; the first to finish writes its
+//       partial sums through to Y and raises a flag, the second stores its own into a
+//       workspace slot and then adds the slot into Y (deterministic: fp32 a + b ==
+//       b + a).
 // Numerics: A rounded once to fp16; W = fl16((q - zp) * fl16(s)); products exact,
 // sums fp32. Requires |A| < 65504 (fp16 range) and fp16-normal scales for the
 // 2^-11 relative bound; the library routes other inputs to mfma_w4.
@@ -58,9 +59,12 @@ struct PipeParams {
     float* y;                // [M][N]
     int row_bytes, M, N, K, C, nb, zrb;
     int tiles_m, tiles_n;
-    int ksplit;              // 1, or 2: each tile's K range is split over two workgroups
-    int* sync;               // ksplit 2: [tiles][2] arrival counter and ready flag, all zero
-    float* part;             // ksplit 2: [tiles][kPipeBM * kPipeBN] partial sums
+    // Tiles [0, full) run whole; each tile from `full` on has its K range split over two
+    // workgroups. Workgroup b runs on XCD x = b % 8: its first xu work items (b / 8 < xu)
+    // are whole tiles x*xu .., the next xv are the halves of split tiles full + x*xv/2 ..
+    int full, xu, xv;
+    int* sync;               // split tiles: [tiles][2] arrival counter and ready flag, all zero
+    float* part;             // split tiles: [tiles][kPipeBM * kPipeBN] partial sums
 };
 
 constexpr int kPipeBM = 256, kPipeBN = 256;
@@ -74,14 +78,30 @@ __device__ __forceinline__ uint32_t pack_h2(float lo, float hi)
     return __builtin_bit_cast(uint32_t, h2_t{(_Float16)lo, (_Float16)hi});
 }
 
-// fp32 -> fp16, 8 values per thread, in the permuted order above.
+// fp32 -> fp16 in the permuted order above: groups of 8 values, kA16Groups groups per
+// thread per pass with all their loads issued before the first store (more bytes in
+// flight per thread than one group at a time).
+constexpr int kA16Groups = 4;
 __global__ __launch_bounds__(256) void a_to_f16_kernel(const float* __restrict__ a, uint32_t* __restrict__ o, int64_t n8)
 {
-    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n8; i += (int64_t)gridDim.x * blockDim.x) {
-        const float4 lo = reinterpret_cast<const float4*>(a)[2 * i];
-        const float4 hi = reinterpret_cast<const float4*>(a)[2 * i + 1];
-        reinterpret_cast<u32x4_t*>(o)[i] =
-            u32x4_t{pack_h2(lo.x, hi.x), pack_h2(lo.y, hi.y), pack_h2(lo.z, hi.z), pack_h2(lo.w, hi.w)};
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i0 = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i0 < n8; i0 += kA16Groups * stride) {
+        float4 lo[kA16Groups], hi[kA16Groups];
+#pragma unroll
+        for (int u = 0; u < kA16Groups; ++u) {
+            const int64_t i = i0 + u * stride;
+            if (i < n8) {
+                lo[u] = reinterpret_cast<const float4*>(a)[2 * i];
+                hi[u] = reinterpret_cast<const float4*>(a)[2 * i + 1];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kA16Groups; ++u) {
+            const int64_t i = i0 + u * stride;
+            if (i < n8)
+                reinterpret_cast<u32x4_t*>(o)[i] = u32x4_t{pack_h2(lo[u].x, hi[u].x), pack_h2(lo[u].y, hi[u].y),
+                                                           pack_h2(lo[u].z, hi[u].z), pack_h2(lo[u].w, hi[u].w)};
+        }
     }
 }
 
@@ -130,13 +150,26 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
     const uint32_t lbase = lds_address(lds);
 
     const int tiles = p.tiles_m * p.tiles_n;
-    // The two K halves of a tile are neighbouring work items, so they land on the same XCD.
-    const int item = xcd_tile(blockIdx.x, tiles * p.ksplit);
-    if (item >= tiles * p.ksplit) return;
-    const int tile = item / p.ksplit, kpart = item - tile * p.ksplit;
+    // Each XCD walks a contiguous (m-major) range of whole tiles, then a contiguous range
+    // of split tiles whose two K halves are neighbouring items of the same XCD.
+    const int xcd = blockIdx.x % kXcds, xj = blockIdx.x / kXcds;
+    int tile, kpart;
+    bool split;
+    if (xj < p.xu) {
+        tile = xcd * p.xu + xj;
+        kpart = 0;
+        split = false;
+        if (tile >= p.full) return;
+    } else {
+        const int q = xj - p.xu;
+        tile = p.full + xcd * (p.xv >> 1) + (q >> 1);
+        kpart = q & 1;
+        split = true;
+        if (tile >= tiles) return;
+    }
     // Steps [c0, c0 + nsteps) of this work item; both halves are whole groups of 4 steps.
-    const int groups = p.C >> 2, g0 = kpart * (groups >> 1);
-    const int c0 = 4 * g0, nsteps = 4 * (p.ksplit == 1 ? groups : kpart == 0 ? (groups >> 1) : groups - g0);
+    const int groups = p.C >> 2, g0 = split ? kpart * (groups >> 1) : 0;
+    const int c0 = 4 * g0, nsteps = 4 * (!split ? groups : kpart == 0 ? (groups >> 1) : groups - g0);
     const int m0 = (tile / p.tiles_n) * BM, n0 = (tile % p.tiles_n) * BN;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int wm = wave & 1, wn = wave >> 1;
@@ -345,7 +378,7 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
     const int rl = p.M - m0, cl = p.N - n0;   // valid rows / columns of this tile
     using plain_store = std::integral_constant<int, 0>;
     using coherent_store = std::integral_constant<int, kDeviceCoherent>;
-    if (p.ksplit == 1) {
+    if (!split) {
         store_tile(ry, p.N, m0, n0, rl, cl, plain_store{});
         return;
     }

@@ -254,7 +254,7 @@ int check_pipe_scales(Weights& w)
 int g_panel_lanes_override = 0;  // knob 0: gemv_w4_panel lanes per row
 int g_gemv_config = 0;           // knob 1: c+1 forces kGemvConfigs[c], -1 forces gemv_w4_panel
 int g_pipe_off = 0;              // knob 2: 1 routes every prefill call to mfma_w4
-int g_pipe_ksplit = 0;           // knob 3: 1 or 2 forces the prefill K split (where K allows 2)
+int g_pipe_ksplit = 0;           // knob 3: 1 no prefill K split, 2 all tiles split, 3 the second half (where K allows)
 int g_skinny = 0;                // knob 4: 1 keeps M <= 16 off skinny_w4, 2 sends every eligible M to it
 int g_skinny_ksw = 0;            // knob 5: workgroups per skinny_w4 row block (0: heuristic)
 int g_rb = 0;                    // knob 6: 1 keeps M > 16 off mfma_w4_rb, 2 sends every eligible M to it
@@ -572,17 +572,42 @@ int device_cus()
     return v;
 }
 
-// K split of the pipelined prefill: 2 when the tiles fill at most half of the compute
-// units (measured: at 128 tiles on 256 CUs the split takes K=11008 from 328 to 268 us;
-// at 344 tiles splitting to 688 items is slower than 1.34 rounds of whole tiles). It
-// needs two groups of 4 steps (K >= 256).
-int pipe_ksplit(const Weights& w, int M)
+// K split of the pipelined prefill. Which tiles have their K range split over two
+// workgroups (they need two groups of 4 steps, K >= 256):
+//   * all of them when the tiles fill at most half of the CUs (measured: at 128 tiles on
+//     256 CUs the split takes K=11008 from 297 to 227 us);
+//   * else the tiles of a last round that would fill at most half of the CUs (344 tiles
+//     on 256: the 88 of the second round run as 176 halves, so the launch takes about
+//     1.5 rounds instead of 2; splitting all 344 into 688 items is slower);
+//   * none otherwise.
+// Knob 3: 1 none, 2 all, 3 the second half of the tiles (a test hook for the mixed form).
+struct PipeSplit {
+    int full, xu, xv;   // whole tiles [0, full); per-XCD whole and split work items
+};
+PipeSplit pipe_split(const Weights& w, int M)
 {
-    const int groups = w.K / 128;
-    if (groups < 2) return 1;
-    if (g_pipe_ksplit) return g_pipe_ksplit;
-    const int64_t tiles = (int64_t)((M + kPipeBM - 1) / kPipeBM) * ((w.N + kPipeBN - 1) / kPipeBN);
-    return 2 * tiles <= device_cus() ? 2 : 1;
+    const int tiles = ((M + kPipeBM - 1) / kPipeBM) * ((w.N + kPipeBN - 1) / kPipeBN);
+    int full = tiles;
+    if (w.K / 128 >= 2) {
+        if (g_pipe_ksplit == 2) {
+            full = 0;
+        } else if (g_pipe_ksplit == 3) {
+            full = tiles / 2;
+        } else if (g_pipe_ksplit == 0) {
+            const int cus = device_cus();
+            if (2 * tiles <= cus) {
+                full = 0;
+            } else {
+                const int rem = tiles % cus;
+                if (rem > 0 && 2 * rem <= cus) full = tiles - rem;
+            }
+        }
+    }
+    PipeSplit sp;
+    sp.full = full;
+    sp.xu = (full + kXcds - 1) / kXcds;
+    sp.xv = 2 * ((tiles - full + kXcds - 1) / kXcds);
+    return sp;
 }
 
 // Returns 1 when the pipelined prefill was launched, 0 when the caller should use
@@ -593,13 +618,13 @@ int launch_pipe(Weights& w, const float* dA, float* dY, int M, hipStream_t strea
     const size_t need = (size_t)M * w.K * 2;
     const int tiles_m = (M + kPipeBM - 1) / kPipeBM, tiles_n = (w.N + kPipeBN - 1) / kPipeBN;
     const int tiles = tiles_m * tiles_n;
-    const int ksplit = pipe_ksplit(w, M);
+    const PipeSplit sp = pipe_split(w, M);
     uint32_t* ws = nullptr;
     int* sync = nullptr;
     float* part = nullptr;
     {
         std::lock_guard<std::mutex> lock(w.ws_mu);
-        const bool grow_ws = w.a16_bytes < need, grow_sync = ksplit > 1 && w.sync_tiles < tiles;
+        const bool grow_ws = w.a16_bytes < need, grow_sync = sp.full < tiles && w.sync_tiles < tiles;
         if (grow_ws || grow_sync) {
             hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
             if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
@@ -641,8 +666,9 @@ int launch_pipe(Weights& w, const float* dA, float* dY, int M, hipStream_t strea
         lds_raised.store(true);
     }
     const int64_t n8 = (int64_t)M * w.K / 8;
-    hipLaunchKernelGGL(a_to_f16_kernel, dim3((unsigned)std::min<int64_t>((n8 + 255) / 256, 4096)), dim3(256), 0,
-                       stream, dA, ws, n8);
+    hipLaunchKernelGGL(a_to_f16_kernel,
+                       dim3((unsigned)std::min<int64_t>((n8 + 256 * kA16Groups - 1) / (256 * kA16Groups), 2048)),
+                       dim3(256), 0, stream, dA, ws, n8);
     PipeParams p;
     p.b = w.d_b;
     p.scales = w.d_scales;
@@ -658,12 +684,12 @@ int launch_pipe(Weights& w, const float* dA, float* dY, int M, hipStream_t strea
     p.zrb = w.zrb;
     p.tiles_m = tiles_m;
     p.tiles_n = tiles_n;
-    p.ksplit = ksplit;
+    p.full = sp.full;
+    p.xu = sp.xu;
+    p.xv = sp.xv;
     p.sync = sync;
     p.part = part;
-    const int items = tiles * ksplit;
-    hipLaunchKernelGGL(mfma_w4_pipe_kernel, dim3(((items + kXcds - 1) / kXcds) * kXcds), dim3(256), kPipeLdsBytes,
-                       stream, p);
+    hipLaunchKernelGGL(mfma_w4_pipe_kernel, dim3(kXcds * (sp.xu + sp.xv)), dim3(256), kPipeLdsBytes, stream, p);
     return hipGetLastError() == hipSuccess ? 1 : -1;
 }
 
@@ -804,7 +830,9 @@ bool use_rb(const Weights& w, int M)
 {
     if (!rb_eligible(w, M)) return false;
     if (g_rb == 2 || !pipe_eligible(w, M)) return true;
-    const int64_t items = (int64_t)((M + kPipeBM - 1) / kPipeBM) * ((w.N + kPipeBN - 1) / kPipeBN) * pipe_ksplit(w, M);
+    const int64_t tiles = (int64_t)((M + kPipeBM - 1) / kPipeBM) * ((w.N + kPipeBN - 1) / kPipeBN);
+    const PipeSplit sp = pipe_split(w, M);
+    const int64_t items = sp.full + 2 * (tiles - sp.full);
     return 2 * items < device_cus();
 }
 
@@ -848,8 +876,9 @@ int launch_rb(Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
         part = w.d_rbpart;
     }
     const int64_t n8 = (int64_t)M * w.K / 8;
-    hipLaunchKernelGGL(a_to_f16_kernel, dim3((unsigned)std::min<int64_t>((n8 + 255) / 256, 4096)), dim3(256), 0,
-                       stream, dA, ws, n8);
+    hipLaunchKernelGGL(a_to_f16_kernel,
+                       dim3((unsigned)std::min<int64_t>((n8 + 256 * kA16Groups - 1) / (256 * kA16Groups), 2048)),
+                       dim3(256), 0, stream, dA, ws, n8);
     RbParams p;
     p.b = w.d_b;
     p.scales = w.d_scales;
@@ -1274,7 +1303,7 @@ int ms_hip_set_tuning(int knob, int value)
             g_pipe_off = value;
             return MS_HIP_OK;
         case 3:
-            if (value < 0 || value > 2) break;
+            if (value < 0 || value > 3) break;
             g_pipe_ksplit = value;
             return MS_HIP_OK;
         case 4:
@@ -1335,8 +1364,8 @@ int ms_hip_nbits_launch_info(void* handle, int M, int* kernel_id, int* lanes_per
         bl = 256;
     } else if (pipe_eligible(*w, M)) {
         kid = 4;
-        const int items = ((M + kPipeBM - 1) / kPipeBM) * ((w->N + kPipeBN - 1) / kPipeBN) * pipe_ksplit(*w, M);
-        gr = ((items + kXcds - 1) / kXcds) * kXcds;
+        const PipeSplit sp = pipe_split(*w, M);
+        gr = kXcds * (sp.xu + sp.xv);
         bl = 256;
     } else {
         kid = 2;

@@ -337,14 +337,17 @@ def test_mfma_parity_sampled_columns(gpu, op, M):
 
 
 def pipe_items(M, N, ksplit):
-    """Workgroups the pipelined prefill launches: 256x256 tiles times the K split, in whole XCD rounds."""
-    items = -(-M // 256) * -(-N // 256) * ksplit
-    return -(-items // 8) * 8
+    """Workgroups the pipelined prefill launches for knob 3 = ksplit (1: no tile split,
+    2: all tiles split, 3: the second half split): 8 XCDs x (whole tiles per XCD + two
+    halves per split tile per XCD)."""
+    tiles = -(-M // 256) * -(-N // 256)
+    full = tiles if ksplit == 1 else 0 if ksplit == 2 else tiles // 2
+    return 8 * (-(-full // 8) + 2 * -(-(tiles - full) // 8))
 
 
 @pytest.mark.parametrize("M", [17, 33, 64, 100, 129, 300])
 def test_mfma_partial_tiles(gpu, M):
-    """Both prefill kernels, and the pipelined one with and without the K split, on
+    """Both prefill kernels, and the pipelined one with no, every and half of its tiles K-split, on
     tiles cut by M and N (N=333 is not a multiple of 256; K=896 is 7 groups of 4
     steps, so the two K halves are unequal: 3 and 4 groups). mfma_w4_rb, which these
     small launches would take, is switched off."""
@@ -354,7 +357,7 @@ def test_mfma_partial_tiles(gpu, M):
     ref = oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, 32)
     try:
         native.set_tuning(6, 1)
-        for ks in (1, 2):
+        for ks in (1, 2, 3):
             native.set_tuning(3, ks)
             info = w.launch_info(M)
             assert info["kernel"] == "mfma_w4_pipe" and info["grid"] == pipe_items(M, op.N, ks)
