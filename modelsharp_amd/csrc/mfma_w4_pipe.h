@@ -39,9 +39,8 @@
 //     * Split K (for launches with too few tiles to fill the CUs, or for the tiles of
 //       a last, partly filled round): the two halves of a split tile (whole groups
 //       of 4 steps each) are neighbouring work items; the first to finish writes its
-//       partial sums through to Y and raises a flag, the second stores its own into a
-//       workspace slot and then adds the slot into Y (deterministic: fp32 a + b ==
-//       b + a).
+//       partial sums through to a workspace slot and raises a flag, the second adds the
+//       slot to its own sums and stores Y once (deterministic: fp32 a + b == b + a).
 // Numerics: A rounded once to fp16; W = fl16((q - zp) * fl16(s)); products exact,
 // sums fp32. Requires |A| < 65504 (fp16 range) and fp16-normal scales for the
 // 2^-11 relative bound; the library routes other inputs to mfma_w4.
@@ -137,6 +136,160 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // 16-byte chunk slot of k-chunk j in row r: conflict-free for 8- and 16-row passes.
 __device__ __forceinline__ int pipe_slot(int r, int j) { return j ^ (((r >> 2) & 3) ^ (r & 2)); }
 
+// One work item of the pipelined launch: a whole tile, or one K half of a split tile.
+struct PipeItem {
+    int tile, c0, nsteps, m0, n0;   // steps [c0, c0 + nsteps) of tile (m0, n0)
+    bool split;
+};
+
+// Decodes workgroup blockIdx.x's work item; false when the grid's padding has none.
+// Each XCD walks a contiguous (m-major) range of whole tiles, then a contiguous range
+// of split tiles whose two K halves are neighbouring items of the same XCD.
+__device__ __forceinline__ bool pipe_item(const PipeParams& p, PipeItem& it)
+{
+    const int tiles = p.tiles_m * p.tiles_n;
+    const int xcd = blockIdx.x % kXcds, xj = blockIdx.x / kXcds;
+    int kpart;
+    if (xj < p.xu) {
+        it.tile = xcd * p.xu + xj;
+        kpart = 0;
+        it.split = false;
+        if (it.tile >= p.full) return false;
+    } else {
+        const int q = xj - p.xu;
+        it.tile = p.full + xcd * (p.xv >> 1) + (q >> 1);
+        kpart = q & 1;
+        it.split = true;
+        if (it.tile >= tiles) return false;
+    }
+    // Both halves are whole groups of 4 steps.
+    const int groups = p.C >> 2, g0 = it.split ? kpart * (groups >> 1) : 0;
+    it.c0 = 4 * g0;
+    it.nsteps = 4 * (!it.split ? groups : kpart == 0 ? (groups >> 1) : groups - g0);
+    it.m0 = (it.tile / p.tiles_n) * kPipeBM;
+    it.n0 = (it.tile % p.tiles_n) * kPipeBN;
+    return true;
+}
+
+// Stores a work item's 256x256 accumulators (4 waves in 2x2, each 4x4 fragments of
+// v_mfma_f32_32x32x16 layout) into Y, through the split-K hand-off for split tiles.
+__device__ __forceinline__ void pipe_epilogue(const PipeParams& p, const PipeItem& it, floatx16_t (&acc)[4][4])
+{
+    constexpr int BM = kPipeBM, BN = kPipeBN, FM = 4, FN = 4;
+    // Lane indices from an opaque copy of the thread id: the compiler cannot share the
+    // epilogue's address terms with the main loop's and keep them live (spilled) across it.
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & (kWave - 1), wave = tid / kWave;
+    const int wm = wave & 1, wn = wave >> 1, lr = lane & 31, lh = lane >> 5;
+    const int m0 = it.m0, n0 = it.n0, tile = it.tile;
+    const bool split = it.split;
+    // acc[i][j][v] is Y[row][col], col = lane % 32, row = 8*(v/4) + 4*(lane/32) + v%4.
+    // Stores go through a buffer resource with an offset that has bit 30 set outside the
+    // valid rows/columns (every destination is smaller than 2^30 bytes, checked by the
+    // host): such stores are dropped, so the epilogue has no branches. The destination
+    // is runtime data: the tile (rb, cb) of an ld-wide matrix with rl x cl valid entries.
+    auto store_tile = [&](__amdgpu_buffer_rsrc_t rd, int ld, int rb, int cb, int rl, int cl, auto cpol) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const int row0 = wm * 128 + 32 * i + 4 * lh;
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int col = wn * 128 + 32 * j + lr;
+                const uint32_t base = ((uint32_t)(rb + row0) * (uint32_t)ld + (uint32_t)(cb + col)) * 4u;
+                const int cfree = cl - 1 - col;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int rv = 8 * (v >> 2) + (v & 3);
+                    const uint32_t outside = (uint32_t)(((rl - 1 - row0 - rv) | cfree) >> 31);   // all ones outside
+                    const int off = (int)((base + (uint32_t)(rv * 4) * (uint32_t)ld) | (outside & (uint32_t)kPipeFar));
+                    const float x = acc[i][j][v];   // bit_cast of a vector element would read element 0
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x), rd, off, 0, decltype(cpol)::value);
+                }
+            }
+        }
+    };
+    const __amdgpu_buffer_rsrc_t ry = buffer_rsrc(p.y, p.M * p.N * 4);
+    const int rl = p.M - m0, cl = p.N - n0;   // valid rows / columns of this tile
+    using plain_store = std::integral_constant<int, 0>;
+    using coherent_store = std::integral_constant<int, kDeviceCoherent>;
+    if (!split) {
+        store_tile(ry, p.N, m0, n0, rl, cl, plain_store{});
+        return;
+    }
+    // Two halves: the first to arrive writes its partial sums through to its tile's slot
+    // of the partials workspace (sc1 stores) and raises the tile's flag once those stores
+    // have completed; the second waits for the flag, reads the slot with device-coherent
+    // loads and stores its own sums plus the slot into Y, once. Per split tile that moves
+    // three tiles of fp32 (slot write, slot read, Y write). Y = p0 + p1 either way (fp32
+    // addition commutes), so the result does not depend on the arrival order. The second
+    // waits only for a workgroup that has already arrived (and is therefore running), so
+    // the wait ends. The hand-off uses no agent-scope fence (on gfx950 those write back or
+    // invalidate the XCD's whole L2, and an acquiring spin would invalidate it on every
+    // poll).
+    __shared__ int arrival;
+    int* const cnt = p.sync + 2 * tile;
+    if (threadIdx.x == 0) arrival = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const bool second = arrival != 0;
+    float* const slot = p.part + (int64_t)tile * (BM * BN);
+    const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(slot, BM * BN * 4);
+    if (!second) {
+        store_tile(rs, BN, 0, 0, rl, cl, coherent_store{});
+        wait_vmem_order_only_release();
+        __syncthreads();
+        if (threadIdx.x == 0) __hip_atomic_store(cnt + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    if (threadIdx.x == 0) {
+        // Bounded: the first half is running and needs no other workgroup to finish, so
+        // the flag comes within microseconds; the bound only keeps a misuse (two launches
+        // on one handle overlapping) from hanging the device.
+        for (int spin = 0; spin < (1 << 22); ++spin) {
+            if (__hip_atomic_load(cnt + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
+            __builtin_amdgcn_s_sleep(2);
+        }
+        // Both halves are past their use of the pair: leave it zero for the next launch.
+        __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(cnt + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    wait_vmem_order_only_acquire();
+    // Y = acc + slot, in the accumulator layout (each lane reads back the slot entries the
+    // first half's lane of the same position wrote), one fragment at a time with the next
+    // fragment's loads issued before this fragment's stores (the compiler cannot move loads
+    // of one buffer above stores to another).
+    constexpr int NF = FM * FN;
+    auto frag_offset = [&](int f, int v, int ld, int rb, int cb) {   // byte offset, bit 30 set outside
+        const int i = f / FN, j = f % FN;
+        const int r = wm * 128 + 32 * i + 4 * lh + 8 * (v >> 2) + (v & 3), col = wn * 128 + 32 * j + lr;
+        const uint32_t far = (uint32_t)(((rl - 1 - r) | (cl - 1 - col)) >> 31) & (uint32_t)kPipeFar;
+        return (int)((((uint32_t)(rb + r) * (uint32_t)ld + (uint32_t)(cb + col)) * 4u) | far);
+    };
+    floatx16_t sv[2];
+    auto load_frag = [&](int f, floatx16_t& sd) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+            sd[v] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, frag_offset(f, v, BN, 0, 0), 0,
+                                                                                   kDeviceCoherent));
+    };
+    load_frag(0, sv[0]);
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        if (f + 1 < NF) load_frag(f + 1, sv[(f + 1) & 1]);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            // Read the accumulator with an AGPR operand: used as a plain float, the register
+            // allocator moves all 256 accumulators out of the AGPRs at the loop exit and spills.
+            float a;
+            asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(a) : "a"(acc[f / FN][f % FN][v]));
+            const float xv = a + sv[f & 1][v];
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, xv), ry, frag_offset(f, v, p.N, m0, n0), 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);   // keeps the scheduler from hoisting every load (and spilling)
+    }
+}
+
 __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
 {
     constexpr int BM = kPipeBM, BN = kPipeBN, FM = 4, FN = 4;
@@ -149,28 +302,9 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
     uint8_t* const lds = pipe_lds;
     const uint32_t lbase = lds_address(lds);
 
-    const int tiles = p.tiles_m * p.tiles_n;
-    // Each XCD walks a contiguous (m-major) range of whole tiles, then a contiguous range
-    // of split tiles whose two K halves are neighbouring items of the same XCD.
-    const int xcd = blockIdx.x % kXcds, xj = blockIdx.x / kXcds;
-    int tile, kpart;
-    bool split;
-    if (xj < p.xu) {
-        tile = xcd * p.xu + xj;
-        kpart = 0;
-        split = false;
-        if (tile >= p.full) return;
-    } else {
-        const int q = xj - p.xu;
-        tile = p.full + xcd * (p.xv >> 1) + (q >> 1);
-        kpart = q & 1;
-        split = true;
-        if (tile >= tiles) return;
-    }
-    // Steps [c0, c0 + nsteps) of this work item; both halves are whole groups of 4 steps.
-    const int groups = p.C >> 2, g0 = split ? kpart * (groups >> 1) : 0;
-    const int c0 = 4 * g0, nsteps = 4 * (!split ? groups : kpart == 0 ? (groups >> 1) : groups - g0);
-    const int m0 = (tile / p.tiles_n) * BM, n0 = (tile % p.tiles_n) * BN;
+    PipeItem it;
+    if (!pipe_item(p, it)) return;
+    const int c0 = it.c0, nsteps = it.nsteps, m0 = it.m0, n0 = it.n0;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int wm = wave & 1, wn = wave >> 1;
 
@@ -349,97 +483,7 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
     }
     wait_vmcnt<0>();
 
-    // acc[i][j][v] is Y[row][col], col = lane % 32, row = 8*(v/4) + 4*(lane/32) + v%4.
-    // Stores go through a buffer resource with an offset that has bit 30 set outside the
-    // valid rows/columns (every destination is smaller than 2^30 bytes, checked by the
-    // host): such stores are dropped, so the epilogue has no branches. The destination
-    // is runtime data: the tile (rb, cb) of an ld-wide matrix with rl x cl valid entries.
-    auto store_tile = [&](__amdgpu_buffer_rsrc_t rd, int ld, int rb, int cb, int rl, int cl, auto cpol) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-            const int row0 = wm * 128 + 32 * i + 4 * lh;
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                const int col = wn * 128 + 32 * j + lr;
-                const uint32_t base = ((uint32_t)(rb + row0) * (uint32_t)ld + (uint32_t)(cb + col)) * 4u;
-                const int cfree = cl - 1 - col;
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int rv = 8 * (v >> 2) + (v & 3);
-                    const uint32_t outside = (uint32_t)(((rl - 1 - row0 - rv) | cfree) >> 31);   // all ones outside
-                    const int off = (int)((base + (uint32_t)(rv * 4) * (uint32_t)ld) | (outside & (uint32_t)kPipeFar));
-                    const float x = acc[i][j][v];   // bit_cast of a vector element would read element 0
-                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x), rd, off, 0, decltype(cpol)::value);
-                }
-            }
-        }
-    };
-    const __amdgpu_buffer_rsrc_t ry = buffer_rsrc(p.y, p.M * p.N * 4);
-    const int rl = p.M - m0, cl = p.N - n0;   // valid rows / columns of this tile
-    using plain_store = std::integral_constant<int, 0>;
-    using coherent_store = std::integral_constant<int, kDeviceCoherent>;
-    if (!split) {
-        store_tile(ry, p.N, m0, n0, rl, cl, plain_store{});
-        return;
-    }
-    // Two halves: the first to arrive stores its partial sums into Y, the second into
-    // its tile's slot of the partials workspace; once the first has raised the tile's
-    // flag the second adds the slot into Y. Y = p0 + p1 either way (fp32 addition
-    // commutes), so the result does not depend on the arrival order. The second waits
-    // only for a workgroup that has already arrived (and is therefore running), so the
-    // wait ends. The hand-off uses no agent-scope fence (on gfx950 those write back or
-    // invalidate the XCD's whole L2, and an acquiring spin would invalidate it on every
-    // poll): the first half writes Y through to device scope (sc1) and raises the flag
-    // only after those stores have completed; the second polls the flag and reads Y with
-    // device-coherent loads.
-    __shared__ int arrival;
-    int* const cnt = p.sync + 2 * tile;
-    if (threadIdx.x == 0) arrival = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    const bool second = arrival != 0;
-    float* const slot = p.part + (int64_t)tile * (BM * BN);
-    const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(slot, BM * BN * 4);
-    if (!second) {
-        store_tile(ry, p.N, m0, n0, rl, cl, coherent_store{});
-        wait_vmem_order_only_release();
-        __syncthreads();
-        if (threadIdx.x == 0) __hip_atomic_store(cnt + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return;
-    }
-    store_tile(rs, BN, 0, 0, rl, cl, plain_store{});
-    if (threadIdx.x == 0) {
-        // Bounded: the first half is running and needs no other workgroup to finish, so
-        // the flag comes within microseconds; the bound only keeps a misuse (two launches
-        // on one handle overlapping) from hanging the device.
-        for (int spin = 0; spin < (1 << 22); ++spin) {
-            if (__hip_atomic_load(cnt + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
-            __builtin_amdgcn_s_sleep(2);
-        }
-        // Both halves are past their use of the pair: leave it zero for the next launch.
-        __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(cnt + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();   // also orders this workgroup's slot stores before its slot loads
-    wait_vmem_order_only_acquire();
-    // Y[m0 + r][n0 + c] += slot[r][c]: thread t takes columns c = t, one row per pass.
-    const int c = threadIdx.x;
-    const uint32_t cfar = (uint32_t)((cl - 1 - c) >> 31) & (uint32_t)kPipeFar;
-    for (int r0 = 0; r0 < BM; r0 += 16) {
-        float yv[16], sv[16];
-        int yo[16];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const int r = r0 + u;
-            const uint32_t far = cfar | ((uint32_t)((rl - 1 - r) >> 31) & (uint32_t)kPipeFar);
-            yo[u] = (int)((((uint32_t)(m0 + r) * (uint32_t)p.N + (uint32_t)(n0 + c)) * 4u) | far);
-            sv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                  rs, (int)(((uint32_t)(r * BN + c) * 4u) | far), 0, 0));
-            yv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ry, yo[u], 0, kDeviceCoherent));
-        }
-#pragma unroll
-        for (int u = 0; u < 16; ++u)
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, yv[u] + sv[u]), ry, yo[u], 0, 0);
-    }
+    pipe_epilogue(p, it, acc);
 }
 
 }  // namespace msnb
