@@ -146,8 +146,6 @@ int ms_hip_sync(void);
  *   6 1 keeps M > 16 off the register-operand prefill kernel, 2 sends every eligible
  *     M > 16 to it;
  *   7 its K split (workgroups per 128 x 256 tile, 1..64, clamped to K / 128).
- *   8 the pipelined prefill's weight path: 1 dequantized by each wave into its MFMA
- *     operand registers (mfma_w4_preg), 2 through an fp16 tile in LDS (mfma_w4_pipe).
  * ms_hip_nbits_launch_info reports what a call with M rows would launch:
  *   kernel_id 0 generic, 1 gemv_w4, 2 mfma_w4, 3 gemv_w4_panel, 4 mfma_w4_pipe,
  *   5 skinny_w4, 6 mfma_w4_rb. */

@@ -30,7 +30,6 @@
 #include "generic_nbits.h"
 #include "mfma_w4.h"
 #include "mfma_w4_pipe.h"
-#include "mfma_w4_preg.h"
 #include "mfma_w4_rb.h"
 #include "skinny_w4.h"
 
@@ -260,7 +259,6 @@ int g_skinny = 0;                // knob 4: 1 keeps M <= 16 off skinny_w4, 2 sen
 int g_skinny_ksw = 0;            // knob 5: workgroups per skinny_w4 row block (0: heuristic)
 int g_rb = 0;                    // knob 6: 1 keeps M > 16 off mfma_w4_rb, 2 sends every eligible M to it
 int g_rb_ksw = 0;                // knob 7: mfma_w4_rb K split (0: heuristic)
-int g_preg = 0;                  // knob 8: 1 takes mfma_w4_preg for the pipelined prefill, 2 mfma_w4_pipe
 
 // gemv_w4 instantiations: [M-1][L slot][config], L slot 0 = block size 32, 1 = block size 128.
 typedef void (*GemvFn)(GemvParams);
@@ -663,9 +661,7 @@ int launch_pipe(Weights& w, const float* dA, float* dY, int M, hipStream_t strea
     static std::atomic<bool> lds_raised{false};
     if (!lds_raised.load()) {
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(mfma_w4_pipe_kernel),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, kPipeLdsBytes) != hipSuccess ||
-            hipFuncSetAttribute(reinterpret_cast<const void*>(mfma_w4_preg_kernel),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, kPregLdsBytes) != hipSuccess)
+                                hipFuncAttributeMaxDynamicSharedMemorySize, kPipeLdsBytes) != hipSuccess)
             return -1;
         lds_raised.store(true);
     }
@@ -693,10 +689,7 @@ int launch_pipe(Weights& w, const float* dA, float* dY, int M, hipStream_t strea
     p.xv = sp.xv;
     p.sync = sync;
     p.part = part;
-    if (g_preg == 1)
-        hipLaunchKernelGGL(mfma_w4_preg_kernel, dim3(kXcds * (sp.xu + sp.xv)), dim3(256), kPregLdsBytes, stream, p);
-    else
-        hipLaunchKernelGGL(mfma_w4_pipe_kernel, dim3(kXcds * (sp.xu + sp.xv)), dim3(256), kPipeLdsBytes, stream, p);
+    hipLaunchKernelGGL(mfma_w4_pipe_kernel, dim3(kXcds * (sp.xu + sp.xv)), dim3(256), kPipeLdsBytes, stream, p);
     return hipGetLastError() == hipSuccess ? 1 : -1;
 }
 
@@ -1328,10 +1321,6 @@ int ms_hip_set_tuning(int knob, int value)
         case 7:
             if (value < 0 || value > 64) break;
             g_rb_ksw = value;
-            return MS_HIP_OK;
-        case 8:
-            if (value < 0 || value > 2) break;
-            g_preg = value;
             return MS_HIP_OK;
         default: break;
     }
