@@ -134,6 +134,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
         float s[RL][U];
         uint32_t z[RL][U];
     };
+    // The codes are read once per call, each 128-byte line whole by one load of G lanes:
+    // non-temporal loads keep them from displacing the activations, outputs, scales and
+    // zero points in L2 / MALL. Scale and zero-point lines serve several steps of a row, so
+    // they stay cached (non-temporal there too refetched them). Measured on the 7B decode
+    // layer: 46.2 -> 43.4 us per step of 4 launches; the gate+up launch 20.1 -> 18.2 us.
     auto load = [&](Batch& bt, int k0) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -141,10 +146,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
             const bool ok = k < nvalid;
 #pragma unroll
             for (int j = 0; j < RL; ++j) {
-                bt.q[j][u] = __builtin_amdgcn_raw_buffer_load_b128(rb, ok ? bbase[j] + k * (SPAN * 16) : kOOB, 0, 0);
-                bt.s[j][u] = __builtin_bit_cast(
-                    float, __builtin_amdgcn_raw_buffer_load_b32(rsc, ok ? sbase[j] + k * (BSPAN * 4) : kOOB, 0, 0));
-                bt.z[j][u] = __builtin_amdgcn_raw_buffer_load_b8(rz, ok ? zbase[j] + k * (BSPAN / 2) : kOOB, 0, 0);
+                bt.q[j][u] = __builtin_amdgcn_raw_buffer_load_b128(rb, ok ? bbase[j] + k * (SPAN * 16) : kOOB, 0,
+                                                                   kNonTemporal);
+                bt.s[j][u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                           rsc, ok ? sbase[j] + k * (BSPAN * 4) : kOOB, 0, 0));
+                bt.z[j][u] = __builtin_amdgcn_raw_buffer_load_b8(rz, ok ? zbase[j] + k * (BSPAN / 2) : kOOB, 0,
+                                                                 0);
             }
         }
     };

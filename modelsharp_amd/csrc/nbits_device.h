@@ -156,6 +156,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 // Buffer cache policy sc1 (device scope): stores write through to where every XCD
 // reads, loads do not return another XCD's stale copy.
 constexpr int kDeviceCoherent = 16;
+// Buffer cache policy nt: streaming data, not kept in the caches for reuse.
+constexpr int kNonTemporal = 2;
 
 // Cross-workgroup hand-off through data written and read with agent-scope atomic
 // stores / loads (those write and read through the caches, so the data needs no L2
