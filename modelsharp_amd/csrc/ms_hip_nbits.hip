@@ -302,8 +302,10 @@ bool gemv_config_fits(const Weights& w, int M, const GemvConfig& c)
 // every lane at least 2 steps. The lists come from sweeping every config over the
 // 7B and Qwen2.5-0.5B decode launches on MI355X (M = 1, 2, 4; single matrices and
 // groups of one input's projections): for M <= 2, two rows per lane at 16 lanes per
-// row win from 16K rows up, 64 lanes per row with two rows per lane around 4-16K rows,
-// 32 lanes per row below; for M = 3-4 the 8-wave configs. N is the launch's total
+// row win from 16K rows up, 64 lanes per row with two rows per lane from 2K to 16K rows
+// (re-swept with the non-temporal code loads: 7B o at M = 1 / 2 5.41 -> 5.26 /
+// 6.83 -> 6.54 us against the 32-lane pick), 32 lanes per row below; for M = 3-4 the
+// 8-wave configs. N is the launch's total
 // rows (summed over a group). Indices are into kGemvConfigs; the streaming-read ceiling
 // of the 7B gate+up launch's bytes (a plain row-pattern read, same rotation) is
 // 14.5-15.1 us, against which its pick runs at about 20 us.
@@ -316,7 +318,7 @@ int pick_gemv_config(const Weights& w, int M, int N)
     }
     static constexpr int kLargeM2[] = {16, 11, 0, 6};   // M <= 2, N >= 16384
     static constexpr int kMidM2[] = {14, 11, 2};        // M <= 2, N >= 4096
-    static constexpr int kSmallM2[] = {13, 6, 8};       // M <= 2, N >= 2048
+    static constexpr int kSmallM2[] = {14, 13, 6, 8};   // M <= 2, N >= 2048
     static constexpr int kTinyM2[] = {3, 14, 8};        // M <= 2
     static constexpr int kLargeM4[] = {7, 6, 0};        // M <= 4, N >= 16384
     static constexpr int kMidM4[] = {15, 7, 8};         // M <= 4, N >= 4096
@@ -335,7 +337,7 @@ int pick_gemv_config(const Weights& w, int M, int N)
     int ci;
     if (M <= 2)
         ci = N >= 16384 ? first_of(kLargeM2, 4) : N >= 4096 ? first_of(kMidM2, 3)
-           : N >= 2048  ? first_of(kSmallM2, 3) : first_of(kTinyM2, 3);
+           : N >= 2048  ? first_of(kSmallM2, 4) : first_of(kTinyM2, 3);
     else
         ci = N >= 16384 ? first_of(kLargeM4, 3) : N >= 4096 ? first_of(kMidM4, 3) : first_of(kSmallM4, 3);
     if (ci < 0) ci = first_of(kWide, 2);
