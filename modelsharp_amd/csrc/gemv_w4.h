@@ -241,17 +241,15 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
         load(bB, k0 + 3 * U);
     }
 
-    // ---- 4. combine: G lanes (butterfly), then KW waves (LDS, in wave order) -----------
+    // ---- 4. combine: G lanes (DPP scan), then KW waves (LDS, in wave order) -----------
+    // The G lanes' sums end in lane g == G - 1 of each group.
 #pragma unroll
-    for (int off = G / 2; off > 0; off >>= 1) {
+    for (int j = 0; j < RL; ++j) {
 #pragma unroll
-        for (int j = 0; j < RL; ++j) {
-#pragma unroll
-            for (int m = 0; m < M; ++m) acc[j][m] += __shfl_xor(acc[j][m], off, kWave);
-        }
+        for (int m = 0; m < M; ++m) acc[j][m] = group_sum_to_last<G>(acc[j][m]);
     }
     if constexpr (KW > 1) {
-        if (g == 0) {
+        if (g == G - 1) {
 #pragma unroll
             for (int j = 0; j < RL; ++j) {
 #pragma unroll
@@ -259,7 +257,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
             }
         }
         __syncthreads();
-        if (wk == 0 && g == 0) {
+        if (wk == 0 && g == G - 1) {
 #pragma unroll
             for (int j = 0; j < RL; ++j) {
 #pragma unroll
@@ -272,7 +270,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
             }
         }
     }
-    if (wk == 0 && g == 0) {
+    if (wk == 0 && g == G - 1) {
 #pragma unroll
         for (int j = 0; j < RL; ++j) {
             const int nj = n0 + j * ROWS0;

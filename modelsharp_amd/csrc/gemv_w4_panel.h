@@ -156,13 +156,10 @@ __global__ __launch_bounds__(kPanelThreads) void gemv_w4_panel_kernel(GemvPanelP
         }
     }
 
-    // ---- combine the G lanes of each row (butterfly, fixed order) ----------------------
+    // ---- combine the G lanes of each row (DPP scan, fixed order; sum in lane G - 1) -----
 #pragma unroll
-    for (int off = G / 2; off > 0; off >>= 1) {
-#pragma unroll
-        for (int m = 0; m < M; ++m) acc[m] += __shfl_xor(acc[m], off, kWave);
-    }
-    if (g == 0 && row_ok) {
+    for (int m = 0; m < M; ++m) acc[m] = group_sum_to_last<G>(acc[m]);
+    if (g == G - 1 && row_ok) {
 #pragma unroll
         for (int m = 0; m < M; ++m) p.y[(int64_t)m * p.N + n] = acc[m];
     }

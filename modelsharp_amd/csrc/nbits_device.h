@@ -159,6 +159,33 @@ constexpr int kDeviceCoherent = 16;
 // Buffer cache policy nt: streaming data, not kept in the caches for reuse.
 constexpr int kNonTemporal = 2;
 
+// x + (x moved by one DPP control); lanes whose source is outside the row, or whose row the
+// mask leaves out, add 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float x)
+{
+    const int y = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROW_MASK, 0xF, false);
+    return x + __builtin_bit_cast(float, y);
+}
+
+// Sum of x over each aligned group of G lanes (G = 16, 32 or 64), left in the group's last
+// lane (the other lanes hold partial sums): an inclusive scan inside each 16-lane row
+// (row_shr 1, 2, 4, 8), then row_bcast:15 into rows 1 and 3 and row_bcast:31 into rows 2
+// and 3. Every step is one VALU op; a ds_bpermute butterfly costs an LDS round trip per
+// level. The order of the additions is fixed, so results are deterministic.
+template <int G>
+__device__ __forceinline__ float group_sum_to_last(float x)
+{
+    static_assert(G == 16 || G == 32 || G == 64, "groups of 16, 32 or 64 lanes");
+    x = dpp_add<0x111, 0xF>(x);   // row_shr:1
+    x = dpp_add<0x112, 0xF>(x);   // row_shr:2
+    x = dpp_add<0x114, 0xF>(x);   // row_shr:4
+    x = dpp_add<0x118, 0xF>(x);   // row_shr:8
+    if constexpr (G >= 32) x = dpp_add<0x142, 0xA>(x);   // row_bcast:15 -> rows 1, 3
+    if constexpr (G == 64) x = dpp_add<0x143, 0xC>(x);   // row_bcast:31 -> rows 2, 3
+    return x;
+}
+
 // Cross-workgroup hand-off through data written and read with agent-scope atomic
 // stores / loads (those write and read through the caches, so the data needs no L2
 // write-back or invalidate). These two only order: the release form waits until every
