@@ -168,6 +168,24 @@ __device__ __forceinline__ float dpp_add(float x)
     return x + __builtin_bit_cast(float, y);
 }
 
+// Maximum of x over each aligned 16-lane row, in every lane of the row: quad_perm swaps
+// of neighbours and pairs (every lane then holds its quad's maximum), row_half_mirror
+// (lane i of each 8-lane half with lane 7 - i: the other quad), row_mirror (lane i with
+// lane 15 - i: the other half). Four VALU ops instead of four ds_bpermute round trips.
+template <int CTRL>
+__device__ __forceinline__ float dpp_read(float x)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_max_all(float x)
+{
+    x = fmaxf(x, dpp_read<0xB1>(x));    // quad_perm [1,0,3,2]
+    x = fmaxf(x, dpp_read<0x4E>(x));    // quad_perm [2,3,0,1]
+    x = fmaxf(x, dpp_read<0x141>(x));   // row_half_mirror
+    x = fmaxf(x, dpp_read<0x140>(x));   // row_mirror
+    return x;
+}
+
 // Sum of x over each aligned group of G lanes (G = 16, 32 or 64), left in the group's last
 // lane (the other lanes hold partial sums): an inclusive scan inside each 16-lane row
 // (row_shr 1, 2, 4, 8), then row_bcast:15 into rows 1 and 3 and row_bcast:31 into rows 2

@@ -145,8 +145,7 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
         float mx = 0.0f;
 #pragma unroll
         for (int r = 0; r < 8; ++r) mx = fmaxf(mx, fabsf(v[r]));
-#pragma unroll
-        for (int off = 8; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+        mx = row16_max_all(mx);   // the 16 lanes of this row and block
         // mx in [2^(E-1), 2^E) with E = frexp exponent; 2^-e with e = E - 15 brings it
         // into [2^14, 2^15) (an all-zero block gets e = -15 and stays zero).
         const int e = __builtin_amdgcn_frexp_expf(mx) - 15;
