@@ -59,8 +59,8 @@ struct PipeParams {
     int row_bytes, M, N, K, C, nb, zrb;
     int tiles_m, tiles_n;
     // Tiles [0, full) run whole; each tile from `full` on has its K range split over two
-    // workgroups. Workgroup b runs on XCD x = b % 8: its first xu work items (b / 8 < xu)
-    // are whole tiles x*xu .., the next xv are the halves of split tiles full + x*xv/2 ..
+    // workgroups. Workgroup b runs on XCD x = b % 8: its first xv work items (b / 8 < xv)
+    // are the halves of split tiles full + x*xv/2 .., the next xu whole tiles x*xu ..
     int full, xu, xv;
     int* sync;               // split tiles: [tiles][2] arrival counter and ready flag, all zero
     float* part;             // split tiles: [tiles][kPipeBM * kPipeBN] partial sums
@@ -143,20 +143,23 @@ struct PipeItem {
 };
 
 // Decodes workgroup blockIdx.x's work item; false when the grid's padding has none.
-// Each XCD walks a contiguous (m-major) range of whole tiles, then a contiguous range
-// of split tiles whose two K halves are neighbouring items of the same XCD.
+// Each XCD walks a contiguous range of split tiles, whose two K halves are neighbouring
+// items of the same XCD, then a contiguous (m-major) range of whole tiles. Split halves
+// go first: their hand-off (slot write, slot read, Y write) then overlaps the whole
+// tiles' MFMAs instead of being the launch's last, exposed burst of stores (measured at
+// M=2048, K=4096, 88 split and 256 whole tiles: 203.0-204.2 -> 194.4-195.1 us).
 __device__ __forceinline__ bool pipe_item(const PipeParams& p, PipeItem& it)
 {
     const int tiles = p.tiles_m * p.tiles_n;
     const int xcd = blockIdx.x % kXcds, xj = blockIdx.x / kXcds;
     int kpart;
-    if (xj < p.xu) {
-        it.tile = xcd * p.xu + xj;
+    if (xj >= p.xv) {
+        it.tile = xcd * p.xu + (xj - p.xv);
         kpart = 0;
         it.split = false;
         if (it.tile >= p.full) return false;
     } else {
-        const int q = xj - p.xu;
+        const int q = xj;
         it.tile = p.full + xcd * (p.xv >> 1) + (q >> 1);
         kpart = q & 1;
         it.split = true;
