@@ -546,12 +546,14 @@ def _captured_before_and_after_eager(w, a, ref, dA, dY, split_grid):
 
 
 
-def test_mfma_full_vs_torch_fp32(gpu):
-    """Every output of an M=2048 call against an fp32 product of the
-    (bit-exact) dequantized weights on the device."""
+@pytest.mark.parametrize("op", workloads.LLAMA7B_PREFILL_OPS, ids=lambda o: f"K{o.K}_N{o.N}")
+def test_mfma_full_vs_torch_fp32(gpu, op):
+    """Every output of an M=2048 call against an fp32 product of the (bit-exact)
+    dequantized weights on the device, on both 7B MLP shapes: the up shape's launch splits
+    its last round of tiles over two workgroups each, the down shape's splits every tile.
+    Two more calls return the same bits (the split hand-off is order-independent)."""
     import torch
     torch.backends.cuda.matmul.allow_tf32 = False
-    op = workloads.LLAMA7B_PREFILL_OPS[0]
     b, s, z, w = weights_for(op, seed=5)
     a = workloads.make_activations(2048, op.K, seed=6, kind="rmsnorm")
     dA = torch.from_numpy(a).cuda()
@@ -562,8 +564,13 @@ def test_mfma_full_vs_torch_fp32(gpu):
     w.dequant_dev(dW.data_ptr(), stream)
     ref = dA.double() @ dW.double().T
     rel = float(torch.linalg.norm(dY.double() - ref) / torch.linalg.norm(ref))
-    log(f"  mfma M=2048 full vs fp64 device product: rel Frobenius {rel:.3e}")
+    log(f"  mfma M=2048 K={op.K} N={op.N} {w.launch_info(2048)} full vs fp64 device product: rel Frobenius {rel:.3e}")
     assert rel <= MFMA_FRO
+    y0 = dY.clone()
+    for i in range(2):
+        w.gemm_dev(dA.data_ptr(), dY.data_ptr(), 2048, stream)
+        torch.cuda.synchronize()
+        assert torch.equal(dY, y0), i
     w.close()
 
 
