@@ -7,8 +7,9 @@ heads of dim 128; block size 32 with packed zero points). Weights, activations
 and outputs are resident in HBM before timing starts. Every step uses a
 different copy of the layer's weights, activations and outputs, rotating over
 enough copies to touch >= 1 GiB, so no op is served from the 256 MiB MALL.
-The steps are enqueued as a HIP graph (captured through torch's stream
-capture) and timed with HIP events on that stream.
+The steps are enqueued eagerly on one stream (--warmup untimed steps, then
+exactly --steps timed ones) and timed with HIP events on that stream; the same
+rotation replayed as a HIP graph is reported beside it.
 
 Prints one JSON line. value = algorithmic bytes per step / time per step
 (weights + fp32 A + fp32 Y, each once). Beside it:
@@ -16,8 +17,9 @@ Prints one JSON line. value = algorithmic bytes per step / time per step
                 mean launch time, against 8 TB/s;
   prefill       M=2048 on the Llama-2-7B MLP shapes (the MFMA kernel), TFLOP/s
                 against the 2.5 PFLOP/s dense fp16 peak;
-  cpu_baseline  the CPU oracle (a C restatement of the reference's managed
-                MatMulNBitsKernel) on the host cores, gate projection sample.
+  cpu_baseline  the CPU oracle (a C++-style C restatement of the reference's
+                managed MatMulNBitsKernel) on the host's cores and on one thread,
+                one bounded sample per workload; value = the 7B decode layer.
 """
 from __future__ import annotations
 
@@ -148,34 +150,94 @@ def measured_traffic(launch):
     return prof["traffic_bytes"] if same else None
 
 
-def cpu_baseline(op, budget_s):
-    import oracle
-    from modelsharp_amd import workloads
-    b, s, z = workloads.make_weights(op, 1234)
-    a = workloads.make_activations(1, op.K, 1235)
-    nthreads = oracle.threads()
-    oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, op.block_size, nthreads=nthreads)   # warm
+def cpu_description() -> dict:
+    """CPU model and the SIMD extensions the restatement can use (from /proc/cpuinfo)."""
+    model, flags = "unknown", set()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name") and model == "unknown":
+                model = line.split(":", 1)[1].strip()
+            elif line.startswith("flags") and not flags:
+                flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    isa = [f for f in ("avx2", "fma", "f16c", "avx512f", "avx512bw", "avx512vl", "avx512_vnni", "avx512_bf16")
+           if f in flags]
+    return {"model": model, "isa": isa, "threads_available": os.cpu_count()}
+
+
+def _time_calls(fn, budget_s):
+    """Calls fn() at least once and until budget_s has passed; returns (calls, seconds)."""
+    fn()   # warm
     calls, t0 = 0, time.perf_counter()
     while True:
-        oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, op.block_size, nthreads=nthreads)
+        fn()
         calls += 1
         el = time.perf_counter() - t0
         if el >= budget_s:
-            break
-    nbytes = workloads.algorithmic_bytes(op, 1)
-    out = {"value": round(nbytes * calls / el / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": "port",
-           "sample": f"{op.name} K={op.K} N={op.N} M=1 bs={op.block_size} zp, {calls} calls in {el:.1f} s "
-                     f"({el / calls * 1e3:.2f} ms/call), C restatement of the managed MatMulNBitsKernel "
-                     f"(column-parallel, {nthreads} threads)"}
-    ref = oracle.ref_lib()
-    if ref is not None:   # the reference's own native ms_qgemm_nbits, when it was built
-        oracle.ref_qgemm_nbits(a, b, s, z, 1, op.N, op.K, 4, op.block_size)
-        calls, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < budget_s / 2:
-            oracle.ref_qgemm_nbits(a, b, s, z, 1, op.N, op.K, 4, op.block_size)
-            calls += 1
-        el = time.perf_counter() - t0
-        out["reference_native_gbs"] = round(nbytes * calls / el / 1e9, 3)
+            return calls, el
+
+
+def cpu_baseline(budget_s):
+    """The oracle (kind "port": a C restatement of MatMulNBitsKernel.Execute's default
+    path, column-parallel over N as MatMulParallel.For) on every workload, on all the
+    host's cores and on one thread, each for a bounded sample of about budget_s / 10."""
+    import oracle
+    from modelsharp_amd import workloads
+    nthreads = oracle.threads()
+    per = max(0.2, budget_s / 10.0)
+
+    def decode_set(name, ops, M, seed, bs_note):
+        host = [workloads.make_weights(op, seed + i) for i, op in enumerate(ops)]
+        acts = [workloads.make_activations(M, op.K, seed + 50 + i) for i, op in enumerate(ops)]
+        nbytes = sum(workloads.algorithmic_bytes(op, M) for op in ops)
+
+        def run(nt):
+            for (b, s, z), a, op in zip(host, acts, ops):
+                oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, op.block_size, nthreads=nt)
+        row = {"workload": name, "sample": f"{'+'.join(op.name for op in ops)} at M={M}, {bs_note}",
+               "bytes_per_call": nbytes}
+        for nt, key in ((nthreads, "all_cores"), (1, "one_thread")):
+            calls, el = _time_calls(lambda: run(nt), per)
+            row[key] = {"threads": nt, "ms_per_call": round(el / calls * 1e3, 3),
+                        "GBs": round(nbytes * calls / el / 1e9, 3)}
+        return row
+
+    rows = []
+    rows.append(decode_set("qwen05b_up", [workloads.QWEN05B_UP], 1, 100, "K=896 N=4864 bs=32 zp"))
+    rows.append(decode_set("qwen05b_decode", workloads.QWEN05B_DECODE, 1, 200, "8 projections, bs=32 zp"))
+    rows.append(decode_set("7b_decode", workloads.DECODE_7B, 1, 300, "7 projections, bs=32 zp"))
+    for M in (1, 16):
+        rows.append(decode_set(f"llama7b_smallm_M{M}", workloads.LLAMA7B_SMALLM_OPS, M, 400,
+                               "bs=128, no zp"))
+    # prefill: M=2048 on a sample of output columns (the full call is ~10^2 s of CPU work)
+    op = workloads.LLAMA7B_PREFILL_OPS[0]
+    b, s, z = workloads.make_weights(op, 500)
+    a = workloads.make_activations(2048, op.K, 501, kind="rmsnorm")
+    prow = {"workload": "llama7b_prefill_M2048", "sample": f"M=2048 K={op.K}, bs=32 zp, output columns sampled"}
+    for nt, key, cols in ((nthreads, "all_cores", 512), (1, "one_thread", 32)):
+        bc, sc = b[:cols], s.reshape(op.N, -1)[:cols]
+        zc = None if z is None else z[:cols]
+        calls, el = _time_calls(lambda: oracle.matmul_nbits(a, bc, sc, zc, cols, op.K, 4, 32, nthreads=nt), per)
+        fl = 2.0 * 2048 * cols * op.K
+        prow[key] = {"threads": nt, "columns": cols, "ms_per_call": round(el / calls * 1e3, 3),
+                     "GFLOPs": round(fl * calls / el / 1e9, 3)}
+    rows.append(prow)
+
+    head = next(r for r in rows if r["workload"] == "7b_decode")
+    out = {"value": head["all_cores"]["GBs"], "unit": "GB/s", "cores": nthreads, "kind": "port",
+           "sample": f"7B decode layer ({head['sample']}), {head['all_cores']['ms_per_call']} ms per layer on "
+                     f"{nthreads} threads; C++-style restatement of the managed MatMulNBitsKernel (the reference's "
+                     f"C# runtime is not available), column-parallel like MatMulParallel.For",
+           "cpu": cpu_description(), "rows": rows}
+    if oracle.ref_lib() is not None:
+        # The reference's own native ms_qgemm_nbits (qgemm.cpp, built from its sources), on
+        # the 7B gate projection, all threads (its OpenMP default).
+        gate = next(o for o in workloads.DECODE_7B if o.name == "gate")
+        b, s, z = workloads.make_weights(gate, 600)
+        a = workloads.make_activations(1, gate.K, 601)
+        calls, el = _time_calls(lambda: oracle.ref_qgemm_nbits(a, b, s, z, 1, gate.N, gate.K, 4, 32), per)
+        out["reference_native_gate_GBs"] = round(workloads.algorithmic_bytes(gate, 1) * calls / el / 1e9, 3)
     return out
 
 
@@ -185,7 +247,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200, help="timed decode-layer steps")
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--rotate-mib", type=int, default=1024, help="bytes the weight rotation touches")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget (0 = skip)")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline budget (0 = skip)")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--detail", default="", help="also write per-op results of every workload to this JSON file")
     ap.add_argument("--op", default="", help="profiling mode: launch only this 7B decode op (q,k,v,o,gate,up,down), "
@@ -225,33 +287,36 @@ def main() -> int:
         for r in range(copies):
             rot.enqueue(r, stream)
 
-    g = graph_of(layer_rotation)
-    replays = max(1, math.ceil(args.steps / copies))
-    warm = max(1, math.ceil(args.warmup / copies))
-    ms_rot = time_graph(g, replays, warm, warm_ms=0)   # exactly the requested warmup steps
-    steps = replays * copies
-    ms_step = ms_rot / copies
+    # The headline: exactly --warmup untimed steps, then exactly --steps timed steps, each
+    # step one batch call over the next copy of the rotation, on one stream; HIP events on
+    # that stream around the timed steps, device synchronisation on both sides.
+    s = torch.cuda.current_stream().cuda_stream
+    steps, warm = max(1, args.steps), max(0, args.warmup)
+    for i in range(warm):
+        rot.enqueue(i % copies, s)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        rot.enqueue((warm + i) % copies, s)
+    e1.record()
+    e1.synchronize()
+    torch.cuda.synchronize()
+    ms_step = e0.elapsed_time(e1) / steps
     value = step_bytes / (ms_step * 1e-3) / 1e9
-    log(f"graph: {ms_step * 1e3:.2f} us/step  {value:.1f} GB/s")
+    log(f"{steps} steps: {ms_step * 1e3:.2f} us/step  {value:.1f} GB/s")
+
+    # the same rotation replayed as a HIP graph
+    g = graph_of(layer_rotation)
+    replays = max(2, math.ceil(200 / copies))
+    ms_step_graph = time_graph(g, replays, 2) / copies
+    log(f"graph: {ms_step_graph * 1e3:.2f} us/step")
 
     # the same step with every op in a launch of its own (no grouping of shared inputs)
     gu = graph_of(lambda stream: [rot.enqueue(r, stream, only=i) for r in range(copies) for i in range(len(ops))])
     ms_step_ungrouped = time_graph(gu, replays, warm) / copies
     log(f"ungrouped: {ms_step_ungrouped * 1e3:.2f} us/step  {step_bytes / (ms_step_ungrouped * 1e-3) / 1e9:.1f} GB/s")
     del gu
-
-    # eager launches (no graph) for comparison
-    torch.cuda.synchronize()
-    s = torch.cuda.current_stream().cuda_stream
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    for r in range(copies):
-        rot.enqueue(r, s)
-    e0.record()
-    for i in range(steps):
-        rot.enqueue(i % copies, s)
-    e1.record()
-    e1.synchronize()
-    ms_step_eager = e0.elapsed_time(e1) / steps
 
     # per-op launch times (graph of one op over all copies)
     per_op = {}
@@ -280,7 +345,8 @@ def main() -> int:
     gate = next(op for op in ops if op.name == "gate")   # the CPU baseline's sample
 
     # host-pointer entry (ms_hip_nbits_gemm): H2D of A, the kernel, D2H of Y, synchronous,
-    # pageable host buffers; rotating over the weight copies. Reported, never `value`.
+    # through the handle's pinned staging; rotating over the weight copies. Reported,
+    # never `value`.
     gi = ops.index(gate)
     a_host = workloads.make_activations(1, gate.K, 99)
     for r in range(copies):
@@ -292,7 +358,8 @@ def main() -> int:
     host_us = (time.perf_counter() - t0) / calls * 1e6
     host = {"op": "gate", "K": gate.K, "N": gate.N, "M": 1, "us_per_call": round(host_us, 2),
             "GBs": round(workloads.algorithmic_bytes(gate, 1) / (host_us * 1e-6) / 1e9, 1),
-            "path": "ms_hip_nbits_gemm: H2D A + kernel + D2H Y, synchronous, pageable host buffers"}
+            "path": "ms_hip_nbits_gemm: host A -> pinned staging -> H2D, kernel, D2H -> pinned -> host Y, "
+                    "synchronous"}
     log(f"  host-pointer gate call: {host_us:.2f} us ({host['GBs']} GB/s, PCIe copies included)")
     traffic = measured_traffic(dom["kernel"])
     rot.close()
@@ -301,12 +368,12 @@ def main() -> int:
 
     result = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps,
-        "warmup": warm * copies, "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak",
+        "warmup": warm, "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": "7b_decode_layer", "ops": {op.name: [op.K, op.N] for op in ops}, "M": 1,
                    "bits": 4, "block_size": 32, "zero_points": "packed uint4", "rotating_copies": copies,
-                   "bytes_per_step": step_bytes, "timing": "HIP graph of the rotation, HIP events"},
-        "ms_per_step_eager": round(ms_step_eager, 5),
+                   "bytes_per_step": step_bytes, "timing": "eager batch calls on one stream, HIP events"},
+        "ms_per_step_graph": round(ms_step_graph, 5),
         "ms_per_step_ungrouped": round(ms_step_ungrouped, 5),
         "per_op": per_op,
         "groups": groups,
@@ -365,7 +432,7 @@ def main() -> int:
 
     if args.cpu_seconds > 0:
         log("cpu baseline ...")
-        result["cpu_baseline"] = cpu_baseline(gate, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     else:
         result["cpu_baseline"] = None
 

@@ -19,9 +19,12 @@
  *     ms_hip_last_error() (thread-local) holds the message and outputs are
  *     untouched;
  *   - add functions rather than change signatures.
- * Threading: every entry may be called from any host thread. A weights handle
- * is immutable after creation; the synchronous host-pointer entries serialise
- * per handle. Device-pointer entries enqueue on the caller's stream.
+ * Threading: every entry may be called from any host thread. A weights handle's
+ * weights are immutable after creation; the synchronous host-pointer entries
+ * serialise per handle. Device-pointer entries enqueue on the caller's stream.
+ * A handle stays valid until ms_hip_nbits_weights_destroy; entries given any
+ * other pointer (a destroyed handle included) return MS_HIP_ERR_INVALID. Destroying
+ * a handle while another thread is calling with it is not allowed.
  */
 #ifndef MS_HIP_KERNELS_H
 #define MS_HIP_KERNELS_H
@@ -36,6 +39,9 @@ extern "C" {
 #define MS_HIP_ERR_NO_DEVICE    2  /* no usable gfx950 device                */
 #define MS_HIP_ERR_HIP          3  /* a HIP runtime call failed              */
 #define MS_HIP_ERR_UNSUPPORTED  4  /* valid operator input this ABI cannot take */
+
+/* ms_hip_nbits_set_tuning value: the handle follows the process default again. */
+#define MS_HIP_TUNING_INHERIT   (-2147483647 - 1)
 
 /* ---- capability / diagnostics ---------------------------------------------
  * Replace ms_build_info / ms_has_avx512 / ms_has_vnni
@@ -83,20 +89,31 @@ int ms_hip_nbits_weights_info(void* handle, int* N, int* K, int* bits, int* bloc
  * path NativeQuant.TryMatMulNBits (NativeQuant.cs:78-115) takes from
  * MatMulNBitsKernel.Execute (MatMulNBitsKernel.cs:174-191), with the weights
  * already resident. M<=16 runs the dequant-fused GEMV (block size 128 and
- * 3 <= M <= 16: its matrix-core form at the same accuracy), larger M the MFMA GEMM. */
+ * 3 <= M <= 16: its matrix-core form at the same accuracy), larger M the MFMA GEMM.
+ * A and Y go through pinned staging buffers owned by the handle. */
 int ms_hip_nbits_gemm(void* handle, const float* a_host, float* y_host, int M);
 
 /* Device-pointer form: enqueues on `stream` (a hipStream_t, NULL = the null
  * stream) and returns without synchronising. dA: [M,K] fp32, dY: [M,N] fp32,
  * both 16-byte aligned device memory. Prefill calls (M > 16) stage A as fp16 in
- * a workspace owned by the handle, and launches with few output tiles split K over
- * two workgroups per tile that meet through the handle's per-tile counters and
- * partial-sum slots; the small-M matrix-core kernel splits K over several
- * workgroups per 128-row tile the same way. These buffers grow on demand, never
- * while `stream` is being captured (a call under capture that would need larger
- * ones takes a workspace-free kernel instead), so such calls on one handle from
- * different streams must not overlap. */
+ * a workspace owned by the handle (each row scaled by an exact power of two), and
+ * launches with few output tiles split K over two workgroups per tile that meet
+ * through the handle's per-tile counters and partial-sum slots; the small-M
+ * matrix-core kernel splits K over several workgroups per 128-row tile the same
+ * way. These buffers grow on demand, never while `stream` is being captured (a
+ * call under capture that would need larger ones takes a workspace-free kernel
+ * instead), so such calls on one handle from different streams must not overlap.
+ * If they do, or a hand-off between the two halves of a split tile does not
+ * complete within its bound, the kernel records it in the handle's error word and
+ * the output of that call is not valid: the next call on the handle (or
+ * ms_hip_nbits_device_error) returns MS_HIP_ERR_HIP and clears the record. */
 int ms_hip_nbits_gemm_dev(void* handle, const float* dA, float* dY, int M, void* stream);
+
+/* The device-side failure recorded for this handle since the last check (see
+ * ms_hip_nbits_gemm_dev): MS_HIP_ERR_HIP with its message, or MS_HIP_OK. Clears
+ * the record. Synchronise the streams of earlier calls first. No counterpart in
+ * the reference (its native calls are synchronous). */
+int ms_hip_nbits_device_error(void* handle);
 
 /* Enqueues `count` device-pointer calls back to back on `stream`, call i on
  * handles[i] with dA[i], dY[i] (all with the same M). For callers that chain
@@ -129,10 +146,14 @@ int ms_hip_download(void* host, const void* dptr, int64_t bytes);
 int ms_hip_sync(void);
 
 /* ---- measurement support ---------------------------------------------------
- * No counterpart in the reference; for launch-shape sweeps. Process-wide.
+ * No counterpart in the reference; for launch-shape sweeps and tests.
+ * ms_hip_set_tuning sets a process-wide default, ms_hip_nbits_set_tuning one
+ * handle's own value (MS_HIP_TUNING_INHERIT: follow the default again); a call
+ * reads its handle's knobs once, so a sweep on one handle cannot change the kernel
+ * another handle's calls take.
  * ms_hip_set_gemv_lanes: lanes per weight row of the gemv_w4_panel kernel
  *   (16, 32 or 64; 0 restores the shape heuristic) — the same as knob 0 below.
- * ms_hip_set_tuning knobs (value 0 restores the heuristic):
+ * Knobs (value 0 restores the heuristic):
  *   0 gemv_w4_panel lanes per row;
  *   1 gemv_w4 launch configuration: c+1 forces configuration c of the library's
  *     table (used only where it fits the shape), -1 forces gemv_w4_panel;
@@ -145,7 +166,14 @@ int ms_hip_sync(void);
  *     [ceil(K / 512), K / 128]);
  *   6 1 keeps M > 16 off the register-operand prefill kernel, 2 sends every eligible
  *     M > 16 to it;
- *   7 its K split (workgroups per 128 x 256 tile, 1..64, clamped to K / 128).
+ *   7 its K split (workgroups per 128 x 256 tile, 1..64, clamped to K / 128);
+ *   8 polls of the pipelined prefill's split-K flag before the second half of a
+ *     tile gives up (0: about 4 million).
+ * ms_hip_nbits_debug_set_counters sets the arrival tag of every split tile of the
+ *   handle's pipelined-prefill counters to `value` (or to the tag the next split-K
+ *   launch will carry, when next_epoch_tag != 0) and clears their ready flags: it
+ *   makes the overlap and time-out reports of ms_hip_nbits_gemm_dev testable with
+ *   every kernel still exiting normally.
  * ms_hip_nbits_launch_info reports what a call with M rows would launch:
  *   kernel_id 0 generic, 1 gemv_w4, 2 mfma_w4, 3 gemv_w4_panel, 4 mfma_w4_pipe,
  *   5 skinny_w4, 6 mfma_w4_rb. */
@@ -156,6 +184,8 @@ int ms_hip_nbits_batch_launch_info(void* const* handles, const float* const* dA,
                                    int* calls, int* kernel_id, int* lanes_per_row, int* grid, int* block);
 int ms_hip_set_gemv_lanes(int lanes_per_row);
 int ms_hip_set_tuning(int knob, int value);
+int ms_hip_nbits_set_tuning(void* handle, int knob, int value);
+int ms_hip_nbits_debug_set_counters(void* handle, int value, int next_epoch_tag);
 int ms_hip_nbits_launch_info(void* handle, int M, int* kernel_id, int* lanes_per_row,
                              int* grid, int* block);
 

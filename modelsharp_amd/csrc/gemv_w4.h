@@ -9,7 +9,7 @@
 //     wave-wide code load reads R contiguous segments of G*16 bytes of packed B
 //     in the reference layout B[n][K/2].
 //   * The whole activation panel A[0..M)[0..K) is staged once per workgroup in
-//     LDS (pre-scaled, plus per-chunk sums; kChunkStride4 float4 per chunk).
+//     LDS (odd k pre-divided by 16; kChunkStride4 float4 per chunk).
 //   * Load order is the design: every vector-memory load returns in issue order,
 //     so the activation loads go first, then two batches of U steps of codes,
 //     scales and zero points, and only then is A written to LDS. The staging
@@ -22,14 +22,16 @@
 //   * End: the G partial sums of a row meet in a butterfly over the G lanes,
 //     the KW wave partials in LDS (fixed orders: deterministic); one lane stores.
 // Arithmetic per chunk (32 codes q_k, zero point zp, scale s):
-//   A code in the low mantissa bits of an fp16 lane is the exact subnormal
-//   q * 2^-24 (code bits 0-3) or 16q * 2^-24 (bits 4-7). With the activations
-//   staged times 2^24 (even k) and 2^20 (odd k) — exact powers of two — one
-//   v_fma_mix_f32 adds exactly a_k * q_k. Per activation row m,
-//       blk = sum_k a_k q_k - zp * sum_k a_k,   acc += s * blk,
-//   i.e. sum_k a_k (q_k - zp) s: the dot product with the dequantized weights
-//   W = (q - zp) s, folded per block. For M <= 2 the 32 products go into two
-//   partial sums (shorter dependency chains).
+//   A code masked into the mantissa of the fp16 1024.0 reads as 1024 + q (code bits
+//   0-3) or 1024 + 16q (bits 4-7); one packed subtract of 1024 + zp (resp.
+//   1024 + 16 zp) leaves q - zp (resp. 16 (q - zp)) exactly. With the activations
+//   staged as a_k (even k) and a_k / 16 (odd k) — exact powers of two — one
+//   v_fma_mix_f32 adds exactly a_k (q_k - zp) into an fp32 sum. Per activation row m,
+//       blk = sum_k a_k (q_k - zp),   acc += s * blk,
+//   the dot product with the dequantized weights W = (q - zp) s with the scale applied
+//   once per block: the reference's sum in another order, with no cancelling terms
+//   (its error stays within eps * sum_k |a_k (q_k - zp) s|). For M <= 2 the 32
+//   products go into two partial sums (shorter dependency chains).
 // HBM traffic is the algorithmic minimum: every byte of B, scales and zero
 // points is read once; A is read once per workgroup (L2-resident).
 #pragma once
@@ -160,20 +162,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
     load(bB, U);
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- 3. stage A: pre-scaled activations and chunk sums ------------------------------
+    // ---- 3. stage A: odd k divided by 16 (exact), matching 16 (q - zp) of the dequant ----
     if (idx < na) {
         float4* dst = &lds_a4[idx * kChunkStride4];
-        float sum = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float4 v = av[j];
-            sum += v.x;
-            sum += v.y;
-            sum += v.z;
-            sum += v.w;
-            dst[j] = float4{v.x * kTwo24, v.y * kTwo20, v.z * kTwo24, v.w * kTwo20};
-        }
-        dst[8] = float4{sum, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < 8; ++j) dst[j] = stage_odd16(av[j]);
     }
     __syncthreads();
 
@@ -203,30 +196,34 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
                         for (int q = 0; q < NP; ++q) t[j][m][q] = 0.0f;
                     }
                 }
+                h2_t zb[RL], zb16[RL];
+#pragma unroll
+                for (int j = 0; j < RL; ++j) {
+                    const uint32_t zp = ozp ? (bt.z[j][u] >> zshift) & 0x0Fu : 8u;
+                    zb[j] = zp_half2(zp);
+                    zb16[j] = zp16_half2(zp);
+                }
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
                     uint32_t pr[RL][4];
 #pragma unroll
                     for (int j = 0; j < RL; ++j) {
                         const uint32_t qd = d == 0 ? bt.q[j][u].x : d == 1 ? bt.q[j][u].y : d == 2 ? bt.q[j][u].z : bt.q[j][u].w;
-                        code_pairs(qd, pr[j]);
+                        diffs8(qd, zb[j], zb16[j], pr[j]);
                     }
 #pragma unroll
                     for (int m = 0; m < M; ++m) {
                         const float4* arow = &lds_a4[(m * C + c) * kChunkStride4];
                         const float4 a0 = arow[2 * d], a1 = arow[2 * d + 1];
 #pragma unroll
-                        for (int j = 0; j < RL; ++j) t[j][m][d % NP] = qdot8(pr[j], a0, a1, t[j][m][d % NP]);
+                        for (int j = 0; j < RL; ++j) t[j][m][d % NP] = dot8(pr[j], a0, a1, t[j][m][d % NP]);
                     }
                 }
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
-                    const float asum = lds_a4[(m * C + c) * kChunkStride4 + 8].x;
 #pragma unroll
                     for (int j = 0; j < RL; ++j) {
-                        float blkacc = NP == 2 ? t[j][m][0] + t[j][m][NP - 1] : t[j][m][0];
-                        const float zpf = ozp ? (float)((bt.z[j][u] >> zshift) & 0x0F) : 8.0f;
-                        blkacc = __builtin_fmaf(-zpf, asum, blkacc);
+                        const float blkacc = NP == 2 ? t[j][m][0] + t[j][m][NP - 1] : t[j][m][0];
                         acc[j][m] = __builtin_fmaf(bt.s[j][u], blkacc, acc[j][m]);
                     }
                 }

@@ -10,24 +10,22 @@
 //     B[n][K/2]. Codes, scales and zero points are read with buffer loads
 //     (32-bit offsets off one scalar resource each).
 //   * The activation slice A[0..M)[panel] is staged once per workgroup in LDS:
-//     a chunk is 32 activations, pre-scaled as below, plus their plain sum in a
-//     ninth float4 (which also pads the chunk stride so that the G distinct
-//     chunk addresses of one wave-wide read fall on different banks). Lanes
-//     with the same chunk index read the same address.
+//     a chunk is 32 activations, pre-scaled as below, in 8 float4 plus one float4 of
+//     padding (so that the G distinct chunk addresses of one wave-wide read fall on
+//     different banks). Lanes with the same chunk index read the same address.
 //   * Weight loads are software-pipelined in two ping-pong batches of U chunks:
 //     one batch is in flight while the other is reduced. The first batch is
 //     issued before A is staged, so the two latencies overlap.
 //   * End: the G partial sums of a row are combined with a butterfly over the
 //     G lanes (fixed order: deterministic); lane 0 of the row stores Y.
-// Arithmetic per chunk (32 codes q_k, zero point zp, scale s):
-//   A code in the low mantissa bits of an fp16 lane is the exact subnormal
-//   q * 2^-24 (code bits 0-3) or 16q * 2^-24 (bits 4-7). With the activations
-//   staged times 2^24 (even k) and 2^20 (odd k) — exact powers of two — one
-//   v_fma_mix_f32 adds exactly a_k * q_k. Per row m,
-//       blk = sum_k a_k q_k - zp * sum_k a_k,   acc += s * blk,
-//   i.e. sum_k a_k (q_k - zp) s: the dot product with the dequantized weights
-//   W = (q - zp) s, folded per block. The code masks (5 ops per 8 codes) are
-//   shared by the M rows; each row costs one fma per code plus two per chunk.
+// Arithmetic per chunk (32 codes q_k, zero point zp, scale s), as in gemv_w4.h:
+//   the packed-half dequant leaves q_k - zp (even k) and 16 (q_k - zp) (odd k) exactly
+//   in fp16, the activations are staged as a_k and a_k / 16, and one v_fma_mix_f32 per
+//   code adds a_k (q_k - zp) exactly into an fp32 sum. Per row m,
+//       blk = sum_k a_k (q_k - zp),   acc += s * blk,
+//   the reference's dot product with the scale applied once per block, with no
+//   cancelling terms. The differences (9 ops per 8 codes) are shared by the M rows;
+//   each row costs one fma per code plus one per chunk.
 // HBM traffic is the algorithmic minimum: every byte of B, scales and zero
 // points is read once; A is read once per workgroup (L2-resident).
 #pragma once
@@ -110,17 +108,8 @@ __global__ __launch_bounds__(kPanelThreads) void gemv_w4_panel_kernel(GemvPanelP
             const int cc = idx - m * pc;
             const float4* src = reinterpret_cast<const float4*>(p.a + (int64_t)m * p.K + (int64_t)(c0 + cc) * 32);
             float4* dst = &lds_a4[(m * P + cc) * kChunkStride4];
-            float sum = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float4 v = src[j];
-                sum += v.x;
-                sum += v.y;
-                sum += v.z;
-                sum += v.w;
-                dst[j] = float4{v.x * kTwo24, v.y * kTwo20, v.z * kTwo24, v.w * kTwo20};
-            }
-            dst[8] = float4{sum, 0.0f, 0.0f, 0.0f};
+            for (int j = 0; j < 8; ++j) dst[j] = stage_odd16(src[j]);
         }
         __syncthreads();
 
@@ -130,18 +119,17 @@ __global__ __launch_bounds__(kPanelThreads) void gemv_w4_panel_kernel(GemvPanelP
                 if (k0 + u < nk) {
                     const int cc = g + G * (k0 + u);
                     const int blk = (c0 + cc) >> p.log2cpb;
-                    const float zpf = (float)((bt.z[u] >> ((blk & 1) * 4)) & 0x0F);
+                    const uint32_t zp = ((uint32_t)bt.z[u] >> ((blk & 1) * 4)) & 0x0Fu;
                     const uint32_t qd[4] = {bt.q[u].x, bt.q[u].y, bt.q[u].z, bt.q[u].w};
                     uint32_t pr[4][4];
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) code_pairs(qd[j], pr[j]);
+                    for (int j = 0; j < 4; ++j) diffs8(qd[j], zp_half2(zp), zp16_half2(zp), pr[j]);
 #pragma unroll
                     for (int m = 0; m < M; ++m) {
                         const float4* arow = &lds_a4[(m * P + cc) * kChunkStride4];
                         float blkacc = 0.0f;
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) blkacc = qdot8(pr[j], arow[2 * j], arow[2 * j + 1], blkacc);
-                        blkacc = __builtin_fmaf(-zpf, arow[8].x, blkacc);
+                        for (int j = 0; j < 4; ++j) blkacc = dot8(pr[j], arow[2 * j], arow[2 * j + 1], blkacc);
                         acc[m] = __builtin_fmaf(bt.s[u], blkacc, acc[m]);
                     }
                 }

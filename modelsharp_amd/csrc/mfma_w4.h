@@ -1,26 +1,35 @@
-// mfma_w4.h — INT4 MatMulNBits GEMM on the CDNA4 matrix cores (M > 16, the
-// prefill path).
+// mfma_w4.h — INT4 MatMulNBits GEMM on the CDNA4 matrix cores (M > 16), the general
+// form: any power-of-two block size from 32 to 256, K a multiple of 32, any fp32 scales,
+// no workspace. At fp32-level accuracy, like the small-M GEMV:
+//   Y[m][n] = 2^e[m] * sum_b s[n][b] * sum_{k in b} (hi + lo)[m][k] * (q[n][k] - zp[n][b])
+// with
+//   * q - zp a small integer, exact in fp16 (packed-half dequant without the scale);
+//   * A split per row into A = 2^e (hi + lo), hi = fp16(A 2^-e), lo = fp16(A 2^-e - hi),
+//     e chosen so the row's max |A| 2^-e lies in [2^14, 2^15): every product
+//     hi (q - zp), lo (q - zp) is exact in fp32, and hi + lo carries A to about 2^-22
+//     of its row's max (no fp16 overflow for any finite A);
+//   * the block sums (fp32, accumulated by the MFMAs) times s in fp32, added to the
+//     running sum once per block; the row's 2^e at the end (exact).
+// So no input range turns into inf or NaN that the fp32 reference would not produce:
+// the library sends here the weights whose scales the fp16 kernels cannot carry, the
+// block sizes and K they do not take, and calls that find no workspace.
 //
-// Y[M,N] = A[M,K] * W[N,K]^T with W dequantized in-kernel:
-//   * A workgroup owns a (4*WM) x BN tile of Y: 4 waves stacked along M, each
-//     wave WM x BN as (WM/32) x (BN/32) v_mfma_f32_32x32x16_f16 fragments with
-//     fp32 accumulators. K advances 32 codes (one 16-byte chunk per weight
-//     row) per step.
-//   * Producer: the 256 threads dequantize the step's BN x 32 weight tile —
-//     each thread 32*BN/256 codes of one row, exactly in fp32
-//     (W = (q - zp) * s, nbits_device.h dequant8), rounded once to fp16 — into a
-//     double-buffered LDS tile Bs[BN][32 (+8 pad)]: one barrier per step. The
-//     next step's codes, scales and zero points are loaded before the current
-//     step's MFMAs are issued.
-//   * Consumer: each wave loads its A rows straight from global memory in the
-//     MFMA operand layout (8 consecutive k per lane), one step ahead, and rounds
-//     them to fp16 in registers; weight fragments come from LDS.
-//   * Tile order is XCD-aware: workgroups are dealt round-robin to the 8 XCDs,
-//     so tile t goes to XCD t % 8; tiles are numbered so that each XCD walks a
-//     contiguous m-major range of tiles, and the CUs of one XCD share the same
-//     A row panel in their L2.
-// Numerics: A and W each carry one fp16 rounding (relative 2^-11); products
-// are exact and sums fp32.
+// Work mapping:
+//   * A workgroup owns a (4*WM) x BN tile of Y: 4 waves stacked along M, each wave
+//     WM x BN as (WM/32) x (BN/32) v_mfma_f32_32x32x16_f16 fragments; K advances 32
+//     codes (one 16-byte chunk per weight row) per step.
+//   * Prologue: each wave reads its A rows once for their max |A| (lanes l and l + 32
+//     share a row), and the exponents go to LDS for the epilogue.
+//   * Producer: the 256 threads turn the step's BN x 32 codes into q - zp (fp16, exact)
+//     in a double-buffered LDS tile, and the block's scales into an LDS row. The next
+//     step's codes, scales and zero points are loaded before the current step's MFMAs.
+//   * Consumer: each wave loads its A rows straight from global memory in the MFMA
+//     operand layout (8 consecutive k per lane), one step ahead, and splits them into
+//     hi / lo in registers; both operands carry the same permutation of each 8-k group
+//     (k0,k4,k1,k5,k2,k6,k3,k7: the order in which one dword of codes dequantizes).
+//   * Tile order is XCD-aware: workgroups are dealt round-robin to the 8 XCDs, so
+//     tile t goes to XCD t % 8; tiles are numbered so that each XCD walks a contiguous
+//     m-major range of tiles, and the CUs of one XCD share the same A row panel in L2.
 #pragma once
 #include <cmath>
 
@@ -57,6 +66,19 @@ __device__ __forceinline__ int xcd_tile(int bid, int tiles)
     return (bid % kXcds) * per + bid / kXcds;
 }
 
+// hi / lo halves of 8 activations times 2^-e, in the order k0,k4,k1,k5,k2,k6,k3,k7.
+__device__ __forceinline__ void split8(const float4& x03, const float4& x47, int e, half8_t& hi, half8_t& lo)
+{
+    const float v[8] = {x03.x, x47.x, x03.y, x47.y, x03.z, x47.z, x03.w, x47.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float x = __builtin_amdgcn_ldexpf(v[i], -e);
+        const _Float16 h = (_Float16)x;
+        hi[i] = h;
+        lo[i] = (_Float16)(x - (float)h);
+    }
+}
+
 template <int WM, int BN>
 __global__ __launch_bounds__(kMfmaThreads) void mfma_w4_kernel(MfmaParams p)
 {
@@ -67,6 +89,8 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_w4_kernel(MfmaParams p)
     constexpr int TPR = 32 / CPT;                 // producer threads per weight row
     static_assert(CPT == 8 || CPT == 16 || CPT == 32, "BN must be 64, 128 or 256");
     __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN][kBsStride];
+    __shared__ float Ss[2][BN];
+    __shared__ int Es[BM];
 
     const int tile = xcd_tile(blockIdx.x, p.tiles_m * p.tiles_n);
     if (tile >= p.tiles_m * p.tiles_n) return;
@@ -76,6 +100,7 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_w4_kernel(MfmaParams p)
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
+    const int cpb = 1 << p.log2cpb;           // steps per quantization block
 
     // ---- producer: row pn, codes [ph*CPT, ph*CPT + CPT) of each 32-code chunk --------
     const int pn = tid / TPR;
@@ -92,12 +117,51 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_w4_kernel(MfmaParams p)
         const int am = min(m0 + wave * WM + 32 * i + (lane & 31), p.M - 1);
         pa[i] = p.a + (int64_t)am * p.K + 8 * (lane >> 5);
     }
+    // A for step t: fragment i, k-substep s -> 8 floats
+    auto load_a = [&](int t, float4 (&f)[MF][4]) {
+#pragma unroll
+        for (int i = 0; i < MF; ++i) {
+            const float* src = pa[i] + (int64_t)t * 32;
+            f[i][0] = *reinterpret_cast<const float4*>(src);
+            f[i][1] = *reinterpret_cast<const float4*>(src + 4);
+            f[i][2] = *reinterpret_cast<const float4*>(src + 16);
+            f[i][3] = *reinterpret_cast<const float4*>(src + 20);
+        }
+    };
 
-    floatx16_t acc[MF][NF];
+    // ---- prologue: row exponents (lanes l and l + 32 read the two halves of each row) ---
+    int ea[MF];
+    {
+        float mx[MF];
+#pragma unroll
+        for (int i = 0; i < MF; ++i) mx[i] = 0.0f;
+        for (int t = 0; t < p.C; ++t) {
+            float4 f[MF][4];
+            load_a(t, f);
+#pragma unroll
+            for (int i = 0; i < MF; ++i) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    mx[i] = fmaxf(mx[i], fmaxf(fmaxf(fabsf(f[i][q].x), fabsf(f[i][q].y)),
+                                               fmaxf(fabsf(f[i][q].z), fabsf(f[i][q].w))));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < MF; ++i) {
+            const float m = fmaxf(mx[i], __shfl_xor(mx[i], 32));
+            ea[i] = (m > 0.0f && m <= 3.402823466e38f) ? __builtin_amdgcn_frexp_expf(m) - 15 : 0;
+            if (lane < 32) Es[wave * WM + 32 * i + lane] = ea[i];
+        }
+    }
+
+    floatx16_t acc[MF][NF], blk[MF][NF];
 #pragma unroll
     for (int i = 0; i < MF; ++i)
 #pragma unroll
-        for (int j = 0; j < NF; ++j) acc[i][j] = floatx16_t{};
+        for (int j = 0; j < NF; ++j) {
+            acc[i][j] = floatx16_t{};
+            blk[i][j] = floatx16_t{};
+        }
 
     struct Codes {
         uint32_t q[CPT / 8];
@@ -115,32 +179,24 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_w4_kernel(MfmaParams p)
         } else {
             c.q[0] = *reinterpret_cast<const uint32_t*>(src);
         }
-        const int blk = t >> p.log2cpb;
-        c.s = ps[blk];
-        c.z = pz ? zp_nibble(pz, blk) : 8;
+        const int bk = t >> p.log2cpb;
+        c.s = ps[bk];
+        c.z = pz ? zp_nibble(pz, bk) : 8;
     };
+    // q - zp for the producer's codes, exact in fp16, each dword in the order
+    // (k0,k4),(k1,k5),(k2,k6),(k3,k7).
     auto store_b = [&](int buf, const Codes& c) {
-        const BlockDq dq = block_dq(c.z, c.s);
+        const h2_t zb = as_h2(kHalfMagic | ((uint32_t)c.z << 16) | (uint32_t)c.z);
 #pragma unroll
         for (int w8 = 0; w8 < CPT / 8; ++w8) {
-            float w[8];
-            dequant8(c.q[w8], dq, w);
-            half8_t h;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) h[e] = (_Float16)w[e];
-            *reinterpret_cast<half8_t*>(&Bs[buf][pn][ph * CPT + 8 * w8]) = h;
+            const uint32_t x = c.q[w8];
+            const u32x4_t d{as_u32(as_h2(and_or(x, 0x000F000Fu, kHalfMagic)) - zb),
+                            as_u32(as_h2(and_or(x >> 4, 0x000F000Fu, kHalfMagic)) - zb),
+                            as_u32(as_h2(and_or(x >> 8, 0x000F000Fu, kHalfMagic)) - zb),
+                            as_u32(as_h2(and_or(x >> 12, 0x000F000Fu, kHalfMagic)) - zb)};
+            *reinterpret_cast<u32x4_t*>(&Bs[buf][pn][ph * CPT + 8 * w8]) = d;
         }
-    };
-    // A for step t: fragment i, k-substep s -> 8 floats
-    auto load_a = [&](int t, float4 (&f)[MF][4]) {
-#pragma unroll
-        for (int i = 0; i < MF; ++i) {
-            const float* src = pa[i] + (int64_t)t * 32;
-            f[i][0] = *reinterpret_cast<const float4*>(src);
-            f[i][1] = *reinterpret_cast<const float4*>(src + 4);
-            f[i][2] = *reinterpret_cast<const float4*>(src + 16);
-            f[i][3] = *reinterpret_cast<const float4*>(src + 20);
-        }
+        if (ph == 0) Ss[buf][pn] = c.s;
     };
 
     Codes cn;
@@ -155,15 +211,11 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_w4_kernel(MfmaParams p)
         const bool more = t + 1 < p.C;
         if (more) load_b(t + 1, cn);
 
-        half8_t ah[MF][2];
+        half8_t ah[MF][2], al[MF][2];
 #pragma unroll
         for (int i = 0; i < MF; ++i) {
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                const float4 lo = fa[i][2 * s], hi = fa[i][2 * s + 1];
-                ah[i][s] = half8_t{(_Float16)lo.x, (_Float16)lo.y, (_Float16)lo.z, (_Float16)lo.w,
-                                   (_Float16)hi.x, (_Float16)hi.y, (_Float16)hi.z, (_Float16)hi.w};
-            }
+            for (int s = 0; s < 2; ++s) split8(fa[i][2 * s], fa[i][2 * s + 1], ea[i], ah[i][s], al[i][s]);
         }
         if (more) load_a(t + 1, fa);
 
@@ -174,8 +226,25 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_w4_kernel(MfmaParams p)
             const half8_t b1 = *reinterpret_cast<const half8_t*>(brow + 16);
 #pragma unroll
             for (int i = 0; i < MF; ++i) {
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][0], b0, acc[i][j], 0, 0, 0);
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][1], b1, acc[i][j], 0, 0, 0);
+                blk[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][0], b0, blk[i][j], 0, 0, 0);
+                blk[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][1], b1, blk[i][j], 0, 0, 0);
+                blk[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][0], b0, blk[i][j], 0, 0, 0);
+                blk[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][1], b1, blk[i][j], 0, 0, 0);
+            }
+        }
+        // End of a quantization block (or of K, inside a partial last block): the block
+        // sums times the scale of their column (lane % 32 of fragment j), into the
+        // running sums.
+        if (((t + 1) & (cpb - 1)) == 0 || !more) {
+#pragma unroll
+            for (int j = 0; j < NF; ++j) {
+                const float sc = Ss[buf][32 * j + (lane & 31)];
+#pragma unroll
+                for (int i = 0; i < MF; ++i) {
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) acc[i][j][v] = __builtin_fmaf(blk[i][j][v], sc, acc[i][j][v]);
+                    blk[i][j] = floatx16_t{};
+                }
             }
         }
 
@@ -183,19 +252,20 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_w4_kernel(MfmaParams p)
         __syncthreads();
     }
 
-    // ---- epilogue: acc[i][j][v] is Y[row][col], col = lane % 32 and
+    // ---- epilogue: acc[i][j][v] is Y[row][col] / 2^Es[row], col = lane % 32 and
     //      row = 8*(v/4) + 4*(lane/32) + v%4 within fragment (i, j).
 #pragma unroll
     for (int i = 0; i < MF; ++i) {
-        const int mrow0 = m0 + wave * WM + 32 * i + 4 * (lane >> 5);
+        const int r0 = wave * WM + 32 * i + 4 * (lane >> 5);
 #pragma unroll
         for (int j = 0; j < NF; ++j) {
             const int col = n0 + 32 * j + (lane & 31);
             if (col < p.N) {
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
-                    const int row = mrow0 + 8 * (v >> 2) + (v & 3);
-                    if (row < p.M) p.y[(int64_t)row * p.N + col] = acc[i][j][v];
+                    const int r = r0 + 8 * (v >> 2) + (v & 3);
+                    const int row = m0 + r;
+                    if (row < p.M) p.y[(int64_t)row * p.N + col] = __builtin_amdgcn_ldexpf(acc[i][j][v], Es[r]);
                 }
             }
         }

@@ -5,11 +5,15 @@
 // Y[M,N] = A[M,K] * W[N,K]^T, W = (q - zp) * s dequantized in-kernel.
 //
 // Two launches per call:
-//   a_to_f16_kernel  A (fp32) -> fp16 workspace, each 8-k group stored in the
-//                    order (k0,k4),(k1,k5),(k2,k6),(k3,k7) — the order in which the
+//   a_rows_f16_kernel  A (fp32) -> fp16 workspace, row m scaled by an exact power of
+//                    two 2^-e[m] that brings its max |A| into [2^14, 2^15) (so no
+//                    finite fp32 row overflows fp16, and small rows stay out of its
+//                    subnormal range), each 8-k group stored in the order
+//                    (k0,k4),(k1,k5),(k2,k6),(k3,k7) — the order in which the
 //                    weight dequant below produces its codes, so both MFMA
 //                    operands carry the same permutation of k (a dot product does
-//                    not depend on the order of its terms).
+//                    not depend on the order of its terms). The epilogue
+//                    multiplies row m's sums by 2^e[m] (exact).
 //   mfma_w4_pipe_kernel
 //     * A 256x256 output tile per workgroup: 4 waves in a 2x2 layout, each wave
 //       128x128 as 4x4 v_mfma_f32_32x32x16_f16 fragments accumulating in AGPRs.
@@ -41,9 +45,11 @@
 //       of 4 steps each) are neighbouring work items; the first to finish writes its
 //       partial sums through to a workspace slot and raises a flag, the second adds the
 //       slot to its own sums and stores Y once (deterministic: fp32 a + b == b + a).
-// Numerics: A rounded once to fp16; W = fl16((q - zp) * fl16(s)); products exact,
-// sums fp32. Requires |A| < 65504 (fp16 range) and fp16-normal scales for the
-// 2^-11 relative bound; the library routes other inputs to mfma_w4.
+// Numerics: A rounded once to fp16 after its row's power-of-two scaling;
+// W = fl16((q - zp) * fl16(s)); products exact, sums fp32, then the row's 2^e.
+// W stays in fp16 range only for scales whose nonzero magnitudes lie in
+// [2^-14, 4364]: the library checks that once per weights handle and sends other
+// weights to mfma_w4 (fp32 scales, exact integer weights).
 #pragma once
 #include "mfma_w4.h"
 #include <type_traits>
@@ -54,7 +60,8 @@ struct PipeParams {
     const uint8_t* b;
     const float* scales;
     const uint8_t* zp;       // nullptr: zp = 8
-    const _Float16* a16;     // [M][K] fp16, permuted within 8-k groups
+    const _Float16* a16;     // [M][K] fp16, permuted within 8-k groups, row m scaled by 2^-rexp[m]
+    const int* rexp;         // [M] row exponents of a16
     float* y;                // [M][N]
     int row_bytes, M, N, K, C, nb, zrb;
     int tiles_m, tiles_n;
@@ -62,12 +69,23 @@ struct PipeParams {
     // workgroups. Workgroup b runs on XCD x = b % 8: its first xv work items (b / 8 < xv)
     // are the halves of split tiles full + x*xv/2 .., the next xu whole tiles x*xu ..
     int full, xu, xv;
-    int* sync;               // split tiles: [tiles][2] arrival counter and ready flag, all zero
-    float* part;             // split tiles: [tiles][kPipeBM * kPipeBN] partial sums
+    int* sync;               // split tile t: sync[2 (t - full) ..] arrival tag and ready flag, zero
+    float* part;             // split tile t: slot t - full of kPipeBM * kPipeBN partial sums
+    int epoch;               // this launch's nonzero tag in sync (tells overlapping launches apart)
+    int spin_limit;          // polls of the first half's flag before the second half gives up
+    int* err;                // set to a nonzero code when a split tile's hand-off fails
 };
 
+// Codes written to PipeParams::err.
+constexpr int kPipeErrTimeout = 1;   // the first half's flag did not come within the bound
+constexpr int kPipeErrOverlap = 2;   // another launch holds the tile's counters
+
 constexpr int kPipeBM = 256, kPipeBN = 256;
-constexpr int kPipeLdsBytes = 4 * kPipeBM * 64 + 3 * (kPipeBN * 64 + kPipeBN * 16 + kPipeBN * 4) + 2 * kPipeBN * 64;
+// A stages, weight groups, fp16 weight tiles, then the tile's row exponents (1 KB): the
+// whole 160 KB of a CU (the kernel declares no static LDS).
+constexpr int kPipeLdsBytes =
+    4 * kPipeBM * 64 + 3 * (kPipeBN * 64 + kPipeBN * 16 + kPipeBN * 4) + 2 * kPipeBN * 64 + kPipeBM * 4;
+static_assert(kPipeLdsBytes <= 160 * 1024, "the pipelined prefill's LDS exceeds a CU's");
 // Base offset of a row beyond the matrix: above every buffer the kernel reads
 // (the host checks each is smaller), so loads from it return zero.
 constexpr int kPipeFar = 0x40000000;
@@ -77,30 +95,99 @@ __device__ __forceinline__ uint32_t pack_h2(float lo, float hi)
     return __builtin_bit_cast(uint32_t, h2_t{(_Float16)lo, (_Float16)hi});
 }
 
-// fp32 -> fp16 in the permuted order above: groups of 8 values, kA16Groups groups per
-// thread per pass with all their loads issued before the first store (more bytes in
-// flight per thread than one group at a time).
-constexpr int kA16Groups = 4;
-__global__ __launch_bounds__(256) void a_to_f16_kernel(const float* __restrict__ a, uint32_t* __restrict__ o, int64_t n8)
+__device__ __forceinline__ float max_abs8(const float4& lo, const float4& hi)
 {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i0 = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i0 < n8; i0 += kA16Groups * stride) {
-        float4 lo[kA16Groups], hi[kA16Groups];
+    return fmaxf(fmaxf(fmaxf(fabsf(lo.x), fabsf(lo.y)), fmaxf(fabsf(lo.z), fabsf(lo.w))),
+                 fmaxf(fmaxf(fabsf(hi.x), fabsf(hi.y)), fmaxf(fabsf(hi.z), fabsf(hi.w))));
+}
+
+// Exponent e of a row whose largest magnitude is mx: mx * 2^-e lies in [2^14, 2^15)
+// (mx in [2^(E-1), 2^E) with E = frexp exponent, e = E - 15). Rows that are all zero,
+// or hold an inf (fmaxf skips NaN), take e = 0: their sums are zero or non-finite
+// whatever the scaling.
+__device__ __forceinline__ int row_exponent(float mx)
+{
+    return (mx > 0.0f && mx <= 3.402823466e38f) ? __builtin_amdgcn_frexp_expf(mx) - 15 : 0;
+}
+
+// Largest value of x over the workgroup of 256 threads, in every thread.
+__device__ __forceinline__ float block256_max(float x, float* red4)
+{
+    x = row16_max_all(x);
+    x = fmaxf(x, __shfl_xor(x, 16));
+    x = fmaxf(x, __shfl_xor(x, 32));
+    const int wave = threadIdx.x / kWave;
+    if ((threadIdx.x & (kWave - 1)) == 0) red4[wave] = x;
+    __syncthreads();
+    return fmaxf(fmaxf(red4[0], red4[1]), fmaxf(red4[2], red4[3]));
+}
+
+__device__ __forceinline__ u32x4_t pack_group(const float4& lo, const float4& hi, int e)
+{
+    auto sc = [&](float v) { return __builtin_amdgcn_ldexpf(v, -e); };
+    return u32x4_t{pack_h2(sc(lo.x), sc(hi.x)), pack_h2(sc(lo.y), sc(hi.y)), pack_h2(sc(lo.z), sc(hi.z)),
+                   pack_h2(sc(lo.w), sc(hi.w))};
+}
+
+// fp32 -> fp16, one workgroup of 256 threads per row m: the row's max |A| gives its
+// exponent e (row_exponent), stored in rexp[m]; the row is written times 2^-e (exact)
+// in the permuted 8-k group order above. Thread t takes groups t, t + 256, ...: with
+// R > 0 the row's R * 256 >= K / 8 groups are held in registers between the max and
+// the conversion (one read of A); R == 0 reads the row twice (the second read hits L2).
+template <int R>
+__global__ __launch_bounds__(256) void a_rows_f16_kernel(const float* __restrict__ a, uint32_t* __restrict__ o,
+                                                         int* __restrict__ rexp, int K)
+{
+    __shared__ float red4[4];
+    const int m = blockIdx.x, tid = threadIdx.x, G8 = K >> 3;
+    const float4* src = reinterpret_cast<const float4*>(a + (int64_t)m * K);
+    u32x4_t* dst = reinterpret_cast<u32x4_t*>(o) + (int64_t)m * G8;
+    float mx = 0.0f;
+    if constexpr (R > 0) {
+        float4 lo[R], hi[R];
 #pragma unroll
-        for (int u = 0; u < kA16Groups; ++u) {
-            const int64_t i = i0 + u * stride;
-            if (i < n8) {
-                lo[u] = reinterpret_cast<const float4*>(a)[2 * i];
-                hi[u] = reinterpret_cast<const float4*>(a)[2 * i + 1];
-            }
+        for (int u = 0; u < R; ++u) {
+            const int i = tid + 256 * u;
+            lo[u] = i < G8 ? src[2 * i] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+            hi[u] = i < G8 ? src[2 * i + 1] : float4{0.0f, 0.0f, 0.0f, 0.0f};
         }
 #pragma unroll
-        for (int u = 0; u < kA16Groups; ++u) {
-            const int64_t i = i0 + u * stride;
-            if (i < n8)
-                reinterpret_cast<u32x4_t*>(o)[i] = u32x4_t{pack_h2(lo[u].x, hi[u].x), pack_h2(lo[u].y, hi[u].y),
-                                                           pack_h2(lo[u].z, hi[u].z), pack_h2(lo[u].w, hi[u].w)};
+        for (int u = 0; u < R; ++u) mx = fmaxf(mx, max_abs8(lo[u], hi[u]));
+        const int e = row_exponent(block256_max(mx, red4));
+        if (tid == 0) rexp[m] = e;
+#pragma unroll
+        for (int u = 0; u < R; ++u) {
+            const int i = tid + 256 * u;
+            if (i < G8) dst[i] = pack_group(lo[u], hi[u], e);
         }
+    } else {
+        for (int i = tid; i < G8; i += 256) mx = fmaxf(mx, max_abs8(src[2 * i], src[2 * i + 1]));
+        const int e = row_exponent(block256_max(mx, red4));
+        if (tid == 0) rexp[m] = e;
+        for (int i = tid; i < G8; i += 256) dst[i] = pack_group(src[2 * i], src[2 * i + 1], e);
+    }
+}
+
+// The register depth a_rows_f16_kernel takes for rows of K (a multiple of 8) values.
+inline int a_rows_depth(int K)
+{
+    const int per = (K / 8 + 255) / 256;
+    for (int r : {1, 2, 4, 6, 8, 12})
+        if (per <= r) return r;
+    return 0;
+}
+
+inline void launch_a_rows_f16(const float* a, uint32_t* o, int* rexp, int M, int K, hipStream_t stream)
+{
+    const dim3 grid((unsigned)M), block(256);
+    switch (a_rows_depth(K)) {
+        case 1: hipLaunchKernelGGL(a_rows_f16_kernel<1>, grid, block, 0, stream, a, o, rexp, K); break;
+        case 2: hipLaunchKernelGGL(a_rows_f16_kernel<2>, grid, block, 0, stream, a, o, rexp, K); break;
+        case 4: hipLaunchKernelGGL(a_rows_f16_kernel<4>, grid, block, 0, stream, a, o, rexp, K); break;
+        case 6: hipLaunchKernelGGL(a_rows_f16_kernel<6>, grid, block, 0, stream, a, o, rexp, K); break;
+        case 8: hipLaunchKernelGGL(a_rows_f16_kernel<8>, grid, block, 0, stream, a, o, rexp, K); break;
+        case 12: hipLaunchKernelGGL(a_rows_f16_kernel<12>, grid, block, 0, stream, a, o, rexp, K); break;
+        default: hipLaunchKernelGGL(a_rows_f16_kernel<0>, grid, block, 0, stream, a, o, rexp, K); break;
     }
 }
 
@@ -121,6 +208,10 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) { return (uint32_
 __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, int voff, int soff, uint32_t m0v)
 {
     asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0v) : "memory");
+}
+__device__ __forceinline__ void lds_load4(__amdgpu_buffer_rsrc_t r, int voff, int soff, uint32_t m0v)
+{
+    asm volatile("buffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0v) : "memory");
 }
 __device__ __forceinline__ void lds_load2(__amdgpu_buffer_rsrc_t r, int voff, int soff, uint32_t m0v)
 {
@@ -176,7 +267,10 @@ __device__ __forceinline__ bool pipe_item(const PipeParams& p, PipeItem& it)
 
 // Stores a work item's 256x256 accumulators (4 waves in 2x2, each 4x4 fragments of
 // v_mfma_f32_32x32x16 layout) into Y, through the split-K hand-off for split tiles.
-__device__ __forceinline__ void pipe_epilogue(const PipeParams& p, const PipeItem& it, floatx16_t (&acc)[4][4])
+// erow[r] (LDS) is the exponent of tile row r: Y = acc * 2^erow (exact).
+// xs (LDS) holds two ints of workgroup-wide state for the split-K hand-off.
+__device__ __forceinline__ void pipe_epilogue(const PipeParams& p, const PipeItem& it, floatx16_t (&acc)[4][4],
+                                              const int* erow, int* xs)
 {
     constexpr int BM = kPipeBM, BN = kPipeBN, FM = 4, FN = 4;
     // Lane indices from an opaque copy of the thread id: the compiler cannot share the
@@ -187,12 +281,19 @@ __device__ __forceinline__ void pipe_epilogue(const PipeParams& p, const PipeIte
     const int wm = wave & 1, wn = wave >> 1, lr = lane & 31, lh = lane >> 5;
     const int m0 = it.m0, n0 = it.n0, tile = it.tile;
     const bool split = it.split;
+    // Exponent of accumulator row v of fragment row block i (four rows per LDS read).
+    auto row_exp = [&](int i, int v) {
+        const int4 e4 = *reinterpret_cast<const int4*>(&erow[wm * 128 + 32 * i + 4 * lh + 8 * (v >> 2)]);
+        const int s = v & 3;
+        return s == 0 ? e4.x : s == 1 ? e4.y : s == 2 ? e4.z : e4.w;
+    };
     // acc[i][j][v] is Y[row][col], col = lane % 32, row = 8*(v/4) + 4*(lane/32) + v%4.
     // Stores go through a buffer resource with an offset that has bit 30 set outside the
     // valid rows/columns (every destination is smaller than 2^30 bytes, checked by the
     // host): such stores are dropped, so the epilogue has no branches. The destination
     // is runtime data: the tile (rb, cb) of an ld-wide matrix with rl x cl valid entries.
-    auto store_tile = [&](__amdgpu_buffer_rsrc_t rd, int ld, int rb, int cb, int rl, int cl, auto cpol) {
+    // SCALE applies the row exponents (the final Y); the split slot holds raw sums.
+    auto store_tile = [&](__amdgpu_buffer_rsrc_t rd, int ld, int rb, int cb, int rl, int cl, auto cpol, auto scale) {
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
             const int row0 = wm * 128 + 32 * i + 4 * lh;
@@ -206,7 +307,12 @@ __device__ __forceinline__ void pipe_epilogue(const PipeParams& p, const PipeIte
                     const int rv = 8 * (v >> 2) + (v & 3);
                     const uint32_t outside = (uint32_t)(((rl - 1 - row0 - rv) | cfree) >> 31);   // all ones outside
                     const int off = (int)((base + (uint32_t)(rv * 4) * (uint32_t)ld) | (outside & (uint32_t)kPipeFar));
-                    const float x = acc[i][j][v];   // bit_cast of a vector element would read element 0
+                    // Read the accumulator with an AGPR operand: used as a plain float in
+                    // arithmetic, the register allocator moves all 256 accumulators out of the
+                    // AGPRs at the loop exit and spills.
+                    float x;
+                    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(x) : "a"(acc[i][j][v]));
+                    if constexpr (decltype(scale)::value) x = __builtin_amdgcn_ldexpf(x, row_exp(i, v));
                     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, x), rd, off, 0, decltype(cpol)::value);
                 }
             }
@@ -219,51 +325,71 @@ __device__ __forceinline__ void pipe_epilogue(const PipeParams& p, const PipeIte
     using y_store = std::integral_constant<int, kNonTemporal>;
     using coherent_store = std::integral_constant<int, kDeviceCoherent>;
     if (!split) {
-        store_tile(ry, p.N, m0, n0, rl, cl, y_store{});
+        store_tile(ry, p.N, m0, n0, rl, cl, y_store{}, std::true_type{});
         return;
     }
-    // Two halves: the first to arrive writes its partial sums through to its tile's slot
-    // of the partials workspace (sc1 stores) and raises the tile's flag once those stores
-    // have completed; the second waits for the flag, reads the slot with device-coherent
-    // loads and stores its own sums plus the slot into Y, once. Per split tile that moves
-    // three tiles of fp32 (slot write, slot read, Y write). Y = p0 + p1 either way (fp32
-    // addition commutes), so the result does not depend on the arrival order. The second
-    // waits only for a workgroup that has already arrived (and is therefore running), so
-    // the wait ends. The hand-off uses no agent-scope fence (on gfx950 those write back or
-    // invalidate the XCD's whole L2, and an acquiring spin would invalidate it on every
-    // poll).
-    __shared__ int arrival;
-    int* const cnt = p.sync + 2 * tile;
-    if (threadIdx.x == 0) arrival = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Two halves: the first to arrive (it swaps the tile's tag from 0 to this launch's
+    // epoch) writes its partial sums through to its tile's slot of the partials workspace
+    // (sc1 stores) and raises the tile's flag to the epoch once those stores have
+    // completed; the second (it finds its own epoch in the tag) waits for the flag, reads
+    // the slot with device-coherent loads and stores its own sums plus the slot into Y,
+    // once. Per split tile that moves three tiles of fp32 (slot write, slot read, Y
+    // write). Y = p0 + p1 either way (fp32 addition commutes), so the result does not
+    // depend on the arrival order. The second waits only for a workgroup that has already
+    // arrived (and is therefore running), so the wait ends; its bound only turns a misuse
+    // into an error instead of a hang. The hand-off uses no agent-scope fence (on gfx950
+    // those write back or invalidate the XCD's whole L2, and an acquiring spin would
+    // invalidate it on every poll). A tag that is neither 0 nor this launch's epoch means
+    // another launch is using the counters (two launches on one workspace overlapping):
+    // the half reports it in p.err and stores nothing, and so does a second half whose
+    // flag does not come. The host turns p.err into an error status.
+    int& arrival = xs[0];
+    int* const cnt = p.sync + 2 * (tile - p.full);
+    if (threadIdx.x == 0) {
+        int seen = 0;
+        if (__hip_atomic_compare_exchange_strong(cnt, &seen, p.epoch, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT))
+            arrival = 0;
+        else
+            arrival = seen == p.epoch ? 1 : 2;
+    }
     __syncthreads();
-    const bool second = arrival != 0;
-    float* const slot = p.part + (int64_t)tile * (BM * BN);
+    float* const slot = p.part + (int64_t)(tile - p.full) * (BM * BN);
     const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(slot, BM * BN * 4);
-    if (!second) {
-        store_tile(rs, BN, 0, 0, rl, cl, coherent_store{});
+    if (arrival == 0) {
+        store_tile(rs, BN, 0, 0, rl, cl, coherent_store{}, std::false_type{});
         wait_vmem_order_only_release();
         __syncthreads();
-        if (threadIdx.x == 0) __hip_atomic_store(cnt + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0) __hip_atomic_store(cnt + 1, p.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
+    if (arrival == 2) {
+        if (threadIdx.x == 0) __hip_atomic_store(p.err, kPipeErrOverlap, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        return;
+    }
+    int& flag_ok = xs[1];
     if (threadIdx.x == 0) {
-        // Bounded: the first half is running and needs no other workgroup to finish, so
-        // the flag comes within microseconds; the bound only keeps a misuse (two launches
-        // on one handle overlapping) from hanging the device.
-        for (int spin = 0; spin < (1 << 22); ++spin) {
-            if (__hip_atomic_load(cnt + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
+        int ok = 0;
+        for (int spin = 0; spin < p.spin_limit; ++spin) {
+            if (__hip_atomic_load(cnt + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == p.epoch) {
+                ok = 1;
+                break;
+            }
             __builtin_amdgcn_s_sleep(2);
         }
+        if (!ok) __hip_atomic_store(p.err, kPipeErrTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        flag_ok = ok;
         // Both halves are past their use of the pair: leave it zero for the next launch.
         __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(cnt + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
+    if (!flag_ok) return;
     wait_vmem_order_only_acquire();
-    // Y = acc + slot, in the accumulator layout (each lane reads back the slot entries the
-    // first half's lane of the same position wrote), one fragment at a time with the next
-    // fragment's loads issued before this fragment's stores (the compiler cannot move loads
-    // of one buffer above stores to another).
+    // Y = (acc + slot) * 2^erow, in the accumulator layout (each lane reads back the slot
+    // entries the first half's lane of the same position wrote), one fragment at a time
+    // with the next fragment's loads issued before this fragment's stores (the compiler
+    // cannot move loads of one buffer above stores to another).
     constexpr int NF = FM * FN;
     auto frag_offset = [&](int f, int v, int ld, int rb, int cb) {   // byte offset, bit 30 set outside
         const int i = f / FN, j = f % FN;
@@ -284,11 +410,9 @@ __device__ __forceinline__ void pipe_epilogue(const PipeParams& p, const PipeIte
         if (f + 1 < NF) load_frag(f + 1, sv[(f + 1) & 1]);
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-            // Read the accumulator with an AGPR operand: used as a plain float, the register
-            // allocator moves all 256 accumulators out of the AGPRs at the loop exit and spills.
-            float a;
+            float a;   // an AGPR operand, as in store_tile
             asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(a) : "a"(acc[f / FN][f % FN][v]));
-            const float xv = a + sv[f & 1][v];
+            const float xv = __builtin_amdgcn_ldexpf(a + sv[f & 1][v], row_exp(f / FN, v));
             __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, xv), ry, frag_offset(f, v, p.N, m0, n0), 0,
                                                   kNonTemporal);
         }
@@ -302,7 +426,8 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
     constexpr int A_ST = BM * 64;                               // one step of A
     constexpr int CG = BN * 64, SG = BN * 16, ZG = BN * 4;      // one group: codes, scales, zp
     constexpr int OFF_A = 0, OFF_C = OFF_A + 4 * A_ST, OFF_S = OFF_C + 3 * CG, OFF_Z = OFF_S + 3 * SG,
-                  OFF_B = OFF_Z + 3 * ZG;
+                  OFF_B = OFF_Z + 3 * ZG, OFF_E = OFF_B + 2 * BN * 64;
+    static_assert(OFF_E + BM * 4 == kPipeLdsBytes, "LDS layout");
     constexpr int B16_SZ = BN * 64;
     extern __shared__ __attribute__((aligned(16))) uint8_t pipe_lds[];
     uint8_t* const lds = pipe_lds;
@@ -425,6 +550,12 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
     // B(t/4+2) [6 loads]; each wait counts the loads issued after the one waited for
     // (the weight group read at step t+1 was issued before A(t+1)).
     Ops R0, R1;
+    // The tile's row exponents go straight to LDS (row t at OFF_E + 4t), oldest of all the
+    // loads, so every wait below covers them too; rows past M read zero.
+    {
+        const int r = m0 + wave * 64 + lane;
+        lds_load4(buffer_rsrc(p.rexp, p.M * 4), r < p.M ? r * 4 : kPipeFar, 0, lbase + OFF_E + wave * 256);
+    }
     issue_b(0, 0);
     issue_b(1, 1);
     issue_a(0, 0);
@@ -488,8 +619,9 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
         b2 = bt;
     }
     wait_vmcnt<0>();
+    __syncthreads();   // every wave is past its last LDS access of the main loop; exponents landed
 
-    pipe_epilogue(p, it, acc);
+    pipe_epilogue(p, it, acc, reinterpret_cast<const int*>(lds + OFF_E), reinterpret_cast<int*>(lds + OFF_A));
 }
 
 }  // namespace msnb

@@ -2,8 +2,8 @@
 // into MFMA operand registers (M > 16, block sizes 32..., K a multiple of 128).
 //
 // Y[M,N] = A[M,K] * W[N,K]^T, W = fl16((q - zp) * fl16(s)), A the fp16 copy made by
-// a_to_f16_kernel (each 8-k group in the order k0,k4,k1,k5,k2,k6,k3,k7, the order in
-// which one dword of packed codes dequantizes).
+// a_rows_f16_kernel (row m scaled by 2^-rexp[m]; each 8-k group in the order
+// k0,k4,k1,k5,k2,k6,k3,k7, the order in which one dword of packed codes dequantizes).
 //
 // A workgroup (4 waves) computes a 128 x 256 tile of Y over a range of 128-k blocks:
 //   * wave w owns weight rows n0 + 64 w .. + 63 (4 fragments of 16) and all 128 rows of
@@ -25,7 +25,10 @@
 //   * K split (ksw > 1, for launches with too few tiles to fill the CUs): workgroup kw of
 //     a tile writes its partial sums to slice kw of a [ksw][M][N] workspace with plain
 //     stores, and rb_reduce_kernel adds the slices in index order into Y afterwards
-//     (deterministic; the kernel boundary orders the two launches).
+//     (deterministic; the kernel boundary orders the two launches). The reduce also
+//     multiplies row m by 2^rexp[m] (exact), so it runs for ksw = 1 too: scaling the
+//     accumulators in this kernel's epilogue moved them out of the AGPRs at the loop exit
+//     (hundreds of spilled registers).
 // Rows past M and columns past N read zeros (out-of-range buffer offsets) and are not
 // stored.
 #pragma once
@@ -41,8 +44,8 @@ struct RbParams {
     const uint8_t* b;          // [N][row_bytes]
     const float* scales;       // [N][nb]
     const uint8_t* zp;         // [N][zrb] or nullptr (zp = 8)
-    const _Float16* a16;       // [M][K] fp16, permuted within 8-k groups
-    float* out;                // Y [M][N] (ksw 1) or the workspace: ksw slices of `slice` floats
+    const _Float16* a16;       // [M][K] fp16, permuted within 8-k groups, row m scaled by 2^-rexp[m]
+    float* out;                // the workspace: ksw slices of `slice` floats
     int64_t slice;             // M * N rounded up to a multiple of 4 (16-byte aligned slices)
     int row_bytes, M, N, K, nb, zrb, log2bs;
     int tiles_m, tiles_n, ksw;
@@ -238,7 +241,7 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
     }
 
     // ---- epilogue: acc[mf][f][v] is out[m0 + 16 mf + 4 ls + v][n0 + 64 wave + 16 f + ln] ----
-    float* const out = p.out + (p.ksw > 1 ? kw * p.slice : 0);
+    float* const out = p.out + kw * p.slice;
     const __amdgpu_buffer_rsrc_t ro = buffer_rsrc(out, p.M * p.N * 4);
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
@@ -256,12 +259,12 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
     }
 }
 
-// y[e] = sum over kw of slice kw at e, in kw order, for e < n; the slices are
-// slice4 float4 groups apart (16-byte aligned), y only 4-byte aligned.
+// y[e] = 2^rexp[e / N] * (sum over kw of slice kw at e, in kw order) for e < n (< 2^31);
+// the slices are slice4 float4 groups apart (16-byte aligned), y only 4-byte aligned.
 __global__ __launch_bounds__(256) void rb_reduce_kernel(const float4* __restrict__ part, float* __restrict__ y,
-                                                        int64_t n, int64_t slice4, int ksw)
+                                                        const int* __restrict__ rexp, int n, int N, int slice4, int ksw)
 {
-    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < slice4; i += (int64_t)gridDim.x * blockDim.x) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < slice4; i += gridDim.x * blockDim.x) {
         float4 t = part[i];
         for (int w = 1; w < ksw; ++w) {
             const float4 v = part[(int64_t)w * slice4 + i];
@@ -271,9 +274,14 @@ __global__ __launch_bounds__(256) void rb_reduce_kernel(const float4* __restrict
             t.w += v.w;
         }
         const float tv[4] = {t.x, t.y, t.z, t.w};
+        int m = (4 * i) / N, col = 4 * i - m * N;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            if (4 * i + c < n) y[4 * i + c] = tv[c];
+            if (4 * i + c < n) y[4 * i + c] = __builtin_amdgcn_ldexpf(tv[c], rexp[m]);
+            if (++col == N) {
+                col = 0;
+                ++m;
+            }
         }
     }
 }

@@ -3,11 +3,14 @@
 // Weights handles hold B, scales and packed zero points resident in HBM in the
 // operator's own layout (uploaded once per initializer); each call dispatches
 //   bits=4, block_size in {32,64,128,256}, K % 32 == 0 ("fast" layouts):
-//     M <= 4, block_size 32 or 128, M*K/32 <= 1024              -> gemv_w4
-//     M <= 16 otherwise                                         -> gemv_w4_panel
-//     M >  16, block_size 32, K % 128 == 0, fp16-safe scales  -> a_to_f16 + mfma_w4_pipe
-//     M >  16 otherwise                                         -> mfma_w4
-//   anything else                                              -> generic
+//     M <= 16, block_size 128, K % 128 == 0, M >= 3          -> skinny_w4
+//     M <= 4, block_size 32 or 128, A panel fits one LDS pass -> gemv_w4
+//     M <= 16 otherwise                                       -> gemv_w4_panel
+//     M >  16, fp16-safe scales, K % 128 == 0:
+//       few output tiles or block_size != 32                  -> a_rows_f16 + mfma_w4_rb
+//       otherwise (block_size 32)                             -> a_rows_f16 + mfma_w4_pipe
+//     M >  16 otherwise                                       -> mfma_w4 (exact, no workspace)
+//   anything else                                             -> generic
 // Declarations and reference citations: include/ms_hip_kernels.h.
 #include "../../include/ms_hip_kernels.h"
 
@@ -16,14 +19,16 @@
 #include <algorithm>
 #include <array>
 #include <atomic>
-#include <cmath>
-#include <utility>
 #include <climits>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <unordered_set>
+#include <utility>
+#include <vector>
 
 #include "gemv_w4.h"
 #include "gemv_w4_panel.h"
@@ -96,7 +101,59 @@ int require_device()
     return MS_HIP_OK;
 }
 
+// ---- tuning knobs ----------------------------------------------------------------------
+// Launch-shape knobs for sweeps and tests (ms_hip_set_tuning: process defaults;
+// ms_hip_nbits_set_tuning: one handle). 0 = the shape heuristics below.
+//   0 gemv_w4_panel lanes per row          5 skinny_w4 workgroups per row tile
+//   1 gemv_w4 configuration (c+1; -1 panel) 6 mfma_w4_rb: 1 off, 2 every eligible M
+//   2 1: every M > 16 call to mfma_w4       7 mfma_w4_rb K split
+//   3 pipelined prefill K split              8 split-K hand-off poll bound (pipelined)
+//   4 skinny_w4: 1 off, 2 every eligible M
+constexpr int kNumKnobs = 9;
+constexpr int kDefaultSpinLimit = 1 << 22;
+std::atomic<int> g_knob[kNumKnobs];   // zero-initialised (static storage)
+
+struct Knobs {
+    int v[kNumKnobs];
+    int panel_lanes() const { return v[0]; }
+    int gemv_config() const { return v[1]; }
+    int pipe_off() const { return v[2]; }
+    int pipe_ksplit() const { return v[3]; }
+    int skinny() const { return v[4]; }
+    int skinny_ksw() const { return v[5]; }
+    int rb() const { return v[6]; }
+    int rb_ksw() const { return v[7]; }
+    int spin_limit() const { return v[8] > 0 ? v[8] : kDefaultSpinLimit; }
+};
+
+int validate_knob(int knob, int value)
+{
+    bool ok = false;
+    switch (knob) {
+        case 0: ok = value == 0 || value == 16 || value == 32 || value == 64; break;
+        case 1: ok = value >= -1 && value <= kNumGemvConfigs; break;
+        case 2: ok = value == 0 || value == 1; break;
+        case 3: ok = value >= 0 && value <= 3; break;
+        case 4: ok = value >= 0 && value <= 2; break;
+        case 5: ok = value >= 0 && value <= 64; break;
+        case 6: ok = value >= 0 && value <= 2; break;
+        case 7: ok = value >= 0 && value <= 64; break;
+        case 8: ok = value >= 0; break;
+        default: break;
+    }
+    return ok ? MS_HIP_OK : fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid tuning knob %d = %d", knob, value);
+}
+
 // ---- weights handle --------------------------------------------------------------------
+// A workspace: data (fp16 activations, row exponents, split-K partial sums) and
+// counters (split-K arrival counters, zero between launches).
+struct Ws {
+    uint8_t* data = nullptr;
+    size_t data_bytes = 0;
+    int* cnt = nullptr;
+    size_t cnt_ints = 0;
+};
+
 struct Weights {
     int N = 0, K = 0, bits = 0, bs = 0, nb = 0, blob = 0, zrb = 0;
     int has_zp = 0;
@@ -107,40 +164,49 @@ struct Weights {
     uint8_t* d_b = nullptr;
     float* d_scales = nullptr;
     uint8_t* d_zp = nullptr;
-    // synchronous host-pointer path: staging buffers + stream, guarded by mu
+    std::atomic<int> knob[kNumKnobs];   // MS_HIP_TUNING_INHERIT: the process default
+    // Device-side failure report: a split-K hand-off that gives up writes a nonzero code
+    // here (pinned host memory the kernels write through d_err); calls check and clear it.
+    int* h_err = nullptr;
+    int* d_err = nullptr;
+    // synchronous host-pointer path: device and pinned host staging + stream, guarded by mu
     std::mutex mu;
     hipStream_t stream = nullptr;
     float* d_stage = nullptr;
     size_t stage_bytes = 0;
-    // prefill pipeline: scales fp16-safe (checked at load), fp16 activation workspace
+    uint8_t* h_stage = nullptr;
+    size_t h_stage_bytes = 0;
+    // prefill kernels: scales fp16-safe (checked at load)
     int pipe_scales_ok = 0;
+    // workspace, grown on demand under ws_mu (never while the launch stream is captured)
     std::mutex ws_mu;
-    uint32_t* d_a16 = nullptr;
-    size_t a16_bytes = 0;
-    int* d_sync = nullptr;      // split-K arrival counters and flags, zero between launches
-    float* d_part = nullptr;    // split-K partial sums, kPipeBM x kPipeBN floats per tile
-    int sync_tiles = 0;         // tiles covered by d_sync and d_part
-    float* d_rbpart = nullptr;  // mfma_w4_rb K-split partial sums [ksw][M][N]
-    size_t rbpart_bytes = 0;
-    // small-M matrix-core GEMV: K-split slots and counters
-    uint8_t* d_sk = nullptr;    // skinny_w4 slots: [row tiles][workgroups per tile][16 x 128 floats]
-    size_t sk_bytes = 0;
-    int* d_sk_sync = nullptr;   // per row tile, zero between launches
-    int sk_blocks = 0;
+    Ws ws;
 };
 
-constexpr uint32_t kHandleMagic = 0x4D534E42u;   // "MSNB"
-struct HandleBox {
-    uint32_t magic = kHandleMagic;
-    Weights w;
-};
+Knobs knobs_of(const Weights& w)
+{
+    Knobs k;
+    for (int i = 0; i < kNumKnobs; ++i) {
+        const int h = w.knob[i].load(std::memory_order_relaxed);
+        k.v[i] = h != MS_HIP_TUNING_INHERIT ? h : g_knob[i].load(std::memory_order_relaxed);
+    }
+    return k;
+}
+
+// Live handles: a handle is valid from create until destroy; calls with any other
+// pointer fail instead of reading freed memory.
+std::mutex g_live_mu;
+std::unordered_set<const void*> g_live;
 
 Weights* from_handle(void* h)
 {
-    HandleBox* box = static_cast<HandleBox*>(h);
-    if (!box || box->magic != kHandleMagic) return nullptr;
-    return &box->w;
+    std::lock_guard<std::mutex> lock(g_live_mu);
+    return h && g_live.count(h) ? static_cast<Weights*>(h) : nullptr;
 }
+
+// Split-K launch tags: nonzero, distinct for launches that could overlap.
+std::atomic<uint32_t> g_epoch{0};
+int next_epoch() { return (int)(g_epoch.fetch_add(1, std::memory_order_relaxed) % 0x7FFFFFFEu) + 1; }
 
 void derive_layout(Weights& w, int N, int K, int bits, int bs)
 {
@@ -183,28 +249,21 @@ void free_weights(Weights& w)
     if (w.d_scales) (void)hipFree(w.d_scales);
     if (w.d_zp) (void)hipFree(w.d_zp);
     if (w.d_stage) (void)hipFree(w.d_stage);
-    if (w.d_a16) (void)hipFree(w.d_a16);
-    if (w.d_sync) (void)hipFree(w.d_sync);
-    if (w.d_part) (void)hipFree(w.d_part);
-    if (w.d_rbpart) (void)hipFree(w.d_rbpart);
-    if (w.d_sk) (void)hipFree(w.d_sk);
-    if (w.d_sk_sync) (void)hipFree(w.d_sk_sync);
+    if (w.h_stage) (void)hipHostFree(w.h_stage);
+    if (w.h_err) (void)hipHostFree(w.h_err);
+    if (w.ws.data) (void)hipFree(w.ws.data);
+    if (w.ws.cnt) (void)hipFree(w.ws.cnt);
     if (w.stream) (void)hipStreamDestroy(w.stream);
     w.d_b = nullptr;
     w.d_scales = nullptr;
     w.d_zp = nullptr;
     w.d_stage = nullptr;
-    w.d_a16 = nullptr;
-    w.a16_bytes = 0;
-    w.d_sync = nullptr;
-    w.d_part = nullptr;
-    w.sync_tiles = 0;
-    w.d_rbpart = nullptr;
-    w.rbpart_bytes = 0;
-    w.d_sk = nullptr;
-    w.sk_bytes = 0;
-    w.d_sk_sync = nullptr;
-    w.sk_blocks = 0;
+    w.stage_bytes = 0;
+    w.h_stage = nullptr;
+    w.h_stage_bytes = 0;
+    w.h_err = nullptr;
+    w.d_err = nullptr;
+    w.ws = Ws{};
     w.stream = nullptr;
 }
 
@@ -223,7 +282,24 @@ __global__ __launch_bounds__(256) void scale_range_kernel(const float* __restric
     atomicMax(&out[1], hi);
 }
 
-// The pipelined prefill rounds scales to fp16 and forms (q - zp) * s in fp16: every
+// Zero fill of n ints (counters), a kernel rather than a memset so that it can sit in
+// a captured graph.
+__global__ __launch_bounds__(256) void zero_ints_kernel(int* __restrict__ p, int64_t n)
+{
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0;
+}
+
+int zero_ints(int* p, int64_t n, hipStream_t stream)
+{
+    if (n <= 0) return MS_HIP_OK;
+    hipLaunchKernelGGL(zero_ints_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 256)), dim3(256), 0,
+                       stream, p, n);
+    MS_HIP_CHECK(hipGetLastError());
+    return MS_HIP_OK;
+}
+
+// The fp16 prefill kernels round scales to fp16 and form (q - zp) * s in fp16: every
 // nonzero |s| must be an fp16 normal (>= 2^-14) and 15 |s| must stay below 65504.
 int check_pipe_scales(Weights& w)
 {
@@ -249,17 +325,64 @@ int check_pipe_scales(Weights& w)
     return MS_HIP_OK;
 }
 
-// ---- GEMV launch shape --------------------------------------------------------------------
-// Tuning knobs (ms_hip_set_tuning); 0 = the shape heuristics below.
-int g_panel_lanes_override = 0;  // knob 0: gemv_w4_panel lanes per row
-int g_gemv_config = 0;           // knob 1: c+1 forces kGemvConfigs[c], -1 forces gemv_w4_panel
-int g_pipe_off = 0;              // knob 2: 1 routes every prefill call to mfma_w4
-int g_pipe_ksplit = 0;           // knob 3: 1 no prefill K split, 2 all tiles split, 3 the second half (where K allows)
-int g_skinny = 0;                // knob 4: 1 keeps M <= 16 off skinny_w4, 2 sends every eligible M to it
-int g_skinny_ksw = 0;            // knob 5: workgroups per skinny_w4 row block (0: heuristic)
-int g_rb = 0;                    // knob 6: 1 keeps M > 16 off mfma_w4_rb, 2 sends every eligible M to it
-int g_rb_ksw = 0;                // knob 7: mfma_w4_rb K split (0: heuristic)
+// A device-side failure recorded in the handle's error word since the last check (the
+// split-K hand-off of a pipelined prefill launch that gave up): clears it, zeroes the
+// workspace counters on `stream` and returns MS_HIP_ERR_HIP; MS_HIP_OK otherwise.
+int take_device_error(Weights& w, hipStream_t stream)
+{
+    if (!w.h_err) return MS_HIP_OK;
+    const int code = __atomic_exchange_n(w.h_err, 0, __ATOMIC_ACQ_REL);
+    if (!code) return MS_HIP_OK;
+    {
+        std::lock_guard<std::mutex> lock(w.ws_mu);
+        if (w.ws.cnt) (void)zero_ints(w.ws.cnt, (int64_t)w.ws.cnt_ints, stream);
+    }
+    return fail(MS_HIP_ERR_HIP,
+                code == kPipeErrOverlap
+                    ? "[ms_hip] split-K prefill: another launch was using this workspace (overlapping calls on one "
+                      "handle); the output of that call is not valid"
+                    : "[ms_hip] split-K prefill: a partial-sum hand-off timed out; the output of that call is not valid");
+}
 
+// Grows the handle's workspace to at least (data_bytes, cnt_ints) — new counters are
+// zeroed on `stream`. Returns 1 with *out set, 0 when it would have to grow while `stream`
+// is being captured (the caller takes a workspace-free kernel), -1 on a HIP error.
+int ensure_ws(Weights& w, size_t data_bytes, size_t cnt_ints, hipStream_t stream, Ws* out)
+{
+    std::lock_guard<std::mutex> lock(w.ws_mu);
+    const bool grow_d = w.ws.data_bytes < data_bytes, grow_c = w.ws.cnt_ints < cnt_ints;
+    if (grow_d || grow_c) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+            (void)hipGetLastError();
+            return 0;
+        }
+        // Earlier launches on this stream may still use the old buffers.
+        if (hipStreamSynchronize(stream) != hipSuccess) return -1;
+    }
+    if (grow_d) {
+        if (w.ws.data && hipFree(w.ws.data) != hipSuccess) return -1;
+        w.ws.data = nullptr;
+        w.ws.data_bytes = 0;
+        if (hipMalloc(&w.ws.data, data_bytes) != hipSuccess) return -1;
+        w.ws.data_bytes = data_bytes;
+    }
+    if (grow_c) {
+        if (w.ws.cnt && hipFree(w.ws.cnt) != hipSuccess) return -1;
+        w.ws.cnt = nullptr;
+        w.ws.cnt_ints = 0;
+        if (hipMalloc(&w.ws.cnt, cnt_ints * sizeof(int)) != hipSuccess) return -1;
+        w.ws.cnt_ints = cnt_ints;
+        // Every launch leaves its counters zero again; they start zero here.
+        if (zero_ints(w.ws.cnt, (int64_t)cnt_ints, stream) != MS_HIP_OK) return -1;
+    }
+    *out = w.ws;
+    return 1;
+}
+
+constexpr size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// ---- GEMV launch shape --------------------------------------------------------------------
 // gemv_w4 instantiations: [M-1][L slot][config], L slot 0 = block size 32, 1 = block size 128.
 typedef void (*GemvFn)(GemvParams);
 template <int M, int L, size_t I>
@@ -305,15 +428,13 @@ bool gemv_config_fits(const Weights& w, int M, const GemvConfig& c)
 // row win from 16K rows up, 64 lanes per row with two rows per lane from 2K to 16K rows
 // (re-swept with the non-temporal code loads: 7B o at M = 1 / 2 5.41 -> 5.26 /
 // 6.83 -> 6.54 us against the 32-lane pick), 32 lanes per row below; for M = 3-4 the
-// 8-wave configs. N is the launch's total
-// rows (summed over a group). Indices are into kGemvConfigs; the streaming-read ceiling
-// of the 7B gate+up launch's bytes (a plain row-pattern read, same rotation) is
-// 14.5-15.1 us, against which its pick runs at about 20 us.
-int pick_gemv_config(const Weights& w, int M, int N)
+// 8-wave configs. N is the launch's total rows (summed over a group). Indices are into
+// kGemvConfigs.
+int pick_gemv_config(const Weights& w, const Knobs& kn, int M, int N)
 {
-    if (g_gemv_config < 0) return -1;
-    if (g_gemv_config > 0) {
-        const int ci = g_gemv_config - 1;
+    if (kn.gemv_config() < 0) return -1;
+    if (kn.gemv_config() > 0) {
+        const int ci = kn.gemv_config() - 1;
         return gemv_config_fits(w, M, kGemvConfigs[ci]) ? ci : -1;
     }
     static constexpr int kLargeM2[] = {16, 11, 0, 6};   // M <= 2, N >= 16384
@@ -400,24 +521,25 @@ bool gemv_groupable(const Weights& a, const Weights& b)
            a.log2cpb == b.log2cpb && l_slot(a) >= 0;
 }
 
+bool skinny_eligible(const Weights& w, const Knobs& kn, int M);
+
 // How many of the calls starting at handles[0] one launch serves: consecutive calls on
 // the same activations (the projections of one input) that gemv_w4 can group, up to
-// kGemvMaxOps; 1 when the first call launches alone. *ci receives the group's config.
-bool skinny_eligible(const Weights& w, int M);
-int skinny_ksw(const Weights& w);
-
-int batch_group(void* const* handles, const float* const* dA, int count, int M, int* ci)
+// kGemvMaxOps; 1 when the first call launches alone. *ci receives the group's config
+// (the first handle's knobs decide it).
+int batch_group(Weights* const* ws, const float* const* dA, int count, int M, int* ci)
 {
-    const Weights* w = from_handle(handles[0]);
+    const Weights* w = ws[0];
+    const Knobs kn = knobs_of(*w);
     if (M <= 0 || M > kGemvMaxM || !dA[0] || (reinterpret_cast<uintptr_t>(dA[0]) & 15)) return 1;
-    if (skinny_eligible(*w, M)) return 1;   // the matrix-core small-M path launches per matrix
+    if (skinny_eligible(*w, kn, M)) return 1;   // the matrix-core small-M path launches per matrix
     int n = 1, ntot = w->N;
-    while (n < count && n < kGemvMaxOps && dA[n] == dA[0] && gemv_groupable(*w, *from_handle(handles[n]))) {
-        ntot += from_handle(handles[n])->N;
+    while (n < count && n < kGemvMaxOps && dA[n] == dA[0] && gemv_groupable(*w, *ws[n])) {
+        ntot += ws[n]->N;
         ++n;
     }
     if (n == 1) return 1;
-    *ci = pick_gemv_config(*w, M, ntot);
+    *ci = pick_gemv_config(*w, kn, M, ntot);
     return *ci >= 0 ? n : 1;
 }
 
@@ -427,9 +549,9 @@ constexpr int kPanelLanes[3] = {16, 32, 64};
 
 // Lanes per row G: lane efficiency on the row's C chunks x wave fill (>= 1024
 // waves) x a penalty when a lane owns fewer than 3 chunks; ties go to the larger G.
-int pick_panel_lanes(int N, int C)
+int pick_panel_lanes(const Knobs& kn, int N, int C)
 {
-    if (g_panel_lanes_override) return g_panel_lanes_override;
+    if (kn.panel_lanes()) return kn.panel_lanes();
     double best = -1.0;
     int best_g = 16;
     for (int G : kPanelLanes) {
@@ -459,38 +581,23 @@ PanelFn panel_for_lanes(int G)
     }
 }
 
-PanelFn panel_kernel(int M, int G)
+template <size_t... I>
+constexpr std::array<PanelFn (*)(int), sizeof...(I)> panel_table(std::index_sequence<I...>)
 {
-    switch (M) {
-        case 1: return panel_for_lanes<1>(G);
-        case 2: return panel_for_lanes<2>(G);
-        case 3: return panel_for_lanes<3>(G);
-        case 4: return panel_for_lanes<4>(G);
-        case 5: return panel_for_lanes<5>(G);
-        case 6: return panel_for_lanes<6>(G);
-        case 7: return panel_for_lanes<7>(G);
-        case 8: return panel_for_lanes<8>(G);
-        case 9: return panel_for_lanes<9>(G);
-        case 10: return panel_for_lanes<10>(G);
-        case 11: return panel_for_lanes<11>(G);
-        case 12: return panel_for_lanes<12>(G);
-        case 13: return panel_for_lanes<13>(G);
-        case 14: return panel_for_lanes<14>(G);
-        case 15: return panel_for_lanes<15>(G);
-        default: return panel_for_lanes<16>(G);
-    }
+    return {panel_for_lanes<(int)I + 1>...};
 }
+constexpr auto kPanelTable = panel_table(std::make_index_sequence<kPanelMaxM>{});
 
 struct PanelShape {
     int G, grid, panel_chunks;
     size_t lds_bytes;
 };
 
-PanelShape panel_shape(const Weights& w, int M)
+PanelShape panel_shape(const Weights& w, const Knobs& kn, int M)
 {
     PanelShape s;
     const int C = w.K / 32;
-    s.G = pick_panel_lanes(w.N, C);
+    s.G = pick_panel_lanes(kn, w.N, C);
     const int rows_per_wg = (kPanelThreads / kWave) * (kWave / s.G);
     s.grid = (w.N + rows_per_wg - 1) / rows_per_wg;
     // LDS panel: <= 40 KiB for M <= 4 (4 workgroups per CU), <= 64 KiB beyond.
@@ -509,9 +616,9 @@ PanelShape panel_shape(const Weights& w, int M)
     return s;
 }
 
-int launch_panel(const Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
+int launch_panel(const Weights& w, const Knobs& kn, const float* dA, float* dY, int M, hipStream_t stream)
 {
-    const PanelShape s = panel_shape(w, M);
+    const PanelShape s = panel_shape(w, kn, M);
     GemvPanelParams p;
     p.b = w.d_b;
     p.scales = w.d_scales;
@@ -526,19 +633,19 @@ int launch_panel(const Weights& w, const float* dA, float* dY, int M, hipStream_
     p.nb = w.nb;
     p.zrb = w.zrb;
     p.panel_chunks = s.panel_chunks;
-    hipLaunchKernelGGL(panel_kernel(M, s.G), dim3(s.grid), dim3(kPanelThreads), s.lds_bytes, stream, p);
+    hipLaunchKernelGGL(kPanelTable[M - 1](s.G), dim3(s.grid), dim3(kPanelThreads), s.lds_bytes, stream, p);
     MS_HIP_CHECK(hipGetLastError());
     return MS_HIP_OK;
 }
 
-int launch_gemv(const Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
+int launch_gemv(const Weights& w, const Knobs& kn, const float* dA, float* dY, int M, hipStream_t stream)
 {
-    const int ci = pick_gemv_config(w, M, w.N);
+    const int ci = pick_gemv_config(w, kn, M, w.N);
     if (ci >= 0) {
         const GemvMember m{&w, dY};
         return launch_gemv_group(&m, 1, dA, M, ci, stream);
     }
-    return launch_panel(w, dA, dY, M, stream);
+    return launch_panel(w, kn, dA, dY, M, stream);
 }
 
 int launch_generic(const Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
@@ -551,11 +658,15 @@ int launch_generic(const Weights& w, const float* dA, float* dY, int M, hipStrea
     return MS_HIP_OK;
 }
 
+// ---- workspace layouts -------------------------------------------------------------------
+// fp16 activations [M][K] then row exponents [M], each 256-byte aligned.
+size_t a16_bytes(int M, int K) { return align256((size_t)M * K * 2) + align256((size_t)M * 4); }
+
 // The pipelined prefill takes M > 16, block size 32, K a multiple of 128, fp16-safe
 // scales, and buffers (Y included) below kPipeFar (its out-of-range offset).
-bool pipe_eligible(const Weights& w, int M)
+bool pipe_eligible(const Weights& w, const Knobs& kn, int M)
 {
-    return !g_pipe_off && w.fast && M > kPanelMaxM && w.log2cpb == 0 && (w.K % 128) == 0 && w.pipe_scales_ok &&
+    return !kn.pipe_off() && w.fast && M > kPanelMaxM && w.log2cpb == 0 && (w.K % 128) == 0 && w.pipe_scales_ok &&
            (int64_t)w.N * w.row_bytes < kPipeFar && (int64_t)M * w.K * 2 < kPipeFar &&
            (int64_t)w.N * w.nb * 4 < kPipeFar && (int64_t)M * w.N * 4 < kPipeFar;
 }
@@ -584,18 +695,18 @@ int device_cus()
 //   * none otherwise.
 // Knob 3: 1 none, 2 all, 3 the second half of the tiles (a test hook for the mixed form).
 struct PipeSplit {
-    int full, xu, xv;   // whole tiles [0, full); per-XCD whole and split work items
+    int tiles, full, xu, xv;   // whole tiles [0, full); per-XCD whole and split work items
 };
-PipeSplit pipe_split(const Weights& w, int M)
+PipeSplit pipe_split(const Weights& w, const Knobs& kn, int M)
 {
     const int tiles = ((M + kPipeBM - 1) / kPipeBM) * ((w.N + kPipeBN - 1) / kPipeBN);
     int full = tiles;
     if (w.K / 128 >= 2) {
-        if (g_pipe_ksplit == 2) {
+        if (kn.pipe_ksplit() == 2) {
             full = 0;
-        } else if (g_pipe_ksplit == 3) {
+        } else if (kn.pipe_ksplit() == 3) {
             full = tiles / 2;
-        } else if (g_pipe_ksplit == 0) {
+        } else if (kn.pipe_ksplit() == 0) {
             const int cus = device_cus();
             if (2 * tiles <= cus) {
                 full = 0;
@@ -606,76 +717,48 @@ PipeSplit pipe_split(const Weights& w, int M)
         }
     }
     PipeSplit sp;
+    sp.tiles = tiles;
     sp.full = full;
     sp.xu = (full + kXcds - 1) / kXcds;
     sp.xv = 2 * ((tiles - full + kXcds - 1) / kXcds);
     return sp;
 }
 
-// Returns 1 when the pipelined prefill was launched, 0 when the caller should use
-// mfma_w4 (the workspace would have to grow while the stream is being captured),
-// or a negative value on a launch error (last error set).
-int launch_pipe(Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
+// Workspace of a pipelined launch: fp16 A and row exponents, then one partial-sum slot
+// per split tile; two counters per split tile.
+struct PipeWs {
+    size_t data, cnt, part_off;
+};
+PipeWs pipe_ws(const Weights& w, int M, const PipeSplit& sp)
 {
-    const size_t need = (size_t)M * w.K * 2;
+    PipeWs r;
+    const int nsplit = sp.tiles - sp.full;
+    r.part_off = a16_bytes(M, w.K);
+    r.data = r.part_off + (size_t)nsplit * kPipeBM * kPipeBN * sizeof(float);
+    r.cnt = (size_t)2 * nsplit;
+    return r;
+}
+
+int launch_pipe(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, float* dY, int M, hipStream_t stream)
+{
     const int tiles_m = (M + kPipeBM - 1) / kPipeBM, tiles_n = (w.N + kPipeBN - 1) / kPipeBN;
-    const int tiles = tiles_m * tiles_n;
-    const PipeSplit sp = pipe_split(w, M);
-    uint32_t* ws = nullptr;
-    int* sync = nullptr;
-    float* part = nullptr;
-    {
-        std::lock_guard<std::mutex> lock(w.ws_mu);
-        const bool grow_ws = w.a16_bytes < need, grow_sync = sp.full < tiles && w.sync_tiles < tiles;
-        if (grow_ws || grow_sync) {
-            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-            if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
-                (void)hipGetLastError();
-                return 0;
-            }
-            if (hipStreamSynchronize(stream) != hipSuccess) return -1;
-        }
-        if (grow_ws) {
-            if (w.d_a16 && hipFree(w.d_a16) != hipSuccess) return -1;
-            w.d_a16 = nullptr;
-            w.a16_bytes = 0;
-            if (hipMalloc(&w.d_a16, need) != hipSuccess) return -1;
-            w.a16_bytes = need;
-        }
-        if (grow_sync) {
-            // The pairs are zeroed once here; every split launch leaves its pairs zero again.
-            if (w.d_sync && hipFree(w.d_sync) != hipSuccess) return -1;
-            if (w.d_part && hipFree(w.d_part) != hipSuccess) return -1;
-            w.d_sync = nullptr;
-            w.d_part = nullptr;
-            w.sync_tiles = 0;
-            if (hipMalloc(&w.d_sync, (size_t)tiles * 2 * sizeof(int)) != hipSuccess) return -1;
-            // On the launch stream: a null-stream memset is not ordered before work on a
-            // non-blocking stream. (Never reached under capture: checked above.)
-            if (hipMemsetAsync(w.d_sync, 0, (size_t)tiles * 2 * sizeof(int), stream) != hipSuccess) return -1;
-            if (hipMalloc(&w.d_part, (size_t)tiles * kPipeBM * kPipeBN * sizeof(float)) != hipSuccess) return -1;
-            w.sync_tiles = tiles;
-        }
-        ws = w.d_a16;
-        sync = w.d_sync;
-        part = w.d_part;
-    }
+    const PipeSplit sp = pipe_split(w, kn, M);
+    const PipeWs L = pipe_ws(w, M, sp);
     static std::atomic<bool> lds_raised{false};
     if (!lds_raised.load()) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(mfma_w4_pipe_kernel),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, kPipeLdsBytes) != hipSuccess)
-            return -1;
+        MS_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(mfma_w4_pipe_kernel),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, kPipeLdsBytes));
         lds_raised.store(true);
     }
-    const int64_t n8 = (int64_t)M * w.K / 8;
-    hipLaunchKernelGGL(a_to_f16_kernel,
-                       dim3((unsigned)std::min<int64_t>((n8 + 256 * kA16Groups - 1) / (256 * kA16Groups), 2048)),
-                       dim3(256), 0, stream, dA, ws, n8);
+    uint32_t* a16 = reinterpret_cast<uint32_t*>(ws.data);
+    int* rexp = reinterpret_cast<int*>(ws.data + align256((size_t)M * w.K * 2));
+    launch_a_rows_f16(dA, a16, rexp, M, w.K, stream);
     PipeParams p;
     p.b = w.d_b;
     p.scales = w.d_scales;
     p.zp = w.has_zp ? w.d_zp : nullptr;
-    p.a16 = reinterpret_cast<const _Float16*>(ws);
+    p.a16 = reinterpret_cast<const _Float16*>(a16);
+    p.rexp = rexp;
     p.y = dY;
     p.row_bytes = (int)w.row_bytes;
     p.M = M;
@@ -689,10 +772,14 @@ int launch_pipe(Weights& w, const float* dA, float* dY, int M, hipStream_t strea
     p.full = sp.full;
     p.xu = sp.xu;
     p.xv = sp.xv;
-    p.sync = sync;
-    p.part = part;
+    p.sync = ws.cnt;
+    p.part = reinterpret_cast<float*>(ws.data + L.part_off);
+    p.epoch = next_epoch();
+    p.spin_limit = kn.spin_limit();
+    p.err = w.d_err;
     hipLaunchKernelGGL(mfma_w4_pipe_kernel, dim3(kXcds * (sp.xu + sp.xv)), dim3(256), kPipeLdsBytes, stream, p);
-    return hipGetLastError() == hipSuccess ? 1 : -1;
+    MS_HIP_CHECK(hipGetLastError());
+    return MS_HIP_OK;
 }
 
 // ---- skinny_w4: M <= 16 on the matrix cores at fp32-level accuracy (block size 128) ----
@@ -702,77 +789,55 @@ int launch_pipe(Weights& w, const float* dA, float* dY, int M, hipStream_t strea
 // on the 7B MLP shapes: M=2 13.2 / 12.5 us against 15.4 / 16.7 us; M=3 20.4 / 24.2 us
 // against 15.8 / 17.3 us), unless knob 4 says otherwise.
 constexpr int kSkinnyMinM = 3;
-bool skinny_eligible(const Weights& w, int M)
+bool skinny_eligible(const Weights& w, const Knobs& kn, int M)
 {
-    if (g_skinny == 1 || !w.fast || w.log2cpb != 2 || (w.K % 128) != 0 || M < 1 || M > kSkinnyMT) return false;
+    if (kn.skinny() == 1 || !w.fast || w.log2cpb != 2 || (w.K % 128) != 0 || M < 1 || M > kSkinnyMT) return false;
     if ((int64_t)kSkinnyMT * w.K * 4 >= INT32_MAX) return false;
-    return g_skinny == 2 || M >= kSkinnyMinM;
+    return kn.skinny() == 2 || M >= kSkinnyMinM;
 }
 
 // Workgroups per row tile: each takes at most kSkinnyNB blocks and at least one; beyond
 // that minimum, more only while the grid has fewer than two workgroups per CU (every
 // extra split adds a slot to write and to sum).
-int skinny_ksw(const Weights& w)
+int skinny_ksw(const Weights& w, const Knobs& kn)
 {
     const int tiles = (w.N + kSkinnyRows - 1) / kSkinnyRows;
     const int G = w.K / 128;
     const int kmin = (G + kSkinnyNB - 1) / kSkinnyNB;
     int ksw = kmin;
-    if (g_skinny_ksw > 0) {
-        ksw = g_skinny_ksw;
+    if (kn.skinny_ksw() > 0) {
+        ksw = kn.skinny_ksw();
     } else {
         while (ksw < G && (int64_t)tiles * ksw < 2 * device_cus()) ++ksw;
     }
     return std::max(kmin, std::min(ksw, G));
 }
 
-// Returns 1 when launched, 0 when the caller should take gemv_w4 / gemv_w4_panel (the
-// workspace would have to grow under capture), negative on a launch error.
-int launch_skinny(Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
+// Workspace of a skinny_w4 launch: one slot per workgroup, one counter per row tile.
+struct SkinnyWs {
+    size_t data, cnt;
+};
+SkinnyWs skinny_ws(const Weights& w, int ksw)
 {
     const int tiles = (w.N + kSkinnyRows - 1) / kSkinnyRows;
-    const int ksw = skinny_ksw(w);
-    const size_t need = ksw > 1 ? (size_t)tiles * ksw * kSkinnySlot * sizeof(float) : 0;
-    uint8_t* ws = nullptr;
-    int* sync = nullptr;
-    if (ksw > 1) {
-        std::lock_guard<std::mutex> lock(w.ws_mu);
-        const bool grow = w.sk_bytes < need, grow_sync = w.sk_blocks < tiles;
-        if (grow || grow_sync) {
-            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-            if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
-                (void)hipGetLastError();
-                return 0;
-            }
-            if (hipStreamSynchronize(stream) != hipSuccess) return -1;
-        }
-        if (grow) {
-            if (w.d_sk && hipFree(w.d_sk) != hipSuccess) return -1;
-            w.d_sk = nullptr;
-            w.sk_bytes = 0;
-            if (hipMalloc(&w.d_sk, need) != hipSuccess) return -1;
-            w.sk_bytes = need;
-        }
-        if (grow_sync) {
-            if (w.d_sk_sync && hipFree(w.d_sk_sync) != hipSuccess) return -1;
-            w.d_sk_sync = nullptr;
-            w.sk_blocks = 0;
-            if (hipMalloc(&w.d_sk_sync, (size_t)tiles * sizeof(int)) != hipSuccess) return -1;
-            // On the launch stream (never reached under capture: checked above).
-            if (hipMemsetAsync(w.d_sk_sync, 0, (size_t)tiles * sizeof(int), stream) != hipSuccess) return -1;
-            w.sk_blocks = tiles;
-        }
-        ws = w.d_sk;
-        sync = w.d_sk_sync;
-    }
+    SkinnyWs r;
+    r.data = ksw > 1 ? (size_t)tiles * ksw * kSkinnySlot * sizeof(float) : 0;
+    r.cnt = ksw > 1 ? (size_t)tiles : 0;
+    return r;
+}
+
+int launch_skinny(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, float* dY, int M, hipStream_t stream)
+{
+    const int tiles = (w.N + kSkinnyRows - 1) / kSkinnyRows;
+    const int ksw = skinny_ksw(w, kn);
     SkinnyParams p;
     p.b = w.d_b;
     p.scales = w.d_scales;
     p.zp = w.has_zp ? w.d_zp : nullptr;
     p.a = dA;
     p.y = dY;
-    p.slots = reinterpret_cast<float*>(ws);
-    p.sync = sync;
+    p.slots = ksw > 1 ? reinterpret_cast<float*>(ws.data) : nullptr;
+    p.sync = ksw > 1 ? ws.cnt : nullptr;
     p.row_bytes = (int)w.row_bytes;
     p.M = M;
     p.N = w.N;
@@ -781,16 +846,17 @@ int launch_skinny(Weights& w, const float* dA, float* dY, int M, hipStream_t str
     p.zrb = w.zrb;
     p.ksw = ksw;
     hipLaunchKernelGGL(skinny_w4_kernel, dim3(tiles * ksw), dim3(256), 0, stream, p);
-    return hipGetLastError() == hipSuccess ? 1 : -1;
+    MS_HIP_CHECK(hipGetLastError());
+    return MS_HIP_OK;
 }
 
 // ---- mfma_w4_rb: prefill with the weights dequantized into MFMA operand registers ----
 // Any power-of-two block size >= 32, K a multiple of 128, fp16-safe scales (as the
 // pipelined kernel: W = fl16((q - zp) * fl16(s))), every buffer below the out-of-range
 // offset the kernel uses for padding rows.
-bool rb_eligible(const Weights& w, int M)
+bool rb_eligible(const Weights& w, const Knobs& kn, int M)
 {
-    return g_rb != 1 && w.fast && M > kPanelMaxM && (w.K % 128) == 0 && w.pipe_scales_ok &&
+    return kn.rb() != 1 && w.fast && M > kPanelMaxM && (w.K % 128) == 0 && w.pipe_scales_ok &&
            (int64_t)w.N * w.row_bytes < kOOB && (int64_t)M * w.K * 2 < kOOB && (int64_t)w.N * w.nb * 4 < kOOB &&
            (int64_t)M * w.N * 4 < kOOB;
 }
@@ -801,11 +867,11 @@ bool rb_eligible(const Weights& w, int M)
 // rate, with t_block the measured time of one 128-k block of a workgroup (about 3.5 us:
 // K=11008 unsplit at M=2048 takes 301 us for 86 blocks). On the 7B MLP shapes this
 // picks the fastest measured split (M=128: 4 and 16; M=512, K=11008: 4).
-int rb_ksw(const Weights& w, int M)
+int rb_ksw(const Weights& w, const Knobs& kn, int M)
 {
     const int G = w.K / 128;
     const int64_t tiles = (int64_t)((M + kRbBM - 1) / kRbBM) * ((w.N + kRbBN - 1) / kRbBN);
-    if (g_rb_ksw > 0) return std::max(1, std::min(g_rb_ksw, G));
+    if (kn.rb_ksw() > 0) return std::max(1, std::min(kn.rb_ksw(), G));
     const int cus = device_cus();
     const double t_block = 3.5e-6, hbm = 4.0e12, t_launch = 2e-6;
     const double ybytes = (double)M * w.N * 4;
@@ -828,66 +894,46 @@ int rb_ksw(const Weights& w, int M)
 // (M=128: 49 / 45 us against 78 / 143 us; M=512, K=11008: 103 against 154 us), while
 // with more tiles the pipelined kernel is faster (M=512, K=4096: 100 against 118 us;
 // M=2048: 262 against 320-355 us).
-bool use_rb(const Weights& w, int M)
+bool use_rb(const Weights& w, const Knobs& kn, int M)
 {
-    if (!rb_eligible(w, M)) return false;
-    if (g_rb == 2 || !pipe_eligible(w, M)) return true;
-    const int64_t tiles = (int64_t)((M + kPipeBM - 1) / kPipeBM) * ((w.N + kPipeBN - 1) / kPipeBN);
-    const PipeSplit sp = pipe_split(w, M);
-    const int64_t items = sp.full + 2 * (tiles - sp.full);
+    if (!rb_eligible(w, kn, M)) return false;
+    if (kn.rb() == 2 || !pipe_eligible(w, kn, M)) return true;
+    const PipeSplit sp = pipe_split(w, kn, M);
+    const int64_t items = sp.full + 2 * (sp.tiles - sp.full);
     return 2 * items < device_cus();
 }
 
-// Returns 1 when launched, 0 when the caller should take another kernel (the workspace
-// would have to grow under capture), negative on a launch error.
-int launch_rb(Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
+// Workspace of an mfma_w4_rb launch: fp16 A and row exponents, then ksw slices of Y
+// (one when K is not split: the reduce applies the row exponents).
+struct RbWs {
+    size_t data, part_off;
+    int64_t slice;
+};
+RbWs rb_ws(const Weights& w, int M, int ksw)
+{
+    RbWs r;
+    r.slice = ((int64_t)M * w.N + 3) / 4 * 4;   // floats per K-split slice, 16-byte multiple
+    r.part_off = a16_bytes(M, w.K);
+    r.data = r.part_off + (size_t)ksw * r.slice * sizeof(float);
+    return r;
+}
+
+int launch_rb(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, float* dY, int M, hipStream_t stream)
 {
     const int tiles_m = (M + kRbBM - 1) / kRbBM, tiles_n = (w.N + kRbBN - 1) / kRbBN;
-    const int ksw = rb_ksw(w, M);
-    const size_t need_a = (size_t)M * w.K * 2;
-    const int64_t slice = ((int64_t)M * w.N + 3) / 4 * 4;   // floats per K-split slice, 16-byte multiple
-    const size_t need_p = ksw > 1 ? (size_t)ksw * slice * sizeof(float) : 0;
-    uint32_t* ws = nullptr;
-    float* part = nullptr;
-    {
-        std::lock_guard<std::mutex> lock(w.ws_mu);
-        const bool grow_a = w.a16_bytes < need_a, grow_p = w.rbpart_bytes < need_p;
-        if (grow_a || grow_p) {
-            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-            if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
-                (void)hipGetLastError();
-                return 0;
-            }
-            if (hipStreamSynchronize(stream) != hipSuccess) return -1;
-        }
-        if (grow_a) {
-            if (w.d_a16 && hipFree(w.d_a16) != hipSuccess) return -1;
-            w.d_a16 = nullptr;
-            w.a16_bytes = 0;
-            if (hipMalloc(&w.d_a16, need_a) != hipSuccess) return -1;
-            w.a16_bytes = need_a;
-        }
-        if (grow_p) {
-            if (w.d_rbpart && hipFree(w.d_rbpart) != hipSuccess) return -1;
-            w.d_rbpart = nullptr;
-            w.rbpart_bytes = 0;
-            if (hipMalloc(&w.d_rbpart, need_p) != hipSuccess) return -1;
-            w.rbpart_bytes = need_p;
-        }
-        ws = w.d_a16;
-        part = w.d_rbpart;
-    }
-    const int64_t n8 = (int64_t)M * w.K / 8;
-    hipLaunchKernelGGL(a_to_f16_kernel,
-                       dim3((unsigned)std::min<int64_t>((n8 + 256 * kA16Groups - 1) / (256 * kA16Groups), 2048)),
-                       dim3(256), 0, stream, dA, ws, n8);
+    const int ksw = rb_ksw(w, kn, M);
+    const RbWs L = rb_ws(w, M, ksw);
+    uint32_t* a16 = reinterpret_cast<uint32_t*>(ws.data);
+    int* rexp = reinterpret_cast<int*>(ws.data + align256((size_t)M * w.K * 2));
+    float* part = reinterpret_cast<float*>(ws.data + L.part_off);
+    launch_a_rows_f16(dA, a16, rexp, M, w.K, stream);
     RbParams p;
     p.b = w.d_b;
     p.scales = w.d_scales;
     p.zp = w.has_zp ? w.d_zp : nullptr;
-    p.a16 = reinterpret_cast<const _Float16*>(ws);
-    p.out = ksw > 1 ? part : dY;
-    p.slice = slice;
+    p.a16 = reinterpret_cast<const _Float16*>(a16);
+    p.out = part;
+    p.slice = L.slice;
     p.row_bytes = (int)w.row_bytes;
     p.M = M;
     p.N = w.N;
@@ -900,44 +946,98 @@ int launch_rb(Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
     p.ksw = ksw;
     const int items = tiles_m * tiles_n * ksw;
     hipLaunchKernelGGL(mfma_w4_rb_kernel, dim3(((items + kXcds - 1) / kXcds) * kXcds), dim3(256), 0, stream, p);
-    if (ksw > 1) {
-        const int64_t slice4 = slice / 4;
-        hipLaunchKernelGGL(rb_reduce_kernel, dim3((unsigned)std::min<int64_t>((slice4 + 255) / 256, 8192)), dim3(256),
-                           0, stream, reinterpret_cast<const float4*>(part), dY, (int64_t)M * w.N, slice4, ksw);
-    }
-    return hipGetLastError() == hipSuccess ? 1 : -1;
+    const int slice4 = (int)(L.slice / 4);
+    hipLaunchKernelGGL(rb_reduce_kernel, dim3((unsigned)std::min((slice4 + 255) / 256, 8192)), dim3(256), 0, stream,
+                       reinterpret_cast<const float4*>(part), dY, rexp, M * w.N, w.N, slice4, ksw);
+    MS_HIP_CHECK(hipGetLastError());
+    return MS_HIP_OK;
 }
 
-int enqueue_gemm(Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
+// ---- dispatch ------------------------------------------------------------------------------
+// Which kernel a call with M rows takes (ids of ms_hip_nbits_launch_info).
+enum KernelId { kGeneric = 0, kGemv = 1, kMfma = 2, kPanel = 3, kPipe = 4, kSkinny = 5, kRb = 6 };
+
+KernelId choose_kernel(const Weights& w, const Knobs& kn, int M)
+{
+    if (!w.fast) return kGeneric;
+    if (M <= kPanelMaxM) {
+        if (skinny_eligible(w, kn, M)) return kSkinny;
+        return pick_gemv_config(w, kn, M, w.N) >= 0 ? kGemv : kPanel;
+    }
+    if (use_rb(w, kn, M)) return kRb;
+    if (pipe_eligible(w, kn, M)) return kPipe;
+    return kMfma;
+}
+
+// Workspace (data bytes, counters) that kernel `k` needs for a call with M rows.
+void workspace_need(const Weights& w, const Knobs& kn, KernelId k, int M, size_t* data, size_t* cnt)
+{
+    *data = 0;
+    *cnt = 0;
+    if (k == kSkinny) {
+        const SkinnyWs L = skinny_ws(w, skinny_ksw(w, kn));
+        *data = L.data;
+        *cnt = L.cnt;
+    } else if (k == kRb) {
+        *data = rb_ws(w, M, rb_ksw(w, kn, M)).data;
+    } else if (k == kPipe) {
+        const PipeWs L = pipe_ws(w, M, pipe_split(w, kn, M));
+        *data = L.data;
+        *cnt = L.cnt;
+    }
+}
+
+// The kernel a call takes when its workspace cannot be had (growth under capture).
+KernelId workspace_free_kernel(const Weights& w, const Knobs& kn, int M)
+{
+    if (M <= kPanelMaxM) return pick_gemv_config(w, kn, M, w.N) >= 0 ? kGemv : kPanel;
+    return kMfma;
+}
+
+int launch_kernel(Weights& w, const Knobs& kn, KernelId k, const Ws& ws, const float* dA, float* dY, int M,
+                  hipStream_t stream)
+{
+    switch (k) {
+        case kGeneric: return launch_generic(w, dA, dY, M, stream);
+        case kGemv:
+        case kPanel: return launch_gemv(w, kn, dA, dY, M, stream);
+        case kSkinny: return launch_skinny(w, kn, ws, dA, dY, M, stream);
+        case kRb: return launch_rb(w, kn, ws, dA, dY, M, stream);
+        case kPipe: return launch_pipe(w, kn, ws, dA, dY, M, stream);
+        case kMfma:
+            return launch_mfma(w.d_b, w.d_scales, w.has_zp ? w.d_zp : nullptr, w.row_bytes, w.N, w.K, w.nb, w.zrb,
+                               w.log2cpb, dA, dY, M, stream)
+                       ? fail(MS_HIP_ERR_HIP, "[ms_hip] MFMA launch failed: %s", hipGetErrorString(hipGetLastError()))
+                       : MS_HIP_OK;
+    }
+    return fail(MS_HIP_ERR_HIP, "[ms_hip] no kernel");
+}
+
+int check_call(const float* dA, float* dY, int M)
 {
     if (M < 0) return fail(MS_HIP_ERR_INVALID, "MatMulNBits M must be non-negative; got %d.", M);
-    if (M == 0) return MS_HIP_OK;
-    if (!dA || !dY) return fail(MS_HIP_ERR_INVALID, "[ms_hip] null activation or output pointer");
-    if ((reinterpret_cast<uintptr_t>(dA) & 15) || (reinterpret_cast<uintptr_t>(dY) & 3))
+    if (M > 0 && (!dA || !dY)) return fail(MS_HIP_ERR_INVALID, "[ms_hip] null activation or output pointer");
+    if (M > 0 && ((reinterpret_cast<uintptr_t>(dA) & 15) || (reinterpret_cast<uintptr_t>(dY) & 3)))
         return fail(MS_HIP_ERR_INVALID, "[ms_hip] A must be 16-byte and Y 4-byte aligned");
-    if (!w.fast) return launch_generic(w, dA, dY, M, stream);
-    if (M <= kPanelMaxM) {
-        if (skinny_eligible(w, M)) {
-            const int r = launch_skinny(w, dA, dY, M, stream);
-            if (r < 0) return fail(MS_HIP_ERR_HIP, "[ms_hip] small-M launch failed: %s", hipGetErrorString(hipGetLastError()));
-            if (r > 0) return MS_HIP_OK;
-        }
-        return launch_gemv(w, dA, dY, M, stream);
+    return MS_HIP_OK;
+}
+
+// One call with the handle's own (growable) workspace.
+int enqueue_gemm(Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
+{
+    int st = check_call(dA, dY, M);
+    if (st || M == 0) return st;
+    const Knobs kn = knobs_of(w);
+    KernelId k = choose_kernel(w, kn, M);
+    size_t need_d = 0, need_c = 0;
+    workspace_need(w, kn, k, M, &need_d, &need_c);
+    Ws ws;
+    if (need_d || need_c) {
+        const int r = ensure_ws(w, need_d, need_c, stream, &ws);
+        if (r < 0) return fail(MS_HIP_ERR_HIP, "[ms_hip] workspace allocation failed: %s", hipGetErrorString(hipGetLastError()));
+        if (r == 0) k = workspace_free_kernel(w, kn, M);
     }
-    if (use_rb(w, M)) {
-        const int r = launch_rb(w, dA, dY, M, stream);
-        if (r < 0) return fail(MS_HIP_ERR_HIP, "[ms_hip] prefill launch failed: %s", hipGetErrorString(hipGetLastError()));
-        if (r > 0) return MS_HIP_OK;
-    }
-    if (pipe_eligible(w, M)) {
-        const int r = launch_pipe(w, dA, dY, M, stream);
-        if (r < 0) return fail(MS_HIP_ERR_HIP, "[ms_hip] prefill launch failed: %s", hipGetErrorString(hipGetLastError()));
-        if (r > 0) return MS_HIP_OK;
-    }
-    return launch_mfma(w.d_b, w.d_scales, w.has_zp ? w.d_zp : nullptr, w.row_bytes, w.N, w.K, w.nb,
-                       w.zrb, w.log2cpb, dA, dY, M, stream)
-               ? fail(MS_HIP_ERR_HIP, "[ms_hip] MFMA launch failed: %s", hipGetErrorString(hipGetLastError()))
-               : MS_HIP_OK;
+    return launch_kernel(w, kn, k, ws, dA, dY, M, stream);
 }
 
 int check_impl(int N, int K, int bits, int bs, int64_t b_len, int64_t scales_len, int zp_kind, int64_t zp_len,
@@ -979,12 +1079,47 @@ int check_impl(int N, int K, int bits, int bs, int64_t b_len, int64_t scales_len
     return MS_HIP_OK;
 }
 
-int alloc_weights(Weights& w, int has_zp)
+// A new handle for the layout (N, K, bits, bs): device buffers for the weights and the
+// pinned error word. On failure everything is freed and *out stays null.
+int new_weights(int N, int K, int bits, int bs, int has_zp, Weights** out)
 {
-    w.has_zp = has_zp;
-    MS_HIP_CHECK(hipMalloc(&w.d_b, (size_t)w.N * w.row_bytes));
-    MS_HIP_CHECK(hipMalloc(&w.d_scales, (size_t)w.N * w.nb * sizeof(float)));
-    if (has_zp) MS_HIP_CHECK(hipMalloc(&w.d_zp, (size_t)w.N * w.zrb));
+    *out = nullptr;
+    Weights* w = new Weights();
+    for (auto& k : w->knob) k.store(MS_HIP_TUNING_INHERIT);
+    w->device = device_info().device;
+    derive_layout(*w, N, K, bits, bs);
+    w->has_zp = has_zp;
+    hipError_t e = hipMalloc(&w->d_b, (size_t)N * w->row_bytes);
+    if (e == hipSuccess) e = hipMalloc(&w->d_scales, (size_t)N * w->nb * sizeof(float));
+    if (e == hipSuccess && has_zp) e = hipMalloc(&w->d_zp, (size_t)N * w->zrb);
+    if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&w->h_err), 64, hipHostMallocMapped);
+    if (e == hipSuccess) {
+        *w->h_err = 0;
+        e = hipHostGetDevicePointer(reinterpret_cast<void**>(&w->d_err), w->h_err, 0);
+    }
+    if (e != hipSuccess) {
+        const int st = fail(MS_HIP_ERR_HIP, "[ms_hip] weight allocation failed: %s", hipGetErrorString(e));
+        free_weights(*w);
+        delete w;
+        return st;
+    }
+    *out = w;
+    return MS_HIP_OK;
+}
+
+int finish_create(Weights* w, int st, void** out_handle)
+{
+    if (!st) st = check_pipe_scales(*w);
+    if (st) {
+        free_weights(*w);
+        delete w;
+        return st;
+    }
+    {
+        std::lock_guard<std::mutex> lock(g_live_mu);
+        g_live.insert(w);
+    }
+    *out_handle = w;
     return MS_HIP_OK;
 }
 
@@ -1021,27 +1156,13 @@ int ms_hip_nbits_weights_create(const uint8_t* bq, int64_t bq_len, const float* 
     if (!bq || !scales) return fail(MS_HIP_ERR_INVALID, "[ms_hip] null B or scales pointer");
     if ((st = require_device())) return st;
     MS_HIP_CHECK(hipSetDevice(device_info().device));
-    HandleBox* box = new HandleBox();
-    Weights& w = box->w;
-    w.device = device_info().device;
-    derive_layout(w, N, K, bits, block_size);
-    st = alloc_weights(w, zero_points != nullptr);
-    if (!st) {
-        hipError_t e = hipMemcpy(w.d_b, bq, (size_t)N * w.row_bytes, hipMemcpyHostToDevice);
-        if (e == hipSuccess)
-            e = hipMemcpy(w.d_scales, scales, (size_t)N * w.nb * sizeof(float), hipMemcpyHostToDevice);
-        if (e == hipSuccess && zero_points)
-            e = hipMemcpy(w.d_zp, zero_points, (size_t)N * w.zrb, hipMemcpyHostToDevice);
-        if (e != hipSuccess) st = fail(MS_HIP_ERR_HIP, "[ms_hip] weight upload failed: %s", hipGetErrorString(e));
-        if (!st) st = check_pipe_scales(w);
-    }
-    if (st) {
-        free_weights(w);
-        delete box;
-        return st;
-    }
-    *out_handle = box;
-    return MS_HIP_OK;
+    Weights* w = nullptr;
+    if ((st = new_weights(N, K, bits, block_size, zero_points != nullptr, &w))) return st;
+    hipError_t e = hipMemcpy(w->d_b, bq, (size_t)N * w->row_bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(w->d_scales, scales, (size_t)N * w->nb * sizeof(float), hipMemcpyHostToDevice);
+    if (e == hipSuccess && zero_points) e = hipMemcpy(w->d_zp, zero_points, (size_t)N * w->zrb, hipMemcpyHostToDevice);
+    if (e != hipSuccess) st = fail(MS_HIP_ERR_HIP, "[ms_hip] weight upload failed: %s", hipGetErrorString(e));
+    return finish_create(w, st, out_handle);
 }
 
 int ms_hip_nbits_weights_create_dev(const uint8_t* d_bq, const float* d_scales, const uint8_t* d_zero_points,
@@ -1056,41 +1177,32 @@ int ms_hip_nbits_weights_create_dev(const uint8_t* d_bq, const float* d_scales, 
     if (!d_bq || !d_scales) return fail(MS_HIP_ERR_INVALID, "[ms_hip] null B or scales pointer");
     if ((st = require_device())) return st;
     MS_HIP_CHECK(hipSetDevice(device_info().device));
-    HandleBox* box = new HandleBox();
-    Weights& w = box->w;
-    w.device = device_info().device;
-    derive_layout(w, N, K, bits, block_size);
-    st = alloc_weights(w, d_zero_points != nullptr);
-    if (!st) {
-        hipError_t e = hipMemcpy(w.d_b, d_bq, (size_t)N * w.row_bytes, hipMemcpyDeviceToDevice);
-        if (e == hipSuccess)
-            e = hipMemcpy(w.d_scales, d_scales, (size_t)N * w.nb * sizeof(float), hipMemcpyDeviceToDevice);
-        if (e == hipSuccess && d_zero_points)
-            e = hipMemcpy(w.d_zp, d_zero_points, (size_t)N * w.zrb, hipMemcpyDeviceToDevice);
-        if (e != hipSuccess) st = fail(MS_HIP_ERR_HIP, "[ms_hip] weight copy failed: %s", hipGetErrorString(e));
-        if (!st) st = check_pipe_scales(w);
-    }
-    if (st) {
-        free_weights(w);
-        delete box;
-        return st;
-    }
-    *out_handle = box;
-    return MS_HIP_OK;
+    Weights* w = nullptr;
+    if ((st = new_weights(N, K, bits, block_size, d_zero_points != nullptr, &w))) return st;
+    hipError_t e = hipMemcpy(w->d_b, d_bq, (size_t)N * w->row_bytes, hipMemcpyDeviceToDevice);
+    if (e == hipSuccess) e = hipMemcpy(w->d_scales, d_scales, (size_t)N * w->nb * sizeof(float), hipMemcpyDeviceToDevice);
+    if (e == hipSuccess && d_zero_points)
+        e = hipMemcpy(w->d_zp, d_zero_points, (size_t)N * w->zrb, hipMemcpyDeviceToDevice);
+    if (e != hipSuccess) st = fail(MS_HIP_ERR_HIP, "[ms_hip] weight copy failed: %s", hipGetErrorString(e));
+    return finish_create(w, st, out_handle);
 }
 
 int ms_hip_nbits_weights_destroy(void* handle)
 {
-    Weights* w = from_handle(handle);
-    if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
+    {
+        std::lock_guard<std::mutex> lock(g_live_mu);
+        if (!handle || !g_live.erase(handle)) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
+    }
+    Weights* w = static_cast<Weights*>(handle);
     {
         std::lock_guard<std::mutex> lock(w->mu);
         if (w->stream) (void)hipStreamSynchronize(w->stream);
+        // Device-pointer calls may still be in flight on other streams: their kernels use
+        // the weights and the workspace until they finish.
+        (void)hipDeviceSynchronize();
         free_weights(*w);
     }
-    HandleBox* box = static_cast<HandleBox*>(handle);
-    box->magic = 0;
-    delete box;
+    delete w;
     return MS_HIP_OK;
 }
 
@@ -1110,7 +1222,17 @@ int ms_hip_nbits_gemm_dev(void* handle, const float* dA, float* dY, int M, void*
 {
     Weights* w = from_handle(handle);
     if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
-    return enqueue_gemm(*w, dA, dY, M, static_cast<hipStream_t>(stream));
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const int st = take_device_error(*w, s);
+    if (st) return st;
+    return enqueue_gemm(*w, dA, dY, M, s);
+}
+
+int ms_hip_nbits_device_error(void* handle)
+{
+    Weights* w = from_handle(handle);
+    if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
+    return take_device_error(*w, nullptr);
 }
 
 int ms_hip_nbits_gemm_dev_batch(void* const* handles, const float* const* dA, float* const* dY, int count, int M,
@@ -1118,23 +1240,29 @@ int ms_hip_nbits_gemm_dev_batch(void* const* handles, const float* const* dA, fl
 {
     if (count < 0 || (count > 0 && (!handles || !dA || !dY)))
         return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid batch arguments");
+    std::vector<Weights*> ws((size_t)count);
     for (int i = 0; i < count; ++i)
-        if (!from_handle(handles[i])) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle at batch index %d", i);
+        if (!(ws[i] = from_handle(handles[i])))
+            return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle at batch index %d", i);
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    for (int i = 0; i < count; ++i) {
+        const int st = take_device_error(*ws[i], s);
+        if (st) return st;
+    }
     for (int i = 0; i < count;) {
         int ci = -1;
-        const int n = batch_group(handles + i, dA + i, count - i, M, &ci);
+        const int n = batch_group(ws.data() + i, dA + i, count - i, M, &ci);
         if (n > 1) {
             GemvMember mem[kGemvMaxOps];
             for (int j = 0; j < n; ++j) {
                 if (!dY[i + j] || (reinterpret_cast<uintptr_t>(dY[i + j]) & 3))
                     return fail(MS_HIP_ERR_INVALID, "[ms_hip] null or misaligned output at batch index %d", i + j);
-                mem[j] = GemvMember{from_handle(handles[i + j]), dY[i + j]};
+                mem[j] = GemvMember{ws[i + j], dY[i + j]};
             }
             const int st = launch_gemv_group(mem, n, dA[i], M, ci, s);
             if (st) return st;
         } else {
-            const int st = enqueue_gemm(*from_handle(handles[i]), dA[i], dY[i], M, s);
+            const int st = enqueue_gemm(*ws[i], dA[i], dY[i], M, s);
             if (st) return st;
         }
         i += n;
@@ -1146,18 +1274,20 @@ int ms_hip_nbits_batch_launch_info(void* const* handles, const float* const* dA,
                                    int* kernel_id, int* lanes_per_row, int* grid, int* block)
 {
     if (count <= 0 || !handles || !dA) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid batch arguments");
+    std::vector<Weights*> ws((size_t)count);
     for (int i = 0; i < count; ++i)
-        if (!from_handle(handles[i])) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle at batch index %d", i);
+        if (!(ws[i] = from_handle(handles[i])))
+            return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle at batch index %d", i);
     if (M <= 0) return fail(MS_HIP_ERR_INVALID, "[ms_hip] M must be positive; got %d", M);
     int ci = -1;
-    const int n = batch_group(handles, dA, count, M, &ci);
+    const int n = batch_group(ws.data(), dA, count, M, &ci);
     if (calls) *calls = n;
     if (n == 1) return ms_hip_nbits_launch_info(handles[0], M, kernel_id, lanes_per_row, grid, block);
     const GemvConfig& c = kGemvConfigs[ci];
     const int rows = gemv_rows(c);
     int gr = 0;
-    for (int j = 0; j < n; ++j) gr += (from_handle(handles[j])->N + rows - 1) / rows;
-    if (kernel_id) *kernel_id = 1;
+    for (int j = 0; j < n; ++j) gr += (ws[j]->N + rows - 1) / rows;
+    if (kernel_id) *kernel_id = kGemv;
     if (lanes_per_row) *lanes_per_row = c.G;
     if (grid) *grid = gr;
     if (block) *block = c.waves * kWave;
@@ -1175,8 +1305,10 @@ int ms_hip_nbits_gemm(void* handle, const float* a_host, float* y_host, int M)
     MS_HIP_CHECK(hipSetDevice(w->device));
     if (!w->stream) MS_HIP_CHECK(hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking));
     const size_t a_bytes = (size_t)M * w->K * sizeof(float);
-    const size_t a_span = (a_bytes + 255) & ~(size_t)255;
+    const size_t a_span = align256(a_bytes);
     const size_t y_bytes = (size_t)M * w->N * sizeof(float);
+    // Device staging, and pinned host staging: the copies then run as DMA at full PCIe
+    // rate instead of going through the runtime's pageable bounce buffers.
     if (w->stage_bytes < a_span + y_bytes) {
         if (w->d_stage) MS_HIP_CHECK(hipFree(w->d_stage));
         w->d_stage = nullptr;
@@ -1184,16 +1316,31 @@ int ms_hip_nbits_gemm(void* handle, const float* a_host, float* y_host, int M)
         MS_HIP_CHECK(hipMalloc(&w->d_stage, a_span + y_bytes));
         w->stage_bytes = a_span + y_bytes;
     }
+    if (w->h_stage_bytes < a_span + y_bytes) {
+        if (w->h_stage) MS_HIP_CHECK(hipHostFree(w->h_stage));
+        w->h_stage = nullptr;
+        w->h_stage_bytes = 0;
+        MS_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&w->h_stage), a_span + y_bytes, hipHostMallocDefault));
+        w->h_stage_bytes = a_span + y_bytes;
+    }
     float* dA = w->d_stage;
     float* dY = reinterpret_cast<float*>(reinterpret_cast<char*>(w->d_stage) + a_span);
-    MS_HIP_CHECK(hipMemcpyAsync(dA, a_host, a_bytes, hipMemcpyHostToDevice, w->stream));
-    const int st = enqueue_gemm(*w, dA, dY, M, w->stream);
+    float* hY = reinterpret_cast<float*>(w->h_stage + a_span);
+    std::memcpy(w->h_stage, a_host, a_bytes);
+    MS_HIP_CHECK(hipMemcpyAsync(dA, w->h_stage, a_bytes, hipMemcpyHostToDevice, w->stream));
+    int st = take_device_error(*w, w->stream);
+    if (!st) st = enqueue_gemm(*w, dA, dY, M, w->stream);
     if (st) {
         (void)hipStreamSynchronize(w->stream);
         return st;
     }
-    MS_HIP_CHECK(hipMemcpyAsync(y_host, dY, y_bytes, hipMemcpyDeviceToHost, w->stream));
+    MS_HIP_CHECK(hipMemcpyAsync(hY, dY, y_bytes, hipMemcpyDeviceToHost, w->stream));
     MS_HIP_CHECK(hipStreamSynchronize(w->stream));
+    if ((st = take_device_error(*w, w->stream))) {
+        (void)hipStreamSynchronize(w->stream);
+        return st;
+    }
+    std::memcpy(y_host, hY, y_bytes);
     return MS_HIP_OK;
 }
 
@@ -1284,49 +1431,48 @@ int ms_hip_sync(void)
     return MS_HIP_OK;
 }
 
-int ms_hip_set_gemv_lanes(int lanes_per_row)
-{
-    if (lanes_per_row != 0 && lanes_per_row != 16 && lanes_per_row != 32 && lanes_per_row != 64)
-        return fail(MS_HIP_ERR_INVALID, "[ms_hip] lanes_per_row must be 0, 16, 32 or 64; got %d", lanes_per_row);
-    g_panel_lanes_override = lanes_per_row;
-    return MS_HIP_OK;
-}
+int ms_hip_set_gemv_lanes(int lanes_per_row) { return ms_hip_set_tuning(0, lanes_per_row); }
 
 int ms_hip_set_tuning(int knob, int value)
 {
-    switch (knob) {
-        case 0: return ms_hip_set_gemv_lanes(value);
-        case 1:
-            if (value < -1 || value > kNumGemvConfigs) break;
-            g_gemv_config = value;
-            return MS_HIP_OK;
-        case 2:
-            if (value != 0 && value != 1) break;
-            g_pipe_off = value;
-            return MS_HIP_OK;
-        case 3:
-            if (value < 0 || value > 3) break;
-            g_pipe_ksplit = value;
-            return MS_HIP_OK;
-        case 4:
-            if (value < 0 || value > 2) break;
-            g_skinny = value;
-            return MS_HIP_OK;
-        case 5:
-            if (value < 0 || value > 64) break;
-            g_skinny_ksw = value;
-            return MS_HIP_OK;
-        case 6:
-            if (value < 0 || value > 2) break;
-            g_rb = value;
-            return MS_HIP_OK;
-        case 7:
-            if (value < 0 || value > 64) break;
-            g_rb_ksw = value;
-            return MS_HIP_OK;
-        default: break;
+    const int st = validate_knob(knob, value);
+    if (st) return st;
+    g_knob[knob].store(value, std::memory_order_relaxed);
+    return MS_HIP_OK;
+}
+
+int ms_hip_nbits_set_tuning(void* handle, int knob, int value)
+{
+    Weights* w = from_handle(handle);
+    if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
+    if (value != MS_HIP_TUNING_INHERIT) {
+        const int st = validate_knob(knob, value);
+        if (st) return st;
+    } else if (knob < 0 || knob >= kNumKnobs) {
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid tuning knob %d", knob);
     }
-    return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid tuning knob %d = %d", knob, value);
+    w->knob[knob].store(value, std::memory_order_relaxed);
+    return MS_HIP_OK;
+}
+
+int ms_hip_nbits_debug_set_counters(void* handle, int value, int next_epoch_tag)
+{
+    Weights* w = from_handle(handle);
+    if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
+    std::lock_guard<std::mutex> lock(w->mu);
+    std::lock_guard<std::mutex> wlock(w->ws_mu);
+    if (!w->ws.cnt) return fail(MS_HIP_ERR_INVALID, "[ms_hip] the handle has no split-K counters yet");
+    MS_HIP_CHECK(hipDeviceSynchronize());
+    int v = value;
+    if (next_epoch_tag) {   // the tag the next split-K launch will carry
+        const uint32_t e = g_epoch.load(std::memory_order_relaxed);
+        v = (int)(e % 0x7FFFFFFEu) + 1;
+    }
+    // Pairs of (arrival tag, ready flag): tags set, flags cleared.
+    std::vector<int> fill(w->ws.cnt_ints, 0);
+    for (size_t i = 0; i < fill.size(); i += 2) fill[i] = v;
+    MS_HIP_CHECK(hipMemcpy(w->ws.cnt, fill.data(), fill.size() * sizeof(int), hipMemcpyHostToDevice));
+    return MS_HIP_OK;
 }
 
 int ms_hip_nbits_launch_info(void* handle, int M, int* kernel_id, int* lanes_per_row, int* grid, int* block)
@@ -1334,44 +1480,36 @@ int ms_hip_nbits_launch_info(void* handle, int M, int* kernel_id, int* lanes_per
     Weights* w = from_handle(handle);
     if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
     if (M <= 0) return fail(MS_HIP_ERR_INVALID, "[ms_hip] M must be positive; got %d", M);
-    int kid = 0, G = 0, gr = 0, bl = 0;
-    if (!w->fast) {
-        kid = 0;
-        gr = (int)(((int64_t)M * w->N + 255) / 256);
-        bl = 256;
-    } else if (M <= kPanelMaxM && skinny_eligible(*w, M)) {
-        kid = 5;
-        gr = ((w->N + kSkinnyRows - 1) / kSkinnyRows) * skinny_ksw(*w);
-        bl = 256;
-    } else if (M <= kPanelMaxM) {
-        const int ci = pick_gemv_config(*w, M, w->N);
-        if (ci >= 0) {
-            const GemvConfig& c = kGemvConfigs[ci];
-            const int rows = gemv_rows(c);
-            kid = 1;
+    const Knobs kn = knobs_of(*w);
+    const KernelId kid = choose_kernel(*w, kn, M);
+    int G = 0, gr = 0, bl = 256;
+    switch (kid) {
+        case kGeneric: gr = (int)(((int64_t)M * w->N + 255) / 256); break;
+        case kSkinny: gr = ((w->N + kSkinnyRows - 1) / kSkinnyRows) * skinny_ksw(*w, kn); break;
+        case kGemv: {
+            const GemvConfig& c = kGemvConfigs[pick_gemv_config(*w, kn, M, w->N)];
             G = c.G;
-            gr = (w->N + rows - 1) / rows;
+            gr = (w->N + gemv_rows(c) - 1) / gemv_rows(c);
             bl = c.waves * kWave;
-        } else {
-            const PanelShape s = panel_shape(*w, M);
-            kid = 3;
+            break;
+        }
+        case kPanel: {
+            const PanelShape s = panel_shape(*w, kn, M);
             G = s.G;
             gr = s.grid;
             bl = kPanelThreads;
+            break;
         }
-    } else if (use_rb(*w, M)) {
-        kid = 6;
-        gr = ((M + kRbBM - 1) / kRbBM) * ((w->N + kRbBN - 1) / kRbBN) * rb_ksw(*w, M);
-        gr = ((gr + kXcds - 1) / kXcds) * kXcds;
-        bl = 256;
-    } else if (pipe_eligible(*w, M)) {
-        kid = 4;
-        const PipeSplit sp = pipe_split(*w, M);
-        gr = kXcds * (sp.xu + sp.xv);
-        bl = 256;
-    } else {
-        kid = 2;
-        mfma_launch_shape(w->N, M, &gr, &bl);
+        case kRb:
+            gr = ((M + kRbBM - 1) / kRbBM) * ((w->N + kRbBN - 1) / kRbBN) * rb_ksw(*w, kn, M);
+            gr = ((gr + kXcds - 1) / kXcds) * kXcds;
+            break;
+        case kPipe: {
+            const PipeSplit sp = pipe_split(*w, kn, M);
+            gr = kXcds * (sp.xu + sp.xv);
+            break;
+        }
+        case kMfma: mfma_launch_shape(w->N, M, &gr, &bl); break;
     }
     if (kernel_id) *kernel_id = kid;
     if (lanes_per_row) *lanes_per_row = G;

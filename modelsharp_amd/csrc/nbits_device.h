@@ -3,9 +3,10 @@
 // Dequantization is W[n,k] = ((float)q - zp) * scale with q the 4-bit code of
 // column k in row n and zp an integer, as in
 // src/ModelSharp/Cpu/Kernels/Quantize/MatMulNBitsSimd.cs:100-111. For integer
-// zp, q - zp is exact, so the product is the only rounding. The library is
-// compiled with -ffp-contract=off, so that product is never fused into the
-// accumulation that follows it; the accumulations are explicit fmaf.
+// zp, q - zp is exact (the kernels form it in fp16 with the packed-half trick
+// below), so the product with the scale is the only rounding. The library is
+// compiled with -ffp-contract=off, so no product is fused into the accumulation
+// that follows it; the accumulations are explicit fmaf.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -28,67 +29,6 @@ __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t o
     uint32_t r;
     asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(orv));
     return r;
-}
-
-// fp32 fma(fp16 lane of h2 widened, s, c): with c = -0.0 (the additive
-// identity) this is the single rounding of (float)h * s.
-__device__ __forceinline__ float mix_lo(uint32_t h2, float s, float c)
-{
-    float r;
-    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(s), "s"(c));
-    return r;
-}
-__device__ __forceinline__ float mix_hi(uint32_t h2, float s, float c)
-{
-    float r;
-    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(s), "s"(c));
-    return r;
-}
-
-// Per-block dequant constants. A 4-bit code sitting in bits 0-3 of an fp16
-// lane with exponent bits 0x6400 reads as 1024 + q; sitting in bits 4-7 it
-// reads as 1024 + 16q. Subtracting 1024 + zp (resp. 1024 + 16zp) in packed fp16
-// is exact and leaves d = q - zp (resp. 16(q - zp)); the fp32 product with s
-// (resp. s/16, exact by a power of two for |s| >= 2^-122) is then the single
-// rounding of (q - zp) * s.
-struct BlockDq {
-    h2_t zb;     // (1024 + zp) x2
-    h2_t zb16;   // (1024 + 16 zp) x2
-    float s;     // scale
-    float s16;   // scale / 16
-};
-
-__device__ __forceinline__ BlockDq block_dq(int zp, float s)
-{
-    BlockDq q;
-    q.zb = as_h2(kHalfMagic | ((uint32_t)zp << 16) | (uint32_t)zp);
-    q.zb16 = as_h2(kHalfMagic | ((uint32_t)zp << 20) | ((uint32_t)zp << 4));
-    q.s = s;
-    q.s16 = s * 0.0625f;
-    return q;
-}
-
-// Dequantizes the eight 4-bit codes of one little-endian dword (codes for
-// k = 8j .. 8j+7 of a chunk: byte i holds k=2i in its low nibble and k=2i+1 in
-// its high nibble) to fp32, w[i] for k = 8j + i. 25 VALU ops for 8 weights:
-// one shift, four and_or, four packed fp16 subtracts, eight fma_mix.
-__device__ __forceinline__ void dequant8(uint32_t x, const BlockDq& q, float (&w)[8])
-{
-    const uint32_t magic = kHalfMagic;
-    const uint32_t x8 = x >> 8;
-    const uint32_t d0 = as_u32(as_h2(and_or(x, 0x000F000Fu, magic)) - q.zb);      // k0, k4
-    const uint32_t d1 = as_u32(as_h2(and_or(x, 0x00F000F0u, magic)) - q.zb16);    // 16*k1, 16*k5
-    const uint32_t d2 = as_u32(as_h2(and_or(x8, 0x000F000Fu, magic)) - q.zb);     // k2, k6
-    const uint32_t d3 = as_u32(as_h2(and_or(x8, 0x00F000F0u, magic)) - q.zb16);   // 16*k3, 16*k7
-    const float nz = -0.0f;
-    w[0] = mix_lo(d0, q.s, nz);
-    w[4] = mix_hi(d0, q.s, nz);
-    w[1] = mix_lo(d1, q.s16, nz);
-    w[5] = mix_hi(d1, q.s16, nz);
-    w[2] = mix_lo(d2, q.s, nz);
-    w[6] = mix_hi(d2, q.s, nz);
-    w[3] = mix_lo(d3, q.s16, nz);
-    w[7] = mix_hi(d3, q.s16, nz);
 }
 
 // acc + (float)h * a for the low / high fp16 lane of h2: an fp32 fma of the
@@ -116,6 +56,18 @@ __device__ __forceinline__ void diffs8(uint32_t x, h2_t zb, h2_t zb16, uint32_t 
     d[3] = as_u32(as_h2(and_or(x8, 0x00F000F0u, magic)) - zb16);
 }
 
+// (1024 + zp, 1024 + zp) and (1024 + 16 zp, 1024 + 16 zp) as fp16 pairs, the subtrahends
+// of diffs8() for a 4-bit zero point.
+__device__ __forceinline__ h2_t zp_half2(uint32_t zp) { return as_h2(kHalfMagic | (zp << 16) | zp); }
+__device__ __forceinline__ h2_t zp16_half2(uint32_t zp) { return as_h2(kHalfMagic | (zp << 20) | (zp << 4)); }
+
+// Activations staged for dot8(): the odd k (y, w of a float4 of k = 4i .. 4i+3) divided
+// by 16, exactly (a power of two).
+__device__ __forceinline__ float4 stage_odd16(const float4& v)
+{
+    return float4{v.x, v.y * 0.0625f, v.z, v.w * 0.0625f};
+}
+
 // acc + sum_i (q_i - zp) * a_i over the 8 codes whose diffs8() are d, with the
 // activations a0 = a[k0..k3], a1 = a[k4..k7] staged with the odd k pre-divided
 // by 16 (exact: a power of two), which cancels the 16 in d[1], d[3]. Every
@@ -136,16 +88,14 @@ __device__ __forceinline__ float dot8(const uint32_t (&d)[4], const float4& a0, 
 // ---- shared by the GEMV kernels ---------------------------------------------------
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
-// A staged activation chunk in LDS: 32 activations pre-scaled (even k by 2^24, odd
-// k by 2^20) in 8 float4, then (sum of the 32 unscaled activations, 0, 0, 0). The
-// ninth float4 also pads the chunk stride off a power of two (fewer bank conflicts).
+// A staged activation chunk in LDS: 32 activations (odd k divided by 16) in 8 float4,
+// then one float4 of padding that keeps the chunk stride off a power of two (fewer bank
+// conflicts).
 constexpr int kChunkStride4 = 9;
 // A buffer offset beyond every resource the kernels build: a load from it returns
 // zero and makes no memory request.
 constexpr int kOOB = 0x7ffffff0;
 constexpr uint32_t kBufferWord3 = 0x00020000u;   // raw buffer resource, gfx9 data format
-constexpr float kTwo24 = 16777216.0f;            // 2^24
-constexpr float kTwo20 = 1048576.0f;             // 2^20
 
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes)
@@ -221,48 +171,11 @@ __device__ __forceinline__ void wait_vmem_order_only_acquire()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
-// acc + a * (fp16 lane widened) — one v_fma_mix_f32.
-__device__ __forceinline__ float mix_lo_acc(uint32_t h2, float a, float acc)
-{
-    return __builtin_fmaf((float)as_h2(h2).x, a, acc);
-}
-__device__ __forceinline__ float mix_hi_acc(uint32_t h2, float a, float acc)
-{
-    return __builtin_fmaf((float)as_h2(h2).y, a, acc);
-}
-
-// The four masked code pairs of dword x: p[0] = (k0, k4) and p[2] = (k2, k6) as
-// q * 2^-24, p[1] = (k1, k5) and p[3] = (k3, k7) as 16 q * 2^-24.
-__device__ __forceinline__ void code_pairs(uint32_t x, uint32_t (&p)[4])
-{
-    const uint32_t x8 = x >> 8;
-    p[0] = x & 0x000F000Fu;
-    p[1] = x & 0x00F000F0u;
-    p[2] = x8 & 0x000F000Fu;
-    p[3] = x8 & 0x00F000F0u;
-}
-
 // Packed zero point of block `blk` from a row of packed nibbles
 // (MatMulNBitsKernel.cs:349-356 with bits=4).
 __device__ __forceinline__ int zp_nibble(const uint8_t* zrow, int blk)
 {
     return (zrow[blk >> 1] >> ((blk & 1) * 4)) & 0x0F;
-}
-
-// acc + sum of a_k q_k over the 8 codes of one dword whose code_pairs() are p,
-// with a0 = a'[k0..k3], a1 = a'[k4..k7] staged pre-scaled. Every product is exact
-// inside its fma; one rounding per accumulation.
-__device__ __forceinline__ float qdot8(const uint32_t (&p)[4], const float4& a0, const float4& a1, float acc)
-{
-    acc = mix_lo_acc(p[0], a0.x, acc);
-    acc = mix_lo_acc(p[1], a0.y, acc);
-    acc = mix_lo_acc(p[2], a0.z, acc);
-    acc = mix_lo_acc(p[3], a0.w, acc);
-    acc = mix_hi_acc(p[0], a1.x, acc);
-    acc = mix_hi_acc(p[1], a1.y, acc);
-    acc = mix_hi_acc(p[2], a1.z, acc);
-    acc = mix_hi_acc(p[3], a1.w, acc);
-    return acc;
 }
 
 }  // namespace msnb

@@ -37,7 +37,7 @@ class HipMatMulNBitsKernel(IKernel):
 
     def __init__(self):
         self._lock = threading.Lock()
-        self._handles: dict[tuple, native.NBitsWeights] = {}
+        self._handles: dict[tuple, tuple] = {}
 
     # ---- validation: MatMulNBitsKernel.cs:79-161 ----------------------------------------
     @staticmethod
@@ -50,7 +50,8 @@ class HipMatMulNBitsKernel(IKernel):
         K = node.attr_int("K", 0)
         bits = node.attr_int("bits", 4)
         block_size = node.attr_int("block_size", 0)
-        scales = ctx.get(node.inputs[2])
+        # The raw tensor: widened to fp32 (GraphContext.cs:106) only when a handle is made.
+        scales = ctx.get_tensor(node.inputs[2])
         lib = native.load()
         st = lib.ms_hip_nbits_check(N, K, bits, block_size, int(np.prod(b.shape)), int(np.prod(scales.shape)),
                                     0, 0, -1)
@@ -79,23 +80,26 @@ class HipMatMulNBitsKernel(IKernel):
         return a, b, scales, zp, N, K, bits, block_size
 
     # ---- device-resident weights -----------------------------------------------------------
-    @staticmethod
-    def _key(node: GraphNode, b, scales, zp):
-        names = tuple(node.inputs[1:4])
-        return names + (id(b), id(scales), id(zp))
-
+    # One handle per (B, scales, zero points) initializer triple, keyed by the input names
+    # as the per-initializer residency of IlgpuEngine.ResidentOrTempInt keys by name
+    # (src/ModelSharp.Gpu/IlgpuEngine.cs:3396). The entry keeps the raw tensors it was made
+    # from: a context that binds those names to other tensors gets a new handle (the old
+    # one is closed), the same tensors always find the same handle.
     def _weights(self, node, b, scales, zp, N, K, bits, block_size) -> native.NBitsWeights:
         if zp is not None and element_type(zp) == "Float32":
             raise DeviceUnsupportedInput(
                 "MatMulNBits float zero_points are not representable in the HIP C ABI; "
                 "run this node on the managed kernel.")
-        key = self._key(node, b, scales, zp)
+        key = tuple(node.inputs[1:4])
         with self._lock:
-            w = self._handles.get(key)
-            if w is None:
-                w = native.NBitsWeights(_to_numpy(b), _to_numpy(scales).astype(np.float32),
-                                        None if zp is None else _to_numpy(zp), N, K, bits, block_size)
-                self._handles[key] = w
+            entry = self._handles.get(key)
+            if entry is not None and entry[0][0] is b and entry[0][1] is scales and entry[0][2] is zp:
+                return entry[1]
+            w = native.NBitsWeights(_to_numpy(b), _to_numpy(scales).astype(np.float32),
+                                    None if zp is None else _to_numpy(zp), N, K, bits, block_size)
+            if entry is not None:
+                entry[1].close()
+            self._handles[key] = ((b, scales, zp), w)
             return w
 
     def preload(self, graph: ModelGraph) -> int:
@@ -110,7 +114,7 @@ class HipMatMulNBitsKernel(IKernel):
             if not all(ctx.has(n) for n in names if n) or not ctx.has(node.inputs[1]):
                 continue
             b = ctx.get_tensor(node.inputs[1])
-            scales = ctx.get(node.inputs[2])
+            scales = ctx.get_tensor(node.inputs[2])
             zp = ctx.get_tensor(node.inputs[3]) if len(node.inputs) > 3 and ctx.has(node.inputs[3]) else None
             before = len(self._handles)
             self._weights(node, b, scales, zp, node.attr_int("N", 0), node.attr_int("K", 0),
@@ -120,9 +124,13 @@ class HipMatMulNBitsKernel(IKernel):
 
     def close(self) -> None:
         with self._lock:
-            for w in self._handles.values():
+            for _, w in self._handles.values():
                 w.close()
             self._handles.clear()
+
+    @property
+    def handle_count(self) -> int:
+        return len(self._handles)
 
     # ---- IKernel.Execute -------------------------------------------------------------------
     def execute(self, node: GraphNode, ctx: GraphContext) -> None:

@@ -27,6 +27,7 @@ MS_HIP_ERR_INVALID = 1
 MS_HIP_ERR_NO_DEVICE = 2
 MS_HIP_ERR_HIP = 3
 MS_HIP_ERR_UNSUPPORTED = 4
+MS_HIP_TUNING_INHERIT = -(2 ** 31)
 
 _c_int = ctypes.c_int
 _c_i64 = ctypes.c_int64
@@ -50,6 +51,7 @@ _PROTOTYPES = {
     "ms_hip_nbits_weights_info": (_c_int, [_vp, _ip, _ip, _ip, _ip, _ip]),
     "ms_hip_nbits_gemm": (_c_int, [_vp, _vp, _vp, _c_int]),
     "ms_hip_nbits_gemm_dev": (_c_int, [_vp, _vp, _vp, _c_int, _vp]),
+    "ms_hip_nbits_device_error": (_c_int, [_vp]),
     "ms_hip_nbits_gemm_dev_batch": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _vp]),
     "ms_hip_qgemm_nbits": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "ms_hip_nbits_dequant": (_c_int, [_vp, _vp]),
@@ -61,6 +63,8 @@ _PROTOTYPES = {
     "ms_hip_sync": (_c_int, []),
     "ms_hip_set_gemv_lanes": (_c_int, [_c_int]),
     "ms_hip_set_tuning": (_c_int, [_c_int, _c_int]),
+    "ms_hip_nbits_set_tuning": (_c_int, [_vp, _c_int, _c_int]),
+    "ms_hip_nbits_debug_set_counters": (_c_int, [_vp, _c_int, _c_int]),
     "ms_hip_nbits_launch_info": (_c_int, [_vp, _c_int, _ip, _ip, _ip, _ip]),
     "ms_hip_nbits_batch_launch_info": (_c_int, [_vp, _vp, _c_int, _c_int, _ip, _ip, _ip, _ip, _ip]),
 }
@@ -191,6 +195,18 @@ class NBitsWeights:
 
     def dequant_dev(self, dW: int, stream: int | None = None) -> None:
         check(load().ms_hip_nbits_dequant_dev(self.handle, _vp(dW), _vp(stream or 0)))
+
+    def set_tuning(self, knob: int, value: int) -> None:
+        """This handle's own value of a launch-shape knob (MS_HIP_TUNING_INHERIT: follow
+        the process default set by set_tuning())."""
+        check(load().ms_hip_nbits_set_tuning(self.handle, int(knob), int(value)))
+
+    def device_error(self) -> None:
+        """Raises HipError when a device-side failure was recorded since the last check."""
+        check(load().ms_hip_nbits_device_error(self.handle))
+
+    def debug_set_counters(self, value: int, next_epoch_tag: bool = False) -> None:
+        check(load().ms_hip_nbits_debug_set_counters(self.handle, int(value), int(bool(next_epoch_tag))))
 
     def launch_info(self, M: int) -> dict:
         k, g, gr, bl = (ctypes.c_int() for _ in range(4))

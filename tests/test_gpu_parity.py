@@ -468,7 +468,8 @@ def test_prefill_kernel_choice(gpu, op, kernel):
 
 
 def test_prefill_scale_range_fallback(gpu):
-    """Scales outside the fp16-normal range send the call to mfma_w4 (fp32 dequant)."""
+    """Scales outside the fp16-normal range send the call to mfma_w4 (fp32 scales, exact
+    integer weights)."""
     op = workloads.Op("tiny", 512, 96, 32, True)
     b, s, z = workloads.make_weights(op, 4)
     s = s.copy()
@@ -694,3 +695,163 @@ def test_batch_entry_matches_single_calls(gpu):
     for w, x, y in zip(ws, As, Ys):
         assert np.array_equal(y.cpu().numpy(), w.gemm(x.cpu().numpy()))
         w.close()
+
+
+# ---- fp16 range: every M > 16 path with inputs outside fp16's range ------------------------
+RANGE_CASES = [(op, M) for op in workloads.LLAMA7B_PREFILL_OPS for M in (17, 128, 2048)]
+
+
+@pytest.mark.parametrize("op,M", RANGE_CASES, ids=lambda v: str(v) if isinstance(v, int) else f"K{v.K}_N{v.N}")
+def test_prefill_dynamic_range(gpu, op, M):
+    """Activation outliers of 1e5 and 3e6, rows near 1e-6, and scales near 1e4 and 1e-6
+    (outside what fp16 carries) on both 7B MLP shapes: every output finite, relative
+    Frobenius error <= 2e-3 against the oracle on sampled columns, and the tiny rows
+    <= 2e-3 on their own (each row is staged in fp16 with its own power-of-two scale,
+    so they keep fp16's precision instead of falling into its subnormal range).
+    fp16-safe scales run the fp16 kernels (mfma_w4_rb / mfma_w4_pipe), the others the
+    exact mfma_w4."""
+    b, s, z = workloads.make_weights(op, seed=M + 11)
+    rng = np.random.default_rng(M + 12)
+    a = workloads.make_activations(M, op.K, seed=M + 13, kind="rmsnorm")
+    rows = rng.permutation(M)
+    big = rows[: max(2, M // 8)]
+    tiny = rows[max(2, M // 8): max(2, M // 8) + max(2, M // 16)]
+    for i, r in enumerate(big):
+        a[r, rng.integers(op.K)] = (1e5 if i % 2 == 0 else -3e6)
+    a[tiny] *= np.float32(1e-6)
+    cols = np.sort(rng.choice(op.N, 96, replace=False))
+    zc = None if z is None else z[cols]
+    fast = "mfma_w4_pipe" if M == 2048 else "mfma_w4_rb"
+    for scales, what, kernel in ((s, "fp16-safe scales", fast),
+                                 (s * np.float32(1e6), "scales 1e3..1e4", "mfma_w4"),
+                                 (s * np.float32(1e-4), "scales 1e-7..1e-6", "mfma_w4")):
+        w = native.NBitsWeights(b, scales, z, op.N, op.K, 4, 32)
+        assert w.launch_info(M)["kernel"] == kernel, (what, w.launch_info(M))
+        log(f"range M={M} K={op.K} N={op.N} {what} -> {kernel}")
+        y = w.gemm(a)
+        w.close()
+        assert np.all(np.isfinite(y)), what
+        ref = oracle.matmul_nbits(a, b[cols], scales.reshape(op.N, -1)[cols], zc, len(cols), op.K, 4, 32)
+        assert np.all(np.isfinite(ref))
+        assert_fro_close(y[:, cols], ref, what)
+        assert_fro_close(y[tiny][:, cols], ref[tiny], what + ", rows near 1e-6")
+
+
+# ---- decode GEMV: exact zero-point differences -------------------------------------------
+def _cancelling_weights(op, seed):
+    """Rows made of blocks whose codes equal the block's zero point except for a few codes
+    one step away: sum_k a_k (q_k - zp) is small while sum_k a_k q_k and zp * sum_k a_k are
+    large, so folding the zero point out of the block sum would cancel."""
+    rng = np.random.default_rng(seed)
+    nb = op.nb
+    zp = rng.integers(1, 15, size=(op.N, nb))
+    codes = np.repeat(zp, op.block_size, axis=1)[:, : nb * op.block_size]
+    for n in range(op.N):
+        ks = rng.choice(op.K, size=4, replace=False)
+        codes[n, ks] += rng.choice([-1, 1], size=4)
+    b = workloads.pack_nibbles(codes.reshape(op.N, nb, op.block_size))
+    s = rng.uniform(op.scale_lo, op.scale_hi, size=op.N * nb).astype(np.float32)
+    return b, s, workloads.pack_nibbles(zp)
+
+
+@pytest.mark.parametrize("M,bs,kernel", [(1, 32, "gemv_w4"), (2, 32, "gemv_w4"), (8, 32, "gemv_w4_panel"),
+                                         (1, 128, "gemv_w4"), (8, 128, "skinny_w4")])
+def test_gemv_exact_zero_point_differences(gpu, M, bs, kernel):
+    """Weight rows that are mostly q == zp blocks against activations up to 1e4: the decode
+    kernels form a_k (q_k - zp) exactly, so they meet the 1e-5 * ||y_row||_inf bar where a
+    folded sum_k a_k q_k - zp * sum_k a_k would not."""
+    op = workloads.Op("cancel", 4096, 2048, bs, True)
+    b, s, z = _cancelling_weights(op, seed=bs + M)
+    w = native.NBitsWeights(b, s, z, op.N, op.K, 4, bs)
+    assert w.launch_info(M)["kernel"] == kernel
+    a = np.random.default_rng(M).uniform(5e3, 1e4, size=(M, op.K)).astype(np.float32)
+    y = w.gemm(a)
+    ref = oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, bs)
+    assert_gemv_close(y, ref, f"{kernel} M={M} bs={bs} cancelling blocks")
+    w.close()
+
+
+# ---- split-K hand-off failures are reported, with every kernel exiting normally ------------
+def _split_pipe_handle(seed):
+    op = workloads.Op("split", 1024, 512, 32, True)
+    b, s, z, w = weights_for(op, seed)
+    w.set_tuning(6, 1)   # the pipelined kernel, not mfma_w4_rb
+    w.set_tuning(3, 2)   # every tile split over two workgroups
+    a = workloads.make_activations(64, op.K, seed=seed + 1, kind="rmsnorm")
+    ref = oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, 32)
+    assert w.launch_info(64)["kernel"] == "mfma_w4_pipe"
+    assert_fro_close(w.gemm(a), ref, "split, first call")   # grows the counters
+    return w, a, ref
+
+
+def test_split_k_overlap_is_reported(gpu):
+    """Counters holding another launch's tag (what two overlapping launches on one handle
+    leave) make both halves of every split tile stand down and the call return an error;
+    the counters are reset and the next call is correct."""
+    w, a, ref = _split_pipe_handle(21)
+    w.debug_set_counters(12345)
+    with pytest.raises(native.HipError) as e:
+        w.gemm(a)
+    assert e.value.status == native.MS_HIP_ERR_HIP and "another launch" in e.value.message
+    assert_fro_close(w.gemm(a), ref, "split, after the reported overlap")
+    w.device_error()   # nothing left to report
+    w.close()
+
+
+def test_split_k_timeout_is_reported(gpu):
+    """A second half whose partner's flag never comes (the tags say both halves arrived
+    second; the poll bound is one) gives up, and the call returns an error instead of a
+    half-summed output; the next call is correct."""
+    w, a, ref = _split_pipe_handle(22)
+    w.set_tuning(8, 1)
+    w.debug_set_counters(0, next_epoch_tag=True)
+    with pytest.raises(native.HipError) as e:
+        w.gemm(a)
+    assert e.value.status == native.MS_HIP_ERR_HIP and "timed out" in e.value.message
+    w.set_tuning(8, 0)
+    assert_fro_close(w.gemm(a), ref, "split, after the reported time-out")
+    w.close()
+
+
+def test_split_k_error_reported_to_the_next_device_call(gpu):
+    """On the device-pointer entry the failure is reported by the next call on the handle
+    (or by ms_hip_nbits_device_error) once the stream has been synchronised."""
+    import torch
+    w, a, ref = _split_pipe_handle(23)
+    dA = torch.from_numpy(a).cuda()
+    dY = torch.zeros((64, 512), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    w.debug_set_counters(777)
+    w.gemm_dev(dA.data_ptr(), dY.data_ptr(), 64, stream)
+    torch.cuda.synchronize()
+    with pytest.raises(native.HipError):
+        w.gemm_dev(dA.data_ptr(), dY.data_ptr(), 64, stream)
+    w.gemm_dev(dA.data_ptr(), dY.data_ptr(), 64, stream)
+    torch.cuda.synchronize()
+    w.device_error()
+    assert_fro_close(dY.cpu().numpy(), ref, "device entry after the reported overlap")
+    w.close()
+
+
+def test_tuning_is_per_handle(gpu):
+    """A knob set on one handle changes that handle's kernel only."""
+    op = workloads.Op("tune", 1024, 512, 32, True)
+    _, _, _, w1 = weights_for(op, 31)
+    _, _, _, w2 = weights_for(op, 31)
+    assert w1.launch_info(64)["kernel"] == w2.launch_info(64)["kernel"] == "mfma_w4_rb"
+    w1.set_tuning(6, 1)
+    assert w1.launch_info(64)["kernel"] == "mfma_w4_pipe" and w2.launch_info(64)["kernel"] == "mfma_w4_rb"
+    w1.set_tuning(6, native.MS_HIP_TUNING_INHERIT)
+    assert w1.launch_info(64)["kernel"] == "mfma_w4_rb"
+    w1.close()
+    w2.close()
+
+
+def test_destroyed_handle_is_rejected(gpu):
+    op = workloads.Op("gone", 256, 64, 32, True)
+    _, _, _, w = weights_for(op, 41)
+    h = w.handle
+    w.close()
+    lib = native.load()
+    assert lib.ms_hip_nbits_weights_info(h, None, None, None, None, None) == native.MS_HIP_ERR_INVALID
+    assert lib.ms_hip_nbits_weights_destroy(h) == native.MS_HIP_ERR_INVALID

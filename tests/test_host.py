@@ -171,3 +171,77 @@ def test_header_is_plain_c():
     out = subprocess.run(["gcc", "-fsyntax-only", "-x", "c", "-std=c99", "-Wall", "-Werror", "-"], input=src,
                          capture_output=True, text=True)
     assert out.returncode == 0, out.stderr
+
+
+class _FakeWeights:
+    """Stands in for native.NBitsWeights on a host without a GPU: records each upload."""
+
+    made: list = []
+
+    def __init__(self, b, scales, zp, N, K, bits, block_size):
+        assert scales.dtype == np.float32
+        self.N, self.closed = N, False
+        _FakeWeights.made.append(self)
+
+    def gemm(self, a):
+        return np.zeros((a.shape[0], self.N), np.float32)
+
+    def close(self):
+        self.closed = True
+
+
+def _fp16_scale_graph():
+    from modelsharp_amd import workloads
+    op = workloads.Op("t", 64, 8, 32, True)
+    b, s, z = workloads.make_weights(op, 0)
+    node = GraphNode("MatMulNBits", "mm", ["A", "B", "S", "Z"], ["Y"],
+                     {"N": op.N, "K": op.K, "bits": 4, "block_size": 32})
+    inits = {"B": b, "S": s.astype(np.float16), "Z": z}
+    return ModelGraph([node], inits, ["A"], ["Y"]), op
+
+
+def test_handle_cache_one_upload_per_initializer(monkeypatch):
+    """Repeated execute() on fp16 scales (a q4f16 export) reuses one device handle, the one
+    preload() made: the handle is keyed by the node's input names and the raw initializer
+    tensors, never by the fp32 copy that widening makes on each call."""
+    monkeypatch.setattr(native, "NBitsWeights", _FakeWeights)
+    _FakeWeights.made = []
+    graph, op = _fp16_scale_graph()
+    kernel = HipMatMulNBitsKernel()
+    assert kernel.preload(graph) == 1
+    engine = Engine(graph, KernelRegistry().register(kernel))
+    a = np.ones((1, op.K), np.float32)
+    for _ in range(20):
+        engine.run({"A": a})
+    assert len(_FakeWeights.made) == 1 and kernel.handle_count == 1
+    # The same names bound to other tensors: a new handle, and the old one is closed.
+    graph.initializers["S"] = graph.initializers["S"].copy()
+    engine.run({"A": a})
+    assert len(_FakeWeights.made) == 2 and _FakeWeights.made[0].closed and kernel.handle_count == 1
+    kernel.close()
+    assert _FakeWeights.made[1].closed
+
+
+def test_tuning_knobs_validated_without_a_device():
+    lib = native.load()
+    assert lib.ms_hip_set_tuning(99, 0) == native.MS_HIP_ERR_INVALID
+    assert "invalid tuning knob" in native.last_error()
+    assert lib.ms_hip_set_tuning(1, 10_000) == native.MS_HIP_ERR_INVALID
+    assert lib.ms_hip_set_tuning(3, 0) == native.MS_HIP_OK
+    bogus = ctypes.c_void_p(0x1234560)
+    assert lib.ms_hip_nbits_set_tuning(bogus, 0, 0) == native.MS_HIP_ERR_INVALID
+    assert "invalid weights handle" in native.last_error()
+
+
+def test_unknown_handles_are_rejected_not_read():
+    """A pointer that is not a live handle (never created, or destroyed) is rejected by
+    every entry without being dereferenced."""
+    lib = native.load()
+    junk = (ctypes.c_uint32 * 64)(*([0x4D534E42] * 64))   # memory that looks like a handle's bytes
+    p = ctypes.c_void_p(ctypes.addressof(junk))
+    n = ctypes.c_int()
+    assert lib.ms_hip_nbits_weights_info(p, ctypes.byref(n), None, None, None, None) == native.MS_HIP_ERR_INVALID
+    assert lib.ms_hip_nbits_weights_destroy(p) == native.MS_HIP_ERR_INVALID
+    assert lib.ms_hip_nbits_gemm_dev(p, None, None, 1, None) == native.MS_HIP_ERR_INVALID
+    assert lib.ms_hip_nbits_device_error(p) == native.MS_HIP_ERR_INVALID
+    assert lib.ms_hip_nbits_weights_destroy(None) == native.MS_HIP_ERR_INVALID
