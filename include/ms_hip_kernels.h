@@ -109,6 +109,18 @@ int ms_hip_nbits_gemm(void* handle, const float* a_host, float* y_host, int M);
  * ms_hip_nbits_device_error) returns MS_HIP_ERR_HIP and clears the record. */
 int ms_hip_nbits_gemm_dev(void* handle, const float* dA, float* dY, int M, void* stream);
 
+/* Allocation-free form of ms_hip_nbits_gemm_dev, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). No counterpart in the reference. Same arguments, kernels and
+ * results as ms_hip_nbits_gemm_dev; the workspace comes from a fixed scratch array
+ * that the library holds on each GPU it runs on until the process ends (96 MiB of
+ * data and 64 Ki counters; enough for M = 2048 on the Llama-2-7B MLP shapes). A call
+ * that needs more returns MS_HIP_ERR_INVALID without launching anything. Every call
+ * on one GPU shares that GPU's scratch: calls that overlap on one GPU (other streams,
+ * other threads) race, and must not be made. The calling thread's current device must
+ * be the handle's. */
+int ms_hip_nbits_gemm_dev_noalloc(void* handle, const float* dA, float* dY, int M, void* stream);
+
 /* The device-side failure recorded for this handle since the last check (see
  * ms_hip_nbits_gemm_dev): MS_HIP_ERR_HIP with its message, or MS_HIP_OK. Clears
  * the record. Synchronise the streams of earlier calls first. No counterpart in

@@ -1123,6 +1123,36 @@ int finish_create(Weights* w, int st, void** out_handle)
     return MS_HIP_OK;
 }
 
+// ---- the allocation-free entry's scratch ---------------------------------------------------
+// A file-scope device array: every GPU the library runs on holds its own copy from the
+// moment the code object is loaded there until the process ends. Host code never uses
+// the name `scratch` as an address (in host code it is only a stand-in for the symbol):
+// the device address comes from hipGetSymbolAddress, once per device, and everything on
+// the host (kernel arguments, fills) uses that pointer.
+constexpr size_t kScratchDataBytes = (size_t)96 << 20;   // fp16 activations, exponents, partial sums
+constexpr size_t kScratchCntInts = (size_t)64 << 10;      // split-K counters
+__device__ __align__(256) uint8_t scratch[kScratchDataBytes + kScratchCntInts * sizeof(int)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of this device's scratch (device `dev` current), looked up once.
+int scratch_for(int dev, uint8_t** out)
+{
+    if (dev < 0 || dev >= kMaxDevices) return fail(MS_HIP_ERR_INVALID, "[ms_hip] device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(MS_HIP_ERR_HIP, "[ms_hip] hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = static_cast<uint8_t*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return MS_HIP_OK;
+}
+
 }  // namespace
 
 // =========================================================================================
@@ -1226,6 +1256,44 @@ int ms_hip_nbits_gemm_dev(void* handle, const float* dA, float* dY, int M, void*
     const int st = take_device_error(*w, s);
     if (st) return st;
     return enqueue_gemm(*w, dA, dY, M, s);
+}
+
+int ms_hip_nbits_gemm_dev_noalloc(void* handle, const float* dA, float* dY, int M, void* stream)
+{
+    Weights* w = from_handle(handle);
+    if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    int st = take_device_error(*w, s);
+    if (st) return st;
+    if ((st = check_call(dA, dY, M)) || M == 0) return st;
+    const Knobs kn = knobs_of(*w);
+    const KernelId k = choose_kernel(*w, kn, M);
+    size_t need_d = 0, need_c = 0;
+    workspace_need(*w, kn, k, M, &need_d, &need_c);
+    if (need_d > kScratchDataBytes || need_c > kScratchCntInts)
+        return fail(MS_HIP_ERR_INVALID,
+                    "[ms_hip] this call (M=%d, N=%d, K=%d) needs %zu bytes and %zu counters of workspace; the "
+                    "allocation-free entry's fixed scratch holds %zu bytes and %zu counters (use "
+                    "ms_hip_nbits_gemm_dev)",
+                    M, w->N, w->K, need_d, need_c, kScratchDataBytes, kScratchCntInts);
+    Ws ws;
+    if (need_d || need_c) {
+        int dev = -1;
+        MS_HIP_CHECK(hipGetDevice(&dev));
+        if (dev != w->device)
+            return fail(MS_HIP_ERR_INVALID, "[ms_hip] the current device (%d) is not the handle's (%d)", dev,
+                        w->device);
+        uint8_t* base = nullptr;
+        if ((st = scratch_for(dev, &base))) return st;
+        ws.data = base;
+        ws.data_bytes = kScratchDataBytes;
+        ws.cnt = reinterpret_cast<int*>(base + kScratchDataBytes);
+        ws.cnt_ints = kScratchCntInts;
+        // The scratch keeps whatever the last call left: the counters this call uses start
+        // at zero (a fill kernel, which a captured graph can hold).
+        if ((st = zero_ints(ws.cnt, (int64_t)need_c, s))) return st;
+    }
+    return launch_kernel(*w, kn, k, ws, dA, dY, M, s);
 }
 
 int ms_hip_nbits_device_error(void* handle)

@@ -51,6 +51,7 @@ _PROTOTYPES = {
     "ms_hip_nbits_weights_info": (_c_int, [_vp, _ip, _ip, _ip, _ip, _ip]),
     "ms_hip_nbits_gemm": (_c_int, [_vp, _vp, _vp, _c_int]),
     "ms_hip_nbits_gemm_dev": (_c_int, [_vp, _vp, _vp, _c_int, _vp]),
+    "ms_hip_nbits_gemm_dev_noalloc": (_c_int, [_vp, _vp, _vp, _c_int, _vp]),
     "ms_hip_nbits_device_error": (_c_int, [_vp]),
     "ms_hip_nbits_gemm_dev_batch": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _vp]),
     "ms_hip_qgemm_nbits": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int]),
@@ -195,6 +196,11 @@ class NBitsWeights:
 
     def dequant_dev(self, dW: int, stream: int | None = None) -> None:
         check(load().ms_hip_nbits_dequant_dev(self.handle, _vp(dW), _vp(stream or 0)))
+
+    def gemm_dev_noalloc(self, dA: int, dY: int, M: int, stream: int | None = None) -> None:
+        """gemm_dev with the library's fixed per-GPU scratch instead of the handle's
+        workspace: allocates nothing; overlapping calls on one GPU race."""
+        check(load().ms_hip_nbits_gemm_dev_noalloc(self.handle, _vp(dA), _vp(dY), int(M), _vp(stream or 0)))
 
     def set_tuning(self, knob: int, value: int) -> None:
         """This handle's own value of a launch-shape knob (MS_HIP_TUNING_INHERIT: follow

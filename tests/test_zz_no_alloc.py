@@ -1,0 +1,81 @@
+"""The allocation-free entry, ms_hip_nbits_gemm_dev_noalloc, against ms_hip_nbits_gemm_dev.
+
+Both run the same kernels on the same inputs, so their outputs must be equal bit for
+bit: on every kernel that uses a workspace (the small-M matrix-core GEMV with its K
+split, the register-operand prefill with its K-split reduce, the pipelined prefill
+with split tiles) and on one that does not (the decode GEMV, the exact general
+prefill), two calls in a row through the C ABI, the second with a smaller input (the
+scratch keeps the first call's larger contents; its counters must start at zero again).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from modelsharp_amd import native, workloads
+
+pytestmark = pytest.mark.gpu
+
+
+def log(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def torch_cuda():
+    import torch
+    from modelsharp_amd import native as nat
+    nat.load()
+    if not nat.available():
+        pytest.fail("gpu test on a host without a gfx950 device: " + nat.last_error())
+    return torch
+
+
+CASES = [
+    # name, op, M of the first call, M of the second, kernel of the first call, scales factor
+    ("gemv", workloads.Op("gate", 3584, 18944, 32, True), 2, 1, "gemv_w4", 1.0),
+    ("skinny", workloads.Op("up", 4096, 11008, 128, False), 16, 4, "skinny_w4", 1.0),
+    ("rb", workloads.Op("up", 4096, 11008, 32, True), 128, 40, "mfma_w4_rb", 1.0),
+    ("pipe", workloads.Op("down", 11008, 4096, 32, True), 2048, 512, "mfma_w4_pipe", 1.0),
+    ("exact", workloads.Op("wide", 1024, 768, 64, True), 300, 33, "mfma_w4", 1e6),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: c[0])
+def test_noalloc_matches_gemm_dev(torch_cuda, case):
+    torch = torch_cuda
+    name, op, m1, m2, kernel, sf = case
+    b, s, z = workloads.make_weights(op, seed=71)
+    s = (s * np.float32(sf)).astype(np.float32)
+    w = native.NBitsWeights(b, s, z, op.N, op.K, 4, op.block_size)
+    assert w.launch_info(m1)["kernel"] == kernel, w.launch_info(m1)
+    stream = torch.cuda.current_stream().cuda_stream
+    for M in (m1, m2):
+        log(f"noalloc {name}: M={M} K={op.K} N={op.N} bs={op.block_size} ({w.launch_info(M)['kernel']})")
+        a = torch.from_numpy(workloads.make_activations(M, op.K, seed=M, kind="rmsnorm")).cuda()
+        y_ref = torch.full((M, op.N), float("nan"), device="cuda")
+        y_na = torch.full((M, op.N), float("nan"), device="cuda")
+        w.gemm_dev(a.data_ptr(), y_ref.data_ptr(), M, stream)
+        w.gemm_dev_noalloc(a.data_ptr(), y_na.data_ptr(), M, stream)
+        torch.cuda.synchronize()
+        yr, yn = y_ref.cpu().numpy(), y_na.cpu().numpy()
+        assert np.all(np.isfinite(yr))
+        assert np.array_equal(yr, yn), f"{name} M={M}: max diff {np.max(np.abs(yr - yn))}"
+    w.device_error()
+    w.close()
+
+
+def test_noalloc_rejects_calls_beyond_its_scratch(torch_cuda):
+    torch = torch_cuda
+    op = workloads.Op("down", 11008, 4096, 32, True)
+    b, s, z = workloads.make_weights(op, seed=72)
+    w = native.NBitsWeights(b, s, z, op.N, op.K, 4, 32)
+    M = 8192   # 180 MB of fp16 activations alone
+    a = torch.zeros((M, op.K), device="cuda")
+    y = torch.zeros((M, op.N), device="cuda")
+    with pytest.raises(native.HipError) as e:
+        w.gemm_dev_noalloc(a.data_ptr(), y.data_ptr(), M, torch.cuda.current_stream().cuda_stream)
+    assert e.value.status == native.MS_HIP_ERR_INVALID and "fixed scratch" in e.value.message
+    torch.cuda.synchronize()
+    assert float(y.abs().max()) == 0.0   # nothing was launched
+    w.close()
