@@ -11,7 +11,7 @@
 //   * The whole activation panel A[0..M)[0..K) is staged once per workgroup in
 //     LDS (odd k pre-divided by 16; kChunkStride4 float4 per chunk).
 //   * Load order is the design: every vector-memory load returns in issue order,
-//     so the activation loads go first, then two batches of U steps of codes,
+//     so the activation loads go first, then NB batches of U steps of codes,
 //     scales and zero points, and only then is A written to LDS. The staging
 //     therefore waits for the activations alone while the weight stream is
 //     already in flight. Loads are unconditional (a lane with no chunk at a step
@@ -69,9 +69,10 @@ __device__ __forceinline__ T op_field(int oi, T v0, T v1, T v2, T v3)
     return oi == 0 ? v0 : oi == 1 ? v1 : oi == 2 ? v2 : v3;
 }
 
-template <int M, int G, int KW, int U, int L, int WAVES, int RL>
+template <int M, int G, int KW, int U, int L, int WAVES, int RL, int NB>
 __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
 {
+    static_assert(NB >= 2 && NB <= 4, "two to four load batches in flight");
     constexpr int R = kWave / G;
     constexpr int WR = WAVES / KW;
     constexpr int ROWS0 = R * WR;      // rows of one layer; a lane owns RL rows, ROWS0 apart
@@ -97,11 +98,15 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
     float* const oy = op_field(oi, p.op[0].y, p.op[1].y, p.op[2].y, p.op[3].y);
     const int N = op_field(oi, p.op[0].N, p.op[1].N, p.op[2].N, p.op[3].N);
     const int first = op_field(oi, p.op[0].first, p.op[1].first, p.op[2].first, p.op[3].first);
-    const int n0 = (bid - first) * ROWS + rl;         // row j of this lane: n0 + j * ROWS0
+    // Row slot rl + j * ROWS0 of this workgroup is row n0 + j * ROWS0; slots past N idle.
+    const int n0 = (bid - first) * ROWS + rl;
+    bool vrow[RL];
+#pragma unroll
+    for (int j = 0; j < RL; ++j) vrow[j] = n0 + j * ROWS0 < N;
     const int C = p.C;
     const int nsteps = (C + SPAN - 1) / SPAN;
     const int lofs = wk * G + g;                       // chunk offset within a step
-    const int nvalid = (lofs < C && n0 < N) ? (C - lofs + SPAN - 1) / SPAN : 0;
+    const int nvalid = lofs < C ? (C - lofs + SPAN - 1) / SPAN : 0;
 
     const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(p.a, M * p.K * 4);
     const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(ob, N * p.row_bytes);
@@ -119,13 +124,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
         av[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ra, aoff + 16 * j, 0, 0));
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- 2. weight stream: two batches of U steps in flight ---------------------------
-    // A row past N (the last workgroup's) streams row N-1 again; its sums are not stored.
+    // ---- 2. weight stream: NB batches of U steps in flight ----------------------------
+    // An idle row slot loads from kOOB (zeros, no memory request); its sums are not stored.
     int bbase[RL], sbase[RL], zbase[RL];
 #pragma unroll
     for (int j = 0; j < RL; ++j) {
-        const int nj = n0 + j * ROWS0;
-        const int nl = nj < N ? nj : N - 1;
+        const int nl = vrow[j] ? n0 + j * ROWS0 : 0;
         bbase[j] = nl * p.row_bytes + lofs * 16;
         sbase[j] = nl * p.nb * 4 + (lofs >> L) * 4;
         zbase[j] = nl * p.zrb + ((lofs >> L) >> 1);
@@ -134,7 +138,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
     struct Batch {
         u32x4_t q[RL][U];
         float s[RL][U];
-        uint32_t z[RL][U];
+        uint8_t z[RL][U];   // bytes: a widened copy could be hoisted ahead of the batch's wait
     };
     // The codes are read once per call, each 128-byte line whole by one load of G lanes:
     // non-temporal loads keep them from displacing the activations, outputs, scales and
@@ -145,9 +149,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int k = k0 + u;
-            const bool ok = k < nvalid;
 #pragma unroll
             for (int j = 0; j < RL; ++j) {
+                const bool ok = k < nvalid && vrow[j];
                 bt.q[j][u] = __builtin_amdgcn_raw_buffer_load_b128(rb, ok ? bbase[j] + k * (SPAN * 16) : kOOB, 0,
                                                                    kNonTemporal);
                 bt.s[j][u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
@@ -157,9 +161,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
             }
         }
     };
-    Batch bA, bB;
-    load(bA, 0);
-    load(bB, U);
+    // A ring of NB batches of U steps: batch b holds steps k0 + b U .. + U - 1; each is
+    // refilled with the steps NB U further on as soon as it has been reduced, so between
+    // (NB - 1) U and NB U steps per lane are always in flight.
+    Batch bt[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) load(bt[b], b * U);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- 3. stage A: odd k divided by 16 (exact), matching 16 (q - zp) of the dequant ----
@@ -199,7 +206,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
                 h2_t zb[RL], zb16[RL];
 #pragma unroll
                 for (int j = 0; j < RL; ++j) {
-                    const uint32_t zp = ozp ? (bt.z[j][u] >> zshift) & 0x0Fu : 8u;
+                    const uint32_t zp = ozp ? ((uint32_t)bt.z[j][u] >> zshift) & 0x0Fu : 8u;
                     zb[j] = zp_half2(zp);
                     zb16[j] = zp16_half2(zp);
                 }
@@ -230,13 +237,18 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
             }
         }
     };
-    for (int k0 = 0; k0 < nsteps; k0 += 2 * U) {
-        reduce(bA, k0);
-        load(bA, k0 + 2 * U);
-        if (k0 + U >= nsteps) break;
-        reduce(bB, k0 + U);
-        load(bB, k0 + 3 * U);
+    // The exit leaves the whole loop (goto): a `break` out of the inner loop alone gives the
+    // compiler a path back to the loop head on which the last batch was not refilled, and
+    // its wait counts at the head then drain every load (vmcnt(0)) on every iteration.
+    for (int k0 = 0;; k0 += NB * U) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            if (k0 + b * U >= nsteps) goto steps_done;
+            reduce(bt[b], k0 + b * U);
+            load(bt[b], k0 + (b + NB) * U);
+        }
     }
+steps_done:
 
     // ---- 4. combine: G lanes (DPP scan), then KW waves (LDS, in wave order) -----------
     // The G lanes' sums end in lane g == G - 1 of each group.
@@ -270,10 +282,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
     if (wk == 0 && g == G - 1) {
 #pragma unroll
         for (int j = 0; j < RL; ++j) {
-            const int nj = n0 + j * ROWS0;
-            if (nj < N) {
+            if (vrow[j]) {
 #pragma unroll
-                for (int m = 0; m < M; ++m) oy[(int64_t)m * N + nj] = acc[j][m];
+                for (int m = 0; m < M; ++m) oy[(int64_t)m * N + n0 + j * ROWS0] = acc[j][m];
             }
         }
     }
@@ -281,13 +292,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
 
 // Launch configurations of gemv_w4_kernel (one instantiation each per M and L).
 struct GemvConfig {
-    int waves, G, KW, U, RL;
+    int waves, G, KW, U, RL, NB;
 };
 constexpr GemvConfig kGemvConfigs[] = {
-    {4, 16, 1, 2, 1},  {4, 16, 1, 4, 1},  {4, 32, 1, 4, 1},  {4, 64, 1, 2, 1},  {4, 16, 4, 2, 1},
-    {4, 32, 2, 2, 1},  {8, 32, 1, 4, 1},  {8, 16, 2, 4, 1},  {8, 16, 4, 2, 1},  {16, 16, 4, 2, 1},
-    {16, 32, 2, 2, 1}, {4, 16, 1, 2, 2},  {4, 16, 1, 4, 2},  {4, 32, 1, 2, 2},  {4, 64, 1, 2, 2},
-    {8, 16, 2, 2, 2},  {4, 16, 1, 1, 2},
+    {4, 16, 1, 2, 1, 2},  {4, 16, 1, 4, 1, 2},  {4, 32, 1, 4, 1, 2},  {4, 64, 1, 2, 1, 2},  {4, 16, 4, 2, 1, 2},
+    {4, 32, 2, 2, 1, 2},  {8, 32, 1, 4, 1, 2},  {8, 16, 2, 4, 1, 2},  {8, 16, 4, 2, 1, 2},  {16, 16, 4, 2, 1, 2},
+    {16, 32, 2, 2, 1, 2}, {4, 16, 1, 2, 2, 2},  {4, 16, 1, 4, 2, 2},  {4, 32, 1, 2, 2, 2},  {4, 64, 1, 2, 2, 2},
+    {8, 16, 2, 2, 2, 2},  {4, 16, 1, 1, 2, 2},
 };
 constexpr int kNumGemvConfigs = sizeof(kGemvConfigs) / sizeof(kGemvConfigs[0]);
 constexpr int kGemvMaxM = 4;

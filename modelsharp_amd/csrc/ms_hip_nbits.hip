@@ -389,7 +389,7 @@ template <int M, int L, size_t I>
 constexpr GemvFn gemv_fn_at()
 {
     constexpr GemvConfig c = kGemvConfigs[I];
-    return gemv_w4_kernel<M, c.G, c.KW, c.U, L, c.waves, c.RL>;
+    return gemv_w4_kernel<M, c.G, c.KW, c.U, L, c.waves, c.RL, c.NB>;
 }
 template <int M, int L, size_t... I>
 constexpr std::array<GemvFn, sizeof...(I)> gemv_row(std::index_sequence<I...>)
@@ -1352,9 +1352,8 @@ int ms_hip_nbits_batch_launch_info(void* const* handles, const float* const* dA,
     if (calls) *calls = n;
     if (n == 1) return ms_hip_nbits_launch_info(handles[0], M, kernel_id, lanes_per_row, grid, block);
     const GemvConfig& c = kGemvConfigs[ci];
-    const int rows = gemv_rows(c);
     int gr = 0;
-    for (int j = 0; j < n; ++j) gr += (ws[j]->N + rows - 1) / rows;
+    for (int j = 0; j < n; ++j) gr += (ws[j]->N + gemv_rows(c) - 1) / gemv_rows(c);
     if (kernel_id) *kernel_id = kGemv;
     if (lanes_per_row) *lanes_per_row = c.G;
     if (grid) *grid = gr;
