@@ -254,6 +254,7 @@ def main() -> int:
                                              "a grouped launch (qkv, gate_up) or prefill_up / prefill_down (M=2048), "
                                              "eagerly over the rotation, then a plain copy of --copy-mib; no JSON line")
     ap.add_argument("--calls", type=int, default=64, help="launches in --op mode")
+    ap.add_argument("--m", type=int, default=2048, help="rows of A for prefill_* in --op mode")
     ap.add_argument("--copy-mib", type=int, default=256, help="size of the calibration copy in --op mode")
     args = ap.parse_args()
 
@@ -449,7 +450,8 @@ def profile_op(args) -> int:
     from modelsharp_amd import native
     if args.op.startswith("prefill_"):
         ops = [next(o for o in workloads.LLAMA7B_PREFILL_OPS if o.name == args.op[len("prefill_"):])]
-        M, copies, kind = 2048, 2, "rmsnorm"
+        M, kind = args.m, "rmsnorm"
+        copies = max(2, workloads.rotation_copies(workloads.algorithmic_bytes_group(ops, M), args.rotate_mib << 20))
     else:
         ops = ([workloads.DECODE_7B[i] for i in GROUPS[args.op]] if args.op in GROUPS else
                [next(o for o in workloads.DECODE_7B if o.name == args.op)])

@@ -40,6 +40,12 @@ extern "C" {
 #define MS_HIP_ERR_HIP          3  /* a HIP runtime call failed              */
 #define MS_HIP_ERR_UNSUPPORTED  4  /* valid operator input this ABI cannot take */
 
+/* Element types of ms_hip_nbits_weights_create_ex's scales and zero points. */
+#define MS_HIP_DTYPE_NONE       0  /* no zero-point tensor (default zero point) */
+#define MS_HIP_DTYPE_F32        1
+#define MS_HIP_DTYPE_F16        2
+#define MS_HIP_DTYPE_U8         3  /* packed codes, as B */
+
 /* ms_hip_nbits_set_tuning value: the handle follows the process default again. */
 #define MS_HIP_TUNING_INHERIT   (-2147483647 - 1)
 
@@ -72,6 +78,17 @@ int ms_hip_nbits_weights_create(const uint8_t* bq, int64_t bq_len,
                                 const uint8_t* zero_points, int64_t zp_len,
                                 int N, int K, int bits, int block_size,
                                 void** out_handle);
+/* The same with the element types the operator accepts (MatMulNBitsKernel.cs:119-145):
+ * scales Float32 or Float16 (q4f16 exports; widened exactly on the device, as
+ * GraphContext.Get widens them on the host, GraphContext.cs:106), zero points packed
+ * UInt8 (MS_HIP_DTYPE_U8), Float32 or Float16 (zpMode 1 of GpuKernels.cs:578-638, float
+ * zero points of MatMulNBitsKernel.cs:239-240; these run the general kernels), or
+ * MS_HIP_DTYPE_NONE. Lengths are element counts. */
+int ms_hip_nbits_weights_create_ex(const uint8_t* bq, int64_t bq_len,
+                                   const void* scales, int64_t scales_len, int scales_type,
+                                   const void* zero_points, int64_t zp_len, int zp_type,
+                                   int N, int K, int bits, int block_size,
+                                   void** out_handle);
 /* Same, from buffers already resident on the device (copied device-to-device). */
 int ms_hip_nbits_weights_create_dev(const uint8_t* d_bq, const float* d_scales,
                                     const uint8_t* d_zero_points,
@@ -108,6 +125,12 @@ int ms_hip_nbits_gemm(void* handle, const float* a_host, float* y_host, int M);
  * the output of that call is not valid: the next call on the handle (or
  * ms_hip_nbits_device_error) returns MS_HIP_ERR_HIP and clears the record. */
 int ms_hip_nbits_gemm_dev(void* handle, const float* dA, float* dY, int M, void* stream);
+
+/* ms_hip_nbits_gemm_dev with fp16 activations (q4f16 exports): dA16 is [M,K] fp16,
+ * widened exactly into the handle's workspace, then the fp32 path runs (the reference
+ * widens fp16 inputs, GraphContext.cs:106). Y stays fp32. Needs the workspace to have
+ * grown outside stream capture (else MS_HIP_ERR_UNSUPPORTED). */
+int ms_hip_nbits_gemm_dev_f16(void* handle, const void* dA16, float* dY, int M, void* stream);
 
 /* Allocation-free form of ms_hip_nbits_gemm_dev, for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses that
@@ -180,7 +203,9 @@ int ms_hip_sync(void);
  *     M > 16 to it;
  *   7 its K split (workgroups per 128 x 256 tile, 1..64, clamped to K / 128);
  *   8 polls of the pipelined prefill's split-K flag before the second half of a
- *     tile gives up (0: about 4 million).
+ *     tile gives up (0: about 4 million);
+ *   9 the register-operand prefill's weight fragments per wave (1, 2 or 4: tiles of
+ *     128 x 64, 128 x 128 or 128 x 256 outputs).
  * ms_hip_nbits_debug_set_counters sets the arrival tag of every split tile of the
  *   handle's pipelined-prefill counters to `value` (or to the tag the next split-K
  *   launch will carry, when next_epoch_tag != 0) and clears their ready flags: it
@@ -188,7 +213,9 @@ int ms_hip_sync(void);
  *   every kernel still exiting normally.
  * ms_hip_nbits_launch_info reports what a call with M rows would launch:
  *   kernel_id 0 generic, 1 gemv_w4, 2 mfma_w4, 3 gemv_w4_panel, 4 mfma_w4_pipe,
- *   5 skinny_w4, 6 mfma_w4_rb. */
+ *   5 skinny_w4, 6 mfma_w4_rb, 7 gemv_general, 8 mfma_general; lanes_per_row is the
+ *   lanes per weight row of the
+ *   GEMV kernels, the output tile width of mfma_w4_rb, 0 otherwise. */
 /* ms_hip_nbits_batch_launch_info: what the first launch of a batch call with these
  * handles and activations would be: `calls` = how many of the leading calls it
  * serves, then as ms_hip_nbits_launch_info. */

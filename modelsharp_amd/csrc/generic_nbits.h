@@ -1,12 +1,14 @@
-// generic_nbits.h — MatMulNBits for every input the fast kernels do not take
-// (bits=8, block sizes that are not 32/64/128/256, K not a multiple of 32),
-// and the dequantized-weight readback.
+// generic_nbits.h — the operator's dequantization for every weight format, one weight
+// at a time: the readback kernel, the per-output kernel the general paths fall back to
+// (K or the block size not a multiple of 8), and the helpers of the general GEMV and
+// GEMM kernels.
 //
-// Both follow the reference's per-block loop directly
-// (MatMulNBitsKernel.cs:236-258): block b of row n starts at byte
-// n*nb*blob + b*blob, its zero point is the b-th packed code of row n
-// (stride zrb bytes) or 2^(bits-1), and the last block may be partial
-// (len = min(bs, K - b*bs), MatMulNBitsKernel.cs:246).
+// All follow the reference's per-block loop directly (MatMulNBitsKernel.cs:236-258):
+// block b of row n starts at byte n*nb*blob + b*blob, its zero point is the b-th float
+// of row n's zero points (zpf, MatMulNBitsKernel.cs:239-240), the b-th packed code of
+// row n (stride zrb bytes, :241) or 2^(bits-1) (:242), and the last block may be partial
+// (len = min(bs, K - b*bs), :246). W = ((float)q - zp) * scale, each operation rounded
+// in fp32 (MatMulNBitsSimd.cs:100-111): bit for bit the reference's weights.
 #pragma once
 #include "nbits_device.h"
 
@@ -15,7 +17,8 @@ namespace msnb {
 struct RawLayout {
     const uint8_t* b;
     const float* scales;
-    const uint8_t* zp;   // nullptr: default 2^(bits-1)
+    const uint8_t* zp;   // packed codes, or nullptr
+    const float* zpf;    // float zero points [N * nb], or nullptr (then zp, else 2^(bits-1))
     int N, K, bits, bs, nb, blob, zrb;
 };
 
@@ -27,6 +30,7 @@ __device__ __forceinline__ int unpack_code(const uint8_t* data, int64_t base, in
 
 __device__ __forceinline__ float block_zp(const RawLayout& L, int n, int bk)
 {
+    if (L.zpf) return L.zpf[(int64_t)n * L.nb + bk];
     if (L.zp) return (float)unpack_code(L.zp, (int64_t)n * L.zrb, bk, L.bits);
     return (float)(1 << (L.bits - 1));
 }

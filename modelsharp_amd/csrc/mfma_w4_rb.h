@@ -5,14 +5,15 @@
 // a_rows_f16_kernel (row m scaled by 2^-rexp[m]; each 8-k group in the order
 // k0,k4,k1,k5,k2,k6,k3,k7, the order in which one dword of packed codes dequantizes).
 //
-// A workgroup (4 waves) computes a 128 x 256 tile of Y over a range of 128-k blocks:
-//   * wave w owns weight rows n0 + 64 w .. + 63 (4 fragments of 16) and all 128 rows of
-//     A (8 fragments of 16): 32 v_mfma_f32_16x16x32_f16 per 32-k step, 128 fp32
-//     accumulators per lane in AGPRs (one wave per SIMD). Every dequantized weight feeds
-//     128 rows of A, so the dequant's VALU work (15 instructions per dword of 8 codes) is
-//     about half the MFMA time. (Two waves per SIMD at 64 x 64 each, which both
-//     dequantize the same rows, measured slower: their dequant alone matches the MFMA
-//     time.)
+// A workgroup (4 waves) computes a 128 x (64 NF) tile of Y over a range of 128-k blocks
+// (NF = 1, 2 or 4: narrower tiles let launches with few rows of A fill the CUs with a
+// smaller K split):
+//   * wave w owns weight rows n0 + 16 NF w .. (NF fragments of 16) and all 128 rows of
+//     A (8 fragments of 16): 8 NF v_mfma_f32_16x16x32_f16 per 32-k step, 32 NF fp32
+//     accumulators per lane. Every dequantized weight feeds 128 rows of A, so the
+//     dequant's VALU work (15 instructions per dword of 8 codes) is about half the MFMA
+//     time. (Two waves per SIMD at 64 x 64 each, which both dequantize the same rows,
+//     measured slower: their dequant alone matches the MFMA time.)
 //   * weights never touch LDS: lane (n = lane % 16, s = lane / 16) loads the 16-byte chunk
 //     s of its row's 64-byte block of codes (plus the chunk's scale and zero point) into a
 //     ring of registers three blocks deep, and dword j of the chunk becomes the B operand
@@ -36,7 +37,7 @@
 
 namespace msnb {
 
-constexpr int kRbBM = 128, kRbBN = 256;
+constexpr int kRbBM = 128;   // rows of A per tile; the tile's columns are 64 * NF (NF = 1, 2, 4)
 constexpr int kRbRing = 3;                     // weight blocks in registers
 constexpr int kRbBufBytes = kRbBM * 128 * 2;   // one block of fp16 A
 
@@ -51,9 +52,10 @@ struct RbParams {
     int tiles_m, tiles_n, ksw;
 };
 
+template <int NF>
 __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
 {
-    constexpr int MF = kRbBM / 16, NF = 4;
+    constexpr int MF = kRbBM / 16, BN = 64 * NF;
     __shared__ __attribute__((aligned(16))) uint8_t lds_a[2 * kRbBufBytes];
 
     const int items = p.tiles_m * p.tiles_n * p.ksw;
@@ -64,7 +66,7 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
     const int kw = rest % p.ksw, mt = rest / p.ksw;
     const int G = p.K >> 7;
     const int g0 = (int)((int64_t)kw * G / p.ksw), cnt = (int)((int64_t)(kw + 1) * G / p.ksw) - g0;
-    const int m0 = mt * kRbBM, n0 = nt * kRbBN;
+    const int m0 = mt * kRbBM, n0 = nt * BN;
 
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int ln = lane & 15, ls = lane >> 4;
@@ -103,7 +105,7 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
     int cb[NF], sb[NF], zb[NF];
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
-        const int n = n0 + 64 * wave + 16 * f + ln;
+        const int n = n0 + 16 * NF * wave + 16 * f + ln;
         const bool in = n < p.N;
         cb[f] = in ? n * p.row_bytes + ls * 16 : kOOB;
         sb[f] = in ? n * p.nb * 4 : kOOB;
@@ -216,7 +218,7 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
             if (t + 2 < 4 * MF) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
 #pragma unroll
-            for (int u = 0; u < 3; ++u) {
+            for (int u = 0; u < NF - 1; ++u) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
             }
@@ -240,12 +242,12 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
         body(i + 2, w[2], w[0]);
     }
 
-    // ---- epilogue: acc[mf][f][v] is out[m0 + 16 mf + 4 ls + v][n0 + 64 wave + 16 f + ln] ----
+    // ---- epilogue: acc[mf][f][v] is out[m0 + 16 mf + 4 ls + v][n0 + 16 NF wave + 16 f + ln] ----
     float* const out = p.out + kw * p.slice;
     const __amdgpu_buffer_rsrc_t ro = buffer_rsrc(out, p.M * p.N * 4);
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
-        const int n = n0 + 64 * wave + 16 * f + ln;
+        const int n = n0 + 16 * NF * wave + 16 * f + ln;
 #pragma unroll
         for (int mf = 0; mf < MF; ++mf) {
 #pragma unroll

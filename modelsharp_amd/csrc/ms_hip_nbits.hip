@@ -10,6 +10,10 @@
 //       few output tiles or block_size != 32                  -> a_rows_f16 + mfma_w4_rb
 //       otherwise (block_size 32)                             -> a_rows_f16 + mfma_w4_pipe
 //     M >  16 otherwise                                       -> mfma_w4 (exact, no workspace)
+//   other formats (bits 8, float zero points, other block sizes or K), K and the block
+//   size multiples of 8:
+//     M <= 16                                                 -> gemv_general
+//     M >  16                                                 -> mfma_general (exact)
 //   anything else                                             -> generic
 // Declarations and reference citations: include/ms_hip_kernels.h.
 #include "../../include/ms_hip_kernels.h"
@@ -30,9 +34,11 @@
 #include <utility>
 #include <vector>
 
+#include "gemv_general.h"
 #include "gemv_w4.h"
 #include "gemv_w4_panel.h"
 #include "generic_nbits.h"
+#include "mfma_general.h"
 #include "mfma_w4.h"
 #include "mfma_w4_pipe.h"
 #include "mfma_w4_rb.h"
@@ -108,8 +114,8 @@ int require_device()
 //   1 gemv_w4 configuration (c+1; -1 panel) 6 mfma_w4_rb: 1 off, 2 every eligible M
 //   2 1: every M > 16 call to mfma_w4       7 mfma_w4_rb K split
 //   3 pipelined prefill K split              8 split-K hand-off poll bound (pipelined)
-//   4 skinny_w4: 1 off, 2 every eligible M
-constexpr int kNumKnobs = 9;
+//   4 skinny_w4: 1 off, 2 every eligible M   9 mfma_w4_rb fragments per wave (1, 2, 4)
+constexpr int kNumKnobs = 10;
 constexpr int kDefaultSpinLimit = 1 << 22;
 std::atomic<int> g_knob[kNumKnobs];   // zero-initialised (static storage)
 
@@ -124,6 +130,7 @@ struct Knobs {
     int rb() const { return v[6]; }
     int rb_ksw() const { return v[7]; }
     int spin_limit() const { return v[8] > 0 ? v[8] : kDefaultSpinLimit; }
+    int rb_nf() const { return v[9]; }
 };
 
 int validate_knob(int knob, int value)
@@ -139,6 +146,7 @@ int validate_knob(int knob, int value)
         case 6: ok = value >= 0 && value <= 2; break;
         case 7: ok = value >= 0 && value <= 64; break;
         case 8: ok = value >= 0; break;
+        case 9: ok = value == 0 || value == 1 || value == 2 || value == 4; break;
         default: break;
     }
     return ok ? MS_HIP_OK : fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid tuning knob %d = %d", knob, value);
@@ -156,7 +164,8 @@ struct Ws {
 
 struct Weights {
     int N = 0, K = 0, bits = 0, bs = 0, nb = 0, blob = 0, zrb = 0;
-    int has_zp = 0;
+    int has_zp = 0;     // packed uint8 zero points in d_zp
+    int zp_float = 0;   // float zero points in d_zpf
     int64_t row_bytes = 0;
     int fast = 0;       // gemv_w4 / mfma_w4 eligible
     int log2cpb = 0;    // log2(bs / 32) when fast
@@ -164,6 +173,8 @@ struct Weights {
     uint8_t* d_b = nullptr;
     float* d_scales = nullptr;
     uint8_t* d_zp = nullptr;
+    float* d_zpf = nullptr;     // float zero points [N * nb]
+    int* d_wexp = nullptr;      // general formats: row exponents of the weights [N]
     std::atomic<int> knob[kNumKnobs];   // MS_HIP_TUNING_INHERIT: the process default
     // Device-side failure report: a split-K hand-off that gives up writes a nonzero code
     // here (pinned host memory the kernels write through d_err); calls check and clear it.
@@ -233,6 +244,7 @@ RawLayout raw_layout(const Weights& w)
     L.b = w.d_b;
     L.scales = w.d_scales;
     L.zp = w.has_zp ? w.d_zp : nullptr;
+    L.zpf = w.zp_float ? w.d_zpf : nullptr;
     L.N = w.N;
     L.K = w.K;
     L.bits = w.bits;
@@ -248,6 +260,8 @@ void free_weights(Weights& w)
     if (w.d_b) (void)hipFree(w.d_b);
     if (w.d_scales) (void)hipFree(w.d_scales);
     if (w.d_zp) (void)hipFree(w.d_zp);
+    if (w.d_zpf) (void)hipFree(w.d_zpf);
+    if (w.d_wexp) (void)hipFree(w.d_wexp);
     if (w.d_stage) (void)hipFree(w.d_stage);
     if (w.h_stage) (void)hipHostFree(w.h_stage);
     if (w.h_err) (void)hipHostFree(w.h_err);
@@ -257,6 +271,8 @@ void free_weights(Weights& w)
     w.d_b = nullptr;
     w.d_scales = nullptr;
     w.d_zp = nullptr;
+    w.d_zpf = nullptr;
+    w.d_wexp = nullptr;
     w.d_stage = nullptr;
     w.stage_bytes = 0;
     w.h_stage = nullptr;
@@ -267,9 +283,11 @@ void free_weights(Weights& w)
     w.stream = nullptr;
 }
 
-// Smallest nonzero and largest |scale| bit patterns (positive floats order as integers).
+// Smallest nonzero and largest |scale| bit patterns (positive floats order as integers):
+// a reduction per workgroup, then one atomic pair per workgroup.
 __global__ __launch_bounds__(256) void scale_range_kernel(const float* __restrict__ s, int64_t n, unsigned* out)
 {
+    __shared__ unsigned red[2][4];
     unsigned lo = 0xFFFFFFFFu, hi = 0u;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
         const unsigned b = __builtin_bit_cast(unsigned, s[i]) & 0x7FFFFFFFu;
@@ -278,8 +296,24 @@ __global__ __launch_bounds__(256) void scale_range_kernel(const float* __restric
             hi = max(hi, b);
         }
     }
-    atomicMin(&out[0], lo);
-    atomicMax(&out[1], hi);
+    for (int o = 32; o > 0; o >>= 1) {
+        lo = min(lo, (unsigned)__shfl_xor((int)lo, o));
+        hi = max(hi, (unsigned)__shfl_xor((int)hi, o));
+    }
+    const int wave = threadIdx.x / kWave;
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+        red[0][wave] = lo;
+        red[1][wave] = hi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w) {
+            lo = min(lo, red[0][w]);
+            hi = max(hi, red[1][w]);
+        }
+        atomicMin(&out[0], lo);
+        atomicMax(&out[1], hi);
+    }
 }
 
 // Zero fill of n ints (counters), a kernel rather than a memset so that it can sit in
@@ -648,6 +682,45 @@ int launch_gemv(const Weights& w, const Knobs& kn, const float* dA, float* dY, i
     return launch_panel(w, kn, dA, dY, M, stream);
 }
 
+// The general kernels take K and the block size multiples of 8 (8-code groups lie in one
+// block and start at 4-byte aligned codes).
+bool general_eligible(const Weights& w)
+{
+    return (w.K % 8) == 0 && (w.bs % 8) == 0 && (int64_t)w.N * w.nb * w.blob < ((int64_t)1 << 40);
+}
+
+typedef void (*GenGemvFn)(RawLayout, const float*, float*);
+template <size_t... I>
+constexpr std::array<GenGemvFn, sizeof...(I)> gen_gemv_table(std::index_sequence<I...>)
+{
+    return {gemv_general_kernel<(int)I + 1>...};
+}
+constexpr auto kGenGemvTable = gen_gemv_table(std::make_index_sequence<16>{});
+
+int launch_gemv_general(const Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
+{
+    hipLaunchKernelGGL(kGenGemvTable[M - 1], dim3((w.N + kGenRowsPerWg - 1) / kGenRowsPerWg), dim3(256), 0, stream,
+                       raw_layout(w), dA, dY);
+    MS_HIP_CHECK(hipGetLastError());
+    return MS_HIP_OK;
+}
+
+int launch_mfma_general(const Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
+{
+    GenParams p;
+    p.L = raw_layout(w);
+    p.wexp = w.d_wexp;
+    p.a = dA;
+    p.y = dY;
+    p.M = M;
+    p.tiles_m = (M + kGenBM - 1) / kGenBM;
+    p.tiles_n = (w.N + kGenBN - 1) / kGenBN;
+    const int tiles = p.tiles_m * p.tiles_n;
+    hipLaunchKernelGGL(mfma_general_kernel, dim3(((tiles + kXcds - 1) / kXcds) * kXcds), dim3(256), 0, stream, p);
+    MS_HIP_CHECK(hipGetLastError());
+    return MS_HIP_OK;
+}
+
 int launch_generic(const Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
 {
     const int64_t total = (int64_t)M * w.N;
@@ -861,31 +934,43 @@ bool rb_eligible(const Weights& w, const Knobs& kn, int M)
            (int64_t)M * w.N * 4 < kOOB;
 }
 
-// K split: the number of workgroups per 128 x 256 tile. A split runs in rounds of one
-// workgroup per CU and pays a reduce pass over ksw + 1 copies of Y (written and read),
-// so the pick minimises rounds x (blocks per workgroup) x t_block + reduce bytes / HBM
-// rate, with t_block the measured time of one 128-k block of a workgroup (about 3.5 us:
-// K=11008 unsplit at M=2048 takes 301 us for 86 blocks). On the 7B MLP shapes this
-// picks the fastest measured split (M=128: 4 and 16; M=512, K=11008: 4).
-int rb_ksw(const Weights& w, const Knobs& kn, int M)
+// Tile width and K split of an mfma_w4_rb launch: tiles of 128 x 64 NF outputs, ksw
+// workgroups per tile (each a contiguous range of 128-k blocks), the partial sums summed
+// (and scaled by the row exponents) by rb_reduce_kernel. The pick minimises
+//   rounds x ceil(G / ksw) x t_block(NF) + (2 ksw + 1) x 4 M N / 4 TB/s + t_launch
+// over NF in {1, 2, 4} and ksw <= min(G, 32): rounds of one workgroup per CU, t_block the
+// time a workgroup spends on one 128-k block (about 3.5 us at NF = 4 with the chip busy,
+// measured: K = 11008 unsplit at M = 2048 took 301 us for 86 blocks; the model charges the
+// A block every workgroup stages whatever its width), and the partial sums written and
+// read back once each, plus Y. Knob 9 forces NF, knob 7 ksw.
+struct RbShape {
+    int nf, ksw, tiles_m, tiles_n;
+};
+RbShape rb_shape(const Weights& w, const Knobs& kn, int M)
 {
     const int G = w.K / 128;
-    const int64_t tiles = (int64_t)((M + kRbBM - 1) / kRbBM) * ((w.N + kRbBN - 1) / kRbBN);
-    if (kn.rb_ksw() > 0) return std::max(1, std::min(kn.rb_ksw(), G));
     const int cus = device_cus();
-    const double t_block = 3.5e-6, hbm = 4.0e12, t_launch = 2e-6;
+    const int tiles_m = (M + kRbBM - 1) / kRbBM;
+    const double hbm = 4.0e12, t_launch = 2e-6;
     const double ybytes = (double)M * w.N * 4;
-    int pick = 1;
-    double best = 1e30;
-    for (int k = 1; k <= std::min(G, 32); ++k) {
-        const double rounds = (double)((tiles * k + cus - 1) / cus);
-        const double t = rounds * std::ceil((double)G / k) * t_block + (k > 1 ? (2.0 * k + 1) * ybytes / hbm + t_launch : 0.0);
-        if (t < best * 0.97) {
-            best = t;
-            pick = k;
+    RbShape best{4, 1, tiles_m, (w.N + 255) / 256};
+    double best_t = 1e30;
+    for (int nf : {4, 2, 1}) {
+        if (kn.rb_nf() > 0 && nf != kn.rb_nf()) continue;
+        const int tiles_n = (w.N + 64 * nf - 1) / (64 * nf);
+        const int64_t tiles = (int64_t)tiles_m * tiles_n;
+        const double t_block = 1.4e-6 + 0.525e-6 * nf;
+        for (int k = 1; k <= std::min(G, 32); ++k) {
+            if (kn.rb_ksw() > 0 && k != std::max(1, std::min(kn.rb_ksw(), G))) continue;
+            const double rounds = (double)((tiles * k + cus - 1) / cus);
+            const double t = rounds * std::ceil((double)G / k) * t_block + (2.0 * k + 1) * ybytes / hbm + t_launch;
+            if (t < best_t * 0.97) {
+                best_t = t;
+                best = RbShape{nf, k, tiles_m, tiles_n};
+            }
         }
     }
-    return pick;
+    return best;
 }
 
 // Which prefill kernel: mfma_w4_rb where the pipelined kernel does not apply (block
@@ -920,8 +1005,8 @@ RbWs rb_ws(const Weights& w, int M, int ksw)
 
 int launch_rb(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, float* dY, int M, hipStream_t stream)
 {
-    const int tiles_m = (M + kRbBM - 1) / kRbBM, tiles_n = (w.N + kRbBN - 1) / kRbBN;
-    const int ksw = rb_ksw(w, kn, M);
+    const RbShape sh = rb_shape(w, kn, M);
+    const int tiles_m = sh.tiles_m, tiles_n = sh.tiles_n, ksw = sh.ksw;
     const RbWs L = rb_ws(w, M, ksw);
     uint32_t* a16 = reinterpret_cast<uint32_t*>(ws.data);
     int* rexp = reinterpret_cast<int*>(ws.data + align256((size_t)M * w.K * 2));
@@ -945,7 +1030,13 @@ int launch_rb(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, float*
     p.tiles_n = tiles_n;
     p.ksw = ksw;
     const int items = tiles_m * tiles_n * ksw;
-    hipLaunchKernelGGL(mfma_w4_rb_kernel, dim3(((items + kXcds - 1) / kXcds) * kXcds), dim3(256), 0, stream, p);
+    const dim3 grid(((items + kXcds - 1) / kXcds) * kXcds);
+    if (sh.nf == 1)
+        hipLaunchKernelGGL(mfma_w4_rb_kernel<1>, grid, dim3(256), 0, stream, p);
+    else if (sh.nf == 2)
+        hipLaunchKernelGGL(mfma_w4_rb_kernel<2>, grid, dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL(mfma_w4_rb_kernel<4>, grid, dim3(256), 0, stream, p);
     const int slice4 = (int)(L.slice / 4);
     hipLaunchKernelGGL(rb_reduce_kernel, dim3((unsigned)std::min((slice4 + 255) / 256, 8192)), dim3(256), 0, stream,
                        reinterpret_cast<const float4*>(part), dY, rexp, M * w.N, w.N, slice4, ksw);
@@ -955,11 +1046,17 @@ int launch_rb(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, float*
 
 // ---- dispatch ------------------------------------------------------------------------------
 // Which kernel a call with M rows takes (ids of ms_hip_nbits_launch_info).
-enum KernelId { kGeneric = 0, kGemv = 1, kMfma = 2, kPanel = 3, kPipe = 4, kSkinny = 5, kRb = 6 };
+enum KernelId {
+    kGeneric = 0, kGemv = 1, kMfma = 2, kPanel = 3, kPipe = 4, kSkinny = 5, kRb = 6, kGemvGeneral = 7,
+    kMfmaGeneral = 8
+};
 
 KernelId choose_kernel(const Weights& w, const Knobs& kn, int M)
 {
-    if (!w.fast) return kGeneric;
+    if (!w.fast) {
+        if (!general_eligible(w)) return kGeneric;
+        return M <= kPanelMaxM ? kGemvGeneral : kMfmaGeneral;
+    }
     if (M <= kPanelMaxM) {
         if (skinny_eligible(w, kn, M)) return kSkinny;
         return pick_gemv_config(w, kn, M, w.N) >= 0 ? kGemv : kPanel;
@@ -979,7 +1076,7 @@ void workspace_need(const Weights& w, const Knobs& kn, KernelId k, int M, size_t
         *data = L.data;
         *cnt = L.cnt;
     } else if (k == kRb) {
-        *data = rb_ws(w, M, rb_ksw(w, kn, M)).data;
+        *data = rb_ws(w, M, rb_shape(w, kn, M).ksw).data;
     } else if (k == kPipe) {
         const PipeWs L = pipe_ws(w, M, pipe_split(w, kn, M));
         *data = L.data;
@@ -999,6 +1096,8 @@ int launch_kernel(Weights& w, const Knobs& kn, KernelId k, const Ws& ws, const f
 {
     switch (k) {
         case kGeneric: return launch_generic(w, dA, dY, M, stream);
+        case kGemvGeneral: return launch_gemv_general(w, dA, dY, M, stream);
+        case kMfmaGeneral: return launch_mfma_general(w, dA, dY, M, stream);
         case kGemv:
         case kPanel: return launch_gemv(w, kn, dA, dY, M, stream);
         case kSkinny: return launch_skinny(w, kn, ws, dA, dY, M, stream);
@@ -1079,19 +1178,55 @@ int check_impl(int N, int K, int bits, int bs, int64_t b_len, int64_t scales_len
     return MS_HIP_OK;
 }
 
-// A new handle for the layout (N, K, bits, bs): device buffers for the weights and the
-// pinned error word. On failure everything is freed and *out stays null.
-int new_weights(int N, int K, int bits, int bs, int has_zp, Weights** out)
+// fp16 -> fp32, exact (the reference widens fp16 tensors the same way, GraphContext.cs:106).
+__global__ __launch_bounds__(256) void f16_to_f32_kernel(const _Float16* __restrict__ in, float* __restrict__ out,
+                                                         int64_t n)
+{
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = (float)in[i];
+}
+
+void launch_widen(const void* in, float* out, int64_t n, hipStream_t stream)
+{
+    hipLaunchKernelGGL(f16_to_f32_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 4096)), dim3(256), 0,
+                       stream, static_cast<const _Float16*>(in), out, n);
+}
+
+// Copies n elements of type `type` (MS_HIP_DTYPE_F32 or _F16) from host or device memory
+// at src into the fp32 device buffer dst, widening fp16 exactly.
+hipError_t upload_f32(float* dst, const void* src, int64_t n, int type, hipMemcpyKind kind)
+{
+    if (type == MS_HIP_DTYPE_F32) return hipMemcpy(dst, src, (size_t)n * 4, kind);
+    void* tmp = nullptr;
+    hipError_t e = hipMalloc(&tmp, (size_t)n * 2);
+    if (e == hipSuccess) e = hipMemcpy(tmp, src, (size_t)n * 2, kind);
+    if (e == hipSuccess) {
+        launch_widen(tmp, dst, n, nullptr);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (tmp) (void)hipFree(tmp);
+    return e;
+}
+
+// A new handle for the layout (N, K, bits, bs) with zero points of kind zp_kind (0 none,
+// 1 packed uint8, 2 float): device buffers for the weights and the pinned error word. On
+// failure everything is freed and *out stays null.
+int new_weights(int N, int K, int bits, int bs, int zp_kind, Weights** out)
 {
     *out = nullptr;
     Weights* w = new Weights();
     for (auto& k : w->knob) k.store(MS_HIP_TUNING_INHERIT);
     w->device = device_info().device;
     derive_layout(*w, N, K, bits, bs);
-    w->has_zp = has_zp;
+    w->has_zp = zp_kind == 1;
+    w->zp_float = zp_kind == 2;
+    if (w->zp_float) w->fast = 0;   // the 4-bit kernels take integer zero points only
     hipError_t e = hipMalloc(&w->d_b, (size_t)N * w->row_bytes);
     if (e == hipSuccess) e = hipMalloc(&w->d_scales, (size_t)N * w->nb * sizeof(float));
-    if (e == hipSuccess && has_zp) e = hipMalloc(&w->d_zp, (size_t)N * w->zrb);
+    if (e == hipSuccess && w->has_zp) e = hipMalloc(&w->d_zp, (size_t)N * w->zrb);
+    if (e == hipSuccess && w->zp_float) e = hipMalloc(&w->d_zpf, (size_t)N * w->nb * sizeof(float));
+    if (e == hipSuccess && !w->fast) e = hipMalloc(&w->d_wexp, (size_t)N * sizeof(int));
     if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&w->h_err), 64, hipHostMallocMapped);
     if (e == hipSuccess) {
         *w->h_err = 0;
@@ -1110,6 +1245,13 @@ int new_weights(int N, int K, int bits, int bs, int has_zp, Weights** out)
 int finish_create(Weights* w, int st, void** out_handle)
 {
     if (!st) st = check_pipe_scales(*w);
+    if (!st && w->d_wexp) {   // row exponents of the general GEMM
+        hipLaunchKernelGGL(weight_row_exponent_kernel, dim3((w->N + 255) / 256), dim3(256), 0, nullptr, raw_layout(*w),
+                           w->d_wexp);
+        hipError_t e = hipGetLastError();
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e != hipSuccess) st = fail(MS_HIP_ERR_HIP, "[ms_hip] weight exponents failed: %s", hipGetErrorString(e));
+    }
     if (st) {
         free_weights(*w);
         delete w;
@@ -1175,24 +1317,41 @@ int ms_hip_nbits_check(int N, int K, int bits, int block_size, int64_t b_len, in
     return check_impl(N, K, bits, block_size, b_len, scales_len, zp_kind, zp_len, a_last_dim);
 }
 
-int ms_hip_nbits_weights_create(const uint8_t* bq, int64_t bq_len, const float* scales, int64_t scales_len,
-                                const uint8_t* zero_points, int64_t zp_len, int N, int K, int bits,
-                                int block_size, void** out_handle)
+int ms_hip_nbits_weights_create_ex(const uint8_t* bq, int64_t bq_len, const void* scales, int64_t scales_len,
+                                   int scales_type, const void* zero_points, int64_t zp_len, int zp_type, int N, int K,
+                                   int bits, int block_size, void** out_handle)
 {
     if (!out_handle) return fail(MS_HIP_ERR_INVALID, "[ms_hip] out_handle is null");
     *out_handle = nullptr;
-    int st = check_impl(N, K, bits, block_size, bq_len, scales_len, zero_points ? 1 : 0, zp_len, -1);
+    if (scales_type != MS_HIP_DTYPE_F32 && scales_type != MS_HIP_DTYPE_F16)
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] scales must be Float32 or Float16");
+    if (!zero_points) zp_type = MS_HIP_DTYPE_NONE;
+    const int zp_kind = zp_type == MS_HIP_DTYPE_NONE ? 0 : zp_type == MS_HIP_DTYPE_U8 ? 1
+                      : (zp_type == MS_HIP_DTYPE_F32 || zp_type == MS_HIP_DTYPE_F16) ? 2 : 3;
+    int st = check_impl(N, K, bits, block_size, bq_len, scales_len, zp_kind, zp_len, -1);
     if (st) return st;
     if (!bq || !scales) return fail(MS_HIP_ERR_INVALID, "[ms_hip] null B or scales pointer");
     if ((st = require_device())) return st;
     MS_HIP_CHECK(hipSetDevice(device_info().device));
     Weights* w = nullptr;
-    if ((st = new_weights(N, K, bits, block_size, zero_points != nullptr, &w))) return st;
+    if ((st = new_weights(N, K, bits, block_size, zp_kind, &w))) return st;
     hipError_t e = hipMemcpy(w->d_b, bq, (size_t)N * w->row_bytes, hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = hipMemcpy(w->d_scales, scales, (size_t)N * w->nb * sizeof(float), hipMemcpyHostToDevice);
-    if (e == hipSuccess && zero_points) e = hipMemcpy(w->d_zp, zero_points, (size_t)N * w->zrb, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = upload_f32(w->d_scales, scales, (int64_t)N * w->nb, scales_type, hipMemcpyHostToDevice);
+    if (e == hipSuccess && zp_kind == 1)
+        e = hipMemcpy(w->d_zp, zero_points, (size_t)N * w->zrb, hipMemcpyHostToDevice);
+    if (e == hipSuccess && zp_kind == 2)
+        e = upload_f32(w->d_zpf, zero_points, (int64_t)N * w->nb, zp_type, hipMemcpyHostToDevice);
     if (e != hipSuccess) st = fail(MS_HIP_ERR_HIP, "[ms_hip] weight upload failed: %s", hipGetErrorString(e));
     return finish_create(w, st, out_handle);
+}
+
+int ms_hip_nbits_weights_create(const uint8_t* bq, int64_t bq_len, const float* scales, int64_t scales_len,
+                                const uint8_t* zero_points, int64_t zp_len, int N, int K, int bits,
+                                int block_size, void** out_handle)
+{
+    return ms_hip_nbits_weights_create_ex(bq, bq_len, scales, scales_len, MS_HIP_DTYPE_F32, zero_points, zp_len,
+                                          zero_points ? MS_HIP_DTYPE_U8 : MS_HIP_DTYPE_NONE, N, K, bits, block_size,
+                                          out_handle);
 }
 
 int ms_hip_nbits_weights_create_dev(const uint8_t* d_bq, const float* d_scales, const uint8_t* d_zero_points,
@@ -1208,7 +1367,7 @@ int ms_hip_nbits_weights_create_dev(const uint8_t* d_bq, const float* d_scales, 
     if ((st = require_device())) return st;
     MS_HIP_CHECK(hipSetDevice(device_info().device));
     Weights* w = nullptr;
-    if ((st = new_weights(N, K, bits, block_size, d_zero_points != nullptr, &w))) return st;
+    if ((st = new_weights(N, K, bits, block_size, d_zero_points ? 1 : 0, &w))) return st;
     hipError_t e = hipMemcpy(w->d_b, d_bq, (size_t)N * w->row_bytes, hipMemcpyDeviceToDevice);
     if (e == hipSuccess) e = hipMemcpy(w->d_scales, d_scales, (size_t)N * w->nb * sizeof(float), hipMemcpyDeviceToDevice);
     if (e == hipSuccess && d_zero_points)
@@ -1256,6 +1415,36 @@ int ms_hip_nbits_gemm_dev(void* handle, const float* dA, float* dY, int M, void*
     const int st = take_device_error(*w, s);
     if (st) return st;
     return enqueue_gemm(*w, dA, dY, M, s);
+}
+
+int ms_hip_nbits_gemm_dev_f16(void* handle, const void* dA16, float* dY, int M, void* stream)
+{
+    Weights* w = from_handle(handle);
+    if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    int st = take_device_error(*w, s);
+    if (st) return st;
+    if (M < 0) return fail(MS_HIP_ERR_INVALID, "MatMulNBits M must be non-negative; got %d.", M);
+    if (M == 0) return MS_HIP_OK;
+    if (!dA16 || !dY) return fail(MS_HIP_ERR_INVALID, "[ms_hip] null activation or output pointer");
+    if ((reinterpret_cast<uintptr_t>(dA16) & 1) || (reinterpret_cast<uintptr_t>(dY) & 3))
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] A must be 2-byte and Y 4-byte aligned");
+    const Knobs kn = knobs_of(*w);
+    const KernelId k = choose_kernel(*w, kn, M);
+    size_t need_d = 0, need_c = 0;
+    workspace_need(*w, kn, k, M, &need_d, &need_c);
+    const size_t a_off = align256(need_d);
+    Ws ws;
+    const int r = ensure_ws(*w, a_off + (size_t)M * w->K * sizeof(float), need_c, s, &ws);
+    if (r < 0) return fail(MS_HIP_ERR_HIP, "[ms_hip] workspace allocation failed: %s", hipGetErrorString(hipGetLastError()));
+    if (r == 0)
+        return fail(MS_HIP_ERR_UNSUPPORTED,
+                    "[ms_hip] fp16 activations need the handle's workspace, which cannot grow under stream capture: "
+                    "make one call of this size outside the capture first");
+    float* a32 = reinterpret_cast<float*>(ws.data + a_off);
+    launch_widen(dA16, a32, (int64_t)M * w->K, s);
+    MS_HIP_CHECK(hipGetLastError());
+    return launch_kernel(*w, kn, k, ws, a32, dY, M, s);
 }
 
 int ms_hip_nbits_gemm_dev_noalloc(void* handle, const float* dA, float* dY, int M, void* stream)
@@ -1552,6 +1741,11 @@ int ms_hip_nbits_launch_info(void* handle, int M, int* kernel_id, int* lanes_per
     int G = 0, gr = 0, bl = 256;
     switch (kid) {
         case kGeneric: gr = (int)(((int64_t)M * w->N + 255) / 256); break;
+        case kGemvGeneral: gr = (w->N + kGenRowsPerWg - 1) / kGenRowsPerWg; G = 16; break;
+        case kMfmaGeneral:
+            gr = ((M + kGenBM - 1) / kGenBM) * ((w->N + kGenBN - 1) / kGenBN);
+            gr = ((gr + kXcds - 1) / kXcds) * kXcds;
+            break;
         case kSkinny: gr = ((w->N + kSkinnyRows - 1) / kSkinnyRows) * skinny_ksw(*w, kn); break;
         case kGemv: {
             const GemvConfig& c = kGemvConfigs[pick_gemv_config(*w, kn, M, w->N)];
@@ -1568,8 +1762,12 @@ int ms_hip_nbits_launch_info(void* handle, int M, int* kernel_id, int* lanes_per
             break;
         }
         case kRb:
-            gr = ((M + kRbBM - 1) / kRbBM) * ((w->N + kRbBN - 1) / kRbBN) * rb_ksw(*w, kn, M);
+        {
+            const RbShape sh = rb_shape(*w, kn, M);
+            gr = sh.tiles_m * sh.tiles_n * sh.ksw;
             gr = ((gr + kXcds - 1) / kXcds) * kXcds;
+            G = 64 * sh.nf;   // reported as the tile width
+        }
             break;
         case kPipe: {
             const PipeSplit sp = pipe_split(*w, kn, M);

@@ -5,10 +5,11 @@ A drop-in for the reference's managed kernel behind the same interface
 src/ModelSharp/Cpu/Kernels/Quantize/MatMulNBitsKernel.cs:79-169 does (same
 checks, same order, same messages), keeps one device-resident weight handle per
 initializer (created at load time by preload(), or on first use), and calls the
-C ABI of libms_hip_nbits.so. It never falls back to a CPU kernel: inputs the C
-ABI cannot take (float zero points, a non-uint8 B) raise
-DeviceUnsupportedInput, which a host engine answers by keeping the reference's
-own managed kernel registered for such nodes (the C# binding does exactly that).
+C ABI of libms_hip_nbits.so. It never falls back to a CPU kernel: every input
+the managed kernel accepts runs on the device — packed or float zero points,
+Float32 or Float16 scales (widened exactly on the device, as GraphContext.Get
+widens them, GraphContext.cs:106), Float32 or Float16 activations, bits 4 or 8,
+any block size.
 """
 from __future__ import annotations
 
@@ -20,16 +21,17 @@ from . import native
 from .graph import GraphContext, GraphNode, IKernel, KernelRegistry, ModelGraph, ModelSharpException, element_type
 
 
-class DeviceUnsupportedInput(ModelSharpException):
-    """Valid operator input that the HIP path does not take (the reference's
-    native seam declines the same inputs: NativeQuant.cs:78-101,
-    MatMulNBitsKernel.cs:172-174)."""
-
-
 def _to_numpy(t):
     if isinstance(t, np.ndarray):
         return t
     return t.detach().cpu().numpy()
+
+
+def _raw_float(t) -> np.ndarray:
+    """Host copy of a float tensor in its stored type when the C ABI takes that type
+    (Float32, Float16), else widened to Float32 as GraphContext.Get does."""
+    x = _to_numpy(t)
+    return x if x.dtype in (np.float32, np.float16) else x.astype(np.float32)
 
 
 class HipMatMulNBitsKernel(IKernel):
@@ -42,7 +44,7 @@ class HipMatMulNBitsKernel(IKernel):
     # ---- validation: MatMulNBitsKernel.cs:79-161 ----------------------------------------
     @staticmethod
     def _validate(node: GraphNode, ctx: GraphContext):
-        a = ctx.get(node.inputs[0])
+        a = ctx.get_tensor(node.inputs[0])   # Float16 stays Float16: widened on the device
         b = ctx.get_tensor(node.inputs[1])
         if element_type(b) != "UInt8":                          # QuantizeKernels.cs:54-56
             raise ModelSharpException(f"Tensor dtype is {element_type(b)}; expected UInt8.")
@@ -86,16 +88,12 @@ class HipMatMulNBitsKernel(IKernel):
     # from: a context that binds those names to other tensors gets a new handle (the old
     # one is closed), the same tensors always find the same handle.
     def _weights(self, node, b, scales, zp, N, K, bits, block_size) -> native.NBitsWeights:
-        if zp is not None and element_type(zp) == "Float32":
-            raise DeviceUnsupportedInput(
-                "MatMulNBits float zero_points are not representable in the HIP C ABI; "
-                "run this node on the managed kernel.")
         key = tuple(node.inputs[1:4])
         with self._lock:
             entry = self._handles.get(key)
             if entry is not None and entry[0][0] is b and entry[0][1] is scales and entry[0][2] is zp:
                 return entry[1]
-            w = native.NBitsWeights(_to_numpy(b), _to_numpy(scales).astype(np.float32),
+            w = native.NBitsWeights(_to_numpy(b), _raw_float(scales),
                                     None if zp is None else _to_numpy(zp), N, K, bits, block_size)
             if entry is not None:
                 entry[1].close()
@@ -139,12 +137,19 @@ class HipMatMulNBitsKernel(IKernel):
         lead = tuple(a.shape[:-1])
         M = int(np.prod(lead)) if lead else 1
         if isinstance(a, np.ndarray):
-            y = w.gemm(a.reshape(M, K)).reshape(lead + (N,))
+            y = w.gemm(a.reshape(M, K).astype(np.float32, copy=False)).reshape(lead + (N,))
         else:
             import torch
-            a2 = a.reshape(M, K).contiguous()
+            a2 = a.reshape(M, K)
+            if a2.dtype not in (torch.float32, torch.float16):
+                a2 = a2.float()
+            a2 = a2.contiguous()
             y = torch.empty(lead + (N,), dtype=torch.float32, device=a.device)
-            w.gemm_dev(a2.data_ptr(), y.data_ptr(), M, torch.cuda.current_stream(a.device).cuda_stream)
+            stream = torch.cuda.current_stream(a.device).cuda_stream
+            if a2.dtype == torch.float16:
+                w.gemm_dev_f16(a2.data_ptr(), y.data_ptr(), M, stream)
+            else:
+                w.gemm_dev(a2.data_ptr(), y.data_ptr(), M, stream)
         ctx.set(node.outputs[0], y)
 
 

@@ -19,7 +19,8 @@ import numpy as np
 _PKG = pathlib.Path(__file__).resolve().parent
 LIB_NAME = "libms_hip_nbits.so"
 # Kernel ids of ms_hip_nbits_launch_info.
-KERNEL_NAMES = ("generic", "gemv_w4", "mfma_w4", "gemv_w4_panel", "mfma_w4_pipe", "skinny_w4", "mfma_w4_rb")
+KERNEL_NAMES = ("generic", "gemv_w4", "mfma_w4", "gemv_w4_panel", "mfma_w4_pipe", "skinny_w4", "mfma_w4_rb",
+                "gemv_general", "mfma_general")
 HEADER = _PKG.parent / "include" / "ms_hip_kernels.h"
 
 MS_HIP_OK = 0
@@ -28,6 +29,9 @@ MS_HIP_ERR_NO_DEVICE = 2
 MS_HIP_ERR_HIP = 3
 MS_HIP_ERR_UNSUPPORTED = 4
 MS_HIP_TUNING_INHERIT = -(2 ** 31)
+MS_HIP_DTYPE_NONE, MS_HIP_DTYPE_F32, MS_HIP_DTYPE_F16, MS_HIP_DTYPE_U8 = 0, 1, 2, 3
+_DTYPE_CODE = {np.dtype(np.float32): MS_HIP_DTYPE_F32, np.dtype(np.float16): MS_HIP_DTYPE_F16,
+               np.dtype(np.uint8): MS_HIP_DTYPE_U8}
 
 _c_int = ctypes.c_int
 _c_i64 = ctypes.c_int64
@@ -45,6 +49,9 @@ _PROTOTYPES = {
     "ms_hip_nbits_check": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_int, _c_i64, _c_i64]),
     "ms_hip_nbits_weights_create": (
         _c_int, [_vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_vp)]),
+    "ms_hip_nbits_weights_create_ex": (
+        _c_int, [_vp, _c_i64, _vp, _c_i64, _c_int, _vp, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int,
+                 ctypes.POINTER(_vp)]),
     "ms_hip_nbits_weights_create_dev": (
         _c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_vp)]),
     "ms_hip_nbits_weights_destroy": (_c_int, [_vp]),
@@ -52,6 +59,7 @@ _PROTOTYPES = {
     "ms_hip_nbits_gemm": (_c_int, [_vp, _vp, _vp, _c_int]),
     "ms_hip_nbits_gemm_dev": (_c_int, [_vp, _vp, _vp, _c_int, _vp]),
     "ms_hip_nbits_gemm_dev_noalloc": (_c_int, [_vp, _vp, _vp, _c_int, _vp]),
+    "ms_hip_nbits_gemm_dev_f16": (_c_int, [_vp, _vp, _vp, _c_int, _vp]),
     "ms_hip_nbits_device_error": (_c_int, [_vp]),
     "ms_hip_nbits_gemm_dev_batch": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _vp]),
     "ms_hip_qgemm_nbits": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int]),
@@ -153,13 +161,24 @@ class NBitsWeights:
 
     def __init__(self, b: np.ndarray, scales: np.ndarray, zero_points: np.ndarray | None,
                  N: int, K: int, bits: int = 4, block_size: int = 32):
+        """scales float32 or float16; zero_points packed uint8, float32 or float16, or None
+        (the operator's element types, ms_hip_nbits_weights_create_ex)."""
         lib = load()
         b = np.ascontiguousarray(b, dtype=np.uint8).reshape(-1)
-        scales = np.ascontiguousarray(scales, dtype=np.float32).reshape(-1)
-        zp = None if zero_points is None else np.ascontiguousarray(zero_points, dtype=np.uint8).reshape(-1)
+        scales = np.ascontiguousarray(scales)
+        if scales.dtype not in (np.float32, np.float16):
+            scales = scales.astype(np.float32)
+        scales = scales.reshape(-1)
+        zp = None
+        if zero_points is not None:
+            zp = np.ascontiguousarray(zero_points)
+            if zp.dtype not in (np.uint8, np.float32, np.float16):
+                raise ValueError(f"zero points of dtype {zp.dtype}")
+            zp = zp.reshape(-1)
         handle = _vp()
-        check(lib.ms_hip_nbits_weights_create(
-            _ptr(b), b.size, _ptr(scales), scales.size, _ptr(zp), 0 if zp is None else zp.size,
+        check(lib.ms_hip_nbits_weights_create_ex(
+            _ptr(b), b.size, _ptr(scales), scales.size, _DTYPE_CODE[scales.dtype], _ptr(zp),
+            0 if zp is None else zp.size, MS_HIP_DTYPE_NONE if zp is None else _DTYPE_CODE[zp.dtype],
             int(N), int(K), int(bits), int(block_size), ctypes.byref(handle)))
         self._init(handle, N, K, bits, block_size, zp is not None)
 
@@ -196,6 +215,10 @@ class NBitsWeights:
 
     def dequant_dev(self, dW: int, stream: int | None = None) -> None:
         check(load().ms_hip_nbits_dequant_dev(self.handle, _vp(dW), _vp(stream or 0)))
+
+    def gemm_dev_f16(self, dA16: int, dY: int, M: int, stream: int | None = None) -> None:
+        """gemm_dev with fp16 activations (widened exactly on the device)."""
+        check(load().ms_hip_nbits_gemm_dev_f16(self.handle, _vp(dA16), _vp(dY), int(M), _vp(stream or 0)))
 
     def gemm_dev_noalloc(self, dA: int, dY: int, M: int, stream: int | None = None) -> None:
         """gemm_dev with the library's fixed per-GPU scratch instead of the handle's

@@ -1,0 +1,228 @@
+"""Device parity for the weight formats outside the 4-bit fast kernels, against the
+oracle (the managed kernel's arithmetic, MatMulNBitsKernel.cs:193-262):
+
+* 8-bit codes (MatMulNBitsSimd.cs:117-132), float zero points
+  (MatMulNBitsKernel.cs:239-240), block sizes other than 32/64/128/256, K not a
+  multiple of 32 — the general GEMV (M <= 16) and the general MFMA GEMM (M > 16);
+* Float16 scales, zero points and activations, widened exactly on the device as
+  GraphContext.Get widens them on the host (GraphContext.cs:106): the results equal
+  those of the same values handed over as Float32, bit for bit.
+
+Tolerances: the dequantized weights are bit-exact; the GEMV sums the same fp32 products
+in another order, so each output lies within 2*gamma_K * sum_k |a_k w_nk| of the
+oracle's; the MFMA GEMM multiplies fp16 hi/lo splits of A and W (each split exact to
+2^-22 relative, below 2^-24 of the row's largest element absolute) and sums in fp32, so
+each output lies within 4*(2*gamma_K) + 2^-20 of sum_k |a_k w_nk| plus 2^-30 of
+max_k |a_k| * sum_k |w_nk|.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from modelsharp_amd import native, workloads
+from modelsharp_amd.workloads import Op
+
+pytestmark = pytest.mark.gpu
+
+
+def log(msg):
+    print(msg, flush=True)
+
+
+def float_zero_points(op: Op, seed: int) -> np.ndarray:
+    """Per-block float zero points in [0, 2^bits - 1], with fractional parts."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    return rng.uniform(0.0, float((1 << op.bits) - 1), size=op.N * op.nb).astype(np.float32)
+
+
+def dot_abs(a, W):
+    return np.abs(a).astype(np.float64) @ np.abs(W).astype(np.float64).T
+
+
+def gamma2(K):
+    u = np.finfo(np.float32).eps / 2
+    return 2 * K * u / (1 - K * u)
+
+
+def assert_within(y, ref, allowed, what):
+    err = np.abs(y.astype(np.float64) - ref.astype(np.float64))
+    ratio = float(np.max(err / np.maximum(allowed, 1e-300)))
+    log(f"  {what}: max err / bound {ratio:.3e}")
+    assert np.all(err <= allowed), f"{what}: err/bound {ratio:.3e}"
+
+
+def check_against_oracle(w, a, b, s, zp, zpf, op, what):
+    M = a.shape[0]
+    kernel = w.launch_info(M)["kernel"]
+    y = w.gemm(a)
+    ref = oracle.matmul_nbits(a, b, s, zp, op.N, op.K, op.bits, op.block_size, zp_float=zpf)
+    W = oracle.dequant_weights(b, s, zp, op.N, op.K, op.bits, op.block_size, zp_float=zpf)
+    cond = dot_abs(a, W)
+    if kernel == "mfma_general":
+        allowed = (4 * gamma2(op.K) + 2.0 ** -20) * cond + 2.0 ** -30 * (
+            np.max(np.abs(a), axis=1, keepdims=True).astype(np.float64) * np.abs(W).sum(axis=1)[None, :])
+    else:
+        allowed = gamma2(op.K) * cond
+    assert_within(y, ref, allowed, f"{what} [{kernel}]")
+    return kernel, W
+
+
+FORMATS = [
+    Op("b8_zp", 512, 72, 32, True, bits=8),
+    Op("b8_sym_bs128", 1024, 40, 128, False, bits=8),
+    Op("b8_bs24_tail", 264, 20, 24, True, bits=8),      # 11 blocks of 24
+    Op("b4_bs16", 256, 50, 16, True),
+    Op("b4_bs48", 480, 33, 48, True),
+    Op("b4_k1000_bs40", 1000, 64, 40, True),            # K % 32 != 0
+    Op("b4_k1000_bs32_tail", 1000, 70, 32, False),      # partial last block of 8
+]
+MS = [1, 3, 16, 17, 40, 130]
+
+
+@pytest.mark.parametrize("op", FORMATS, ids=lambda o: o.name)
+@pytest.mark.parametrize("M", MS)
+def test_general_formats(gpu, op, M):
+    b, s, z = workloads.make_weights(op, seed=op.K + op.N + M)
+    a = workloads.make_activations(M, op.K, seed=3 * M + op.N)
+    w = native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
+    log(f"general {op.name} M={M} {w.launch_info(M)}")
+    kernel, W = check_against_oracle(w, a, b, s, z, None, op, f"{op.name} M={M}")
+    assert kernel == ("gemv_general" if M <= 16 else "mfma_general")
+    assert np.array_equal(w.dequant(), W)
+    w.close()
+
+
+FLOAT_ZP = [
+    Op("fzp_b4_bs32", 512, 96, 32, True),
+    Op("fzp_b4_bs128", 2048, 64, 128, True),
+    Op("fzp_b8_bs64", 640, 48, 64, True, bits=8),
+    Op("fzp_b4_bs40", 1000, 30, 40, True),
+]
+
+
+@pytest.mark.parametrize("op", FLOAT_ZP, ids=lambda o: o.name)
+@pytest.mark.parametrize("M", [1, 7, 16, 33, 200])
+def test_float_zero_points(gpu, op, M):
+    b, s, _ = workloads.make_weights(op, seed=op.K * 3 + M)
+    zpf = float_zero_points(op, seed=op.N + M)
+    a = workloads.make_activations(M, op.K, seed=M + 11)
+    w = native.NBitsWeights(b, s, zpf, op.N, op.K, op.bits, op.block_size)
+    log(f"float zp {op.name} M={M} {w.launch_info(M)}")
+    kernel, W = check_against_oracle(w, a, b, s, None, zpf, op, f"{op.name} M={M}")
+    assert kernel == ("gemv_general" if M <= 16 else "mfma_general")
+    assert np.array_equal(w.dequant(), W)
+    w.close()
+
+
+def test_general_mfma_full_size_8bit(gpu):
+    """8-bit weights at a 7B projection's shape (K=4096, N=4096) over 128 rows."""
+    op = Op("b8_7b", 4096, 4096, 32, True, bits=8)
+    b, s, z = workloads.make_weights(op, seed=5)
+    a = workloads.make_activations(128, op.K, seed=6, kind="rmsnorm")
+    w = native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
+    log(f"8-bit 4096x4096 M=128 {w.launch_info(128)}")
+    kernel, _ = check_against_oracle(w, a, b, s, z, None, op, "b8 K=4096 N=4096 M=128")
+    assert kernel == "mfma_general"
+    y1 = w.gemm(a)
+    assert np.array_equal(y1, w.gemm(a))   # deterministic
+    a1 = a[:1]
+    kernel, _ = check_against_oracle(w, a1, b, s, z, None, op, "b8 K=4096 N=4096 M=1")
+    assert kernel == "gemv_general"
+    w.close()
+
+
+def test_dynamic_range_general_mfma(gpu):
+    """Rows of A and W scaled over 2^-40 .. 2^40: the per-row power-of-two splits keep
+    every row at fp32-level accuracy."""
+    op = Op("range", 512, 64, 32, True, bits=8)
+    b, s, z = workloads.make_weights(op, seed=21)
+    s = (s.reshape(op.N, op.nb) * np.float32(2.0) ** np.arange(-32, 32, dtype=np.float32)[:, None]).reshape(-1)
+    s = s.astype(np.float32)
+    a = workloads.make_activations(48, op.K, seed=22)
+    a = (a * np.float32(2.0) ** np.linspace(-40, 40, 48).round().astype(np.float32)[:, None]).astype(np.float32)
+    w = native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
+    kernel, _ = check_against_oracle(w, a, b, s, z, None, op, "range M=48")
+    assert kernel == "mfma_general"
+    w.close()
+
+
+# ---- Float16 inputs ------------------------------------------------------------------------
+F16_OPS = [Op("f16_fast", 4096, 256, 32, True), Op("f16_fast_bs128", 2048, 192, 128, False),
+           Op("f16_b8", 512, 64, 32, True, bits=8)]
+
+
+@pytest.mark.parametrize("op", F16_OPS, ids=lambda o: o.name)
+def test_f16_scales_equal_widened(gpu, op):
+    b, s, z = workloads.make_weights(op, seed=op.N)
+    s16 = s.astype(np.float16)
+    w16 = native.NBitsWeights(b, s16, z, op.N, op.K, op.bits, op.block_size)
+    w32 = native.NBitsWeights(b, s16.astype(np.float32), z, op.N, op.K, op.bits, op.block_size)
+    assert np.array_equal(w16.dequant(), w32.dequant())
+    for M in (1, 8, 64):
+        a = workloads.make_activations(M, op.K, seed=M)
+        log(f"f16 scales {op.name} M={M} {w16.launch_info(M)}")
+        assert np.array_equal(w16.gemm(a), w32.gemm(a)), f"{op.name} M={M}"
+    w16.close()
+    w32.close()
+
+
+def test_f16_zero_points_equal_widened(gpu):
+    op = Op("f16_zp", 512, 40, 32, True)
+    b, s, _ = workloads.make_weights(op, seed=3)
+    z16 = float_zero_points(op, seed=4).astype(np.float16)
+    w16 = native.NBitsWeights(b, s, z16, op.N, op.K, op.bits, op.block_size)
+    w32 = native.NBitsWeights(b, s, z16.astype(np.float32), op.N, op.K, op.bits, op.block_size)
+    assert np.array_equal(w16.dequant(), w32.dequant())
+    for M in (1, 20):
+        a = workloads.make_activations(M, op.K, seed=M + 1)
+        assert np.array_equal(w16.gemm(a), w32.gemm(a))
+    w16.close()
+    w32.close()
+
+
+@pytest.mark.parametrize("op", F16_OPS, ids=lambda o: o.name)
+def test_f16_activations_equal_widened(gpu, op):
+    import torch
+    b, s, z = workloads.make_weights(op, seed=op.K)
+    w = native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
+    dev = torch.device("cuda", 0)
+    for M in (1, 5, 16, 64, 300):
+        a16 = torch.from_numpy(workloads.make_activations(M, op.K, seed=M + 2)).to(torch.float16).to(dev)
+        a32 = a16.float().contiguous()
+        y16 = torch.empty((M, op.N), dtype=torch.float32, device=dev)
+        y32 = torch.empty_like(y16)
+        log(f"f16 A {op.name} M={M} {w.launch_info(M)}")
+        w.gemm_dev_f16(a16.data_ptr(), y16.data_ptr(), M)
+        w.gemm_dev(a32.data_ptr(), y32.data_ptr(), M)
+        torch.cuda.synchronize()
+        assert torch.equal(y16, y32), f"{op.name} M={M}"
+    w.close()
+
+
+def test_operator_routes_float16_and_float_zero_points(gpu):
+    """The operator mirror runs Float16 scales, float zero points and Float16
+    activations on the device and matches the oracle on the widened values."""
+    import torch
+    from modelsharp_amd.graph import GraphContext, GraphNode
+    from modelsharp_amd.hip_kernel import HipMatMulNBitsKernel
+
+    op = Op("op_f16", 640, 56, 64, True)
+    b, s, _ = workloads.make_weights(op, seed=8)
+    s16 = s.astype(np.float16)
+    zpf = float_zero_points(op, seed=9)
+    a16 = workloads.make_activations(24, op.K, seed=10).astype(np.float16)
+    node = GraphNode("MatMulNBits", "n0", ["A", "B", "scales", "zp"], ["Y"],
+                     {"N": op.N, "K": op.K, "bits": 4, "block_size": op.block_size})
+    k = HipMatMulNBitsKernel()
+    ctx = GraphContext({"A": torch.from_numpy(a16).cuda(), "B": b, "scales": s16, "zp": zpf})
+    k.execute(node, ctx)
+    y = ctx.get_tensor("Y").cpu().numpy()
+    a32 = a16.astype(np.float32)
+    ref = oracle.matmul_nbits(a32, b, s16.astype(np.float32), None, op.N, op.K, 4, op.block_size, zp_float=zpf)
+    W = oracle.dequant_weights(b, s16.astype(np.float32), None, op.N, op.K, 4, op.block_size, zp_float=zpf)
+    allowed = (4 * gamma2(op.K) + 2.0 ** -20) * dot_abs(a32, W) + 2.0 ** -30 * (
+        np.max(np.abs(a32), axis=1, keepdims=True).astype(np.float64) * np.abs(W).sum(axis=1)[None, :])
+    assert_within(y, ref, allowed, "operator f16 / float zp M=24")
+    k.close()
