@@ -39,6 +39,8 @@ extern "C" {
 #define MS_HIP_ERR_NO_DEVICE    2  /* no usable gfx950 device                */
 #define MS_HIP_ERR_HIP          3  /* a HIP runtime call failed              */
 #define MS_HIP_ERR_UNSUPPORTED  4  /* valid operator input this ABI cannot take */
+#define MS_HIP_ERR_DISABLED     5  /* MODELSHARP_HIP=0 (off, false) turned the library off */
+#define MS_HIP_ERR_FORCED       6  /* forced failure: MS_HIP_FORCE_FAIL=1 or ms_hip_debug_force_failure */
 
 /* Element types of ms_hip_nbits_weights_create_ex's scales and zero points. */
 #define MS_HIP_DTYPE_NONE       0  /* no zero-point tensor (default zero point) */
@@ -53,10 +55,23 @@ extern "C" {
  * Replace ms_build_info / ms_has_avx512 / ms_has_vnni
  * (native/ms_kernels.h:23-25, native/src/info.cpp:10-26) for the GPU library:
  * the C# guard probes these before routing (NativeQuant.cs:41-56). */
-int         ms_hip_available(void);     /* 1 if a gfx950 device is usable, else 0 */
+int         ms_hip_available(void);     /* 1 if a gfx950 device is usable, else 0
+                                           (0 also under MODELSHARP_HIP=0)          */
 const char* ms_hip_device_name(void);   /* "" when unavailable                    */
 const char* ms_hip_build_info(void);
 const char* ms_hip_last_error(void);    /* thread-local, "" when none              */
+
+/* Switches (the reference's MODELSHARP_NATIVE / MODELSHARP_NATIVE_QUANT convention,
+ * NativeGemm.cs:42-57, NativeQuant.cs:33-56), read once on first use:
+ *   MODELSHARP_HIP in {0, off, false}: the library is off — ms_hip_available() returns 0
+ *     and every entry that creates weights or computes returns MS_HIP_ERR_DISABLED
+ *     without a HIP call;
+ *   MS_HIP_FORCE_FAIL in {1, on, true}: those entries return MS_HIP_ERR_FORCED, so a
+ *     caller's managed fallback can be exercised on any host.
+ * ms_hip_debug_force_failure(on) sets the forced failure at run time (the reference's
+ * enable flags are likewise settable for tests, NativeQuant.cs:33-39). Validation
+ * (ms_hip_nbits_check), queries and ms_hip_last_error keep working. */
+int ms_hip_debug_force_failure(int on);
 
 /* ---- validation ------------------------------------------------------------
  * The operator's input rules, MatMulNBitsKernel.cs:87-145 and :158-161, with

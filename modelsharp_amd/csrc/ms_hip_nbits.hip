@@ -27,12 +27,16 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 #include <mutex>
 #include <string>
 #include <unordered_set>
 #include <utility>
 #include <vector>
+
+#include <strings.h>
 
 #include "gemv_general.h"
 #include "gemv_w4.h"
@@ -100,8 +104,46 @@ const DeviceInfo& device_info()
     return info;
 }
 
+// ---- switches ---------------------------------------------------------------------------
+// MODELSHARP_HIP in {0, off, false} turns the library off for the process (read once, on
+// first use, before any HIP call): ms_hip_available() answers 0 and every entry that
+// creates weights or computes returns MS_HIP_ERR_DISABLED, as MODELSHARP_NATIVE=0 keeps
+// the reference's native library out (NativeGemm.cs:42-57). MS_HIP_FORCE_FAIL in
+// {1, on, true}, or ms_hip_debug_force_failure(1), makes those entries fail with
+// MS_HIP_ERR_FORCED before touching anything, so a caller's fallback can be tested on any
+// host (the reference's switches are settable for tests, NativeQuant.cs:33-39).
+bool env_is(const char* name, std::initializer_list<const char*> values)
+{
+    const char* v = std::getenv(name);
+    if (!v) return false;
+    for (const char* x : values)
+        if (strcasecmp(v, x) == 0) return true;
+    return false;
+}
+
+bool disabled()
+{
+    static const bool off = env_is("MODELSHARP_HIP", {"0", "off", "false"});
+    return off;
+}
+
+std::atomic<int>& forced_failure()
+{
+    static std::atomic<int> on{env_is("MS_HIP_FORCE_FAIL", {"1", "on", "true"}) ? 1 : 0};
+    return on;
+}
+
+int gate()
+{
+    if (disabled()) return fail(MS_HIP_ERR_DISABLED, "[ms_hip] disabled by MODELSHARP_HIP=%s", std::getenv("MODELSHARP_HIP"));
+    if (forced_failure().load(std::memory_order_relaxed))
+        return fail(MS_HIP_ERR_FORCED, "[ms_hip] forced failure (MS_HIP_FORCE_FAIL / ms_hip_debug_force_failure)");
+    return MS_HIP_OK;
+}
+
 int require_device()
 {
+    if (int st = gate()) return st;
     const DeviceInfo& d = device_info();
     if (!d.ok) return fail(MS_HIP_ERR_NO_DEVICE, "[ms_hip] no gfx950 device is available");
     return MS_HIP_OK;
@@ -1300,7 +1342,13 @@ int scratch_for(int dev, uint8_t** out)
 // =========================================================================================
 extern "C" {
 
-int ms_hip_available(void) { return device_info().ok; }
+int ms_hip_available(void) { return disabled() ? 0 : device_info().ok; }
+
+int ms_hip_debug_force_failure(int on)
+{
+    forced_failure().store(on ? 1 : 0, std::memory_order_relaxed);
+    return MS_HIP_OK;
+}
 
 const char* ms_hip_device_name(void) { return device_info().name.c_str(); }
 
@@ -1409,6 +1457,7 @@ int ms_hip_nbits_weights_info(void* handle, int* N, int* K, int* bits, int* bloc
 
 int ms_hip_nbits_gemm_dev(void* handle, const float* dA, float* dY, int M, void* stream)
 {
+    if (int st = gate()) return st;
     Weights* w = from_handle(handle);
     if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
     const hipStream_t s = static_cast<hipStream_t>(stream);
@@ -1419,6 +1468,7 @@ int ms_hip_nbits_gemm_dev(void* handle, const float* dA, float* dY, int M, void*
 
 int ms_hip_nbits_gemm_dev_f16(void* handle, const void* dA16, float* dY, int M, void* stream)
 {
+    if (int st = gate()) return st;
     Weights* w = from_handle(handle);
     if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
     const hipStream_t s = static_cast<hipStream_t>(stream);
@@ -1449,6 +1499,7 @@ int ms_hip_nbits_gemm_dev_f16(void* handle, const void* dA16, float* dY, int M, 
 
 int ms_hip_nbits_gemm_dev_noalloc(void* handle, const float* dA, float* dY, int M, void* stream)
 {
+    if (int st = gate()) return st;
     Weights* w = from_handle(handle);
     if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
     const hipStream_t s = static_cast<hipStream_t>(stream);
@@ -1495,6 +1546,7 @@ int ms_hip_nbits_device_error(void* handle)
 int ms_hip_nbits_gemm_dev_batch(void* const* handles, const float* const* dA, float* const* dY, int count, int M,
                                 void* stream)
 {
+    if (int st = gate()) return st;
     if (count < 0 || (count > 0 && (!handles || !dA || !dY)))
         return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid batch arguments");
     std::vector<Weights*> ws((size_t)count);
@@ -1552,6 +1604,7 @@ int ms_hip_nbits_batch_launch_info(void* const* handles, const float* const* dA,
 
 int ms_hip_nbits_gemm(void* handle, const float* a_host, float* y_host, int M)
 {
+    if (int st = gate()) return st;
     Weights* w = from_handle(handle);
     if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
     if (M < 0) return fail(MS_HIP_ERR_INVALID, "MatMulNBits M must be non-negative; got %d.", M);
@@ -1603,6 +1656,7 @@ int ms_hip_nbits_gemm(void* handle, const float* a_host, float* y_host, int M)
 int ms_hip_qgemm_nbits(const float* a, const uint8_t* bq, const float* scales, const uint8_t* zero_points,
                        float* y, int M, int N, int K, int bits, int block_size)
 {
+    if (int st = gate()) return st;
     // Buffer lengths are implied by the dimensions here, as in ms_qgemm_nbits.
     if (N <= 0 || K <= 0 || (bits != 4 && bits != 8) || block_size <= 0)
         return check_impl(N, K, bits, block_size, 0, 0, 0, 0, -1);
@@ -1622,6 +1676,7 @@ int ms_hip_qgemm_nbits(const float* a, const uint8_t* bq, const float* scales, c
 
 int ms_hip_nbits_dequant_dev(void* handle, float* dW, void* stream)
 {
+    if (int st = gate()) return st;
     Weights* w = from_handle(handle);
     if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
     if (!dW) return fail(MS_HIP_ERR_INVALID, "[ms_hip] null output pointer");
@@ -1634,6 +1689,7 @@ int ms_hip_nbits_dequant_dev(void* handle, float* dW, void* stream)
 
 int ms_hip_nbits_dequant(void* handle, float* w_host)
 {
+    if (int st = gate()) return st;
     Weights* w = from_handle(handle);
     if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
     if (!w_host) return fail(MS_HIP_ERR_INVALID, "[ms_hip] null output pointer");

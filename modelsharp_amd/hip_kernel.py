@@ -13,6 +13,7 @@ any block size.
 """
 from __future__ import annotations
 
+import os
 import threading
 
 import numpy as np
@@ -153,7 +154,17 @@ class HipMatMulNBitsKernel(IKernel):
         ctx.set(node.outputs[0], y)
 
 
+def hip_enabled() -> bool:
+    """False under MODELSHARP_HIP in {0, off, false}: the kill switch (the convention of
+    MODELSHARP_NATIVE, NativeGemm.cs:53-57)."""
+    return os.environ.get("MODELSHARP_HIP", "").lower() not in ("0", "off", "false")
+
+
 def register_kernels(registry: KernelRegistry) -> KernelRegistry:
     """Routes MatMulNBits to the HIP kernel; last registration wins, as for
-    ImageSharpRegistration.RegisterKernels (src/ModelSharp.ImageSharp/ImageSharpRegistration.cs:52-60)."""
+    ImageSharpRegistration.RegisterKernels (src/ModelSharp.ImageSharp/ImageSharpRegistration.cs:52-60).
+    Under the kill switch the registry is left as it is (the kernel registered before
+    keeps the op)."""
+    if not hip_enabled():
+        return registry
     return registry.register(HipMatMulNBitsKernel())

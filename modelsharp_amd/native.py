@@ -28,6 +28,8 @@ MS_HIP_ERR_INVALID = 1
 MS_HIP_ERR_NO_DEVICE = 2
 MS_HIP_ERR_HIP = 3
 MS_HIP_ERR_UNSUPPORTED = 4
+MS_HIP_ERR_DISABLED = 5
+MS_HIP_ERR_FORCED = 6
 MS_HIP_TUNING_INHERIT = -(2 ** 31)
 MS_HIP_DTYPE_NONE, MS_HIP_DTYPE_F32, MS_HIP_DTYPE_F16, MS_HIP_DTYPE_U8 = 0, 1, 2, 3
 _DTYPE_CODE = {np.dtype(np.float32): MS_HIP_DTYPE_F32, np.dtype(np.float16): MS_HIP_DTYPE_F16,
@@ -59,6 +61,7 @@ _PROTOTYPES = {
     "ms_hip_nbits_gemm": (_c_int, [_vp, _vp, _vp, _c_int]),
     "ms_hip_nbits_gemm_dev": (_c_int, [_vp, _vp, _vp, _c_int, _vp]),
     "ms_hip_nbits_gemm_dev_noalloc": (_c_int, [_vp, _vp, _vp, _c_int, _vp]),
+    "ms_hip_debug_force_failure": (_c_int, [_c_int]),
     "ms_hip_nbits_gemm_dev_f16": (_c_int, [_vp, _vp, _vp, _c_int, _vp]),
     "ms_hip_nbits_device_error": (_c_int, [_vp]),
     "ms_hip_nbits_gemm_dev_batch": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _vp]),

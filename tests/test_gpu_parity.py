@@ -862,3 +862,27 @@ def test_destroyed_handle_is_rejected(gpu):
     lib = native.load()
     assert lib.ms_hip_nbits_weights_info(h, None, None, None, None, None) == native.MS_HIP_ERR_INVALID
     assert lib.ms_hip_nbits_weights_destroy(h) == native.MS_HIP_ERR_INVALID
+
+
+def test_forced_failure_leaves_output_untouched(gpu):
+    """A forced failure (the fallback test switch) refuses a live handle's call before any
+    launch; switched off, the same handle computes normally."""
+    import torch
+    op = workloads.Op("ff", 256, 64)
+    b, s, z, w = weights_for(op, 2)
+    a = torch.from_numpy(workloads.make_activations(3, op.K, seed=1)).cuda()
+    y = torch.full((3, op.N), 7.0, device="cuda")
+    lib = native.load()
+    try:
+        lib.ms_hip_debug_force_failure(1)
+        st = lib.ms_hip_nbits_gemm_dev(w.handle, native._vp(a.data_ptr()), native._vp(y.data_ptr()), 3, None)
+        assert st == native.MS_HIP_ERR_FORCED
+    finally:
+        lib.ms_hip_debug_force_failure(0)
+    torch.cuda.synchronize()
+    assert bool((y == 7.0).all())
+    w.gemm_dev(a.data_ptr(), y.data_ptr(), 3)
+    torch.cuda.synchronize()
+    ref = oracle.matmul_nbits(a.cpu().numpy(), b, s, z, op.N, op.K, 4, 32)
+    assert_gemv_close(y.cpu().numpy(), ref, "after forced failure")
+    w.close()

@@ -237,3 +237,87 @@ def test_unknown_handles_are_rejected_not_read():
     assert lib.ms_hip_nbits_gemm_dev(p, None, None, 1, None) == native.MS_HIP_ERR_INVALID
     assert lib.ms_hip_nbits_device_error(p) == native.MS_HIP_ERR_INVALID
     assert lib.ms_hip_nbits_weights_destroy(None) == native.MS_HIP_ERR_INVALID
+
+
+# ---- switches: MODELSHARP_HIP kill switch and forced failure (NativeGemm.cs:42-57) --------
+_SWITCH_PROBE = r"""
+import ctypes, json, sys
+sys.path.insert(0, sys.argv[1])
+from modelsharp_amd import native
+lib = native.load()
+h = ctypes.c_void_p()
+b = (ctypes.c_uint8 * 16)()
+s = (ctypes.c_float * 1)()
+st_create = lib.ms_hip_nbits_weights_create(b, 16, s, 1, None, 0, 1, 32, 4, 32, ctypes.byref(h))
+err = native.last_error()
+st_check = lib.ms_hip_nbits_check(1, 32, 4, 32, 16, 1, 0, 0, -1)
+print(json.dumps({"available": lib.ms_hip_available(), "create": st_create, "err": err, "check": st_check,
+                  "gemm": lib.ms_hip_nbits_gemm_dev(None, None, None, 1, None)}))
+"""
+
+
+def _probe_switches(env_extra):
+    import json
+    import os
+    import sys
+    env = {k: v for k, v in os.environ.items() if k not in ("MODELSHARP_HIP", "MS_HIP_FORCE_FAIL")}
+    env.update(env_extra)
+    out = subprocess.run([sys.executable, "-c", _SWITCH_PROBE, str(ROOT)], env=env, capture_output=True, text=True,
+                         timeout=120)
+    assert out.returncode == 0, out.stderr
+    return json.loads(out.stdout.strip().splitlines()[-1])
+
+
+@pytest.mark.parametrize("value", ["0", "off", "FALSE"])
+def test_kill_switch_turns_the_library_off(value):
+    r = _probe_switches({"MODELSHARP_HIP": value})
+    assert r["available"] == 0
+    assert r["create"] == native.MS_HIP_ERR_DISABLED and "MODELSHARP_HIP" in r["err"]
+    assert r["gemm"] == native.MS_HIP_ERR_DISABLED
+    assert r["check"] == 0   # validation keeps working
+
+
+@pytest.mark.parametrize("value", ["1", "on", "True"])
+def test_forced_failure_env(value):
+    r = _probe_switches({"MS_HIP_FORCE_FAIL": value})
+    assert r["create"] == native.MS_HIP_ERR_FORCED and "forced failure" in r["err"]
+    assert r["gemm"] == native.MS_HIP_ERR_FORCED
+    assert r["check"] == 0
+
+
+def test_switches_off_by_default():
+    r = _probe_switches({"MODELSHARP_HIP": "1", "MS_HIP_FORCE_FAIL": "0"})
+    assert r["create"] not in (native.MS_HIP_ERR_DISABLED, native.MS_HIP_ERR_FORCED)
+
+
+def test_forced_failure_settable_at_run_time():
+    lib = native.load()
+    h = ctypes.c_void_p()
+    b = (ctypes.c_uint8 * 16)()
+    s = (ctypes.c_float * 1)()
+    try:
+        assert lib.ms_hip_debug_force_failure(1) == 0
+        assert lib.ms_hip_nbits_weights_create(b, 16, s, 1, None, 0, 1, 32, 4, 32, ctypes.byref(h)) == \
+            native.MS_HIP_ERR_FORCED
+        assert not h.value
+    finally:
+        lib.ms_hip_debug_force_failure(0)
+    st = lib.ms_hip_nbits_weights_create(b, 16, s, 1, None, 0, 1, 32, 4, 32, ctypes.byref(h))
+    assert st != native.MS_HIP_ERR_FORCED
+    if st == 0:
+        lib.ms_hip_nbits_weights_destroy(h)
+
+
+def test_kill_switch_leaves_registry_alone(monkeypatch):
+    class Managed:
+        op_type = "MatMulNBits"
+
+        def execute(self, node, ctx):
+            pass
+
+    m = Managed()
+    monkeypatch.setenv("MODELSHARP_HIP", "off")
+    r = register_kernels(KernelRegistry().register(m))
+    assert r.try_get("MatMulNBits") == (True, m)
+    monkeypatch.setenv("MODELSHARP_HIP", "1")
+    assert isinstance(register_kernels(r).try_get("MatMulNBits")[1], HipMatMulNBitsKernel)
