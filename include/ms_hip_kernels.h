@@ -181,6 +181,26 @@ int ms_hip_qgemm_nbits(const float* a, const uint8_t* bq, const float* scales,
                        const uint8_t* zero_points, float* y,
                        int M, int N, int K, int bits, int block_size);
 
+/* ---- W4A8: the opt-in approximate product (MODELSHARP_W4A8) ------------------
+ * Replace ms_qgemm_w4a8 (native/ms_kernels.h:47-53, native/src/qgemm_w4a8.cpp), the
+ * kernel NativeQuant.TryMatMulNBits runs when W4A8Enabled (NativeQuant.cs:78-115):
+ * activations quantized to int8 per (row, K-block), s_a = max|a| / 127, codes
+ * lrint(a / s_a) clamped to [-127, 127]; weight codes code - zp clamped to [-127, 127];
+ * int32 block dots; y = sum over blocks, in block order, of (s_a * s_w) * (float)dot.
+ * Bit for bit the reference's result (built without floating-point contraction).
+ * bits 4 or 8, packed or default zero points (a handle with float zero points returns
+ * MS_HIP_ERR_UNSUPPORTED, as the native seam declines them, NativeQuant.cs:87-89).
+ * The workspace (M*ceil32(nb*bs) + 4*M*nb + 4*nb*ceil4(M) bytes, each 256-aligned)
+ * is the handle's; it cannot grow under stream capture (MS_HIP_ERR_UNSUPPORTED). */
+int ms_hip_nbits_gemm_dev_w4a8(void* handle, const float* dA, float* dY, int M, void* stream);
+int ms_hip_nbits_gemm_w4a8(void* handle, const float* a_host, float* y_host, int M);
+int ms_hip_qgemm_w4a8(const float* a, const uint8_t* bq, const float* scales,
+                      const uint8_t* zero_points, float* y,
+                      int M, int N, int K, int bits, int block_size);
+/* Which W4A8 kernel a call with M rows takes: 9 gemv_w4a8, 10 mfma_w4a8,
+ * 11 w4a8_generic; and its grid. */
+int ms_hip_nbits_launch_info_w4a8(void* handle, int M, int* kernel_id, int* grid);
+
 /* ---- dequantized weights ---------------------------------------------------
  * W[N,K] fp32 as the device stores it, W[n,k] = ((float)q - zp) * scale
  * (MatMulNBitsSimd.cs:40-111); for the bit-exact dequant check. */

@@ -43,6 +43,7 @@
 #include "gemv_w4_panel.h"
 #include "generic_nbits.h"
 #include "mfma_general.h"
+#include "w4a8.h"
 #include "mfma_w4.h"
 #include "mfma_w4_pipe.h"
 #include "mfma_w4_rb.h"
@@ -1181,6 +1182,106 @@ int enqueue_gemm(Weights& w, const float* dA, float* dY, int M, hipStream_t stre
     return launch_kernel(w, kn, k, ws, dA, dY, M, stream);
 }
 
+// ---- W4A8 (the opt-in approximate product) --------------------------------------------------
+// Workspace of one call: activation codes [M][padK], their scales [M][nb] and the
+// transposed scales [nb][Mp], each 256-byte aligned.
+struct W4a8Layout {
+    int padK = 0, Mp = 0;
+    size_t sa_off = 0, sat_off = 0, total = 0;
+};
+
+W4a8Layout w4a8_layout(const Weights& w, int M)
+{
+    W4a8Layout L;
+    L.padK = ((w.nb * w.bs + 31) / 32) * 32;
+    L.Mp = ((M + 3) / 4) * 4;
+    L.sa_off = align256((size_t)M * L.padK);
+    L.sat_off = L.sa_off + align256((size_t)M * w.nb * sizeof(float));
+    L.total = L.sat_off + align256((size_t)w.nb * L.Mp * sizeof(float));
+    return L;
+}
+
+enum W4a8KernelId { kW8Gemv = 9, kW8Mfma = 10, kW8Generic = 11 };
+
+W4a8KernelId w4a8_kernel(const Weights& w, int M)
+{
+    if (w.bits == 4 && w.bs % 32 == 0) return M <= 16 ? kW8Gemv : kW8Mfma;
+    return kW8Generic;
+}
+
+int w4a8_grid(const Weights& w, int M, W4a8KernelId k)
+{
+    if (k == kW8Gemv) return (w.N + kW8RowsPerWg - 1) / kW8RowsPerWg;
+    if (k == kW8Mfma) {
+        const int tiles = ((M + kW8BM - 1) / kW8BM) * ((w.N + kW8BN - 1) / kW8BN);
+        return ((tiles + kXcds - 1) / kXcds) * kXcds;
+    }
+    return (int)(((int64_t)M * w.N + 255) / 256);
+}
+
+typedef void (*W8GemvFn)(RawLayout, W4a8Args, float*);
+template <size_t... I>
+constexpr std::array<W8GemvFn, sizeof...(I)> w8_gemv_table(std::index_sequence<I...>)
+{
+    return {gemv_w4a8_kernel<(int)I + 1>...};
+}
+constexpr auto kW8GemvTable = w8_gemv_table(std::make_index_sequence<16>{});
+
+int launch_w4a8(const Weights& w, const Ws& ws, const float* dA, float* dY, int M, hipStream_t stream)
+{
+    const W4a8Layout Lw = w4a8_layout(w, M);
+    int8_t* aq = reinterpret_cast<int8_t*>(ws.data);
+    float* sa = reinterpret_cast<float*>(ws.data + Lw.sa_off);
+    float* sat = reinterpret_cast<float*>(ws.data + Lw.sat_off);
+    const int64_t threads = (int64_t)Lw.Mp * w.nb * 8;
+    hipLaunchKernelGGL(w4a8_quantize_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, dA, aq,
+                       sa, sat, M, Lw.Mp, w.K, w.bs, w.nb, Lw.padK);
+    MS_HIP_CHECK(hipGetLastError());
+    W4a8Args A;
+    A.aq = aq;
+    A.sa = sa;
+    A.sat = sat;
+    A.M = M;
+    A.Mp = Lw.Mp;
+    A.padK = Lw.padK;
+    const RawLayout L = raw_layout(w);
+    const W4a8KernelId k = w4a8_kernel(w, M);
+    const int grid = w4a8_grid(w, M, k);
+    if (k == kW8Gemv) {
+        hipLaunchKernelGGL(kW8GemvTable[M - 1], dim3(grid), dim3(256), 0, stream, L, A, dY);
+    } else if (k == kW8Mfma) {
+        W4a8MfmaParams p;
+        p.L = L;
+        p.A = A;
+        p.y = dY;
+        p.tiles_m = (M + kW8BM - 1) / kW8BM;
+        p.tiles_n = (w.N + kW8BN - 1) / kW8BN;
+        hipLaunchKernelGGL(mfma_w4a8_kernel, dim3(grid), dim3(256), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL(w4a8_generic_kernel, dim3(grid), dim3(256), 0, stream, L, A, dY);
+    }
+    MS_HIP_CHECK(hipGetLastError());
+    return MS_HIP_OK;
+}
+
+int enqueue_w4a8(Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
+{
+    if (w.zp_float)
+        return fail(MS_HIP_ERR_UNSUPPORTED,
+                    "[ms_hip] W4A8 takes packed or default zero points, as the native ms_qgemm_w4a8 does "
+                    "(NativeQuant.cs:78-101); this handle has float zero points");
+    int st = check_call(dA, dY, M);
+    if (st || M == 0) return st;
+    Ws ws;
+    const int r = ensure_ws(w, w4a8_layout(w, M).total, 0, stream, &ws);
+    if (r < 0) return fail(MS_HIP_ERR_HIP, "[ms_hip] workspace allocation failed: %s", hipGetErrorString(hipGetLastError()));
+    if (r == 0)
+        return fail(MS_HIP_ERR_UNSUPPORTED,
+                    "[ms_hip] W4A8 needs the handle's workspace, which cannot grow under stream capture: "
+                    "make one call of this size outside the capture first");
+    return launch_w4a8(w, ws, dA, dY, M, stream);
+}
+
 int check_impl(int N, int K, int bits, int bs, int64_t b_len, int64_t scales_len, int zp_kind, int64_t zp_len,
                int64_t a_last_dim)
 {
@@ -1602,7 +1703,12 @@ int ms_hip_nbits_batch_launch_info(void* const* handles, const float* const* dA,
     return MS_HIP_OK;
 }
 
-int ms_hip_nbits_gemm(void* handle, const float* a_host, float* y_host, int M)
+}  // extern "C"
+
+namespace {
+
+// The synchronous host-pointer call (exact or W4A8): pinned staging, one stream, one sync.
+int host_gemm(void* handle, const float* a_host, float* y_host, int M, bool w4a8)
 {
     if (int st = gate()) return st;
     Weights* w = from_handle(handle);
@@ -1638,7 +1744,7 @@ int ms_hip_nbits_gemm(void* handle, const float* a_host, float* y_host, int M)
     std::memcpy(w->h_stage, a_host, a_bytes);
     MS_HIP_CHECK(hipMemcpyAsync(dA, w->h_stage, a_bytes, hipMemcpyHostToDevice, w->stream));
     int st = take_device_error(*w, w->stream);
-    if (!st) st = enqueue_gemm(*w, dA, dY, M, w->stream);
+    if (!st) st = w4a8 ? enqueue_w4a8(*w, dA, dY, M, w->stream) : enqueue_gemm(*w, dA, dY, M, w->stream);
     if (st) {
         (void)hipStreamSynchronize(w->stream);
         return st;
@@ -1651,6 +1757,63 @@ int ms_hip_nbits_gemm(void* handle, const float* a_host, float* y_host, int M)
     }
     std::memcpy(y_host, hY, y_bytes);
     return MS_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ms_hip_nbits_gemm(void* handle, const float* a_host, float* y_host, int M)
+{
+    return host_gemm(handle, a_host, y_host, M, false);
+}
+
+int ms_hip_nbits_gemm_w4a8(void* handle, const float* a_host, float* y_host, int M)
+{
+    return host_gemm(handle, a_host, y_host, M, true);
+}
+
+int ms_hip_nbits_gemm_dev_w4a8(void* handle, const float* dA, float* dY, int M, void* stream)
+{
+    if (int st = gate()) return st;
+    Weights* w = from_handle(handle);
+    if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    int st = take_device_error(*w, s);
+    if (st) return st;
+    return enqueue_w4a8(*w, dA, dY, M, s);
+}
+
+int ms_hip_nbits_launch_info_w4a8(void* handle, int M, int* kernel_id, int* grid)
+{
+    Weights* w = from_handle(handle);
+    if (!w) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
+    if (M <= 0) return fail(MS_HIP_ERR_INVALID, "[ms_hip] M must be positive; got %d", M);
+    if (w->zp_float) return fail(MS_HIP_ERR_UNSUPPORTED, "[ms_hip] W4A8 takes packed or default zero points");
+    const W4a8KernelId k = w4a8_kernel(*w, M);
+    if (kernel_id) *kernel_id = (int)k;
+    if (grid) *grid = w4a8_grid(*w, M, k);
+    return MS_HIP_OK;
+}
+
+int ms_hip_qgemm_w4a8(const float* a, const uint8_t* bq, const float* scales, const uint8_t* zero_points, float* y,
+                      int M, int N, int K, int bits, int block_size)
+{
+    if (int st = gate()) return st;
+    if (N <= 0 || K <= 0 || (bits != 4 && bits != 8) || block_size <= 0)
+        return check_impl(N, K, bits, block_size, 0, 0, 0, 0, -1);
+    const int64_t nb = (K + block_size - 1) / block_size;
+    const int64_t blob = (block_size * bits + 7) / 8;
+    const int64_t zrb = (nb * bits + 7) / 8;
+    void* h = nullptr;
+    int st = ms_hip_nbits_weights_create(bq, (int64_t)N * nb * blob, scales, (int64_t)N * nb, zero_points,
+                                         (int64_t)N * zrb, N, K, bits, block_size, &h);
+    if (st) return st;
+    st = ms_hip_nbits_gemm_w4a8(h, a, y, M);
+    const std::string err = g_last_error;
+    ms_hip_nbits_weights_destroy(h);
+    if (st) g_last_error = err;
+    return st;
 }
 
 int ms_hip_qgemm_nbits(const float* a, const uint8_t* bq, const float* scales, const uint8_t* zero_points,

@@ -35,12 +35,24 @@ def _raw_float(t) -> np.ndarray:
     return x if x.dtype in (np.float32, np.float16) else x.astype(np.float32)
 
 
+def w4a8_flag() -> bool:
+    """MODELSHARP_W4A8, read as MatMulNBitsKernel.ReadW4A8Flag reads it
+    (MatMulNBitsKernel.cs:67-75)."""
+    return os.environ.get("MODELSHARP_W4A8", "") in ("1", "true", "TRUE", "True", "on", "ON", "yes", "YES")
+
+
 class HipMatMulNBitsKernel(IKernel):
     op_type = "MatMulNBits"
 
-    def __init__(self):
+    def __init__(self, w4a8: bool | None = None):
+        """w4a8: the opt-in approximate product (ms_hip_nbits_gemm_dev_w4a8), default
+        from MODELSHARP_W4A8 at construction, as the reference reads it once per process.
+        It covers packed and default zero points, as the native W4A8 kernel the
+        reference routes them to does (MatMulNBitsKernel.cs:172-186, NativeQuant.cs:78-115);
+        nodes with float zero points keep the exact product."""
         self._lock = threading.Lock()
         self._handles: dict[tuple, tuple] = {}
+        self.w4a8 = w4a8_flag() if w4a8 is None else bool(w4a8)
 
     # ---- validation: MatMulNBitsKernel.cs:79-161 ----------------------------------------
     @staticmethod
@@ -137,17 +149,21 @@ class HipMatMulNBitsKernel(IKernel):
         w = self._weights(node, b, scales, zp, N, K, bits, block_size)
         lead = tuple(a.shape[:-1])
         M = int(np.prod(lead)) if lead else 1
+        w4a8 = self.w4a8 and (zp is None or element_type(zp) != "Float32")
         if isinstance(a, np.ndarray):
-            y = w.gemm(a.reshape(M, K).astype(np.float32, copy=False)).reshape(lead + (N,))
+            a2 = a.reshape(M, K).astype(np.float32, copy=False)
+            y = (w.gemm_w4a8(a2) if w4a8 else w.gemm(a2)).reshape(lead + (N,))
         else:
             import torch
             a2 = a.reshape(M, K)
-            if a2.dtype not in (torch.float32, torch.float16):
+            if a2.dtype not in (torch.float32, torch.float16) or (w4a8 and a2.dtype != torch.float32):
                 a2 = a2.float()
             a2 = a2.contiguous()
             y = torch.empty(lead + (N,), dtype=torch.float32, device=a.device)
             stream = torch.cuda.current_stream(a.device).cuda_stream
-            if a2.dtype == torch.float16:
+            if w4a8:
+                w.gemm_dev_w4a8(a2.data_ptr(), y.data_ptr(), M, stream)
+            elif a2.dtype == torch.float16:
                 w.gemm_dev_f16(a2.data_ptr(), y.data_ptr(), M, stream)
             else:
                 w.gemm_dev(a2.data_ptr(), y.data_ptr(), M, stream)

@@ -20,7 +20,7 @@ _PKG = pathlib.Path(__file__).resolve().parent
 LIB_NAME = "libms_hip_nbits.so"
 # Kernel ids of ms_hip_nbits_launch_info.
 KERNEL_NAMES = ("generic", "gemv_w4", "mfma_w4", "gemv_w4_panel", "mfma_w4_pipe", "skinny_w4", "mfma_w4_rb",
-                "gemv_general", "mfma_general")
+                "gemv_general", "mfma_general", "gemv_w4a8", "mfma_w4a8", "w4a8_generic")
 HEADER = _PKG.parent / "include" / "ms_hip_kernels.h"
 
 MS_HIP_OK = 0
@@ -61,6 +61,10 @@ _PROTOTYPES = {
     "ms_hip_nbits_gemm": (_c_int, [_vp, _vp, _vp, _c_int]),
     "ms_hip_nbits_gemm_dev": (_c_int, [_vp, _vp, _vp, _c_int, _vp]),
     "ms_hip_nbits_gemm_dev_noalloc": (_c_int, [_vp, _vp, _vp, _c_int, _vp]),
+    "ms_hip_nbits_gemm_dev_w4a8": (_c_int, [_vp, _vp, _vp, _c_int, _vp]),
+    "ms_hip_nbits_gemm_w4a8": (_c_int, [_vp, _vp, _vp, _c_int]),
+    "ms_hip_qgemm_w4a8": (_c_int, [_vp, _vp, _vp, _vp, _vp] + [_c_int] * 5),
+    "ms_hip_nbits_launch_info_w4a8": (_c_int, [_vp, _c_int, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int)]),
     "ms_hip_debug_force_failure": (_c_int, [_c_int]),
     "ms_hip_nbits_gemm_dev_f16": (_c_int, [_vp, _vp, _vp, _c_int, _vp]),
     "ms_hip_nbits_device_error": (_c_int, [_vp]),
@@ -211,6 +215,22 @@ class NBitsWeights:
     def gemm_dev(self, dA: int, dY: int, M: int, stream: int | None = None) -> None:
         check(load().ms_hip_nbits_gemm_dev(self.handle, _vp(dA), _vp(dY), int(M), _vp(stream or 0)))
 
+    def gemm_w4a8(self, a: np.ndarray) -> np.ndarray:
+        """Host-pointer W4A8 call (the approximate opt-in product of ms_qgemm_w4a8)."""
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        M = a.size // self.K
+        y = np.empty((M, self.N), dtype=np.float32)
+        check(load().ms_hip_nbits_gemm_w4a8(self.handle, _ptr(a), _ptr(y), M))
+        return y
+
+    def gemm_dev_w4a8(self, dA: int, dY: int, M: int, stream: int | None = None) -> None:
+        check(load().ms_hip_nbits_gemm_dev_w4a8(self.handle, _vp(dA), _vp(dY), int(M), _vp(stream or 0)))
+
+    def launch_info_w4a8(self, M: int) -> dict:
+        k, gr = ctypes.c_int(), ctypes.c_int()
+        check(load().ms_hip_nbits_launch_info_w4a8(self.handle, int(M), ctypes.byref(k), ctypes.byref(gr)))
+        return {"kernel": KERNEL_NAMES[k.value], "grid": gr.value}
+
     def dequant(self) -> np.ndarray:
         w = np.empty((self.N, self.K), dtype=np.float32)
         check(load().ms_hip_nbits_dequant(self.handle, _ptr(w)))
@@ -297,4 +317,15 @@ def qgemm_nbits(a, b, scales, zero_points, M, N, K, bits, block_size) -> np.ndar
     scales = np.ascontiguousarray(scales, dtype=np.float32)
     zp = None if zero_points is None else np.ascontiguousarray(zero_points, dtype=np.uint8)
     check(load().ms_hip_qgemm_nbits(_ptr(a), _ptr(b), _ptr(scales), _ptr(zp), _ptr(y), M, N, K, bits, block_size))
+    return y
+
+
+def qgemm_w4a8(a, b, scales, zero_points, M, N, K, bits, block_size) -> np.ndarray:
+    """One-shot W4A8 call with ms_qgemm_w4a8's argument meaning."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    y = np.empty((M, N), dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    scales = np.ascontiguousarray(scales, dtype=np.float32)
+    zp = None if zero_points is None else np.ascontiguousarray(zero_points, dtype=np.uint8)
+    check(load().ms_hip_qgemm_w4a8(_ptr(a), _ptr(b), _ptr(scales), _ptr(zp), _ptr(y), M, N, K, bits, block_size))
     return y

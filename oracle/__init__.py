@@ -3,8 +3,10 @@
 Loaded only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
 leg, as the checker or as the timed CPU baseline; the product never imports
 it. liboracle_nbits.so is the C restatement of the reference's managed kernel
-(ms_nbits_oracle.c, citations there); _ref/libms_ref_qgemm.so, when present, is
-the reference's own native ms_qgemm_nbits compiled from its sources.
+and of its native W4A8 kernel (ms_nbits_oracle.c, citations there);
+_ref/libms_ref_qgemm.so and _ref/libms_ref_w4a8.so, when present, are the
+reference's own native ms_qgemm_nbits and ms_qgemm_w4a8 compiled from its
+sources.
 """
 from __future__ import annotations
 
@@ -18,6 +20,7 @@ HERE = pathlib.Path(__file__).resolve().parent
 _vp = ctypes.c_void_p
 _lib = None
 _ref = None
+_ref_w4a8 = None
 
 
 def _ptr(a):
@@ -42,6 +45,8 @@ def lib() -> ctypes.CDLL:
         L.msor_matmul_nbits.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp] + [ctypes.c_int] * 6
         L.msor_dequant_weights.argtypes = [_vp, _vp, _vp, _vp, _vp] + [ctypes.c_int] * 5
         L.msor_matmul_f64.argtypes = [_vp, _vp, _vp] + [ctypes.c_int] * 4
+        L.msor_w4a8_quantize.argtypes = [_vp, _vp, _vp] + [ctypes.c_int] * 3
+        L.msor_qgemm_w4a8.argtypes = [_vp, _vp, _vp, _vp, _vp] + [ctypes.c_int] * 6
         _lib = L
     return _lib
 
@@ -58,6 +63,20 @@ def ref_lib():
         L.ms_qgemm_nbits.argtypes = [_vp, _vp, _vp, _vp, _vp] + [ctypes.c_int] * 5
         _ref = L
     return _ref
+
+
+def ref_w4a8_lib():
+    """The reference's own ms_qgemm_w4a8 (built from its sources), or None."""
+    global _ref_w4a8
+    if _ref_w4a8 is None:
+        path = HERE / "_ref" / "libms_ref_w4a8.so"
+        if not path.is_file():
+            return None
+        L = ctypes.CDLL(str(path))
+        L.ms_qgemm_w4a8.restype = None
+        L.ms_qgemm_w4a8.argtypes = [_vp, _vp, _vp, _vp, _vp] + [ctypes.c_int] * 5
+        _ref_w4a8 = L
+    return _ref_w4a8
 
 
 def threads() -> int:
@@ -124,4 +143,42 @@ def ref_qgemm_nbits(a, b, scales, zp_packed, M, N, K, bits, block_size):
     scales = np.ascontiguousarray(scales, dtype=np.float32)
     zp_packed = None if zp_packed is None else np.ascontiguousarray(zp_packed, dtype=np.uint8)
     L.ms_qgemm_nbits(_ptr(a), _ptr(b), _ptr(scales), _ptr(zp_packed), _ptr(y), M, N, K, bits, block_size)
+    return y
+
+
+def w4a8_quantize(a, K, block_size):
+    """(aq int8 [M, nb*bs], sa fp32 [M, nb]) of qgemm_w4a8.cpp:257-285."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    M = a.size // K
+    nb = (K + block_size - 1) // block_size
+    aq = np.empty((M, nb * block_size), dtype=np.int8)
+    sa = np.empty((M, nb), dtype=np.float32)
+    lib().msor_w4a8_quantize(_ptr(a), _ptr(aq), _ptr(sa), M, K, block_size)
+    return aq, sa
+
+
+def qgemm_w4a8(a, b, scales, zp_packed, N, K, bits, block_size, nthreads=None):
+    """y[M,N] of the native W4A8 kernel (qgemm_w4a8.cpp)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    M = a.size // K
+    y = np.empty((M, N), dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    scales = np.ascontiguousarray(scales, dtype=np.float32)
+    zp_packed = None if zp_packed is None else np.ascontiguousarray(zp_packed, dtype=np.uint8)
+    lib().msor_qgemm_w4a8(_ptr(a), _ptr(b), _ptr(scales), _ptr(zp_packed), _ptr(y), M, N, K, bits, block_size,
+                          nthreads or threads())
+    return y
+
+
+def ref_qgemm_w4a8(a, b, scales, zp_packed, M, N, K, bits, block_size):
+    """The reference's native ms_qgemm_w4a8, or None if not built."""
+    L = ref_w4a8_lib()
+    if L is None:
+        return None
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    y = np.empty((M, N), dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    scales = np.ascontiguousarray(scales, dtype=np.float32)
+    zp_packed = None if zp_packed is None else np.ascontiguousarray(zp_packed, dtype=np.uint8)
+    L.ms_qgemm_w4a8(_ptr(a), _ptr(b), _ptr(scales), _ptr(zp_packed), _ptr(y), M, N, K, bits, block_size)
     return y

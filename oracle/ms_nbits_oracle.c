@@ -227,3 +227,92 @@ void msor_matmul_f64(const float* a, const float* w, double* y, int M, int N, in
         }
     }
 }
+
+/* ---- W4A8: the opt-in approximate path (MODELSHARP_W4A8) ---------------------------------
+ * Restates the reference's native ms_qgemm_w4a8 (native/src/qgemm_w4a8.cpp), the kernel
+ * NativeQuant.TryMatMulNBits runs when MODELSHARP_W4A8 is on (NativeQuant.cs:78-115).
+ *
+ * Pinning (tests/test_oracle.py): bit-exact against the reference's own qgemm_w4a8.cpp
+ * built from source (both its VNNI driver and, under MODELSHARP_FORCE_NOAVX512, its
+ * scalar driver); exact on activations that quantize without error (integer rows whose
+ * block max is 127: sa = 1, aq = a) against the integer dot; the reference test's
+ * accuracy bar (rel-L2 < 0.03, cosine > 0.999 against the f64 dequantized product,
+ * qgemm_w4a8_test.cpp:49-85) on its case grid; the quantizer against its closed form. */
+
+void msor_w4a8_quantize(const float* a, int8_t* aq, float* sa, int M, int K, int block_size)
+{
+    /* qgemm_w4a8.cpp:257-285: per (row, K-block) symmetric int8, s = max|a| / 127,
+     * q = lrintf(a * (1 / s)) clamped to [-127, 127]; the padding past K stays 0. */
+    const int nb = (K + block_size - 1) / block_size;
+    const int64_t padK = (int64_t)nb * block_size;
+    for (int m = 0; m < M; ++m) {
+        const float* arow = a + (int64_t)m * K;
+        int8_t* qrow = aq + (int64_t)m * padK;
+        for (int bk = 0; bk < nb; ++bk) {
+            const int k0 = bk * block_size;
+            const int k1 = (k0 + block_size < K) ? k0 + block_size : K;
+            float amax = 0.0f;
+            for (int k = k0; k < k1; ++k) {
+                const float v = fabsf(arow[k]);
+                if (v > amax) amax = v;
+            }
+            const float s = amax / 127.0f;
+            sa[(int64_t)m * nb + bk] = s;
+            const float inv = (s > 0.0f) ? (1.0f / s) : 0.0f;
+            for (int k = k0; k < k1; ++k) {
+                int q = (int)lrintf(arow[k] * inv);
+                if (q > 127) q = 127;
+                else if (q < -127) q = -127;
+                qrow[k] = (int8_t)q;
+            }
+            for (int k = k1; k < k0 + block_size; ++k) qrow[k] = 0;
+        }
+    }
+}
+
+void msor_qgemm_w4a8(const float* a, const uint8_t* b, const float* scales, const uint8_t* zp_packed,
+                     float* y, int M, int N, int K, int bits, int block_size, int nthreads)
+{
+    const int nb = (K + block_size - 1) / block_size;
+    const int blob = (block_size * bits + 7) / 8;
+    const int zrb = (nb * bits + 7) / 8;
+    const int64_t row_bytes = (int64_t)nb * blob;
+    const int64_t padK = (int64_t)nb * block_size;
+    if (nthreads < 1) nthreads = 1;
+    int8_t* aq = (int8_t*)malloc((size_t)(M > 0 ? M : 1) * (size_t)padK);
+    float* sa = (float*)malloc(sizeof(float) * (size_t)(M > 0 ? M : 1) * (size_t)nb);
+    msor_w4a8_quantize(a, aq, sa, M, K, block_size);
+#pragma omp parallel num_threads(nthreads)
+    {
+        int* wc = (int*)malloc(sizeof(int) * (size_t)block_size);
+#pragma omp for schedule(static)
+        for (int n = 0; n < N; ++n) {
+            for (int m = 0; m < M; ++m) {
+                float acc = 0.0f;
+                for (int bk = 0; bk < nb; ++bk) {
+                    /* qgemm_w4a8.cpp:640-652: signed codes wc = code - zp, clamped to
+                     * [-127, 127] (only 8-bit codes can reach the clamp) */
+                    const int zp = zp_packed ? msor_unpack_nbit(zp_packed, (int64_t)n * zrb, bk, bits)
+                                             : (1 << (bits - 1));
+                    const int k0 = bk * block_size;
+                    const int len = (block_size < K - k0) ? block_size : K - k0;
+                    const int64_t blob_base = (int64_t)n * row_bytes + (int64_t)bk * blob;
+                    int32_t dot = 0;
+                    for (int i = 0; i < len; ++i) {
+                        int v = msor_unpack_nbit(b, blob_base, i, bits) - zp;
+                        if (v > 127) v = 127;
+                        else if (v < -127) v = -127;
+                        wc[i] = v;
+                        dot += (int32_t)aq[(int64_t)m * padK + k0 + i] * v;
+                    }
+                    /* :676-689: the block's term, sa * s_w * (float)dot, added in block order */
+                    acc += sa[(int64_t)m * nb + bk] * scales[(int64_t)n * nb + bk] * (float)dot;
+                }
+                y[(int64_t)m * N + n] = acc;
+            }
+        }
+        free(wc);
+    }
+    free(aq);
+    free(sa);
+}

@@ -63,6 +63,12 @@ void msor_dequant_weights(const uint8_t* b, const float* scales,
 void msor_matmul_f64(const float* a, const float* w, double* y,
                      int M, int N, int K, int nthreads);
 
+/* W4A8 (native/src/qgemm_w4a8.cpp): per (row, block) int8 activations aq [M][nb*bs]
+ * (zero past K) and their scales sa [M][nb]; the approximate product. */
+void msor_w4a8_quantize(const float* a, int8_t* aq, float* sa, int M, int K, int block_size);
+void msor_qgemm_w4a8(const float* a, const uint8_t* b, const float* scales, const uint8_t* zp_packed,
+                     float* y, int M, int N, int K, int bits, int block_size, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -64,3 +64,14 @@ def kat_arrays(case):
         zp = np.array(case["zp"], np.uint8 if case["zp_dtype"] == "uint8" else np.float32)
     y = np.array(case["y"], np.float32).reshape(case["y_shape"])
     return a, b, s, zp, y
+
+
+@pytest.fixture(scope="session")
+def w4a8_vectors():
+    with np.load(GOLDEN / "ref_w4a8_vectors.npz") as z:
+        data = {k: z[k] for k in z.files}
+    groups: dict[str, dict] = {}
+    for k, v in data.items():
+        g, field = k.split("/")
+        groups.setdefault(g, {})[field] = v
+    return groups

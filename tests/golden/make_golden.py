@@ -15,6 +15,13 @@ ref_qgemm_vectors.npz
     reference returns its dequantized weights W^T exactly (every output is a
     single product 1*w plus zeros).
 
+ref_w4a8_vectors.npz
+    Outputs of the reference's own native ms_qgemm_w4a8 (native/src/qgemm_w4a8.cpp,
+    compiled from source by oracle/Makefile `ref` with -ffp-contract=off) on seeded
+    inputs over a reduced version of its accuracy grid
+    (native/test/qgemm_w4a8_test.cpp:140-166: M in {1, 8}, bits 4 sym/asym and 8
+    sym/asym, block size 32/128, and its three odd shapes).
+
 Run in the container that holds the reference checkout:
     python tests/golden/make_golden.py
 """
@@ -111,13 +118,44 @@ def ref_vectors() -> dict:
     return out
 
 
+W4A8_SHAPES = [(1, 64, 128), (8, 40, 512)]
+W4A8_ODD = [(1, 16, 4000, 4, 128, False), (8, 9, 320, 4, 128, True), (32, 130, 200, 8, 128, False),
+            (5, 65, 128, 4, 32, True), (13, 257, 128, 8, 32, False)]
+
+
+def ref_w4a8_vectors() -> dict:
+    import oracle
+    from modelsharp_amd import workloads
+
+    if oracle.ref_w4a8_lib() is None:
+        raise SystemExit("oracle/_ref/libms_ref_w4a8.so is not built (make -C oracle ref)")
+    cases = [(M, N, K, bits, bs, asym) for (M, N, K) in W4A8_SHAPES for bs in GRID_BS
+             for bits, asym in GRID_MODES] + W4A8_ODD
+    out = {}
+    seed = 500
+    for (M, N, K, bits, bs, asym) in cases:
+        seed += 1
+        op = workloads.Op("w4a8", K, N, bs, asym, 0.005, 0.05, bits)
+        b, s, z = workloads.make_weights(op, seed)
+        a = workloads.make_activations(M, K, seed + 1000, kind="rmsnorm" if seed % 2 else "normal")
+        y = oracle.ref_qgemm_w4a8(a, b, s, z, M, N, K, bits, bs)
+        key = f"w4a8_M{M}_N{N}_K{K}_bits{bits}_bs{bs}_{'asym' if asym else 'sym'}"
+        out.update({f"{key}/a": a, f"{key}/b": b, f"{key}/scales": s, f"{key}/y": y,
+                    f"{key}/dims": np.array([M, N, K, bits, bs], np.int32)})
+        if z is not None:
+            out[f"{key}/zp"] = z
+    return out
+
+
 def main() -> None:
     (HERE / "kat_vectors.json").write_text(json.dumps(
         {"source": "tests/ModelSharp.Tests/MatMulNBitsTests.cs:57-267", "tolerance": 1e-4,
          "cases": kat_cases()}, indent=1))
     vec = ref_vectors()
     np.savez_compressed(HERE / "ref_qgemm_vectors.npz", **vec)
-    print(f"wrote {len(kat_cases())} KATs and {len(vec)} reference arrays")
+    w4a8 = ref_w4a8_vectors()
+    np.savez_compressed(HERE / "ref_w4a8_vectors.npz", **w4a8)
+    print(f"wrote {len(kat_cases())} KATs, {len(vec)} reference arrays and {len(w4a8)} W4A8 arrays")
 
 
 if __name__ == "__main__":

@@ -1,0 +1,166 @@
+"""Device parity of the opt-in W4A8 product (MODELSHARP_W4A8) against the oracle's
+restatement of the reference's native ms_qgemm_w4a8 (native/src/qgemm_w4a8.cpp), which
+is itself pinned bit for bit to the reference built from source.
+
+Bar: bit-exact. The quantizer, the integer block dots and the order and rounding of the
+fp32 block terms are the reference's, so every output equals the oracle's. The accuracy
+bar of the reference's own test (rel-L2 < 0.03, cosine > 0.999 against the f64 product,
+qgemm_w4a8_test.cpp:49-85) is checked as well, at the 7B shapes.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from modelsharp_amd import native, workloads
+from modelsharp_amd.workloads import Op
+
+pytestmark = pytest.mark.gpu
+
+
+def log(msg):
+    print(msg, flush=True)
+
+
+def test_w4a8_golden_through_the_device(gpu, w4a8_vectors):
+    for key, g in sorted(w4a8_vectors.items()):
+        M, N, K, bits, bs = (int(x) for x in g["dims"])
+        w = native.NBitsWeights(g["b"], g["scales"], g.get("zp"), N, K, bits, bs)
+        log(f"golden {key} {w.launch_info_w4a8(M)}")
+        assert np.array_equal(w.gemm_w4a8(g["a"]), g["y"]), key
+        w.close()
+        y1 = native.qgemm_w4a8(g["a"], g["b"], g["scales"], g.get("zp"), M, N, K, bits, bs)
+        assert np.array_equal(y1, g["y"]), key
+
+
+FAST = [Op("b4_bs32_zp", 1024, 200, 32, True), Op("b4_bs64_sym", 768, 130, 64, False),
+        Op("b4_bs128_zp", 1152, 70, 128, True), Op("b4_nb17", 544, 64, 32, True),
+        Op("b4_ktail", 200, 18, 32, True)]   # K % 32 != 0: codes past K meet zero activations
+
+
+@pytest.mark.parametrize("op", FAST, ids=lambda o: o.name)
+@pytest.mark.parametrize("M", [1, 2, 5, 16, 17, 64, 130, 300])
+def test_w4a8_fast_kernels_bit_exact(gpu, op, M):
+    b, s, z = workloads.make_weights(op, seed=op.K + M)
+    a = workloads.make_activations(M, op.K, seed=M, kind="rmsnorm")
+    w = native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
+    info = w.launch_info_w4a8(M)
+    log(f"w4a8 {op.name} M={M} {info}")
+    assert info["kernel"] == ("gemv_w4a8" if M <= 16 else "mfma_w4a8")
+    y = w.gemm_w4a8(a)
+    ref = oracle.qgemm_w4a8(a, b, s, z, op.N, op.K, op.bits, op.block_size)
+    assert np.array_equal(y, ref), f"max diff {np.max(np.abs(y - ref))}"
+    w.close()
+
+
+GENERIC = [Op("w8a8_zp", 256, 40, 32, True, bits=8), Op("w8a8_sym_bs128", 640, 24, 128, False, bits=8),
+           Op("b4_bs16", 160, 30, 16, True), Op("b4_bs48", 480, 21, 48, True), Op("b4_bs20", 100, 9, 20, True)]
+
+
+@pytest.mark.parametrize("op", GENERIC, ids=lambda o: o.name)
+@pytest.mark.parametrize("M", [1, 7, 33])
+def test_w4a8_generic_bit_exact(gpu, op, M):
+    b, s, z = workloads.make_weights(op, seed=op.N + M)
+    a = workloads.make_activations(M, op.K, seed=2 * M)
+    w = native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
+    assert w.launch_info_w4a8(M)["kernel"] == "w4a8_generic"
+    log(f"w4a8 generic {op.name} M={M}")
+    assert np.array_equal(w.gemm_w4a8(a), oracle.qgemm_w4a8(a, b, s, z, op.N, op.K, op.bits, op.block_size))
+    w.close()
+
+
+def _rows(b, s, z, cols):
+    return b[cols], s.reshape(b.shape[0], -1)[cols].reshape(-1), None if z is None else z[cols]
+
+
+@pytest.mark.parametrize("op", workloads.LLAMA7B_PREFILL_OPS, ids=lambda o: f"K{o.K}_N{o.N}")
+@pytest.mark.parametrize("M", [1, 16, 128, 2048])
+def test_w4a8_7b_shapes(gpu, op, M):
+    """The 7B MLP projections: bit-exact on sampled output columns, and within the
+    reference test's accuracy bar of the exact product."""
+    b, s, z = workloads.make_weights(op, seed=op.N)
+    a = workloads.make_activations(M, op.K, seed=M + 5, kind="rmsnorm")
+    w = native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
+    log(f"w4a8 7B K={op.K} N={op.N} M={M} {w.launch_info_w4a8(M)}")
+    y = w.gemm_w4a8(a)
+    assert np.isfinite(y).all()
+    cols = np.random.default_rng(M).choice(op.N, size=48, replace=False)
+    cols.sort()
+    bc, sc, zc = _rows(b, s, z, cols)
+    ref = oracle.qgemm_w4a8(a, bc, sc, zc, cols.size, op.K, 4, op.block_size)
+    assert np.array_equal(y[:, cols], ref)
+    exact = oracle.matmul_f64(a, oracle.dequant_weights(bc, sc, zc, cols.size, op.K, 4, op.block_size))
+    d = y[:, cols].astype(np.float64)
+    rel = np.linalg.norm(d - exact) / np.linalg.norm(exact)
+    cos = float(np.sum(d * exact) / (np.linalg.norm(d) * np.linalg.norm(exact)))
+    log(f"  rel-L2 {rel:.4e} cosine {cos:.6f}")
+    assert rel < 0.03 and cos > 0.999
+    assert np.array_equal(w.gemm_w4a8(a), y)   # deterministic
+    w.close()
+
+
+def test_w4a8_device_pointers_and_capture(gpu):
+    """Device-pointer entry on a side stream, then captured into a graph (after a call
+    of the same size sized the workspace) and replayed: every replay equals the eager
+    result."""
+    import torch
+    op = Op("cap", 1024, 192, 32, True)
+    b, s, z = workloads.make_weights(op, seed=3)
+    w = native.NBitsWeights(b, s, z, op.N, op.K, 4, 32)
+    for M in (4, 40):
+        a = torch.from_numpy(workloads.make_activations(M, op.K, seed=M)).cuda()
+        y = torch.empty((M, op.N), device="cuda")
+        w.gemm_dev_w4a8(a.data_ptr(), y.data_ptr(), M)
+        torch.cuda.synchronize()
+        ref = oracle.qgemm_w4a8(a.cpu().numpy(), b, s, z, op.N, op.K, 4, 32)
+        assert np.array_equal(y.cpu().numpy(), ref)
+        g = torch.cuda.CUDAGraph()
+        y2 = torch.zeros_like(y)
+        with torch.cuda.graph(g):
+            w.gemm_dev_w4a8(a.data_ptr(), y2.data_ptr(), M, torch.cuda.current_stream().cuda_stream)
+        for _ in range(3):
+            y2.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y2, y)
+        del g
+    w.close()
+
+
+def test_w4a8_declines_float_zero_points(gpu):
+    op = Op("fzp", 256, 16, 32, True)
+    b, s, _ = workloads.make_weights(op, seed=1)
+    zpf = np.full(op.N * op.nb, 7.5, np.float32)
+    w = native.NBitsWeights(b, s, zpf, op.N, op.K, 4, 32)
+    with pytest.raises(native.HipError) as e:
+        w.gemm_w4a8(np.ones((1, op.K), np.float32))
+    assert e.value.status == native.MS_HIP_ERR_UNSUPPORTED
+    w.close()
+
+
+def test_operator_w4a8_switch(gpu):
+    """HipMatMulNBitsKernel(w4a8=True) (MODELSHARP_W4A8) runs the W4A8 product; off, the
+    exact one."""
+    import torch
+    from modelsharp_amd.graph import GraphContext, GraphNode
+    from modelsharp_amd.hip_kernel import HipMatMulNBitsKernel
+    op = Op("sw", 512, 96, 32, True)
+    b, s, z = workloads.make_weights(op, seed=4)
+    a = workloads.make_activations(3, op.K, seed=5)
+    node = GraphNode("MatMulNBits", "n", ["A", "B", "scales", "zp"], ["Y"],
+                     {"N": op.N, "K": op.K, "bits": 4, "block_size": 32})
+    for flag, ref in ((True, oracle.qgemm_w4a8(a, b, s, z, op.N, op.K, 4, 32)),
+                      (False, None)):
+        k = HipMatMulNBitsKernel(w4a8=flag)
+        for A in (a, torch.from_numpy(a).cuda()):
+            ctx = GraphContext({"A": A, "B": b, "scales": s, "zp": z})
+            k.execute(node, ctx)
+            y = ctx.get_tensor("Y")
+            y = y if isinstance(y, np.ndarray) else y.cpu().numpy()
+            if flag:
+                assert np.array_equal(y, ref)
+            else:
+                exact = oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, 32)
+                assert np.max(np.abs(y - exact)) <= 1e-5 * np.max(np.abs(exact))
+        k.close()

@@ -166,3 +166,110 @@ def test_threading_does_not_change_results():
     y1 = oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, 32, nthreads=1)
     y8 = oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, 32, nthreads=8)
     assert np.array_equal(y1, y8)
+
+
+# ---- W4A8 (native/src/qgemm_w4a8.cpp) -----------------------------------------------------------
+def test_w4a8_matches_reference_golden(w4a8_vectors):
+    """Bit-exact against the reference's own ms_qgemm_w4a8 (built from source) on its
+    reduced accuracy grid."""
+    assert len(w4a8_vectors) == 21
+    for key, g in sorted(w4a8_vectors.items()):
+        M, N, K, bits, bs = (int(x) for x in g["dims"])
+        y = oracle.qgemm_w4a8(g["a"], g["b"], g["scales"], g.get("zp"), N, K, bits, bs)
+        assert np.array_equal(y, g["y"]), key
+
+
+def test_w4a8_live_reference_both_drivers():
+    """Where the reference checkout is built: its VNNI driver and its scalar driver
+    (MODELSHARP_FORCE_NOAVX512, read once per process, hence the subprocess) both equal
+    the restatement bit for bit."""
+    import subprocess
+    import sys
+    if oracle.ref_w4a8_lib() is None:
+        pytest.skip("oracle/_ref/libms_ref_w4a8.so not built (no reference checkout)")
+    cases = [(3, 70, 384, 4, 32, True), (17, 33, 1000, 4, 128, False), (4, 20, 256, 8, 64, True),
+             (2, 12, 96, 8, 32, False)]
+    for (M, N, K, bits, bs, asym) in cases:
+        op = workloads.Op("w", K, N, bs, asym, 0.005, 0.05, bits)
+        b, s, z = workloads.make_weights(op, K + N)
+        a = workloads.make_activations(M, K, M + K, kind="rmsnorm")
+        y = oracle.qgemm_w4a8(a, b, s, z, N, K, bits, bs)
+        assert np.array_equal(y, oracle.ref_qgemm_w4a8(a, b, s, z, M, N, K, bits, bs)), (M, N, K, bits, bs)
+    script = (
+        "import sys, numpy as np; sys.path.insert(0, sys.argv[1]); import oracle; "
+        "from modelsharp_amd import workloads as W; op = W.Op('w', 1000, 33, 128, True, 0.005, 0.05, 4); "
+        "b, s, z = W.make_weights(op, 9); a = W.make_activations(5, 1000, 3); "
+        "print(int(np.array_equal(oracle.ref_qgemm_w4a8(a, b, s, z, 5, 33, 1000, 4, 128), "
+        "oracle.qgemm_w4a8(a, b, s, z, 33, 1000, 4, 128))))")
+    import os
+    from conftest import ROOT
+    out = subprocess.run([sys.executable, "-c", script, str(ROOT)], capture_output=True, text=True, timeout=120,
+                         env={**os.environ, "MODELSHARP_FORCE_NOAVX512": "1"})
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.strip().splitlines()[-1] == "1"
+
+
+def test_w4a8_quantizer_closed_form():
+    """Per (row, block): s = max|a|/127; the largest element maps to +-127; every code is
+    within half a step of a/s; an all-zero block gives s = 0 and zero codes; the padding
+    past K is zero."""
+    rng = np.random.default_rng(1)
+    K, bs = 200, 64
+    a = rng.standard_normal((3, K)).astype(np.float32) * np.float32(3.0)
+    a[1, 64:128] = 0.0
+    aq, sa = oracle.w4a8_quantize(a, K, bs)
+    assert aq.shape == (3, 256) and sa.shape == (3, 4)
+    for m in range(3):
+        for bk in range(4):
+            blk = a[m, bk * bs:min(K, (bk + 1) * bs)].astype(np.float64)
+            q = aq[m, bk * bs:bk * bs + blk.size].astype(np.float64)
+            amax = np.max(np.abs(blk))
+            assert sa[m, bk] == np.float32(np.float32(amax) / np.float32(127.0))
+            if amax == 0:
+                assert not q.any()
+                continue
+            assert np.max(np.abs(q)) == 127
+            assert np.all(np.abs(q - blk / float(sa[m, bk])) <= 0.5 + 1e-4)
+    assert not aq[:, K:].any()
+
+
+def test_w4a8_exact_when_activations_quantize_exactly():
+    """Integer activations whose every block holds +-127 quantize with s = 1 and no
+    error: the product then equals the exact integer-weight product up to fp32 rounding
+    of the block terms, whatever the zero points (a dropped zero-point term, a sign or
+    an index slip would not)."""
+    for bits, bs, asym in [(4, 32, True), (4, 128, False), (8, 64, True), (8, 32, False)]:
+        M, N, K = 3, 24, 256
+        op = workloads.Op("x", K, N, bs, asym, 0.01, 0.1, bits)
+        b, s, z = workloads.make_weights(op, bits + bs)
+        rng = np.random.default_rng(bs)
+        a = rng.integers(-127, 128, size=(M, K)).astype(np.float32)
+        a[:, ::bs] = 127.0
+        y = oracle.qgemm_w4a8(a, b, s, z, N, K, bits, bs)
+        # wc = clamp(code - zp, +-127): the reference's signed weight codes
+        W = oracle.dequant_weights(b, np.ones_like(s), z, N, K, bits, bs).astype(np.int64)
+        Wc = np.clip(W, -127, 127)
+        sc = np.repeat(s.reshape(N, -1), bs, axis=1)[:, :K].astype(np.float64)
+        exact = a.astype(np.float64) @ (Wc * sc).T
+        bound = 1e-6 * (np.abs(a).astype(np.float64) @ np.abs(Wc * sc).T) + 1e-30
+        assert np.all(np.abs(y - exact) <= bound), (bits, bs, asym)
+
+
+@pytest.mark.parametrize("bits,asym", [(4, False), (4, True), (8, False)])
+@pytest.mark.parametrize("M,N,K,bs", [(1, 64, 128, 32), (8, 512, 4096, 128), (32, 64, 4096, 32)])
+def test_w4a8_accuracy_bar_of_the_reference_test(bits, asym, M, N, K, bs):
+    """qgemm_w4a8_test.cpp:49-85: rel-L2 < 0.03 and cosine > 0.999 against the f64
+    product of the dequantized weights."""
+    op = workloads.Op("acc", K, N, bs, asym, 0.005, 0.05, bits)
+    b, s, z = workloads.make_weights(op, M + N + K)
+    a = workloads.make_activations(M, K, 7)
+    y = oracle.qgemm_w4a8(a, b, s, z, N, K, bits, bs).astype(np.float64)
+    W = oracle.dequant_weights(b, s, z, N, K, bits, bs)
+    if bits == 8:
+        # the W8A8 path clamps code - zp to +-127 (qgemm_w4a8.cpp:650)
+        W = (np.clip(oracle.dequant_weights(b, np.ones_like(s), z, N, K, bits, bs), -127, 127)
+             * np.repeat(s.reshape(N, -1), bs, axis=1)[:, :K])
+    ref = oracle.matmul_f64(a, W.astype(np.float32))
+    rel = np.linalg.norm(y - ref) / np.linalg.norm(ref)
+    cos = float(np.sum(y * ref) / (np.linalg.norm(y) * np.linalg.norm(ref)))
+    assert rel < 0.03 and cos > 0.999, (rel, cos)
