@@ -263,6 +263,61 @@ int ms_hip_nbits_debug_set_counters(void* handle, int value, int next_epoch_tag)
 int ms_hip_nbits_launch_info(void* handle, int M, int* kernel_id, int* lanes_per_row,
                              int* grid, int* block);
 
+/* ---- decoder-layer neighbours of MatMulNBits ---------------------------------
+ * The operators either side of the projections of a Llama-family decoder layer, on
+ * device pointers and a stream, so activations stay in HBM from one MatMulNBits to
+ * the next (no host copies, nothing allocated). fp32, row-major, 4-byte aligned.
+ *
+ * SimplifiedLayerNormalization (Cpu/Kernels/Llm/SimplifiedLayerNormalizationKernel.cs:
+ * 24-64): rows x norm; inv = 1 / sqrt(sum(x^2) / norm + eps), y = (x * inv) * scale;
+ * dInvStd [rows] optional. dY may equal dX. */
+int ms_hip_rmsnorm(const float* dX, const float* dScale, float* dY, float* dInvStd,
+                   int64_t rows, int norm, float eps, void* stream);
+/* SkipSimplifiedLayerNormalization (SkipSimplifiedLayerNormalizationKernel.cs:29-86):
+ * t = (input + skip) + bias, out = (t * inv) * gamma + beta; dBeta, dBias, dSum
+ * (input_skip_bias_sum, output 3) and dInvStd (output 2) optional. dOut and dSum may
+ * equal dInput or dSkip (a residual stream updated in place). */
+int ms_hip_skip_rmsnorm(const float* dInput, const float* dSkip, const float* dGamma,
+                        const float* dBeta, const float* dBias, float* dOut, float* dSum,
+                        float* dInvStd, int64_t rows, int norm, float eps, void* stream);
+/* The MLP gate of Llama-family exports, Sigmoid -> Mul -> Mul fused
+ * (Activations/SigmoidKernel.cs:13-22 and the elementwise Mul):
+ * y = (g * (1 / (1 + exp(-g)))) * u over n elements; dY may equal an input. */
+int ms_hip_silu_mul(const float* dGate, const float* dUp, float* dY, int64_t n, void* stream);
+/* Elementwise Add of equal shapes (the residual stream), y = a + b; and the unfused
+ * Sigmoid (SigmoidKernel.cs:13-22, 1 / (1 + exp(-x))) and Mul of equal shapes. */
+int ms_hip_add(const float* dA, const float* dB, float* dY, int64_t n, void* stream);
+int ms_hip_sigmoid(const float* dX, float* dY, int64_t n, void* stream);
+int ms_hip_mul(const float* dA, const float* dB, float* dY, int64_t n, void* stream);
+
+/* GroupQueryAttention (com.microsoft; Cpu/Kernels/Llm/GroupQueryAttentionKernel.cs).
+ * query [batch, q_seq, num_heads*head_dim] (packed_qkv: [batch, q_seq,
+ * (num_heads + 2*kv_num_heads)*head_dim] with K and V the row tails, dK/dV unused);
+ * key/value [batch, kv_seq, kv_num_heads*head_dim]; past K/V [batch, kv_num_heads,
+ * past_seq, head_dim]; present K/V [batch, kv_num_heads, present_capacity, head_dim],
+ * rows [0, past_seq + kv_seq) written (past_in_present: the past rows are already
+ * there and only the new rows are appended — the cache stays resident); seqlens_k
+ * int32 [seqlens_len] on the device (0: none); cos/sin caches [cos_rows, cos_cols]
+ * (do_rotary); output [batch, q_seq, num_heads*head_dim]. Causal with the reference's
+ * key range min(past + qi, seqlens_k[b]) and local_window_size lower bound; scale 0
+ * means 1/sqrt(head_dim). The softmax keeps a unit's scores in LDS: past + kv_seq up
+ * to about 40K keys (MS_HIP_ERR_UNSUPPORTED beyond). */
+typedef struct ms_hip_gqa_desc {
+    int batch, q_seq, kv_seq;
+    int num_heads, kv_num_heads, head_dim;
+    int packed_qkv;
+    int past_seq, past_in_present, present_capacity;
+    int do_rotary, rotary_interleaved, cos_rows, cos_cols;
+    int local_window_size;
+    float scale;
+    int seqlens_len;
+} ms_hip_gqa_desc;
+int ms_hip_gqa_check(const ms_hip_gqa_desc* desc);
+int ms_hip_gqa(const ms_hip_gqa_desc* desc, const float* dQ, const float* dK, const float* dV,
+               const float* dPastK, const float* dPastV, const int32_t* dSeqlensK,
+               const float* dCos, const float* dSin, float* dOut,
+               float* dPresentK, float* dPresentV, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

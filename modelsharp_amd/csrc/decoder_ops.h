@@ -1,0 +1,121 @@
+// decoder_ops.h — the decoder-layer operators on either side of MatMulNBits, so that
+// activations stay in HBM between projections:
+//
+//   rmsnorm_kernel       SimplifiedLayerNormalization
+//                        (Cpu/Kernels/Llm/SimplifiedLayerNormalizationKernel.cs:24-64):
+//                        inv = 1 / sqrt(sum(x^2) / norm + eps), y = (x * inv) * scale
+//   skip_rmsnorm_kernel  SkipSimplifiedLayerNormalization
+//                        (SkipSimplifiedLayerNormalizationKernel.cs:29-86):
+//                        t = (input + skip) + bias, y = (t * inv) * gamma + beta, with t,
+//                        inv and (optionally) t written out
+//   silu_mul_kernel      the MLP gate of Llama-family exports, Sigmoid -> Mul -> Mul
+//                        (Activations/SigmoidKernel.cs:13-22, the elementwise Mul):
+//                        y = (g * (1 / (1 + exp(-g)))) * u
+//   add_kernel           the elementwise Add of the residual stream
+//   sigmoid_kernel,      the unfused Sigmoid and Mul nodes, y = 1 / (1 + exp(-x)) and
+//   mul_kernel           y = a * b, for graphs the fusion does not match
+//
+// One workgroup per row for the norms (the row's sum of squares is one fixed-order tree
+// over the workgroup's partial sums, so a row's result does not depend on the launch);
+// grid-stride loops for the elementwise kernels. Every operation is rounded on its own
+// (the library is built with -ffp-contract=off); sqrt and the divisions are IEEE.
+#pragma once
+#include "nbits_device.h"
+
+namespace msnb {
+
+constexpr int kNormThreads = 256;
+
+// Sum over the workgroup in a fixed order: wave sums by xor butterflies, then the four
+// wave sums in index order.
+__device__ __forceinline__ float block_sum256(float v, float* red)
+{
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    const float s = ((red[0] + red[1]) + red[2]) + red[3];
+    __syncthreads();
+    return s;
+}
+
+// y may alias x (each element is read before it is written, by the same thread).
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* x, const float* __restrict__ scale,
+                                                               float* y, float* __restrict__ inv_std, int norm,
+                                                               float eps)
+{
+    __shared__ float red[4];
+    const int64_t off = (int64_t)blockIdx.x * norm;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < norm; i += kNormThreads) {
+        const float v = x[off + i];
+        ss = ss + v * v;
+    }
+    const float sum_sq = block_sum256(ss, red);
+    const float inv = 1.0f / __builtin_sqrtf(sum_sq / (float)norm + eps);
+    if (inv_std && threadIdx.x == 0) inv_std[blockIdx.x] = inv;
+    for (int i = threadIdx.x; i < norm; i += kNormThreads) y[off + i] = (x[off + i] * inv) * scale[i];
+}
+
+// out and sum_out may alias input or skip (the residual stream updated in place): every
+// element is read and written by one thread, and the second pass reads t back from
+// sum_out when it was written.
+__global__ __launch_bounds__(kNormThreads) void skip_rmsnorm_kernel(
+    const float* input, const float* skip, const float* __restrict__ gamma, const float* __restrict__ beta,
+    const float* __restrict__ bias, float* out, float* sum_out, float* __restrict__ inv_std, int norm, float eps)
+{
+    __shared__ float red[4];
+    const int64_t off = (int64_t)blockIdx.x * norm;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < norm; i += kNormThreads) {
+        float t = input[off + i] + skip[off + i];
+        if (bias) t = t + bias[i];
+        if (sum_out) sum_out[off + i] = t;
+        ss = ss + t * t;
+    }
+    const float sum_sq = block_sum256(ss, red);
+    const float inv = 1.0f / __builtin_sqrtf(sum_sq / (float)norm + eps);
+    if (inv_std && threadIdx.x == 0) inv_std[blockIdx.x] = inv;
+    for (int i = threadIdx.x; i < norm; i += kNormThreads) {
+        float t;
+        if (sum_out) {
+            t = sum_out[off + i];
+        } else {   // recomputed: the same roundings
+            t = input[off + i] + skip[off + i];
+            if (bias) t = t + bias[i];
+        }
+        float v = (t * inv) * gamma[i];
+        if (beta) v = v + beta[i];
+        out[off + i] = v;
+    }
+}
+
+// Elementwise: y may alias an input.
+__global__ __launch_bounds__(256) void silu_mul_kernel(const float* g, const float* u, float* y, int64_t n)
+{
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const float x = g[i];
+        const float s = 1.0f / (1.0f + expf(-x));
+        y[i] = (x * s) * u[i];
+    }
+}
+
+__global__ __launch_bounds__(256) void add_kernel(const float* a, const float* b, float* y, int64_t n)
+{
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = a[i] + b[i];
+}
+
+__global__ __launch_bounds__(256) void sigmoid_kernel(const float* x, float* y, int64_t n)
+{
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = 1.0f / (1.0f + expf(-x[i]));
+}
+
+__global__ __launch_bounds__(256) void mul_kernel(const float* a, const float* b, float* y, int64_t n)
+{
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = a[i] * b[i];
+}
+
+}  // namespace msnb

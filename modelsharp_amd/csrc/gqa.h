@@ -1,0 +1,204 @@
+// gqa.h — GroupQueryAttention (com.microsoft), the attention of Llama-family decoder
+// layers between the q/k/v and o projections (Cpu/Kernels/Llm/GroupQueryAttentionKernel.cs).
+//
+//   num_heads query heads share kv_num_heads key/value heads (group = num_heads / kv_heads);
+//   causal: query qi (absolute position past + qi) sees keys
+//     [max(0, qAbs - local_window_size + 1) if the window is set, else 0,
+//      min(qAbs, seqlens_k[b])];
+//   optional rotary on Q and K (not V) from cos/sin caches indexed by absolute position
+//     (half-split or interleaved pairs, channels past the rotary span unchanged);
+//   present K/V = past rows, then the new rows, [B, kv_heads, capacity, head_dim];
+//   out = softmax(scale * q.K^T) V with the row maximum subtracted before exp.
+//
+// Present buffers carry a row capacity: a caller that keeps its cache in HBM passes the
+// same buffer as past and present (past_in_present) and each step appends only its new
+// rows — the append-only cache the reference's CPU kernel cannot keep (:239-253).
+//
+// Kernels:
+//   gqa_copy_past_kernel  past -> present rows [0, past) (skipped for an in-place cache)
+//   gqa_append_kernel     one thread per channel of each new (token, kv head) row: K
+//                         rotated exactly as the reference's ApplyRotary (:330-370,
+//                         a * c - b * s and b * c + a * s, each product rounded), V copied
+//   gqa_attention_kernel  one workgroup per (batch, head, query) unit, the reference's
+//                         unit order (:283-287): the rotated query row and the unit's
+//                         scores in LDS; keys strided over the 256 threads for q.k; a
+//                         fixed-order tree for the maximum and the sum; the weighted sum
+//                         of V rows split into contiguous key chunks per channel, chunks
+//                         added in order
+#pragma once
+#include "decoder_ops.h"
+
+namespace msnb {
+
+struct GqaArgs {
+    const float* q;       // query rows [B * Sq][q_stride]
+    const float* k;       // new key rows [B * Skv][kv_stride] (packed: inside the query rows)
+    const float* v;
+    const float* past_k;  // [B, kvH, past, D] (unused when past_in_present)
+    const float* past_v;
+    const int32_t* seqlens;
+    const float* cos;     // [cache_rows][half]
+    const float* sin;
+    float* out;           // [B * Sq][H * D]
+    float* pk;            // [B, kvH, cap, D]
+    float* pv;
+    int B, Sq, Skv, H, kvH, D, past, cap, total;
+    int q_stride, kv_stride;
+    int seqlens_len;
+    int do_rotary, interleaved, half, rot_half, cache_rows;
+    int window;
+    float scale;
+};
+
+__device__ __forceinline__ float rotated(const float* row, int d, int pos, const GqaArgs& p)
+{
+    const int rot = 2 * p.rot_half;
+    if (!p.do_rotary || d >= rot) return row[d];
+    int j, i0, i1;
+    if (p.interleaved) {
+        j = d >> 1;
+        i0 = 2 * j;
+        i1 = i0 + 1;
+    } else {
+        j = d < p.rot_half ? d : d - p.rot_half;
+        i0 = j;
+        i1 = j + p.rot_half;
+    }
+    const float c = p.cos[(int64_t)pos * p.half + j], s = p.sin[(int64_t)pos * p.half + j];
+    const float a = row[i0], b = row[i1];
+    return d == i0 ? a * c - b * s : b * c + a * s;
+}
+
+__device__ __forceinline__ int rotary_pos(int pos, const GqaArgs& p)
+{
+    return pos >= p.cache_rows ? p.cache_rows - 1 : pos;
+}
+
+__global__ __launch_bounds__(256) void gqa_copy_past_kernel(GqaArgs p)
+{
+    const int64_t n = (int64_t)p.B * p.kvH * p.past * p.D;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t bg = i / ((int64_t)p.past * p.D);
+        const int64_t rem = i - bg * p.past * p.D;
+        const int64_t dst = bg * p.cap * p.D + rem;
+        p.pk[dst] = p.past_k[i];
+        p.pv[dst] = p.past_v[i];
+    }
+}
+
+// grid: B * Skv * kvH rows, blockDim >= D (one thread per channel)
+__global__ __launch_bounds__(256) void gqa_append_kernel(GqaArgs p)
+{
+    const int row = blockIdx.x;   // (b, s, g) in the reference's scatter order (:255-263)
+    const int g = row % p.kvH, bs = row / p.kvH;
+    const int s = bs % p.Skv, b = bs / p.Skv;
+    const float* krow = p.k + (int64_t)(b * p.Skv + s) * p.kv_stride + g * p.D;
+    const float* vrow = p.v + (int64_t)(b * p.Skv + s) * p.kv_stride + g * p.D;
+    const int pos = rotary_pos(p.past + s, p);
+    const int64_t dst = ((int64_t)(b * p.kvH + g) * p.cap + p.past + s) * p.D;
+    for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
+        p.pk[dst + d] = rotated(krow, d, pos, p);
+        p.pv[dst + d] = vrow[d];
+    }
+}
+
+constexpr int kGqaThreads = 256;
+
+__device__ __forceinline__ float block_max256(float v, float* red)
+{
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    return m;
+}
+
+// Dynamic LDS: q[D], part[max(256, D)], scores[total]
+__global__ __launch_bounds__(kGqaThreads) void gqa_attention_kernel(GqaArgs p)
+{
+    extern __shared__ float lds[];
+    __shared__ float red[4];
+    float* qs = lds;
+    float* part = lds + p.D;
+    float* scores = part + max(kGqaThreads, p.D);
+    const int unit = blockIdx.x;
+    const int qi = unit % p.Sq, hb = unit / p.Sq;
+    const int h = hb % p.H, b = hb / p.H;
+    const int g = h / (p.H / p.kvH);
+    const int tid = threadIdx.x;
+
+    int bound = p.total - 1;
+    if (p.seqlens_len > 0) bound = min(bound, p.seqlens[min(b, p.seqlens_len - 1)]);
+    const int q_abs = p.past + qi;
+    const int k_limit = min(q_abs, bound);
+    const int k_start = p.window >= 0 ? max(0, q_abs - p.window + 1) : 0;
+    const int L = k_limit - k_start + 1;
+
+    const float* qrow = p.q + (int64_t)(b * p.Sq + qi) * p.q_stride + h * p.D;
+    const int pos = rotary_pos(q_abs, p);
+    for (int d = tid; d < p.D; d += kGqaThreads) qs[d] = rotated(qrow, d, pos, p);
+    __syncthreads();
+
+    const float* kbase = p.pk + ((int64_t)(b * p.kvH + g) * p.cap + k_start) * p.D;
+    const float* vbase = p.pv + ((int64_t)(b * p.kvH + g) * p.cap + k_start) * p.D;
+    float* orow = p.out + (int64_t)(b * p.Sq + qi) * p.H * p.D + h * p.D;
+
+    // scores
+    float mx = -__builtin_inff();
+    for (int j = tid; j < L; j += kGqaThreads) {
+        const float* kr = kbase + (int64_t)j * p.D;
+        float dot = 0.0f;
+        if ((p.D & 3) == 0) {
+            for (int d = 0; d < p.D; d += 4) {
+                const float4 k4 = *reinterpret_cast<const float4*>(kr + d);
+                dot = __builtin_fmaf(qs[d], k4.x, dot);
+                dot = __builtin_fmaf(qs[d + 1], k4.y, dot);
+                dot = __builtin_fmaf(qs[d + 2], k4.z, dot);
+                dot = __builtin_fmaf(qs[d + 3], k4.w, dot);
+            }
+        } else {
+            for (int d = 0; d < p.D; ++d) dot = __builtin_fmaf(qs[d], kr[d], dot);
+        }
+        const float sc = dot * p.scale;
+        scores[j] = sc;
+        mx = fmaxf(mx, sc);
+    }
+    mx = block_max256(mx, red);
+    float sum = 0.0f;
+    for (int j = tid; j < L; j += kGqaThreads) {
+        const float e = expf(scores[j] - mx);
+        scores[j] = e;
+        sum = sum + e;
+    }
+    sum = block_sum256(sum, red);   // also orders the score writes before the reads below
+    const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+
+    // out[d] = sum_j (e_j * inv) * v[j][d]: chunk c of the keys per thread group
+    const int nch = p.D <= kGqaThreads ? kGqaThreads / p.D : 1;
+    const int c = tid / p.D;
+    if (p.D <= kGqaThreads) {
+        const int d = tid - c * p.D;
+        if (c < nch) {
+            const int j0 = (int)(((int64_t)L * c) / nch), j1 = (int)(((int64_t)L * (c + 1)) / nch);
+            float acc = 0.0f;
+            for (int j = j0; j < j1; ++j) acc = __builtin_fmaf(scores[j] * inv, vbase[(int64_t)j * p.D + d], acc);
+            part[c * p.D + d] = acc;
+        }
+        __syncthreads();
+        if (tid < p.D) {
+            float o = part[tid];
+            for (int cc = 1; cc < nch; ++cc) o = o + part[cc * p.D + tid];
+            orow[tid] = L > 0 ? o : 0.0f;
+        }
+    } else {
+        for (int d = tid; d < p.D; d += kGqaThreads) {
+            float acc = 0.0f;
+            for (int j = 0; j < L; ++j) acc = __builtin_fmaf(scores[j] * inv, vbase[(int64_t)j * p.D + d], acc);
+            orow[d] = acc;
+        }
+    }
+}
+
+}  // namespace msnb

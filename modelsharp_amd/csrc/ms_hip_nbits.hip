@@ -44,6 +44,7 @@
 #include "generic_nbits.h"
 #include "mfma_general.h"
 #include "w4a8.h"
+#include "gqa.h"
 #include "mfma_w4.h"
 #include "mfma_w4_pipe.h"
 #include "mfma_w4_rb.h"
@@ -1999,6 +2000,216 @@ int ms_hip_nbits_launch_info(void* handle, int M, int* kernel_id, int* lanes_per
     if (lanes_per_row) *lanes_per_row = G;
     if (grid) *grid = gr;
     if (block) *block = bl;
+    return MS_HIP_OK;
+}
+
+}  // extern "C"
+
+// =========================================================================================
+// Decoder-layer neighbours of MatMulNBits (device pointers, stream-ordered, no allocation).
+namespace {
+
+int elementwise_grid(int64_t n) { return (int)std::min<int64_t>((n + 255) / 256, 8192); }
+
+bool misaligned4(const void* p) { return p && (reinterpret_cast<uintptr_t>(p) & 3); }
+
+}  // namespace
+
+extern "C" {
+
+int ms_hip_rmsnorm(const float* dX, const float* dScale, float* dY, float* dInvStd, int64_t rows, int norm, float eps,
+                   void* stream)
+{
+    if (int st = gate()) return st;
+    if (rows < 0 || norm <= 0 || rows > INT_MAX)
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] rmsnorm needs 0 <= rows <= 2^31-1 and norm > 0 (rows=%lld, norm=%d)",
+                    (long long)rows, norm);
+    if (rows == 0) return MS_HIP_OK;
+    if (!dX || !dScale || !dY) return fail(MS_HIP_ERR_INVALID, "[ms_hip] rmsnorm: null input, scale or output");
+    if (misaligned4(dX) || misaligned4(dScale) || misaligned4(dY) || misaligned4(dInvStd))
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] rmsnorm: buffers must be 4-byte aligned");
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(kNormThreads), 0, static_cast<hipStream_t>(stream),
+                       dX, dScale, dY, dInvStd, norm, eps);
+    MS_HIP_CHECK(hipGetLastError());
+    return MS_HIP_OK;
+}
+
+int ms_hip_skip_rmsnorm(const float* dInput, const float* dSkip, const float* dGamma, const float* dBeta,
+                        const float* dBias, float* dOut, float* dSum, float* dInvStd, int64_t rows, int norm,
+                        float eps, void* stream)
+{
+    if (int st = gate()) return st;
+    if (rows < 0 || norm <= 0 || rows > INT_MAX)
+        return fail(MS_HIP_ERR_INVALID,
+                    "[ms_hip] skip_rmsnorm needs 0 <= rows <= 2^31-1 and norm > 0 (rows=%lld, norm=%d)",
+                    (long long)rows, norm);
+    if (rows == 0) return MS_HIP_OK;
+    if (!dInput || !dSkip || !dGamma || !dOut)
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] skip_rmsnorm: null input, skip, gamma or output");
+    for (const void* q : {(const void*)dInput, (const void*)dSkip, (const void*)dGamma, (const void*)dBeta,
+                          (const void*)dBias, (const void*)dOut, (const void*)dSum, (const void*)dInvStd})
+        if (misaligned4(q)) return fail(MS_HIP_ERR_INVALID, "[ms_hip] skip_rmsnorm: buffers must be 4-byte aligned");
+    hipLaunchKernelGGL(skip_rmsnorm_kernel, dim3((unsigned)rows), dim3(kNormThreads), 0,
+                       static_cast<hipStream_t>(stream), dInput, dSkip, dGamma, dBeta, dBias, dOut, dSum, dInvStd,
+                       norm, eps);
+    MS_HIP_CHECK(hipGetLastError());
+    return MS_HIP_OK;
+}
+
+int ms_hip_silu_mul(const float* dGate, const float* dUp, float* dY, int64_t n, void* stream)
+{
+    if (int st = gate()) return st;
+    if (n < 0) return fail(MS_HIP_ERR_INVALID, "[ms_hip] silu_mul: negative length");
+    if (n == 0) return MS_HIP_OK;
+    if (!dGate || !dUp || !dY) return fail(MS_HIP_ERR_INVALID, "[ms_hip] silu_mul: null buffer");
+    hipLaunchKernelGGL(silu_mul_kernel, dim3(elementwise_grid(n)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       dGate, dUp, dY, n);
+    MS_HIP_CHECK(hipGetLastError());
+    return MS_HIP_OK;
+}
+
+int ms_hip_add(const float* dA, const float* dB, float* dY, int64_t n, void* stream)
+{
+    if (int st = gate()) return st;
+    if (n < 0) return fail(MS_HIP_ERR_INVALID, "[ms_hip] add: negative length");
+    if (n == 0) return MS_HIP_OK;
+    if (!dA || !dB || !dY) return fail(MS_HIP_ERR_INVALID, "[ms_hip] add: null buffer");
+    hipLaunchKernelGGL(add_kernel, dim3(elementwise_grid(n)), dim3(256), 0, static_cast<hipStream_t>(stream), dA, dB,
+                       dY, n);
+    MS_HIP_CHECK(hipGetLastError());
+    return MS_HIP_OK;
+}
+
+int ms_hip_sigmoid(const float* dX, float* dY, int64_t n, void* stream)
+{
+    if (int st = gate()) return st;
+    if (n < 0) return fail(MS_HIP_ERR_INVALID, "[ms_hip] sigmoid: negative length");
+    if (n == 0) return MS_HIP_OK;
+    if (!dX || !dY) return fail(MS_HIP_ERR_INVALID, "[ms_hip] sigmoid: null buffer");
+    hipLaunchKernelGGL(sigmoid_kernel, dim3(elementwise_grid(n)), dim3(256), 0, static_cast<hipStream_t>(stream), dX,
+                       dY, n);
+    MS_HIP_CHECK(hipGetLastError());
+    return MS_HIP_OK;
+}
+
+int ms_hip_mul(const float* dA, const float* dB, float* dY, int64_t n, void* stream)
+{
+    if (int st = gate()) return st;
+    if (n < 0) return fail(MS_HIP_ERR_INVALID, "[ms_hip] mul: negative length");
+    if (n == 0) return MS_HIP_OK;
+    if (!dA || !dB || !dY) return fail(MS_HIP_ERR_INVALID, "[ms_hip] mul: null buffer");
+    hipLaunchKernelGGL(mul_kernel, dim3(elementwise_grid(n)), dim3(256), 0, static_cast<hipStream_t>(stream), dA, dB,
+                       dY, n);
+    MS_HIP_CHECK(hipGetLastError());
+    return MS_HIP_OK;
+}
+
+int ms_hip_gqa_check(const ms_hip_gqa_desc* d)
+{
+    // Messages of GroupQueryAttentionKernel.cs:69-76, :104-107, :136-145, :163-171.
+    if (!d) return fail(MS_HIP_ERR_INVALID, "[ms_hip] null GroupQueryAttention descriptor");
+    if (d->num_heads <= 0 || d->kv_num_heads <= 0)
+        return fail(MS_HIP_ERR_INVALID, "GroupQueryAttention requires positive 'num_heads' and 'kv_num_heads'.");
+    if (d->num_heads % d->kv_num_heads != 0)
+        return fail(MS_HIP_ERR_INVALID, "GroupQueryAttention num_heads=%d must be a multiple of kv_num_heads=%d.",
+                    d->num_heads, d->kv_num_heads);
+    if (d->batch < 0 || d->q_seq < 0 || d->kv_seq < 0 || d->head_dim <= 0 || d->past_seq < 0)
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] GroupQueryAttention: negative sizes or head_dim <= 0");
+    if (d->packed_qkv && d->kv_seq != d->q_seq)
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] packed QKV: kv_seq must equal q_seq");
+    const int64_t total = (int64_t)d->past_seq + d->kv_seq;
+    if (d->present_capacity < total)
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] present capacity %d is below past + new rows (%lld)",
+                    d->present_capacity, (long long)total);
+    if (d->do_rotary && (d->cos_rows <= 0 || d->cos_cols <= 0))
+        return fail(MS_HIP_ERR_INVALID,
+                    "GroupQueryAttention do_rotary=1 requires cos_cache (input 7) and sin_cache (input 8).");
+    const int64_t lds = ((int64_t)d->head_dim + std::max(kGqaThreads, d->head_dim) + total) * (int64_t)sizeof(float);
+    if (lds > 160 * 1024)
+        return fail(MS_HIP_ERR_UNSUPPORTED,
+                    "[ms_hip] GroupQueryAttention keeps a unit's scores in LDS: total sequence %lld with head_dim %d "
+                    "exceeds 160 KiB",
+                    (long long)total, d->head_dim);
+    return MS_HIP_OK;
+}
+
+int ms_hip_gqa(const ms_hip_gqa_desc* d, const float* dQ, const float* dK, const float* dV, const float* dPastK,
+               const float* dPastV, const int32_t* dSeqlensK, const float* dCos, const float* dSin, float* dOut,
+               float* dPresentK, float* dPresentV, void* stream)
+{
+    if (int st = gate()) return st;
+    if (int st = ms_hip_gqa_check(d)) return st;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    GqaArgs p;
+    p.B = d->batch;
+    p.Sq = d->q_seq;
+    p.Skv = d->kv_seq;
+    p.H = d->num_heads;
+    p.kvH = d->kv_num_heads;
+    p.D = d->head_dim;
+    p.past = d->past_seq;
+    p.cap = d->present_capacity;
+    p.total = d->past_seq + d->kv_seq;
+    const int qh = p.H * p.D, kvh = p.kvH * p.D;
+    if (!dQ || !dOut || !dPresentK || !dPresentV || (!d->packed_qkv && (!dK || !dV)))
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] GroupQueryAttention: null query, key, value, output or present");
+    if (p.past > 0 && !d->past_in_present && (!dPastK || !dPastV))
+        return fail(MS_HIP_ERR_INVALID, "GroupQueryAttention past_key provided without past_value.");
+    if (d->seqlens_len > 0 && !dSeqlensK) return fail(MS_HIP_ERR_INVALID, "[ms_hip] seqlens_len > 0 with null seqlens_k");
+    for (const void* q : {(const void*)dQ, (const void*)dK, (const void*)dV, (const void*)dPastK, (const void*)dPastV,
+                          (const void*)dCos, (const void*)dSin, (const void*)dOut, (const void*)dSeqlensK})
+        if (misaligned4(q)) return fail(MS_HIP_ERR_INVALID, "[ms_hip] GroupQueryAttention: buffers must be 4-byte aligned");
+    if ((p.D & 3) == 0 && ((reinterpret_cast<uintptr_t>(dPresentK) & 15) || (reinterpret_cast<uintptr_t>(dPresentV) & 15)))
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] GroupQueryAttention: present buffers must be 16-byte aligned");
+    if (misaligned4(dPresentK) || misaligned4(dPresentV))
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] GroupQueryAttention: buffers must be 4-byte aligned");
+    if (d->packed_qkv) {
+        p.q_stride = qh + 2 * kvh;
+        p.kv_stride = p.q_stride;
+        p.k = dQ + qh;
+        p.v = dQ + qh + kvh;
+    } else {
+        p.q_stride = qh;
+        p.kv_stride = kvh;
+        p.k = dK;
+        p.v = dV;
+    }
+    p.q = dQ;
+    p.past_k = dPastK;
+    p.past_v = dPastV;
+    p.seqlens = dSeqlensK;
+    p.seqlens_len = d->seqlens_len;
+    p.cos = dCos;
+    p.sin = dSin;
+    p.out = dOut;
+    p.pk = dPresentK;
+    p.pv = dPresentV;
+    p.do_rotary = d->do_rotary ? 1 : 0;
+    p.interleaved = d->rotary_interleaved ? 1 : 0;
+    p.half = d->cos_cols;
+    p.rot_half = d->do_rotary ? std::min(2 * d->cos_cols, p.D) / 2 : 0;   // :333-336
+    p.cache_rows = d->cos_rows;
+    p.window = d->local_window_size;
+    p.scale = d->scale != 0.0f ? d->scale : 1.0f / std::sqrt((float)p.D);   // :214-215
+    if (p.B == 0 || (p.Sq == 0 && p.Skv == 0)) return MS_HIP_OK;
+    if (p.past > 0 && !d->past_in_present) {
+        const int64_t n = (int64_t)p.B * p.kvH * p.past * p.D;
+        hipLaunchKernelGGL(gqa_copy_past_kernel, dim3(elementwise_grid(n)), dim3(256), 0, s, p);
+        MS_HIP_CHECK(hipGetLastError());
+    }
+    if (p.Skv > 0) {
+        const int threads = std::min(256, ((p.D + 63) / 64) * 64);
+        hipLaunchKernelGGL(gqa_append_kernel, dim3((unsigned)(p.B * p.Skv * p.kvH)), dim3(threads), 0, s, p);
+        MS_HIP_CHECK(hipGetLastError());
+    }
+    if (p.Sq > 0) {
+        const size_t lds = ((size_t)p.D + std::max(kGqaThreads, p.D) + p.total) * sizeof(float);
+        if (lds > 64 * 1024)
+            MS_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_attention_kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        hipLaunchKernelGGL(gqa_attention_kernel, dim3((unsigned)(p.B * p.H * p.Sq)), dim3(kGqaThreads), lds, s, p);
+        MS_HIP_CHECK(hipGetLastError());
+    }
     return MS_HIP_OK;
 }
 

@@ -1,0 +1,367 @@
+"""The decoder-layer operators next to MatMulNBits, on the device, behind the reference's
+operator interface (IKernel, KernelRegistry).
+
+Each kernel mirrors the reference's managed kernel of the same OpType — same inputs,
+attributes, outputs and error messages — and computes on the device through the C ABI
+of libms_hip_nbits.so, so a decoder layer's activations stay in HBM from one
+MatMulNBits to the next:
+
+  SimplifiedLayerNormalization      Cpu/Kernels/Llm/SimplifiedLayerNormalizationKernel.cs
+  SkipSimplifiedLayerNormalization  Cpu/Kernels/Llm/SkipSimplifiedLayerNormalizationKernel.cs
+  GroupQueryAttention               Cpu/Kernels/Llm/GroupQueryAttentionKernel.cs
+  Sigmoid, Mul, Add                 Activations/SigmoidKernel.cs, the elementwise Mul/Add
+                                    (equal shapes: the residual stream and the MLP gate)
+  SiluMul                           Sigmoid -> Mul -> Mul fused by fuse_silu_mul()
+
+Activations are torch tensors on the device (host arrays are uploaded once per call);
+initializers (norm weights, rotary caches) are uploaded once and kept. Nothing here
+computes on the CPU: an input the device kernels do not take raises
+ModelSharpException.
+"""
+from __future__ import annotations
+
+import dataclasses
+
+import numpy as np
+
+from . import native
+from .graph import GraphContext, GraphNode, IKernel, KernelRegistry, ModelGraph, ModelSharpException
+
+
+def _torch():
+    import torch
+    return torch
+
+
+class _DeviceInputs:
+    """Device copies of host arrays, one per array object (initializers)."""
+
+    def __init__(self):
+        self._cache: dict[int, tuple] = {}
+
+    def f32(self, t):
+        torch = _torch()
+        if isinstance(t, np.ndarray):
+            hit = self._cache.get(id(t))
+            if hit is not None and hit[0] is t:
+                return hit[1]
+            d = torch.from_numpy(np.ascontiguousarray(t, dtype=np.float32)).cuda()
+            self._cache[id(t)] = (t, d)
+            return d
+        if t.dtype != torch.float32:
+            t = t.float()
+        return t.contiguous()
+
+    def i32(self, t):
+        torch = _torch()
+        if isinstance(t, np.ndarray):
+            return torch.from_numpy(np.ascontiguousarray(t, dtype=np.int32)).cuda()
+        return t.to(torch.int32).contiguous()
+
+
+def _stream(t):
+    return _torch().cuda.current_stream(t.device).cuda_stream
+
+
+def _attr_float(node: GraphNode, key: str, default: float) -> float:
+    """Attr.Float (Cpu/Kernels/Internal/Attr.cs)."""
+    return float(node.attributes.get(key, default))
+
+
+def _present(node: GraphNode, i: int) -> bool:
+    return len(node.outputs) > i and len(node.outputs[i]) > 0
+
+
+class HipSimplifiedLayerNormalizationKernel(IKernel):
+    op_type = "SimplifiedLayerNormalization"
+
+    def __init__(self):
+        self._dev = _DeviceInputs()
+
+    def execute(self, node: GraphNode, ctx: GraphContext) -> None:
+        torch = _torch()
+        x = self._dev.f32(ctx.get_tensor(node.inputs[0]))
+        scale = self._dev.f32(ctx.get_tensor(node.inputs[1]))
+        rank = x.dim()
+        axis = node.attr_int("axis", -1)
+        if axis < 0:
+            axis += rank
+        eps = _attr_float(node, "epsilon", 1e-5)
+        outer = int(np.prod(x.shape[:axis])) if axis > 0 else 1
+        norm = int(np.prod(x.shape[axis:]))
+        if scale.numel() != norm:
+            raise ModelSharpException(f"SimplifiedLayerNormalization scale has {scale.numel()} elements; "
+                                      f"expected {norm}.")
+        y = torch.empty_like(x)
+        inv = torch.empty(outer, dtype=torch.float32, device=x.device) if _present(node, 1) else None
+        native.rmsnorm(x.data_ptr(), scale.data_ptr(), y.data_ptr(), None if inv is None else inv.data_ptr(),
+                       outer, norm, eps, _stream(x))
+        ctx.set(node.outputs[0], y)
+        if inv is not None:
+            ctx.set(node.outputs[1], inv)
+
+
+class HipSkipSimplifiedLayerNormalizationKernel(IKernel):
+    op_type = "SkipSimplifiedLayerNormalization"
+
+    def __init__(self):
+        self._dev = _DeviceInputs()
+
+    def execute(self, node: GraphNode, ctx: GraphContext) -> None:
+        torch = _torch()
+        inp = self._dev.f32(ctx.get_tensor(node.inputs[0]))
+        skip = self._dev.f32(ctx.get_tensor(node.inputs[1]))
+        gamma = self._dev.f32(ctx.get_tensor(node.inputs[2]))
+        beta = self._dev.f32(ctx.get_tensor(node.inputs[3])) if len(node.inputs) > 3 and node.inputs[3] else None
+        bias = self._dev.f32(ctx.get_tensor(node.inputs[4])) if len(node.inputs) > 4 and node.inputs[4] else None
+        eps = _attr_float(node, "epsilon", 1e-5)
+        norm = gamma.numel()
+        total = inp.numel()
+        outer = 0 if norm == 0 else total // norm
+        if skip.numel() != total:
+            raise ModelSharpException("SkipSimplifiedLayerNormalization skip must have the input's shape.")
+        out = torch.empty_like(inp)
+        want_sum = _present(node, 3)
+        total_t = torch.empty_like(inp) if want_sum else None
+        inv = torch.empty(outer, dtype=torch.float32, device=inp.device) if _present(node, 2) else None
+        ptr = lambda t: None if t is None else t.data_ptr()   # noqa: E731
+        native.skip_rmsnorm(inp.data_ptr(), skip.data_ptr(), gamma.data_ptr(), ptr(beta), ptr(bias), out.data_ptr(),
+                            ptr(total_t), ptr(inv), outer, norm, eps, _stream(inp))
+        ctx.set(node.outputs[0], out)
+        if _present(node, 1):   # mean: undefined for RMSNorm, zeros (:80-81)
+            ctx.set(node.outputs[1], torch.zeros(outer, dtype=torch.float32, device=inp.device))
+        if inv is not None:
+            ctx.set(node.outputs[2], inv)
+        if want_sum:
+            ctx.set(node.outputs[3], total_t)
+
+
+class _Elementwise(IKernel):
+    def __init__(self):
+        self._dev = _DeviceInputs()
+
+    def _same_shape(self, node, ctx):
+        a = self._dev.f32(ctx.get_tensor(node.inputs[0]))
+        b = self._dev.f32(ctx.get_tensor(node.inputs[1]))
+        if tuple(a.shape) != tuple(b.shape):
+            raise ModelSharpException(
+                f"{self.op_type} on the device takes equal shapes; got {list(a.shape)} and {list(b.shape)}.")
+        return a, b
+
+
+class HipAddKernel(_Elementwise):
+    op_type = "Add"
+
+    def execute(self, node, ctx):
+        a, b = self._same_shape(node, ctx)
+        y = _torch().empty_like(a)
+        native.add(a.data_ptr(), b.data_ptr(), y.data_ptr(), a.numel(), _stream(a))
+        ctx.set(node.outputs[0], y)
+
+
+class HipMulKernel(_Elementwise):
+    op_type = "Mul"
+
+    def execute(self, node, ctx):
+        a, b = self._same_shape(node, ctx)
+        y = _torch().empty_like(a)
+        native.mul(a.data_ptr(), b.data_ptr(), y.data_ptr(), a.numel(), _stream(a))
+        ctx.set(node.outputs[0], y)
+
+
+class HipSigmoidKernel(_Elementwise):
+    op_type = "Sigmoid"
+
+    def execute(self, node, ctx):
+        x = self._dev.f32(ctx.get_tensor(node.inputs[0]))
+        y = _torch().empty_like(x)
+        native.sigmoid(x.data_ptr(), y.data_ptr(), x.numel(), _stream(x))
+        ctx.set(node.outputs[0], y)
+
+
+class HipSiluMulKernel(_Elementwise):
+    """SiluMul(gate, up) = (gate * Sigmoid(gate)) * up: the three nodes fuse_silu_mul
+    replaces, with the same roundings."""
+    op_type = "SiluMul"
+
+    def execute(self, node, ctx):
+        g, u = self._same_shape(node, ctx)
+        y = _torch().empty_like(g)
+        native.silu_mul(g.data_ptr(), u.data_ptr(), y.data_ptr(), g.numel(), _stream(g))
+        ctx.set(node.outputs[0], y)
+
+
+def fuse_silu_mul(graph: ModelGraph) -> int:
+    """Rewrites Sigmoid(x) -> s, Mul(x, s) -> a, Mul(a, u) -> y (either operand order) into
+    one SiluMul(x, u) -> y node when s and a feed nothing else. Returns the number of
+    patterns fused."""
+    uses: dict[str, int] = {}
+    for n in graph.nodes:
+        for i in n.inputs:
+            uses[i] = uses.get(i, 0) + 1
+    for o in graph.outputs:
+        uses[o] = uses.get(o, 0) + 1
+    producer = {o: n for n in graph.nodes for o in n.outputs}
+    fused = 0
+    drop: set[int] = set()
+    replace: dict[int, GraphNode] = {}
+    for mul2 in graph.nodes:
+        if mul2.op_type != "Mul" or len(mul2.inputs) != 2:
+            continue
+        for ai in (0, 1):
+            a_name, u_name = mul2.inputs[ai], mul2.inputs[1 - ai]
+            mul1 = producer.get(a_name)
+            if mul1 is None or mul1.op_type != "Mul" or uses.get(a_name, 0) != 1 or id(mul1) in drop:
+                continue
+            sig = None
+            for si in (0, 1):
+                s_name, x_name = mul1.inputs[si], mul1.inputs[1 - si]
+                cand = producer.get(s_name)
+                if (cand is not None and cand.op_type == "Sigmoid" and cand.inputs[0] == x_name
+                        and uses.get(s_name, 0) == 1 and id(cand) not in drop):
+                    sig = cand
+                    break
+            if sig is None:
+                continue
+            drop.update({id(sig), id(mul1)})
+            replace[id(mul2)] = GraphNode("SiluMul", mul2.name + "/silu_mul", [sig.inputs[0], u_name],
+                                          list(mul2.outputs))
+            fused += 1
+            break
+    graph.nodes = [replace.get(id(n), n) for n in graph.nodes if id(n) not in drop]
+    return fused
+
+
+@dataclasses.dataclass
+class _Cache:
+    k: object
+    v: object
+    capacity: int
+
+
+class HipGroupQueryAttentionKernel(IKernel):
+    """GroupQueryAttention (GroupQueryAttentionKernel.cs:64-323). Present K/V are views
+    into per-node capacity buffers: when the next step passes them back as past K/V,
+    the new rows are appended in place (ms_hip_gqa past_in_present) instead of
+    copying the past, and the buffer doubles when it fills."""
+    op_type = "GroupQueryAttention"
+
+    def __init__(self):
+        self._dev = _DeviceInputs()
+        self._caches: dict[str, _Cache] = {}
+
+    def _cache_for(self, node, B, KH, D, past_k, total, device):
+        torch = _torch()
+        c = self._caches.get(node.name)
+        if (c is not None and past_k is not None and c.capacity >= total and isinstance(past_k, torch.Tensor)
+                and past_k.data_ptr() == c.k.data_ptr() and tuple(c.k.shape[:2]) == (B, KH)
+                and c.k.shape[3] == D):
+            return c, True
+        cap = max(total, 2 * (c.capacity if c is not None else 0), 64)
+        k = torch.empty((B, KH, cap, D), dtype=torch.float32, device=device)
+        v = torch.empty_like(k)
+        c = _Cache(k, v, cap)
+        self._caches[node.name] = c
+        return c, False
+
+    def execute(self, node: GraphNode, ctx: GraphContext) -> None:
+        torch = _torch()
+        H = node.attr_int("num_heads", 0)
+        KH = node.attr_int("kv_num_heads", 0)
+        if H <= 0 or KH <= 0:
+            raise ModelSharpException("GroupQueryAttention requires positive 'num_heads' and 'kv_num_heads'.")
+        if H % KH != 0:
+            raise ModelSharpException(
+                f"GroupQueryAttention num_heads={H} must be a multiple of kv_num_heads={KH}.")
+        q = self._dev.f32(ctx.get_tensor(node.inputs[0]))
+        if q.dim() != 3:
+            raise ModelSharpException(
+                f"GroupQueryAttention supports only 3-D query [B, S, hidden]; got rank {q.dim()}.")
+        key_name = node.inputs[1] if len(node.inputs) > 1 else ""
+        value_name = node.inputs[2] if len(node.inputs) > 2 else ""
+        packed = len(key_name) == 0 or len(value_name) == 0
+        B, Sq = int(q.shape[0]), int(q.shape[1])
+        k = v = None
+        if packed:
+            hidden = int(q.shape[2])
+            unit = H + 2 * KH
+            if hidden % unit != 0:
+                raise ModelSharpException(
+                    f"GroupQueryAttention packed-QKV hidden {hidden} not divisible by "
+                    f"(num_heads + 2·kv_num_heads) = {unit}.")
+            D = hidden // unit
+            Skv = Sq
+        else:
+            k = self._dev.f32(ctx.get_tensor(key_name))
+            v = self._dev.f32(ctx.get_tensor(value_name))
+            if k.dim() != 3 or v.dim() != 3:
+                raise ModelSharpException("GroupQueryAttention supports only unpacked 3-D key/value.")
+            q_hidden = int(q.shape[2])
+            Skv, kv_hidden = int(k.shape[1]), int(k.shape[2])
+            if int(k.shape[0]) != B or int(v.shape[0]) != B:
+                raise ModelSharpException("GroupQueryAttention query/key/value batch sizes disagree.")
+            if int(v.shape[1]) != Skv or int(v.shape[2]) != kv_hidden:
+                raise ModelSharpException("GroupQueryAttention key/value shapes disagree.")
+            if q_hidden % H != 0:
+                raise ModelSharpException(
+                    f"GroupQueryAttention query hidden {q_hidden} not divisible by num_heads={H}.")
+            D = q_hidden // H
+            if kv_hidden != KH * D:
+                raise ModelSharpException(
+                    f"GroupQueryAttention key/value hidden {kv_hidden} must equal kv_num_heads·head_dim = {KH * D}.")
+        past_k = ctx.get_tensor(node.inputs[3]) if len(node.inputs) > 3 and node.inputs[3] else None
+        past_v = ctx.get_tensor(node.inputs[4]) if len(node.inputs) > 4 and node.inputs[4] else None
+        past = 0
+        if past_k is not None:
+            if past_v is None:
+                raise ModelSharpException("GroupQueryAttention past_key provided without past_value.")
+            shp = tuple(int(x) for x in past_k.shape)
+            if len(shp) != 4 or shp[0] != B or shp[1] != KH or shp[3] != D:
+                raise ModelSharpException(
+                    "GroupQueryAttention past_key must be [B, kv_num_heads, pastSeq, head_dim].")
+            past = shp[2]
+        total = past + Skv
+        seqlens = None
+        if len(node.inputs) > 5 and node.inputs[5]:
+            seqlens = self._dev.i32(ctx.get_tensor(node.inputs[5])).reshape(-1)
+        do_rotary = node.attr_int("do_rotary", 0) != 0
+        cos = sin = None
+        if do_rotary:
+            if len(node.inputs) <= 8 or not node.inputs[7] or not node.inputs[8]:
+                raise ModelSharpException(
+                    "GroupQueryAttention do_rotary=1 requires cos_cache (input 7) and sin_cache (input 8).")
+            cos = self._dev.f32(ctx.get_tensor(node.inputs[7]))
+            sin = self._dev.f32(ctx.get_tensor(node.inputs[8]))
+        cache, in_place = self._cache_for(node, B, KH, D, past_k, total, q.device)
+        if past and not in_place:
+            pk_src, pv_src = self._dev.f32(past_k), self._dev.f32(past_v)
+        else:
+            pk_src = pv_src = None
+        d = native.GqaDesc(batch=B, q_seq=Sq, kv_seq=Skv, num_heads=H, kv_num_heads=KH, head_dim=D,
+                           packed_qkv=int(packed), past_seq=past, past_in_present=int(in_place and past > 0),
+                           present_capacity=cache.capacity, do_rotary=int(do_rotary),
+                           rotary_interleaved=int(node.attr_int("rotary_interleaved", 0) != 0),
+                           cos_rows=0 if cos is None else int(cos.shape[0]),
+                           cos_cols=0 if cos is None else int(cos.shape[-1]),
+                           local_window_size=node.attr_int("local_window_size", -1),
+                           scale=_attr_float(node, "scale", 0.0),
+                           seqlens_len=0 if seqlens is None else int(seqlens.numel()))
+        out = torch.empty((B, Sq, H * D), dtype=torch.float32, device=q.device)
+        ptr = lambda t: None if t is None else t.data_ptr()   # noqa: E731
+        native.gqa(d, q.data_ptr(), ptr(k), ptr(v), ptr(pk_src), ptr(pv_src), ptr(seqlens), ptr(cos), ptr(sin),
+                   out.data_ptr(), cache.k.data_ptr(), cache.v.data_ptr(), _stream(q))
+        ctx.set(node.outputs[0], out)
+        if _present(node, 1):
+            ctx.set(node.outputs[1], cache.k[:, :, :total, :])
+        if _present(node, 2):
+            ctx.set(node.outputs[2], cache.v[:, :, :total, :])
+
+
+def register_decoder_kernels(registry: KernelRegistry) -> KernelRegistry:
+    """Registers the device kernels of the decoder-layer operators (last registration
+    wins, KernelRegistry.cs:20-24)."""
+    for k in (HipSimplifiedLayerNormalizationKernel(), HipSkipSimplifiedLayerNormalizationKernel(),
+              HipGroupQueryAttentionKernel(), HipAddKernel(), HipMulKernel(), HipSigmoidKernel(),
+              HipSiluMulKernel()):
+        registry.register(k)
+    return registry

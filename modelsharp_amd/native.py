@@ -65,6 +65,14 @@ _PROTOTYPES = {
     "ms_hip_nbits_gemm_w4a8": (_c_int, [_vp, _vp, _vp, _c_int]),
     "ms_hip_qgemm_w4a8": (_c_int, [_vp, _vp, _vp, _vp, _vp] + [_c_int] * 5),
     "ms_hip_nbits_launch_info_w4a8": (_c_int, [_vp, _c_int, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int)]),
+    "ms_hip_rmsnorm": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_int, ctypes.c_float, _vp]),
+    "ms_hip_skip_rmsnorm": (_c_int, [_vp] * 8 + [_c_i64, _c_int, ctypes.c_float, _vp]),
+    "ms_hip_silu_mul": (_c_int, [_vp, _vp, _vp, _c_i64, _vp]),
+    "ms_hip_add": (_c_int, [_vp, _vp, _vp, _c_i64, _vp]),
+    "ms_hip_sigmoid": (_c_int, [_vp, _vp, _c_i64, _vp]),
+    "ms_hip_mul": (_c_int, [_vp, _vp, _vp, _c_i64, _vp]),
+    "ms_hip_gqa_check": (_c_int, [_vp]),
+    "ms_hip_gqa": (_c_int, [_vp] * 13),
     "ms_hip_debug_force_failure": (_c_int, [_c_int]),
     "ms_hip_nbits_gemm_dev_f16": (_c_int, [_vp, _vp, _vp, _c_int, _vp]),
     "ms_hip_nbits_device_error": (_c_int, [_vp]),
@@ -329,3 +337,47 @@ def qgemm_w4a8(a, b, scales, zero_points, M, N, K, bits, block_size) -> np.ndarr
     zp = None if zero_points is None else np.ascontiguousarray(zero_points, dtype=np.uint8)
     check(load().ms_hip_qgemm_w4a8(_ptr(a), _ptr(b), _ptr(scales), _ptr(zp), _ptr(y), M, N, K, bits, block_size))
     return y
+
+
+# ---- decoder-layer neighbours (device pointers; 0 / None for an absent optional buffer) ----
+class GqaDesc(ctypes.Structure):
+    """ms_hip_gqa_desc."""
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "batch", "q_seq", "kv_seq", "num_heads", "kv_num_heads", "head_dim", "packed_qkv", "past_seq",
+        "past_in_present", "present_capacity", "do_rotary", "rotary_interleaved", "cos_rows", "cos_cols",
+        "local_window_size")] + [("scale", ctypes.c_float), ("seqlens_len", ctypes.c_int)]
+
+
+def _d(p):
+    return _vp(p or 0)
+
+
+def rmsnorm(dX, dScale, dY, dInvStd, rows, norm, eps, stream=None):
+    check(load().ms_hip_rmsnorm(_d(dX), _d(dScale), _d(dY), _d(dInvStd), int(rows), int(norm), ctypes.c_float(eps),
+                                _d(stream)))
+
+
+def skip_rmsnorm(dInput, dSkip, dGamma, dBeta, dBias, dOut, dSum, dInvStd, rows, norm, eps, stream=None):
+    check(load().ms_hip_skip_rmsnorm(_d(dInput), _d(dSkip), _d(dGamma), _d(dBeta), _d(dBias), _d(dOut), _d(dSum),
+                                     _d(dInvStd), int(rows), int(norm), ctypes.c_float(eps), _d(stream)))
+
+
+def silu_mul(dGate, dUp, dY, n, stream=None):
+    check(load().ms_hip_silu_mul(_d(dGate), _d(dUp), _d(dY), int(n), _d(stream)))
+
+
+def add(dA, dB, dY, n, stream=None):
+    check(load().ms_hip_add(_d(dA), _d(dB), _d(dY), int(n), _d(stream)))
+
+
+def sigmoid(dX, dY, n, stream=None):
+    check(load().ms_hip_sigmoid(_d(dX), _d(dY), int(n), _d(stream)))
+
+
+def mul(dA, dB, dY, n, stream=None):
+    check(load().ms_hip_mul(_d(dA), _d(dB), _d(dY), int(n), _d(stream)))
+
+
+def gqa(desc: GqaDesc, dQ, dK, dV, dPastK, dPastV, dSeqlens, dCos, dSin, dOut, dPresentK, dPresentV, stream=None):
+    check(load().ms_hip_gqa(ctypes.byref(desc), _d(dQ), _d(dK), _d(dV), _d(dPastK), _d(dPastV), _d(dSeqlens),
+                            _d(dCos), _d(dSin), _d(dOut), _d(dPresentK), _d(dPresentV), _d(stream)))

@@ -23,6 +23,14 @@ _ref = None
 _ref_w4a8 = None
 
 
+class GqaDesc(ctypes.Structure):
+    """msor_gqa_desc / ms_hip_gqa_desc (the same field order)."""
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "batch", "q_seq", "kv_seq", "num_heads", "kv_num_heads", "head_dim", "packed_qkv", "past_seq",
+        "past_in_present", "present_capacity", "do_rotary", "rotary_interleaved", "cos_rows", "cos_cols",
+        "local_window_size")] + [("scale", ctypes.c_float), ("seqlens_len", ctypes.c_int)]
+
+
 def _ptr(a):
     return None if a is None else a.ctypes.data_as(_vp)
 
@@ -46,6 +54,10 @@ def lib() -> ctypes.CDLL:
         L.msor_dequant_weights.argtypes = [_vp, _vp, _vp, _vp, _vp] + [ctypes.c_int] * 5
         L.msor_matmul_f64.argtypes = [_vp, _vp, _vp] + [ctypes.c_int] * 4
         L.msor_w4a8_quantize.argtypes = [_vp, _vp, _vp] + [ctypes.c_int] * 3
+        L.msor_rmsnorm.argtypes = [_vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int, ctypes.c_float]
+        L.msor_skip_rmsnorm.argtypes = [_vp] * 8 + [ctypes.c_int64, ctypes.c_int, ctypes.c_float]
+        L.msor_silu_mul.argtypes = [_vp, _vp, _vp, ctypes.c_int64]
+        L.msor_gqa.argtypes = [ctypes.POINTER(GqaDesc)] + [_vp] * 11
         L.msor_qgemm_w4a8.argtypes = [_vp, _vp, _vp, _vp, _vp] + [ctypes.c_int] * 6
         _lib = L
     return _lib
@@ -182,3 +194,50 @@ def ref_qgemm_w4a8(a, b, scales, zp_packed, M, N, K, bits, block_size):
     zp_packed = None if zp_packed is None else np.ascontiguousarray(zp_packed, dtype=np.uint8)
     L.ms_qgemm_w4a8(_ptr(a), _ptr(b), _ptr(scales), _ptr(zp_packed), _ptr(y), M, N, K, bits, block_size)
     return y
+
+
+def _f32(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.float32)
+
+
+def rmsnorm(x, scale, eps):
+    """SimplifiedLayerNormalization over the last axis: (y, inv_std)."""
+    x = _f32(x)
+    norm = x.shape[-1]
+    rows = x.size // norm
+    y = np.empty_like(x)
+    inv = np.empty(rows, np.float32)
+    lib().msor_rmsnorm(_ptr(x), _ptr(_f32(scale)), _ptr(y), _ptr(inv), rows, norm, ctypes.c_float(eps))
+    return y, inv
+
+
+def skip_rmsnorm(inp, skip, gamma, beta, bias, eps):
+    """SkipSimplifiedLayerNormalization: (out, inv_std, input_skip_bias_sum)."""
+    inp, skip = _f32(inp), _f32(skip)
+    norm = _f32(gamma).size
+    rows = inp.size // norm
+    out, total = np.empty_like(inp), np.empty_like(inp)
+    inv = np.empty(rows, np.float32)
+    lib().msor_skip_rmsnorm(_ptr(inp), _ptr(skip), _ptr(_f32(gamma)), _ptr(_f32(beta)), _ptr(_f32(bias)), _ptr(out),
+                            _ptr(total), _ptr(inv), rows, norm, ctypes.c_float(eps))
+    return out, inv, total
+
+
+def silu_mul(g, u):
+    g, u = _f32(g), _f32(u)
+    y = np.empty_like(g)
+    lib().msor_silu_mul(_ptr(g), _ptr(u), _ptr(y), g.size)
+    return y
+
+
+def gqa(desc: GqaDesc, q, k=None, v=None, past_k=None, past_v=None, seqlens=None, cos=None, sin=None):
+    """GroupQueryAttention: (out [B, Sq, H*D], present_k, present_v [B, kvH, past+Skv, D])."""
+    d = desc
+    total = d.past_seq + d.kv_seq
+    out = np.empty((d.batch, d.q_seq, d.num_heads * d.head_dim), np.float32)
+    pk = np.empty((d.batch, d.kv_num_heads, total, d.head_dim), np.float32)
+    pv = np.empty_like(pk)
+    sl = None if seqlens is None else np.ascontiguousarray(seqlens, dtype=np.int32)
+    lib().msor_gqa(ctypes.byref(d), _ptr(_f32(q)), _ptr(_f32(k)), _ptr(_f32(v)), _ptr(_f32(past_k)),
+                   _ptr(_f32(past_v)), _ptr(sl), _ptr(_f32(cos)), _ptr(_f32(sin)), _ptr(out), _ptr(pk), _ptr(pv))
+    return out, pk, pv

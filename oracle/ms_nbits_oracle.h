@@ -69,6 +69,27 @@ void msor_w4a8_quantize(const float* a, int8_t* aq, float* sa, int M, int K, int
 void msor_qgemm_w4a8(const float* a, const uint8_t* b, const float* scales, const uint8_t* zp_packed,
                      float* y, int M, int N, int K, int bits, int block_size, int nthreads);
 
+/* Decoder-layer neighbours (ms_decoder_oracle.c). */
+void msor_rmsnorm(const float* x, const float* scale, float* y, float* inv_std, int64_t rows, int norm, float eps);
+void msor_skip_rmsnorm(const float* input, const float* skip, const float* gamma, const float* beta,
+                       const float* bias, float* out, float* sum, float* inv_std, int64_t rows, int norm, float eps);
+void msor_silu_mul(const float* g, const float* u, float* y, int64_t n);
+
+typedef struct msor_gqa_desc {
+    int batch, q_seq, kv_seq;
+    int num_heads, kv_num_heads, head_dim;
+    int packed_qkv;
+    int past_seq, past_in_present, present_capacity;
+    int do_rotary, rotary_interleaved, cos_rows, cos_cols;
+    int local_window_size;
+    float scale;
+    int seqlens_len;
+} msor_gqa_desc;
+/* present K/V are [B, kv_heads, past + kv_seq, head_dim] (the reference's layout) */
+void msor_gqa(const msor_gqa_desc* d, const float* q, const float* k, const float* v, const float* past_k,
+              const float* past_v, const int32_t* seqlens, const float* cos_c, const float* sin_c, float* out,
+              float* present_k, float* present_v);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,282 @@
+"""Device parity of the decoder-layer neighbours of MatMulNBits against the oracle
+(oracle/ms_decoder_oracle.c), and one decoder layer run end to end on the device.
+
+Bars: the residual sums, Add, Mul and the present V rows are bit-exact; rotated K rows
+are bit-exact (the same four roundings per pair); norms, SiLU and attention differ only in
+summation order and exp's last bits: elementwise rtol 2e-6 for the norms and activations
+(4e-6 for those through exp), attention within 1e-5 of max|out| per call.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from modelsharp_amd import native, workloads
+from modelsharp_amd.decoder_kernels import (HipGroupQueryAttentionKernel, fuse_silu_mul, register_decoder_kernels)
+from modelsharp_amd.graph import Engine, GraphContext, GraphNode, KernelRegistry, ModelGraph
+from modelsharp_amd.hip_kernel import register_kernels
+
+pytestmark = pytest.mark.gpu
+
+
+def log(msg):
+    print(msg, flush=True)
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+@pytest.mark.parametrize("rows,norm", [(1, 4096), (7, 100), (2048, 4096), (3, 3)])
+def test_rmsnorm(gpu, rows, norm):
+    import torch
+    r = np.random.default_rng(rows + norm)
+    x = (r.standard_normal((rows, norm)) * 2).astype(np.float32)
+    w = r.uniform(0.5, 1.5, norm).astype(np.float32)
+    dx, dw = dev(x), dev(w)
+    y, inv = torch.empty_like(dx), torch.empty(rows, device="cuda")
+    native.rmsnorm(dx.data_ptr(), dw.data_ptr(), y.data_ptr(), inv.data_ptr(), rows, norm, 1e-5)
+    ref, inv_ref = oracle.rmsnorm(x, w, 1e-5)
+    assert np.allclose(host(inv), inv_ref, rtol=2e-6, atol=0)
+    assert np.allclose(host(y), ref, rtol=2e-6, atol=1e-7 * np.abs(ref).max())
+    native.rmsnorm(dx.data_ptr(), dw.data_ptr(), dx.data_ptr(), None, rows, norm, 1e-5)   # in place
+    assert np.array_equal(host(dx), host(y))
+
+
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_skip_rmsnorm_in_place_residual(gpu, with_bias):
+    import torch
+    r = np.random.default_rng(5)
+    rows, norm = 5, 4096
+    a = r.standard_normal((rows, norm)).astype(np.float32)
+    s = r.standard_normal((rows, norm)).astype(np.float32)
+    g = r.uniform(0.5, 1.5, norm).astype(np.float32)
+    beta = r.standard_normal(norm).astype(np.float32) if with_bias else None
+    bias = r.standard_normal(norm).astype(np.float32) if with_bias else None
+    out_ref, inv_ref, sum_ref = oracle.skip_rmsnorm(a, s, g, beta, bias, 1e-6)
+    da, ds, dg = dev(a), dev(s), dev(g)
+    db = None if beta is None else dev(beta)
+    dbi = None if bias is None else dev(bias)
+    out, inv = torch.empty_like(da), torch.empty(rows, device="cuda")
+    ptr = lambda t: None if t is None else t.data_ptr()   # noqa: E731
+    # the residual stream updated in place: sum written over the skip input
+    native.skip_rmsnorm(da.data_ptr(), ds.data_ptr(), dg.data_ptr(), ptr(db), ptr(dbi), out.data_ptr(),
+                        ds.data_ptr(), inv.data_ptr(), rows, norm, 1e-6)
+    assert np.array_equal(host(ds), sum_ref)
+    assert np.allclose(host(out), out_ref, rtol=2e-6, atol=1e-7 * np.abs(out_ref).max())
+    assert np.allclose(host(inv), inv_ref, rtol=2e-6, atol=0)
+
+
+def test_elementwise(gpu):
+    import torch
+    r = np.random.default_rng(9)
+    n = 11008 * 3 + 5
+    g = (r.standard_normal(n) * 5).astype(np.float32)
+    u = r.standard_normal(n).astype(np.float32)
+    dg, du, y = dev(g), dev(u), torch.empty(n, device="cuda")
+    native.silu_mul(dg.data_ptr(), du.data_ptr(), y.data_ptr(), n)
+    ref = oracle.silu_mul(g, u)
+    assert np.allclose(host(y), ref, rtol=4e-6, atol=1e-30)
+    native.add(dg.data_ptr(), du.data_ptr(), y.data_ptr(), n)
+    assert np.array_equal(host(y), g + u)
+    native.mul(dg.data_ptr(), du.data_ptr(), y.data_ptr(), n)
+    assert np.array_equal(host(y), g * u)
+    native.sigmoid(dg.data_ptr(), y.data_ptr(), n)
+    assert np.allclose(host(y), 1 / (1 + np.exp(-g.astype(np.float64))), rtol=4e-6, atol=1e-30)
+    # SiluMul equals Sigmoid -> Mul -> Mul on the device bit for bit
+    s, a, y2 = torch.empty_like(dg), torch.empty_like(dg), torch.empty_like(dg)
+    native.sigmoid(dg.data_ptr(), s.data_ptr(), n)
+    native.mul(dg.data_ptr(), s.data_ptr(), a.data_ptr(), n)
+    native.mul(a.data_ptr(), du.data_ptr(), y2.data_ptr(), n)
+    native.silu_mul(dg.data_ptr(), du.data_ptr(), y.data_ptr(), n)
+    assert torch.equal(y, y2)
+
+
+# ---- GroupQueryAttention ---------------------------------------------------------------------
+from test_oracle_decoder import GQA_CASES, make_case   # noqa: E402
+
+
+def run_device_gqa(d, q, k, v, pk, pv, sl, cos, sin, capacity=None):
+    import torch
+    total = d.past_seq + d.kv_seq
+    cap = capacity or total
+    nd = native.GqaDesc(**{f: getattr(d, f) for f, _ in d._fields_})
+    nd.present_capacity = cap
+    PK = torch.zeros((d.batch, d.kv_num_heads, cap, d.head_dim), device="cuda")
+    PV = torch.zeros_like(PK)
+    out = torch.empty((d.batch, d.q_seq, d.num_heads * d.head_dim), device="cuda")
+    t = {n: (None if a is None else dev(a)) for n, a in dict(q=q, k=k, v=v, pk=pk, pv=pv, sl=sl, cos=cos,
+                                                                sin=sin).items()}
+    ptr = lambda x: None if x is None else x.data_ptr()   # noqa: E731
+    native.gqa(nd, ptr(t["q"]), ptr(t["k"]), ptr(t["v"]), ptr(t["pk"]), ptr(t["pv"]), ptr(t["sl"]), ptr(t["cos"]),
+               ptr(t["sin"]), out.data_ptr(), PK.data_ptr(), PV.data_ptr())
+    return host(out), host(PK)[:, :, :total], host(PV)[:, :, :total]
+
+
+def check_gqa(out, PK, PV, ref, rk, rv, what):
+    assert np.array_equal(PK, rk), what
+    assert np.array_equal(PV, rv), what
+    err = np.max(np.abs(out - ref)) / max(np.abs(ref).max(), 1e-30)
+    log(f"  {what}: max err / max|out| {err:.2e}")
+    assert err <= 1e-5, what
+
+
+@pytest.mark.parametrize("case", GQA_CASES, ids=lambda c: f"seed{c['seed']}")
+def test_gqa_cases(gpu, case):
+    d, q, k, v, pk, pv, sl, cos, sin = make_case(**case)
+    ref, rk, rv = oracle.gqa(d, q, k, v, pk, pv, sl, cos, sin)
+    check_gqa(*run_device_gqa(d, q, k, v, pk, pv, sl, cos, sin, capacity=d.past_seq + d.kv_seq + 7),
+              ref, rk, rv, f"seed {case['seed']}")
+
+
+@pytest.mark.parametrize("Sq,past,KH", [(1, 2047, 8), (1, 4095, 32), (128, 0, 8), (16, 300, 8)])
+def test_gqa_7b_shapes(gpu, Sq, past, KH):
+    d, q, k, v, pk, pv, sl, cos, sin = make_case(20 + Sq, B=1, Sq=Sq, H=32, KH=KH, D=128, past=past, packed=True,
+                                                 cos_rows=4096 + 128)
+    ref, rk, rv = oracle.gqa(d, q, k, v, pk, pv, sl, cos, sin)
+    check_gqa(*run_device_gqa(d, q, k, v, pk, pv, sl, cos, sin), ref, rk, rv, f"7B Sq={Sq} past={past} KH={KH}")
+
+
+def test_gqa_resident_cache_appends_in_place(gpu):
+    """Five decode steps through the operator kernel, each passing the previous present
+    K/V back as past: the cache buffer stays put and every step matches the oracle run
+    on the whole history."""
+    r = np.random.default_rng(3)
+    H, KH, D, S0 = 4, 2, 64, 6
+    cos_rows = 64
+    ang = np.outer(np.arange(cos_rows), 1.0 / 10000 ** (np.arange(D // 2) / (D // 2)))
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    node = GraphNode("GroupQueryAttention", "attn0", ["qkv", "", "", "past_k", "past_v", "", "", "cos", "sin"],
+                     ["out", "present_k", "present_v"],
+                     {"num_heads": H, "kv_num_heads": KH, "do_rotary": 1})
+    node0 = GraphNode("GroupQueryAttention", "attn0", ["qkv", "", "", "", "", "", "", "cos", "sin"],
+                      ["out", "present_k", "present_v"], node.attributes)
+    k = HipGroupQueryAttentionKernel()
+    hist_k = hist_v = None
+    ptr0 = None
+    for step in range(6):
+        S = S0 if step == 0 else 1
+        qkv = r.standard_normal((1, S, (H + 2 * KH) * D)).astype(np.float32)
+        ctx = GraphContext({"qkv": dev(qkv), "cos": cos, "sin": sin})
+        if step:
+            ctx.set("past_k", pres_k)
+            ctx.set("past_v", pres_v)
+        k.execute(node if step else node0, ctx)
+        out, pres_k, pres_v = ctx.get_tensor("out"), ctx.get_tensor("present_k"), ctx.get_tensor("present_v")
+        if step == 0:
+            ptr0 = pres_k.data_ptr()
+        assert pres_k.data_ptr() == ptr0   # appended in place (capacity 64)
+        past = 0 if step == 0 else hist_k.shape[2]
+        d = oracle.GqaDesc(batch=1, q_seq=S, kv_seq=S, num_heads=H, kv_num_heads=KH, head_dim=D, packed_qkv=1,
+                           past_seq=past, present_capacity=past + S, do_rotary=1, cos_rows=cos_rows, cos_cols=D // 2,
+                           local_window_size=-1)
+        ref, hist_k, hist_v = oracle.gqa(d, qkv, None, None, hist_k, hist_v, None, cos, sin)
+        check_gqa(host(out), host(pres_k), host(pres_v), ref, hist_k, hist_v, f"step {step}")
+    k._caches.clear()
+
+
+# ---- one decoder layer end to end ---------------------------------------------------------------
+def layer_graph(hid, H, KH, D, inter, bs, seed):
+    """A Llama-family decoder layer as the onnxruntime-genai INT4 exports lay it out:
+    SkipSimplifiedLayerNormalization, packed q/k/v MatMulNBits, GroupQueryAttention with
+    in-op rotary, o projection, SkipSimplifiedLayerNormalization, gate/up MatMulNBits,
+    Sigmoid -> Mul -> Mul, down MatMulNBits."""
+    r = np.random.default_rng(seed)
+    inits = {}
+
+    def mm(name, K, N):
+        op = workloads.Op(name, K, N, bs, True)
+        b, s, z = workloads.make_weights(op, seed + K + N)
+        inits.update({f"{name}.B": b, f"{name}.s": s, f"{name}.z": z})
+        return GraphNode("MatMulNBits", name, ["", f"{name}.B", f"{name}.s", f"{name}.z"], [""],
+                         {"K": K, "N": N, "bits": 4, "block_size": bs})
+
+    def wire(n, inputs, outputs):
+        n.inputs[0] = inputs
+        n.outputs = outputs
+        return n
+
+    inits["ln1.g"] = r.uniform(0.5, 1.5, hid).astype(np.float32)
+    inits["ln2.g"] = r.uniform(0.5, 1.5, hid).astype(np.float32)
+    ang = np.outer(np.arange(256), 1.0 / 10000 ** (np.arange(D // 2) / (D // 2)))
+    inits["cos"], inits["sin"] = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    nodes = [
+        GraphNode("SkipSimplifiedLayerNormalization", "ln1", ["x", "resid", "ln1.g"], ["n1", "", "", "t1"],
+                  {"epsilon": 1e-5}),
+        wire(mm("qkv", hid, (H + 2 * KH) * D), "n1", ["qkv_out"]),
+        GraphNode("GroupQueryAttention", "attn", ["qkv_out", "", "", "past_k", "past_v", "", "", "cos", "sin"],
+                  ["attn_out", "present_k", "present_v"], {"num_heads": H, "kv_num_heads": KH, "do_rotary": 1}),
+        wire(mm("o", H * D, hid), "attn_out", ["o_out"]),
+        GraphNode("SkipSimplifiedLayerNormalization", "ln2", ["o_out", "t1", "ln2.g"], ["n2", "", "", "t2"],
+                  {"epsilon": 1e-5}),
+        wire(mm("gate", hid, inter), "n2", ["g"]),
+        wire(mm("up", hid, inter), "n2", ["u"]),
+        GraphNode("Sigmoid", "sig", ["g"], ["sg"]),
+        GraphNode("Mul", "m1", ["g", "sg"], ["act0"]),
+        GraphNode("Mul", "m2", ["act0", "u"], ["act"]),
+        wire(mm("down", inter, hid), "act", ["y"]),
+    ]
+    return ModelGraph(nodes, inits, ["x", "resid", "past_k", "past_v"], ["y", "t2", "present_k", "present_v"])
+
+
+def layer_oracle(g, x, resid, past_k, past_v, hid, H, KH, D, inter, bs):
+    I = g.initializers
+
+    def mm(name, a, K, N):
+        return oracle.matmul_nbits(a.reshape(-1, K), I[f"{name}.B"], I[f"{name}.s"], I[f"{name}.z"], N, K, 4, bs)
+
+    S = x.shape[1]
+    n1, _, t1 = oracle.skip_rmsnorm(x.reshape(-1, hid), resid.reshape(-1, hid), I["ln1.g"], None, None, 1e-5)
+    qkv = mm("qkv", n1, hid, (H + 2 * KH) * D).reshape(1, S, -1)
+    past = 0 if past_k is None else past_k.shape[2]
+    d = oracle.GqaDesc(batch=1, q_seq=S, kv_seq=S, num_heads=H, kv_num_heads=KH, head_dim=D, packed_qkv=1,
+                       past_seq=past, present_capacity=past + S, do_rotary=1, cos_rows=256, cos_cols=D // 2,
+                       local_window_size=-1)
+    attn, pk, pv = oracle.gqa(d, qkv, None, None, past_k, past_v, None, I["cos"], I["sin"])
+    o = mm("o", attn, H * D, hid)
+    n2, _, t2 = oracle.skip_rmsnorm(o, t1, I["ln2.g"], None, None, 1e-5)
+    act = oracle.silu_mul(mm("gate", n2, hid, inter), mm("up", n2, hid, inter))
+    y = mm("down", act, inter, hid)
+    return y.reshape(1, S, hid), t2.reshape(1, S, hid), pk, pv
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_decoder_layer_end_to_end(gpu, fused):
+    """Prefill of 5 tokens, then 3 decode steps, the whole layer on the device (no host
+    round trip between operators), against the oracle composed on the CPU."""
+    import torch
+    hid, H, KH, D, inter, bs = 512, 8, 2, 64, 1024, 32
+    g = layer_graph(hid, H, KH, D, inter, bs, seed=1)
+    if fused:
+        assert fuse_silu_mul(g) == 1 and [n.op_type for n in g.nodes].count("SiluMul") == 1
+    reg = register_decoder_kernels(register_kernels(KernelRegistry()))
+    eng = Engine(g, reg)
+    r = np.random.default_rng(2)
+    pk = pv = None
+    hk = hv = None
+    for step, S in enumerate([5, 1, 1, 1]):
+        x = r.standard_normal((1, S, hid)).astype(np.float32)
+        resid = r.standard_normal((1, S, hid)).astype(np.float32)
+        feeds = {"x": dev(x), "resid": dev(resid)}
+        if pk is not None:
+            feeds.update(past_k=pk, past_v=pv)
+        else:
+            g.nodes[[n.op_type for n in g.nodes].index("GroupQueryAttention")].inputs[3:5] = ["", ""]
+        res = eng.run(feeds)
+        y, t2, pk, pv = res["y"], res["t2"], res["present_k"], res["present_v"]
+        assert isinstance(y, torch.Tensor) and y.is_cuda
+        ry, rt2, hk, hv = layer_oracle(g, x, resid, hk, hv, hid, H, KH, D, inter, bs)
+        if step == 0:
+            g.nodes[[n.op_type for n in g.nodes].index("GroupQueryAttention")].inputs[3:5] = ["past_k", "past_v"]
+        err = np.max(np.abs(host(y) - ry)) / np.abs(ry).max()
+        log(f"  step {step} (S={S}) fused={fused}: max err / max|y| {err:.2e}")
+        assert err <= 1e-4
+        assert np.allclose(host(t2), rt2, rtol=1e-5, atol=1e-5 * np.abs(rt2).max())

@@ -321,3 +321,51 @@ def test_kill_switch_leaves_registry_alone(monkeypatch):
     assert r.try_get("MatMulNBits") == (True, m)
     monkeypatch.setenv("MODELSHARP_HIP", "1")
     assert isinstance(register_kernels(r).try_get("MatMulNBits")[1], HipMatMulNBitsKernel)
+
+
+# ---- decoder-layer kernels: graph fusion and validation (no device needed) -----------------
+def test_fuse_silu_mul_patterns():
+    from modelsharp_amd.decoder_kernels import fuse_silu_mul
+    mk = lambda: ModelGraph(nodes=[   # noqa: E731
+        GraphNode("MatMulNBits", "gate", ["n", "B"], ["g"]),
+        GraphNode("Sigmoid", "sig", ["g"], ["s"]),
+        GraphNode("Mul", "m1", ["s", "g"], ["a"]),
+        GraphNode("Mul", "m2", ["u", "a"], ["y"]),
+    ], initializers={}, inputs=["n", "u"], outputs=["y"])
+    g = mk()
+    assert fuse_silu_mul(g) == 1
+    assert [(n.op_type, n.inputs, n.outputs) for n in g.nodes] == [
+        ("MatMulNBits", ["n", "B"], ["g"]), ("SiluMul", ["g", "u"], ["y"])]
+    g = mk()
+    g.outputs.append("s")   # the sigmoid is used elsewhere: no fusion
+    assert fuse_silu_mul(g) == 0 and len(g.nodes) == 4
+    g = mk()
+    g.nodes[2].inputs = ["s", "other"]   # Mul of the sigmoid with another tensor
+    assert fuse_silu_mul(g) == 0
+
+
+def test_gqa_kernel_validation_messages():
+    from modelsharp_amd.decoder_kernels import HipGroupQueryAttentionKernel
+    k = HipGroupQueryAttentionKernel()
+    node = GraphNode("GroupQueryAttention", "a", ["q"], ["o"], {"num_heads": 0, "kv_num_heads": 1})
+    with pytest.raises(ModelSharpException, match=r"^GroupQueryAttention requires positive 'num_heads' and 'kv_num_heads'\.$"):
+        k.execute(node, GraphContext({}))
+    node.attributes = {"num_heads": 6, "kv_num_heads": 4}
+    with pytest.raises(ModelSharpException, match=r"^GroupQueryAttention num_heads=6 must be a multiple of kv_num_heads=4\.$"):
+        k.execute(node, GraphContext({}))
+
+
+def test_gqa_descriptor_checks():
+    lib = native.load()
+    d = native.GqaDesc(batch=1, q_seq=2, kv_seq=2, num_heads=4, kv_num_heads=2, head_dim=64, packed_qkv=1,
+                       present_capacity=1)
+    assert lib.ms_hip_gqa_check(ctypes.byref(d)) == native.MS_HIP_ERR_INVALID
+    assert "present capacity" in native.last_error()
+    d.present_capacity = 2
+    d.do_rotary = 1
+    assert lib.ms_hip_gqa_check(ctypes.byref(d)) == native.MS_HIP_ERR_INVALID
+    assert "cos_cache" in native.last_error()
+    d.do_rotary = 0
+    assert lib.ms_hip_gqa_check(ctypes.byref(d)) == 0
+    d.past_seq, d.present_capacity = 50000, 50002
+    assert lib.ms_hip_gqa_check(ctypes.byref(d)) == native.MS_HIP_ERR_UNSUPPORTED
