@@ -104,6 +104,22 @@ int ms_hip_nbits_weights_create_ex(const uint8_t* bq, int64_t bq_len,
                                    const void* zero_points, int64_t zp_len, int zp_type,
                                    int N, int K, int bits, int block_size,
                                    void** out_handle);
+/* The load-time path from the model file (OnnxModelLoader.cs:236-431 reads these
+ * initializers; :468-511 maps external data): each tensor given as a slice of a file
+ * (the .onnx itself for inline raw_data, or an external-data file), streamed from disk
+ * into the handle's device buffers through pinned double buffers — no host copy of the
+ * weights. dtype: B MS_HIP_DTYPE_U8; scales F32 or F16; zero points U8, F32 or F16
+ * (zero_points or its path NULL: none). length is in bytes. */
+typedef struct ms_hip_file_slice {
+    const char* path;
+    int64_t offset;
+    int64_t length;
+    int dtype;
+} ms_hip_file_slice;
+int ms_hip_nbits_weights_create_from_files(const ms_hip_file_slice* b, const ms_hip_file_slice* scales,
+                                           const ms_hip_file_slice* zero_points,
+                                           int N, int K, int bits, int block_size,
+                                           void** out_handle);
 /* Same, from buffers already resident on the device (copied device-to-device). */
 int ms_hip_nbits_weights_create_dev(const uint8_t* d_bq, const float* d_scales,
                                     const uint8_t* d_zero_points,
@@ -300,8 +316,8 @@ int ms_hip_mul(const float* dA, const float* dB, float* dY, int64_t n, void* str
  * int32 [seqlens_len] on the device (0: none); cos/sin caches [cos_rows, cos_cols]
  * (do_rotary); output [batch, q_seq, num_heads*head_dim]. Causal with the reference's
  * key range min(past + qi, seqlens_k[b]) and local_window_size lower bound; scale 0
- * means 1/sqrt(head_dim). The softmax keeps a unit's scores in LDS: past + kv_seq up
- * to about 40K keys (MS_HIP_ERR_UNSUPPORTED beyond). */
+ * means 1/sqrt(head_dim). The softmax keeps a unit's (or a key split's) scores in
+ * LDS. */
 typedef struct ms_hip_gqa_desc {
     int batch, q_seq, kv_seq;
     int num_heads, kv_num_heads, head_dim;
@@ -313,10 +329,16 @@ typedef struct ms_hip_gqa_desc {
     int seqlens_len;
 } ms_hip_gqa_desc;
 int ms_hip_gqa_check(const ms_hip_gqa_desc* desc);
+/* Bytes of the optional workspace that lets few (batch, head, query) units over a long
+ * history split their keys over several workgroups (0: no split for this shape). With
+ * a smaller or NULL workspace ms_hip_gqa runs unsplit, or returns MS_HIP_ERR_UNSUPPORTED
+ * when one workgroup cannot hold the history's scores. */
+int64_t ms_hip_gqa_workspace_size(const ms_hip_gqa_desc* desc);
 int ms_hip_gqa(const ms_hip_gqa_desc* desc, const float* dQ, const float* dK, const float* dV,
                const float* dPastK, const float* dPastV, const int32_t* dSeqlensK,
                const float* dCos, const float* dSin, float* dOut,
-               float* dPresentK, float* dPresentV, void* stream);
+               float* dPresentK, float* dPresentV, void* dWorkspace, int64_t workspace_bytes,
+               void* stream);
 
 #ifdef __cplusplus
 }

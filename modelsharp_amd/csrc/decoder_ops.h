@@ -39,13 +39,59 @@ __device__ __forceinline__ float block_sum256(float v, float* red)
     return s;
 }
 
+// Rows of up to kNormRegs * 4 * kNormThreads floats (vec: norm % 4 == 0, every buffer
+// 16-byte aligned)
+// are held in registers between the two passes: every load of a row is issued before any
+// store, which the compiler cannot arrange by itself when the output may alias an input.
+constexpr int kNormRegs = 8;
+
+__device__ __forceinline__ float4 f4add(float4 a, float4 b)
+{
+    return float4{a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w};
+}
+
+__device__ __forceinline__ float f4sq(float4 t, float ss)
+{
+    ss = ss + t.x * t.x;
+    ss = ss + t.y * t.y;
+    ss = ss + t.z * t.z;
+    return ss + t.w * t.w;
+}
+
+__device__ __forceinline__ float4 f4norm(float4 t, float inv, float4 g)
+{
+    return float4{(t.x * inv) * g.x, (t.y * inv) * g.y, (t.z * inv) * g.z, (t.w * inv) * g.w};
+}
+
 // y may alias x (each element is read before it is written, by the same thread).
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* x, const float* __restrict__ scale,
                                                                float* y, float* __restrict__ inv_std, int norm,
-                                                               float eps)
+                                                               float eps, int vec)
 {
     __shared__ float red[4];
     const int64_t off = (int64_t)blockIdx.x * norm;
+    if (vec && (norm & 3) == 0 && norm <= 4 * kNormThreads * kNormRegs) {
+        const int n4 = norm >> 2;
+        const float4* x4 = reinterpret_cast<const float4*>(x + off);
+        float4 t[kNormRegs];
+        float ss = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kNormRegs; ++u) {
+            const int i = threadIdx.x + u * kNormThreads;
+            t[u] = i < n4 ? x4[i] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int u = 0; u < kNormRegs; ++u) ss = f4sq(t[u], ss);
+        const float inv = 1.0f / __builtin_sqrtf(block_sum256(ss, red) / (float)norm + eps);
+        if (inv_std && threadIdx.x == 0) inv_std[blockIdx.x] = inv;
+        float4* y4 = reinterpret_cast<float4*>(y + off);
+#pragma unroll
+        for (int u = 0; u < kNormRegs; ++u) {
+            const int i = threadIdx.x + u * kNormThreads;
+            if (i < n4) y4[i] = f4norm(t[u], inv, reinterpret_cast<const float4*>(scale)[i]);
+        }
+        return;
+    }
     float ss = 0.0f;
     for (int i = threadIdx.x; i < norm; i += kNormThreads) {
         const float v = x[off + i];
@@ -62,10 +108,45 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* x, c
 // sum_out when it was written.
 __global__ __launch_bounds__(kNormThreads) void skip_rmsnorm_kernel(
     const float* input, const float* skip, const float* __restrict__ gamma, const float* __restrict__ beta,
-    const float* __restrict__ bias, float* out, float* sum_out, float* __restrict__ inv_std, int norm, float eps)
+    const float* __restrict__ bias, float* out, float* sum_out, float* __restrict__ inv_std, int norm, float eps,
+    int vec)
 {
     __shared__ float red[4];
     const int64_t off = (int64_t)blockIdx.x * norm;
+    if (vec && (norm & 3) == 0 && norm <= 4 * kNormThreads * kNormRegs) {
+        const int n4 = norm >> 2;
+        const float4* a4 = reinterpret_cast<const float4*>(input + off);
+        const float4* b4 = reinterpret_cast<const float4*>(skip + off);
+        float4 t[kNormRegs];
+        float ss = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kNormRegs; ++u) {
+            const int i = threadIdx.x + u * kNormThreads;
+            t[u] = i < n4 ? f4add(a4[i], b4[i]) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (bias && i < n4) t[u] = f4add(t[u], reinterpret_cast<const float4*>(bias)[i]);
+        }
+#pragma unroll
+        for (int u = 0; u < kNormRegs; ++u) ss = f4sq(t[u], ss);
+        if (sum_out) {
+#pragma unroll
+            for (int u = 0; u < kNormRegs; ++u) {
+                const int i = threadIdx.x + u * kNormThreads;
+                if (i < n4) reinterpret_cast<float4*>(sum_out + off)[i] = t[u];
+            }
+        }
+        const float inv = 1.0f / __builtin_sqrtf(block_sum256(ss, red) / (float)norm + eps);
+        if (inv_std && threadIdx.x == 0) inv_std[blockIdx.x] = inv;
+#pragma unroll
+        for (int u = 0; u < kNormRegs; ++u) {
+            const int i = threadIdx.x + u * kNormThreads;
+            if (i < n4) {
+                float4 v = f4norm(t[u], inv, reinterpret_cast<const float4*>(gamma)[i]);
+                if (beta) v = f4add(v, reinterpret_cast<const float4*>(beta)[i]);
+                reinterpret_cast<float4*>(out + off)[i] = v;
+            }
+        }
+        return;
+    }
     float ss = 0.0f;
     for (int i = threadIdx.x; i < norm; i += kNormThreads) {
         float t = input[off + i] + skip[off + i];

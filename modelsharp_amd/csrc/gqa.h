@@ -19,12 +19,18 @@
 //   gqa_append_kernel     one thread per channel of each new (token, kv head) row: K
 //                         rotated exactly as the reference's ApplyRotary (:330-370,
 //                         a * c - b * s and b * c + a * s, each product rounded), V copied
-//   gqa_attention_kernel  one workgroup per (batch, head, query) unit, the reference's
-//                         unit order (:283-287): the rotated query row and the unit's
-//                         scores in LDS; keys strided over the 256 threads for q.k; a
-//                         fixed-order tree for the maximum and the sum; the weighted sum
-//                         of V rows split into contiguous key chunks per channel, chunks
-//                         added in order
+//   gqa_rows_kernel<G>    head_dim = 4 G in {32, 64, 128, 256}: one workgroup per (unit,
+//                         key split), units in the reference's order (:283-287). G lanes
+//                         read one key (value) row as float4s, coalesced; 256 / G rows are
+//                         in flight per pass, four passes' loads issued before their math.
+//                         q.k is reduced over the G lanes by xor shuffles; the split's
+//                         scores sit in LDS; a fixed-order tree gives the maximum and the
+//                         sum; the weighted V rows are summed per lane group and the groups
+//                         added in order. One split: the output row. Several (few units,
+//                         long history): each writes (max, sum, unnormalised row) and
+//   gqa_combine_kernel    rescales the splits to the common maximum and normalises
+//   gqa_attention_kernel  any other head_dim: one workgroup per unit, keys strided over
+//                         the threads
 #pragma once
 #include "decoder_ops.h"
 
@@ -198,6 +204,153 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_attention_kernel(GqaArgs p)
             for (int j = 0; j < L; ++j) acc = __builtin_fmaf(scores[j] * inv, vbase[(int64_t)j * p.D + d], acc);
             orow[d] = acc;
         }
+    }
+}
+
+constexpr int kGqaMaxSplits = 64;
+
+// Geometry of one (batch, head, query) unit.
+struct GqaUnit {
+    int b, h, qi, g, k_start, L;
+};
+
+__device__ __forceinline__ GqaUnit gqa_unit(const GqaArgs& p, int unit)
+{
+    GqaUnit u;
+    u.qi = unit % p.Sq;
+    const int hb = unit / p.Sq;
+    u.h = hb % p.H;
+    u.b = hb / p.H;
+    u.g = u.h / (p.H / p.kvH);
+    int bound = p.total - 1;
+    if (p.seqlens_len > 0) bound = min(bound, p.seqlens[min(u.b, p.seqlens_len - 1)]);
+    const int q_abs = p.past + u.qi;
+    const int k_limit = min(q_abs, bound);
+    u.k_start = p.window >= 0 ? max(0, q_abs - p.window + 1) : 0;
+    u.L = k_limit - u.k_start + 1;
+    return u;
+}
+
+// Dynamic LDS: q[D], part[(256 / G) * D], scores[ceil(L / splits)]
+template <int G>
+__global__ __launch_bounds__(kGqaThreads) void gqa_rows_kernel(GqaArgs p, float* __restrict__ ws, int splits)
+{
+    constexpr int NG = kGqaThreads / G, D = 4 * G, U = 4;
+    extern __shared__ float lds[];
+    __shared__ float red[4];
+    float* qs = lds;
+    float* part = qs + D;
+    float* scores = part + NG * D;
+    const int unit = blockIdx.x / splits, sp = blockIdx.x - unit * splits;
+    const GqaUnit u = gqa_unit(p, unit);
+    const int L = max(u.L, 0);
+    const int j0 = (int)(((int64_t)L * sp) / splits), j1 = (int)(((int64_t)L * (sp + 1)) / splits);
+    const int Ls = j1 - j0;
+    const int tid = threadIdx.x, kg = tid / G, e = tid - kg * G;
+
+    const float* qrow = p.q + (int64_t)(u.b * p.Sq + u.qi) * p.q_stride + u.h * D;
+    const int pos = rotary_pos(p.past + u.qi, p);
+    for (int d = tid; d < D; d += kGqaThreads) qs[d] = rotated(qrow, d, pos, p);
+    __syncthreads();
+    const float4 q4 = *reinterpret_cast<const float4*>(qs + 4 * e);
+    const int64_t row0 = ((int64_t)(u.b * p.kvH + u.g) * p.cap + u.k_start + j0) * D + 4 * e;
+    const float* kb = p.pk + row0;
+    const float* vb = p.pv + row0;
+
+    float mx = -__builtin_inff();
+    for (int j = kg; j < Ls; j += U * NG) {
+        float4 k4[U];
+#pragma unroll
+        for (int t = 0; t < U; ++t) {
+            const int jj = j + t * NG;
+            k4[t] = jj < Ls ? *reinterpret_cast<const float4*>(kb + (int64_t)jj * D) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int t = 0; t < U; ++t) {
+            float d = q4.x * k4[t].x;
+            d = __builtin_fmaf(q4.y, k4[t].y, d);
+            d = __builtin_fmaf(q4.z, k4[t].z, d);
+            d = __builtin_fmaf(q4.w, k4[t].w, d);
+#pragma unroll
+            for (int o = G / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, G);
+            const int jj = j + t * NG;
+            if (jj < Ls) {
+                const float sc = d * p.scale;
+                if (e == 0) scores[jj] = sc;
+                mx = fmaxf(mx, sc);
+            }
+        }
+    }
+    mx = block_max256(mx, red);
+    float sum = 0.0f;
+    for (int j = tid; j < Ls; j += kGqaThreads) {
+        const float ex = expf(scores[j] - mx);
+        scores[j] = ex;
+        sum = sum + ex;
+    }
+    sum = block_sum256(sum, red);   // also orders the score writes before the reads below
+    const float inv = splits == 1 ? (sum > 0.0f ? 1.0f / sum : 0.0f) : 1.0f;
+
+    float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = kg; j < Ls; j += U * NG) {
+        float4 v4[U];
+#pragma unroll
+        for (int t = 0; t < U; ++t) {
+            const int jj = j + t * NG;
+            v4[t] = jj < Ls ? *reinterpret_cast<const float4*>(vb + (int64_t)jj * D) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int t = 0; t < U; ++t) {
+            const int jj = j + t * NG;
+            if (jj < Ls) {
+                const float w = scores[jj] * inv;
+                acc.x = __builtin_fmaf(w, v4[t].x, acc.x);
+                acc.y = __builtin_fmaf(w, v4[t].y, acc.y);
+                acc.z = __builtin_fmaf(w, v4[t].z, acc.z);
+                acc.w = __builtin_fmaf(w, v4[t].w, acc.w);
+            }
+        }
+    }
+    *reinterpret_cast<float4*>(part + kg * D + 4 * e) = acc;
+    __syncthreads();
+    for (int d = tid; d < D; d += kGqaThreads) {
+        float o = part[d];
+        for (int c = 1; c < NG; ++c) o = o + part[c * D + d];
+        if (splits == 1) {
+            p.out[(int64_t)(u.b * p.Sq + u.qi) * p.H * D + u.h * D + d] = L > 0 ? o : 0.0f;
+        } else {
+            ws[(int64_t)blockIdx.x * (D + 2) + d] = o;
+        }
+    }
+    if (splits > 1 && tid == 0) {
+        ws[(int64_t)blockIdx.x * (D + 2) + D] = mx;
+        ws[(int64_t)blockIdx.x * (D + 2) + D + 1] = sum;
+    }
+}
+
+// One workgroup per unit: out = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s.
+__global__ __launch_bounds__(256) void gqa_combine_kernel(GqaArgs p, const float* __restrict__ ws, int splits)
+{
+    const int unit = blockIdx.x;
+    const GqaUnit u = gqa_unit(p, unit);
+    const int D = p.D;
+    const float* w = ws + (int64_t)unit * splits * (D + 2);
+    float M = -__builtin_inff();
+    for (int s = 0; s < splits; ++s)
+        if (w[s * (D + 2) + D + 1] > 0.0f) M = fmaxf(M, w[s * (D + 2) + D]);
+    float f[kGqaMaxSplits];
+    float lsum = 0.0f;
+    for (int s = 0; s < splits; ++s) {
+        const float l = w[s * (D + 2) + D + 1];
+        f[s] = l > 0.0f ? expf(w[s * (D + 2) + D] - M) : 0.0f;
+        lsum = lsum + l * f[s];
+    }
+    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+    float* orow = p.out + (int64_t)(u.b * p.Sq + u.qi) * p.H * D + u.h * D;
+    for (int d = threadIdx.x; d < D; d += blockDim.x) {
+        float o = 0.0f;
+        for (int s = 0; s < splits; ++s) o = __builtin_fmaf(w[s * (D + 2) + d], f[s], o);
+        orow[d] = o * inv;
     }
 }
 

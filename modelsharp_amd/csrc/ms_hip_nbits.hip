@@ -24,6 +24,7 @@
 #include <array>
 #include <atomic>
 #include <climits>
+#include <cerrno>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -36,7 +37,9 @@
 #include <utility>
 #include <vector>
 
+#include <fcntl.h>
 #include <strings.h>
+#include <unistd.h>
 
 #include "gemv_general.h"
 #include "gemv_w4.h"
@@ -1495,6 +1498,120 @@ int ms_hip_nbits_weights_create_ex(const uint8_t* bq, int64_t bq_len, const void
     return finish_create(w, st, out_handle);
 }
 
+}  // extern "C"
+
+namespace {
+
+// Streams bytes [offset, offset + length) of a file into device memory: pread into two
+// pinned chunks alternately while the DMA engine copies the other one, so disk reads and
+// PCIe transfers overlap and no host copy of the tensor is ever made.
+int stream_file(const char* path, int64_t offset, int64_t length, void* dst)
+{
+    constexpr size_t kChunk = (size_t)8 << 20;
+    if (length == 0) return MS_HIP_OK;
+    const int fd = open(path, O_RDONLY | O_CLOEXEC);
+    if (fd < 0) return fail(MS_HIP_ERR_INVALID, "[ms_hip] cannot open '%s': %s", path, std::strerror(errno));
+    uint8_t* pinned[2] = {nullptr, nullptr};
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    hipStream_t s = nullptr;
+    int st = MS_HIP_OK;
+    hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    for (int i = 0; i < 2 && e == hipSuccess; ++i) {
+        e = hipHostMalloc(reinterpret_cast<void**>(&pinned[i]), kChunk, hipHostMallocDefault);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&ev[i], hipEventDisableTiming);
+    }
+    if (e != hipSuccess) st = fail(MS_HIP_ERR_HIP, "[ms_hip] staging set-up failed: %s", hipGetErrorString(e));
+    int64_t done = 0;
+    for (int i = 0; st == MS_HIP_OK && done < length; ++i) {
+        const int b = i & 1;
+        if (i >= 2 && (e = hipEventSynchronize(ev[b])) != hipSuccess) {
+            st = fail(MS_HIP_ERR_HIP, "[ms_hip] staging copy failed: %s", hipGetErrorString(e));
+            break;
+        }
+        const size_t n = (size_t)std::min<int64_t>((int64_t)kChunk, length - done);
+        size_t got = 0;
+        while (got < n) {
+            const ssize_t r = pread(fd, pinned[b] + got, n - got, (off_t)(offset + done + (int64_t)got));
+            if (r < 0 && errno == EINTR) continue;
+            if (r <= 0) {
+                st = fail(MS_HIP_ERR_INVALID, "[ms_hip] '%s' ends before byte %lld", path,
+                          (long long)(offset + length));
+                break;
+            }
+            got += (size_t)r;
+        }
+        if (st) break;
+        e = hipMemcpyAsync(static_cast<uint8_t*>(dst) + done, pinned[b], n, hipMemcpyHostToDevice, s);
+        if (e == hipSuccess) e = hipEventRecord(ev[b], s);
+        if (e != hipSuccess) st = fail(MS_HIP_ERR_HIP, "[ms_hip] staging copy failed: %s", hipGetErrorString(e));
+        done += (int64_t)n;
+    }
+    if (s) (void)hipStreamSynchronize(s);
+    for (int i = 0; i < 2; ++i) {
+        if (ev[i]) (void)hipEventDestroy(ev[i]);
+        if (pinned[i]) (void)hipHostFree(pinned[i]);
+    }
+    if (s) (void)hipStreamDestroy(s);
+    close(fd);
+    return st;
+}
+
+int elem_bytes(int dtype) { return dtype == MS_HIP_DTYPE_F32 ? 4 : dtype == MS_HIP_DTYPE_F16 ? 2 : 1; }
+
+// A file slice of n fp32 values, or of n fp16 values widened on the device.
+int stream_file_f32(const ms_hip_file_slice& sl, int64_t n, float* dst)
+{
+    if (sl.dtype == MS_HIP_DTYPE_F32) return stream_file(sl.path, sl.offset, n * 4, dst);
+    void* tmp = nullptr;
+    hipError_t e = hipMalloc(&tmp, (size_t)n * 2);
+    if (e != hipSuccess) return fail(MS_HIP_ERR_HIP, "[ms_hip] allocation failed: %s", hipGetErrorString(e));
+    int st = stream_file(sl.path, sl.offset, n * 2, tmp);
+    if (!st) {
+        launch_widen(tmp, dst, n, nullptr);
+        e = hipGetLastError();
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e != hipSuccess) st = fail(MS_HIP_ERR_HIP, "[ms_hip] widening failed: %s", hipGetErrorString(e));
+    }
+    (void)hipFree(tmp);
+    return st;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ms_hip_nbits_weights_create_from_files(const ms_hip_file_slice* b, const ms_hip_file_slice* scales,
+                                           const ms_hip_file_slice* zero_points, int N, int K, int bits,
+                                           int block_size, void** out_handle)
+{
+    if (!out_handle) return fail(MS_HIP_ERR_INVALID, "[ms_hip] out_handle is null");
+    *out_handle = nullptr;
+    if (!b || !scales || !b->path || !scales->path)
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] B and scales need a file slice");
+    if (b->dtype != MS_HIP_DTYPE_U8) return fail(MS_HIP_ERR_INVALID, "Tensor dtype is not UInt8; expected UInt8.");
+    if (scales->dtype != MS_HIP_DTYPE_F32 && scales->dtype != MS_HIP_DTYPE_F16)
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] scales must be Float32 or Float16");
+    const bool has_zp = zero_points && zero_points->path;
+    const int zp_type = has_zp ? zero_points->dtype : MS_HIP_DTYPE_NONE;
+    const int zp_kind = zp_type == MS_HIP_DTYPE_NONE ? 0 : zp_type == MS_HIP_DTYPE_U8 ? 1
+                      : (zp_type == MS_HIP_DTYPE_F32 || zp_type == MS_HIP_DTYPE_F16) ? 2 : 3;
+    for (const ms_hip_file_slice* sl : {b, scales, has_zp ? zero_points : nullptr})
+        if (sl && (sl->offset < 0 || sl->length < 0 || sl->length % elem_bytes(sl->dtype)))
+            return fail(MS_HIP_ERR_INVALID, "[ms_hip] bad file slice of '%s'", sl->path);
+    int st = check_impl(N, K, bits, block_size, b->length, scales->length / elem_bytes(scales->dtype), zp_kind,
+                        has_zp ? zero_points->length / elem_bytes(zp_type) : 0, -1);
+    if (st) return st;
+    if ((st = require_device())) return st;
+    MS_HIP_CHECK(hipSetDevice(device_info().device));
+    Weights* w = nullptr;
+    if ((st = new_weights(N, K, bits, block_size, zp_kind, &w))) return st;
+    st = stream_file(b->path, b->offset, (int64_t)N * w->row_bytes, w->d_b);
+    if (!st) st = stream_file_f32(*scales, (int64_t)N * w->nb, w->d_scales);
+    if (!st && zp_kind == 1) st = stream_file(zero_points->path, zero_points->offset, (int64_t)N * w->zrb, w->d_zp);
+    if (!st && zp_kind == 2) st = stream_file_f32(*zero_points, (int64_t)N * w->nb, w->d_zpf);
+    return finish_create(w, st, out_handle);
+}
+
 int ms_hip_nbits_weights_create(const uint8_t* bq, int64_t bq_len, const float* scales, int64_t scales_len,
                                 const uint8_t* zero_points, int64_t zp_len, int N, int K, int bits,
                                 int block_size, void** out_handle)
@@ -2012,6 +2129,7 @@ namespace {
 int elementwise_grid(int64_t n) { return (int)std::min<int64_t>((n + 255) / 256, 8192); }
 
 bool misaligned4(const void* p) { return p && (reinterpret_cast<uintptr_t>(p) & 3); }
+bool misaligned16(const void* p) { return p && (reinterpret_cast<uintptr_t>(p) & 15); }
 
 }  // namespace
 
@@ -2028,8 +2146,9 @@ int ms_hip_rmsnorm(const float* dX, const float* dScale, float* dY, float* dInvS
     if (!dX || !dScale || !dY) return fail(MS_HIP_ERR_INVALID, "[ms_hip] rmsnorm: null input, scale or output");
     if (misaligned4(dX) || misaligned4(dScale) || misaligned4(dY) || misaligned4(dInvStd))
         return fail(MS_HIP_ERR_INVALID, "[ms_hip] rmsnorm: buffers must be 4-byte aligned");
+    const int vec = !misaligned16(dX) && !misaligned16(dScale) && !misaligned16(dY);
     hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(kNormThreads), 0, static_cast<hipStream_t>(stream),
-                       dX, dScale, dY, dInvStd, norm, eps);
+                       dX, dScale, dY, dInvStd, norm, eps, vec);
     MS_HIP_CHECK(hipGetLastError());
     return MS_HIP_OK;
 }
@@ -2049,9 +2168,13 @@ int ms_hip_skip_rmsnorm(const float* dInput, const float* dSkip, const float* dG
     for (const void* q : {(const void*)dInput, (const void*)dSkip, (const void*)dGamma, (const void*)dBeta,
                           (const void*)dBias, (const void*)dOut, (const void*)dSum, (const void*)dInvStd})
         if (misaligned4(q)) return fail(MS_HIP_ERR_INVALID, "[ms_hip] skip_rmsnorm: buffers must be 4-byte aligned");
+    int vec = 1;
+    for (const void* q : {(const void*)dInput, (const void*)dSkip, (const void*)dGamma, (const void*)dBeta,
+                          (const void*)dBias, (const void*)dOut, (const void*)dSum})
+        if (misaligned16(q)) vec = 0;
     hipLaunchKernelGGL(skip_rmsnorm_kernel, dim3((unsigned)rows), dim3(kNormThreads), 0,
                        static_cast<hipStream_t>(stream), dInput, dSkip, dGamma, dBeta, dBias, dOut, dSum, dInvStd,
-                       norm, eps);
+                       norm, eps, vec);
     MS_HIP_CHECK(hipGetLastError());
     return MS_HIP_OK;
 }
@@ -2104,6 +2227,60 @@ int ms_hip_mul(const float* dA, const float* dB, float* dY, int64_t n, void* str
     return MS_HIP_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+// How one GroupQueryAttention call runs: the lane-group kernel for head_dim 32/64/128/256
+// (with key splits when few units meet a long history and a workspace is given), else the
+// per-unit kernel; and the LDS each needs.
+struct GqaPlan {
+    int G = 0;          // lanes per row of gqa_rows_kernel<G>, 0: gqa_attention_kernel
+    int splits = 1;
+    size_t lds = 0;
+    int64_t ws_bytes = 0;
+};
+
+constexpr size_t kGqaMaxLds = 160 * 1024;
+
+GqaPlan gqa_plan(const ms_hip_gqa_desc& d, int64_t ws_avail)
+{
+    GqaPlan pl;
+    const int D = d.head_dim;
+    const int64_t total = (int64_t)d.past_seq + d.kv_seq;
+    const int64_t units = (int64_t)d.batch * d.num_heads * d.q_seq;
+    if (D == 32 || D == 64 || D == 128 || D == 256) {
+        pl.G = D / 4;
+        const int64_t fixed = D + (int64_t)(kGqaThreads / pl.G) * D + 1;
+        // Few units: split the keys so that each workgroup reads its rows in one pass of
+        // 4 * 256 / G rows (its loads in flight together), up to 4096 workgroups.
+        const int64_t pass = 4 * (int64_t)(kGqaThreads / pl.G);
+        int splits = 1;
+        if (units > 0 && units < 1024 && total > pass)
+            splits = (int)std::min<int64_t>({(int64_t)kGqaMaxSplits, (total + pass - 1) / pass,
+                                             std::max<int64_t>(1, 4096 / units)});
+        // a split's scores must fit in LDS
+        while (splits < kGqaMaxSplits && (fixed + (total + splits - 1) / splits) * 4 > (int64_t)kGqaMaxLds) ++splits;
+        const int64_t ws = splits > 1 ? units * splits * (D + 2) * (int64_t)sizeof(float) : 0;
+        if (ws_avail >= 0 && ws > ws_avail) splits = 1;   // no room: one split per unit
+        pl.splits = splits;
+        pl.ws_bytes = splits > 1 ? units * splits * (D + 2) * (int64_t)sizeof(float) : 0;
+        pl.lds = (size_t)(fixed + (total + splits - 1) / splits) * sizeof(float);
+    } else {
+        pl.lds = ((size_t)D + std::max(kGqaThreads, D) + (size_t)total) * sizeof(float);
+    }
+    return pl;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t ms_hip_gqa_workspace_size(const ms_hip_gqa_desc* d)
+{
+    return d ? gqa_plan(*d, -1).ws_bytes : 0;
+}
+
 int ms_hip_gqa_check(const ms_hip_gqa_desc* d)
 {
     // Messages of GroupQueryAttentionKernel.cs:69-76, :104-107, :136-145, :163-171.
@@ -2124,8 +2301,8 @@ int ms_hip_gqa_check(const ms_hip_gqa_desc* d)
     if (d->do_rotary && (d->cos_rows <= 0 || d->cos_cols <= 0))
         return fail(MS_HIP_ERR_INVALID,
                     "GroupQueryAttention do_rotary=1 requires cos_cache (input 7) and sin_cache (input 8).");
-    const int64_t lds = ((int64_t)d->head_dim + std::max(kGqaThreads, d->head_dim) + total) * (int64_t)sizeof(float);
-    if (lds > 160 * 1024)
+    const int64_t lds = (int64_t)gqa_plan(*d, -1).lds;
+    if (lds > (int64_t)kGqaMaxLds)
         return fail(MS_HIP_ERR_UNSUPPORTED,
                     "[ms_hip] GroupQueryAttention keeps a unit's scores in LDS: total sequence %lld with head_dim %d "
                     "exceeds 160 KiB",
@@ -2135,7 +2312,7 @@ int ms_hip_gqa_check(const ms_hip_gqa_desc* d)
 
 int ms_hip_gqa(const ms_hip_gqa_desc* d, const float* dQ, const float* dK, const float* dV, const float* dPastK,
                const float* dPastV, const int32_t* dSeqlensK, const float* dCos, const float* dSin, float* dOut,
-               float* dPresentK, float* dPresentV, void* stream)
+               float* dPresentK, float* dPresentV, void* dWorkspace, int64_t workspace_bytes, void* stream)
 {
     if (int st = gate()) return st;
     if (int st = ms_hip_gqa_check(d)) return st;
@@ -2203,12 +2380,39 @@ int ms_hip_gqa(const ms_hip_gqa_desc* d, const float* dQ, const float* dK, const
         MS_HIP_CHECK(hipGetLastError());
     }
     if (p.Sq > 0) {
-        const size_t lds = ((size_t)p.D + std::max(kGqaThreads, p.D) + p.total) * sizeof(float);
-        if (lds > 64 * 1024)
-            MS_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(gqa_attention_kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        hipLaunchKernelGGL(gqa_attention_kernel, dim3((unsigned)(p.B * p.H * p.Sq)), dim3(kGqaThreads), lds, s, p);
+        const GqaPlan pl = gqa_plan(*d, dWorkspace && !misaligned4(dWorkspace) ? workspace_bytes : 0);
+        if (pl.lds > kGqaMaxLds)
+            return fail(MS_HIP_ERR_UNSUPPORTED, "[ms_hip] GroupQueryAttention: history too long for one workgroup's "
+                                                "scores without a workspace (ms_hip_gqa_workspace_size)");
+        const void* fn = reinterpret_cast<const void*>(gqa_attention_kernel);
+        switch (pl.G) {
+            case 8: fn = reinterpret_cast<const void*>(gqa_rows_kernel<8>); break;
+            case 16: fn = reinterpret_cast<const void*>(gqa_rows_kernel<16>); break;
+            case 32: fn = reinterpret_cast<const void*>(gqa_rows_kernel<32>); break;
+            case 64: fn = reinterpret_cast<const void*>(gqa_rows_kernel<64>); break;
+            default: break;
+        }
+        if (pl.lds > 64 * 1024)
+            MS_HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pl.lds));
+        const unsigned units = (unsigned)(p.B * p.H * p.Sq);
+        float* ws = static_cast<float*>(dWorkspace);
+        switch (pl.G) {
+            case 8: hipLaunchKernelGGL(gqa_rows_kernel<8>, dim3(units * pl.splits), dim3(kGqaThreads), pl.lds, s, p, ws,
+                                       pl.splits); break;
+            case 16: hipLaunchKernelGGL(gqa_rows_kernel<16>, dim3(units * pl.splits), dim3(kGqaThreads), pl.lds, s, p,
+                                        ws, pl.splits); break;
+            case 32: hipLaunchKernelGGL(gqa_rows_kernel<32>, dim3(units * pl.splits), dim3(kGqaThreads), pl.lds, s, p,
+                                        ws, pl.splits); break;
+            case 64: hipLaunchKernelGGL(gqa_rows_kernel<64>, dim3(units * pl.splits), dim3(kGqaThreads), pl.lds, s, p,
+                                        ws, pl.splits); break;
+            default: hipLaunchKernelGGL(gqa_attention_kernel, dim3(units), dim3(kGqaThreads), pl.lds, s, p); break;
+        }
         MS_HIP_CHECK(hipGetLastError());
+        if (pl.splits > 1) {
+            hipLaunchKernelGGL(gqa_combine_kernel, dim3(units), dim3(std::min(256, ((p.D + 63) / 64) * 64)), 0, s, p,
+                               ws, pl.splits);
+            MS_HIP_CHECK(hipGetLastError());
+        }
     }
     return MS_HIP_OK;
 }

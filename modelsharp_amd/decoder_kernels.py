@@ -249,6 +249,7 @@ class HipGroupQueryAttentionKernel(IKernel):
     def __init__(self):
         self._dev = _DeviceInputs()
         self._caches: dict[str, _Cache] = {}
+        self._workspace: dict[str, object] = {}   # key-split workspace per node (ms_hip_gqa_workspace_size)
 
     def _cache_for(self, node, B, KH, D, past_k, total, device):
         torch = _torch()
@@ -347,9 +348,16 @@ class HipGroupQueryAttentionKernel(IKernel):
                            scale=_attr_float(node, "scale", 0.0),
                            seqlens_len=0 if seqlens is None else int(seqlens.numel()))
         out = torch.empty((B, Sq, H * D), dtype=torch.float32, device=q.device)
+        ws_bytes = native.gqa_workspace_size(d)
+        ws = None
+        if ws_bytes:
+            ws = self._workspace.get(node.name)
+            if ws is None or ws.numel() * 4 < ws_bytes:
+                ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=q.device)
+                self._workspace[node.name] = ws
         ptr = lambda t: None if t is None else t.data_ptr()   # noqa: E731
         native.gqa(d, q.data_ptr(), ptr(k), ptr(v), ptr(pk_src), ptr(pv_src), ptr(seqlens), ptr(cos), ptr(sin),
-                   out.data_ptr(), cache.k.data_ptr(), cache.v.data_ptr(), _stream(q))
+                   out.data_ptr(), cache.k.data_ptr(), cache.v.data_ptr(), ptr(ws), ws_bytes, _stream(q))
         ctx.set(node.outputs[0], out)
         if _present(node, 1):
             ctx.set(node.outputs[1], cache.k[:, :, :total, :])

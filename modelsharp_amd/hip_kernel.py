@@ -53,6 +53,7 @@ class HipMatMulNBitsKernel(IKernel):
         self._lock = threading.Lock()
         self._handles: dict[tuple, tuple] = {}
         self.w4a8 = w4a8_flag() if w4a8 is None else bool(w4a8)
+        self.file_uploads = 0   # handles streamed from file slices by preload()
 
     # ---- validation: MatMulNBitsKernel.cs:79-161 ----------------------------------------
     @staticmethod
@@ -115,8 +116,13 @@ class HipMatMulNBitsKernel(IKernel):
 
     def preload(self, graph: ModelGraph) -> int:
         """Load-time upload: one handle per MatMulNBits node whose B, scales and
-        zero points are initializers. Returns the number of handles created."""
+        zero points are initializers. Returns the number of handles created.
+
+        Initializers that a file-backed load located in their files (graph.sources,
+        onnx_loader.load_model) are streamed from disk straight into HBM
+        (ms_hip_nbits_weights_create_from_files); the others are uploaded from memory."""
         made = 0
+        sources = getattr(graph, "sources", {}) or {}
         ctx = GraphContext(graph.initializers)
         for node in graph.nodes:
             if node.op_type != self.op_type:
@@ -128,10 +134,29 @@ class HipMatMulNBitsKernel(IKernel):
             scales = ctx.get_tensor(node.inputs[2])
             zp = ctx.get_tensor(node.inputs[3]) if len(node.inputs) > 3 and ctx.has(node.inputs[3]) else None
             before = len(self._handles)
-            self._weights(node, b, scales, zp, node.attr_int("N", 0), node.attr_int("K", 0),
-                          node.attr_int("bits", 4), node.attr_int("block_size", 0))
+            names = [n for n in node.inputs[1:4] if n]
+            if all(n in sources for n in names):
+                self._weights_from_files(node, b, scales, zp, [sources[n] for n in node.inputs[1:3]]
+                                         + [sources[node.inputs[3]] if zp is not None else None])
+            else:
+                self._weights(node, b, scales, zp, node.attr_int("N", 0), node.attr_int("K", 0),
+                              node.attr_int("bits", 4), node.attr_int("block_size", 0))
             made += len(self._handles) - before
         return made
+
+    def _weights_from_files(self, node, b, scales, zp, slices) -> None:
+        key = tuple(node.inputs[1:4])
+        with self._lock:
+            entry = self._handles.get(key)
+            if entry is not None and entry[0][0] is b and entry[0][1] is scales and entry[0][2] is zp:
+                return
+            w = native.NBitsWeights.from_files(slices[0], slices[1], slices[2], node.attr_int("N", 0),
+                                               node.attr_int("K", 0), node.attr_int("bits", 4),
+                                               node.attr_int("block_size", 0))
+            if entry is not None:
+                entry[1].close()
+            self._handles[key] = ((b, scales, zp), w)
+            self.file_uploads += 1
 
     def close(self) -> None:
         with self._lock:

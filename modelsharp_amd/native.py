@@ -72,7 +72,10 @@ _PROTOTYPES = {
     "ms_hip_sigmoid": (_c_int, [_vp, _vp, _c_i64, _vp]),
     "ms_hip_mul": (_c_int, [_vp, _vp, _vp, _c_i64, _vp]),
     "ms_hip_gqa_check": (_c_int, [_vp]),
-    "ms_hip_gqa": (_c_int, [_vp] * 13),
+    "ms_hip_gqa": (_c_int, [_vp] * 13 + [_c_i64, _vp]),
+    "ms_hip_gqa_workspace_size": (_c_i64, [_vp]),
+    "ms_hip_nbits_weights_create_from_files": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
+                                                        ctypes.POINTER(_vp)]),
     "ms_hip_debug_force_failure": (_c_int, [_c_int]),
     "ms_hip_nbits_gemm_dev_f16": (_c_int, [_vp, _vp, _vp, _c_int, _vp]),
     "ms_hip_nbits_device_error": (_c_int, [_vp]),
@@ -166,6 +169,12 @@ def _ptr(arr):
     return None if arr is None else arr.ctypes.data_as(_vp)
 
 
+class FileSlice(ctypes.Structure):
+    """ms_hip_file_slice."""
+    _fields_ = [("path", ctypes.c_char_p), ("offset", ctypes.c_int64), ("length", ctypes.c_int64),
+                ("dtype", ctypes.c_int)]
+
+
 class NBitsWeights:
     """A device-resident MatMulNBits weight (B, scales, packed zero points).
 
@@ -206,6 +215,27 @@ class NBitsWeights:
                                                   N, K, bits, block_size, ctypes.byref(handle)))
         self = cls.__new__(cls)
         self._init(handle, N, K, bits, block_size, bool(d_zp))
+        return self
+
+    @classmethod
+    def from_files(cls, b, scales, zero_points, N: int, K: int, bits: int = 4, block_size: int = 32):
+        """Weights streamed from file slices (FileSlice-like: path, offset, length in bytes,
+        data_type as the ONNX TensorProto code) straight into device memory
+        (ms_hip_nbits_weights_create_from_files)."""
+        onnx_to_ms = {2: MS_HIP_DTYPE_U8, 1: MS_HIP_DTYPE_F32, 10: MS_HIP_DTYPE_F16}
+
+        def sl(x):
+            if x is None:
+                return None
+            return FileSlice(x.path.encode(), int(x.offset), int(x.length), onnx_to_ms.get(int(x.data_type), -1))
+
+        self = cls.__new__(cls)
+        slices = [sl(b), sl(scales), sl(zero_points)]
+        handle = _vp()
+        check(load().ms_hip_nbits_weights_create_from_files(
+            ctypes.byref(slices[0]), ctypes.byref(slices[1]), None if slices[2] is None else ctypes.byref(slices[2]),
+            int(N), int(K), int(bits), int(block_size), ctypes.byref(handle)))
+        self._init(handle, N, K, bits, block_size, zero_points is not None)
         return self
 
     def _init(self, handle, N, K, bits, block_size, has_zp):
@@ -378,6 +408,12 @@ def mul(dA, dB, dY, n, stream=None):
     check(load().ms_hip_mul(_d(dA), _d(dB), _d(dY), int(n), _d(stream)))
 
 
-def gqa(desc: GqaDesc, dQ, dK, dV, dPastK, dPastV, dSeqlens, dCos, dSin, dOut, dPresentK, dPresentV, stream=None):
+def gqa_workspace_size(desc: GqaDesc) -> int:
+    return int(load().ms_hip_gqa_workspace_size(ctypes.byref(desc)))
+
+
+def gqa(desc: GqaDesc, dQ, dK, dV, dPastK, dPastV, dSeqlens, dCos, dSin, dOut, dPresentK, dPresentV,
+        dWorkspace=None, workspace_bytes=0, stream=None):
     check(load().ms_hip_gqa(ctypes.byref(desc), _d(dQ), _d(dK), _d(dV), _d(dPastK), _d(dPastV), _d(dSeqlens),
-                            _d(dCos), _d(dSin), _d(dOut), _d(dPresentK), _d(dPresentV), _d(stream)))
+                            _d(dCos), _d(dSin), _d(dOut), _d(dPresentK), _d(dPresentV), _d(dWorkspace),
+                            int(workspace_bytes), _d(stream)))

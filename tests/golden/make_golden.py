@@ -22,6 +22,11 @@ ref_w4a8_vectors.npz
     (native/test/qgemm_w4a8_test.cpp:140-166: M in {1, 8}, bits 4 sym/asym and 8
     sym/asym, block size 32/128, and its three odd shapes).
 
+onnx/
+    The reference's own ONNX test assets (tests/ModelSharp.Tests/assets:
+    test_matmul_{2d,3d,4d}/ with their test_data_set_0 tensors, and mnist-12.onnx),
+    copied as data for the loader tests; read only by the repository's own parser.
+
 Run in the container that holds the reference checkout:
     python tests/golden/make_golden.py
 """

@@ -104,12 +104,14 @@ def test_elementwise(gpu):
 from test_oracle_decoder import GQA_CASES, make_case   # noqa: E402
 
 
-def run_device_gqa(d, q, k, v, pk, pv, sl, cos, sin, capacity=None):
+def run_device_gqa(d, q, k, v, pk, pv, sl, cos, sin, capacity=None, workspace=False):
     import torch
     total = d.past_seq + d.kv_seq
     cap = capacity or total
     nd = native.GqaDesc(**{f: getattr(d, f) for f, _ in d._fields_})
     nd.present_capacity = cap
+    ws_bytes = native.gqa_workspace_size(nd) if workspace else 0
+    ws = torch.empty(max(1, ws_bytes // 4), device="cuda") if ws_bytes else None
     PK = torch.zeros((d.batch, d.kv_num_heads, cap, d.head_dim), device="cuda")
     PV = torch.zeros_like(PK)
     out = torch.empty((d.batch, d.q_seq, d.num_heads * d.head_dim), device="cuda")
@@ -117,7 +119,7 @@ def run_device_gqa(d, q, k, v, pk, pv, sl, cos, sin, capacity=None):
                                                                 sin=sin).items()}
     ptr = lambda x: None if x is None else x.data_ptr()   # noqa: E731
     native.gqa(nd, ptr(t["q"]), ptr(t["k"]), ptr(t["v"]), ptr(t["pk"]), ptr(t["pv"]), ptr(t["sl"]), ptr(t["cos"]),
-               ptr(t["sin"]), out.data_ptr(), PK.data_ptr(), PV.data_ptr())
+               ptr(t["sin"]), out.data_ptr(), PK.data_ptr(), PV.data_ptr(), ptr(ws), ws_bytes)
     return host(out), host(PK)[:, :, :total], host(PV)[:, :, :total]
 
 
@@ -137,12 +139,27 @@ def test_gqa_cases(gpu, case):
               ref, rk, rv, f"seed {case['seed']}")
 
 
+@pytest.mark.parametrize("workspace", [False, True], ids=["one_split", "key_splits"])
 @pytest.mark.parametrize("Sq,past,KH", [(1, 2047, 8), (1, 4095, 32), (128, 0, 8), (16, 300, 8)])
-def test_gqa_7b_shapes(gpu, Sq, past, KH):
+def test_gqa_7b_shapes(gpu, Sq, past, KH, workspace):
     d, q, k, v, pk, pv, sl, cos, sin = make_case(20 + Sq, B=1, Sq=Sq, H=32, KH=KH, D=128, past=past, packed=True,
                                                  cos_rows=4096 + 128)
     ref, rk, rv = oracle.gqa(d, q, k, v, pk, pv, sl, cos, sin)
-    check_gqa(*run_device_gqa(d, q, k, v, pk, pv, sl, cos, sin), ref, rk, rv, f"7B Sq={Sq} past={past} KH={KH}")
+    check_gqa(*run_device_gqa(d, q, k, v, pk, pv, sl, cos, sin, workspace=workspace), ref, rk, rv,
+              f"7B Sq={Sq} past={past} KH={KH} workspace={workspace}")
+
+
+@pytest.mark.parametrize("D", [32, 64, 256, 40])
+def test_gqa_head_dims_and_long_history(gpu, D):
+    """Every lane-group width, the per-unit kernel (head_dim 40), and a history longer than
+    one workgroup's LDS holds (key splits required)."""
+    past = 60000 if D == 64 else 700
+    d, q, k, v, pk, pv, sl, cos, sin = make_case(40 + D, B=1, Sq=1, H=4, KH=2, D=D, past=past, packed=False,
+                                                 cos_rows=past + 8)
+    ref, rk, rv = oracle.gqa(d, q, k, v, pk, pv, sl, cos, sin)
+    check_gqa(*run_device_gqa(d, q, k, v, pk, pv, sl, cos, sin, workspace=True), ref, rk, rv, f"D={D} past={past}")
+    if D != 64:
+        check_gqa(*run_device_gqa(d, q, k, v, pk, pv, sl, cos, sin), ref, rk, rv, f"D={D} unsplit")
 
 
 def test_gqa_resident_cache_appends_in_place(gpu):

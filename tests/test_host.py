@@ -368,4 +368,8 @@ def test_gqa_descriptor_checks():
     d.do_rotary = 0
     assert lib.ms_hip_gqa_check(ctypes.byref(d)) == 0
     d.past_seq, d.present_capacity = 50000, 50002
+    # head_dim 64: the keys split over workgroups, given the workspace it asks for
+    assert lib.ms_hip_gqa_check(ctypes.byref(d)) == 0
+    assert native.gqa_workspace_size(d) == 2 * 4 * 64 * (64 + 2) * 4   # units x splits x (D + 2) floats
+    d.head_dim = 40   # the per-unit kernel keeps every score of a unit in LDS
     assert lib.ms_hip_gqa_check(ctypes.byref(d)) == native.MS_HIP_ERR_UNSUPPORTED
