@@ -256,7 +256,10 @@ int ms_hip_sync(void);
  *   8 polls of the pipelined prefill's split-K flag before the second half of a
  *     tile gives up (0: about 4 million);
  *   9 the register-operand prefill's weight fragments per wave (1, 2 or 4: tiles of
- *     128 x 64, 128 x 128 or 128 x 256 outputs).
+ *     128 x 64, 128 x 128 or 128 x 256 outputs);
+ *  10 the host-pointer entries' staging, value - 1 as bits: bit 0 copies A to the
+ *     device with a kernel reading the pinned host buffer (else a DMA copy), bit 1
+ *     has the GEMM store Y straight into pinned host memory (else a DMA copy back).
  * ms_hip_nbits_debug_set_counters sets the arrival tag of every split tile of the
  *   handle's pipelined-prefill counters to `value` (or to the tag the next split-K
  *   launch will carry, when next_epoch_tag != 0) and clears their ready flags: it
