@@ -345,9 +345,8 @@ def main() -> int:
     dom = groups["gate_up"]
     gate = next(op for op in ops if op.name == "gate")   # the CPU baseline's sample
 
-    # host-pointer entry (ms_hip_nbits_gemm): A through the handle's pinned staging and a
-    # DMA copy, the kernel storing Y straight into pinned host memory, synchronous;
-    # rotating over the weight copies. Reported, never `value`.
+    # host-pointer entry (ms_hip_nbits_gemm): A and Y through the handle's pinned staging
+    # and DMA copies, synchronous; rotating over the weight copies. Reported, never `value`.
     gi = ops.index(gate)
     a_host = workloads.make_activations(1, gate.K, 99)
     for r in range(copies):
@@ -359,8 +358,8 @@ def main() -> int:
     host_us = (time.perf_counter() - t0) / calls * 1e6
     host = {"op": "gate", "K": gate.K, "N": gate.N, "M": 1, "us_per_call": round(host_us, 2),
             "GBs": round(workloads.algorithmic_bytes(gate, 1) / (host_us * 1e-6) / 1e9, 1),
-            "path": "ms_hip_nbits_gemm: host A -> pinned staging -> H2D copy, kernel storing Y into pinned "
-                    "host memory -> host Y, synchronous"}
+            "path": "ms_hip_nbits_gemm: host A -> pinned staging -> H2D, kernel, D2H -> pinned -> host Y, "
+                    "synchronous"}
     log(f"  host-pointer gate call: {host_us:.2f} us ({host['GBs']} GB/s, PCIe copies included)")
     traffic = measured_traffic(dom["kernel"])
     rot.close()
