@@ -126,14 +126,19 @@ def time_graph(g, replays, warmup, warm_ms=WARM_MS):
 TRAFFIC_PROFILE = "profiles/gemv_w4_gate_up_7b_hbm_traffic.json"
 
 
+# The device sources of the roofline kernel (gemv_w4): a traffic profile is used only
+# for the code it measured (its launch shape is checked separately).
+GEMV_SOURCES = ("gemv_w4.h", "nbits_device.h")
+
+
 def kernel_source_digest() -> str:
-    """sha256 over the device sources, so a profile is used only for the code it measured."""
+    """sha256 over the roofline kernel's device sources."""
     import hashlib
     h = hashlib.sha256()
-    for f in sorted((ROOT / "modelsharp_amd" / "csrc").glob("*")):
-        if f.suffix in (".h", ".hip"):
-            h.update(f.name.encode())
-            h.update(f.read_bytes())
+    for name in GEMV_SOURCES:
+        f = ROOT / "modelsharp_amd" / "csrc" / name
+        h.update(name.encode())
+        h.update(f.read_bytes())
     return h.hexdigest()[:16]
 
 
