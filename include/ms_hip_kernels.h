@@ -259,7 +259,9 @@ int ms_hip_sync(void);
  *     128 x 64, 128 x 128 or 128 x 256 outputs);
  *  10 the host-pointer entries' staging, value - 1 as bits: bit 0 copies A to the
  *     device with a kernel reading the pinned host buffer (else a DMA copy), bit 1
- *     has the GEMM store Y straight into pinned host memory (else a DMA copy back).
+ *     has the GEMM store Y straight into pinned host memory (else a DMA copy back);
+ *  11 the 8-bit GEMV's launch configuration: c+1 forces configuration c (0..8) of the
+ *     library's table, -1 keeps 8-bit calls on gemv_general.
  * ms_hip_nbits_debug_set_counters sets the arrival tag of every split tile of the
  *   handle's pipelined-prefill counters to `value` (or to the tag the next split-K
  *   launch will carry, when next_epoch_tag != 0) and clears their ready flags: it
@@ -267,7 +269,8 @@ int ms_hip_sync(void);
  *   every kernel still exiting normally.
  * ms_hip_nbits_launch_info reports what a call with M rows would launch:
  *   kernel_id 0 generic, 1 gemv_w4, 2 mfma_w4, 3 gemv_w4_panel, 4 mfma_w4_pipe,
- *   5 skinny_w4, 6 mfma_w4_rb, 7 gemv_general, 8 mfma_general; lanes_per_row is the
+ *   5 skinny_w4, 6 mfma_w4_rb, 7 gemv_general, 8 mfma_general, 12 gemv_w8 (9-11 are
+ *   the W4A8 kernels of ms_hip_nbits_launch_info_w4a8); lanes_per_row is the
  *   lanes per weight row of the
  *   GEMV kernels, the output tile width of mfma_w4_rb, 0 otherwise. */
 /* ms_hip_nbits_batch_launch_info: what the first launch of a batch call with these

@@ -10,6 +10,8 @@
 //       few output tiles or block_size != 32                  -> a_rows_f16 + mfma_w4_rb
 //       otherwise (block_size 32)                             -> a_rows_f16 + mfma_w4_pipe
 //     M >  16 otherwise                                       -> mfma_w4 (exact, no workspace)
+//   bits=8, packed or no zero points, power-of-two block size >= 16, K % 16 == 0:
+//     M <= 4, A panel fits LDS                                -> gemv_w8
 //   other formats (bits 8, float zero points, other block sizes or K), K and the block
 //   size multiples of 8:
 //     M <= 16                                                 -> gemv_general
@@ -42,6 +44,7 @@
 #include <unistd.h>
 
 #include "gemv_general.h"
+#include "gemv_w8.h"
 #include "gemv_w4.h"
 #include "gemv_w4_panel.h"
 #include "generic_nbits.h"
@@ -164,7 +167,8 @@ int require_device()
 //   4 skinny_w4: 1 off, 2 every eligible M   9 mfma_w4_rb fragments per wave (1, 2, 4)
 //  10 host-pointer staging: bit 0 A by kernel, bit 1 Y straight to pinned host memory
 //     (value + 1; 0 = the default for the call's size)
-constexpr int kNumKnobs = 11;
+//  11 gemv_w8 configuration (c+1; -1 keeps 8-bit calls on gemv_general)
+constexpr int kNumKnobs = 12;
 constexpr int kDefaultSpinLimit = 1 << 22;
 std::atomic<int> g_knob[kNumKnobs];   // zero-initialised (static storage)
 
@@ -181,6 +185,7 @@ struct Knobs {
     int spin_limit() const { return v[8] > 0 ? v[8] : kDefaultSpinLimit; }
     int rb_nf() const { return v[9]; }
     int host_staging() const { return v[10]; }
+    int gemv8_config() const { return v[11]; }
 };
 
 int validate_knob(int knob, int value)
@@ -198,6 +203,7 @@ int validate_knob(int knob, int value)
         case 8: ok = value >= 0; break;
         case 9: ok = value == 0 || value == 1 || value == 2 || value == 4; break;
         case 10: ok = value >= 0 && value <= 4; break;
+        case 11: ok = value >= -1 && value <= kNumGemv8Configs; break;
         default: break;
     }
     return ok ? MS_HIP_OK : fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid tuning knob %d = %d", knob, value);
@@ -756,6 +762,96 @@ int launch_gemv_general(const Weights& w, const float* dA, float* dY, int M, hip
     return MS_HIP_OK;
 }
 
+// ---- gemv_w8: 8-bit decode GEMV ------------------------------------------------------------
+// Instantiations [M-1][config][panel slot]: slot 0 stages the activations through
+// registers (up to kGemv8Av float4 per thread), slot 1 in a loop.
+typedef void (*Gemv8Fn)(Gemv8Params);
+template <int M, size_t I>
+constexpr std::array<Gemv8Fn, 2> gemv8_pair()
+{
+    constexpr Gemv8Config c = kGemv8Configs[I];
+    constexpr int av = kGemv8Av * 4 / c.waves;   // the same panel bytes per workgroup
+    return {gemv_w8_kernel<M, c.waves, c.G, c.KW, c.U, c.RL, av>, gemv_w8_kernel<M, c.waves, c.G, c.KW, c.U, c.RL, 0>};
+}
+template <int M, size_t... I>
+constexpr std::array<std::array<Gemv8Fn, 2>, sizeof...(I)> gemv8_row(std::index_sequence<I...>)
+{
+    return {gemv8_pair<M, I>()...};
+}
+template <int M>
+constexpr std::array<std::array<Gemv8Fn, 2>, kNumGemv8Configs> gemv8_row()
+{
+    return gemv8_row<M>(std::make_index_sequence<kNumGemv8Configs>{});
+}
+const std::array<std::array<Gemv8Fn, 2>, kNumGemv8Configs> kGemv8Table[kGemvMaxM] = {
+    gemv8_row<1>(), gemv8_row<2>(), gemv8_row<3>(), gemv8_row<4>(),
+};
+std::atomic<bool> g_gemv8_lds_raised[kGemvMaxM][kNumGemv8Configs][2];
+
+int log2_exact(int v)
+{
+    int l = 0;
+    while ((1 << l) < v) ++l;
+    return (1 << l) == v ? l : -1;
+}
+
+// gemv_w8 takes 8-bit codes with packed or default zero points, M <= 4, a power-of-two
+// block size >= 16, K a multiple of 16, an activation panel that fits LDS, and buffers
+// within 32-bit offsets.
+bool gemv8_eligible(const Weights& w, int M)
+{
+    return w.bits == 8 && !w.zp_float && M >= 1 && M <= kGemvMaxM && (w.K % 16) == 0 && w.bs >= 16 &&
+           log2_exact(w.bs) >= 0 && (int64_t)M * w.K * 4 <= kGemv8MaxLds &&
+           (int64_t)w.N * w.row_bytes <= INT32_MAX && (int64_t)w.N * w.nb * 4 <= INT32_MAX;
+}
+
+// Config choice (knob 11: c + 1 forces configuration c, -1 keeps 8-bit calls on
+// gemv_general). From sweeping every config over 7B-shaped launches (K x N = 4096 x
+// 4096, 4096 x 11008, 11008 x 4096, 4096 x 12288, 4096 x 32000, block sizes 32 and 128)
+// and 896 x 896 at M = 1, 2, 4 on MI355X: 8 waves at 64 lanes per row for M <= 2 (gate
+// 4096 x 11008 at M = 1: 12.4 us against 13.2-18.1 for the others), 16 waves for M >= 3
+// and for K >= 8192 (gate at M = 4: 20.9 us against 21.0-39.2; 11008 x 4096 at M = 2:
+// 16.4 us against 21.3 with 8 waves), 4 waves below 2048 rows (fewer, fuller
+// workgroups; 3.4 us for 896 x 896 at M = 1).
+int pick_gemv8_config(const Weights& w, const Knobs& kn, int M)
+{
+    if (!gemv8_eligible(w, M) || kn.gemv8_config() < 0) return -1;
+    if (kn.gemv8_config() > 0) return kn.gemv8_config() - 1;
+    if (w.N < 2048) return 7;
+    return M >= 3 || w.K >= 8192 ? 3 : 0;
+}
+
+int gemv8_grid(const Weights& w, int ci) { return (w.N + gemv8_rows(kGemv8Configs[ci]) - 1) / gemv8_rows(kGemv8Configs[ci]); }
+
+int launch_gemv_w8(const Weights& w, const Knobs& kn, const float* dA, float* dY, int M, hipStream_t stream)
+{
+    const int ci = pick_gemv8_config(w, kn, M);
+    const int slot = (int64_t)M * w.K / 4 <= 256 * kGemv8Av ? 0 : 1;
+    Gemv8Fn fn = kGemv8Table[M - 1][ci][slot];
+    const size_t lds = (size_t)M * w.K * 4;
+    if (lds > 64 * 1024 && !g_gemv8_lds_raised[M - 1][ci][slot].load()) {
+        MS_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        g_gemv8_lds_raised[M - 1][ci][slot].store(true);
+    }
+    Gemv8Params p;
+    p.b = w.d_b;
+    p.scales = w.d_scales;
+    p.zp = w.has_zp ? w.d_zp : nullptr;
+    p.a = dA;
+    p.y = dY;
+    p.N = w.N;
+    p.K = w.K;
+    p.C = w.K / 16;
+    p.row_bytes = (int)w.row_bytes;
+    p.nb = w.nb;
+    p.zrb = w.zrb;
+    p.lcpb = log2_exact(w.bs / 16);
+    hipLaunchKernelGGL(fn, dim3(gemv8_grid(w, ci)), dim3(kGemv8Configs[ci].waves * kWave), lds, stream, p);
+    MS_HIP_CHECK(hipGetLastError());
+    return MS_HIP_OK;
+}
+
 int launch_mfma_general(const Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
 {
     GenParams p;
@@ -1099,12 +1195,13 @@ int launch_rb(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, float*
 // Which kernel a call with M rows takes (ids of ms_hip_nbits_launch_info).
 enum KernelId {
     kGeneric = 0, kGemv = 1, kMfma = 2, kPanel = 3, kPipe = 4, kSkinny = 5, kRb = 6, kGemvGeneral = 7,
-    kMfmaGeneral = 8
+    kMfmaGeneral = 8, kGemvW8 = 12
 };
 
 KernelId choose_kernel(const Weights& w, const Knobs& kn, int M)
 {
     if (!w.fast) {
+        if (pick_gemv8_config(w, kn, M) >= 0) return kGemvW8;
         if (!general_eligible(w)) return kGeneric;
         return M <= kPanelMaxM ? kGemvGeneral : kMfmaGeneral;
     }
@@ -1149,6 +1246,7 @@ int launch_kernel(Weights& w, const Knobs& kn, KernelId k, const Ws& ws, const f
         case kGeneric: return launch_generic(w, dA, dY, M, stream);
         case kGemvGeneral: return launch_gemv_general(w, dA, dY, M, stream);
         case kMfmaGeneral: return launch_mfma_general(w, dA, dY, M, stream);
+        case kGemvW8: return launch_gemv_w8(w, kn, dA, dY, M, stream);
         case kGemv:
         case kPanel: return launch_gemv(w, kn, dA, dY, M, stream);
         case kSkinny: return launch_skinny(w, kn, ws, dA, dY, M, stream);
@@ -2109,6 +2207,13 @@ int ms_hip_nbits_launch_info(void* handle, int M, int* kernel_id, int* lanes_per
     switch (kid) {
         case kGeneric: gr = (int)(((int64_t)M * w->N + 255) / 256); break;
         case kGemvGeneral: gr = (w->N + kGenRowsPerWg - 1) / kGenRowsPerWg; G = 16; break;
+        case kGemvW8: {
+            const int ci = pick_gemv8_config(*w, kn, M);
+            G = kGemv8Configs[ci].G;
+            gr = gemv8_grid(*w, ci);
+            bl = kGemv8Configs[ci].waves * kWave;
+            break;
+        }
         case kMfmaGeneral:
             gr = ((M + kGenBM - 1) / kGenBM) * ((w->N + kGenBN - 1) / kGenBN);
             gr = ((gr + kXcds - 1) / kXcds) * kXcds;

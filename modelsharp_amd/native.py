@@ -20,7 +20,7 @@ _PKG = pathlib.Path(__file__).resolve().parent
 LIB_NAME = "libms_hip_nbits.so"
 # Kernel ids of ms_hip_nbits_launch_info.
 KERNEL_NAMES = ("generic", "gemv_w4", "mfma_w4", "gemv_w4_panel", "mfma_w4_pipe", "skinny_w4", "mfma_w4_rb",
-                "gemv_general", "mfma_general", "gemv_w4a8", "mfma_w4a8", "w4a8_generic")
+                "gemv_general", "mfma_general", "gemv_w4a8", "mfma_w4a8", "w4a8_generic", "gemv_w8")
 HEADER = _PKG.parent / "include" / "ms_hip_kernels.h"
 
 MS_HIP_OK = 0

@@ -4,6 +4,9 @@ oracle (the managed kernel's arithmetic, MatMulNBitsKernel.cs:193-262):
 * 8-bit codes (MatMulNBitsSimd.cs:117-132), float zero points
   (MatMulNBitsKernel.cs:239-240), block sizes other than 32/64/128/256, K not a
   multiple of 32 — the general GEMV (M <= 16) and the general MFMA GEMM (M > 16);
+* the 8-bit decode GEMV (packed or default zero points, power-of-two block sizes
+  >= 16, K % 16 == 0, M <= 4): every launch configuration, the K % block-size tail,
+  blocks longer than one step, activation panels above 64 KiB of LDS;
 * Float16 scales, zero points and activations, widened exactly on the device as
   GraphContext.Get widens them on the host (GraphContext.cs:106): the results equal
   those of the same values handed over as Float32, bit for bit.
@@ -53,6 +56,15 @@ def assert_within(y, ref, allowed, what):
     assert np.all(err <= allowed), f"{what}: err/bound {ratio:.3e}"
 
 
+def expected_kernel(op: Op, M: int, float_zp: bool = False) -> str:
+    """The kernel the dispatch rules give a call with M rows."""
+    pow2 = op.block_size >= 16 and (op.block_size & (op.block_size - 1)) == 0
+    if (op.bits == 8 and not float_zp and pow2 and op.K % 16 == 0 and M <= 4
+            and M * op.K * 4 <= 159 * 1024):
+        return "gemv_w8"
+    return "gemv_general" if M <= 16 else "mfma_general"
+
+
 def check_against_oracle(w, a, b, s, zp, zpf, op, what):
     M = a.shape[0]
     kernel = w.launch_info(M)["kernel"]
@@ -89,7 +101,7 @@ def test_general_formats(gpu, op, M):
     w = native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
     log(f"general {op.name} M={M} {w.launch_info(M)}")
     kernel, W = check_against_oracle(w, a, b, s, z, None, op, f"{op.name} M={M}")
-    assert kernel == ("gemv_general" if M <= 16 else "mfma_general")
+    assert kernel == expected_kernel(op, M)
     assert np.array_equal(w.dequant(), W)
     w.close()
 
@@ -111,7 +123,7 @@ def test_float_zero_points(gpu, op, M):
     w = native.NBitsWeights(b, s, zpf, op.N, op.K, op.bits, op.block_size)
     log(f"float zp {op.name} M={M} {w.launch_info(M)}")
     kernel, W = check_against_oracle(w, a, b, s, None, zpf, op, f"{op.name} M={M}")
-    assert kernel == ("gemv_general" if M <= 16 else "mfma_general")
+    assert kernel == expected_kernel(op, M, float_zp=True)
     assert np.array_equal(w.dequant(), W)
     w.close()
 
@@ -129,7 +141,72 @@ def test_general_mfma_full_size_8bit(gpu):
     assert np.array_equal(y1, w.gemm(a))   # deterministic
     a1 = a[:1]
     kernel, _ = check_against_oracle(w, a1, b, s, z, None, op, "b8 K=4096 N=4096 M=1")
-    assert kernel == "gemv_general"
+    assert kernel == "gemv_w8"
+    w.close()
+
+
+# ---- 8-bit decode GEMV ---------------------------------------------------------------------
+W8_OPS = [
+    Op("w8_gate_7b", 4096, 11008, 32, True, bits=8),     # 7B gate/up projection
+    Op("w8_down_7b", 11008, 4096, 32, True, bits=8),     # panel staged in a loop (K = 11008)
+    Op("w8_sym_bs16", 1024, 300, 16, False, bits=8),     # default zero point 128
+    Op("w8_bs64_tail", 1040, 77, 64, True, bits=8),      # 17 blocks, the last of 16 codes
+    Op("w8_bs512", 2048, 130, 512, True, bits=8),        # a block spans several steps
+    Op("w8_k16", 16, 40, 16, True, bits=8),              # one chunk per row
+    Op("w8_k8192", 8192, 96, 128, True, bits=8),         # M = 3, 4: 96 / 128 KiB of LDS
+]
+
+
+@pytest.mark.parametrize("op", W8_OPS, ids=lambda o: o.name)
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_gemv_w8(gpu, op, M):
+    b, s, z = workloads.make_weights(op, seed=op.K + 7 * op.N + M)
+    a = workloads.make_activations(M, op.K, seed=5 * M + op.K, kind="rmsnorm")
+    w = native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
+    log(f"gemv_w8 {op.name} M={M} {w.launch_info(M)}")
+    kernel, _ = check_against_oracle(w, a, b, s, z, None, op, f"{op.name} M={M}")
+    assert kernel == expected_kernel(op, M)
+    y = w.gemm(a)
+    assert np.array_equal(y, w.gemm(a))   # deterministic
+    w.close()
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_gemv_w8_every_config(gpu, M):
+    """Every launch configuration of the 8-bit GEMV (forced through tuning knob 11) on a
+    shape whose rows do not fill the last workgroup; knob value -1 keeps the call on the
+    general GEMV."""
+    op = Op("w8_cfg", 2560, 1000, 64, True, bits=8)
+    b, s, z = workloads.make_weights(op, seed=31 + M)
+    a = workloads.make_activations(M, op.K, seed=32 + M)
+    w = native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
+    try:
+        for cfg in range(1, 10):
+            w.set_tuning(11, cfg)
+            info = w.launch_info(M)
+            log(f"gemv_w8 config {cfg - 1} M={M} {info}")
+            assert info["kernel"] == "gemv_w8"
+            check_against_oracle(w, a, b, s, z, None, op, f"config {cfg - 1} M={M}")
+        w.set_tuning(11, -1)
+        assert w.launch_info(M)["kernel"] == "gemv_general"
+        check_against_oracle(w, a, b, s, z, None, op, f"knob -1 M={M}")
+    finally:
+        w.set_tuning(11, 0)
+    w.close()
+
+
+def test_gemv_w8_extreme_codes(gpu):
+    """Codes and zero points at 0 and 255 (q - zp = +-255, the widest difference)."""
+    op = Op("w8_ext", 512, 64, 32, True, bits=8)
+    rng = np.random.Generator(np.random.PCG64(77))
+    b = rng.choice(np.array([0, 255], dtype=np.uint8), size=(op.N, op.nb, op.blob))
+    z = rng.choice(np.array([0, 255], dtype=np.uint8), size=(op.N, op.zrb))
+    s = rng.uniform(op.scale_lo, op.scale_hi, size=op.N * op.nb).astype(np.float32)
+    w = native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
+    for M in (1, 4):
+        a = workloads.make_activations(M, op.K, seed=M)
+        kernel, _ = check_against_oracle(w, a, b, s, z, None, op, f"extreme codes M={M}")
+        assert kernel == "gemv_w8"
     w.close()
 
 

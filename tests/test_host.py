@@ -220,6 +220,10 @@ def test_tuning_knobs_validated_without_a_device():
     assert "invalid tuning knob" in native.last_error()
     assert lib.ms_hip_set_tuning(1, 10_000) == native.MS_HIP_ERR_INVALID
     assert lib.ms_hip_set_tuning(3, 0) == native.MS_HIP_OK
+    assert lib.ms_hip_set_tuning(11, 10) == native.MS_HIP_ERR_INVALID   # 9 gemv_w8 configurations
+    assert lib.ms_hip_set_tuning(11, -2) == native.MS_HIP_ERR_INVALID
+    assert lib.ms_hip_set_tuning(12, 0) == native.MS_HIP_ERR_INVALID
+    assert lib.ms_hip_set_tuning(11, 0) == native.MS_HIP_OK
     bogus = ctypes.c_void_p(0x1234560)
     assert lib.ms_hip_nbits_set_tuning(bogus, 0, 0) == native.MS_HIP_ERR_INVALID
     assert "invalid weights handle" in native.last_error()
