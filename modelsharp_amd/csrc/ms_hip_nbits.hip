@@ -519,8 +519,9 @@ bool gemv_config_fits(const Weights& w, int M, const GemvConfig& c)
 // row win from 16K rows up, 64 lanes per row with two rows per lane from 2K to 16K rows
 // (re-swept with the non-temporal code loads: 7B o at M = 1 / 2 5.41 -> 5.26 /
 // 6.83 -> 6.54 us against the 32-lane pick), 32 lanes per row below; for M = 3-4 the
-// 8-wave configs. N is the launch's total rows (summed over a group). Indices are into
-// kGemvConfigs.
+// 8-wave configs. From 2K to 4K rows at M <= 2, 8 waves of 64 lanes per row with two rows
+// per lane (7B q / o, 3584 x 3584: M = 1 / 2 5.27 -> 5.14 / 6.62 -> 6.12 us). N is the
+// launch's total rows (summed over a group). Indices are into kGemvConfigs.
 int pick_gemv_config(const Weights& w, const Knobs& kn, int M, int N)
 {
     if (kn.gemv_config() < 0) return -1;
@@ -530,7 +531,7 @@ int pick_gemv_config(const Weights& w, const Knobs& kn, int M, int N)
     }
     static constexpr int kLargeM2[] = {16, 11, 0, 6};   // M <= 2, N >= 16384
     static constexpr int kMidM2[] = {14, 11, 2};        // M <= 2, N >= 4096
-    static constexpr int kSmallM2[] = {14, 13, 6, 8};   // M <= 2, N >= 2048
+    static constexpr int kSmallM2[] = {17, 14, 13, 6};  // M <= 2, N >= 2048
     static constexpr int kTinyM2[] = {3, 14, 8};        // M <= 2
     static constexpr int kLargeM4[] = {7, 6, 0};        // M <= 4, N >= 16384
     static constexpr int kMidM4[] = {15, 7, 8};         // M <= 4, N >= 4096
@@ -1013,6 +1014,8 @@ bool skinny_eligible(const Weights& w, const Knobs& kn, int M)
 {
     if (kn.skinny() == 1 || !w.fast || w.log2cpb != 2 || (w.K % 128) != 0 || M < 1 || M > kSkinnyMT) return false;
     if ((int64_t)kSkinnyMT * w.K * 4 >= INT32_MAX) return false;
+    // the partial-sum slices stay within the reduce's 32-bit buffer offsets
+    if ((int64_t)(w.K / 128) * ((int64_t)kSkinnyMT * w.N + 3) / 4 * 16 >= kOOB) return false;
     return kn.skinny() == 2 || M >= kSkinnyMinM;
 }
 
@@ -1034,16 +1037,18 @@ int skinny_ksw(const Weights& w, const Knobs& kn)
 }
 
 // Workspace of a skinny_w4 launch: one slot per workgroup, one counter per row tile.
-struct SkinnyWs {
-    size_t data, cnt;
-};
-SkinnyWs skinny_ws(const Weights& w, int ksw)
+// Workspace of a K-split call: up to kSkinnyHandoffMax workgroups per tile, a slot per
+// workgroup and an arrival counter per row tile (the in-kernel hand-off); wider splits,
+// ksw slices of M * N floats, each rounded up to a multiple of 4 (16-byte aligned), for
+// skinny_reduce_kernel.
+int skinny_slice4(const Weights& w, int M) { return (int)(((int64_t)M * w.N + 3) / 4); }
+void skinny_ws(const Weights& w, int ksw, int M, size_t* data, size_t* cnt)
 {
     const int tiles = (w.N + kSkinnyRows - 1) / kSkinnyRows;
-    SkinnyWs r;
-    r.data = ksw > 1 ? (size_t)tiles * ksw * kSkinnySlot * sizeof(float) : 0;
-    r.cnt = ksw > 1 ? (size_t)tiles : 0;
-    return r;
+    *data = ksw <= 1 ? 0
+          : ksw <= kSkinnyHandoffMax ? (size_t)tiles * ksw * kSkinnySlot * sizeof(float)
+                                      : (size_t)ksw * skinny_slice4(w, M) * 16;
+    *cnt = ksw > 1 && ksw <= kSkinnyHandoffMax ? (size_t)tiles : 0;
 }
 
 int launch_skinny(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, float* dY, int M, hipStream_t stream)
@@ -1056,8 +1061,11 @@ int launch_skinny(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, fl
     p.zp = w.has_zp ? w.d_zp : nullptr;
     p.a = dA;
     p.y = dY;
-    p.slots = ksw > 1 ? reinterpret_cast<float*>(ws.data) : nullptr;
-    p.sync = ksw > 1 ? ws.cnt : nullptr;
+    const bool handoff = ksw > 1 && ksw <= kSkinnyHandoffMax;
+    p.part = ksw > 1 && !handoff ? reinterpret_cast<float*>(ws.data) : nullptr;
+    p.slice4 = skinny_slice4(w, M);
+    p.slots = handoff ? reinterpret_cast<float*>(ws.data) : nullptr;
+    p.sync = handoff ? ws.cnt : nullptr;
     p.row_bytes = (int)w.row_bytes;
     p.M = M;
     p.N = w.N;
@@ -1067,6 +1075,11 @@ int launch_skinny(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, fl
     p.ksw = ksw;
     hipLaunchKernelGGL(skinny_w4_kernel, dim3(tiles * ksw), dim3(256), 0, stream, p);
     MS_HIP_CHECK(hipGetLastError());
+    if (p.part) {
+        hipLaunchKernelGGL(skinny_reduce_kernel, dim3((p.slice4 + 255) / 256), dim3(256), 0, stream, p.part, dY,
+                           M * w.N, p.slice4, ksw);
+        MS_HIP_CHECK(hipGetLastError());
+    }
     return MS_HIP_OK;
 }
 
@@ -1220,9 +1233,7 @@ void workspace_need(const Weights& w, const Knobs& kn, KernelId k, int M, size_t
     *data = 0;
     *cnt = 0;
     if (k == kSkinny) {
-        const SkinnyWs L = skinny_ws(w, skinny_ksw(w, kn));
-        *data = L.data;
-        *cnt = L.cnt;
+        skinny_ws(w, skinny_ksw(w, kn), M, data, cnt);
     } else if (k == kRb) {
         *data = rb_ws(w, M, rb_shape(w, kn, M).ksw).data;
     } else if (k == kPipe) {

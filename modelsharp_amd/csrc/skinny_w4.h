@@ -17,9 +17,10 @@
 //
 // Work mapping. A workgroup (4 waves) owns kSkinnyRows weight rows and a range of at
 // most kSkinnyNB blocks; each wave owns 16 * kSkinnyNF of the rows. The workgroup
-//   1. issues its activation loads, then every weight load of every wave (all blocks in
-//      flight at once: a block costs a wave 6 * kSkinnyNF registers, the activations
-//      live in LDS);
+//   1. issues its activation loads, then the scales and zero points of its rows (the
+//      NB lanes of a row read its NB blocks' values together and hand them on by
+//      ds_bpermute), then every weight load of every wave (all blocks in flight at
+//      once: a block costs a wave 4 * kSkinnyNF registers, the activations live in LDS);
 //   2. converts the activations of its K range to hi / lo / 2^e straight into LDS, in
 //      the MFMA operand order, while the weights are in flight;
 //   3. per block and fragment: lane (n = lane % 16, s = lane / 16) holds the 16-byte
@@ -27,9 +28,18 @@
 //      (j = 0..3): step j covers k = 32 s + 8 j + [0, 8) for s = 0..3, so the four
 //      steps cover the block, and the activations in LDS are laid out to match (lane
 //      (m, s) of step j reads 16 contiguous bytes, a whole step 1 KB);
-//   4. `ksw` workgroups split a row tile's blocks and meet through per-workgroup slots
-//      (rows m < M only), the last to arrive summing the slots in index order
-//      (deterministic; the arrival counters reset themselves).
+//   4. `ksw` workgroups split a row tile's blocks and meet in one of two ways (both
+//      deterministic: partial sums are added in index order):
+//        - ksw <= kSkinnyHandoffMax: through per-workgroup slots (rows m < M only), the
+//          last to arrive summing the slots (the arrival counters reset themselves);
+//        - wider splits: workgroup kw stores its sums to slice kw of a [ksw][M][N]
+//          workspace with plain stores, and skinny_reduce_kernel adds the slices into Y
+//          (the kernel boundary orders the two launches).
+//      The hand-off's store completion, arrival atomic and slot loads form one latency
+//      chain at the end of each tile that grows with ksw; the separate reduce costs a
+//      launch. Measured (graph-timed, K=4096/N=11008, ksw 8, M = 4 / 16): hand-off 13.7 /
+//      15.9 us, reduce 14.4 / 16.9; K=11008/N=4096, ksw 22: hand-off 17.0 / 20.8, reduce
+//      14.7 / 17.0.
 // The activation permutation within an 8-k group is k0,k4,k1,k5,k2,k6,k3,k7: the order
 // in which the dequant produces fp16 pairs from one dword of packed nibbles.
 #pragma once
@@ -44,7 +54,8 @@ constexpr int kSkinnyRows = 4 * 16 * kSkinnyNF;          // weight rows per work
 constexpr int kSkinnyNB = 4;                             // blocks per workgroup, at most
 constexpr int kSkinnyStepBytes = 1024;                   // one MFMA step's activations (hi or lo)
 constexpr int kSkinnyBlockBytes = 4 * 2 * kSkinnyStepBytes;   // one block: 4 steps x (hi, lo)
-constexpr int kSkinnySlot = kSkinnyMT * kSkinnyRows;     // floats per workgroup slot
+constexpr int kSkinnySlot = kSkinnyMT * kSkinnyRows;     // floats per workgroup slot (hand-off)
+constexpr int kSkinnyHandoffMax = 8;                     // widest K split that uses the hand-off
 
 struct SkinnyParams {
     const uint8_t* b;          // [N][row_bytes]
@@ -52,8 +63,10 @@ struct SkinnyParams {
     const uint8_t* zp;         // [N][zrb] or nullptr (zp = 8)
     const float* a;            // [M][K]
     float* y;                  // [M][N]
-    float* slots;              // [row tiles][ksw][kSkinnySlot] (ksw > 1)
-    int* sync;                 // [row tiles] arrival counters, zero between launches (ksw > 1)
+    float* part;               // [ksw][slice4 * 4] partial sums of Y (ksw > kSkinnyHandoffMax), or nullptr
+    int slice4;                // float4 per slice: M * N rounded up
+    float* slots;              // [row tiles][ksw][kSkinnySlot] (1 < ksw <= kSkinnyHandoffMax)
+    int* sync;                 // [row tiles] arrival counters, zero between launches (idem)
     int row_bytes, M, N, K, nb, zrb;
     int ksw;                   // workgroups per row tile: ksw * kSkinnyNB >= K / 128, ksw <= K / 128
 };
@@ -94,21 +107,32 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    int cbase[NF], sbase[NF], zbase[NF];
+    // Scales and zero points of the wave's rows and blocks: for fragment f, lane l takes
+    // (row 16 f + l / NB, block l % NB), so the NB neighbouring lanes of a row read its
+    // blocks together (one line request per row and instruction; a load per lane, block
+    // and fragment made four times as many, and cost about 3 us of a 24 MB launch). The
+    // lane that computes (row 16 f + ln, block lg) reads them from lane NB ln + lg.
+    static_assert(16 * NB == kWave, "one lane per (row, block) of a fragment");
+    float sv[NF];
+    uint8_t zv[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        const int n = n0 + 16 * f + lane / NB, blk = lane % NB, g = g0 + blk;
+        const bool ok = n < p.N && blk < cnt;
+        sv[f] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc, ok ? n * p.nb * 4 + g * 4 : kOOB, 0, 0));
+        zv[f] = __builtin_amdgcn_raw_buffer_load_b8(rz, ok ? n * p.zrb + (g >> 1) : kOOB, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    int cbase[NF];
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
         const int n = n0 + 16 * f + ln;
-        const bool in = n < p.N;
-        cbase[f] = in ? n * p.row_bytes + ls * 16 : kOOB;
-        sbase[f] = in ? n * p.nb * 4 : kOOB;
-        zbase[f] = in ? n * p.zrb : kOOB;
+        cbase[f] = n < p.N ? n * p.row_bytes + ls * 16 : kOOB;
     }
     // One load group per block, issued in block order, so computing block lg waits only
-    // for its own group (the scheduling barriers keep the groups apart). The zero-point
-    // bytes stay bytes: a widened copy could be moved by the compiler ahead of its group.
+    // for its own group (the scheduling barriers keep the groups apart).
     u32x4_t c[NB][NF];
-    float sc[NB][NF];
-    uint8_t zq[NB][NF];
 #pragma unroll
     for (int lg = 0; lg < NB; ++lg) {
         const int g = g0 + lg;
@@ -116,8 +140,6 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
         for (int f = 0; f < NF; ++f) {
             const bool ok = lg < cnt && cbase[f] != kOOB;
             c[lg][f] = __builtin_amdgcn_raw_buffer_load_b128(rb_, ok ? cbase[f] + g * 64 : kOOB, 0, 0);
-            sc[lg][f] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc, ok ? sbase[f] + g * 4 : kOOB, 0, 0));
-            zq[lg][f] = __builtin_amdgcn_raw_buffer_load_b8(rz, ok ? zbase[f] + (g >> 1) : kOOB, 0, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -188,11 +210,15 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
         if (lg >= cnt) break;
         floatx4_t th[NF], tl[NF];
         uint32_t zb[NF];
+        float sc[NF];
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
             th[f] = floatx4_t{};
             tl[f] = floatx4_t{};
-            const uint32_t zp = (((uint32_t)zq[lg][f] >> (((g0 + lg) & 1) * 4)) & 0x0F) + zdef;
+            const int src = (NB * ln + lg) * 4;   // ds_bpermute byte address of lane NB ln + lg
+            sc[f] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, sv[f])));
+            const uint32_t zq = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)zv[f]);
+            const uint32_t zp = ((zq >> (((g0 + lg) & 1) * 4)) & 0x0F) + zdef;
             zb[f] = kHalfMagic | (zp << 16) | zp;
         }
 #pragma unroll
@@ -219,19 +245,21 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) acc[f][v] = __builtin_fmaf((th[f][v] + tl[f][v]) * ev[v], sc[lg][f], acc[f][v]);
+            for (int v = 0; v < 4; ++v) acc[f][v] = __builtin_fmaf((th[f][v] + tl[f][v]) * ev[v], sc[f], acc[f][v]);
         }
     }
 
-    // ---- 4. output ----
-    if (p.ksw == 1) {
+    // ---- 4. output: Y itself, slice kw of the partial sums (summed by skinny_reduce_kernel),
+    // or the hand-off ----
+    if (p.ksw == 1 || p.part) {
+        float* const out = p.ksw == 1 ? p.y : p.part + (int64_t)kw * p.slice4 * 4;
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
             const int n = n0 + 16 * f + ln;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int m = 4 * ls + v;
-                if (m < p.M && n < p.N) p.y[(int64_t)m * p.N + n] = acc[f][v];
+                if (m < p.M && n < p.N) out[(int64_t)m * p.N + n] = acc[f][v];
             }
         }
         return;
@@ -262,27 +290,27 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
     if (arrival != p.ksw - 1) return;
     wait_vmem_order_only_acquire();
     if (tid == 0) __hip_atomic_store(p.sync + rt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // The slots are loaded kBatch at a time, all in flight together, then added in index
-    // order (slots past ksw load as zeros): one device round trip per batch instead of
-    // one per slot.
-    constexpr int kBatch = 16;
+    // Thread t sums the 4 columns at e_i = 4 (t + 256 i) of every slot (i < kI), rows
+    // e_i / kSkinnyRows = (t + 256 i) / 32, i.e. 8 i .. 8 i + 7: only i < ceil(M / 8) carry
+    // rows of A. All its slot loads (ksw <= kSkinnyHandoffMax per i) are in flight
+    // together, then added per element in slot order.
+    constexpr int kI = kSkinnySlot / (4 * 256);
     const int first = rt * p.ksw * kSkinnySlot;
 #pragma unroll
-    for (int i = 0; i < kSkinnySlot / (4 * 256); ++i) {
+    for (int i = 0; i < kI; ++i) {
         const int e = 4 * (tid + 256 * i), m = e / kSkinnyRows, col = e - m * kSkinnyRows;
-        if (m >= p.M) break;
+        if (8 * i >= p.M) break;
+        u32x4_t sl[kSkinnyHandoffMax];
+#pragma unroll
+        for (int w = 0; w < kSkinnyHandoffMax; ++w)
+            sl[w] = __builtin_amdgcn_raw_buffer_load_b128(
+                rsl, w < p.ksw && m < p.M ? (first + w * kSkinnySlot + e) * 4 : kOOB, 0, kDeviceCoherent);
+        if (m >= p.M) continue;
         float4 tot = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int w0 = 0; w0 < p.ksw; w0 += kBatch) {
-            u32x4_t sl[kBatch];
 #pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                const int w = w0 + u;
-                sl[u] = __builtin_amdgcn_raw_buffer_load_b128(rsl, w < p.ksw ? (first + w * kSkinnySlot + e) * 4 : kOOB,
-                                                              0, kDeviceCoherent);
-            }
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                const float4 v = __builtin_bit_cast(float4, sl[u]);
+        for (int w = 0; w < kSkinnyHandoffMax; ++w) {
+            if (w < p.ksw) {
+                const float4 v = __builtin_bit_cast(float4, sl[w]);
                 tot.x += v.x;
                 tot.y += v.y;
                 tot.z += v.z;
@@ -296,6 +324,39 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
             if (nb0 + t < p.N) p.y[(int64_t)m * p.N + nb0 + t] = tv[t];
         }
     }
+}
+
+// Y[j] = sum over the ksw slices of part[w][j], in slice order (deterministic), for the
+// n = M * N elements of Y; thread i takes elements 4i .. 4i + 3 with every slice's load
+// in flight at once (up to kSkinnyRedBatch per round trip).
+constexpr int kSkinnyRedBatch = 32;
+__global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restrict__ part, float* __restrict__ y,
+                                                            int n, int slice4, int ksw)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= slice4) return;
+    const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(part, ksw * slice4 * 16);
+    float4 t = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int w0 = 0; w0 < ksw; w0 += kSkinnyRedBatch) {
+        u32x4_t v[kSkinnyRedBatch];
+#pragma unroll
+        for (int u = 0; u < kSkinnyRedBatch; ++u)
+            v[u] = __builtin_amdgcn_raw_buffer_load_b128(rp, w0 + u < ksw ? ((w0 + u) * slice4 + i) * 16 : kOOB, 0, 0);
+#pragma unroll
+        for (int u = 0; u < kSkinnyRedBatch; ++u) {
+            if (w0 + u < ksw) {
+                const float4 f = __builtin_bit_cast(float4, v[u]);
+                t.x += f.x;
+                t.y += f.y;
+                t.z += f.z;
+                t.w += f.w;
+            }
+        }
+    }
+    const float tv[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        if (4 * i + c < n) y[4 * i + c] = tv[c];
 }
 
 }  // namespace msnb

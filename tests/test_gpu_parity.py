@@ -123,8 +123,10 @@ def test_gemv_parity(gpu, op, M):
 
 
 # (K, knob 5): K=640 is 5 blocks, split 5 ways by default (one block per workgroup) or
-# 2 ways (2 and 3 blocks); K=512 in one workgroup per row tile (no slots, direct stores).
-SKINNY_SPLITS = [(640, 0), (640, 2), (512, 1)]
+# 2 ways (2 and 3 blocks), both through the in-kernel hand-off; K=512 in one workgroup
+# per row tile (no slots, direct stores); K=1408 is 11 blocks, split 11 ways by default or
+# 9 ways, both wider than the hand-off takes: partial-sum slices and the reduce launch.
+SKINNY_SPLITS = [(640, 0), (640, 2), (512, 1), (1408, 0), (1408, 9)]
 
 
 @pytest.mark.parametrize("K,ksw", SKINNY_SPLITS, ids=lambda v: str(v))
