@@ -18,6 +18,11 @@
 //     s of its row's 64-byte block of codes (plus the chunk's scale and zero point) into a
 //     ring of registers three blocks deep, and dword j of the chunk becomes the B operand
 //     of step j (k = 32 s + 8 j + [0, 8));
+//   * the scales and zero points come from the handle's chunk-major copy (rb_chunk_layout
+//     _kernel, built once): scale and zero point of (128-k block g, row n, chunk c) at
+//     (g N + n) 4 + c, so a fragment's 16 rows read 256 contiguous bytes of scales and 64
+//     of zero points per block (from the operator's [N][nb] layout they touched 16 lines
+//     each; that cost 2-23 us of 43-127 us on the 7B prefill shapes);
 //   * A goes through LDS, double-buffered, one block (128 rows x 128 k, 32 KB) per buffer,
 //     laid out so that the A operand of (step j, fragment f) is 1 KB read by the 64 lanes
 //     in order (no bank conflicts). The next block's A is loaded into registers while the
@@ -43,12 +48,12 @@ constexpr int kRbBufBytes = kRbBM * 128 * 2;   // one block of fp16 A
 
 struct RbParams {
     const uint8_t* b;          // [N][row_bytes]
-    const float* scales;       // [N][nb]
-    const uint8_t* zp;         // [N][zrb] or nullptr (zp = 8)
+    const float* s4;           // [K / 128][N][4] scale of each 32-code chunk
+    const uint8_t* z4;         // [K / 128][N][4] zero point of each 32-code chunk (8 without zero points)
     const _Float16* a16;       // [M][K] fp16, permuted within 8-k groups, row m scaled by 2^-rexp[m]
     float* out;                // the workspace: ksw slices of `slice` floats
     int64_t slice;             // M * N rounded up to a multiple of 4 (16-byte aligned slices)
-    int row_bytes, M, N, K, nb, zrb, log2bs;
+    int row_bytes, M, N, K;
     int tiles_m, tiles_n, ksw;
 };
 
@@ -73,9 +78,8 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
 
     const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(p.a16, p.M * p.K * 2);
     const __amdgpu_buffer_rsrc_t rb_ = buffer_rsrc(p.b, p.N * p.row_bytes);
-    const __amdgpu_buffer_rsrc_t rsc = buffer_rsrc(p.scales, p.N * p.nb * 4);
-    const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(p.zp ? (const void*)p.zp : (const void*)p.scales,
-                                                  p.zp ? p.N * p.zrb : 0);
+    const __amdgpu_buffer_rsrc_t rsc = buffer_rsrc(p.s4, G * p.N * 16);
+    const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(p.z4, G * p.N * 4);
 
     // ---- A staging: thread t moves chunks q = t + 256 u (u = 0..7) of a block; chunk q is
     // (step j = q >> 9, fragment f = (q >> 6) & 7, s = (q >> 4) & 3, row r = q & 15) and
@@ -108,8 +112,8 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
         const int n = n0 + 16 * NF * wave + 16 * f + ln;
         const bool in = n < p.N;
         cb[f] = in ? n * p.row_bytes + ls * 16 : kOOB;
-        sb[f] = in ? n * p.nb * 4 : kOOB;
-        zb[f] = in ? n * p.zrb : kOOB;
+        sb[f] = in ? n * 16 + ls * 4 : kOOB;
+        zb[f] = in ? n * 4 + ls : kOOB;
     }
     struct WBlk {
         u32x4_t c[NF];
@@ -119,13 +123,13 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
     WBlk w[kRbRing];
     auto load_w = [&](WBlk& wb, int i) {
         const bool ok = i < cnt;
-        const int blk = ((g0 + i) * 128 + 32 * ls) >> p.log2bs;   // the quantization block of this chunk
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
             const bool okf = ok && cb[f] != kOOB;
             wb.c[f] = __builtin_amdgcn_raw_buffer_load_b128(rb_, okf ? cb[f] + (g0 + i) * 64 : kOOB, 0, 0);
-            wb.s[f] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc, okf ? sb[f] + blk * 4 : kOOB, 0, 0));
-            wb.z[f] = __builtin_amdgcn_raw_buffer_load_b8(rz, okf ? zb[f] + (blk >> 1) : kOOB, 0, 0);
+            wb.s[f] = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(rsc, okf ? sb[f] + (g0 + i) * p.N * 16 : kOOB, 0, 0));
+            wb.z[f] = __builtin_amdgcn_raw_buffer_load_b8(rz, okf ? zb[f] + (g0 + i) * p.N * 4 : kOOB, 0, 0);
         }
     };
 
@@ -135,15 +139,13 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
 #pragma unroll
         for (int e = 0; e < NF; ++e) acc[f][e] = floatx4_t{};
     }
-    const uint32_t zdef = p.zp ? 0u : 8u;
 
     // Per-block dequant constants of ring slot wb (block g0 + i): (1024 + zp) and fl16(s),
     // both twice, per fragment.
     auto prep = [&](const WBlk& wb, int i, uint32_t (&zz)[NF], h2_t (&s2)[NF]) {
-        const int blk = ((g0 + i) * 128 + 32 * ls) >> p.log2bs;
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
-            const uint32_t zp = (((uint32_t)wb.z[f] >> ((blk & 1) * 4)) & 0x0F) + zdef;
+            const uint32_t zp = wb.z[f];
             zz[f] = kHalfMagic | (zp << 16) | zp;
             const _Float16 sh = (_Float16)wb.s[f];
             s2[f] = h2_t{sh, sh};
@@ -285,6 +287,25 @@ __global__ __launch_bounds__(256) void rb_reduce_kernel(const float4* __restrict
                 ++m;
             }
         }
+    }
+}
+
+// The chunk-major copy of a handle's scales and zero points that mfma_w4_rb reads: entry
+// (g, n, c) is the scale and the zero point (8 without zero points) of the quantization
+// block that holds codes 128 g + 32 c .. + 31 of row n. Exact copies.
+__global__ __launch_bounds__(256) void rb_chunk_layout_kernel(const float* __restrict__ scales,
+                                                              const uint8_t* __restrict__ zp, float* __restrict__ s4,
+                                                              uint8_t* __restrict__ z4, int N, int G, int nb, int zrb,
+                                                              int log2bs)
+{
+    const int64_t total = (int64_t)G * N * 4;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+        const int c = (int)(e & 3);
+        const int64_t gn = e >> 2;
+        const int g = (int)(gn / N), n = (int)(gn - (int64_t)g * N);
+        const int blk = (g * 128 + 32 * c) >> log2bs;
+        s4[e] = scales[(int64_t)n * nb + blk];
+        z4[e] = zp ? (uint8_t)((zp[(int64_t)n * zrb + (blk >> 1)] >> ((blk & 1) * 4)) & 0x0F) : (uint8_t)8;
     }
 }
 

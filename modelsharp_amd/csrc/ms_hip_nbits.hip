@@ -232,6 +232,11 @@ struct Weights {
     uint8_t* d_zp = nullptr;
     float* d_zpf = nullptr;     // float zero points [N * nb]
     int* d_wexp = nullptr;      // general formats: row exponents of the weights [N]
+    // mfma_w4_rb's chunk-major scales / zero points [K / 128][N][4], built by the first
+    // eager call that takes it (rb_ready then 1; guarded by ws_mu)
+    float* d_s4 = nullptr;
+    uint8_t* d_z4 = nullptr;
+    std::atomic<int> rb_ready{0};
     std::atomic<int> knob[kNumKnobs];   // MS_HIP_TUNING_INHERIT: the process default
     // Device-side failure report: a split-K hand-off that gives up writes a nonzero code
     // here (pinned host memory the kernels write through d_err); calls check and clear it.
@@ -316,6 +321,8 @@ void free_weights(Weights& w)
 {
     if (w.d_b) (void)hipFree(w.d_b);
     if (w.d_scales) (void)hipFree(w.d_scales);
+    if (w.d_s4) (void)hipFree(w.d_s4);
+    if (w.d_z4) (void)hipFree(w.d_z4);
     if (w.d_zp) (void)hipFree(w.d_zp);
     if (w.d_zpf) (void)hipFree(w.d_zpf);
     if (w.d_wexp) (void)hipFree(w.d_wexp);
@@ -1090,7 +1097,7 @@ int launch_skinny(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, fl
 bool rb_eligible(const Weights& w, const Knobs& kn, int M)
 {
     return kn.rb() != 1 && w.fast && M > kPanelMaxM && (w.K % 128) == 0 && w.pipe_scales_ok &&
-           (int64_t)w.N * w.row_bytes < kOOB && (int64_t)M * w.K * 2 < kOOB && (int64_t)w.N * w.nb * 4 < kOOB &&
+           (int64_t)w.N * w.row_bytes < kOOB && (int64_t)M * w.K * 2 < kOOB && (int64_t)w.N * w.K / 8 < kOOB &&
            (int64_t)M * w.N * 4 < kOOB;
 }
 
@@ -1174,8 +1181,8 @@ int launch_rb(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, float*
     launch_a_rows_f16(dA, a16, rexp, M, w.K, stream);
     RbParams p;
     p.b = w.d_b;
-    p.scales = w.d_scales;
-    p.zp = w.has_zp ? w.d_zp : nullptr;
+    p.s4 = w.d_s4;
+    p.z4 = w.d_z4;
     p.a16 = reinterpret_cast<const _Float16*>(a16);
     p.out = part;
     p.slice = L.slice;
@@ -1183,9 +1190,6 @@ int launch_rb(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, float*
     p.M = M;
     p.N = w.N;
     p.K = w.K;
-    p.nb = w.nb;
-    p.zrb = w.zrb;
-    p.log2bs = w.log2cpb + 5;
     p.tiles_m = tiles_m;
     p.tiles_n = tiles_n;
     p.ksw = ksw;
@@ -1202,6 +1206,32 @@ int launch_rb(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, float*
                        reinterpret_cast<const float4*>(part), dY, rexp, M * w.N, w.N, slice4, ksw);
     MS_HIP_CHECK(hipGetLastError());
     return MS_HIP_OK;
+}
+
+// mfma_w4_rb's chunk-major scales and zero points: built once, on the call's stream, by
+// the first call that takes the kernel outside stream capture (then the stream is
+// synchronised once, so calls on other streams find the copy complete). Returns 1 when
+// the copy is there, 0 when it cannot be built now (capture), -1 on a HIP failure.
+int ensure_rb_layout(Weights& w, hipStream_t stream)
+{
+    if (w.rb_ready.load(std::memory_order_acquire)) return 1;
+    std::lock_guard<std::mutex> lock(w.ws_mu);
+    if (w.rb_ready.load(std::memory_order_relaxed)) return 1;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    const int G = w.K / 128;
+    const int64_t entries = (int64_t)G * w.N * 4;
+    if (!w.d_s4 && hipMalloc(&w.d_s4, (size_t)entries * sizeof(float)) != hipSuccess) return -1;
+    if (!w.d_z4 && hipMalloc(&w.d_z4, (size_t)entries) != hipSuccess) return -1;
+    const int grid = (int)std::min<int64_t>((entries + 255) / 256, 8192);
+    hipLaunchKernelGGL(rb_chunk_layout_kernel, dim3(grid), dim3(256), 0, stream, w.d_scales,
+                       w.has_zp ? w.d_zp : nullptr, w.d_s4, w.d_z4, w.N, G, w.nb, w.zrb, w.log2cpb + 5);
+    if (hipGetLastError() != hipSuccess || hipStreamSynchronize(stream) != hipSuccess) return -1;
+    w.rb_ready.store(1, std::memory_order_release);
+    return 1;
 }
 
 // ---- dispatch ------------------------------------------------------------------------------
@@ -1281,6 +1311,18 @@ int check_call(const float* dA, float* dY, int M)
     return MS_HIP_OK;
 }
 
+// A call routed to mfma_w4_rb needs the handle's chunk-major scales: built here when
+// `may_build` (and the stream is not capturing), else the call takes the exact
+// workspace-free kernel instead.
+int resolve_rb(Weights& w, const Knobs& kn, KernelId* k, int M, hipStream_t stream, bool may_build)
+{
+    if (*k != kRb || w.rb_ready.load(std::memory_order_acquire)) return MS_HIP_OK;
+    const int r = may_build ? ensure_rb_layout(w, stream) : 0;
+    if (r < 0) return fail(MS_HIP_ERR_HIP, "[ms_hip] scale re-layout failed: %s", hipGetErrorString(hipGetLastError()));
+    if (r == 0) *k = workspace_free_kernel(w, kn, M);
+    return MS_HIP_OK;
+}
+
 // One call with the handle's own (growable) workspace.
 int enqueue_gemm(Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
 {
@@ -1288,6 +1330,7 @@ int enqueue_gemm(Weights& w, const float* dA, float* dY, int M, hipStream_t stre
     if (st || M == 0) return st;
     const Knobs kn = knobs_of(w);
     KernelId k = choose_kernel(w, kn, M);
+    if ((st = resolve_rb(w, kn, &k, M, stream, true))) return st;
     size_t need_d = 0, need_c = 0;
     workspace_need(w, kn, k, M, &need_d, &need_c);
     Ws ws;
@@ -1812,7 +1855,8 @@ int ms_hip_nbits_gemm_dev_f16(void* handle, const void* dA16, float* dY, int M, 
     if ((reinterpret_cast<uintptr_t>(dA16) & 1) || (reinterpret_cast<uintptr_t>(dY) & 3))
         return fail(MS_HIP_ERR_INVALID, "[ms_hip] A must be 2-byte and Y 4-byte aligned");
     const Knobs kn = knobs_of(*w);
-    const KernelId k = choose_kernel(*w, kn, M);
+    KernelId k = choose_kernel(*w, kn, M);
+    if ((st = resolve_rb(*w, kn, &k, M, s, true))) return st;
     size_t need_d = 0, need_c = 0;
     workspace_need(*w, kn, k, M, &need_d, &need_c);
     const size_t a_off = align256(need_d);
@@ -1839,7 +1883,9 @@ int ms_hip_nbits_gemm_dev_noalloc(void* handle, const float* dA, float* dY, int 
     if (st) return st;
     if ((st = check_call(dA, dY, M)) || M == 0) return st;
     const Knobs kn = knobs_of(*w);
-    const KernelId k = choose_kernel(*w, kn, M);
+    KernelId k = choose_kernel(*w, kn, M);
+    // the chunk-major scales are not built here (that allocates): without them, mfma_w4
+    if ((st = resolve_rb(*w, kn, &k, M, s, false))) return st;
     size_t need_d = 0, need_c = 0;
     workspace_need(*w, kn, k, M, &need_d, &need_c);
     if (need_d > kScratchDataBytes || need_c > kScratchCntInts)
