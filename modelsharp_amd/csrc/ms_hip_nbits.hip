@@ -1128,6 +1128,8 @@ RbShape rb_shape(const Weights& w, const Knobs& kn, int M)
         const int64_t tiles = (int64_t)tiles_m * tiles_n;
         const double t_block = 1.4e-6 + 0.525e-6 * nf;
         for (int k = 1; k <= std::min(G, 32); ++k) {
+            // the slices stay within the reduce's 32-bit buffer offsets
+            if (k > 1 && (int64_t)k * (((int64_t)M * w.N + 3) / 4) * 16 >= kOOB) break;
             if (kn.rb_ksw() > 0 && k != std::max(1, std::min(kn.rb_ksw(), G))) continue;
             const double rounds = (double)((tiles * k + cus - 1) / cus);
             const double t = rounds * std::ceil((double)G / k) * t_block + (2.0 * k + 1) * ybytes / hbm + t_launch;
