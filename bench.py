@@ -256,10 +256,11 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--detail", default="", help="also write per-op results of every workload to this JSON file")
     ap.add_argument("--op", default="", help="profiling mode: launch only this 7B decode op (q,k,v,o,gate,up,down), "
-                                             "a grouped launch (qkv, gate_up) or prefill_up / prefill_down (M=2048), "
+                                             "a grouped launch (qkv, gate_up), prefill_up / prefill_down or the "
+                                             "block-size-128 small-batch smallm_up / smallm_down (M from --m), "
                                              "eagerly over the rotation, then a plain copy of --copy-mib; no JSON line")
     ap.add_argument("--calls", type=int, default=64, help="launches in --op mode")
-    ap.add_argument("--m", type=int, default=2048, help="rows of A for prefill_* in --op mode")
+    ap.add_argument("--m", type=int, default=2048, help="rows of A for prefill_* and smallm_* in --op mode")
     ap.add_argument("--copy-mib", type=int, default=256, help="size of the calibration copy in --op mode")
     args = ap.parse_args()
 
@@ -456,12 +457,16 @@ def profile_op(args) -> int:
         ops = [next(o for o in workloads.LLAMA7B_PREFILL_OPS if o.name == args.op[len("prefill_"):])]
         M, kind = args.m, "rmsnorm"
         copies = max(2, workloads.rotation_copies(workloads.algorithmic_bytes_group(ops, M), args.rotate_mib << 20))
+    elif args.op.startswith("smallm_"):
+        ops = [next(o for o in workloads.LLAMA7B_SMALLM_OPS if o.name == args.op[len("smallm_"):])]
+        M, kind = args.m, "normal"
+        copies = workloads.rotation_copies(workloads.algorithmic_bytes_group(ops, M), args.rotate_mib << 20)
     else:
         ops = ([workloads.DECODE_7B[i] for i in GROUPS[args.op]] if args.op in GROUPS else
                [next(o for o in workloads.DECODE_7B if o.name == args.op)])
         M, kind = 1, "normal"
     fp = workloads.algorithmic_bytes_group(ops, M)
-    if M == 1:
+    if M == 1 and not args.op.startswith("smallm_"):
         copies = workloads.rotation_copies(fp, args.rotate_mib << 20)
     rot = Rotation(ops, M, copies, seed=7, kind=kind, share=[0] * len(ops))
     stream = torch.cuda.current_stream().cuda_stream
