@@ -352,8 +352,9 @@ def main() -> int:
     dom = groups["gate_up"]
     gate = next(op for op in ops if op.name == "gate")   # the CPU baseline's sample
 
-    # host-pointer entry (ms_hip_nbits_gemm): A and Y through the handle's pinned staging
-    # and DMA copies, synchronous; rotating over the weight copies. Reported, never `value`.
+    # host-pointer entry (ms_hip_nbits_gemm): A through the handle's pinned staging and a
+    # DMA copy, the kernel storing Y straight into pinned host memory (calls of up to 1 MB
+    # of A and Y), synchronous; rotating over the weight copies. Reported, never `value`.
     # Each call is timed on its own: the first few hundred calls of a process include one
     # stall of tens of milliseconds in the runtime (measured: one call of 43 ms among 256
     # whose median was 42 us), so a full untimed series goes first and the median is reported
@@ -372,8 +373,8 @@ def main() -> int:
     host = {"op": "gate", "K": gate.K, "N": gate.N, "M": 1, "us_per_call": round(host_us, 2),
             "mean_us": round(statistics.mean(per_call), 2), "max_us": round(max(per_call), 1), "calls": calls,
             "GBs": round(workloads.algorithmic_bytes(gate, 1) / (host_us * 1e-6) / 1e9, 1),
-            "path": "ms_hip_nbits_gemm: host A -> pinned staging -> H2D, kernel, D2H -> pinned -> host Y, "
-                    "synchronous; median of per-call times"}
+            "path": "ms_hip_nbits_gemm: host A -> pinned staging -> H2D copy, kernel storing Y into pinned "
+                    "host memory -> host Y, synchronous; median of per-call times"}
     log(f"  host-pointer gate call: median {host_us:.2f} us, mean {host['mean_us']} us, max {host['max_us']} us "
         f"({host['GBs']} GB/s, PCIe copies included)")
     traffic = measured_traffic(dom["kernel"])

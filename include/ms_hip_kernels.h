@@ -138,7 +138,9 @@ int ms_hip_nbits_weights_info(void* handle, int* N, int* K, int* bits, int* bloc
  * MatMulNBitsKernel.Execute (MatMulNBitsKernel.cs:174-191), with the weights
  * already resident. M<=16 runs the dequant-fused GEMV (block size 128 and
  * 3 <= M <= 16: its matrix-core form at the same accuracy), larger M the MFMA GEMM.
- * A and Y go through pinned staging buffers owned by the handle. */
+ * A and Y go through pinned staging buffers owned by the handle: A as a DMA copy;
+ * Y stored by the kernel straight into the pinned buffer when A and Y each fit in
+ * 1 MiB, else a DMA copy back. */
 int ms_hip_nbits_gemm(void* handle, const float* a_host, float* y_host, int M);
 
 /* Device-pointer form: enqueues on `stream` (a hipStream_t, NULL = the null
@@ -260,6 +262,7 @@ int ms_hip_sync(void);
  *  10 the host-pointer entries' staging, value - 1 as bits: bit 0 copies A to the
  *     device with a kernel reading the pinned host buffer (else a DMA copy), bit 1
  *     has the GEMM store Y straight into pinned host memory (else a DMA copy back);
+ *     0 = the default (Y straight for calls of up to 1 MiB of A and Y, else DMA);
  *  11 the 8-bit GEMV's launch configuration: c+1 forces configuration c (0..8) of the
  *     library's table, -1 keeps 8-bit calls on gemv_general.
  * ms_hip_nbits_debug_set_counters sets the arrival tag of every split tile of the

@@ -1986,6 +1986,8 @@ int ms_hip_nbits_batch_launch_info(void* const* handles, const float* const* dA,
 
 namespace {
 
+constexpr size_t kDirectStageBytes = (size_t)1 << 20;
+
 // Device copy of n floats from pinned host memory (read across PCIe by the kernel).
 __global__ __launch_bounds__(256) void stage_copy_kernel(const float* __restrict__ src, float* __restrict__ dst,
                                                          int64_t n)
@@ -2030,14 +2032,17 @@ int host_gemm(void* handle, const float* a_host, float* y_host, int M, bool w4a8
     float* hA = reinterpret_cast<float*>(w->h_stage);
     float* hY = reinterpret_cast<float*>(w->h_stage + a_span);
     std::memcpy(hA, a_host, a_bytes);
-    // A and Y cross PCIe as DMA copies through the pinned staging. Knob 10 can instead have
-    // a kernel pull A from the pinned (device-mapped) buffer and/or the GEMM store Y straight
-    // into it (every kernel writes Y once and never reads it back). Measured on the 7B gate
-    // at M=1: one handle called in a loop, direct Y took 30.4 us per call against 39-42 us
-    // with both copies; but eight handles called in turn under a rotating weight stream took
-    // 180 us per call with direct Y (50 us with both direct) — the stores then wait on the
-    // GPU's translations of the host pages — so the copies stay the default.
-    const int mode = knobs_of(*w).host_staging() > 0 ? knobs_of(*w).host_staging() - 1 : 0;
+    // A crosses PCIe as a DMA copy through the pinned staging. For small calls (decode:
+    // A and Y up to kDirectStageBytes each) the GEMM stores Y straight into the pinned
+    // (device-mapped) host buffer, which saves the copy back and its set-up: every kernel
+    // writes Y once and never reads it back. Measured on the 7B gate at M=1, eight handles
+    // called in turn under a rotating weight stream, medians of per-call times: 32 us per
+    // call with direct Y against 42 us with both copies; a kernel pulling A from the pinned
+    // buffer instead of the DMA copy gained nothing. Large calls keep both DMA copies, which
+    // stream at full PCIe rate without holding the GEMM's waves. Knob 10 selects the
+    // staging for measurements.
+    const bool small = a_bytes <= kDirectStageBytes && y_bytes <= kDirectStageBytes;
+    const int mode = knobs_of(*w).host_staging() > 0 ? knobs_of(*w).host_staging() - 1 : (small ? 2 : 0);
     const bool direct_a = mode & 1, direct = mode & 2;
     if (direct_a) {
         const int64_t n = (int64_t)M * w->K;
