@@ -1,5 +1,5 @@
-// mfma_w4_rb.h — INT4 MatMulNBits prefill GEMM with the weights dequantized straight
-// into MFMA operand registers (M > 16, block sizes 32..., K a multiple of 128).
+// mfma_w4_rb.h — 4- and 8-bit MatMulNBits prefill GEMM with the weights dequantized
+// straight into MFMA operand registers (M > 16, block sizes 32..., K a multiple of 128).
 //
 // Y[M,N] = A[M,K] * W[N,K]^T, W = fl16((q - zp) * fl16(s)), A the fp16 copy made by
 // a_rows_f16_kernel (row m scaled by 2^-rexp[m]; each 8-k group in the order
@@ -17,7 +17,9 @@
 //   * weights never touch LDS: lane (n = lane % 16, s = lane / 16) loads the 16-byte chunk
 //     s of its row's 64-byte block of codes (plus the chunk's scale and zero point) into a
 //     ring of registers three blocks deep, and dword j of the chunk becomes the B operand
-//     of step j (k = 32 s + 8 j + [0, 8));
+//     of step j (k = 32 s + 8 j + [0, 8)). With 8-bit codes (B8) a row's block is 128
+//     bytes: the lane loads its 32 codes as two chunks, and dwords 2j, 2j + 1 make step j
+//     (dequant8_f16_b8, the same pair order and rounding);
 //   * the scales and zero points come from the handle's chunk-major copy (rb_chunk_layout
 //     _kernel, built once): scale and zero point of (128-k block g, row n, chunk c) at
 //     (g N + n) 4 + c, so a fragment's 16 rows read 256 contiguous bytes of scales and 64
@@ -42,6 +44,20 @@
 
 namespace msnb {
 
+// Eight 8-bit codes (d0 = codes 0..3, d1 = codes 4..7, one byte each) as four fp16 pairs
+// (k_t, k_{t+4}), t = 0..3, the order of dequant8_f16's pairs (and of the permuted A):
+// v_perm gathers byte t of d0 and byte t of d1 into halves 0 and 1, v_and_or puts them
+// under the exponent of 1024.0 (1024 + q exactly), then (1024 + q) - (1024 + zp) = q - zp
+// exactly (|q - zp| <= 255) and one rounding to fp16 of (q - zp) * fl16(s).
+__device__ __forceinline__ void dequant8_f16_b8(uint32_t d0, uint32_t d1, h2_t zb, h2_t s2, uint32_t (&o)[4])
+{
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const uint32_t pr = __builtin_amdgcn_perm(d1, d0, (uint32_t)(((4 + t) << 16) | t));
+        o[t] = as_u32((as_h2(and_or(pr, 0x00FF00FFu, kHalfMagic)) - zb) * s2);
+    }
+}
+
 constexpr int kRbBM = 128;   // rows of A per tile; the tile's columns are 64 * NF (NF = 1, 2, 4)
 constexpr int kRbRing = 3;                     // weight blocks in registers
 constexpr int kRbBufBytes = kRbBM * 128 * 2;   // one block of fp16 A
@@ -57,9 +73,11 @@ struct RbParams {
     int tiles_m, tiles_n, ksw;
 };
 
-template <int NF>
+template <int NF, bool B8>
 __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
 {
+    constexpr int CW = B8 ? 2 : 1;       // 16-byte code chunks per lane and 128-k block
+    constexpr int BLK = 64 * CW;         // code bytes per row and 128-k block
     constexpr int MF = kRbBM / 16, BN = 64 * NF;
     __shared__ __attribute__((aligned(16))) uint8_t lds_a[2 * kRbBufBytes];
 
@@ -111,12 +129,12 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
     for (int f = 0; f < NF; ++f) {
         const int n = n0 + 16 * NF * wave + 16 * f + ln;
         const bool in = n < p.N;
-        cb[f] = in ? n * p.row_bytes + ls * 16 : kOOB;
+        cb[f] = in ? n * p.row_bytes + ls * 16 * CW : kOOB;
         sb[f] = in ? n * 16 + ls * 4 : kOOB;
         zb[f] = in ? n * 4 + ls : kOOB;
     }
     struct WBlk {
-        u32x4_t c[NF];
+        u32x4_t c[NF][CW];
         float s[NF];
         uint8_t z[NF];   // a byte, so the compiler cannot hoist a widening ahead of the block's wait
     };
@@ -126,7 +144,9 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
             const bool okf = ok && cb[f] != kOOB;
-            wb.c[f] = __builtin_amdgcn_raw_buffer_load_b128(rb_, okf ? cb[f] + (g0 + i) * 64 : kOOB, 0, 0);
+#pragma unroll
+            for (int h = 0; h < CW; ++h)
+                wb.c[f][h] = __builtin_amdgcn_raw_buffer_load_b128(rb_, okf ? cb[f] + (g0 + i) * BLK + 16 * h : kOOB, 0, 0);
             wb.s[f] = __builtin_bit_cast(
                 float, __builtin_amdgcn_raw_buffer_load_b32(rsc, okf ? sb[f] + (g0 + i) * p.N * 16 : kOOB, 0, 0));
             wb.z[f] = __builtin_amdgcn_raw_buffer_load_b8(rz, okf ? zb[f] + (g0 + i) * p.N * 4 : kOOB, 0, 0);
@@ -157,9 +177,17 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
     };
     // B operands of step j, fragment f only.
     auto deq1 = [&](const WBlk& wb, int j, int f, uint32_t zzf, h2_t s2f) {
-        const uint32_t x = j == 0 ? wb.c[f].x : j == 1 ? wb.c[f].y : j == 2 ? wb.c[f].z : wb.c[f].w;
         uint32_t o[4];
-        dequant8_f16(x, as_h2(zzf), s2f, o);
+        if constexpr (B8) {
+            // step j: codes 8j .. 8j + 7 of the lane's 32, dwords 2j (k0..k3) and 2j + 1 (k4..k7)
+            const u32x4_t& cw = wb.c[f][j >> 1];
+            const uint32_t d0 = (j & 1) ? cw.z : cw.x, d1 = (j & 1) ? cw.w : cw.y;
+            dequant8_f16_b8(d0, d1, as_h2(zzf), s2f, o);
+        } else {
+            const u32x4_t& cw = wb.c[f][0];
+            const uint32_t x = j == 0 ? cw.x : j == 1 ? cw.y : j == 2 ? cw.z : cw.w;
+            dequant8_f16(x, as_h2(zzf), s2f, o);
+        }
         return __builtin_bit_cast(half8_t, u32x4_t{o[0], o[1], o[2], o[3]});
     };
 
@@ -308,12 +336,12 @@ __global__ __launch_bounds__(256) void rb_reduce_kernel(const float4* __restrict
 }
 
 // The chunk-major copy of a handle's scales and zero points that mfma_w4_rb reads: entry
-// (g, n, c) is the scale and the zero point (8 without zero points) of the quantization
-// block that holds codes 128 g + 32 c .. + 31 of row n. Exact copies.
+// (g, n, c) is the scale and the zero point (2^(bits-1) without zero points) of the
+// quantization block that holds codes 128 g + 32 c .. + 31 of row n. Exact copies.
 __global__ __launch_bounds__(256) void rb_chunk_layout_kernel(const float* __restrict__ scales,
                                                               const uint8_t* __restrict__ zp, float* __restrict__ s4,
                                                               uint8_t* __restrict__ z4, int N, int G, int nb, int zrb,
-                                                              int log2bs)
+                                                              int log2bs, int bits)
 {
     const int64_t total = (int64_t)G * N * 4;
     for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
@@ -322,7 +350,10 @@ __global__ __launch_bounds__(256) void rb_chunk_layout_kernel(const float* __res
         const int g = (int)(gn / N), n = (int)(gn - (int64_t)g * N);
         const int blk = (g * 128 + 32 * c) >> log2bs;
         s4[e] = scales[(int64_t)n * nb + blk];
-        z4[e] = zp ? (uint8_t)((zp[(int64_t)n * zrb + (blk >> 1)] >> ((blk & 1) * 4)) & 0x0F) : (uint8_t)8;
+        if (bits == 8)
+            z4[e] = zp ? zp[(int64_t)n * zrb + blk] : (uint8_t)128;
+        else
+            z4[e] = zp ? (uint8_t)((zp[(int64_t)n * zrb + (blk >> 1)] >> ((blk & 1) * 4)) & 0x0F) : (uint8_t)8;
     }
 }
 

@@ -398,11 +398,12 @@ int zero_ints(int* p, int64_t n, hipStream_t stream)
 }
 
 // The fp16 prefill kernels round scales to fp16 and form (q - zp) * s in fp16: every
-// nonzero |s| must be an fp16 normal (>= 2^-14) and 15 |s| must stay below 65504.
+// nonzero |s| must be an fp16 normal (>= 2^-14) and max|q - zp| |s| (15, or 255 for 8-bit
+// codes) must stay below 65504.
 int check_pipe_scales(Weights& w)
 {
     w.pipe_scales_ok = 0;
-    if (!w.fast) return MS_HIP_OK;
+    if (!w.fast && !(w.bits == 8 && !w.zp_float)) return MS_HIP_OK;
     unsigned* d = nullptr;
     MS_HIP_CHECK(hipMalloc(&d, 2 * sizeof(unsigned)));
     const unsigned init[2] = {0xFFFFFFFFu, 0u};
@@ -418,7 +419,8 @@ int check_pipe_scales(Weights& w)
     (void)hipFree(d);
     if (e != hipSuccess) return fail(MS_HIP_ERR_HIP, "[ms_hip] scale range check failed: %s", hipGetErrorString(e));
     const unsigned kMinNormal16 = 0x38800000u;   // 2^-14
-    const unsigned kMaxScale = 0x45886000u;      // 4364.0: 15 * s < 65504
+    const unsigned kMaxScale = w.bits == 8 ? 0x43800000u    // 256.0: 255 * s < 65504
+                                           : 0x45886000u;   // 4364.0: 15 * s < 65504
     w.pipe_scales_ok = (r[0] == 0xFFFFFFFFu) || (r[0] >= kMinNormal16 && r[1] <= kMaxScale);
     return MS_HIP_OK;
 }
@@ -1096,7 +1098,10 @@ int launch_skinny(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, fl
 // offset the kernel uses for padding rows.
 bool rb_eligible(const Weights& w, const Knobs& kn, int M)
 {
-    return kn.rb() != 1 && w.fast && M > kPanelMaxM && (w.K % 128) == 0 && w.pipe_scales_ok &&
+    // 4-bit fast layouts, or 8-bit codes with packed or no zero points and a power-of-two
+    // block size >= 32 (one scale per 32-code chunk)
+    const bool fmt = w.fast || (w.bits == 8 && !w.zp_float && w.bs >= 32 && log2_exact(w.bs) >= 0);
+    return kn.rb() != 1 && fmt && M > kPanelMaxM && (w.K % 128) == 0 && w.pipe_scales_ok &&
            (int64_t)w.N * w.row_bytes < kOOB && (int64_t)M * w.K * 2 < kOOB && (int64_t)w.N * w.K / 8 < kOOB &&
            (int64_t)M * w.N * 4 < kOOB;
 }
@@ -1120,10 +1125,15 @@ RbShape rb_shape(const Weights& w, const Knobs& kn, int M)
     const int tiles_m = (M + kRbBM - 1) / kRbBM;
     const double hbm = 4.0e12, t_launch = 2e-6;
     const double ybytes = (double)M * w.N * 4;
-    RbShape best{4, 1, tiles_m, (w.N + 255) / 256};
+    // The 8-bit form is instantiated for NF 1 and 2 only (twice the code registers per
+    // fragment); a forced NF of 4 falls back to the pick there.
+    const bool b8 = w.bits == 8;
+    const int force_nf = b8 && kn.rb_nf() == 4 ? 0 : kn.rb_nf();
+    RbShape best = b8 ? RbShape{2, 1, tiles_m, (w.N + 127) / 128} : RbShape{4, 1, tiles_m, (w.N + 255) / 256};
     double best_t = 1e30;
     for (int nf : {4, 2, 1}) {
-        if (kn.rb_nf() > 0 && nf != kn.rb_nf()) continue;
+        if (force_nf > 0 && nf != force_nf) continue;
+        if (b8 && nf == 4) continue;
         const int tiles_n = (w.N + 64 * nf - 1) / (64 * nf);
         const int64_t tiles = (int64_t)tiles_m * tiles_n;
         const double t_block = 1.4e-6 + 0.525e-6 * nf;
@@ -1197,12 +1207,18 @@ int launch_rb(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, float*
     p.ksw = ksw;
     const int items = tiles_m * tiles_n * ksw;
     const dim3 grid(((items + kXcds - 1) / kXcds) * kXcds);
-    if (sh.nf == 1)
-        hipLaunchKernelGGL(mfma_w4_rb_kernel<1>, grid, dim3(256), 0, stream, p);
-    else if (sh.nf == 2)
-        hipLaunchKernelGGL(mfma_w4_rb_kernel<2>, grid, dim3(256), 0, stream, p);
-    else
-        hipLaunchKernelGGL(mfma_w4_rb_kernel<4>, grid, dim3(256), 0, stream, p);
+    if (w.bits == 8) {
+        if (sh.nf == 1)
+            hipLaunchKernelGGL((mfma_w4_rb_kernel<1, true>), grid, dim3(256), 0, stream, p);
+        else
+            hipLaunchKernelGGL((mfma_w4_rb_kernel<2, true>), grid, dim3(256), 0, stream, p);
+    } else if (sh.nf == 1) {
+        hipLaunchKernelGGL((mfma_w4_rb_kernel<1, false>), grid, dim3(256), 0, stream, p);
+    } else if (sh.nf == 2) {
+        hipLaunchKernelGGL((mfma_w4_rb_kernel<2, false>), grid, dim3(256), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((mfma_w4_rb_kernel<4, false>), grid, dim3(256), 0, stream, p);
+    }
     const int slice4 = (int)(L.slice / 4);
     hipLaunchKernelGGL(rb_reduce_kernel, dim3((unsigned)std::min((slice4 + 255) / 256, 8192)), dim3(256), 0, stream,
                        reinterpret_cast<const float4*>(part), dY, rexp, M * w.N, w.N, slice4, ksw);
@@ -1230,7 +1246,7 @@ int ensure_rb_layout(Weights& w, hipStream_t stream)
     if (!w.d_z4 && hipMalloc(&w.d_z4, (size_t)entries) != hipSuccess) return -1;
     const int grid = (int)std::min<int64_t>((entries + 255) / 256, 8192);
     hipLaunchKernelGGL(rb_chunk_layout_kernel, dim3(grid), dim3(256), 0, stream, w.d_scales,
-                       w.has_zp ? w.d_zp : nullptr, w.d_s4, w.d_z4, w.N, G, w.nb, w.zrb, w.log2cpb + 5);
+                       w.has_zp ? w.d_zp : nullptr, w.d_s4, w.d_z4, w.N, G, w.nb, w.zrb, log2_exact(w.bs), w.bits);
     if (hipGetLastError() != hipSuccess || hipStreamSynchronize(stream) != hipSuccess) return -1;
     w.rb_ready.store(1, std::memory_order_release);
     return 1;
@@ -1247,6 +1263,7 @@ KernelId choose_kernel(const Weights& w, const Knobs& kn, int M)
 {
     if (!w.fast) {
         if (pick_gemv8_config(w, kn, M) >= 0) return kGemvW8;
+        if (rb_eligible(w, kn, M)) return kRb;   // 8-bit prefill
         if (!general_eligible(w)) return kGeneric;
         return M <= kPanelMaxM ? kGemvGeneral : kMfmaGeneral;
     }
@@ -1278,6 +1295,11 @@ void workspace_need(const Weights& w, const Knobs& kn, KernelId k, int M, size_t
 // The kernel a call takes when its workspace cannot be had (growth under capture).
 KernelId workspace_free_kernel(const Weights& w, const Knobs& kn, int M)
 {
+    if (!w.fast) {
+        if (pick_gemv8_config(w, kn, M) >= 0) return kGemvW8;
+        if (!general_eligible(w)) return kGeneric;
+        return M <= kPanelMaxM ? kGemvGeneral : kMfmaGeneral;
+    }
     if (M <= kPanelMaxM) return pick_gemv_config(w, kn, M, w.N) >= 0 ? kGemv : kPanel;
     return kMfma;
 }

@@ -56,12 +56,16 @@ def assert_within(y, ref, allowed, what):
     assert np.all(err <= allowed), f"{what}: err/bound {ratio:.3e}"
 
 
-def expected_kernel(op: Op, M: int, float_zp: bool = False) -> str:
-    """The kernel the dispatch rules give a call with M rows."""
+def expected_kernel(op: Op, M: int, float_zp: bool = False, fp16_scales: bool = True) -> str:
+    """The kernel the dispatch rules give a call with M rows (fp16_scales: every nonzero
+    |scale| lies in [2^-14, 256], as make_weights draws them)."""
     pow2 = op.block_size >= 16 and (op.block_size & (op.block_size - 1)) == 0
     if (op.bits == 8 and not float_zp and pow2 and op.K % 16 == 0 and M <= 4
             and M * op.K * 4 <= 159 * 1024):
         return "gemv_w8"
+    if (op.bits == 8 and not float_zp and pow2 and op.block_size >= 32 and op.K % 128 == 0 and M > 16
+            and fp16_scales):
+        return "mfma_w4_rb"
     return "gemv_general" if M <= 16 else "mfma_general"
 
 
@@ -75,6 +79,16 @@ def check_against_oracle(w, a, b, s, zp, zpf, op, what):
     if kernel == "mfma_general":
         allowed = (4 * gamma2(op.K) + 2.0 ** -20) * cond + 2.0 ** -30 * (
             np.max(np.abs(a), axis=1, keepdims=True).astype(np.float64) * np.abs(W).sum(axis=1)[None, :])
+    elif kernel == "mfma_w4_rb":
+        # fp16 prefill numerics: A rounded once to fp16 after its row's power-of-two scaling
+        # (2^-11 relative; below the fp16 normal range, 2^-39 of the row's max absolute)
+        # and W = fl16((q - zp) fl16(s)) (2^-10 relative: fl16(s) and the product), exact
+        # products, fp32 sums; and the relative Frobenius tolerance of the prefill path, 2e-3.
+        allowed = (2.0 ** -11 + 2.0 ** -10 + 2.0 ** -20 + gamma2(op.K)) * 1.01 * cond + 2.0 ** -30 * (
+            np.max(np.abs(a), axis=1, keepdims=True).astype(np.float64) * np.abs(W).sum(axis=1)[None, :])
+        rel = float(np.linalg.norm(y.astype(np.float64) - ref) / max(np.linalg.norm(ref.astype(np.float64)), 1e-300))
+        log(f"  {what}: relative Frobenius error {rel:.3e}")
+        assert rel <= 2e-3, f"{what}: rel_fro {rel:.3e}"
     else:
         allowed = gamma2(op.K) * cond
     assert_within(y, ref, allowed, f"{what} [{kernel}]")
@@ -129,14 +143,15 @@ def test_float_zero_points(gpu, op, M):
 
 
 def test_general_mfma_full_size_8bit(gpu):
-    """8-bit weights at a 7B projection's shape (K=4096, N=4096) over 128 rows."""
+    """8-bit weights at a 7B projection's shape (K=4096, N=4096) over 128 rows (the fp16
+    prefill kernel) and over one row (the 8-bit GEMV)."""
     op = Op("b8_7b", 4096, 4096, 32, True, bits=8)
     b, s, z = workloads.make_weights(op, seed=5)
     a = workloads.make_activations(128, op.K, seed=6, kind="rmsnorm")
     w = native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
     log(f"8-bit 4096x4096 M=128 {w.launch_info(128)}")
     kernel, _ = check_against_oracle(w, a, b, s, z, None, op, "b8 K=4096 N=4096 M=128")
-    assert kernel == "mfma_general"
+    assert kernel == "mfma_w4_rb"
     y1 = w.gemm(a)
     assert np.array_equal(y1, w.gemm(a))   # deterministic
     a1 = a[:1]
@@ -303,3 +318,59 @@ def test_operator_routes_float16_and_float_zero_points(gpu):
         np.max(np.abs(a32), axis=1, keepdims=True).astype(np.float64) * np.abs(W).sum(axis=1)[None, :])
     assert_within(y, ref, allowed, "operator f16 / float zp M=24")
     k.close()
+
+
+# ---- 8-bit prefill on the fp16 matrix cores -----------------------------------------------
+B8_PREFILL = [
+    Op("b8p_bs32_zp", 1024, 1000, 32, True, bits=8),     # ragged N (not a multiple of the tiles)
+    Op("b8p_bs64_sym", 2048, 600, 64, False, bits=8),    # default zero point 128
+    Op("b8p_bs128_zp", 1536, 384, 128, True, bits=8),
+    Op("b8p_bs256_zp", 2304, 256, 256, True, bits=8),    # K % 256 != 0: a partial last block
+]
+
+
+@pytest.mark.parametrize("op", B8_PREFILL, ids=lambda o: o.name)
+@pytest.mark.parametrize("M", [17, 130, 300])
+def test_prefill_8bit(gpu, op, M):
+    b, s, z = workloads.make_weights(op, seed=op.N + M)
+    a = workloads.make_activations(M, op.K, seed=M + 5, kind="rmsnorm")
+    w = native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
+    log(f"8-bit prefill {op.name} M={M} {w.launch_info(M)}")
+    kernel, _ = check_against_oracle(w, a, b, s, z, None, op, f"{op.name} M={M}")
+    assert kernel == "mfma_w4_rb"
+    assert np.array_equal(w.gemm(a), w.gemm(a))   # deterministic
+    w.close()
+
+
+def test_prefill_8bit_every_split(gpu):
+    """Every tile width and K split of the 8-bit prefill (knobs 9 and 7), and the exact general
+    kernel it leaves to when switched off (knob 6 = 1) or when a scale is outside the fp16
+    range (|s| > 256)."""
+    op = Op("b8p_split", 2048, 520, 32, True, bits=8)
+    b, s, z = workloads.make_weights(op, seed=41)
+    a = workloads.make_activations(96, op.K, seed=42, kind="rmsnorm")
+    w = native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
+    try:
+        for nf in (1, 2, 4):            # 4 is not instantiated for 8-bit codes: the pick is used
+            for ksw in (1, 3, 16):
+                w.set_tuning(9, nf)
+                w.set_tuning(7, ksw)
+                log(f"8-bit prefill nf={nf} ksw={ksw} {w.launch_info(96)}")
+                kernel, _ = check_against_oracle(w, a, b, s, z, None, op, f"nf={nf} ksw={ksw}")
+                assert kernel == "mfma_w4_rb"
+        w.set_tuning(9, 0)
+        w.set_tuning(7, 0)
+        w.set_tuning(6, 1)
+        kernel, _ = check_against_oracle(w, a, b, s, z, None, op, "rb off")
+        assert kernel == "mfma_general"
+    finally:
+        w.set_tuning(9, 0)
+        w.set_tuning(7, 0)
+        w.set_tuning(6, 0)
+    w.close()
+    s_big = s.copy()
+    s_big[7] = np.float32(300.0)        # 255 * 300 overflows fp16
+    w = native.NBitsWeights(b, s_big, z, op.N, op.K, op.bits, op.block_size)
+    kernel, _ = check_against_oracle(w, a, b, s_big, z, None, op, "scale 300")
+    assert kernel == "mfma_general"
+    w.close()
