@@ -2,8 +2,8 @@
 
 Both run the same kernels on the same inputs, so their outputs must be equal bit for
 bit: on every kernel that uses a workspace (the small-M matrix-core GEMV with its K
-split, the register-operand prefill with its K-split reduce, the pipelined prefill
-with split tiles) and on one that does not (the decode GEMV, the exact general
+split, the register-operand prefill with its K-split reduce, for 4- and 8-bit codes, the
+pipelined prefill with split tiles) and on one that does not (the decode GEMV, the exact general
 prefill), two calls in a row through the C ABI, the second with a smaller input (the
 scratch keeps the first call's larger contents; its counters must start at zero again).
 """
@@ -36,6 +36,7 @@ CASES = [
     ("gemv", workloads.Op("gate", 3584, 18944, 32, True), 2, 1, "gemv_w4", 1.0),
     ("skinny", workloads.Op("up", 4096, 11008, 128, False), 16, 4, "skinny_w4", 1.0),
     ("rb", workloads.Op("up", 4096, 11008, 32, True), 128, 40, "mfma_w4_rb", 1.0),
+    ("rb8", workloads.Op("b8", 4096, 4096, 64, True, bits=8), 130, 24, "mfma_w4_rb", 1.0),
     ("pipe", workloads.Op("down", 11008, 4096, 32, True), 2048, 512, "mfma_w4_pipe", 1.0),
     ("exact", workloads.Op("wide", 1024, 768, 64, True), 300, 33, "mfma_w4", 1e6),
 ]
@@ -47,7 +48,7 @@ def test_noalloc_matches_gemm_dev(torch_cuda, case):
     name, op, m1, m2, kernel, sf = case
     b, s, z = workloads.make_weights(op, seed=71)
     s = (s * np.float32(sf)).astype(np.float32)
-    w = native.NBitsWeights(b, s, z, op.N, op.K, 4, op.block_size)
+    w = native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
     assert w.launch_info(m1)["kernel"] == kernel, w.launch_info(m1)
     stream = torch.cuda.current_stream().cuda_stream
     for M in (m1, m2):
