@@ -633,7 +633,11 @@ int batch_group(Weights* const* ws, const float* const* dA, int count, int M, in
     const Weights* w = ws[0];
     const Knobs kn = knobs_of(*w);
     if (M <= 0 || M > kGemvMaxM || !dA[0] || (reinterpret_cast<uintptr_t>(dA[0]) & 15)) return 1;
-    if (skinny_eligible(*w, kn, M)) return 1;   // the matrix-core small-M path launches per matrix
+    // Block size 128 takes the matrix-core small-M path per matrix from M = 3; other block
+    // sizes group the projections of one input on gemv_w4 where its panel fits (7B q+k+v,
+    // bs 32, M = 3 / 4: 10.5 / 12.0 us grouped against 27.9 / 28.4 us as three matrix-core
+    // launches; the small k and v leave that kernel's row tiles too few).
+    if (w->log2cpb == 2 && skinny_eligible(*w, kn, M)) return 1;
     int n = 1, ntot = w->N;
     while (n < count && n < kGemvMaxOps && dA[n] == dA[0] && gemv_groupable(*w, *ws[n])) {
         ntot += ws[n]->N;
@@ -1012,20 +1016,33 @@ int launch_pipe(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, floa
     return MS_HIP_OK;
 }
 
-// ---- skinny_w4: M <= 16 on the matrix cores at fp32-level accuracy (block size 128) ----
+// ---- skinny_w4: M <= 16 on the matrix cores at fp32-level accuracy (block sizes 32-128) ----
 
-// The small-M matrix-core path takes block size 128 (a block is one group of four MFMA
-// steps), K a multiple of 128, and 3 <= M <= 16: at M <= 2 gemv_w4 is faster (measured
-// on the 7B MLP shapes: M=2 13.2 / 12.5 us against 15.4 / 16.7 us; M=3 20.4 / 24.2 us
-// against 15.8 / 17.3 us), unless knob 4 says otherwise.
+// The small-M matrix-core path takes block sizes 32, 64 and 128 (a 128-k block is one group
+// of four MFMA steps; with 32 and 64 the code dwords are transposed so that each step is
+// one quantization block), K a multiple of 128, and M <= 16 by the rules below: at M <= 2
+// gemv_w4 is faster where its panel fits (measured on the Llama-2-7B MLP shapes, bs 128:
+// M=2 13.2 / 12.5 us against 15.4 / 16.7 us; M=3 20.4 / 24.2 us against 15.8 / 17.3 us),
+// unless knob 4 says otherwise.
 constexpr int kSkinnyMinM = 3;
 bool skinny_eligible(const Weights& w, const Knobs& kn, int M)
 {
-    if (kn.skinny() == 1 || !w.fast || w.log2cpb != 2 || (w.K % 128) != 0 || M < 1 || M > kSkinnyMT) return false;
+    if (kn.skinny() == 1 || !w.fast || w.log2cpb > 2 || (w.K % 128) != 0 || M < 1 || M > kSkinnyMT) return false;
     if ((int64_t)kSkinnyMT * w.K * 4 >= INT32_MAX) return false;
     // the partial-sum slices stay within the reduce's 32-bit buffer offsets
     if ((int64_t)(w.K / 128) * ((int64_t)kSkinnyMT * w.N + 3) / 4 * 16 >= kOOB) return false;
-    return kn.skinny() == 2 || M >= kSkinnyMinM;
+    if (kn.skinny() == 2) return true;
+    const bool gemv_fits = pick_gemv_config(w, kn, M, w.N) >= 0;
+    // Block size 128: from M = 3. Block sizes 32 and 64 (a scale per 32-k step): from M = 5,
+    // and from M = 3 for large matrices (N >= 8192); measured on the 7B decode launches
+    // (bs 32, zero points), gate 3584 x 18944 at M = 3 / 4: 19.0 / 19.3 us against 21.2 /
+    // 24.5 with gemv_w4, but o 3584 x 3584: 12.5 / 12.7 against 7.6 / 9.0 (few row tiles
+    // force a wide K split). Either way at M = 2 where the VALU GEMV's panel does not fit
+    // one workgroup (the panel kernel would take it: 7B down, K=18944, bs 32: 26.9 us
+    // against 23.2 us here).
+    if (M == 2) return !gemv_fits;
+    if (w.log2cpb == 2) return M >= kSkinnyMinM;
+    return M >= 5 || !gemv_fits || (M >= kSkinnyMinM && w.N >= 8192);
 }
 
 // Workgroups per row tile: each takes at most kSkinnyNB blocks and at least one; beyond
@@ -1082,7 +1099,13 @@ int launch_skinny(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, fl
     p.nb = w.nb;
     p.zrb = w.zrb;
     p.ksw = ksw;
-    hipLaunchKernelGGL(skinny_w4_kernel, dim3(tiles * ksw), dim3(256), 0, stream, p);
+    // quantization blocks per 128-k block: 1 (bs 128), 2 (bs 64), 4 (bs 32)
+    if (w.log2cpb == 2)
+        hipLaunchKernelGGL(skinny_w4_kernel<1>, dim3(tiles * ksw), dim3(256), 0, stream, p);
+    else if (w.log2cpb == 1)
+        hipLaunchKernelGGL(skinny_w4_kernel<2>, dim3(tiles * ksw), dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL(skinny_w4_kernel<4>, dim3(tiles * ksw), dim3(256), 0, stream, p);
     MS_HIP_CHECK(hipGetLastError());
     if (p.part) {
         hipLaunchKernelGGL(skinny_reduce_kernel, dim3((p.slice4 + 255) / 256), dim3(256), 0, stream, p.part, dY,

@@ -71,8 +71,11 @@ struct SkinnyParams {
     int ksw;                   // workgroups per row tile: ksw * kSkinnyNB >= K / 128, ksw <= K / 128
 };
 
+template <int QPB>
 __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
 {
+    static_assert(QPB == 1 || QPB == 2 || QPB == 4, "block sizes 128, 64, 32");
+    constexpr bool PS = QPB > 1;   // a scale per 32-k step (bs 32, 64), not per 128-k block
     constexpr int NF = kSkinnyNF, NB = kSkinnyNB;
     __shared__ __attribute__((aligned(16))) uint32_t lds_a[NB * kSkinnyBlockBytes / 4];
     __shared__ __attribute__((aligned(16))) float lds_e[NB * kSkinnyMT];
@@ -113,14 +116,38 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
     // and fragment made four times as many, and cost about 3 us of a 24 MB launch). The
     // lane that computes (row 16 f + ln, block lg) reads them from lane NB ln + lg.
     static_assert(16 * NB == kWave, "one lane per (row, block) of a fragment");
-    float sv[NF];
-    uint8_t zv[NF];
+    // With QPB > 1 quantization blocks per 128-k block (block sizes 32, 64), lane (ln, ls)
+    // of fragment f loads instead the QPB scales of its row's block ls (one aligned 8- or
+    // 16-byte load: nb is a multiple of QPB) and their zero-point nibbles, and the lane that
+    // computes step j of block lg takes them from lane (ln, lg).
+    float sv[NF][QPB];
+    uint32_t zv[NF];
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
-        const int n = n0 + 16 * f + lane / NB, blk = lane % NB, g = g0 + blk;
-        const bool ok = n < p.N && blk < cnt;
-        sv[f] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc, ok ? n * p.nb * 4 + g * 4 : kOOB, 0, 0));
-        zv[f] = __builtin_amdgcn_raw_buffer_load_b8(rz, ok ? n * p.zrb + (g >> 1) : kOOB, 0, 0);
+        if constexpr (PS) {
+            const int n = n0 + 16 * f + ln, q0 = (g0 + ls) * QPB;
+            const bool ok = n < p.N && ls < cnt;
+            const int so = ok ? (n * p.nb + q0) * 4 : kOOB;
+            if constexpr (QPB == 4) {
+                const float4 v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsc, so, 0, 0));
+                sv[f][0] = v.x;
+                sv[f][1] = v.y;
+                sv[f][2] = v.z;
+                sv[f][3] = v.w;
+                zv[f] = __builtin_amdgcn_raw_buffer_load_b16(rz, ok ? n * p.zrb + q0 / 2 : kOOB, 0, 0);
+            } else {
+                const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rsc, so, 0, 0));
+                sv[f][0] = __builtin_bit_cast(float, v.x);
+                sv[f][1] = __builtin_bit_cast(float, v.y);
+                zv[f] = __builtin_amdgcn_raw_buffer_load_b8(rz, ok ? n * p.zrb + q0 / 2 : kOOB, 0, 0);
+            }
+        } else {
+            const int n = n0 + 16 * f + lane / NB, blk = lane % NB, g = g0 + blk;
+            const bool ok = n < p.N && blk < cnt;
+            sv[f][0] = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(rsc, ok ? n * p.nb * 4 + g * 4 : kOOB, 0, 0));
+            zv[f] = __builtin_amdgcn_raw_buffer_load_b8(rz, ok ? n * p.zrb + (g >> 1) : kOOB, 0, 0);
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -182,7 +209,11 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
                 hw[t] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
                 lw[t] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
             }
-            const int s = pl >> 2, j = pl & 3, c = ((s & 1) << 3) | (j << 1);
+            // k = 8 pl .. 8 pl + 7 of the block is step j, lane group s: k = 32 s + 8 j
+            // per 128-k block scale (the codes' 16-byte chunk s is one step's k range of
+            // lane group s), k = 32 j + 8 s with a scale per 32-k step (after the 4 x 4
+            // transpose of the code dwords, step j is quantization block j).
+            const int s = PS ? (pl & 3) : (pl >> 2), j = PS ? (pl >> 2) : (pl & 3), c = ((s & 1) << 3) | (j << 1);
             const int base = (lg * 4 + j) * 2 * kSkinnyStepBytes + s * 256;
             *reinterpret_cast<u32x4_t*>(&lds_a[(base + (m ^ c) * 16) / 4]) = u32x4_t{hw[0], hw[1], hw[2], hw[3]};
             *reinterpret_cast<u32x4_t*>(&lds_a[(base + kSkinnyStepBytes + (m ^ (c | 1)) * 16) / 4]) =
@@ -208,44 +239,89 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
 #pragma unroll
     for (int lg = 0; lg < NB; ++lg) {
         if (lg >= cnt) break;
-        floatx4_t th[NF], tl[NF];
-        uint32_t zb[NF];
-        float sc[NF];
-#pragma unroll
-        for (int f = 0; f < NF; ++f) {
-            th[f] = floatx4_t{};
-            tl[f] = floatx4_t{};
-            const int src = (NB * ln + lg) * 4;   // ds_bpermute byte address of lane NB ln + lg
-            sc[f] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, sv[f])));
-            const uint32_t zq = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)zv[f]);
-            const uint32_t zp = ((zq >> (((g0 + lg) & 1) * 4)) & 0x0F) + zdef;
-            zb[f] = kHalfMagic | (zp << 16) | zp;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const half8_t ah = *reinterpret_cast<const half8_t*>(&lds_a[(lg * kSkinnyBlockBytes + aoff[j][0]) / 4]);
-            const half8_t al = *reinterpret_cast<const half8_t*>(&lds_a[(lg * kSkinnyBlockBytes + aoff[j][1]) / 4]);
-#pragma unroll
-            for (int f = 0; f < NF; ++f) {
-                const uint32_t x = j == 0 ? c[lg][f].x : j == 1 ? c[lg][f].y : j == 2 ? c[lg][f].z : c[lg][f].w;
-                const h2_t z2 = as_h2(zb[f]);
-                const uint32_t o0 = as_u32(as_h2(and_or(x, 0x000F000Fu, kHalfMagic)) - z2);
-                const uint32_t o1 = as_u32(as_h2(and_or(x >> 4, 0x000F000Fu, kHalfMagic)) - z2);
-                const uint32_t o2 = as_u32(as_h2(and_or(x >> 8, 0x000F000Fu, kHalfMagic)) - z2);
-                const uint32_t o3 = as_u32(as_h2(and_or(x >> 12, 0x000F000Fu, kHalfMagic)) - z2);
-                const half8_t bq = __builtin_bit_cast(half8_t, u32x4_t{o0, o1, o2, o3});
-                th[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq, th[f], 0, 0, 0);
-                tl[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq, tl[f], 0, 0, 0);
-            }
-        }
-        // th / tl[f][v]: block sums for activation row m = 4 ls + v and weight row
-        // n0 + 16 f + ln; times 2^e[m] (exact) and s[n], into the running sum.
         const float4 e4 = *reinterpret_cast<const float4*>(&lds_e[lg * kSkinnyMT + 4 * ls]);
         const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
+        if constexpr (PS) {
+            // Transpose the code dwords across the four 16-lane rows (lane (ln, s) had
+            // dword j of quantization block s; after it, dword s of block j): step j is
+            // block j. The permlane swaps exchange whole rows, lane ln stays lane ln.
+            uint32_t t[NF][4];
 #pragma unroll
-        for (int f = 0; f < NF; ++f) {
+            for (int f = 0; f < NF; ++f) {
+                const auto a0 = __builtin_amdgcn_permlane32_swap(c[lg][f].x, c[lg][f].z, false, false);
+                const auto a1 = __builtin_amdgcn_permlane32_swap(c[lg][f].y, c[lg][f].w, false, false);
+                const auto b0 = __builtin_amdgcn_permlane16_swap(a0[0], a1[0], false, false);
+                const auto b1 = __builtin_amdgcn_permlane16_swap(a0[1], a1[1], false, false);
+                t[f][0] = b0[0];
+                t[f][1] = b0[1];
+                t[f][2] = b1[0];
+                t[f][3] = b1[1];
+            }
+            const int src = (ln + 16 * lg) * 4;   // ds_bpermute byte address of lane (ln, lg)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) acc[f][v] = __builtin_fmaf((th[f][v] + tl[f][v]) * ev[v], sc[f], acc[f][v]);
+            for (int j = 0; j < 4; ++j) {
+                const int qj = j * QPB / 4;   // quantization block of step j within block lg
+                const half8_t ah = *reinterpret_cast<const half8_t*>(&lds_a[(lg * kSkinnyBlockBytes + aoff[j][0]) / 4]);
+                const half8_t al = *reinterpret_cast<const half8_t*>(&lds_a[(lg * kSkinnyBlockBytes + aoff[j][1]) / 4]);
+#pragma unroll
+                for (int f = 0; f < NF; ++f) {
+                    const float sc =
+                        __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, sv[f][qj])));
+                    const uint32_t zq = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)zv[f]);
+                    const uint32_t zp = ((zq >> (4 * qj)) & 0x0F) + zdef;
+                    const h2_t z2 = as_h2(kHalfMagic | (zp << 16) | zp);
+                    const uint32_t x = t[f][j];
+                    const uint32_t o0 = as_u32(as_h2(and_or(x, 0x000F000Fu, kHalfMagic)) - z2);
+                    const uint32_t o1 = as_u32(as_h2(and_or(x >> 4, 0x000F000Fu, kHalfMagic)) - z2);
+                    const uint32_t o2 = as_u32(as_h2(and_or(x >> 8, 0x000F000Fu, kHalfMagic)) - z2);
+                    const uint32_t o3 = as_u32(as_h2(and_or(x >> 12, 0x000F000Fu, kHalfMagic)) - z2);
+                    const half8_t bq = __builtin_bit_cast(half8_t, u32x4_t{o0, o1, o2, o3});
+                    const floatx4_t th = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq, floatx4_t{}, 0, 0, 0);
+                    const floatx4_t tl = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq, floatx4_t{}, 0, 0, 0);
+                    // step sums for activation row m = 4 ls + v and weight row n0 + 16 f + ln:
+                    // times 2^e[m] (exact) and the step's scale, into the running sum
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) acc[f][v] = __builtin_fmaf((th[v] + tl[v]) * ev[v], sc, acc[f][v]);
+                }
+            }
+        } else {
+            floatx4_t th[NF], tl[NF];
+            uint32_t zb[NF];
+            float sc[NF];
+#pragma unroll
+            for (int f = 0; f < NF; ++f) {
+                th[f] = floatx4_t{};
+                tl[f] = floatx4_t{};
+                const int src = (NB * ln + lg) * 4;   // ds_bpermute byte address of lane NB ln + lg
+                sc[f] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, sv[f][0])));
+                const uint32_t zq = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)zv[f]);
+                const uint32_t zp = ((zq >> (((g0 + lg) & 1) * 4)) & 0x0F) + zdef;
+                zb[f] = kHalfMagic | (zp << 16) | zp;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const half8_t ah = *reinterpret_cast<const half8_t*>(&lds_a[(lg * kSkinnyBlockBytes + aoff[j][0]) / 4]);
+                const half8_t al = *reinterpret_cast<const half8_t*>(&lds_a[(lg * kSkinnyBlockBytes + aoff[j][1]) / 4]);
+#pragma unroll
+                for (int f = 0; f < NF; ++f) {
+                    const uint32_t x = j == 0 ? c[lg][f].x : j == 1 ? c[lg][f].y : j == 2 ? c[lg][f].z : c[lg][f].w;
+                    const h2_t z2 = as_h2(zb[f]);
+                    const uint32_t o0 = as_u32(as_h2(and_or(x, 0x000F000Fu, kHalfMagic)) - z2);
+                    const uint32_t o1 = as_u32(as_h2(and_or(x >> 4, 0x000F000Fu, kHalfMagic)) - z2);
+                    const uint32_t o2 = as_u32(as_h2(and_or(x >> 8, 0x000F000Fu, kHalfMagic)) - z2);
+                    const uint32_t o3 = as_u32(as_h2(and_or(x >> 12, 0x000F000Fu, kHalfMagic)) - z2);
+                    const half8_t bq = __builtin_bit_cast(half8_t, u32x4_t{o0, o1, o2, o3});
+                    th[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq, th[f], 0, 0, 0);
+                    tl[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq, tl[f], 0, 0, 0);
+                }
+            }
+            // th / tl[f][v]: block sums for activation row m = 4 ls + v and weight row
+            // n0 + 16 f + ln; times 2^e[m] (exact) and s[n], into the running sum.
+#pragma unroll
+            for (int f = 0; f < NF; ++f) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[f][v] = __builtin_fmaf((th[f][v] + tl[f][v]) * ev[v], sc[f], acc[f][v]);
+            }
         }
     }
 

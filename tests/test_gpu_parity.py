@@ -129,15 +129,18 @@ def test_gemv_parity(gpu, op, M):
 SKINNY_SPLITS = [(640, 0), (640, 2), (512, 1), (1408, 0), (1408, 9)]
 
 
+@pytest.mark.parametrize("bs", [128, 64, 32])
 @pytest.mark.parametrize("K,ksw", SKINNY_SPLITS, ids=lambda v: str(v))
 @pytest.mark.parametrize("zp", [False, True], ids=["nozp", "zp"])
-def test_skinny_every_m_dynamic_range(gpu, zp, K, ksw):
-    """The small-M matrix-core path (block size 128) for every M in 1..16 (M = 1 forced),
-    on a ragged shape (N=333 is no multiple of the 128-row tiles), with activations spanning
-    1e-4..1e5 across rows and blocks and a lone outlier: the per-block power-of-two split of
-    A keeps the GEMV bar, whatever the number of workgroups per row tile. Two calls agree
-    bit for bit."""
-    op = workloads.Op("sk", K, 333, 128, zp)
+def test_skinny_every_m_dynamic_range(gpu, zp, K, ksw, bs):
+    """The small-M matrix-core path for every M in 1..16 (M = 1 forced), on a ragged shape
+    (N=333 is no multiple of the 128-row tiles), with activations spanning 1e-4..1e5 across
+    rows and blocks and a lone outlier: the per-block power-of-two split of A keeps the GEMV
+    bar, whatever the number of workgroups per row tile. Block size 128 applies the scale
+    per 128-k block; 64 and 32 per 32-k step, after the transpose of the code dwords across
+    the wave's rows that makes each MFMA step one quantization block. Two calls agree bit
+    for bit."""
+    op = workloads.Op("sk", K, 333, bs, zp)
     b, s, z, w = weights_for(op, seed=70 + zp)
     rng = np.random.default_rng(71)
     try:
@@ -151,7 +154,7 @@ def test_skinny_every_m_dynamic_range(gpu, zp, K, ksw):
             info = w.launch_info(M)
             assert info["kernel"] == "skinny_w4", info
             y = w.gemm(a)
-            assert_gemv_close(y, oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, 128), f"skinny M={M} zp={zp} K={K}")
+            assert_gemv_close(y, oracle.matmul_nbits(a, b, s, z, op.N, op.K, 4, bs), f"skinny M={M} zp={zp} K={K} bs={bs}")
             assert np.array_equal(w.gemm(a), y), M
     finally:
         native.set_tuning(4, 0)
@@ -764,14 +767,17 @@ def _cancelling_weights(op, seed):
 
 
 @pytest.mark.parametrize("M,bs,kernel", [(1, 32, "gemv_w4"), (2, 32, "gemv_w4"), (8, 32, "gemv_w4_panel"),
-                                         (1, 128, "gemv_w4"), (8, 128, "skinny_w4")])
+                                         (8, 32, "skinny_w4"), (1, 128, "gemv_w4"), (8, 128, "skinny_w4")])
 def test_gemv_exact_zero_point_differences(gpu, M, bs, kernel):
     """Weight rows that are mostly q == zp blocks against activations up to 1e4: the decode
     kernels form a_k (q_k - zp) exactly, so they meet the 1e-5 * ||y_row||_inf bar where a
-    folded sum_k a_k q_k - zp * sum_k a_k would not."""
+    folded sum_k a_k q_k - zp * sum_k a_k would not. (The panel kernel is reached with the
+    small-M matrix-core path switched off, knob 4 = 1.)"""
     op = workloads.Op("cancel", 4096, 2048, bs, True)
     b, s, z = _cancelling_weights(op, seed=bs + M)
     w = native.NBitsWeights(b, s, z, op.N, op.K, 4, bs)
+    if kernel == "gemv_w4_panel":
+        w.set_tuning(4, 1)
     assert w.launch_info(M)["kernel"] == kernel
     a = np.random.default_rng(M).uniform(5e3, 1e4, size=(M, op.K)).astype(np.float32)
     y = w.gemm(a)
