@@ -21,10 +21,11 @@
 //     bytes: the lane loads its 32 codes as two chunks, and dwords 2j, 2j + 1 make step j
 //     (dequant8_f16_b8, the same pair order and rounding);
 //   * the scales and zero points come from the handle's chunk-major copy (rb_chunk_layout
-//     _kernel, built once): scale and zero point of (128-k block g, row n, chunk c) at
-//     (g N + n) 4 + c, so a fragment's 16 rows read 256 contiguous bytes of scales and 64
-//     of zero points per block (from the operator's [N][nb] layout they touched 16 lines
-//     each; that cost 2-23 us of 43-127 us on the 7B prefill shapes);
+//     _kernel, built once): one dword per (128-k block g, row n, chunk c) at (g N + n) 4 + c
+//     holding fl16(s) in its low half and the fp16 1024 + zp in its high half (the two
+//     constants of the dequant, exact), so a fragment's 16 rows read 256 contiguous bytes
+//     per block (from the operator's [N][nb] layout they touched 16 lines each; that cost
+//     2-23 us of 43-127 us on the 7B prefill shapes);
 //   * A goes through LDS, double-buffered, one block (128 rows x 128 k, 32 KB) per buffer,
 //     laid out so that the A operand of (step j, fragment f) is 1 KB read by the 64 lanes
 //     in order (no bank conflicts). The next block's A is loaded into registers while the
@@ -64,8 +65,7 @@ constexpr int kRbBufBytes = kRbBM * 128 * 2;   // one block of fp16 A
 
 struct RbParams {
     const uint8_t* b;          // [N][row_bytes]
-    const float* s4;           // [K / 128][N][4] scale of each 32-code chunk
-    const uint8_t* z4;         // [K / 128][N][4] zero point of each 32-code chunk (8 without zero points)
+    const uint32_t* sz4;       // [K / 128][N][4] fl16(s) | fp16(1024 + zp) << 16 of each 32-code chunk
     const _Float16* a16;       // [M][K] fp16, permuted within 8-k groups, row m scaled by 2^-rexp[m]
     float* out;                // the workspace: ksw slices of `slice` floats
     int64_t slice;             // M * N rounded up to a multiple of 4 (16-byte aligned slices)
@@ -96,8 +96,7 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
 
     const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(p.a16, p.M * p.K * 2);
     const __amdgpu_buffer_rsrc_t rb_ = buffer_rsrc(p.b, p.N * p.row_bytes);
-    const __amdgpu_buffer_rsrc_t rsc = buffer_rsrc(p.s4, G * p.N * 16);
-    const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(p.z4, G * p.N * 4);
+    const __amdgpu_buffer_rsrc_t rsc = buffer_rsrc(p.sz4, G * p.N * 16);
 
     // ---- A staging: thread t moves chunks q = t + 256 u (u = 0..7) of a block; chunk q is
     // (step j = q >> 9, fragment f = (q >> 6) & 7, s = (q >> 4) & 3, row r = q & 15) and
@@ -124,19 +123,17 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
     };
 
     // ---- weights: lane (ln, ls) of fragment f is row n0 + 64 wave + 16 f + ln ----
-    int cb[NF], sb[NF], zb[NF];
+    int cb[NF], sb[NF];
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
         const int n = n0 + 16 * NF * wave + 16 * f + ln;
         const bool in = n < p.N;
         cb[f] = in ? n * p.row_bytes + ls * 16 * CW : kOOB;
         sb[f] = in ? n * 16 + ls * 4 : kOOB;
-        zb[f] = in ? n * 4 + ls : kOOB;
     }
     struct WBlk {
         u32x4_t c[NF][CW];
-        float s[NF];
-        uint8_t z[NF];   // a byte, so the compiler cannot hoist a widening ahead of the block's wait
+        uint32_t sz[NF];
     };
     WBlk w[kRbRing];
     auto load_w = [&](WBlk& wb, int i) {
@@ -147,9 +144,7 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
 #pragma unroll
             for (int h = 0; h < CW; ++h)
                 wb.c[f][h] = __builtin_amdgcn_raw_buffer_load_b128(rb_, okf ? cb[f] + (g0 + i) * BLK + 16 * h : kOOB, 0, 0);
-            wb.s[f] = __builtin_bit_cast(
-                float, __builtin_amdgcn_raw_buffer_load_b32(rsc, okf ? sb[f] + (g0 + i) * p.N * 16 : kOOB, 0, 0));
-            wb.z[f] = __builtin_amdgcn_raw_buffer_load_b8(rz, okf ? zb[f] + (g0 + i) * p.N * 4 : kOOB, 0, 0);
+            wb.sz[f] = __builtin_amdgcn_raw_buffer_load_b32(rsc, okf ? sb[f] + (g0 + i) * p.N * 16 : kOOB, 0, 0);
         }
     };
 
@@ -161,14 +156,12 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
     }
 
     // Per-block dequant constants of ring slot wb (block g0 + i): (1024 + zp) and fl16(s),
-    // both twice, per fragment.
+    // both twice, per fragment (one v_perm each from the packed dword).
     auto prep = [&](const WBlk& wb, int i, uint32_t (&zz)[NF], h2_t (&s2)[NF]) {
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
-            const uint32_t zp = wb.z[f];
-            zz[f] = kHalfMagic | (zp << 16) | zp;
-            const _Float16 sh = (_Float16)wb.s[f];
-            s2[f] = h2_t{sh, sh};
+            zz[f] = __builtin_amdgcn_perm(wb.sz[f], wb.sz[f], 0x03020302u);
+            s2[f] = as_h2(__builtin_amdgcn_perm(wb.sz[f], wb.sz[f], 0x01000100u));
         }
     };
     // A operand of (step j, fragment mf): 1 KB, lane-ordered.
@@ -213,19 +206,24 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
     }
     __syncthreads();
 
-    // ---- main loop, unrolled by the ring depth so each ring slot is a register set ----
+    // ---- main loop ----
     // Block i: (A(i+1) registers -> LDS; issue A(i+2)); 32 groups (step j, fragment mf) of
-    // 4 MFMAs; the A operand of group t + 2 is read under the MFMAs of group t (a 3-entry
-    // window), and the B operands of step j + 1 are dequantized one fragment per group
-    // under the first 4 groups of step j (the last step prepares step 0 of block i+1 from
-    // the next ring slot); then W(i+3) goes into the slot just used; barrier. At the top of
+    // NF MFMAs, in chunks of RC groups: the A operands of a chunk (RC fragments of 1 KB,
+    // lane-ordered) are read from LDS in one burst while the previous chunk computes
+    // (sched_barrier keeps each burst ahead of the chunk before it), and the B operands of
+    // step j + 1 are dequantized one fragment per group under the first NF groups of step j
+    // (the last step prepares step 0 of block i+1 from the next ring slot); then W(i+3)
+    // goes into the slot just used, which becomes the ring's last; barrier. At the top of
     // block i the outstanding loads are A(i+1) then W(i+2), so the A store waits for A(i+1)
-    // alone.
+    // alone. (A window of three single-fragment reads, one per group, was compiled into a
+    // read followed by its wait before every group's MFMAs.) RC = 8 (a whole step) where
+    // the registers allow, 4 at NF = 4.
+    constexpr int RC = NF == 4 ? 4 : 8, NCH = 4 * MF / RC;
     auto body = [&](int i, WBlk& wb, const WBlk& wbn) {
         const int buf = i & 1;
-        half8_t aw[3];
-        aw[0] = read_a1(buf, 0, 0);
-        aw[1] = read_a1(buf, 0, 1);
+        half8_t aw[2][RC];
+#pragma unroll
+        for (int r = 0; r < RC; ++r) aw[0][r] = read_a1(buf, r / MF, r % MF);
         if (i + 1 < cnt) store_a((i + 1) & 1);
         load_a(i + 2);
         __builtin_amdgcn_sched_barrier(0);
@@ -237,39 +235,50 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
 #pragma unroll
         for (int f = 0; f < NF; ++f) bq[f] = bq0[f];
 #pragma unroll
-        for (int t = 0; t < 4 * MF; ++t) {
-            const int j = t / MF, mf = t % MF;
-            if (t + 2 < 4 * MF) aw[(t + 2) % 3] = read_a1(buf, (t + 2) / MF, (t + 2) % MF);
+        for (int c = 0; c < NCH; ++c) {
+            if (c + 1 < NCH) {
 #pragma unroll
-            for (int f = 0; f < NF; ++f)
-                acc[mf][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[t % 3], bq[f], acc[mf][f], 0, 0, 0);
-            if (mf < NF) bqn[mf] = j < 3 ? deq1(wb, j + 1, mf, zz[mf], s2[mf]) : deq1(wbn, 0, mf, zzn[mf], s2n[mf]);
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            if (t + 2 < 4 * MF) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-#pragma unroll
-            for (int u = 0; u < NF - 1; ++u) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+                for (int r = 0; r < RC; ++r) {
+                    const int t = (c + 1) * RC + r;
+                    aw[(c + 1) & 1][r] = read_a1(buf, t / MF, t % MF);
+                }
             }
-            if (mf == MF - 1) {
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int f = 0; f < NF; ++f) bq[f] = bqn[f];
+            for (int r = 0; r < RC; ++r) {
+                const int t = c * RC + r, j = t / MF, mf = t % MF;
+#pragma unroll
+                for (int f = 0; f < NF; ++f)
+                    acc[mf][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[c & 1][r], bq[f], acc[mf][f], 0, 0, 0);
+                if (mf < NF) bqn[mf] = j < 3 ? deq1(wb, j + 1, mf, zz[mf], s2[mf]) : deq1(wbn, 0, mf, zzn[mf], s2n[mf]);
+#pragma unroll
+                for (int u = 0; u < NF; ++u) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+                }
+                if (mf == MF - 1) {
+#pragma unroll
+                    for (int f = 0; f < NF; ++f) bq[f] = bqn[f];
+                }
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int f = 0; f < NF; ++f) bq0[f] = bq[f];
         load_w(wb, i + kRbRing);
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
     };
-    for (int i = 0; i < cnt; i += kRbRing) {
+    // One body per iteration and the ring rotated by value (a few register moves per
+    // block): with the body unrolled once per ring slot, three exits and three register
+    // sets per slot, the register allocator moved every accumulator through VGPRs around
+    // its MFMAs (four v_accvgpr_write per MFMA at NF = 4).
+    for (int i = 0; i < cnt; ++i) {
         body(i, w[0], w[1]);
-        if (i + 1 >= cnt) break;
-        body(i + 1, w[1], w[2]);
-        if (i + 2 >= cnt) break;
-        body(i + 2, w[2], w[0]);
+        const WBlk t0 = w[0];
+        w[0] = w[1];
+        w[1] = w[2];
+        w[2] = t0;
     }
 
     // ---- epilogue: acc[mf][f][v] is out[m0 + 16 mf + 4 ls + v][n0 + 16 NF wave + 16 f + ln] ----
@@ -336,12 +345,12 @@ __global__ __launch_bounds__(256) void rb_reduce_kernel(const float4* __restrict
 }
 
 // The chunk-major copy of a handle's scales and zero points that mfma_w4_rb reads: entry
-// (g, n, c) is the scale and the zero point (2^(bits-1) without zero points) of the
-// quantization block that holds codes 128 g + 32 c .. + 31 of row n. Exact copies.
+// (g, n, c) packs fl16 of the scale and 1024 + the zero point (2^(bits-1) without zero
+// points) of the quantization block that holds codes 128 g + 32 c .. + 31 of row n.
 __global__ __launch_bounds__(256) void rb_chunk_layout_kernel(const float* __restrict__ scales,
-                                                              const uint8_t* __restrict__ zp, float* __restrict__ s4,
-                                                              uint8_t* __restrict__ z4, int N, int G, int nb, int zrb,
-                                                              int log2bs, int bits)
+                                                              const uint8_t* __restrict__ zp,
+                                                              uint32_t* __restrict__ sz4, int N, int G, int nb,
+                                                              int zrb, int log2bs, int bits)
 {
     const int64_t total = (int64_t)G * N * 4;
     for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
@@ -349,11 +358,15 @@ __global__ __launch_bounds__(256) void rb_chunk_layout_kernel(const float* __res
         const int64_t gn = e >> 2;
         const int g = (int)(gn / N), n = (int)(gn - (int64_t)g * N);
         const int blk = (g * 128 + 32 * c) >> log2bs;
-        s4[e] = scales[(int64_t)n * nb + blk];
+        uint32_t z;
         if (bits == 8)
-            z4[e] = zp ? zp[(int64_t)n * zrb + blk] : (uint8_t)128;
+            z = zp ? zp[(int64_t)n * zrb + blk] : 128u;
         else
-            z4[e] = zp ? (uint8_t)((zp[(int64_t)n * zrb + (blk >> 1)] >> ((blk & 1) * 4)) & 0x0F) : (uint8_t)8;
+            z = zp ? (zp[(int64_t)n * zrb + (blk >> 1)] >> ((blk & 1) * 4)) & 0x0Fu : 8u;
+        // fl16(s) (round to nearest even, the dequant's rounding of the scale) and the fp16
+        // 1024 + zp (exact for zp < 1024)
+        const _Float16 sh = (_Float16)scales[(int64_t)n * nb + blk];
+        sz4[e] = (uint32_t)__builtin_bit_cast(uint16_t, sh) | ((0x6400u | z) << 16);
     }
 }
 

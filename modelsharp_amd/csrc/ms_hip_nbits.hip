@@ -234,8 +234,7 @@ struct Weights {
     int* d_wexp = nullptr;      // general formats: row exponents of the weights [N]
     // mfma_w4_rb's chunk-major scales / zero points [K / 128][N][4], built by the first
     // eager call that takes it (rb_ready then 1; guarded by ws_mu)
-    float* d_s4 = nullptr;
-    uint8_t* d_z4 = nullptr;
+    uint32_t* d_sz4 = nullptr;
     std::atomic<int> rb_ready{0};
     std::atomic<int> knob[kNumKnobs];   // MS_HIP_TUNING_INHERIT: the process default
     // Device-side failure report: a split-K hand-off that gives up writes a nonzero code
@@ -321,8 +320,7 @@ void free_weights(Weights& w)
 {
     if (w.d_b) (void)hipFree(w.d_b);
     if (w.d_scales) (void)hipFree(w.d_scales);
-    if (w.d_s4) (void)hipFree(w.d_s4);
-    if (w.d_z4) (void)hipFree(w.d_z4);
+    if (w.d_sz4) (void)hipFree(w.d_sz4);
     if (w.d_zp) (void)hipFree(w.d_zp);
     if (w.d_zpf) (void)hipFree(w.d_zpf);
     if (w.d_wexp) (void)hipFree(w.d_wexp);
@@ -1216,8 +1214,7 @@ int launch_rb(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, float*
     launch_a_rows_f16(dA, a16, rexp, M, w.K, stream);
     RbParams p;
     p.b = w.d_b;
-    p.s4 = w.d_s4;
-    p.z4 = w.d_z4;
+    p.sz4 = w.d_sz4;
     p.a16 = reinterpret_cast<const _Float16*>(a16);
     p.out = part;
     p.slice = L.slice;
@@ -1265,11 +1262,10 @@ int ensure_rb_layout(Weights& w, hipStream_t stream)
     }
     const int G = w.K / 128;
     const int64_t entries = (int64_t)G * w.N * 4;
-    if (!w.d_s4 && hipMalloc(&w.d_s4, (size_t)entries * sizeof(float)) != hipSuccess) return -1;
-    if (!w.d_z4 && hipMalloc(&w.d_z4, (size_t)entries) != hipSuccess) return -1;
+    if (!w.d_sz4 && hipMalloc(&w.d_sz4, (size_t)entries * sizeof(uint32_t)) != hipSuccess) return -1;
     const int grid = (int)std::min<int64_t>((entries + 255) / 256, 8192);
     hipLaunchKernelGGL(rb_chunk_layout_kernel, dim3(grid), dim3(256), 0, stream, w.d_scales,
-                       w.has_zp ? w.d_zp : nullptr, w.d_s4, w.d_z4, w.N, G, w.nb, w.zrb, log2_exact(w.bs), w.bits);
+                       w.has_zp ? w.d_zp : nullptr, w.d_sz4, w.N, G, w.nb, w.zrb, log2_exact(w.bs), w.bits);
     if (hipGetLastError() != hipSuccess || hipStreamSynchronize(stream) != hipSuccess) return -1;
     w.rb_ready.store(1, std::memory_order_release);
     return 1;
