@@ -298,7 +298,7 @@ constexpr GemvConfig kGemvConfigs[] = {
     {4, 16, 1, 2, 1, 2},  {4, 16, 1, 4, 1, 2},  {4, 32, 1, 4, 1, 2},  {4, 64, 1, 2, 1, 2},  {4, 16, 4, 2, 1, 2},
     {4, 32, 2, 2, 1, 2},  {8, 32, 1, 4, 1, 2},  {8, 16, 2, 4, 1, 2},  {8, 16, 4, 2, 1, 2},  {16, 16, 4, 2, 1, 2},
     {16, 32, 2, 2, 1, 2}, {4, 16, 1, 2, 2, 2},  {4, 16, 1, 4, 2, 2},  {4, 32, 1, 2, 2, 2},  {4, 64, 1, 2, 2, 2},
-    {8, 16, 2, 2, 2, 2},  {4, 16, 1, 1, 2, 2},  {8, 64, 1, 1, 2, 2},
+    {8, 16, 2, 2, 2, 2},  {4, 16, 1, 1, 2, 2},  {8, 64, 1, 1, 2, 2},  {16, 16, 4, 1, 1, 2},
 };
 constexpr int kNumGemvConfigs = sizeof(kGemvConfigs) / sizeof(kGemvConfigs[0]);
 constexpr int kGemvMaxM = 4;

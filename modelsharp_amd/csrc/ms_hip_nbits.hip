@@ -543,7 +543,7 @@ int pick_gemv_config(const Weights& w, const Knobs& kn, int M, int N)
     static constexpr int kLargeM4[] = {7, 6, 0};        // M <= 4, N >= 16384
     static constexpr int kMidM4[] = {15, 7, 8};         // M <= 4, N >= 4096
     static constexpr int kSmallM4[] = {6, 8, 0};        // M <= 4
-    static constexpr int kWide[] = {9, 10};             // panels that need 16 waves to stage
+    static constexpr int kWide[] = {18, 9, 10};         // panels that need 16 waves to stage
     const int C = w.K / 32;
     auto usable = [&](int ci) {
         const GemvConfig& c = kGemvConfigs[ci];
@@ -560,7 +560,7 @@ int pick_gemv_config(const Weights& w, const Knobs& kn, int M, int N)
            : N >= 2048  ? first_of(kSmallM2, 4) : first_of(kTinyM2, 3);
     else
         ci = N >= 16384 ? first_of(kLargeM4, 3) : N >= 4096 ? first_of(kMidM4, 3) : first_of(kSmallM4, 3);
-    if (ci < 0) ci = first_of(kWide, 2);
+    if (ci < 0) ci = first_of(kWide, 3);
     if (ci < 0) {   // short rows (a lane gets a single step): any config that fits
         for (int i = 0; i < kNumGemvConfigs && ci < 0; ++i)
             if (gemv_config_fits(w, M, kGemvConfigs[i])) ci = i;
