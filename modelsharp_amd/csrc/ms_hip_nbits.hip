@@ -631,11 +631,14 @@ int batch_group(Weights* const* ws, const float* const* dA, int count, int M, in
     const Weights* w = ws[0];
     const Knobs kn = knobs_of(*w);
     if (M <= 0 || M > kGemvMaxM || !dA[0] || (reinterpret_cast<uintptr_t>(dA[0]) & 15)) return 1;
-    // Block size 128 takes the matrix-core small-M path per matrix from M = 3; other block
-    // sizes group the projections of one input on gemv_w4 where its panel fits (7B q+k+v,
-    // bs 32, M = 3 / 4: 10.5 / 12.0 us grouped against 27.9 / 28.4 us as three matrix-core
-    // launches; the small k and v leave that kernel's row tiles too few).
-    if (w->log2cpb == 2 && skinny_eligible(*w, kn, M)) return 1;
+    // Block size 128 takes the matrix-core small-M path per matrix from M = 3, and so do the
+    // large matrices of other block sizes from M = 4 (7B gate and up, bs 32, M = 4: two
+    // launches of 19.3 us against 41.8 us grouped on gemv_w4; at M = 3 the grouped launch
+    // is faster, 35.1 against 2 x 19.0 us). Otherwise the projections of one input group on
+    // gemv_w4 where its panel fits (7B q+k+v, bs 32, M = 3 / 4: 10.5 / 12.0 us grouped
+    // against 27.9 / 28.4 us as three matrix-core launches; the small k and v leave that
+    // kernel's row tiles too few).
+    if (skinny_eligible(*w, kn, M) && (w->log2cpb == 2 || (M >= 4 && w->N >= 8192))) return 1;
     int n = 1, ntot = w->N;
     while (n < count && n < kGemvMaxOps && dA[n] == dA[0] && gemv_groupable(*w, *ws[n])) {
         ntot += ws[n]->N;
@@ -1035,9 +1038,11 @@ bool skinny_eligible(const Weights& w, const Knobs& kn, int M)
     // and from M = 3 for large matrices (N >= 8192); measured on the 7B decode launches
     // (bs 32, zero points), gate 3584 x 18944 at M = 3 / 4: 19.0 / 19.3 us against 21.2 /
     // 24.5 with gemv_w4, but o 3584 x 3584: 12.5 / 12.7 against 7.6 / 9.0 (few row tiles
-    // force a wide K split). Either way at M = 2 where the VALU GEMV's panel does not fit
-    // one workgroup (the panel kernel would take it: 7B down, K=18944, bs 32: 26.9 us
-    // against 23.2 us here).
+    // force a wide K split). At M = 5 the panel kernel is a little faster on the short-K
+    // q+k+v and o (27.8 / 12.4 against 28.8 / 12.8 us) and far slower on down (K=18944:
+    // 54.1 against 24.1 us); from M = 6 this kernel leads on all four. Either way at M = 2
+    // where the VALU GEMV's panel does not fit one workgroup (the panel kernel would take
+    // it: 7B down, K=18944, bs 32: 26.9 us against 23.2 us here).
     if (M == 2) return !gemv_fits;
     if (w.log2cpb == 2) return M >= kSkinnyMinM;
     return M >= 5 || !gemv_fits || (M >= kSkinnyMinM && w.N >= 8192);

@@ -641,10 +641,11 @@ def test_one_shot_entry_matches_handle_path(gpu):
     w.close()
 
 
-@pytest.mark.parametrize("M", [1, 2, 4])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
 def test_batch_shared_activations_grouped(gpu, M):
-    """The decode layer as an engine issues it: q/k/v on one input and gate/up on
-    another go through one grouped gemv_w4 launch each; every output against the oracle."""
+    """The decode layer as an engine issues it: q/k/v on one input go through one grouped
+    gemv_w4 launch, and so do gate/up on another up to M = 3 (from M = 4 each takes the
+    matrix-core small-M kernel on its own); every output against the oracle."""
     import torch
     ops = workloads.DECODE_7B            # q, k, v, o, gate, up, down
     share = workloads.DECODE_7B_SHARE   # activation buffer each call reads
@@ -656,7 +657,11 @@ def test_batch_shared_activations_grouped(gpu, M):
     info = native.batch_launch_info([h[3] for h in host], ptrs, M)
     assert info["calls"] == 3 and info["kernel"] == "gemv_w4", info          # q, k, v in one launch
     assert native.batch_launch_info([h[3] for h in host[3:]], ptrs[3:], M)["calls"] == 1   # o alone
-    assert native.batch_launch_info([h[3] for h in host[4:]], ptrs[4:], M)["calls"] == 2   # gate, up
+    gu = native.batch_launch_info([h[3] for h in host[4:]], ptrs[4:], M)
+    if M >= 4:
+        assert gu["calls"] == 1 and gu["kernel"] == "skinny_w4", gu                  # gate alone
+    else:
+        assert gu["calls"] == 2 and gu["kernel"] == "gemv_w4", gu                    # gate, up
     native.gemm_dev_batch([h[3] for h in host], ptrs, [y.data_ptr() for y in Ys], M,
                           torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
