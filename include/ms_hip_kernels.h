@@ -189,7 +189,8 @@ int ms_hip_nbits_device_error(void* handle);
  * calls (M <= 4) on the same dA pointer whose weights share K and block size (the
  * projections of one input: q/k/v, gate/up) run as one grouped launch of up to
  * four matrices; results are those of the same calls made one by one, to the
- * decode tolerance. */
+ * decode tolerance. Prefill calls (M > 16) on the same dA pointer, M and K share
+ * one fp16 copy of A (made by the first of them; bit-identical results). */
 int ms_hip_nbits_gemm_dev_batch(void* const* handles, const float* const* dA,
                                 float* const* dY, int count, int M, void* stream);
 

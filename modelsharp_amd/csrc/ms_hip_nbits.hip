@@ -959,6 +959,31 @@ PipeSplit pipe_split(const Weights& w, const Knobs& kn, int M)
     return sp;
 }
 
+// The fp16 copy of A (and its row exponents) that the prefill kernels read, made by
+// a_rows_f16_kernel in the call's workspace. Consecutive calls of one batch on the same
+// activations (gate and up) share it: the first call records where it wrote the copy,
+// and a later call with the same A, M and K reads that copy instead of converting again
+// (the copy lives in the first call's handle workspace, untouched until the batch ends).
+struct AConv {
+    const float* dA = nullptr;   // the activations the copy was made from (nullptr: none)
+    int M = 0, K = 0;
+    const uint32_t* a16 = nullptr;
+    const int* rexp = nullptr;
+};
+struct AConvView {
+    const uint32_t* a16;
+    const int* rexp;
+};
+AConvView a_conv_for(AConv* conv, const Ws& ws, const float* dA, int M, int K, hipStream_t stream)
+{
+    if (conv && conv->dA == dA && conv->M == M && conv->K == K && conv->a16) return {conv->a16, conv->rexp};
+    uint32_t* a16 = reinterpret_cast<uint32_t*>(ws.data);
+    int* rexp = reinterpret_cast<int*>(ws.data + align256((size_t)M * K * 2));
+    launch_a_rows_f16(dA, a16, rexp, M, K, stream);
+    if (conv) *conv = AConv{dA, M, K, a16, rexp};
+    return {a16, rexp};
+}
+
 // Workspace of a pipelined launch: fp16 A and row exponents, then one partial-sum slot
 // per split tile; two counters per split tile.
 struct PipeWs {
@@ -974,7 +999,8 @@ PipeWs pipe_ws(const Weights& w, int M, const PipeSplit& sp)
     return r;
 }
 
-int launch_pipe(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, float* dY, int M, hipStream_t stream)
+int launch_pipe(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, float* dY, int M, hipStream_t stream,
+                AConv* conv)
 {
     const int tiles_m = (M + kPipeBM - 1) / kPipeBM, tiles_n = (w.N + kPipeBN - 1) / kPipeBN;
     const PipeSplit sp = pipe_split(w, kn, M);
@@ -985,9 +1011,9 @@ int launch_pipe(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, floa
                                          hipFuncAttributeMaxDynamicSharedMemorySize, kPipeLdsBytes));
         lds_raised.store(true);
     }
-    uint32_t* a16 = reinterpret_cast<uint32_t*>(ws.data);
-    int* rexp = reinterpret_cast<int*>(ws.data + align256((size_t)M * w.K * 2));
-    launch_a_rows_f16(dA, a16, rexp, M, w.K, stream);
+    const AConvView av = a_conv_for(conv, ws, dA, M, w.K, stream);
+    const uint32_t* a16 = av.a16;
+    const int* rexp = av.rexp;
     PipeParams p;
     p.b = w.d_b;
     p.scales = w.d_scales;
@@ -1208,15 +1234,16 @@ RbWs rb_ws(const Weights& w, int M, int ksw)
     return r;
 }
 
-int launch_rb(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, float* dY, int M, hipStream_t stream)
+int launch_rb(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, float* dY, int M, hipStream_t stream,
+              AConv* conv)
 {
     const RbShape sh = rb_shape(w, kn, M);
     const int tiles_m = sh.tiles_m, tiles_n = sh.tiles_n, ksw = sh.ksw;
     const RbWs L = rb_ws(w, M, ksw);
-    uint32_t* a16 = reinterpret_cast<uint32_t*>(ws.data);
-    int* rexp = reinterpret_cast<int*>(ws.data + align256((size_t)M * w.K * 2));
+    const AConvView av = a_conv_for(conv, ws, dA, M, w.K, stream);
+    const uint32_t* a16 = av.a16;
+    const int* rexp = av.rexp;
     float* part = reinterpret_cast<float*>(ws.data + L.part_off);
-    launch_a_rows_f16(dA, a16, rexp, M, w.K, stream);
     RbParams p;
     p.b = w.d_b;
     p.sz4 = w.d_sz4;
@@ -1329,7 +1356,7 @@ KernelId workspace_free_kernel(const Weights& w, const Knobs& kn, int M)
 }
 
 int launch_kernel(Weights& w, const Knobs& kn, KernelId k, const Ws& ws, const float* dA, float* dY, int M,
-                  hipStream_t stream)
+                  hipStream_t stream, AConv* conv = nullptr)
 {
     switch (k) {
         case kGeneric: return launch_generic(w, dA, dY, M, stream);
@@ -1339,8 +1366,8 @@ int launch_kernel(Weights& w, const Knobs& kn, KernelId k, const Ws& ws, const f
         case kGemv:
         case kPanel: return launch_gemv(w, kn, dA, dY, M, stream);
         case kSkinny: return launch_skinny(w, kn, ws, dA, dY, M, stream);
-        case kRb: return launch_rb(w, kn, ws, dA, dY, M, stream);
-        case kPipe: return launch_pipe(w, kn, ws, dA, dY, M, stream);
+        case kRb: return launch_rb(w, kn, ws, dA, dY, M, stream, conv);
+        case kPipe: return launch_pipe(w, kn, ws, dA, dY, M, stream, conv);
         case kMfma:
             return launch_mfma(w.d_b, w.d_scales, w.has_zp ? w.d_zp : nullptr, w.row_bytes, w.N, w.K, w.nb, w.zrb,
                                w.log2cpb, dA, dY, M, stream)
@@ -1372,7 +1399,7 @@ int resolve_rb(Weights& w, const Knobs& kn, KernelId* k, int M, hipStream_t stre
 }
 
 // One call with the handle's own (growable) workspace.
-int enqueue_gemm(Weights& w, const float* dA, float* dY, int M, hipStream_t stream)
+int enqueue_gemm(Weights& w, const float* dA, float* dY, int M, hipStream_t stream, AConv* conv = nullptr)
 {
     int st = check_call(dA, dY, M);
     if (st || M == 0) return st;
@@ -1387,7 +1414,7 @@ int enqueue_gemm(Weights& w, const float* dA, float* dY, int M, hipStream_t stre
         if (r < 0) return fail(MS_HIP_ERR_HIP, "[ms_hip] workspace allocation failed: %s", hipGetErrorString(hipGetLastError()));
         if (r == 0) k = workspace_free_kernel(w, kn, M);
     }
-    return launch_kernel(w, kn, k, ws, dA, dY, M, stream);
+    return launch_kernel(w, kn, k, ws, dA, dY, M, stream, conv);
 }
 
 // ---- W4A8 (the opt-in approximate product) --------------------------------------------------
@@ -1984,6 +2011,12 @@ int ms_hip_nbits_gemm_dev_batch(void* const* handles, const float* const* dA, fl
         const int st = take_device_error(*ws[i], s);
         if (st) return st;
     }
+    // The prefill kernels' fp16 copy of an input, shared by the calls that read it (gate and
+    // up at M > 16: one conversion instead of two). The copy sits in the workspace of the
+    // handle that made it; a later call on that same handle could regrow the workspace, so
+    // the copy is dropped before such a call.
+    AConv conv;
+    const Weights* conv_owner = nullptr;
     for (int i = 0; i < count;) {
         int ci = -1;
         const int n = batch_group(ws.data() + i, dA + i, count - i, M, &ci);
@@ -1997,8 +2030,14 @@ int ms_hip_nbits_gemm_dev_batch(void* const* handles, const float* const* dA, fl
             const int st = launch_gemv_group(mem, n, dA[i], M, ci, s);
             if (st) return st;
         } else {
-            const int st = enqueue_gemm(*ws[i], dA[i], dY[i], M, s);
+            if (ws[i] == conv_owner) {
+                conv = AConv{};
+                conv_owner = nullptr;
+            }
+            const uint32_t* before = conv.a16;
+            const int st = enqueue_gemm(*ws[i], dA[i], dY[i], M, s, &conv);
             if (st) return st;
+            if (conv.a16 != before) conv_owner = ws[i];
         }
         i += n;
     }

@@ -700,6 +700,40 @@ def test_batch_group_every_launch_config(gpu):
         h[3].close()
 
 
+@pytest.mark.parametrize("M,rb", [(300, 0), (300, 2), (2048, 0)])
+def test_batch_prefill_shares_the_fp16_copy(gpu, M, rb):
+    """Prefill calls of one batch on the same input (gate and up) convert A to fp16 once:
+    the second reads the first's copy. Outputs equal single calls bit for bit, on the
+    pipelined and the few-tile kernel (knob 6 = 2), and when a handle appears twice (its
+    own earlier copy is dropped first) or a call on another input sits in between."""
+    import torch
+    gate, up = workloads.Op("gate", 1024, 700, 32, True), workloads.Op("up", 1024, 520, 32, True)
+    other = workloads.Op("other", 640, 300, 32, True)
+    hg, hu, ho = weights_for(gate, 81)[3], weights_for(up, 82)[3], weights_for(other, 83)[3]
+    a = torch.from_numpy(workloads.make_activations(M, 1024, 84, kind="rmsnorm")).cuda()
+    b = torch.from_numpy(workloads.make_activations(M, 640, 85, kind="rmsnorm")).cuda()
+    stream = torch.cuda.current_stream().cuda_stream
+    try:
+        native.set_tuning(6, rb)
+        calls = [(hg, a), (hu, a), (hg, a), (hu, a), (ho, b), (hu, a), (hg, a)]
+        Ys = [torch.full((M, h.N), float("nan"), device="cuda") for h, _ in calls]
+        kernels = {h.launch_info(M)["kernel"] for h, _ in calls}
+        log(f"shared fp16 copy M={M} rb={rb}: {kernels}")
+        assert kernels <= {"mfma_w4_pipe", "mfma_w4_rb"} and (rb == 0 or kernels == {"mfma_w4_rb"}), kernels
+        native.gemm_dev_batch([h for h, _ in calls], [x.data_ptr() for _, x in calls], [y.data_ptr() for y in Ys],
+                              M, stream)
+        torch.cuda.synchronize()
+        for (h, x), y in zip(calls, Ys):
+            ref = torch.full_like(y, float("nan"))
+            h.gemm_dev(x.data_ptr(), ref.data_ptr(), M, stream)
+            torch.cuda.synchronize()
+            assert torch.equal(y, ref), h.N
+    finally:
+        native.set_tuning(6, 0)
+        for h in (hg, hu, ho):
+            h.close()
+
+
 def test_batch_entry_matches_single_calls(gpu):
     import torch
     ops = workloads.DECODE_7B[:4]
