@@ -265,7 +265,7 @@ int ms_hip_sync(void);
  *     has the GEMM store Y straight into pinned host memory (else a DMA copy back);
  *     0 = the default (Y straight for calls of up to 1 MiB of A and Y, else DMA);
  *  11 the 8-bit GEMV's launch configuration: c+1 forces configuration c (0..8) of the
- *     library's table, -1 keeps 8-bit calls on gemv_general.
+ *     library's table, -1 sends the 8-bit calls of M <= 4 to gemv_general.
  * ms_hip_nbits_debug_set_counters sets the arrival tag of every split tile of the
  *   handle's pipelined-prefill counters to `value` (or to the tag the next split-K
  *   launch will carry, when next_epoch_tag != 0) and clears their ready flags: it

@@ -1052,13 +1052,32 @@ int launch_pipe(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, floa
 // M=2 13.2 / 12.5 us against 15.4 / 16.7 us; M=3 20.4 / 24.2 us against 15.8 / 17.3 us),
 // unless knob 4 says otherwise.
 constexpr int kSkinnyMinM = 3;
+// Quantization blocks per 128-k block of a layout the small-M matrix-core kernel takes
+// (4-bit or 8-bit codes with packed or no zero points, block size 32, 64 or 128), else 0.
+int skinny_qpb(const Weights& w)
+{
+    const bool fmt = w.fast || (w.bits == 8 && !w.zp_float);
+    if (!fmt) return 0;
+    return w.bs == 128 ? 1 : w.bs == 64 ? 2 : w.bs == 32 ? 4 : 0;
+}
 bool skinny_eligible(const Weights& w, const Knobs& kn, int M)
 {
-    if (kn.skinny() == 1 || !w.fast || w.log2cpb > 2 || (w.K % 128) != 0 || M < 1 || M > kSkinnyMT) return false;
-    if ((int64_t)kSkinnyMT * w.K * 4 >= INT32_MAX) return false;
+    if (kn.skinny() == 1 || skinny_qpb(w) == 0 || (w.K % 128) != 0 || M < 1 || M > kSkinnyMT) return false;
+    if ((int64_t)kSkinnyMT * w.K * 4 >= INT32_MAX || (int64_t)w.N * w.row_bytes >= kOOB) return false;
     // the partial-sum slices stay within the reduce's 32-bit buffer offsets
     if ((int64_t)(w.K / 128) * ((int64_t)kSkinnyMT * w.N + 3) / 4 * 16 >= kOOB) return false;
     if (kn.skinny() == 2) return true;
+    // 8-bit codes: from M = 5, where gemv_w8 stops; below that by default where it measured
+    // faster than gemv_w8 (K=4096/N=11008: bs 128 from M = 3, 15.9 against 17.8 us; bs 32
+    // from M = 4, 19.1 against 20.9 us, while at M = 3 gemv_w8 leads, 18.5 against 19.2) and
+    // wherever gemv_w8's panel does not fit (K=11008, M = 4: 22.1 us against 202 us on
+    // gemv_general). A forced gemv_w8 configuration or knob 11 = -1 keeps M <= 4 where that
+    // knob sends it.
+    if (w.bits == 8) {
+        if (M >= 5) return true;
+        if (M < kSkinnyMinM || kn.gemv8_config() != 0) return false;
+        return pick_gemv8_config(w, kn, M) < 0 || M >= (w.bs == 128 ? 3 : 4);
+    }
     const bool gemv_fits = pick_gemv_config(w, kn, M, w.N) >= 0;
     // Block size 128: from M = 3. Block sizes 32 and 64 (a scale per 32-k step): from M = 5,
     // and from M = 3 for large matrices (N >= 8192); measured on the 7B decode launches
@@ -1128,13 +1147,23 @@ int launch_skinny(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, fl
     p.nb = w.nb;
     p.zrb = w.zrb;
     p.ksw = ksw;
-    // quantization blocks per 128-k block: 1 (bs 128), 2 (bs 64), 4 (bs 32)
-    if (w.log2cpb == 2)
-        hipLaunchKernelGGL(skinny_w4_kernel<1>, dim3(tiles * ksw), dim3(256), 0, stream, p);
-    else if (w.log2cpb == 1)
-        hipLaunchKernelGGL(skinny_w4_kernel<2>, dim3(tiles * ksw), dim3(256), 0, stream, p);
-    else
-        hipLaunchKernelGGL(skinny_w4_kernel<4>, dim3(tiles * ksw), dim3(256), 0, stream, p);
+    // quantization blocks per 128-k block: 1 (bs 128), 2 (bs 64), 4 (bs 32); 4- or 8-bit codes
+    const int qpb = skinny_qpb(w);
+    const dim3 grid(tiles * ksw), block(256);
+    if (w.bits == 8) {
+        if (qpb == 1)
+            hipLaunchKernelGGL((skinny_w4_kernel<1, true>), grid, block, 0, stream, p);
+        else if (qpb == 2)
+            hipLaunchKernelGGL((skinny_w4_kernel<2, true>), grid, block, 0, stream, p);
+        else
+            hipLaunchKernelGGL((skinny_w4_kernel<4, true>), grid, block, 0, stream, p);
+    } else if (qpb == 1) {
+        hipLaunchKernelGGL((skinny_w4_kernel<1, false>), grid, block, 0, stream, p);
+    } else if (qpb == 2) {
+        hipLaunchKernelGGL((skinny_w4_kernel<2, false>), grid, block, 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((skinny_w4_kernel<4, false>), grid, block, 0, stream, p);
+    }
     MS_HIP_CHECK(hipGetLastError());
     if (p.part) {
         hipLaunchKernelGGL(skinny_reduce_kernel, dim3((p.slice4 + 255) / 256), dim3(256), 0, stream, p.part, dY,
@@ -1313,6 +1342,7 @@ enum KernelId {
 KernelId choose_kernel(const Weights& w, const Knobs& kn, int M)
 {
     if (!w.fast) {
+        if (M <= kPanelMaxM && skinny_eligible(w, kn, M)) return kSkinny;   // 8-bit small M
         if (pick_gemv8_config(w, kn, M) >= 0) return kGemvW8;
         if (rb_eligible(w, kn, M)) return kRb;   // 8-bit prefill
         if (!general_eligible(w)) return kGeneric;

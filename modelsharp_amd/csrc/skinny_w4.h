@@ -71,11 +71,36 @@ struct SkinnyParams {
     int ksw;                   // workgroups per row tile: ksw * kSkinnyNB >= K / 128, ksw <= K / 128
 };
 
-template <int QPB>
+// The 8 codes of MFMA step j of a lane's 128-k block as four fp16 pairs (q - zp), in the
+// order (k_t, k_{t+4}) of the permuted activations, exact (|q - zp| <= 255). 4-bit codes:
+// dword j of the lane's 16-byte chunk; 8-bit codes (B8): dwords 2j, 2j + 1 of its 32
+// bytes, whose byte t and byte t of the next dword v_perm puts side by side.
+template <bool B8>
+__device__ __forceinline__ half8_t skinny_step_codes(uint32_t d0, uint32_t d1, h2_t z2)
+{
+    uint32_t o[4];
+    if constexpr (B8) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            o[t] = as_u32(as_h2(and_or(__builtin_amdgcn_perm(d1, d0, (uint32_t)(((4 + t) << 16) | t)), 0x00FF00FFu,
+                                       kHalfMagic)) - z2);
+    } else {
+        (void)d1;
+        o[0] = as_u32(as_h2(and_or(d0, 0x000F000Fu, kHalfMagic)) - z2);
+        o[1] = as_u32(as_h2(and_or(d0 >> 4, 0x000F000Fu, kHalfMagic)) - z2);
+        o[2] = as_u32(as_h2(and_or(d0 >> 8, 0x000F000Fu, kHalfMagic)) - z2);
+        o[3] = as_u32(as_h2(and_or(d0 >> 12, 0x000F000Fu, kHalfMagic)) - z2);
+    }
+    return __builtin_bit_cast(half8_t, u32x4_t{o[0], o[1], o[2], o[3]});
+}
+
+template <int QPB, bool B8>
 __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
 {
     static_assert(QPB == 1 || QPB == 2 || QPB == 4, "block sizes 128, 64, 32");
     constexpr bool PS = QPB > 1;   // a scale per 32-k step (bs 32, 64), not per 128-k block
+    constexpr int CW = B8 ? 2 : 1; // 16-byte code chunks per lane and block (8-bit: 32 codes in 32 bytes)
+    constexpr int ZB = B8 ? 8 : 4; // bits per zero point
     constexpr int NF = kSkinnyNF, NB = kSkinnyNB;
     __shared__ __attribute__((aligned(16))) uint32_t lds_a[NB * kSkinnyBlockBytes / 4];
     __shared__ __attribute__((aligned(16))) float lds_e[NB * kSkinnyMT];
@@ -128,25 +153,30 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
             const int n = n0 + 16 * f + ln, q0 = (g0 + ls) * QPB;
             const bool ok = n < p.N && ls < cnt;
             const int so = ok ? (n * p.nb + q0) * 4 : kOOB;
+            // the QPB zero points: 4-bit nibbles (2 or 1 bytes at q0 / 2), 8-bit bytes
+            // (4 or 2 bytes at q0; zrb = nb, a multiple of QPB, keeps them aligned)
+            const int zo = ok ? n * p.zrb + (B8 ? q0 : q0 / 2) : kOOB;
             if constexpr (QPB == 4) {
                 const float4 v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsc, so, 0, 0));
                 sv[f][0] = v.x;
                 sv[f][1] = v.y;
                 sv[f][2] = v.z;
                 sv[f][3] = v.w;
-                zv[f] = __builtin_amdgcn_raw_buffer_load_b16(rz, ok ? n * p.zrb + q0 / 2 : kOOB, 0, 0);
+                zv[f] = B8 ? __builtin_amdgcn_raw_buffer_load_b32(rz, zo, 0, 0)
+                           : __builtin_amdgcn_raw_buffer_load_b16(rz, zo, 0, 0);
             } else {
                 const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rsc, so, 0, 0));
                 sv[f][0] = __builtin_bit_cast(float, v.x);
                 sv[f][1] = __builtin_bit_cast(float, v.y);
-                zv[f] = __builtin_amdgcn_raw_buffer_load_b8(rz, ok ? n * p.zrb + q0 / 2 : kOOB, 0, 0);
+                zv[f] = B8 ? __builtin_amdgcn_raw_buffer_load_b16(rz, zo, 0, 0)
+                           : __builtin_amdgcn_raw_buffer_load_b8(rz, zo, 0, 0);
             }
         } else {
             const int n = n0 + 16 * f + lane / NB, blk = lane % NB, g = g0 + blk;
             const bool ok = n < p.N && blk < cnt;
             sv[f][0] = __builtin_bit_cast(
                 float, __builtin_amdgcn_raw_buffer_load_b32(rsc, ok ? n * p.nb * 4 + g * 4 : kOOB, 0, 0));
-            zv[f] = __builtin_amdgcn_raw_buffer_load_b8(rz, ok ? n * p.zrb + (g >> 1) : kOOB, 0, 0);
+            zv[f] = __builtin_amdgcn_raw_buffer_load_b8(rz, ok ? n * p.zrb + (B8 ? g : g >> 1) : kOOB, 0, 0);
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -155,18 +185,20 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
         const int n = n0 + 16 * f + ln;
-        cbase[f] = n < p.N ? n * p.row_bytes + ls * 16 : kOOB;
+        cbase[f] = n < p.N ? n * p.row_bytes + ls * 16 * CW : kOOB;
     }
     // One load group per block, issued in block order, so computing block lg waits only
     // for its own group (the scheduling barriers keep the groups apart).
-    u32x4_t c[NB][NF];
+    u32x4_t c[NB][NF][CW];
 #pragma unroll
     for (int lg = 0; lg < NB; ++lg) {
         const int g = g0 + lg;
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
             const bool ok = lg < cnt && cbase[f] != kOOB;
-            c[lg][f] = __builtin_amdgcn_raw_buffer_load_b128(rb_, ok ? cbase[f] + g * 64 : kOOB, 0, 0);
+#pragma unroll
+            for (int h = 0; h < CW; ++h)
+                c[lg][f][h] = __builtin_amdgcn_raw_buffer_load_b128(rb_, ok ? cbase[f] + g * 64 * CW + 16 * h : kOOB, 0, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -227,7 +259,7 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
     floatx4_t acc[NF];
 #pragma unroll
     for (int f = 0; f < NF; ++f) acc[f] = floatx4_t{};
-    const uint32_t zdef = p.zp ? 0u : 8u;    // without zero points the zp loads read zeros
+    const uint32_t zdef = p.zp ? 0u : (B8 ? 128u : 8u);   // without zero points the zp loads read zeros
     // This lane's chunk (s = ls, m = ln) of each step j and part, within a block's 8 KB.
     int aoff[4][2];
 #pragma unroll
@@ -244,18 +276,35 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
         if constexpr (PS) {
             // Transpose the code dwords across the four 16-lane rows (lane (ln, s) had
             // dword j of quantization block s; after it, dword s of block j): step j is
-            // block j. The permlane swaps exchange whole rows, lane ln stays lane ln.
-            uint32_t t[NF][4];
+            // block j. The permlane swaps exchange whole rows, lane ln stays lane ln. With
+            // 8-bit codes a step is a pair of dwords (2 j, 2 j + 1): the even and the odd
+            // dwords are transposed alike.
+            uint32_t t[NF][CW][4];
 #pragma unroll
             for (int f = 0; f < NF; ++f) {
-                const auto a0 = __builtin_amdgcn_permlane32_swap(c[lg][f].x, c[lg][f].z, false, false);
-                const auto a1 = __builtin_amdgcn_permlane32_swap(c[lg][f].y, c[lg][f].w, false, false);
-                const auto b0 = __builtin_amdgcn_permlane16_swap(a0[0], a1[0], false, false);
-                const auto b1 = __builtin_amdgcn_permlane16_swap(a0[1], a1[1], false, false);
-                t[f][0] = b0[0];
-                t[f][1] = b0[1];
-                t[f][2] = b1[0];
-                t[f][3] = b1[1];
+#pragma unroll
+                for (int h = 0; h < CW; ++h) {
+                    uint32_t d[4];   // dword i (4-bit) or 2 i + h (8-bit) of the lane's codes, i = 0..3
+                    if constexpr (B8) {
+                        d[0] = h ? c[lg][f][0].y : c[lg][f][0].x;
+                        d[1] = h ? c[lg][f][0].w : c[lg][f][0].z;
+                        d[2] = h ? c[lg][f][1].y : c[lg][f][1].x;
+                        d[3] = h ? c[lg][f][1].w : c[lg][f][1].z;
+                    } else {
+                        d[0] = c[lg][f][0].x;
+                        d[1] = c[lg][f][0].y;
+                        d[2] = c[lg][f][0].z;
+                        d[3] = c[lg][f][0].w;
+                    }
+                    const auto a0 = __builtin_amdgcn_permlane32_swap(d[0], d[2], false, false);
+                    const auto a1 = __builtin_amdgcn_permlane32_swap(d[1], d[3], false, false);
+                    const auto b0 = __builtin_amdgcn_permlane16_swap(a0[0], a1[0], false, false);
+                    const auto b1 = __builtin_amdgcn_permlane16_swap(a0[1], a1[1], false, false);
+                    t[f][h][0] = b0[0];
+                    t[f][h][1] = b0[1];
+                    t[f][h][2] = b1[0];
+                    t[f][h][3] = b1[1];
+                }
             }
             const int src = (ln + 16 * lg) * 4;   // ds_bpermute byte address of lane (ln, lg)
 #pragma unroll
@@ -268,14 +317,9 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
                     const float sc =
                         __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, sv[f][qj])));
                     const uint32_t zq = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)zv[f]);
-                    const uint32_t zp = ((zq >> (4 * qj)) & 0x0F) + zdef;
+                    const uint32_t zp = ((zq >> (ZB * qj)) & ((1u << ZB) - 1)) + zdef;
                     const h2_t z2 = as_h2(kHalfMagic | (zp << 16) | zp);
-                    const uint32_t x = t[f][j];
-                    const uint32_t o0 = as_u32(as_h2(and_or(x, 0x000F000Fu, kHalfMagic)) - z2);
-                    const uint32_t o1 = as_u32(as_h2(and_or(x >> 4, 0x000F000Fu, kHalfMagic)) - z2);
-                    const uint32_t o2 = as_u32(as_h2(and_or(x >> 8, 0x000F000Fu, kHalfMagic)) - z2);
-                    const uint32_t o3 = as_u32(as_h2(and_or(x >> 12, 0x000F000Fu, kHalfMagic)) - z2);
-                    const half8_t bq = __builtin_bit_cast(half8_t, u32x4_t{o0, o1, o2, o3});
+                    const half8_t bq = skinny_step_codes<B8>(t[f][0][j], t[f][CW - 1][j], z2);
                     const floatx4_t th = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq, floatx4_t{}, 0, 0, 0);
                     const floatx4_t tl = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq, floatx4_t{}, 0, 0, 0);
                     // step sums for activation row m = 4 ls + v and weight row n0 + 16 f + ln:
@@ -295,7 +339,7 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
                 const int src = (NB * ln + lg) * 4;   // ds_bpermute byte address of lane NB ln + lg
                 sc[f] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, sv[f][0])));
                 const uint32_t zq = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)zv[f]);
-                const uint32_t zp = ((zq >> (((g0 + lg) & 1) * 4)) & 0x0F) + zdef;
+                const uint32_t zp = (B8 ? (zq & 0xFFu) : ((zq >> (((g0 + lg) & 1) * 4)) & 0x0Fu)) + zdef;
                 zb[f] = kHalfMagic | (zp << 16) | zp;
             }
 #pragma unroll
@@ -304,13 +348,11 @@ __global__ __launch_bounds__(256) void skinny_w4_kernel(SkinnyParams p)
                 const half8_t al = *reinterpret_cast<const half8_t*>(&lds_a[(lg * kSkinnyBlockBytes + aoff[j][1]) / 4]);
 #pragma unroll
                 for (int f = 0; f < NF; ++f) {
-                    const uint32_t x = j == 0 ? c[lg][f].x : j == 1 ? c[lg][f].y : j == 2 ? c[lg][f].z : c[lg][f].w;
-                    const h2_t z2 = as_h2(zb[f]);
-                    const uint32_t o0 = as_u32(as_h2(and_or(x, 0x000F000Fu, kHalfMagic)) - z2);
-                    const uint32_t o1 = as_u32(as_h2(and_or(x >> 4, 0x000F000Fu, kHalfMagic)) - z2);
-                    const uint32_t o2 = as_u32(as_h2(and_or(x >> 8, 0x000F000Fu, kHalfMagic)) - z2);
-                    const uint32_t o3 = as_u32(as_h2(and_or(x >> 12, 0x000F000Fu, kHalfMagic)) - z2);
-                    const half8_t bq = __builtin_bit_cast(half8_t, u32x4_t{o0, o1, o2, o3});
+                    // step j: dword j of the 16-byte chunk (4-bit), dwords 2 j, 2 j + 1 of the 32 bytes (8-bit)
+                    const u32x4_t& cw = c[lg][f][B8 ? (j >> 1) : 0];
+                    const uint32_t d0 = B8 ? ((j & 1) ? cw.z : cw.x) : (j == 0 ? cw.x : j == 1 ? cw.y : j == 2 ? cw.z : cw.w);
+                    const uint32_t d1 = B8 ? ((j & 1) ? cw.w : cw.y) : 0u;
+                    const half8_t bq = skinny_step_codes<B8>(d0, d1, as_h2(zb[f]));
                     th[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq, th[f], 0, 0, 0);
                     tl[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq, tl[f], 0, 0, 0);
                 }

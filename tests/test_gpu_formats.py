@@ -56,12 +56,17 @@ def assert_within(y, ref, allowed, what):
     assert np.all(err <= allowed), f"{what}: err/bound {ratio:.3e}"
 
 
-def expected_kernel(op: Op, M: int, float_zp: bool = False, fp16_scales: bool = True) -> str:
+def expected_kernel(op: Op, M: int, float_zp: bool = False, fp16_scales: bool = True, skinny: bool = True) -> str:
     """The kernel the dispatch rules give a call with M rows (fp16_scales: every nonzero
-    |scale| lies in [2^-14, 256], as make_weights draws them)."""
+    |scale| lies in [2^-14, 256], as make_weights draws them; skinny=False: knob 4 = 1)."""
     pow2 = op.block_size >= 16 and (op.block_size & (op.block_size - 1)) == 0
-    if (op.bits == 8 and not float_zp and pow2 and op.K % 16 == 0 and M <= 4
-            and M * op.K * 4 <= 159 * 1024):
+    gemv8 = (op.bits == 8 and not float_zp and pow2 and op.K % 16 == 0 and M <= 4
+             and M * op.K * 4 <= 159 * 1024)
+    low = 3 if op.block_size == 128 else 4   # the default takes 8-bit M <= 4 from here
+    if (skinny and op.bits == 8 and not float_zp and op.block_size in (32, 64, 128) and op.K % 128 == 0
+            and (5 <= M <= 16 or (3 <= M <= 4 and (not gemv8 or M >= low)))):
+        return "skinny_w4"
+    if gemv8:
         return "gemv_w8"
     if (op.bits == 8 and not float_zp and pow2 and op.block_size >= 32 and op.K % 128 == 0 and M > 16
             and fp16_scales):
@@ -89,6 +94,12 @@ def check_against_oracle(w, a, b, s, zp, zpf, op, what):
         rel = float(np.linalg.norm(y.astype(np.float64) - ref) / max(np.linalg.norm(ref.astype(np.float64)), 1e-300))
         log(f"  {what}: relative Frobenius error {rel:.3e}")
         assert rel <= 2e-3, f"{what}: rel_fro {rel:.3e}"
+    elif kernel == "skinny_w4":
+        # the small-M matrix-core kernel: A as 2^e (hi + lo) per (row, 128-k block), exact to
+        # 2^-22 of the block's max |a| (so within 2^-22 of the row's), exact products and
+        # fp32 sums of the MFMA steps, the blocks and the scales
+        allowed = 2 * gamma2(op.K) * cond + 2.0 ** -21 * (
+            np.max(np.abs(a), axis=1, keepdims=True).astype(np.float64) * np.abs(W).sum(axis=1)[None, :])
     else:
         allowed = gamma2(op.K) * cond
     assert_within(y, ref, allowed, f"{what} [{kernel}]")
@@ -183,6 +194,11 @@ def test_gemv_w8(gpu, op, M):
     assert kernel == expected_kernel(op, M)
     y = w.gemm(a)
     assert np.array_equal(y, w.gemm(a))   # deterministic
+    if kernel == "skinny_w4":   # the 8-bit GEMV itself, with the small-M matrix-core kernel off
+        w.set_tuning(4, 1)
+        kernel, _ = check_against_oracle(w, a, b, s, z, None, op, f"{op.name} M={M} knob 4 = 1")
+        assert kernel == expected_kernel(op, M, skinny=False)
+        w.set_tuning(4, 0)
     w.close()
 
 
@@ -211,17 +227,23 @@ def test_gemv_w8_every_config(gpu, M):
 
 
 def test_gemv_w8_extreme_codes(gpu):
-    """Codes and zero points at 0 and 255 (q - zp = +-255, the widest difference)."""
+    """Codes and zero points at 0 and 255 (q - zp = +-255, the widest difference), on the
+    8-bit GEMV and (M = 4, by default) the small-M matrix-core kernel."""
     op = Op("w8_ext", 512, 64, 32, True, bits=8)
     rng = np.random.Generator(np.random.PCG64(77))
     b = rng.choice(np.array([0, 255], dtype=np.uint8), size=(op.N, op.nb, op.blob))
     z = rng.choice(np.array([0, 255], dtype=np.uint8), size=(op.N, op.zrb))
     s = rng.uniform(op.scale_lo, op.scale_hi, size=op.N * op.nb).astype(np.float32)
     w = native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
-    for M in (1, 4):
-        a = workloads.make_activations(M, op.K, seed=M)
-        kernel, _ = check_against_oracle(w, a, b, s, z, None, op, f"extreme codes M={M}")
-        assert kernel == "gemv_w8"
+    try:
+        for M in (1, 4):
+            a = workloads.make_activations(M, op.K, seed=M)
+            for knob in (0, 1):
+                w.set_tuning(4, knob)
+                kernel, _ = check_against_oracle(w, a, b, s, z, None, op, f"extreme codes M={M} knob 4 = {knob}")
+                assert kernel == expected_kernel(op, M, skinny=knob == 0)
+    finally:
+        w.set_tuning(4, 0)
     w.close()
 
 
@@ -373,4 +395,49 @@ def test_prefill_8bit_every_split(gpu):
     w = native.NBitsWeights(b, s_big, z, op.N, op.K, op.bits, op.block_size)
     kernel, _ = check_against_oracle(w, a, b, s_big, z, None, op, "scale 300")
     assert kernel == "mfma_general"
+    w.close()
+
+
+# (K, knob 5): K=640 is 5 blocks of 128 k, split 5 ways (the in-kernel hand-off) or 2;
+# K=512 in one workgroup per row tile; K=1408 (11 blocks) split wider than the hand-off
+# takes: partial-sum slices and the reduce launch.
+B8_SKINNY_SPLITS = [(640, 0), (640, 2), (512, 1), (1408, 0)]
+
+
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("K,ksw", B8_SKINNY_SPLITS, ids=lambda v: str(v))
+@pytest.mark.parametrize("zp", [False, True], ids=["nozp", "zp"])
+def test_skinny_8bit(gpu, zp, K, ksw, bs):
+    """The small-M matrix-core kernel on 8-bit codes for every M in 1..16 (below M = 5 forced
+    by knob 4 = 2), ragged N, codes and zero points spanning 0..255 (|q - zp| up to 255,
+    still exact in fp16), activations spanning 1e-4..1e5 across rows with one outlier; two
+    calls agree bit for bit. Block size 128 applies the scale per 128-k block, 64 and 32 per
+    32-k step after the transpose of the code dword pairs across the wave's rows."""
+    op = Op("sk8", K, 333, bs, zp, bits=8)
+    b, s, z = workloads.make_weights(op, seed=90 + bs + zp)
+    rng = np.random.default_rng(91)
+    b = rng.integers(0, 256, size=b.shape, dtype=np.uint8)
+    b[:7, :] = 255                                   # extreme codes in a few rows
+    b[7:14, :] = 0
+    if z is not None:
+        z = rng.integers(0, 256, size=z.shape, dtype=np.uint8)
+        z[:7] = 0
+        z[7:14] = 255
+    w = native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
+    try:
+        w.set_tuning(4, 2)
+        w.set_tuning(5, ksw)
+        for M in range(1, 17):
+            a = workloads.make_activations(M, op.K, seed=92 + M)
+            a *= (10.0 ** rng.uniform(-4, 5, size=(M, 1))).astype(np.float32)
+            a[M // 2, 300] = np.float32(3e6)
+            kernel, _ = check_against_oracle(w, a, b, s, z, None, op, f"8-bit skinny M={M} K={K} bs={bs} zp={zp}")
+            assert kernel == "skinny_w4"
+            assert np.array_equal(w.gemm(a), w.gemm(a)), M
+        w.set_tuning(4, 0)
+        for M in (3, 4, 5, 16):
+            assert w.launch_info(M)["kernel"] == expected_kernel(op, M), M
+    finally:
+        w.set_tuning(4, 0)
+        w.set_tuning(5, 0)
     w.close()
