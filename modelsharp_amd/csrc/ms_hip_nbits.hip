@@ -1238,11 +1238,14 @@ RbShape rb_shape(const Weights& w, const Knobs& kn, int M)
 // CUs: measured on the 7B MLP shapes, 128 x 256 tiles with a wide K split beat it there
 // (M=128: 49 / 45 us against 78 / 143 us; M=512, K=11008: 103 against 154 us), while
 // with more tiles the pipelined kernel is faster (M=512, K=4096: 100 against 118 us;
-// M=2048: 262 against 320-355 us).
+// M=2048: 262 against 320-355 us). Whenever M fits one 128-row tile as well: the
+// pipelined kernel's 256-row tiles then compute mostly padding (7B gate, K=3584,
+// N=18944: M = 17 / 64 / 128 39.0 / 44.0 / 52.1 us against 66.9 / 67.2 / 67.8 us, while
+// from M = 192 the pipelined kernel leads there, 68.6 against 86.0 us).
 bool use_rb(const Weights& w, const Knobs& kn, int M)
 {
     if (!rb_eligible(w, kn, M)) return false;
-    if (kn.rb() == 2 || !pipe_eligible(w, kn, M)) return true;
+    if (kn.rb() == 2 || !pipe_eligible(w, kn, M) || M <= kRbBM) return true;
     const PipeSplit sp = pipe_split(w, kn, M);
     const int64_t items = sp.full + 2 * (sp.tiles - sp.full);
     return 2 * items < device_cus();
