@@ -527,8 +527,10 @@ bool gemv_config_fits(const Weights& w, int M, const GemvConfig& c)
 // (re-swept with the non-temporal code loads: 7B o at M = 1 / 2 5.41 -> 5.26 /
 // 6.83 -> 6.54 us against the 32-lane pick), 32 lanes per row below; for M = 3-4 the
 // 8-wave configs. From 2K to 4K rows at M <= 2, 8 waves of 64 lanes per row with two rows
-// per lane (7B q / o, 3584 x 3584: M = 1 / 2 5.27 -> 5.14 / 6.62 -> 6.12 us). N is the
-// launch's total rows (summed over a group). Indices are into kGemvConfigs.
+// per lane (7B q / o, 3584 x 3584: M = 1 / 2 5.27 -> 5.14 / 6.62 -> 6.12 us), and the
+// same 8-wave config from 8K to 16K rows (Llama-2-7B up, K = 4096, N = 11008, bs 128,
+// no zero points: M = 1 / 2 9.61 -> 8.89 / 12.87 -> 11.03 us). N is the launch's total
+// rows (summed over a group). Indices are into kGemvConfigs.
 int pick_gemv_config(const Weights& w, const Knobs& kn, int M, int N)
 {
     if (kn.gemv_config() < 0) return -1;
@@ -537,6 +539,7 @@ int pick_gemv_config(const Weights& w, const Knobs& kn, int M, int N)
         return gemv_config_fits(w, M, kGemvConfigs[ci]) ? ci : -1;
     }
     static constexpr int kLargeM2[] = {16, 11, 0, 6};   // M <= 2, N >= 16384
+    static constexpr int kUpperM2[] = {17, 14, 11, 2};  // M <= 2, N >= 8192
     static constexpr int kMidM2[] = {14, 11, 2};        // M <= 2, N >= 4096
     static constexpr int kSmallM2[] = {17, 14, 13, 6};  // M <= 2, N >= 2048
     static constexpr int kTinyM2[] = {3, 14, 8};        // M <= 2
@@ -556,7 +559,8 @@ int pick_gemv_config(const Weights& w, const Knobs& kn, int M, int N)
     };
     int ci;
     if (M <= 2)
-        ci = N >= 16384 ? first_of(kLargeM2, 4) : N >= 4096 ? first_of(kMidM2, 3)
+        ci = N >= 16384 ? first_of(kLargeM2, 4) : N >= 8192 ? first_of(kUpperM2, 4)
+           : N >= 4096  ? first_of(kMidM2, 3)
            : N >= 2048  ? first_of(kSmallM2, 4) : first_of(kTinyM2, 3);
     else
         ci = N >= 16384 ? first_of(kLargeM4, 3) : N >= 4096 ? first_of(kMidM4, 3) : first_of(kSmallM4, 3);
