@@ -307,8 +307,11 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
 // Bound by the slices' bytes: (ksw + 1) * 4 M N (28 MB in 7.8 us at M = 128, N = 11008,
 // ksw = 4).
 constexpr int kRbRedBatch = 16;
+// With vec set (N % 4 == 0 and y 16-byte aligned) the four elements of thread i lie in one
+// row and go out as one 16-byte store.
 __global__ __launch_bounds__(256) void rb_reduce_kernel(const float4* __restrict__ part, float* __restrict__ y,
-                                                        const int* __restrict__ rexp, int n, int N, int slice4, int ksw)
+                                                        const int* __restrict__ rexp, int n, int N, int slice4, int ksw,
+                                                        int vec)
 {
     const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(part, ksw * slice4 * 16);
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < slice4; i += gridDim.x * blockDim.x) {
@@ -330,6 +333,13 @@ __global__ __launch_bounds__(256) void rb_reduce_kernel(const float4* __restrict
                     t.w += f.w;
                 }
             }
+        }
+        if (vec) {
+            const int e = rexp[(4 * i) / N];
+            const float4 o = {__builtin_amdgcn_ldexpf(t.x, e), __builtin_amdgcn_ldexpf(t.y, e),
+                              __builtin_amdgcn_ldexpf(t.z, e), __builtin_amdgcn_ldexpf(t.w, e)};
+            *reinterpret_cast<float4*>(y + 4 * i) = o;
+            continue;
         }
         const float tv[4] = {t.x, t.y, t.z, t.w};
         int m = (4 * i) / N, col = 4 * i - m * N;

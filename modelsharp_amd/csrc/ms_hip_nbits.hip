@@ -1309,7 +1309,8 @@ int launch_rb(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, float*
     }
     const int slice4 = (int)(L.slice / 4);
     hipLaunchKernelGGL(rb_reduce_kernel, dim3((unsigned)std::min((slice4 + 255) / 256, 8192)), dim3(256), 0, stream,
-                       reinterpret_cast<const float4*>(part), dY, rexp, M * w.N, w.N, slice4, ksw);
+                       reinterpret_cast<const float4*>(part), dY, rexp, M * w.N, w.N, slice4, ksw,
+                       (w.N % 4 == 0 && (reinterpret_cast<uintptr_t>(dY) & 15) == 0) ? 1 : 0);
     MS_HIP_CHECK(hipGetLastError());
     return MS_HIP_OK;
 }
