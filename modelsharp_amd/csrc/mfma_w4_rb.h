@@ -209,15 +209,19 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
     // ---- main loop ----
     // Block i: (A(i+1) registers -> LDS; issue A(i+2)); 32 groups (step j, fragment mf) of
     // NF MFMAs, in chunks of RC groups: the A operands of a chunk (RC fragments of 1 KB,
-    // lane-ordered) are read from LDS in one burst while the previous chunk computes
-    // (sched_barrier keeps each burst ahead of the chunk before it), and the B operands of
-    // step j + 1 are dequantized one fragment per group under the first NF groups of step j
-    // (the last step prepares step 0 of block i+1 from the next ring slot); then W(i+3)
-    // goes into the slot just used, which becomes the ring's last; barrier. At the top of
-    // block i the outstanding loads are A(i+1) then W(i+2), so the A store waits for A(i+1)
-    // alone. (A window of three single-fragment reads, one per group, was compiled into a
-    // read followed by its wait before every group's MFMAs.) RC = 8 (a whole step) where
-    // the registers allow, 4 at NF = 4.
+    // lane-ordered) are read from LDS in one burst while the previous chunk computes, and
+    // the B operands of step j + 1 are dequantized one fragment per group under the first
+    // NF groups of step j (the last step prepares step 0 of block i+1 from the next ring
+    // slot); then W(i+3) goes into the slot just used, which becomes the ring's last;
+    // barrier. At the top of block i the outstanding loads are A(i+1) then W(i+2), so the A
+    // store waits for A(i+1) alone. RC = 8 (a whole step) where the registers allow, 4 at
+    // NF = 4. The loop body carries no scheduling pins: with `sched_barrier` between the
+    // bursts and a `sched_group_barrier` pattern of 1 MFMA then 4 VALU, the register
+    // allocator kept 14 of the 32 accumulator fragments at NF = 4 in other AGPRs across the
+    // back edge (112 AGPR<->VGPR moves per block, 76 s_nop); the compiler's own schedule has
+    // none (443 VALU-side instructions and 21 s_nop per block) and measured faster at every
+    // NF (7B gate, M = 17 / 64: 40.0 / 44.2 -> 34.8 / 39.1 us; M=128, K=4096: 41.6 -> 38.3 us;
+    // M=512, K=11008: 81.4 -> 73.6 us; NF = 2 at M=128, K=11008: 35.5 -> 34.9 us).
     constexpr int RC = NF == 4 ? 4 : 8, NCH = 4 * MF / RC;
     auto body = [&](int i, WBlk& wb, const WBlk& wbn) {
         const int buf = i & 1;
@@ -226,7 +230,6 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
         for (int r = 0; r < RC; ++r) aw[0][r] = read_a1(buf, r / MF, r % MF);
         if (i + 1 < cnt) store_a((i + 1) & 1);
         load_a(i + 2);
-        __builtin_amdgcn_sched_barrier(0);
         uint32_t zz[NF], zzn[NF];
         h2_t s2[NF], s2n[NF];
         prep(wb, i, zz, s2);
@@ -243,7 +246,6 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
                     aw[(c + 1) & 1][r] = read_a1(buf, t / MF, t % MF);
                 }
             }
-            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int r = 0; r < RC; ++r) {
                 const int t = c * RC + r, j = t / MF, mf = t % MF;
@@ -251,22 +253,15 @@ __global__ __launch_bounds__(256) void mfma_w4_rb_kernel(RbParams p)
                 for (int f = 0; f < NF; ++f)
                     acc[mf][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw[c & 1][r], bq[f], acc[mf][f], 0, 0, 0);
                 if (mf < NF) bqn[mf] = j < 3 ? deq1(wb, j + 1, mf, zz[mf], s2[mf]) : deq1(wbn, 0, mf, zzn[mf], s2n[mf]);
-#pragma unroll
-                for (int u = 0; u < NF; ++u) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-                }
                 if (mf == MF - 1) {
 #pragma unroll
                     for (int f = 0; f < NF; ++f) bq[f] = bqn[f];
                 }
             }
-            __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
         for (int f = 0; f < NF; ++f) bq0[f] = bq[f];
         load_w(wb, i + kRbRing);
-        __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
     };
     // One body per iteration and the ring rotated by value (a few register moves per
