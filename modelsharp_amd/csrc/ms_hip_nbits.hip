@@ -1199,7 +1199,11 @@ bool rb_eligible(const Weights& w, const Knobs& kn, int M)
 // time a workgroup spends on one 128-k block (about 3.5 us at NF = 4 with the chip busy,
 // measured: K = 11008 unsplit at M = 2048 took 301 us for 86 blocks; the model charges the
 // A block every workgroup stages whatever its width), and the partial sums written and
-// read back once each, plus Y. Knob 9 forces NF, knob 7 ksw.
+// read back once each, plus Y, charged at 2 TB/s: the slices leave in one burst at the end
+// of the GEMM with no MFMA work beside it (a sweep of NF x K split on the 7B shapes put
+// K=11008, N=4096, M=64 at NF 2 / split 8, 29.6 us, where the 4 TB/s charge picked NF 4 /
+// split 15, 32.1 us; the other few-tile shapes keep their picks). Knob 9 forces NF, knob 7
+// ksw.
 struct RbShape {
     int nf, ksw, tiles_m, tiles_n;
 };
@@ -1208,7 +1212,7 @@ RbShape rb_shape(const Weights& w, const Knobs& kn, int M)
     const int G = w.K / 128;
     const int cus = device_cus();
     const int tiles_m = (M + kRbBM - 1) / kRbBM;
-    const double hbm = 4.0e12, t_launch = 2e-6;
+    const double hbm = 2.0e12, t_launch = 2e-6;
     const double ybytes = (double)M * w.N * 4;
     // The 8-bit form is instantiated for NF 1 and 2 only (twice the code registers per
     // fragment); a forced NF of 4 falls back to the pick there.
