@@ -598,12 +598,9 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
         mfma_ops(R1);
         issue_a(t + 3, (ph + 3) & 3);
         if constexpr (ph == 0) issue_b((t >> 2) + 2, nbuf);
-#pragma unroll
-        for (int g = 0; g < 8; ++g) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+        // The second half is left to the compiler's scheduler: a pattern of one MFMA per LDS
+        // read (8 reads, then 8 MFMAs) measured 0.2-0.5% slower (M=2048 K=11008 214.8 against
+        // 213.8 us; K=4096 201.3 against 201.0 us).
         __builtin_amdgcn_sched_barrier(0);
     };
     using std::integral_constant;
