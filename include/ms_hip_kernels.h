@@ -168,7 +168,11 @@ int ms_hip_nbits_gemm_dev_f16(void* handle, const void* dA16, float* dY, int M, 
 /* Allocation-free form of ms_hip_nbits_gemm_dev, for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc). No counterpart in the reference. Same arguments, kernels and
- * results as ms_hip_nbits_gemm_dev; the workspace comes from a fixed scratch array
+ * results as ms_hip_nbits_gemm_dev, with one exception: a call that
+ * ms_hip_nbits_gemm_dev would run on mfma_w4_rb (M > 16 prefill) needs the handle's
+ * chunk-major scale copy, which the first such eager call builds (an allocation); until
+ * one has, this entry runs the call on mfma_w4 (the exact-scale prefill kernel: the same
+ * 2e-3 relative Frobenius bar, not bit-identical). The workspace comes from a fixed scratch array
  * that the library holds on each GPU it runs on until the process ends (96 MiB of
  * data and 64 Ki counters; enough for M = 2048 on the Llama-2-7B MLP shapes). A call
  * that needs more returns MS_HIP_ERR_INVALID without launching anything. Every call

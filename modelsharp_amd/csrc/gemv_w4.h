@@ -119,9 +119,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
     const int am = idx / C, ac = idx - am * C;
     const int aoff = idx < na ? (am * p.K + ac * 32) * 4 : kOOB;
     float4 av[8];
+    // The chunk's 16-byte offsets ride in the scalar offset, so kOOB itself is never
+    // added to in int arithmetic (the hardware adds them as unsigned 32-bit values, and
+    // kOOB + 112 still lies past every buffer).
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-        av[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ra, aoff + 16 * j, 0, 0));
+        av[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ra, aoff, 16 * j, 0));
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- 2. weight stream: NB batches of U steps in flight ----------------------------

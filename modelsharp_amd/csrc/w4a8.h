@@ -1,6 +1,6 @@
 // w4a8.h — the opt-in W4A8 product (MODELSHARP_W4A8): activations quantized to int8 per
 // (row, K-block), integer block dots against signed weight codes, fp32 block terms added
-// in block order. Bit for bit the reference's native ms_qgemm_w4a8
+// in block order. Bit for bit the reference's native ms_qgemm_w4a8 built without FP contraction
 // (native/src/qgemm_w4a8.cpp:247-296 quantizer, :622-679 reduce, which its VNNI driver
 // reproduces value for value):
 //   s_a(m, b) = max|a[m, block b]| / 127,  aq = lrint(a * (1 / s_a)) clamped to [-127, 127];

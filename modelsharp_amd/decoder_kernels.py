@@ -34,19 +34,31 @@ def _torch():
 
 
 class _DeviceInputs:
-    """Device copies of host arrays, one per array object (initializers)."""
+    """Device copies of host arrays. Initializers (names the context marks constant: norm
+    weights, rotary caches) are uploaded once and kept, keyed by the array object; any
+    other host array (a feed of this run) is uploaded for the call and not kept."""
 
-    def __init__(self):
+    def __init__(self, device="cuda"):
         self._cache: dict[int, tuple] = {}
+        self._device = device
 
-    def f32(self, t):
+    @property
+    def cached(self) -> int:
+        return len(self._cache)
+
+    def input(self, ctx: GraphContext, name: str):
+        return self.f32(ctx.get_tensor(name), keep=ctx.is_constant(name))
+
+    def f32(self, t, keep=False):
         torch = _torch()
         if isinstance(t, np.ndarray):
-            hit = self._cache.get(id(t))
-            if hit is not None and hit[0] is t:
-                return hit[1]
-            d = torch.from_numpy(np.ascontiguousarray(t, dtype=np.float32)).cuda()
-            self._cache[id(t)] = (t, d)
+            if keep:
+                hit = self._cache.get(id(t))
+                if hit is not None and hit[0] is t:
+                    return hit[1]
+            d = torch.from_numpy(np.ascontiguousarray(t, dtype=np.float32)).to(self._device)
+            if keep:
+                self._cache[id(t)] = (t, d)
             return d
         if t.dtype != torch.float32:
             t = t.float()
@@ -55,7 +67,7 @@ class _DeviceInputs:
     def i32(self, t):
         torch = _torch()
         if isinstance(t, np.ndarray):
-            return torch.from_numpy(np.ascontiguousarray(t, dtype=np.int32)).cuda()
+            return torch.from_numpy(np.ascontiguousarray(t, dtype=np.int32)).to(self._device)
         return t.to(torch.int32).contiguous()
 
 
@@ -80,8 +92,8 @@ class HipSimplifiedLayerNormalizationKernel(IKernel):
 
     def execute(self, node: GraphNode, ctx: GraphContext) -> None:
         torch = _torch()
-        x = self._dev.f32(ctx.get_tensor(node.inputs[0]))
-        scale = self._dev.f32(ctx.get_tensor(node.inputs[1]))
+        x = self._dev.input(ctx, node.inputs[0])
+        scale = self._dev.input(ctx, node.inputs[1])
         rank = x.dim()
         axis = node.attr_int("axis", -1)
         if axis < 0:
@@ -109,11 +121,11 @@ class HipSkipSimplifiedLayerNormalizationKernel(IKernel):
 
     def execute(self, node: GraphNode, ctx: GraphContext) -> None:
         torch = _torch()
-        inp = self._dev.f32(ctx.get_tensor(node.inputs[0]))
-        skip = self._dev.f32(ctx.get_tensor(node.inputs[1]))
-        gamma = self._dev.f32(ctx.get_tensor(node.inputs[2]))
-        beta = self._dev.f32(ctx.get_tensor(node.inputs[3])) if len(node.inputs) > 3 and node.inputs[3] else None
-        bias = self._dev.f32(ctx.get_tensor(node.inputs[4])) if len(node.inputs) > 4 and node.inputs[4] else None
+        inp = self._dev.input(ctx, node.inputs[0])
+        skip = self._dev.input(ctx, node.inputs[1])
+        gamma = self._dev.input(ctx, node.inputs[2])
+        beta = self._dev.input(ctx, node.inputs[3]) if len(node.inputs) > 3 and node.inputs[3] else None
+        bias = self._dev.input(ctx, node.inputs[4]) if len(node.inputs) > 4 and node.inputs[4] else None
         eps = _attr_float(node, "epsilon", 1e-5)
         norm = gamma.numel()
         total = inp.numel()
@@ -141,8 +153,8 @@ class _Elementwise(IKernel):
         self._dev = _DeviceInputs()
 
     def _same_shape(self, node, ctx):
-        a = self._dev.f32(ctx.get_tensor(node.inputs[0]))
-        b = self._dev.f32(ctx.get_tensor(node.inputs[1]))
+        a = self._dev.input(ctx, node.inputs[0])
+        b = self._dev.input(ctx, node.inputs[1])
         if tuple(a.shape) != tuple(b.shape):
             raise ModelSharpException(
                 f"{self.op_type} on the device takes equal shapes; got {list(a.shape)} and {list(b.shape)}.")
@@ -173,7 +185,7 @@ class HipSigmoidKernel(_Elementwise):
     op_type = "Sigmoid"
 
     def execute(self, node, ctx):
-        x = self._dev.f32(ctx.get_tensor(node.inputs[0]))
+        x = self._dev.input(ctx, node.inputs[0])
         y = _torch().empty_like(x)
         native.sigmoid(x.data_ptr(), y.data_ptr(), x.numel(), _stream(x))
         ctx.set(node.outputs[0], y)
@@ -237,13 +249,17 @@ class _Cache:
     k: object
     v: object
     capacity: int
+    returned: int = -1   # rows of the present K/V views the last call handed out
 
 
 class HipGroupQueryAttentionKernel(IKernel):
     """GroupQueryAttention (GroupQueryAttentionKernel.cs:64-323). Present K/V are views
-    into per-node capacity buffers: when the next step passes them back as past K/V,
-    the new rows are appended in place (ms_hip_gqa past_in_present) instead of
-    copying the past, and the buffer doubles when it fills."""
+    into per-node capacity buffers: when the next step passes back exactly the views the
+    last call returned (same K and V buffers, past equal to the rows handed out), the
+    new rows are appended in place (ms_hip_gqa past_in_present) instead of copying the
+    past, and the buffer doubles when it fills. Any other past (an older step's present,
+    two candidates from one past, a rollback) is copied into a fresh buffer, so present
+    tensors handed out earlier never change, as with the reference's fresh tensors."""
     op_type = "GroupQueryAttention"
 
     def __init__(self):
@@ -251,14 +267,19 @@ class HipGroupQueryAttentionKernel(IKernel):
         self._caches: dict[str, _Cache] = {}
         self._workspace: dict[str, object] = {}   # key-split workspace per node (ms_hip_gqa_workspace_size)
 
-    def _cache_for(self, node, B, KH, D, past_k, total, device):
+    def _cache_for(self, node, B, KH, D, past_k, past_v, past, total, device):
         torch = _torch()
         c = self._caches.get(node.name)
-        if (c is not None and past_k is not None and c.capacity >= total and isinstance(past_k, torch.Tensor)
-                and past_k.data_ptr() == c.k.data_ptr() and tuple(c.k.shape[:2]) == (B, KH)
-                and c.k.shape[3] == D):
+        follows = (c is not None and past_k is not None and past > 0 and past == c.returned
+                   and isinstance(past_k, torch.Tensor) and isinstance(past_v, torch.Tensor)
+                   and past_k.data_ptr() == c.k.data_ptr() and past_v.data_ptr() == c.v.data_ptr()
+                   and tuple(c.k.shape[:2]) == (B, KH) and c.k.shape[3] == D)
+        if follows and c.capacity >= total:
             return c, True
-        cap = max(total, 2 * (c.capacity if c is not None else 0), 64)
+        # A fresh buffer (the old one may back present tensors the caller still holds):
+        # twice the old capacity when a followed cache fills, else room to append as much
+        # again as this call holds.
+        cap = max(total, 2 * c.capacity, 64) if follows else max(2 * total, 64)
         k = torch.empty((B, KH, cap, D), dtype=torch.float32, device=device)
         v = torch.empty_like(k)
         c = _Cache(k, v, cap)
@@ -274,7 +295,7 @@ class HipGroupQueryAttentionKernel(IKernel):
         if H % KH != 0:
             raise ModelSharpException(
                 f"GroupQueryAttention num_heads={H} must be a multiple of kv_num_heads={KH}.")
-        q = self._dev.f32(ctx.get_tensor(node.inputs[0]))
+        q = self._dev.input(ctx, node.inputs[0])
         if q.dim() != 3:
             raise ModelSharpException(
                 f"GroupQueryAttention supports only 3-D query [B, S, hidden]; got rank {q.dim()}.")
@@ -293,8 +314,8 @@ class HipGroupQueryAttentionKernel(IKernel):
             D = hidden // unit
             Skv = Sq
         else:
-            k = self._dev.f32(ctx.get_tensor(key_name))
-            v = self._dev.f32(ctx.get_tensor(value_name))
+            k = self._dev.input(ctx, key_name)
+            v = self._dev.input(ctx, value_name)
             if k.dim() != 3 or v.dim() != 3:
                 raise ModelSharpException("GroupQueryAttention supports only unpacked 3-D key/value.")
             q_hidden = int(q.shape[2])
@@ -331,9 +352,9 @@ class HipGroupQueryAttentionKernel(IKernel):
             if len(node.inputs) <= 8 or not node.inputs[7] or not node.inputs[8]:
                 raise ModelSharpException(
                     "GroupQueryAttention do_rotary=1 requires cos_cache (input 7) and sin_cache (input 8).")
-            cos = self._dev.f32(ctx.get_tensor(node.inputs[7]))
-            sin = self._dev.f32(ctx.get_tensor(node.inputs[8]))
-        cache, in_place = self._cache_for(node, B, KH, D, past_k, total, q.device)
+            cos = self._dev.input(ctx, node.inputs[7])
+            sin = self._dev.input(ctx, node.inputs[8])
+        cache, in_place = self._cache_for(node, B, KH, D, past_k, past_v, past, total, q.device)
         if past and not in_place:
             pk_src, pv_src = self._dev.f32(past_k), self._dev.f32(past_v)
         else:
@@ -359,6 +380,7 @@ class HipGroupQueryAttentionKernel(IKernel):
         native.gqa(d, q.data_ptr(), ptr(k), ptr(v), ptr(pk_src), ptr(pv_src), ptr(seqlens), ptr(cos), ptr(sin),
                    out.data_ptr(), cache.k.data_ptr(), cache.v.data_ptr(), ptr(ws), ws_bytes, _stream(q))
         ctx.set(node.outputs[0], out)
+        cache.returned = total
         if _present(node, 1):
             ctx.set(node.outputs[1], cache.k[:, :, :total, :])
         if _present(node, 2):

@@ -71,8 +71,13 @@ class ModelGraph:
 class GraphContext:
     """Name -> tensor environment of one run (GraphContext.cs)."""
 
-    def __init__(self, values: dict[str, Any] | None = None):
+    def __init__(self, values: dict[str, Any] | None = None, constants=()):
         self.values: dict[str, Any] = dict(values or {})
+        # Names bound to the graph's initializers: device kernels may keep their uploads.
+        self.constants: frozenset[str] = frozenset(constants)
+
+    def is_constant(self, name: str) -> bool:
+        return name in self.constants
 
     def get_tensor(self, name: str):
         if name not in self.values:
@@ -133,7 +138,7 @@ class Engine:
     def run(self, feeds: dict[str, Any]) -> dict[str, Any]:
         env = dict(self.graph.initializers)
         env.update(feeds)
-        ctx = GraphContext(env)
+        ctx = GraphContext(env, constants=set(self.graph.initializers) - set(feeds))
         for node in self.graph.nodes:
             ok, kernel = self.kernels.try_get(node.op_type)
             if not ok:

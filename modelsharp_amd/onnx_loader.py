@@ -233,6 +233,12 @@ class _Parser:
         if dt in _RAW_DTYPE or dt in (DT_BOOL, DT_BFLOAT16):
             if raw is not None and count > 0:
                 buf, s, e, path, off = raw
+                # Every raw type reads itemsize * count bytes of its own field and no more.
+                itemsize = 1 if dt == DT_BOOL else 2 if dt == DT_BFLOAT16 else np.dtype(_RAW_DTYPE[dt]).itemsize
+                if itemsize * count > e - s:
+                    raise ModelSharpException(
+                        f"Initializer '{name}' declares {count} elements but only {(e - s) // itemsize} "
+                        "are available in its data (malformed, truncated, or adversarial model).")
                 if dt == DT_BOOL:
                     arr = np.frombuffer(buf, np.uint8, count, s) != 0
                 elif dt == DT_BFLOAT16:
@@ -240,10 +246,6 @@ class _Parser:
                     arr = bits.view(np.float32)
                 else:
                     npdt = np.dtype(_RAW_DTYPE[dt])
-                    if npdt.itemsize * count > e - s:
-                        raise ModelSharpException(
-                            f"Initializer '{name}' declares {count} elements but only {(e - s) // npdt.itemsize} "
-                            "are available in its data (malformed, truncated, or adversarial model).")
                     arr = np.frombuffer(buf, npdt, count, s)
                     if path is not None:
                         src = FileSlice(path, off, npdt.itemsize * count, dt)

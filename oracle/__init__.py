@@ -6,7 +6,8 @@ it. liboracle_nbits.so is the C restatement of the reference's managed kernel
 and of its native W4A8 kernel (ms_nbits_oracle.c, citations there);
 _ref/libms_ref_qgemm.so and _ref/libms_ref_w4a8.so, when present, are the
 reference's own native ms_qgemm_nbits and ms_qgemm_w4a8 compiled from its
-sources.
+sources (without FP contraction), and _ref/libms_ref_w4a8_shipped.so its
+ms_qgemm_w4a8 with the reference Makefile's own flags (-ffast-math).
 """
 from __future__ import annotations
 
@@ -20,7 +21,6 @@ HERE = pathlib.Path(__file__).resolve().parent
 _vp = ctypes.c_void_p
 _lib = None
 _ref = None
-_ref_w4a8 = None
 
 
 class GqaDesc(ctypes.Structure):
@@ -59,6 +59,7 @@ def lib() -> ctypes.CDLL:
         L.msor_silu_mul.argtypes = [_vp, _vp, _vp, ctypes.c_int64]
         L.msor_gqa.argtypes = [ctypes.POINTER(GqaDesc)] + [_vp] * 11
         L.msor_qgemm_w4a8.argtypes = [_vp, _vp, _vp, _vp, _vp] + [ctypes.c_int] * 6
+        L.msor_w4a8_managed.argtypes = [_vp] * 6 + [ctypes.c_int] * 5
         _lib = L
     return _lib
 
@@ -77,18 +78,23 @@ def ref_lib():
     return _ref
 
 
-def ref_w4a8_lib():
-    """The reference's own ms_qgemm_w4a8 (built from its sources), or None."""
-    global _ref_w4a8
-    if _ref_w4a8 is None:
-        path = HERE / "_ref" / "libms_ref_w4a8.so"
+_W4A8_LIBS = {"plain": "libms_ref_w4a8.so", "shipped": "libms_ref_w4a8_shipped.so"}
+_ref_w4a8_libs: dict = {}
+
+
+def ref_w4a8_lib(build="plain"):
+    """The reference's own ms_qgemm_w4a8 built from its sources, or None: "plain" without FP
+    contraction (the bit-exact witness), "shipped" with its native/Makefile's CXXFLAGS
+    (-ffast-math)."""
+    if build not in _ref_w4a8_libs:
+        path = HERE / "_ref" / _W4A8_LIBS[build]
         if not path.is_file():
             return None
         L = ctypes.CDLL(str(path))
         L.ms_qgemm_w4a8.restype = None
         L.ms_qgemm_w4a8.argtypes = [_vp, _vp, _vp, _vp, _vp] + [ctypes.c_int] * 5
-        _ref_w4a8 = L
-    return _ref_w4a8
+        _ref_w4a8_libs[build] = L
+    return _ref_w4a8_libs[build]
 
 
 def threads() -> int:
@@ -182,9 +188,22 @@ def qgemm_w4a8(a, b, scales, zp_packed, N, K, bits, block_size, nthreads=None):
     return y
 
 
-def ref_qgemm_w4a8(a, b, scales, zp_packed, M, N, K, bits, block_size):
-    """The reference's native ms_qgemm_w4a8, or None if not built."""
-    L = ref_w4a8_lib()
+def w4a8_managed(a, b, scales, zp_packed, N, K, block_size, zp_float=None, nthreads=None):
+    """The reference's managed W4A8 product (4-bit codes), msor_w4a8_managed."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    M = a.size // K
+    y = np.empty((M, N), np.float32)
+    zp_packed = None if zp_packed is None else np.ascontiguousarray(zp_packed, dtype=np.uint8)
+    zp_float = None if zp_float is None else np.ascontiguousarray(zp_float, dtype=np.float32)
+    lib().msor_w4a8_managed(_ptr(a), _ptr(np.ascontiguousarray(b, dtype=np.uint8)),
+                            _ptr(np.ascontiguousarray(scales, dtype=np.float32)), _ptr(zp_packed), _ptr(zp_float),
+                            _ptr(y), M, N, K, block_size, threads() if nthreads is None else nthreads)
+    return y
+
+
+def ref_qgemm_w4a8(a, b, scales, zp_packed, M, N, K, bits, block_size, build="plain"):
+    """The reference's native ms_qgemm_w4a8 (see ref_w4a8_lib), or None if not built."""
+    L = ref_w4a8_lib(build)
     if L is None:
         return None
     a = np.ascontiguousarray(a, dtype=np.float32)

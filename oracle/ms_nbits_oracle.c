@@ -316,3 +316,97 @@ void msor_qgemm_w4a8(const float* a, const uint8_t* b, const float* scales, cons
     free(aq);
     free(sa);
 }
+
+/* ---- W4A8, the managed variant ----------------------------------------------------------
+ * Restates MatMulNBitsKernel.ExecuteColumnW4A8 (MatMulNBitsKernel.cs:275-331) with
+ * MatMulNBitsSimd.QuantizeActivationInt8 (MatMulNBitsSimd.cs:225-255) and DotU8xU8
+ * (:268-298, an exact integer dot): what the reference runs under MODELSHARP_W4A8 for 4-bit
+ * codes when its native library does not take the call (library absent, or float zero
+ * points, MatMulNBitsKernel.cs:174, :209).
+ *
+ * Against the native kernel above it differs in the quantizer's reciprocal
+ * (inv = 127 / absmax instead of 1 / (absmax / 127), so a code can move by one where
+ * a * inv lies next to a rounding tie), in the clamp (-128 instead of -127, unreachable
+ * since |a * inv| <= 127 up to rounding), in skipping all-zero activation blocks (the
+ * native kernel adds a zero term) and in taking float zero points: the block term is
+ * s_w * s_a * (float)(dot(aq, q) - zp * sum(aq)), with q the raw code.
+ *
+ * Pinning (tests/test_oracle.py): equal bit for bit to msor_qgemm_w4a8 when every
+ * activation block quantizes exactly (integer rows whose block maximum is 127: both
+ * reciprocals are 1), codes within one step of the native quantizer's, and the reference
+ * test's accuracy bar against the exact product. */
+void msor_w4a8_managed(const float* a, const uint8_t* b, const float* scales, const uint8_t* zp_packed,
+                       const float* zp_float, float* y, int M, int N, int K, int block_size, int nthreads)
+{
+    const int bits = 4;
+    const int nb = (K + block_size - 1) / block_size;
+    const int blob = (block_size * bits + 7) / 8;
+    const int zrb = (nb * bits + 7) / 8;
+    const int64_t row_bytes = (int64_t)nb * blob;
+    if (nthreads < 1) nthreads = 1;
+    /* the activation codes do not depend on the column: quantize every (row, block) once */
+    int8_t* aq = (int8_t*)malloc((size_t)(M > 0 ? M : 1) * (size_t)nb * (size_t)block_size);
+    float* sa = (float*)malloc(sizeof(float) * (size_t)(M > 0 ? M : 1) * (size_t)nb);
+    int* sum_aq = (int*)malloc(sizeof(int) * (size_t)(M > 0 ? M : 1) * (size_t)nb);
+    for (int m = 0; m < M; ++m) {
+        for (int bk = 0; bk < nb; ++bk) {
+            const int k0 = bk * block_size;
+            const int len = (block_size < K - k0) ? block_size : K - k0;
+            const float* src = a + (int64_t)m * K + k0;
+            int8_t* dst = aq + ((int64_t)m * nb + bk) * block_size;
+            /* MatMulNBitsSimd.cs:228-254 */
+            float absmax = 0.0f;
+            for (int i = 0; i < len; ++i) {
+                const float v = fabsf(src[i]);
+                if (v > absmax) absmax = v;
+            }
+            int sum = 0;
+            if (absmax == 0.0f) {
+                memset(dst, 0, (size_t)block_size);
+                sa[(int64_t)m * nb + bk] = 0.0f;
+            } else {
+                const float inv = 127.0f / absmax;
+                sa[(int64_t)m * nb + bk] = absmax / 127.0f;
+                for (int i = 0; i < len; ++i) {
+                    /* MathF.Round: to nearest, ties to even (rintf in the default mode) */
+                    int q = (int)rintf(src[i] * inv);
+                    if (q > 127) q = 127;
+                    else if (q < -128) q = -128;
+                    dst[i] = (int8_t)q;
+                    sum += q;
+                }
+            }
+            sum_aq[(int64_t)m * nb + bk] = sum;
+        }
+    }
+#pragma omp parallel for num_threads(nthreads) schedule(static)
+    for (int n = 0; n < N; ++n) {
+        for (int m = 0; m < M; ++m) {
+            float total = 0.0f;
+            for (int bk = 0; bk < nb; ++bk) {
+                const float sw = scales[(int64_t)n * nb + bk];
+                float zp;
+                if (zp_float) zp = zp_float[(int64_t)n * nb + bk];
+                else if (zp_packed) zp = (float)msor_unpack_nbit(zp_packed, (int64_t)n * zrb, bk, bits);
+                else zp = 8.0f;
+                const int k0 = bk * block_size;
+                const int len = (block_size < K - k0) ? block_size : K - k0;
+                if (len <= 0) break;
+                const float s_a = sa[(int64_t)m * nb + bk];
+                if (s_a == 0.0f) continue;   /* MatMulNBitsKernel.cs:310 */
+                const int8_t* q8 = aq + ((int64_t)m * nb + bk) * block_size;
+                const int64_t blob_base = (int64_t)n * row_bytes + (int64_t)bk * blob;
+                /* :314-322: sum over (aq + 128) * q, less 128 * sum(q): exactly sum(aq * q) */
+                int32_t dot = 0;
+                for (int i = 0; i < len; ++i) dot += (int32_t)q8[i] * msor_unpack_nbit(b, blob_base, i, bits);
+                /* :325: scaleW * scaleA * (dotAqQ - zp * sumAq), float arithmetic throughout */
+                const float comp = zp * (float)sum_aq[(int64_t)m * nb + bk];
+                total += sw * s_a * ((float)dot - comp);
+            }
+            y[(int64_t)m * N + n] = total;
+        }
+    }
+    free(aq);
+    free(sa);
+    free(sum_aq);
+}

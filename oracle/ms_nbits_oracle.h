@@ -68,6 +68,10 @@ void msor_matmul_f64(const float* a, const float* w, double* y,
 void msor_w4a8_quantize(const float* a, int8_t* aq, float* sa, int M, int K, int block_size);
 void msor_qgemm_w4a8(const float* a, const uint8_t* b, const float* scales, const uint8_t* zp_packed,
                      float* y, int M, int N, int K, int bits, int block_size, int nthreads);
+/* The managed W4A8 variant (MatMulNBitsKernel.ExecuteColumnW4A8, 4-bit codes): packed,
+ * float (zp_float, [N][nb]) or no zero points. */
+void msor_w4a8_managed(const float* a, const uint8_t* b, const float* scales, const uint8_t* zp_packed,
+                       const float* zp_float, float* y, int M, int N, int K, int block_size, int nthreads);
 
 /* Decoder-layer neighbours (ms_decoder_oracle.c). */
 void msor_rmsnorm(const float* x, const float* scale, float* y, float* inv_std, int64_t rows, int norm, float eps);

@@ -200,6 +200,60 @@ def test_gqa_resident_cache_appends_in_place(gpu):
     k._caches.clear()
 
 
+def test_gqa_two_steps_from_one_past_leave_earlier_presents_alone(gpu):
+    """Two candidate tokens decoded from the same past (beam search, a retry): the second
+    call must not write into the rows the first call returned as its present K/V. Each
+    call's outputs and presents are checked against the oracle after both calls, and a
+    third step that follows the second call's present appends in place again."""
+    r = np.random.default_rng(8)
+    H, KH, D, S0 = 4, 2, 64, 5
+    cos_rows = 64
+    ang = np.outer(np.arange(cos_rows), 1.0 / 10000 ** (np.arange(D // 2) / (D // 2)))
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    attrs = {"num_heads": H, "kv_num_heads": KH, "do_rotary": 1}
+    node0 = GraphNode("GroupQueryAttention", "attn0", ["qkv", "", "", "", "", "", "", "cos", "sin"],
+                      ["out", "present_k", "present_v"], attrs)
+    node = GraphNode("GroupQueryAttention", "attn0", ["qkv", "", "", "past_k", "past_v", "", "", "cos", "sin"],
+                     ["out", "present_k", "present_v"], attrs)
+    k = HipGroupQueryAttentionKernel()
+
+    def desc(S, past):
+        return oracle.GqaDesc(batch=1, q_seq=S, kv_seq=S, num_heads=H, kv_num_heads=KH, head_dim=D, packed_qkv=1,
+                              past_seq=past, present_capacity=past + S, do_rotary=1, cos_rows=cos_rows,
+                              cos_cols=D // 2, local_window_size=-1)
+
+    qkv0 = r.standard_normal((1, S0, (H + 2 * KH) * D)).astype(np.float32)
+    ctx = GraphContext({"qkv": dev(qkv0), "cos": cos, "sin": sin})
+    k.execute(node0, ctx)
+    pk0, pv0 = ctx.get_tensor("present_k"), ctx.get_tensor("present_v")
+    _, hk0, hv0 = oracle.gqa(desc(S0, 0), qkv0, None, None, None, None, None, cos, sin)
+    runs = []
+    for cand in range(2):
+        qkv = r.standard_normal((1, 1, (H + 2 * KH) * D)).astype(np.float32)
+        c = GraphContext({"qkv": dev(qkv), "cos": cos, "sin": sin, "past_k": pk0, "past_v": pv0})
+        k.execute(node, c)
+        runs.append((qkv, c.get_tensor("out"), c.get_tensor("present_k"), c.get_tensor("present_v")))
+    log(f"candidate presents at {runs[0][2].data_ptr():#x} and {runs[1][2].data_ptr():#x}")
+    for i, (qkv, out, pk, pv) in enumerate(runs):
+        ref, rk, rv = oracle.gqa(desc(1, S0), qkv, None, None, hk0, hv0, None, cos, sin)
+        check_gqa(host(out), host(pk), host(pv), ref, rk, rv, f"candidate {i} after both calls")
+    check_gqa(host(runs[0][1]), host(pk0), host(pv0), oracle.gqa(desc(1, S0), runs[0][0], None, None, hk0, hv0,
+                                                                   None, cos, sin)[0], hk0, hv0, "the shared past")
+    # the next step from the second candidate's present follows the cache: in place
+    qkv2 = r.standard_normal((1, 1, (H + 2 * KH) * D)).astype(np.float32)
+    c = GraphContext({"qkv": dev(qkv2), "cos": cos, "sin": sin, "past_k": runs[1][2], "past_v": runs[1][3]})
+    k.execute(node, c)
+    assert c.get_tensor("present_k").data_ptr() == runs[1][2].data_ptr()
+    _, rk1, rv1 = oracle.gqa(desc(1, S0), runs[1][0], None, None, hk0, hv0, None, cos, sin)
+    ref, rk, rv = oracle.gqa(desc(1, S0 + 1), qkv2, None, None, rk1, rv1, None, cos, sin)
+    check_gqa(host(c.get_tensor("out")), host(c.get_tensor("present_k")), host(c.get_tensor("present_v")), ref, rk,
+              rv, "step after candidate 1")
+    # the first candidate's present is still its own
+    _, rk0, rv0 = oracle.gqa(desc(1, S0), runs[0][0], None, None, hk0, hv0, None, cos, sin)
+    assert np.array_equal(host(runs[0][2]), rk0) and np.array_equal(host(runs[0][3]), rv0)
+    k._caches.clear()
+
+
 # ---- one decoder layer end to end ---------------------------------------------------------------
 def layer_graph(hid, H, KH, D, inter, bs, seed):
     """A Llama-family decoder layer as the onnxruntime-genai INT4 exports lay it out:
@@ -297,3 +351,18 @@ def test_decoder_layer_end_to_end(gpu, fused):
         log(f"  step {step} (S={S}) fused={fused}: max err / max|y| {err:.2e}")
         assert err <= 1e-4
         assert np.allclose(host(t2), rt2, rtol=1e-5, atol=1e-5 * np.abs(rt2).max())
+
+
+# ---- the reference's own known answers (tests/golden/decoder_kats.json) -------------------------
+import decoder_kats  # noqa: E402
+
+_KAT_TOL, _KAT_CASES = decoder_kats.load()
+
+
+@pytest.mark.parametrize("case", _KAT_CASES, ids=[c["name"] for c in _KAT_CASES])
+def test_reference_known_answers(gpu, case):
+    """FusedLlmNormTests.cs:47-131, GqaGenaiTests.cs:106-381, GqaSlidingWindowTests.cs:110-245
+    through the device kernels behind the operator interface, at the reference tests' 1e-4
+    (host arrays in the context, as those tests build it)."""
+    log(f"decoder known answer {case['name']}")
+    decoder_kats.check(case, decoder_kats.device_run(case), _KAT_TOL)

@@ -12,7 +12,8 @@ import pytest
 
 from conftest import ROOT, kat_arrays
 from modelsharp_amd import native
-from modelsharp_amd.graph import (Engine, GraphContext, GraphNode, KernelRegistry, ModelGraph, ModelSharpException,
+from modelsharp_amd.graph import (Engine, GraphContext, GraphNode, IKernel, KernelRegistry, ModelGraph,
+                                  ModelSharpException,
                                   UnsupportedOperatorException)
 from modelsharp_amd.hip_kernel import HipMatMulNBitsKernel, register_kernels
 
@@ -377,3 +378,37 @@ def test_gqa_descriptor_checks():
     assert native.gqa_workspace_size(d) == 2 * 4 * 64 * (64 + 2) * 4   # units x splits x (D + 2) floats
     d.head_dim = 40   # the per-unit kernel keeps every score of a unit in LDS
     assert lib.ms_hip_gqa_check(ctypes.byref(d)) == native.MS_HIP_ERR_UNSUPPORTED
+
+
+def test_device_inputs_keep_initializers_only():
+    """Feeds arrive as new host arrays every run: uploading them must not grow the
+    kernels' upload cache, while an initializer is uploaded once and reused."""
+    import torch
+    from modelsharp_amd.decoder_kernels import _DeviceInputs
+    dev = _DeviceInputs(device="cpu")
+    w = np.arange(8, dtype=np.float32)
+    first = None
+    for i in range(6):
+        ctx = GraphContext({"w": w, "x": np.full(8, i, np.float32)}, constants={"w"})
+        dw, dx = dev.input(ctx, "w"), dev.input(ctx, "x")
+        first = dw if first is None else first
+        assert dw is first and torch.equal(dx, torch.full((8,), float(i)))
+        assert dev.cached == 1
+
+
+def test_engine_marks_initializers_constant():
+    """Engine.run binds the graph's initializers as constants; a feed that shadows one
+    is not."""
+    seen = {}
+
+    class Probe(IKernel):
+        op_type = "Probe"
+
+        def execute(self, node, ctx):
+            seen.update({n: ctx.is_constant(n) for n in node.inputs})
+            ctx.set(node.outputs[0], ctx.get_tensor(node.inputs[0]))
+
+    g = ModelGraph([GraphNode("Probe", "p", ["x", "w", "v"], ["y"])],
+                   {"w": np.ones(2, np.float32), "v": np.zeros(2, np.float32)}, ["x"], ["y"])
+    Engine(g, KernelRegistry().register(Probe())).run({"x": np.ones(2, np.float32), "v": np.ones(2, np.float32)})
+    assert seen == {"x": False, "w": True, "v": False}

@@ -118,3 +118,20 @@ def test_error_messages(tmp_path):
         L.parse_model(W.vi(1, 8))
     with pytest.raises(ModelSharpException, match="Unsupported tensor data_type 13"):
         load([W.vi(1, 1) + W.vi(2, 13) + W.s(8, "u") + W.ld(9, b"\0" * 8)])
+
+
+def test_truncated_bfloat16_raw_data_is_rejected(tmp_path):
+    """A bf16 initializer declaring more elements than its raw bytes hold raises the
+    loader's element-count error instead of reading the next fields or tensors of the file
+    (the count guard alone, count <= bytes, would let 3 elements read 6 bytes of a 4-byte
+    field)."""
+    p = tmp_path / "b.onnx"
+    raw = np.array([0x3FC0, 0xC000], np.uint16).tobytes()
+    bad = W.vi(1, 3) + W.vi(2, L.DT_BFLOAT16) + W.s(8, "h") + W.ld(9, raw)
+    after = W.tensor("next", np.arange(4, dtype=np.float32))
+    p.write_bytes(W.model([], [bad, after], [], []))
+    with pytest.raises(ModelSharpException, match="'h' declares 3 elements but only 2 are available"):
+        L.load_model(str(p))
+    ok = W.vi(1, 2) + W.vi(2, L.DT_BFLOAT16) + W.s(8, "h") + W.ld(9, raw)
+    p.write_bytes(W.model([], [ok, after], [], []))
+    assert np.array_equal(L.load_model(str(p)).initializers["h"], np.array([1.5, -2.0], np.float32))

@@ -209,6 +209,35 @@ def test_w4a8_live_reference_both_drivers():
     assert out.stdout.strip().splitlines()[-1] == "1"
 
 
+def test_w4a8_against_the_shipped_build_of_the_reference():
+    """The reference's native/Makefile builds qgemm_w4a8.cpp with -ffast-math, which lets the
+    compiler contract and reassociate the per-block fp32 terms. The restatement (bit-exact
+    to the source's own order, and through it the device) is held to the W4A8 accuracy bar
+    against that build and, far tighter, to the fp32 rounding of the block terms: each
+    output within 4 * nb * eps * sum_b |s_a * s_w * dot_b|."""
+    if oracle.ref_w4a8_lib("shipped") is None:
+        pytest.skip("oracle/_ref/libms_ref_w4a8_shipped.so not built (no reference checkout)")
+    for (M, N, K, bits, bs, asym) in [(3, 70, 384, 4, 32, True), (17, 33, 1000, 4, 128, False),
+                                      (4, 20, 256, 8, 64, True), (16, 256, 4096, 4, 32, True)]:
+        op = workloads.Op("w", K, N, bs, asym, 0.005, 0.05, bits)
+        b, s, z = workloads.make_weights(op, K + N + 1)
+        a = workloads.make_activations(M, K, M + K + 1, kind="rmsnorm")
+        y = oracle.qgemm_w4a8(a, b, s, z, N, K, bits, bs).astype(np.float64)
+        ys = oracle.ref_qgemm_w4a8(a, b, s, z, M, N, K, bits, bs, build="shipped").astype(np.float64)
+        rel = np.linalg.norm(y - ys) / np.linalg.norm(ys)
+        cos = float(np.sum(y * ys) / (np.linalg.norm(y) * np.linalg.norm(ys)))
+        assert rel < 0.03 and cos > 0.999, (rel, cos)
+        # |block terms|: s_a * s_w * |dot| summed over blocks, from the quantized operands
+        aq, sa = oracle.w4a8_quantize(a, K, bs)
+        nb = (K + bs - 1) // bs
+        Wc = np.clip(oracle.dequant_weights(b, np.ones_like(s), z, N, K, bits, bs), -127, 127).astype(np.float64)
+        Wc = np.pad(Wc, ((0, 0), (0, nb * bs - K)))
+        dots = np.einsum("mbk,nbk->mnb", aq.reshape(M, nb, bs).astype(np.float64), Wc.reshape(N, nb, bs))
+        terms = np.abs(dots) * sa[:, None, :].astype(np.float64) * s.reshape(N, nb)[None, :, :].astype(np.float64)
+        bound = 4 * nb * np.finfo(np.float32).eps * terms.sum(axis=2) + 1e-30
+        assert np.all(np.abs(y - ys) <= bound), (M, N, K, bits, bs, float(np.max(np.abs(y - ys) / bound)))
+
+
 def test_w4a8_quantizer_closed_form():
     """Per (row, block): s = max|a|/127; the largest element maps to +-127; every code is
     within half a step of a/s; an all-zero block gives s = 0 and zero codes; the padding
@@ -273,3 +302,86 @@ def test_w4a8_accuracy_bar_of_the_reference_test(bits, asym, M, N, K, bs):
     rel = np.linalg.norm(y - ref) / np.linalg.norm(ref)
     cos = float(np.sum(y * ref) / (np.linalg.norm(y) * np.linalg.norm(ref)))
     assert rel < 0.03 and cos > 0.999, (rel, cos)
+
+
+# ---- W4A8, the managed variant (MatMulNBitsKernel.cs:275-331) ------------------------------------
+def _exact_rows(M, K, bs, seed):
+    """Integer activations whose every block holds 127: both W4A8 quantizers then use a
+    reciprocal of exactly 1 and take the activations unchanged."""
+    a = np.random.default_rng(seed).integers(-127, 128, size=(M, K)).astype(np.float32)
+    a[:, ::bs] = 127.0
+    return a
+
+
+@pytest.mark.parametrize("bs,zp", [(32, "packed"), (128, "none"), (64, "packed")])
+def test_w4a8_managed_equals_native_when_quantization_is_exact(bs, zp):
+    """With exact activation codes the managed block term s_w * s_a * (dot(aq, q) - zp *
+    sum(aq)) is the native one, s_a * s_w * dot(aq, q - zp), in the same block order: the two
+    oracles must agree bit for bit (the native one is pinned bit-exact to the reference's
+    own qgemm_w4a8.cpp). A dropped zero-point term, a sign slip or a wrong code index in
+    the managed restatement breaks this."""
+    M, N, K = 3, 40, 512
+    op = workloads.Op("x", K, N, bs, zp == "packed", 0.01, 0.1)
+    b, s, z = workloads.make_weights(op, bs)
+    a = _exact_rows(M, K, bs, bs + 1)
+    y_m = oracle.w4a8_managed(a, b, s, z, N, K, bs)
+    y_n = oracle.qgemm_w4a8(a, b, s, z, N, K, 4, bs)
+    assert np.array_equal(y_m, y_n)
+
+
+def test_w4a8_managed_float_zero_points_exact_case():
+    """Float zero points (the case only the managed variant takes): with exact activation
+    codes the product is sum_b s_w * (dot(a, q) - zp * sum(a)) in fp32, which equals the
+    f64 product with W = (q - zp) * s to the fp32 rounding of the block terms."""
+    M, N, K, bs = 2, 24, 256, 32
+    op = workloads.Op("x", K, N, bs, False, 0.01, 0.1)
+    b, s, _ = workloads.make_weights(op, 5)
+    zf = np.random.default_rng(6).uniform(0, 15, size=N * (K // bs)).astype(np.float32)
+    a = _exact_rows(M, K, bs, 7)
+    y = oracle.w4a8_managed(a, b, s, None, N, K, bs, zp_float=zf)
+    q = oracle.dequant_weights(b, np.ones_like(s), None, N, K, 4, bs).astype(np.float64) + 8.0   # raw codes
+    zk = np.repeat(zf.reshape(N, -1), bs, axis=1).astype(np.float64)
+    sk = np.repeat(s.reshape(N, -1), bs, axis=1).astype(np.float64)
+    W = (q - zk) * sk
+    exact = a.astype(np.float64) @ W.T
+    bound = 4e-6 * (np.abs(a).astype(np.float64) @ np.abs(W).T) + 1e-6 * np.abs(a).astype(np.float64) @ (zk * sk).T
+    assert np.all(np.abs(y - exact) <= bound)
+
+
+@pytest.mark.parametrize("zp", ["packed", "none", "float"])
+@pytest.mark.parametrize("M,N,K,bs", [(1, 64, 128, 32), (8, 512, 4096, 128), (32, 64, 4096, 32)])
+def test_w4a8_managed_accuracy_bar(zp, M, N, K, bs):
+    """The W4A8 accuracy bar (rel-L2 < 0.03, cosine > 0.999, qgemm_w4a8_test.cpp:49-85)
+    against the f64 product of the dequantized weights, for every zero-point form the
+    managed variant takes."""
+    op = workloads.Op("acc", K, N, bs, zp == "packed", 0.005, 0.05)
+    b, s, z = workloads.make_weights(op, M + N + K)
+    zf = None
+    if zp == "float":
+        zf = np.random.default_rng(K).uniform(0, 15, size=N * (K // bs)).astype(np.float32)
+    a = workloads.make_activations(M, K, 7)
+    y = oracle.w4a8_managed(a, b, s, z, N, K, bs, zp_float=zf).astype(np.float64)
+    W = oracle.dequant_weights(b, s, z, N, K, 4, bs, zp_float=zf)
+    ref = oracle.matmul_f64(a, W.astype(np.float32))
+    rel = np.linalg.norm(y - ref) / np.linalg.norm(ref)
+    cos = float(np.sum(y * ref) / (np.linalg.norm(y) * np.linalg.norm(ref)))
+    assert rel < 0.03 and cos > 0.999, (rel, cos)
+
+
+def test_w4a8_managed_close_to_native_on_random_activations():
+    """On general activations the two variants differ only where a code sits next to a
+    rounding tie of the two reciprocals: at most one step of one code, so each output moves by
+    at most sum over such codes of s_a * s_w * |q - zp|; far below the W4A8 tolerance."""
+    M, N, K, bs = 4, 256, 2048, 32
+    op = workloads.Op("x", K, N, bs, True, 0.005, 0.05)
+    b, s, z = workloads.make_weights(op, 11)
+    a = workloads.make_activations(M, K, 12)
+    y_m = oracle.w4a8_managed(a, b, s, z, N, K, bs).astype(np.float64)
+    y_n = oracle.qgemm_w4a8(a, b, s, z, N, K, 4, bs).astype(np.float64)
+    _, sa = oracle.w4a8_quantize(a, K, bs)
+    Wabs = np.abs(oracle.dequant_weights(b, s, z, N, K, 4, bs)).astype(np.float64)
+    # one step of every code in a block: s_a * sum_k |W| per block, summed over blocks
+    per_block = np.add.reduceat(Wabs, np.arange(0, K, bs), axis=1)       # [N, nb]
+    bound = sa.astype(np.float64) @ per_block.T + 1e-6 * np.abs(y_n)
+    assert np.all(np.abs(y_m - y_n) <= bound)
+    assert np.linalg.norm(y_m - y_n) / np.linalg.norm(y_n) < 1e-3

@@ -6,9 +6,12 @@ SigmoidKernel.cs, GroupQueryAttentionKernel.cs (src/ModelSharp/Cpu/Kernels/...).
 """
 from __future__ import annotations
 
+import json
+
 import numpy as np
 import pytest
 
+import decoder_kats
 import oracle
 
 
@@ -204,3 +207,26 @@ def test_gqa_rotary_identity_and_norms():
     kk = k.reshape(2, 2, 16).transpose(1, 0, 2).astype(np.float64)
     pairs = lambda x: x[..., :8] ** 2 + x[..., 8:] ** 2
     assert np.allclose(pairs(Kr.astype(np.float64)), pairs(kk), rtol=1e-5)
+
+
+# ---- the reference's own known answers (tests/golden/decoder_kats.json) -------------------------
+_KAT_TOL, _KAT_CASES = decoder_kats.load()
+
+
+@pytest.mark.parametrize("case", _KAT_CASES, ids=[c["name"] for c in _KAT_CASES])
+def test_reference_known_answers(case):
+    """FusedLlmNormTests.cs:47-131, GqaGenaiTests.cs:106-381, GqaSlidingWindowTests.cs:110-245:
+    the oracle meets each case's expected outputs at the reference tests' 1e-4, including
+    the reading of seqlens_k as the last valid key index (Decode_WithPast_AndSeqlensK,
+    SeqlensK_BoundsKeyRange, DecodeWithPast_WindowExcludesOldCachedKeys)."""
+    decoder_kats.check(case, decoder_kats.oracle_run(case), _KAT_TOL)
+
+
+def test_reference_known_answers_catch_a_planted_mistake():
+    """The fixture rejects a seqlens_k read as a key count instead of the last valid index:
+    SeqlensK_BoundsKeyRange then lets both queries see key 1 as well."""
+    case = next(c for c in _KAT_CASES if c["name"] == "SeqlensK_BoundsKeyRange")
+    wrong = json.loads(json.dumps(case))
+    wrong["inputs"]["seqlens_k"]["data"] = [1]
+    with pytest.raises(AssertionError):
+        decoder_kats.check(case, decoder_kats.oracle_run(wrong), _KAT_TOL)

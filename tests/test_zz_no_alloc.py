@@ -66,6 +66,40 @@ def test_noalloc_matches_gemm_dev(torch_cuda, case):
     w.close()
 
 
+def test_noalloc_first_on_a_fresh_handle(torch_cuda):
+    """A fresh handle has no chunk-major scale copy (the first eager mfma_w4_rb call builds
+    it, which allocates): the allocation-free entry runs such a call on mfma_w4 instead,
+    within the prefill bar of the oracle; once an eager call has built the copy, the two
+    entries are bit-identical again."""
+    import oracle
+    torch = torch_cuda
+    op = workloads.Op("up", 4096, 11008, 32, True)
+    b, s, z = workloads.make_weights(op, seed=73)
+    w = native.NBitsWeights(b, s, z, op.N, op.K, 4, 32)
+    M = 128
+    assert w.launch_info(M)["kernel"] == "mfma_w4_rb"
+    stream = torch.cuda.current_stream().cuda_stream
+    a_h = workloads.make_activations(M, op.K, seed=74, kind="rmsnorm")
+    a = torch.from_numpy(a_h).cuda()
+    y_na = torch.full((M, op.N), float("nan"), device="cuda")
+    log(f"noalloc first: M={M} K={op.K} N={op.N} on a fresh handle")
+    w.gemm_dev_noalloc(a.data_ptr(), y_na.data_ptr(), M, stream)
+    torch.cuda.synchronize()
+    cols = np.arange(0, op.N, 41)
+    ref = oracle.matmul_nbits(a_h, b[cols], s.reshape(op.N, -1)[cols].ravel(), z[cols], len(cols), op.K, 4, 32)
+    got = y_na.cpu().numpy()[:, cols].astype(np.float64)
+    rel = np.linalg.norm(got - ref) / np.linalg.norm(ref.astype(np.float64))
+    log(f"  relative Frobenius error against the oracle {rel:.2e}")
+    assert rel <= 2e-3
+    y_ref = torch.full((M, op.N), float("nan"), device="cuda")
+    w.gemm_dev(a.data_ptr(), y_ref.data_ptr(), M, stream)
+    w.gemm_dev_noalloc(a.data_ptr(), y_na.data_ptr(), M, stream)
+    torch.cuda.synchronize()
+    assert np.array_equal(y_ref.cpu().numpy(), y_na.cpu().numpy())
+    w.device_error()
+    w.close()
+
+
 def test_noalloc_rejects_calls_beyond_its_scratch(torch_cuda):
     torch = torch_cuda
     op = workloads.Op("down", 11008, 4096, 32, True)
