@@ -255,6 +255,7 @@ def main() -> int:
     ap.add_argument("--rotate-mib", type=int, default=1024, help="bytes the weight rotation touches")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline budget (0 = skip)")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-layer", action="store_true", help="skip the device-resident decoder layer")
     ap.add_argument("--detail", default="", help="also write per-op results of every workload to this JSON file")
     ap.add_argument("--op", default="", help="profiling mode: launch only this 7B decode op (q,k,v,o,gate,up,down), "
                                              "a grouped launch (qkv, gate_up), prefill_up / prefill_down or the "
@@ -401,6 +402,10 @@ def main() -> int:
                      "algorithmic_bytes_per_launch": dom["bytes"]},
     }
 
+    # ---- the whole decoder layer on the device ------------------------------------------
+    if not args.no_layer:
+        result["decoder_layer"] = decoder_layer(args)
+
     # ---- prefill, M=2048 ----------------------------------------------------------------
     if not args.no_prefill:
         pre = {}
@@ -469,6 +474,132 @@ def main() -> int:
 
     print(json.dumps(result), flush=True)
     return 0
+
+
+class LayerRotation:
+    """R copies of one 7B decoder layer held on the device (the seven INT4 projections, two
+    RMSNorm weights, a KV cache of `capacity` rows per kv head already holding `past` rows,
+    rotary caches) and the activation buffers of a step at M = 1."""
+    HID, H, KH, D, INTER = 3584, 28, 4, 128, 18944
+
+    def __init__(self, copies, past, seed):
+        import torch
+        from modelsharp_amd import native, workloads
+        self.copies, self.past, self.capacity = copies, past, past + 1
+        ops = workloads.DECODE_7B
+        host = [workloads.make_weights(op, seed + i) for i, op in enumerate(ops)]
+        self.h = [[native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
+                   for (b, s, z), op in zip(host, ops)] for _ in range(copies)]
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        dev = lambda *shape: torch.randn(*shape, generator=g).cuda()   # noqa: E731
+        HID, KH, D = self.HID, self.KH, self.D
+        self.g1 = [torch.rand(HID, generator=g).cuda() + 0.5 for _ in range(copies)]
+        self.g2 = [torch.rand(HID, generator=g).cuda() + 0.5 for _ in range(copies)]
+        self.kc = [dev(1, KH, self.capacity, D) for _ in range(copies)]
+        self.vc = [dev(1, KH, self.capacity, D) for _ in range(copies)]
+        ang = torch.outer(torch.arange(self.capacity, dtype=torch.float64),
+                          1.0 / 10000 ** (torch.arange(D // 2, dtype=torch.float64) / (D // 2)))
+        self.cos, self.sin = torch.cos(ang).float().cuda(), torch.sin(ang).float().cuda()
+        self.x = [dev(1, HID) for _ in range(copies)]
+        self.resid = [dev(1, HID) for _ in range(copies)]
+        e = lambda n: torch.empty(1, n, device="cuda")   # noqa: E731
+        self.n1, self.q, self.k, self.v, self.attn, self.o = e(HID), e(HID), e(KH * D), e(KH * D), e(HID), e(HID)
+        self.n2, self.gt, self.up, self.act, self.y = e(HID), e(self.INTER), e(self.INTER), e(self.INTER), e(HID)
+        self.desc = native.GqaDesc(batch=1, q_seq=1, kv_seq=1, num_heads=self.H, kv_num_heads=KH, head_dim=D,
+                                   packed_qkv=0, past_seq=past, past_in_present=1, present_capacity=self.capacity,
+                                   do_rotary=1, rotary_interleaved=0, cos_rows=self.capacity, cos_cols=D // 2,
+                                   local_window_size=-1, scale=0.0, seqlens_len=0)
+        self.ws_bytes = native.gqa_workspace_size(self.desc)
+        self.ws = torch.empty(max(1, (self.ws_bytes + 3) // 4), device="cuda")
+
+    def stage(self, r, name, stream):
+        """One stage of copy r's step on `stream` (the residual stream updated in place)."""
+        from modelsharp_amd import native
+        h, HID, eps = self.h[r], self.HID, 1e-6
+        if name == "norm1":
+            native.skip_rmsnorm(self.x[r].data_ptr(), self.resid[r].data_ptr(), self.g1[r].data_ptr(), None, None,
+                                self.n1.data_ptr(), self.resid[r].data_ptr(), None, 1, HID, eps, stream)
+        elif name == "qkv":
+            native.gemm_dev_batch(h[0:3], [self.n1.data_ptr()] * 3,
+                                  [self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr()], 1, stream)
+        elif name == "attention":
+            native.gqa(self.desc, self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), None, None, None,
+                       self.cos.data_ptr(), self.sin.data_ptr(), self.attn.data_ptr(),
+                       self.kc[r].data_ptr(), self.vc[r].data_ptr(), self.ws.data_ptr(), self.ws_bytes, stream)
+        elif name == "o":
+            h[3].gemm_dev(self.attn.data_ptr(), self.o.data_ptr(), 1, stream)
+        elif name == "norm2":
+            native.skip_rmsnorm(self.o.data_ptr(), self.resid[r].data_ptr(), self.g2[r].data_ptr(), None, None,
+                                self.n2.data_ptr(), self.resid[r].data_ptr(), None, 1, HID, eps, stream)
+        elif name == "gate_up":
+            native.gemm_dev_batch(h[4:6], [self.n2.data_ptr()] * 2, [self.gt.data_ptr(), self.up.data_ptr()], 1,
+                                  stream)
+        elif name == "silu_mul":
+            native.silu_mul(self.gt.data_ptr(), self.up.data_ptr(), self.act.data_ptr(), self.INTER, stream)
+        elif name == "down":
+            h[6].gemm_dev(self.act.data_ptr(), self.x[r].data_ptr(), 1, stream)
+
+    STAGES = ("norm1", "qkv", "attention", "o", "norm2", "gate_up", "silu_mul", "down")
+
+    def close(self):
+        for row in self.h:
+            for w in row:
+                w.close()
+
+
+def decoder_layer(args):
+    """The 7B decoder layer at decode on the device: SkipSimplifiedLayerNormalization ->
+    q/k/v (one grouped launch) -> GroupQueryAttention (28 query / 4 kv heads of 128, rotary,
+    past 2047 rows appended in place) -> o -> SkipSimplifiedLayerNormalization -> gate/up
+    (one grouped launch) -> SiLU*Mul -> down, device pointers throughout; rotating copies of
+    the layer (weights and KV cache) over >= 1 GiB. Then GroupQueryAttention at prefill
+    (2048 query rows, past 0)."""
+    import torch
+    from modelsharp_amd import native, workloads
+    past = 2047
+    per_copy = sum(workloads.algorithmic_bytes(op, 1) for op in workloads.DECODE_7B) + 2 * 4 * (past + 1) * 128 * 4
+    copies = workloads.rotation_copies(per_copy, args.rotate_mib << 20)
+    lay = LayerRotation(copies, past, seed=21)
+    g = graph_of(lambda st: [lay.stage(r, n, st) for r in range(copies) for n in LayerRotation.STAGES])
+    ms = time_graph(g, max(4, math.ceil(200 / copies)), 2) / copies
+    del g
+    stages = {}
+    for n in LayerRotation.STAGES:
+        gs = graph_of(lambda st, n=n: [lay.stage(r, n, st) for r in range(copies)])
+        stages[n] = round(time_graph(gs, max(4, math.ceil(200 / copies)), 2) / copies * 1e3, 3)
+        del gs
+    finite = bool(torch.isfinite(lay.x[0]).all())
+    log(f"decoder layer step (past {past}): {ms * 1e3:.2f} us; stages {stages}; finite output {finite}")
+    out = {"workload": "7B decoder layer at decode, M=1, past 2047, device-resident (hidden 3584, 28/4 heads of "
+                       "128, intermediate 18944, bs 32 zp)", "rotating_copies": copies,
+           "us_per_step": round(ms * 1e3, 3), "stage_us": stages,
+           "bytes_per_step": per_copy, "GBs": round(per_copy / (ms * 1e-3) / 1e9, 1), "finite": finite}
+    lay.close()
+    del lay
+    torch.cuda.empty_cache()
+    # attention at prefill: 2048 query rows over themselves (causal), rotary, past 0
+    S, H, KH, D = 2048, LayerRotation.H, LayerRotation.KH, LayerRotation.D
+    gen = torch.Generator(device="cpu").manual_seed(5)
+    q = torch.randn(1, S, H * D, generator=gen).cuda()
+    k = torch.randn(1, S, KH * D, generator=gen).cuda()
+    v = torch.randn(1, S, KH * D, generator=gen).cuda()
+    ang = torch.outer(torch.arange(S, dtype=torch.float64), 1.0 / 10000 ** (torch.arange(D // 2, dtype=torch.float64) / (D // 2)))
+    cos, sin = torch.cos(ang).float().cuda(), torch.sin(ang).float().cuda()
+    pk, pv = torch.empty(1, KH, S, D, device="cuda"), torch.empty(1, KH, S, D, device="cuda")
+    o = torch.empty(1, S, H * D, device="cuda")
+    d = native.GqaDesc(batch=1, q_seq=S, kv_seq=S, num_heads=H, kv_num_heads=KH, head_dim=D, packed_qkv=0, past_seq=0,
+                       past_in_present=0, present_capacity=S, do_rotary=1, rotary_interleaved=0, cos_rows=S,
+                       cos_cols=D // 2, local_window_size=-1, scale=0.0, seqlens_len=0)
+    wsb = native.gqa_workspace_size(d)
+    ws = torch.empty(max(1, (wsb + 3) // 4), device="cuda")
+    gp = graph_of(lambda st: native.gqa(d, q.data_ptr(), k.data_ptr(), v.data_ptr(), None, None, None, cos.data_ptr(),
+                                        sin.data_ptr(), o.data_ptr(), pk.data_ptr(), pv.data_ptr(), ws.data_ptr(), wsb, st))
+    msp = time_graph(gp, 5, 1)
+    flops = 2 * 2 * H * D * S * (S + 1) / 2   # q.k and p.v over the causal half
+    out["attention_prefill"] = {"q_seq": S, "past": 0, "us": round(msp * 1e3, 1),
+                                "TFLOPs": round(flops / (msp * 1e-3) / 1e12, 2)}
+    log(f"attention prefill S={S}: {msp * 1e3:.1f} us")
+    return out
 
 
 def profile_op(args) -> int:

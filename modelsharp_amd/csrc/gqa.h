@@ -354,4 +354,212 @@ __global__ __launch_bounds__(256) void gqa_combine_kernel(GqaArgs p, const float
     }
 }
 
+// Decode and short queries, head_dim D in {64, 128}, up to 8 query heads per kv head:
+// one workgroup per (batch, kv head, query, key split) serves every query head of the
+// group, so each key and value row is read once per split instead of once per query head
+// (the 7B layer's 28 / 4 heads read the 2048-row history once, not 7 times). The split's
+// keys go through LDS in chunks of 32 rows with an online softmax (running max, sum and
+// weighted V rows per head); the partial (max, sum, row) per (unit, split) goes to the
+// workspace in gqa_combine_kernel's layout, or straight to the output with one split.
+constexpr int kGqaChunk = 32;
+constexpr int kGqaGroupMax = 8;
+
+template <int D>
+__global__ __launch_bounds__(kGqaThreads) void gqa_group_kernel(GqaArgs p, float* __restrict__ ws, int splits)
+{
+    constexpr int KP = D + 4;            // padded K row: float4 reads of 16 different rows hit distinct banks
+    constexpr int HPT = kGqaThreads / D; // heads per pass of the P.V loop
+    __shared__ __attribute__((aligned(16))) float qs[kGqaGroupMax * D];
+    __shared__ __attribute__((aligned(16))) float ks[kGqaChunk * KP];
+    __shared__ __attribute__((aligned(16))) float vs[kGqaChunk * D];
+    __shared__ float ps[kGqaGroupMax * kGqaChunk];
+    __shared__ float alpha[kGqaGroupMax];
+    const int grp = p.H / p.kvH;
+    const int sp = blockIdx.x % splits, ug = blockIdx.x / splits;
+    const int qi = ug % p.Sq, bg = ug / p.Sq;
+    const int g = bg % p.kvH, b = bg / p.kvH;
+    const int tid = threadIdx.x;
+
+    // the unit's key range (the same for every head of the group)
+    int bound = p.total - 1;
+    if (p.seqlens_len > 0) bound = min(bound, p.seqlens[min(b, p.seqlens_len - 1)]);
+    const int q_abs = p.past + qi;
+    const int k_limit = min(q_abs, bound);
+    const int k_start = p.window >= 0 ? max(0, q_abs - p.window + 1) : 0;
+    const int L = max(k_limit - k_start + 1, 0);
+    const int j0 = k_start + (int)(((int64_t)L * sp) / splits);
+    const int j1 = k_start + (int)(((int64_t)L * (sp + 1)) / splits);
+
+    const int pos = rotary_pos(q_abs, p);
+    float* const kb = p.pk + (int64_t)(b * p.kvH + g) * p.cap * D;
+    float* const vb = p.pv + (int64_t)(b * p.kvH + g) * p.cap * D;
+    // The new rows [past, past + Skv) of this kv head: the first workgroup of each (batch, kv
+    // head) writes them to the present cache (K rotated as gqa_append_kernel does); a chunk
+    // that holds one of them builds it from the input row itself, so no workgroup reads a
+    // cache row another one writes.
+    if (qi == 0 && sp == 0) {
+        for (int i = tid; i < p.Skv * D; i += kGqaThreads) {
+            const int sr = i / D, d = i - sr * D;
+            const float* krow = p.k + (int64_t)(b * p.Skv + sr) * p.kv_stride + g * D;
+            const float* vrow = p.v + (int64_t)(b * p.Skv + sr) * p.kv_stride + g * D;
+            kb[(int64_t)(p.past + sr) * D + d] = rotated(krow, d, rotary_pos(p.past + sr, p), p);
+            vb[(int64_t)(p.past + sr) * D + d] = vrow[d];
+        }
+    }
+
+    // score phase: thread (h = tid / 32, j = tid % 32); P.V phase: thread (d = tid % D, heads
+    // tid / D, tid / D + HPT, ...)
+    const int sh = tid >> 5, sj = tid & 31;
+    float m_run = -__builtin_inff(), l_run = 0.0f;   // per head, held by the 32 lanes of head sh
+    const int dd = tid % D, h0 = tid / D;
+    float acc[kGqaGroupMax / HPT];
+#pragma unroll
+    for (int i = 0; i < kGqaGroupMax / HPT; ++i) acc[i] = 0.0f;
+
+    constexpr int PER = kGqaChunk * (D / 4) / kGqaThreads;   // float4s of K (and of V) per thread
+    static_assert(PER * kGqaThreads == kGqaChunk * (D / 4), "chunk shape");
+    for (int c0 = j0; c0 < j1; c0 += kGqaChunk) {
+        const int n = min(kGqaChunk, j1 - c0);
+        // this chunk's K and V rows into registers first (every load in flight together) ...
+        float4 k4[PER], v4[PER];
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int i = tid + u * kGqaThreads;
+            const int r = i / (D / 4), c4 = i - r * (D / 4);
+            const int key = c0 + r;
+            k4[u] = v4[u] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (r < n && key < p.past) {
+                k4[u] = *reinterpret_cast<const float4*>(kb + (int64_t)key * D + 4 * c4);
+                v4[u] = *reinterpret_cast<const float4*>(vb + (int64_t)key * D + 4 * c4);
+            } else if (r < n) {   // a new row: from the input
+                const int sr = key - p.past;
+                const float* krow = p.k + (int64_t)(b * p.Skv + sr) * p.kv_stride + g * D;
+                const float* vrow = p.v + (int64_t)(b * p.Skv + sr) * p.kv_stride + g * D;
+                const int kp = rotary_pos(key, p);
+                k4[u] = float4{rotated(krow, 4 * c4, kp, p), rotated(krow, 4 * c4 + 1, kp, p),
+                               rotated(krow, 4 * c4 + 2, kp, p), rotated(krow, 4 * c4 + 3, kp, p)};
+                v4[u] = float4{vrow[4 * c4], vrow[4 * c4 + 1], vrow[4 * c4 + 2], vrow[4 * c4 + 3]};
+            }
+        }
+        // ... then, on the first chunk, the group's rotated query rows, while they land
+        if (c0 == j0) {
+            for (int i = tid; i < grp * D; i += kGqaThreads) {
+                const int r = i / D, d = i - r * D;
+                const float* qrow = p.q + (int64_t)(b * p.Sq + qi) * p.q_stride + (g * grp + r) * D;
+                qs[i] = rotated(qrow, d, pos, p);
+            }
+        }
+        __syncthreads();   // the previous chunk's readers are done with ks / vs / ps
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int i = tid + u * kGqaThreads;
+            const int r = i / (D / 4), c4 = i - r * (D / 4);
+            *reinterpret_cast<float4*>(ks + r * KP + 4 * c4) = k4[u];
+            *reinterpret_cast<float4*>(vs + r * D + 4 * c4) = v4[u];
+        }
+        __syncthreads();
+        if (sh < grp) {
+            float sc = -__builtin_inff();
+            if (sj < n) {
+                const float* qh = qs + sh * D;
+                const float* kr = ks + sj * KP;
+                // four partial sums (channels d % 4), added in order at the end
+                float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
+#pragma unroll 8
+                for (int d = 0; d < D; d += 4) {
+                    const float4 q4 = *reinterpret_cast<const float4*>(qh + d);
+                    const float4 kk = *reinterpret_cast<const float4*>(kr + d);
+                    d0 = __builtin_fmaf(q4.x, kk.x, d0);
+                    d1 = __builtin_fmaf(q4.y, kk.y, d1);
+                    d2 = __builtin_fmaf(q4.z, kk.z, d2);
+                    d3 = __builtin_fmaf(q4.w, kk.w, d3);
+                }
+                sc = ((d0 + d1) + (d2 + d3)) * p.scale;
+            }
+            float cm = sc;
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) cm = fmaxf(cm, __shfl_xor(cm, o, 32));
+            const float m_new = fmaxf(m_run, cm);   // finite: the chunk holds at least one key
+            const float a = expf(m_run - m_new);    // 0 on the first chunk
+            const float e = sj < n ? expf(sc - m_new) : 0.0f;
+            float cs = e;
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) cs += __shfl_xor(cs, o, 32);
+            l_run = l_run * a + cs;
+            m_run = m_new;
+            ps[sh * kGqaChunk + sj] = e;
+            if (sj == 0) alpha[sh] = a;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kGqaGroupMax / HPT; ++i) {
+            const int h = h0 + i * HPT;
+            if (h < grp) {
+                float o = acc[i] * alpha[h];
+                const float* ph = ps + h * kGqaChunk;
+                for (int j = 0; j < n; ++j) o = __builtin_fmaf(ph[j], vs[j * D + dd], o);
+                acc[i] = o;
+            }
+        }
+    }
+    // the per-head (max, sum) live in the score lanes: hand them to the P.V threads via LDS
+    __syncthreads();
+    if (sh < grp && sj == 0) {
+        ps[sh * kGqaChunk] = m_run;
+        ps[sh * kGqaChunk + 1] = l_run;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kGqaGroupMax / HPT; ++i) {
+        const int h = h0 + i * HPT;
+        if (h < grp) {
+            const int hh = g * grp + h;
+            const int64_t unit = ((int64_t)b * p.H + hh) * p.Sq + qi;
+            const float mh = ps[h * kGqaChunk], lh = ps[h * kGqaChunk + 1];
+            if (splits == 1) {
+                p.out[(int64_t)(b * p.Sq + qi) * p.H * D + hh * D + dd] = lh > 0.0f ? acc[i] * (1.0f / lh) : 0.0f;
+            } else {
+                float* w = ws + (unit * splits + sp) * (D + 2);
+                w[dd] = acc[i];
+                if (dd == 0) {
+                    w[D] = mh;
+                    w[D + 1] = lh;
+                }
+            }
+        }
+    }
+}
+
+// The splits of gqa_group_kernel meet here: one wave per (unit, 64 channels). Lane s reads
+// split s's maximum and sum; the maximum, the rescale factors and the normaliser come from
+// wave reductions; then each lane adds its channel over the splits with every split's
+// load issued together (fixed order, so deterministic).
+__global__ __launch_bounds__(64) void gqa_merge_kernel(GqaArgs p, const float* __restrict__ ws, int splits)
+{
+    const int D = p.D, slices = (D + 63) / 64;
+    const int unit = blockIdx.x / slices, d = (blockIdx.x % slices) * 64 + threadIdx.x;
+    const int lane = threadIdx.x;
+    const GqaUnit u = gqa_unit(p, unit);
+    const float* w = ws + (int64_t)unit * splits * (D + 2);
+    const float ml = lane < splits ? w[lane * (D + 2) + D] : -__builtin_inff();
+    const float ll = lane < splits ? w[lane * (D + 2) + D + 1] : 0.0f;
+    float M = ll > 0.0f ? ml : -__builtin_inff();
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+    const float f = ll > 0.0f ? expf(ml - M) : 0.0f;
+    float lsum = ll * f;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o);
+    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+    if (d >= D) return;
+    float vals[kGqaMaxSplits];
+#pragma unroll
+    for (int s = 0; s < kGqaMaxSplits; ++s) vals[s] = s < splits ? w[s * (D + 2) + d] : 0.0f;
+    float o = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kGqaMaxSplits; ++s)
+        if (s < splits) o = __builtin_fmaf(vals[s], __shfl(f, s), o);
+    p.out[(int64_t)(u.b * p.Sq + u.qi) * p.H * D + u.h * D + d] = o * inv;
+}
+
 }  // namespace msnb

@@ -2562,6 +2562,7 @@ namespace {
 // per-unit kernel; and the LDS each needs.
 struct GqaPlan {
     int G = 0;          // lanes per row of gqa_rows_kernel<G>, 0: gqa_attention_kernel
+    bool grouped = false;   // gqa_group_kernel<D> (every query head of a kv group per workgroup)
     int splits = 1;
     size_t lds = 0;
     int64_t ws_bytes = 0;
@@ -2575,6 +2576,25 @@ GqaPlan gqa_plan(const ms_hip_gqa_desc& d, int64_t ws_avail)
     const int D = d.head_dim;
     const int64_t total = (int64_t)d.past_seq + d.kv_seq;
     const int64_t units = (int64_t)d.batch * d.num_heads * d.q_seq;
+    const int grp = d.kv_num_heads > 0 ? d.num_heads / d.kv_num_heads : 0;
+    if ((D == 64 || D == 128) && grp >= 1 && grp <= kGqaGroupMax && d.q_seq >= 1 && d.q_seq <= 8) {
+        // Decode and short queries: one workgroup per (batch, kv head, query, key split),
+        // enough splits for about 512 workgroups (at most 64, at least 16 keys each). The
+        // keys stream through LDS, so any history length fits; without a workspace for the
+        // splits' partials, one split per group.
+        pl.grouped = true;
+        const int64_t groups = (int64_t)d.batch * d.kv_num_heads * d.q_seq;
+        int splits = (int)std::min<int64_t>({(int64_t)kGqaMaxSplits, std::max<int64_t>(1, (512 + groups - 1) / groups),
+                                             std::max<int64_t>(1, (total + 15) / 16)});
+        int64_t ws = splits > 1 ? units * splits * (D + 2) * (int64_t)sizeof(float) : 0;
+        if (ws_avail >= 0 && ws > ws_avail) {
+            splits = 1;
+            ws = 0;
+        }
+        pl.splits = splits;
+        pl.ws_bytes = ws;
+        return pl;
+    }
     if (D == 32 || D == 64 || D == 128 || D == 256) {
         pl.G = D / 4;
         const int64_t fixed = D + (int64_t)(kGqaThreads / pl.G) * D + 1;
@@ -2700,13 +2720,29 @@ int ms_hip_gqa(const ms_hip_gqa_desc* d, const float* dQ, const float* dK, const
         hipLaunchKernelGGL(gqa_copy_past_kernel, dim3(elementwise_grid(n)), dim3(256), 0, s, p);
         MS_HIP_CHECK(hipGetLastError());
     }
-    if (p.Skv > 0) {
+    const GqaPlan plan = p.Sq > 0 ? gqa_plan(*d, dWorkspace && !misaligned4(dWorkspace) ? workspace_bytes : 0) : GqaPlan{};
+    if (p.Skv > 0 && !plan.grouped) {   // the grouped kernel writes the new rows itself
         const int threads = std::min(256, ((p.D + 63) / 64) * 64);
         hipLaunchKernelGGL(gqa_append_kernel, dim3((unsigned)(p.B * p.Skv * p.kvH)), dim3(threads), 0, s, p);
         MS_HIP_CHECK(hipGetLastError());
     }
     if (p.Sq > 0) {
-        const GqaPlan pl = gqa_plan(*d, dWorkspace && !misaligned4(dWorkspace) ? workspace_bytes : 0);
+        const GqaPlan& pl = plan;
+        if (pl.grouped) {
+            const unsigned grid = (unsigned)(p.B * p.kvH * p.Sq * pl.splits);
+            float* ws = static_cast<float*>(dWorkspace);
+            if (p.D == 128)
+                hipLaunchKernelGGL(gqa_group_kernel<128>, dim3(grid), dim3(kGqaThreads), 0, s, p, ws, pl.splits);
+            else
+                hipLaunchKernelGGL(gqa_group_kernel<64>, dim3(grid), dim3(kGqaThreads), 0, s, p, ws, pl.splits);
+            MS_HIP_CHECK(hipGetLastError());
+            if (pl.splits > 1) {
+                hipLaunchKernelGGL(gqa_merge_kernel, dim3((unsigned)(p.B * p.H * p.Sq * ((p.D + 63) / 64))), dim3(64), 0,
+                                   s, p, ws, pl.splits);
+                MS_HIP_CHECK(hipGetLastError());
+            }
+            return MS_HIP_OK;
+        }
         if (pl.lds > kGqaMaxLds)
             return fail(MS_HIP_ERR_UNSUPPORTED, "[ms_hip] GroupQueryAttention: history too long for one workgroup's "
                                                 "scores without a workspace (ms_hip_gqa_workspace_size)");

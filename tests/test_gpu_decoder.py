@@ -139,6 +139,30 @@ def test_gqa_cases(gpu, case):
               ref, rk, rv, f"seed {case['seed']}")
 
 
+# The grouped kernel (head_dim 64 / 128, up to 8 query heads per kv head, up to 8 queries):
+# every option of the operator at those head dims, with and without key splits.
+GROUPED_CASES = [
+    dict(seed=101, B=1, Sq=1, H=28, KH=4, D=128, past=2047, cos_rows=2048),          # the 7B decode step
+    dict(seed=102, B=2, Sq=5, H=8, KH=1, D=64, past=3),                              # MQA, 8 heads per kv head
+    dict(seed=103, B=1, Sq=4, H=6, KH=3, D=128, past=0, packed=True),                # packed QKV, no past
+    dict(seed=104, B=1, Sq=3, H=4, KH=2, D=64, past=600, interleaved=True, cos_rows=700),
+    dict(seed=105, B=2, Sq=8, H=4, KH=2, D=128, past=45, window=7),                  # sliding window
+    dict(seed=106, B=2, Sq=2, H=4, KH=2, D=64, past=70, seqlens=[40, 71], cos_rows=80),   # seqlens_k bound
+    dict(seed=107, B=1, Sq=3, H=6, KH=2, D=128, past=33, cos_cols=24),               # partial rotary span
+    dict(seed=108, B=1, Sq=2, H=2, KH=2, D=64, past=90, cos_rows=64),                # positions past the cache
+    dict(seed=109, B=1, Sq=1, H=14, KH=2, D=128, past=5000, rotary=False, cos_rows=8),
+]
+
+
+@pytest.mark.parametrize("workspace", [False, True], ids=["one_split", "key_splits"])
+@pytest.mark.parametrize("case", GROUPED_CASES, ids=lambda c: f"seed{c['seed']}")
+def test_gqa_grouped_cases(gpu, case, workspace):
+    d, q, k, v, pk, pv, sl, cos, sin = make_case(**case)
+    ref, rk, rv = oracle.gqa(d, q, k, v, pk, pv, sl, cos, sin)
+    check_gqa(*run_device_gqa(d, q, k, v, pk, pv, sl, cos, sin, capacity=d.past_seq + d.kv_seq + 3,
+                              workspace=workspace), ref, rk, rv, f"grouped seed {case['seed']} workspace={workspace}")
+
+
 @pytest.mark.parametrize("workspace", [False, True], ids=["one_split", "key_splits"])
 @pytest.mark.parametrize("Sq,past,KH", [(1, 2047, 8), (1, 4095, 32), (128, 0, 8), (16, 300, 8)])
 def test_gqa_7b_shapes(gpu, Sq, past, KH, workspace):
