@@ -562,4 +562,156 @@ __global__ __launch_bounds__(64) void gqa_merge_kernel(GqaArgs p, const float* _
     p.out[(int64_t)(u.b * p.Sq + u.qi) * p.H * D + u.h * D + d] = o * inv;
 }
 
+// Prefill (more than 8 queries), head_dim D in {64, 128}: flash attention on the fp32 matrix
+// cores. A workgroup of 4 waves takes 64 consecutive queries of one (batch, head); wave w
+// owns 16 of them. Keys go through LDS in chunks of 64 rows of K and V. Per chunk:
+//   S^T = K Q^T with v_mfma_f32_16x16x4f32 (keys are the M dimension, queries N, head
+//   channels K): lane l holds the scores of keys 4(l/16) + i, i < 4, of each 16-key tile for
+//   query l % 16 — exactly the A-operand layout that P V needs (queries M, keys K), so the
+//   probabilities never leave their registers. Channel j = 4t + i of a k step reads channel
+//   16t + 4(l/16) + i, so each lane's K and Q operands of four steps are one 16-byte read.
+//   Online softmax per query (max and sum over the 16-lane groups by shuffles), then
+//   O += P V, O rows rescaled by exp(m_old - m_new) fetched from the lane that owns the
+//   query's statistics.
+// fp32 products and sums throughout: the same 1e-5-of-max|out| bar as the VALU kernels.
+constexpr int kFlashQ = 64, kFlashK = 64;
+
+template <int D>
+__global__ __launch_bounds__(256) void gqa_flash_kernel(GqaArgs p)
+{
+    typedef float floatx4_t __attribute__((ext_vector_type(4)));
+    constexpr int KP = D + 4;   // padded rows: the 16-byte reads of 16 rows and the dword reads of V hit distinct banks
+    constexpr int T = D / 16;   // k steps of four per 16-channel group
+    extern __shared__ __attribute__((aligned(16))) float flash_lds[];
+    float* const ks = flash_lds;
+    float* const vs = flash_lds + kFlashK * KP;
+    const int nqb = (p.Sq + kFlashQ - 1) / kFlashQ;
+    // heaviest blocks (latest queries) first
+    const int qb = nqb - 1 - (int)(blockIdx.x % nqb), hb = (int)(blockIdx.x / nqb);
+    const int h = hb % p.H, b = hb / p.H, g = h / (p.H / p.kvH);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r16 = lane & 15, c = lane >> 4;
+    const int q0 = qb * kFlashQ;
+
+    int bound = p.total - 1;
+    if (p.seqlens_len > 0) bound = min(bound, p.seqlens[min(b, p.seqlens_len - 1)]);
+    auto k_first = [&](int qi) { return p.window >= 0 ? max(0, p.past + qi - p.window + 1) : 0; };
+    auto k_last = [&](int qi) { return min(p.past + qi, bound); };
+
+    // this lane's query (S columns) and its rotated channels 16t + 4c + i
+    const int qs_i = q0 + wave * 16 + r16;
+    const bool q_in = qs_i < p.Sq;
+    floatx4_t qreg[T];
+    {
+        const float* qrow = p.q + (int64_t)(b * p.Sq + min(qs_i, p.Sq - 1)) * p.q_stride + h * D;
+        const int pos = rotary_pos(p.past + qs_i, p);
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) qreg[t][i] = q_in ? rotated(qrow, 16 * t + 4 * c + i, pos, p) : 0.0f;
+    }
+    const int kf_q = k_first(qs_i), kl_q = q_in ? k_last(qs_i) : -1;
+    // the workgroup's key range
+    const int qlast = min(q0 + kFlashQ, p.Sq) - 1;
+    const int kmin = k_first(q0), kmax = k_last(qlast);
+    const float* kb = p.pk + (int64_t)(b * p.kvH + g) * p.cap * D;
+    const float* vb = p.pv + (int64_t)(b * p.kvH + g) * p.cap * D;
+
+    float m_run = -__builtin_inff(), l_run = 0.0f;   // statistics of query r16 (in the 4 lanes of each c)
+    floatx4_t acc_o[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc_o[t] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int c0 = (kmin / kFlashK) * kFlashK; c0 <= kmax; c0 += kFlashK) {
+        __syncthreads();   // the previous chunk's readers are done
+        for (int i4 = tid; i4 < kFlashK * (D / 4); i4 += 256) {
+            const int r = i4 / (D / 4), c4 = i4 - r * (D / 4);
+            const int key = c0 + r;
+            float4 k4 = {0.0f, 0.0f, 0.0f, 0.0f}, v4 = k4;
+            if (key < p.total) {
+                k4 = *reinterpret_cast<const float4*>(kb + (int64_t)key * D + 4 * c4);
+                v4 = *reinterpret_cast<const float4*>(vb + (int64_t)key * D + 4 * c4);
+            }
+            *reinterpret_cast<float4*>(ks + r * KP + 4 * c4) = k4;
+            *reinterpret_cast<float4*>(vs + r * KP + 4 * c4) = v4;
+        }
+        __syncthreads();
+        // S^T tiles: 4 x (16 keys x 16 queries)
+        floatx4_t st[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+            floatx4_t a = {0.0f, 0.0f, 0.0f, 0.0f};
+            const float* krow = ks + (kt * 16 + r16) * KP + 4 * c;
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const float4 kv = *reinterpret_cast<const float4*>(krow + 16 * t);
+                a = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, qreg[t][0], a, 0, 0, 0);
+                a = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, qreg[t][1], a, 0, 0, 0);
+                a = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, qreg[t][2], a, 0, 0, 0);
+                a = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, qreg[t][3], a, 0, 0, 0);
+            }
+            st[kt] = a;
+        }
+        // scale, mask, chunk maximum of query r16
+        float cm = -__builtin_inff();
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = c0 + kt * 16 + 4 * c + i;
+                const bool ok = key >= kf_q && key <= kl_q;
+                const float sc = ok ? st[kt][i] * p.scale : -__builtin_inff();
+                st[kt][i] = sc;
+                cm = fmaxf(cm, sc);
+            }
+        cm = fmaxf(cm, __shfl_xor(cm, 16));
+        cm = fmaxf(cm, __shfl_xor(cm, 32));
+        const float m_new = fmaxf(m_run, cm);
+        const bool none = m_new == -__builtin_inff();   // no key of this query so far
+        const float alpha = none ? 1.0f : expf(m_run - m_new);
+        float ls = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float e = none ? 0.0f : expf(st[kt][i] - m_new);
+                st[kt][i] = e;
+                ls = ls + e;
+            }
+        ls = ls + __shfl_xor(ls, 16);
+        ls = ls + __shfl_xor(ls, 32);
+        l_run = l_run * alpha + ls;
+        m_run = m_new;
+        // rescale O rows (queries 4c + i of the wave) by their alpha
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float ai = __shfl(alpha, 4 * c + i);
+#pragma unroll
+            for (int t = 0; t < T; ++t) acc_o[t][i] = acc_o[t][i] * ai;
+        }
+        // O += P V: A = P (queries x keys, from st), B = V (keys x channels)
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float* vrow = vs + (kt * 16 + 4 * c + i) * KP + r16;
+#pragma unroll
+                for (int t = 0; t < T; ++t)
+                    acc_o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(st[kt][i], vrow[16 * t], acc_o[t], 0, 0, 0);
+            }
+    }
+    // out rows: queries 4c + i of the wave, channels 16t + r16
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float li = __shfl(l_run, 4 * c + i);
+        const int qo = q0 + wave * 16 + 4 * c + i;
+        if (qo < p.Sq) {
+            float* orow = p.out + (int64_t)(b * p.Sq + qo) * p.H * D + h * D;
+            const float inv = li > 0.0f ? 1.0f / li : 0.0f;
+#pragma unroll
+            for (int t = 0; t < T; ++t) orow[16 * t + r16] = acc_o[t][i] * inv;
+        }
+    }
+}
+
 }  // namespace msnb

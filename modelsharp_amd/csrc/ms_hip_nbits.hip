@@ -2563,6 +2563,7 @@ namespace {
 struct GqaPlan {
     int G = 0;          // lanes per row of gqa_rows_kernel<G>, 0: gqa_attention_kernel
     bool grouped = false;   // gqa_group_kernel<D> (every query head of a kv group per workgroup)
+    bool flash = false;     // gqa_flash_kernel<D> (prefill on the fp32 matrix cores)
     int splits = 1;
     size_t lds = 0;
     int64_t ws_bytes = 0;
@@ -2593,6 +2594,12 @@ GqaPlan gqa_plan(const ms_hip_gqa_desc& d, int64_t ws_avail)
         }
         pl.splits = splits;
         pl.ws_bytes = ws;
+        return pl;
+    }
+    if ((D == 64 || D == 128) && d.q_seq > 8) {
+        // Prefill: flash attention, K and V streaming through LDS (any history length).
+        pl.flash = true;
+        pl.lds = (size_t)2 * kFlashK * (D + 4) * sizeof(float);
         return pl;
     }
     if (D == 32 || D == 64 || D == 128 || D == 256) {
@@ -2728,6 +2735,19 @@ int ms_hip_gqa(const ms_hip_gqa_desc* d, const float* dQ, const float* dK, const
     }
     if (p.Sq > 0) {
         const GqaPlan& pl = plan;
+        if (pl.flash) {
+            const void* fn = p.D == 128 ? reinterpret_cast<const void*>(gqa_flash_kernel<128>)
+                                        : reinterpret_cast<const void*>(gqa_flash_kernel<64>);
+            if (pl.lds > 64 * 1024)
+                MS_HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pl.lds));
+            const unsigned grid = (unsigned)(p.B * p.H * ((p.Sq + kFlashQ - 1) / kFlashQ));
+            if (p.D == 128)
+                hipLaunchKernelGGL(gqa_flash_kernel<128>, dim3(grid), dim3(256), pl.lds, s, p);
+            else
+                hipLaunchKernelGGL(gqa_flash_kernel<64>, dim3(grid), dim3(256), pl.lds, s, p);
+            MS_HIP_CHECK(hipGetLastError());
+            return MS_HIP_OK;
+        }
         if (pl.grouped) {
             const unsigned grid = (unsigned)(p.B * p.kvH * p.Sq * pl.splits);
             float* ws = static_cast<float*>(dWorkspace);

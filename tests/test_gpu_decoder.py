@@ -163,6 +163,28 @@ def test_gqa_grouped_cases(gpu, case, workspace):
                               workspace=workspace), ref, rk, rv, f"grouped seed {case['seed']} workspace={workspace}")
 
 
+# The flash kernel (head_dim 64 / 128, more than 8 queries): every option of the operator.
+FLASH_CASES = [
+    dict(seed=201, B=1, Sq=200, H=28, KH=4, D=128, past=0, cos_rows=256),            # 7B heads, ragged block
+    dict(seed=202, B=2, Sq=70, H=8, KH=1, D=64, past=5, cos_rows=128),               # MQA, past
+    dict(seed=203, B=1, Sq=33, H=6, KH=3, D=128, past=100, packed=True, cos_rows=160),
+    dict(seed=204, B=1, Sq=64, H=4, KH=2, D=64, past=0, interleaved=True, cos_rows=64),
+    dict(seed=205, B=2, Sq=90, H=4, KH=2, D=128, past=30, window=17, cos_rows=128),  # sliding window
+    dict(seed=206, B=2, Sq=40, H=4, KH=2, D=64, past=10, seqlens=[20, 49], cos_rows=64),   # seqlens_k bound
+    dict(seed=207, B=1, Sq=65, H=6, KH=2, D=128, past=0, cos_cols=24, cos_rows=80),  # partial rotary span
+    dict(seed=208, B=1, Sq=20, H=2, KH=2, D=64, past=90, cos_rows=64),               # positions past the cache
+    dict(seed=209, B=1, Sq=129, H=14, KH=2, D=128, past=700, rotary=False, cos_rows=8),
+]
+
+
+@pytest.mark.parametrize("case", FLASH_CASES, ids=lambda c: f"seed{c['seed']}")
+def test_gqa_flash_cases(gpu, case):
+    d, q, k, v, pk, pv, sl, cos, sin = make_case(**case)
+    ref, rk, rv = oracle.gqa(d, q, k, v, pk, pv, sl, cos, sin)
+    check_gqa(*run_device_gqa(d, q, k, v, pk, pv, sl, cos, sin, capacity=d.past_seq + d.kv_seq + 5), ref, rk, rv,
+              f"flash seed {case['seed']}")
+
+
 @pytest.mark.parametrize("workspace", [False, True], ids=["one_split", "key_splits"])
 @pytest.mark.parametrize("Sq,past,KH", [(1, 2047, 8), (1, 4095, 32), (128, 0, 8), (16, 300, 8)])
 def test_gqa_7b_shapes(gpu, Sq, past, KH, workspace):
