@@ -577,7 +577,7 @@ __global__ __launch_bounds__(64) void gqa_merge_kernel(GqaArgs p, const float* _
 constexpr int kFlashQ = 64, kFlashK = 64;
 
 template <int D>
-__global__ __launch_bounds__(256) void gqa_flash_kernel(GqaArgs p)
+__global__ __launch_bounds__(256, 2) void gqa_flash_kernel(GqaArgs p)
 {
     typedef float floatx4_t __attribute__((ext_vector_type(4)));
     constexpr int KP = D + 4;   // padded rows: the 16-byte reads of 16 rows and the dword reads of V hit distinct banks
@@ -622,44 +622,64 @@ __global__ __launch_bounds__(256) void gqa_flash_kernel(GqaArgs p)
 #pragma unroll
     for (int t = 0; t < T; ++t) acc_o[t] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    for (int c0 = (kmin / kFlashK) * kFlashK; c0 <= kmax; c0 += kFlashK) {
-        __syncthreads();   // the previous chunk's readers are done
-        for (int i4 = tid; i4 < kFlashK * (D / 4); i4 += 256) {
+    // A chunk's K and V rows pass through registers: the next chunk's loads are in flight
+    // while this chunk computes.
+    constexpr int PER = kFlashK * (D / 4) / 256;
+    float4 kr[PER], vr[PER];
+    auto load_chunk = [&](int c0) {
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int i4 = tid + 256 * u;
             const int r = i4 / (D / 4), c4 = i4 - r * (D / 4);
             const int key = c0 + r;
-            float4 k4 = {0.0f, 0.0f, 0.0f, 0.0f}, v4 = k4;
+            kr[u] = vr[u] = float4{0.0f, 0.0f, 0.0f, 0.0f};
             if (key < p.total) {
-                k4 = *reinterpret_cast<const float4*>(kb + (int64_t)key * D + 4 * c4);
-                v4 = *reinterpret_cast<const float4*>(vb + (int64_t)key * D + 4 * c4);
+                kr[u] = *reinterpret_cast<const float4*>(kb + (int64_t)key * D + 4 * c4);
+                vr[u] = *reinterpret_cast<const float4*>(vb + (int64_t)key * D + 4 * c4);
             }
-            *reinterpret_cast<float4*>(ks + r * KP + 4 * c4) = k4;
-            *reinterpret_cast<float4*>(vs + r * KP + 4 * c4) = v4;
+        }
+    };
+    const int cfirst = (kmin / kFlashK) * kFlashK;
+    if (cfirst <= kmax) load_chunk(cfirst);
+    for (int c0 = cfirst; c0 <= kmax; c0 += kFlashK) {
+        __syncthreads();   // the previous chunk's readers are done
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int i4 = tid + 256 * u;
+            const int r = i4 / (D / 4), c4 = i4 - r * (D / 4);
+            *reinterpret_cast<float4*>(ks + r * KP + 4 * c4) = kr[u];
+            *reinterpret_cast<float4*>(vs + r * KP + 4 * c4) = vr[u];
         }
         __syncthreads();
-        // S^T tiles: 4 x (16 keys x 16 queries)
+        if (c0 + kFlashK <= kmax) load_chunk(c0 + kFlashK);
+        // S^T tiles: 4 x (16 keys x 16 queries), the four tiles' chains interleaved
         floatx4_t st[4];
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-            floatx4_t a = {0.0f, 0.0f, 0.0f, 0.0f};
-            const float* krow = ks + (kt * 16 + r16) * KP + 4 * c;
+        for (int kt = 0; kt < 4; ++kt) st[kt] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int t = 0; t < T; ++t) {
-                const float4 kv = *reinterpret_cast<const float4*>(krow + 16 * t);
-                a = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, qreg[t][0], a, 0, 0, 0);
-                a = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, qreg[t][1], a, 0, 0, 0);
-                a = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, qreg[t][2], a, 0, 0, 0);
-                a = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, qreg[t][3], a, 0, 0, 0);
-            }
-            st[kt] = a;
+        for (int t = 0; t < T; ++t) {
+            float4 kv[4];
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+                kv[kt] = *reinterpret_cast<const float4*>(ks + (kt * 16 + r16) * KP + 4 * c + 16 * t);
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[kt].x, qreg[t][0], st[kt], 0, 0, 0);
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[kt].y, qreg[t][1], st[kt], 0, 0, 0);
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[kt].z, qreg[t][2], st[kt], 0, 0, 0);
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[kt].w, qreg[t][3], st[kt], 0, 0, 0);
         }
-        // scale, mask, chunk maximum of query r16
+        // scale, mask (only chunks that cross a query's key range), chunk maximum of query r16
+        const bool full = __all(c0 >= kf_q && c0 + kFlashK - 1 <= kl_q);
         float cm = -__builtin_inff();
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int key = c0 + kt * 16 + 4 * c + i;
-                const bool ok = key >= kf_q && key <= kl_q;
+                const bool ok = full || (key >= kf_q && key <= kl_q);
                 const float sc = ok ? st[kt][i] * p.scale : -__builtin_inff();
                 st[kt][i] = sc;
                 cm = fmaxf(cm, sc);
