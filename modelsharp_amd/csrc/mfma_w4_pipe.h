@@ -81,11 +81,20 @@ constexpr int kPipeErrTimeout = 1;   // the first half's flag did not come withi
 constexpr int kPipeErrOverlap = 2;   // another launch holds the tile's counters
 
 constexpr int kPipeBM = 256, kPipeBN = 256;
-// A stages, weight groups, fp16 weight tiles, then the tile's row exponents (1 KB): the
-// whole 160 KB of a CU (the kernel declares no static LDS).
-constexpr int kPipeLdsBytes =
-    4 * kPipeBM * 64 + 3 * (kPipeBN * 64 + kPipeBN * 16 + kPipeBN * 4) + 2 * kPipeBN * 64 + kPipeBM * 4;
-static_assert(kPipeLdsBytes <= 160 * 1024, "the pipelined prefill's LDS exceeds a CU's");
+// LDS of a launch: NA stages of A (one step each), NG weight groups (codes, scales, zero
+// points of 4 steps), two fp16 weight tiles, then the tile's row exponents (1 KB); the
+// kernel declares no static LDS. 4-bit codes: 4 stages and 3 groups, all 160 KB of a CU;
+// 8-bit codes (128 bytes per row and group): 3 stages and 2 groups (155 KB).
+template <bool B8>
+struct PipeLds {
+    static constexpr int NA = B8 ? 3 : 4, NG = B8 ? 2 : 3;
+    static constexpr int CROW = B8 ? 128 : 64;   // code bytes per row and group
+    static constexpr int A_ST = kPipeBM * 64, CG = kPipeBN * CROW, SG = kPipeBN * 16, ZG = kPipeBN * 4;
+    static constexpr int OFF_A = 0, OFF_C = NA * A_ST, OFF_S = OFF_C + NG * CG, OFF_Z = OFF_S + NG * SG,
+                         OFF_B = OFF_Z + NG * ZG, OFF_E = OFF_B + 2 * kPipeBN * 64;
+    static constexpr int BYTES = OFF_E + kPipeBM * 4;
+    static_assert(BYTES <= 160 * 1024, "the pipelined prefill's LDS exceeds a CU's");
+};
 // Base offset of a row beyond the matrix: above every buffer the kernel reads
 // (the host checks each is smaller), so loads from it return zero.
 constexpr int kPipeFar = 0x40000000;
@@ -199,6 +208,20 @@ __device__ __forceinline__ void dequant8_f16(uint32_t x, h2_t zb, h2_t s2, uint3
     o[1] = as_u32((as_h2(and_or(x >> 4, 0x000F000Fu, m)) - zb) * s2);
     o[2] = as_u32((as_h2(and_or(x >> 8, 0x000F000Fu, m)) - zb) * s2);
     o[3] = as_u32((as_h2(and_or(x >> 12, 0x000F000Fu, m)) - zb) * s2);
+}
+
+// Eight 8-bit codes (d0 = codes 0..3, d1 = codes 4..7, one byte each) as four fp16 pairs
+// (k_t, k_{t+4}), t = 0..3, the order of dequant8_f16's pairs (and of the permuted A):
+// v_perm gathers byte t of d0 and byte t of d1 into halves 0 and 1, v_and_or puts them
+// under the exponent of 1024.0 (1024 + q exactly), then (1024 + q) - (1024 + zp) = q - zp
+// exactly (|q - zp| <= 255) and one rounding to fp16 of (q - zp) * fl16(s).
+__device__ __forceinline__ void dequant8_f16_b8(uint32_t d0, uint32_t d1, h2_t zb, h2_t s2, uint32_t (&o)[4])
+{
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const uint32_t pr = __builtin_amdgcn_perm(d1, d0, (uint32_t)(((4 + t) << 16) | t));
+        o[t] = as_u32((as_h2(and_or(pr, 0x00FF00FFu, kHalfMagic)) - zb) * s2);
+    }
 }
 
 typedef __attribute__((address_space(3))) uint8_t lds_byte_t;
@@ -420,15 +443,18 @@ __device__ __forceinline__ void pipe_epilogue(const PipeParams& p, const PipeIte
     }
 }
 
+// B8: 8-bit codes (32 bytes per row and step, one zero-point byte per block); otherwise
+// 4-bit codes.
+template <bool B8>
 __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
 {
+    using L = PipeLds<B8>;
     constexpr int BM = kPipeBM, BN = kPipeBN, FM = 4, FN = 4;
-    constexpr int A_ST = BM * 64;                               // one step of A
-    constexpr int CG = BN * 64, SG = BN * 16, ZG = BN * 4;      // one group: codes, scales, zp
-    constexpr int OFF_A = 0, OFF_C = OFF_A + 4 * A_ST, OFF_S = OFF_C + 3 * CG, OFF_Z = OFF_S + 3 * SG,
-                  OFF_B = OFF_Z + 3 * ZG, OFF_E = OFF_B + 2 * BN * 64;
-    static_assert(OFF_E + BM * 4 == kPipeLdsBytes, "LDS layout");
+    constexpr int A_ST = L::A_ST, CG = L::CG, SG = L::SG, ZG = L::ZG;
+    constexpr int OFF_A = L::OFF_A, OFF_C = L::OFF_C, OFF_S = L::OFF_S, OFF_Z = L::OFF_Z, OFF_B = L::OFF_B,
+                  OFF_E = L::OFF_E;
     constexpr int B16_SZ = BN * 64;
+    constexpr int CQ = B8 ? 8 : 4;   // code loads per wave and group
     extern __shared__ __attribute__((aligned(16))) uint8_t pipe_lds[];
     uint8_t* const lds = pipe_lds;
     const uint32_t lbase = lds_address(lds);
@@ -445,19 +471,34 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
     const __amdgpu_buffer_rsrc_t rz = buffer_rsrc(p.zp ? (const void*)p.zp : (const void*)p.scales,
                                                   p.zp ? p.N * p.zrb : 0);
     // Loop-invariant per-lane offsets; the step advance rides in the scalar soffset.
-    int avo[4], cvo[4];
+    // Codes: 4-bit, load q of a wave moves rows wave*64 + 16q .. + 15, 64 bytes each (lane
+    // i: row i/4, chunk i%4); 8-bit, rows wave*64 + 8q .. + 7, 128 bytes each, lane i
+    // fetching chunk (i%8) ^ (row%8) of row i/8 into slot i%8 (so that the dequant's
+    // 32-byte reads of 8 consecutive rows hit distinct banks).
+    int avo[4], cvo[CQ];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int r = wave * 64 + 16 * q + (lane >> 2);
         const int m = m0 + r;
         avo[q] = m < p.M ? m * p.K * 2 + c0 * 64 + pipe_slot(r, lane & 3) * 16 : kPipeFar;
-        const int n = n0 + r;
-        cvo[q] = n < p.N ? n * p.row_bytes + c0 * 16 + (lane & 3) * 16 : kPipeFar;
+    }
+#pragma unroll
+    for (int q = 0; q < CQ; ++q) {
+        if constexpr (B8) {
+            const int r = wave * 64 + 8 * q + (lane >> 3), n = n0 + r;
+            cvo[q] = n < p.N ? n * p.row_bytes + c0 * 32 + (((lane & 7) ^ (r & 7)) * 16) : kPipeFar;
+        } else {
+            const int n = n0 + wave * 64 + 16 * q + (lane >> 2);
+            cvo[q] = n < p.N ? n * p.row_bytes + c0 * 16 + (lane & 3) * 16 : kPipeFar;
+        }
     }
     const int brow = wave * 64 + lane;   // the weight row this lane loads scales for and dequantizes
     const int bn = n0 + brow;
     const int svo = bn < p.N ? bn * p.nb * 4 + c0 * 4 : kPipeFar;
-    const int zvo = bn < p.N ? bn * p.zrb + c0 / 2 : kPipeFar;
+    const int zvo = bn < p.N ? bn * p.zrb + (B8 ? c0 : c0 / 2) : kPipeFar;
+    // Without zero points the zero-point loads read 0 (an empty buffer) and zadd is the
+    // operator's default, 2^(bits - 1).
+    const uint32_t zadd = p.zp ? 0u : (B8 ? 128u : 8u);
     const int last = nsteps - 1;
 
     auto issue_a = [&](int t, int st) {   // step t -> stage st (clamped: a prefetch past the end re-reads)
@@ -466,38 +507,53 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
         for (int q = 0; q < 4; ++q)
             lds_load16(ra, avo[q], tc * 64, lbase + OFF_A + st * A_ST + (wave * 64 + 16 * q) * 64);
     };
-    auto issue_b = [&](int g, int buf) {  // steps 4g .. 4g+3 -> buffer buf
+    auto issue_b = [&](int g, int buf) {  // steps 4g .. 4g+3 -> buffer buf (CQ + 2 loads)
         const int gc = min(g, last >> 2);
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            lds_load16(rb, cvo[q], gc * 64, lbase + OFF_C + buf * CG + (wave * 64 + 16 * q) * 64);
+        for (int q = 0; q < CQ; ++q)
+            lds_load16(rb, cvo[q], gc * L::CROW, lbase + OFF_C + buf * CG + (wave * 64 + (64 / CQ) * q) * L::CROW);
         lds_load16(rsc, svo, gc * 16, lbase + OFF_S + buf * SG + wave * 64 * 16);
-        lds_load2(rz, zvo, gc * 2, lbase + OFF_Z + buf * ZG + wave * 64 * 4);
+        if constexpr (B8)
+            lds_load4(rz, zvo, gc * 4, lbase + OFF_Z + buf * ZG + wave * 64 * 4);
+        else
+            lds_load2(rz, zvo, gc * 2, lbase + OFF_Z + buf * ZG + wave * 64 * 4);
     };
     struct Raw {
-        u32x4_t q;
+        u32x4_t q[B8 ? 2 : 1];
         float s;
         uint32_t zb;
     };
     auto read_raw = [&](int t, int buf) {
         Raw r;
         const int ph = t & 3;
-        r.q = *reinterpret_cast<const u32x4_t*>(lds + OFF_C + buf * CG + brow * 64 + ph * 16);
+        if constexpr (B8) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                r.q[h] = *reinterpret_cast<const u32x4_t*>(lds + OFF_C + buf * CG + brow * 128 +
+                                                           (((2 * ph + h) ^ (brow & 7)) * 16));
+        } else {
+            r.q[0] = *reinterpret_cast<const u32x4_t*>(lds + OFF_C + buf * CG + brow * 64 + ph * 16);
+        }
         r.s = *reinterpret_cast<const float*>(lds + OFF_S + buf * SG + brow * 16 + ph * 4);
         r.zb = *reinterpret_cast<const uint32_t*>(lds + OFF_Z + buf * ZG + brow * 4);
         return r;
     };
     auto dequant = [&](const Raw& raw, int t) {
-        const int zp = p.zp ? (int)((raw.zb >> ((t & 3) * 4)) & 0x0F) : 8;
-        const h2_t zb = as_h2(kHalfMagic | ((uint32_t)zp << 16) | (uint32_t)zp);
+        const uint32_t zp = B8 ? ((raw.zb >> ((t & 3) * 8)) & 0xFFu) + zadd : ((raw.zb >> ((t & 3) * 4)) & 0x0Fu) + zadd;
+        const h2_t zb = as_h2(kHalfMagic | (zp << 16) | zp);
         const _Float16 sh = (_Float16)raw.s;
         const h2_t s2 = h2_t{sh, sh};
         uint8_t* dst = lds + OFF_B + (t & 1) * B16_SZ + brow * 64;
-        const uint32_t qd[4] = {raw.q.x, raw.q.y, raw.q.z, raw.q.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             uint32_t o[4];
-            dequant8_f16(qd[j], zb, s2, o);
+            if constexpr (B8) {
+                const u32x4_t& c = raw.q[j >> 1];
+                dequant8_f16_b8((j & 1) ? c.z : c.x, (j & 1) ? c.w : c.y, zb, s2, o);
+            } else {
+                const u32x4_t& c = raw.q[0];
+                dequant8_f16(j == 0 ? c.x : j == 1 ? c.y : j == 2 ? c.z : c.w, zb, s2, o);
+            }
             *reinterpret_cast<u32x4_t*>(dst + pipe_slot(brow, j) * 16) = u32x4_t{o[0], o[1], o[2], o[3]};
         }
     };
@@ -537,18 +593,23 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
         }
     };
 
-    // Step t (A stage t % 4, fp16 weight tile t & 1), with R0 holding the operands of its
+    // Step t (A stage t % NA, fp16 weight tile t & 1), with R0 holding the operands of its
     // first half (k 0-15):
     //   first half:  read R1 (k 16-31) and the raw weights of step t+2; MFMAs on R0,
     //                interleaved with the dequant of step t+1 into tile (t+1) & 1;
     //                wait for A(t+1); barrier;
-    //   second half: read R0 of step t+1; MFMAs on R1, interleaved with the issue of
-    //                A(t+3) and, at t % 4 == 0, of weight group t/4 + 2.
-    // So every LDS read runs under MFMAs that do not depend on it. Weight group g lives
-    // in raw buffer g % 3 and is issued two groups (8 steps) ahead. Issue order per
-    // wave: B(0) B(1) A(0) A(1) A(2), then per step A(t+3) [4 loads] and, at t % 4 == 0,
-    // B(t/4+2) [6 loads]; each wait counts the loads issued after the one waited for
-    // (the weight group read at step t+1 was issued before A(t+1)).
+    //   second half: read R0 of step t+1; MFMAs on R1, interleaved with the issue of the
+    //                next loads.
+    // So every LDS read runs under MFMAs that do not depend on it. Each wait is a vmcnt
+    // count of the loads issued after the one waited for:
+    //   4-bit: A issued 3 steps ahead into 4 stages; weight group g lives in raw buffer
+    //   g % 3 and is issued two groups (8 steps) ahead, at t % 4 == 0 after A(t+3). Issue
+    //   order per wave: B(0) B(1) A(0) A(1) A(2), then per step A(t+3) [4 loads] and, at
+    //   t % 4 == 0, B(t/4+2) [6 loads].
+    //   8-bit: A issued 2 steps ahead into 3 stages; group g lives in raw buffer g % 2 and
+    //   is issued at t % 4 == 1 of group g - 2, after A(t+2), once the last raw reads of
+    //   group g - 2 (at step 4g - 7) are behind the step's barrier. Issue order: B(0) B(1)
+    //   A(0) A(1), then per step A(t+2) [4] and, at t % 4 == 1, B(t/4+2) [10].
     Ops R0, R1;
     // The tile's row exponents go straight to LDS (row t at OFF_E + 4t), oldest of all the
     // loads, so every wait below covers them too; rows past M read zero.
@@ -560,25 +621,32 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
     issue_b(1, 1);
     issue_a(0, 0);
     issue_a(1, 1);
-    issue_a(2, 2);
-    wait_vmcnt<8>();                     // B(0), B(1), A(0): then A(1), A(2)
+    if constexpr (!B8) {
+        issue_a(2, 2);
+        wait_vmcnt<8>();                     // B(0), B(1), A(0): then A(1), A(2)
+    } else {
+        wait_vmcnt<4>();                     // B(0), B(1), A(0): then A(1)
+    }
     Raw raw = read_raw(0, 0);
     dequant(raw, 0);
     raw = read_raw(1, 0);
     lds_barrier();
     load_ops(0, 0, 0, R0);
-    auto step = [&](int t, auto phase, auto wait, int rbuf, int nbuf) {
+    // st: A stage of step t; rbuf: raw buffer of step t+2; nbuf: the buffer of the weight
+    // group this step issues (if any).
+    auto step = [&](int t, auto phase, auto wait, int st, int rbuf, int nbuf) {
         constexpr int ph = decltype(phase)::value;
         __builtin_amdgcn_sched_barrier(0);
-        load_ops(ph, ph & 1, 1, R1);
+        load_ops(st, ph & 1, 1, R1);
         Raw rn = read_raw(t + 2, rbuf);
         mfma_ops(R0);
         dequant(raw, t + 1);
-        // 16 MFMAs, each followed by one LDS operation (the 11 reads, then the dequant's 4
+        // 16 MFMAs, each followed by one LDS operation (the reads, then the dequant's 4
         // writes) and a share of the dequant's VALU work: about 5 VALU instructions fit
         // in the shadow of one 32-cycle MFMA.
+        constexpr int NR = B8 ? 12 : 11;
 #pragma unroll
-        for (int g = 0; g < 11; ++g) {
+        for (int g = 0; g < NR; ++g) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
@@ -589,31 +657,55 @@ __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
             __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if constexpr (!B8) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_barrier(0);
         raw = rn;
         wait_vmcnt<decltype(wait)::value>();
         lds_barrier();
-        load_ops((ph + 1) & 3, (ph + 1) & 1, 0, R0);
-        mfma_ops(R1);
-        issue_a(t + 3, (ph + 3) & 3);
-        if constexpr (ph == 0) issue_b((t >> 2) + 2, nbuf);
+        if constexpr (B8) {
+            const int st1 = st == 2 ? 0 : st + 1;
+            load_ops(st1, (ph + 1) & 1, 0, R0);
+            mfma_ops(R1);
+            issue_a(t + 2, st1 == 2 ? 0 : st1 + 1);
+            if constexpr (ph == 1) issue_b((t >> 2) + 2, nbuf);
+        } else {
+            load_ops((ph + 1) & 3, (ph + 1) & 1, 0, R0);
+            mfma_ops(R1);
+            issue_a(t + 3, (ph + 3) & 3);
+            if constexpr (ph == 0) issue_b((t >> 2) + 2, nbuf);
+        }
         // The second half is left to the compiler's scheduler: a pattern of one MFMA per LDS
         // read (8 reads, then 8 MFMAs) measured 0.2-0.5% slower (M=2048 K=11008 214.8 against
         // 213.8 us; K=4096 201.3 against 201.0 us).
         __builtin_amdgcn_sched_barrier(0);
     };
     using std::integral_constant;
-    int b0 = 0, b1 = 1, b2 = 2;           // raw buffers of groups g, g+1, g+2
-    for (int t = 0; t < nsteps; t += 4) {
-        step(t, integral_constant<int, 0>{}, integral_constant<int, 4>{}, b0, b2);       // A(t+1): then A(t+2)
-        step(t + 1, integral_constant<int, 1>{}, integral_constant<int, 10>{}, b0, b2);  // A(t+2): then A(t+3), B(g+2)
-        step(t + 2, integral_constant<int, 2>{}, integral_constant<int, 10>{}, b1, b2);  // A(t+3): then B(g+2), A(t+4)
-        step(t + 3, integral_constant<int, 3>{}, integral_constant<int, 4>{}, b1, b2);   // A(t+4): then A(t+5)
-        const int bt = b0;
-        b0 = b1;
-        b1 = b2;
-        b2 = bt;
+    if constexpr (B8) {
+        int b0 = 0, b1 = 1;                // raw buffers of groups g, g+1
+        int st = 0;                        // A stage of step t
+        for (int t = 0; t < nsteps; t += 4) {
+            const int s1 = st == 2 ? 0 : st + 1, s2 = s1 == 2 ? 0 : s1 + 1;
+            step(t, integral_constant<int, 0>{}, integral_constant<int, 0>{}, st, b0, b0);        // A(t+1): last issued
+            step(t + 1, integral_constant<int, 1>{}, integral_constant<int, 0>{}, s1, b0, b0);    // A(t+2): last issued
+            step(t + 2, integral_constant<int, 2>{}, integral_constant<int, 10>{}, s2, b1, b0);   // A(t+3): then B(g+2)
+            step(t + 3, integral_constant<int, 3>{}, integral_constant<int, 0>{}, st, b1, b0);    // A(t+4): last issued
+            st = s1;                        // (t + 4) % 3
+            const int bt = b0;
+            b0 = b1;
+            b1 = bt;
+        }
+    } else {
+        int b0 = 0, b1 = 1, b2 = 2;           // raw buffers of groups g, g+1, g+2
+        for (int t = 0; t < nsteps; t += 4) {
+            step(t, integral_constant<int, 0>{}, integral_constant<int, 4>{}, 0, b0, b2);       // A(t+1): then A(t+2)
+            step(t + 1, integral_constant<int, 1>{}, integral_constant<int, 10>{}, 1, b0, b2);  // A(t+2): then A(t+3), B(g+2)
+            step(t + 2, integral_constant<int, 2>{}, integral_constant<int, 10>{}, 2, b1, b2);  // A(t+3): then B(g+2), A(t+4)
+            step(t + 3, integral_constant<int, 3>{}, integral_constant<int, 4>{}, 3, b1, b2);   // A(t+4): then A(t+5)
+            const int bt = b0;
+            b0 = b1;
+            b1 = b2;
+            b2 = bt;
+        }
     }
     wait_vmcnt<0>();
     __syncthreads();   // every wave is past its last LDS access of the main loop; exponents landed

@@ -45,20 +45,6 @@
 
 namespace msnb {
 
-// Eight 8-bit codes (d0 = codes 0..3, d1 = codes 4..7, one byte each) as four fp16 pairs
-// (k_t, k_{t+4}), t = 0..3, the order of dequant8_f16's pairs (and of the permuted A):
-// v_perm gathers byte t of d0 and byte t of d1 into halves 0 and 1, v_and_or puts them
-// under the exponent of 1024.0 (1024 + q exactly), then (1024 + q) - (1024 + zp) = q - zp
-// exactly (|q - zp| <= 255) and one rounding to fp16 of (q - zp) * fl16(s).
-__device__ __forceinline__ void dequant8_f16_b8(uint32_t d0, uint32_t d1, h2_t zb, h2_t s2, uint32_t (&o)[4])
-{
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const uint32_t pr = __builtin_amdgcn_perm(d1, d0, (uint32_t)(((4 + t) << 16) | t));
-        o[t] = as_u32((as_h2(and_or(pr, 0x00FF00FFu, kHalfMagic)) - zb) * s2);
-    }
-}
-
 constexpr int kRbBM = 128;   // rows of A per tile; the tile's columns are 64 * NF (NF = 1, 2, 4)
 constexpr int kRbRing = 3;                     // weight blocks in registers
 constexpr int kRbBufBytes = kRbBM * 128 * 2;   // one block of fp16 A

@@ -901,11 +901,13 @@ int launch_generic(const Weights& w, const float* dA, float* dY, int M, hipStrea
 // fp16 activations [M][K] then row exponents [M], each 256-byte aligned.
 size_t a16_bytes(int M, int K) { return align256((size_t)M * K * 2) + align256((size_t)M * 4); }
 
-// The pipelined prefill takes M > 16, block size 32, K a multiple of 128, fp16-safe
-// scales, and buffers (Y included) below kPipeFar (its out-of-range offset).
+// The pipelined prefill takes M > 16, 4-bit codes (a fast layout) or 8-bit codes with
+// packed or no zero points, block size 32, K a multiple of 128, fp16-safe scales, and
+// buffers (Y included) below kPipeFar (its out-of-range offset).
 bool pipe_eligible(const Weights& w, const Knobs& kn, int M)
 {
-    return !kn.pipe_off() && w.fast && M > kPanelMaxM && w.log2cpb == 0 && (w.K % 128) == 0 && w.pipe_scales_ok &&
+    const bool fmt = (w.fast && w.log2cpb == 0) || (w.bits == 8 && !w.zp_float && w.bs == 32);
+    return !kn.pipe_off() && fmt && M > kPanelMaxM && (w.K % 128) == 0 && w.pipe_scales_ok &&
            (int64_t)w.N * w.row_bytes < kPipeFar && (int64_t)M * w.K * 2 < kPipeFar &&
            (int64_t)w.N * w.nb * 4 < kPipeFar && (int64_t)M * w.N * 4 < kPipeFar;
 }
@@ -1009,11 +1011,16 @@ int launch_pipe(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, floa
     const int tiles_m = (M + kPipeBM - 1) / kPipeBM, tiles_n = (w.N + kPipeBN - 1) / kPipeBN;
     const PipeSplit sp = pipe_split(w, kn, M);
     const PipeWs L = pipe_ws(w, M, sp);
-    static std::atomic<bool> lds_raised{false};
-    if (!lds_raised.load()) {
-        MS_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(mfma_w4_pipe_kernel),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, kPipeLdsBytes));
-        lds_raised.store(true);
+    const bool b8 = w.bits == 8;
+    static std::atomic<bool> lds_raised[2] = {false, false};
+    if (!lds_raised[b8].load()) {
+        if (b8)
+            MS_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(mfma_w4_pipe_kernel<true>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, PipeLds<true>::BYTES));
+        else
+            MS_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(mfma_w4_pipe_kernel<false>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, PipeLds<false>::BYTES));
+        lds_raised[b8].store(true);
     }
     const AConvView av = a_conv_for(conv, ws, dA, M, w.K, stream);
     const uint32_t* a16 = av.a16;
@@ -1042,7 +1049,11 @@ int launch_pipe(Weights& w, const Knobs& kn, const Ws& ws, const float* dA, floa
     p.epoch = next_epoch();
     p.spin_limit = kn.spin_limit();
     p.err = w.d_err;
-    hipLaunchKernelGGL(mfma_w4_pipe_kernel, dim3(kXcds * (sp.xu + sp.xv)), dim3(256), kPipeLdsBytes, stream, p);
+    const dim3 grid(kXcds * (sp.xu + sp.xv)), block(256);
+    if (b8)
+        hipLaunchKernelGGL(mfma_w4_pipe_kernel<true>, grid, block, PipeLds<true>::BYTES, stream, p);
+    else
+        hipLaunchKernelGGL(mfma_w4_pipe_kernel<false>, grid, block, PipeLds<false>::BYTES, stream, p);
     MS_HIP_CHECK(hipGetLastError());
     return MS_HIP_OK;
 }
@@ -1356,7 +1367,9 @@ KernelId choose_kernel(const Weights& w, const Knobs& kn, int M)
     if (!w.fast) {
         if (M <= kPanelMaxM && skinny_eligible(w, kn, M)) return kSkinny;   // 8-bit small M
         if (pick_gemv8_config(w, kn, M) >= 0) return kGemvW8;
-        if (rb_eligible(w, kn, M)) return kRb;   // 8-bit prefill
+        // 8-bit prefill: the pipelined kernel (block size 32) by the same rule as 4-bit codes
+        if (M > kPanelMaxM && pipe_eligible(w, kn, M) && !use_rb(w, kn, M)) return kPipe;
+        if (rb_eligible(w, kn, M)) return kRb;
         if (!general_eligible(w)) return kGeneric;
         return M <= kPanelMaxM ? kGemvGeneral : kMfmaGeneral;
     }

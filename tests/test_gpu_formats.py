@@ -70,8 +70,38 @@ def expected_kernel(op: Op, M: int, float_zp: bool = False, fp16_scales: bool = 
         return "gemv_w8"
     if (op.bits == 8 and not float_zp and pow2 and op.block_size >= 32 and op.K % 128 == 0 and M > 16
             and fp16_scales):
-        return "mfma_w4_rb"
+        return "mfma_w4_pipe" if op.block_size == 32 and pipe_over_rb(M, op.N, op.K) else "mfma_w4_rb"
     return "gemv_general" if M <= 16 else "mfma_general"
+
+
+def pipe_items(M, N, K, ksplit=0):
+    """Work items of a pipelined prefill launch on 256 CUs (ksplit: knob 3; 0 the default
+    rule: every tile K-split when the tiles fill at most half of the CUs, else the tiles of
+    a last round that would; 1 none; 2 all; 3 the second half)."""
+    tiles = -(-M // 256) * -(-N // 256)
+    full = tiles
+    if K // 128 >= 2:
+        if ksplit == 2 or (ksplit == 0 and 2 * tiles <= 256):
+            full = 0
+        elif ksplit == 3:
+            full = tiles // 2
+        elif ksplit == 0 and 0 < tiles % 256 <= 128:
+            full = tiles - tiles % 256
+    return full, tiles
+
+
+def pipe_over_rb(M, N, K):
+    """The library's choice of the pipelined kernel over mfma_w4_rb: more than one 128-row
+    tile of A, and work items that fill at least half of the 256 CUs."""
+    full, tiles = pipe_items(M, N, K)
+    return M > 128 and 2 * (full + 2 * (tiles - full)) >= 256
+
+
+def pipe_grid(M, N, K, ksplit):
+    """The pipelined launch's grid: 8 XCDs x (whole tiles per XCD + two halves per split
+    tile per XCD)."""
+    full, tiles = pipe_items(M, N, K, ksplit)
+    return 8 * (-(-full // 8) + 2 * -(-(tiles - full) // 8))
 
 
 def check_against_oracle(w, a, b, s, zp, zpf, op, what):
@@ -84,7 +114,7 @@ def check_against_oracle(w, a, b, s, zp, zpf, op, what):
     if kernel == "mfma_general":
         allowed = (4 * gamma2(op.K) + 2.0 ** -20) * cond + 2.0 ** -30 * (
             np.max(np.abs(a), axis=1, keepdims=True).astype(np.float64) * np.abs(W).sum(axis=1)[None, :])
-    elif kernel == "mfma_w4_rb":
+    elif kernel in ("mfma_w4_rb", "mfma_w4_pipe"):
         # fp16 prefill numerics: A rounded once to fp16 after its row's power-of-two scaling
         # (2^-11 relative; below the fp16 normal range, 2^-39 of the row's max absolute)
         # and W = fl16((q - zp) fl16(s)) (2^-10 relative: fl16(s) and the product), exact
@@ -365,9 +395,9 @@ def test_prefill_8bit(gpu, op, M):
 
 
 def test_prefill_8bit_every_split(gpu):
-    """Every tile width and K split of the 8-bit prefill (knobs 9 and 7), and the exact general
-    kernel it leaves to when switched off (knob 6 = 1) or when a scale is outside the fp16
-    range (|s| > 256)."""
+    """Every tile width and K split of the 8-bit prefill (knobs 9 and 7); the pipelined
+    kernel when it is switched off (knob 6 = 1), and the exact general kernel when both are
+    (knob 2 = 1) or when a scale is outside the fp16 range (|s| > 256)."""
     op = Op("b8p_split", 2048, 520, 32, True, bits=8)
     b, s, z = workloads.make_weights(op, seed=41)
     a = workloads.make_activations(96, op.K, seed=42, kind="rmsnorm")
@@ -384,17 +414,87 @@ def test_prefill_8bit_every_split(gpu):
         w.set_tuning(7, 0)
         w.set_tuning(6, 1)
         kernel, _ = check_against_oracle(w, a, b, s, z, None, op, "rb off")
+        assert kernel == "mfma_w4_pipe"   # block size 32: the pipelined kernel's 8-bit form
+        w.set_tuning(2, 1)
+        kernel, _ = check_against_oracle(w, a, b, s, z, None, op, "rb and pipe off")
         assert kernel == "mfma_general"
     finally:
         w.set_tuning(9, 0)
         w.set_tuning(7, 0)
         w.set_tuning(6, 0)
+        w.set_tuning(2, 0)
     w.close()
     s_big = s.copy()
     s_big[7] = np.float32(300.0)        # 255 * 300 overflows fp16
     w = native.NBitsWeights(b, s_big, z, op.N, op.K, op.bits, op.block_size)
     kernel, _ = check_against_oracle(w, a, b, s_big, z, None, op, "scale 300")
     assert kernel == "mfma_general"
+    w.close()
+
+
+# ---- 8-bit codes on the pipelined prefill kernel -------------------------------------------
+@pytest.mark.parametrize("zp", [True, False], ids=["zp", "default_zp"])
+@pytest.mark.parametrize("M", [17, 33, 100, 129, 300])
+def test_prefill_8bit_pipelined_partial_tiles(gpu, M, zp):
+    """The pipelined kernel's 8-bit form (mfma_w4_rb, which these small launches take by
+    default, switched off: knob 6) on tiles cut by M and N (N=333 is not a multiple of 256;
+    K=896 is 7 groups of 4 steps, so the two K halves are unequal), with no, every and half
+    of its tiles K-split (knob 3), against the oracle at the prefill bar; without zero
+    points the codes are centred on 128."""
+    op = Op("b8pp", 896, 333, 32, zp, bits=8)
+    b, s, z = workloads.make_weights(op, seed=M + 3)
+    a = workloads.make_activations(M, op.K, seed=M + 4, kind="rmsnorm")
+    w = native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
+    try:
+        w.set_tuning(6, 1)
+        for ks in (1, 2, 3):
+            w.set_tuning(3, ks)
+            info = w.launch_info(M)
+            log(f"8-bit pipelined M={M} zp={zp} ksplit={ks} {info}")
+            assert info["kernel"] == "mfma_w4_pipe" and info["grid"] == pipe_grid(M, op.N, op.K, ks), info
+            check_against_oracle(w, a, b, s, z, None, op, f"8-bit pipelined ksplit={ks} M={M}")
+    finally:
+        w.set_tuning(3, 0)
+        w.set_tuning(6, 0)
+    w.close()
+
+
+B8_PIPE_FULL = [(Op("b8_up", 4096, 11008, 32, True, bits=8), 2048),
+                (Op("b8_down", 11008, 4096, 32, True, bits=8), 2048),
+                (Op("b8_up", 4096, 11008, 32, True, bits=8), 512),
+                (Op("b8_up_sym", 4096, 11008, 32, False, bits=8), 300)]
+
+
+@pytest.mark.parametrize("op,M", B8_PIPE_FULL, ids=lambda v: str(v) if isinstance(v, int) else v.name)
+def test_prefill_8bit_pipelined_full_size(gpu, op, M):
+    """8-bit codes at the Llama-2-7B MLP shapes on the library's own choice (the pipelined
+    kernel; K=11008 with its tiles K-split at M=2048), with activation outliers of 1e5 and
+    -3e6 and rows near 1e-6: every output finite, relative Frobenius error <= 2e-3 against
+    the oracle on 96 sampled columns (the rows near 1e-6 on their own too), and bit-identical
+    on a second call."""
+    b, s, z = workloads.make_weights(op, seed=M + op.K)
+    rng = np.random.default_rng(M + 1)
+    a = workloads.make_activations(M, op.K, seed=M + 2, kind="rmsnorm")
+    rows = rng.permutation(M)
+    big, tiny = rows[:4], rows[4:8]
+    for i, r in enumerate(big):
+        a[r, rng.integers(op.K)] = (1e5 if i % 2 == 0 else -3e6)
+    a[tiny] *= np.float32(1e-6)
+    w = native.NBitsWeights(b, s, z, op.N, op.K, op.bits, op.block_size)
+    info = w.launch_info(M)
+    log(f"8-bit pipelined full size {op.name} M={M} K={op.K} N={op.N} {info}")
+    assert info["kernel"] == "mfma_w4_pipe" == expected_kernel(op, M), info
+    y = w.gemm(a)
+    assert np.all(np.isfinite(y))
+    cols = np.sort(rng.choice(op.N, 96, replace=False))
+    ref = oracle.matmul_nbits(a, b[cols], s.reshape(op.N, -1)[cols], None if z is None else z[cols], len(cols),
+                              op.K, op.bits, op.block_size)
+    for sel, what in ((slice(None), "all rows"), (tiny, "rows near 1e-6")):
+        got, exp = y[sel][:, cols].astype(np.float64), ref[sel].astype(np.float64)
+        rel = float(np.linalg.norm(got - exp) / np.linalg.norm(exp))
+        log(f"  {what}: relative Frobenius error {rel:.3e}")
+        assert rel <= 2e-3, what
+    assert np.array_equal(w.gemm(a), y)
     w.close()
 
 

@@ -3,7 +3,7 @@
 Both run the same kernels on the same inputs, so their outputs must be equal bit for
 bit: on every kernel that uses a workspace (the small-M matrix-core GEMV with its K
 split, the register-operand prefill with its K-split reduce, for 4- and 8-bit codes, the
-pipelined prefill with split tiles) and on one that does not (the decode GEMV, the exact general
+pipelined prefill with split tiles, for 4- and 8-bit codes) and on one that does not (the decode GEMV, the exact general
 prefill), two calls in a row through the C ABI, the second with a smaller input (the
 scratch keeps the first call's larger contents; its counters must start at zero again).
 """
@@ -38,6 +38,7 @@ CASES = [
     ("rb", workloads.Op("up", 4096, 11008, 32, True), 128, 40, "mfma_w4_rb", 1.0),
     ("rb8", workloads.Op("b8", 4096, 4096, 64, True, bits=8), 130, 24, "mfma_w4_rb", 1.0),
     ("pipe", workloads.Op("down", 11008, 4096, 32, True), 2048, 512, "mfma_w4_pipe", 1.0),
+    ("pipe8", workloads.Op("up8", 4096, 11008, 32, True, bits=8), 1024, 300, "mfma_w4_pipe", 1.0),
     ("exact", workloads.Op("wide", 1024, 768, 64, True), 300, 33, "mfma_w4", 1e6),
 ]
 
