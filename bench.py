@@ -263,7 +263,9 @@ def main() -> int:
     ap.add_argument("--op", default="", help="profiling mode: launch only this 7B decode op (q,k,v,o,gate,up,down), "
                                              "a grouped launch (qkv, gate_up), prefill_up / prefill_down or the "
                                              "block-size-128 small-batch smallm_up / smallm_down (M from --m), "
-                                             "eagerly over the rotation, then a plain copy of --copy-mib; no JSON line")
+                                             "eagerly over the rotation, then a plain copy of --copy-mib; or "
+                                             "decoder_layer (--calls steps of the device-resident 7B layer) or "
+                                             "attention_prefill (--calls launches); no JSON line")
     ap.add_argument("--calls", type=int, default=64, help="launches in --op mode")
     ap.add_argument("--m", type=int, default=2048, help="rows of A for prefill_* and smallm_* in --op mode")
     ap.add_argument("--copy-mib", type=int, default=256, help="size of the calibration copy in --op mode")
@@ -573,6 +575,38 @@ class LayerRotation:
                 w.close()
 
 
+class AttentionPrefill:
+    """GroupQueryAttention at prefill on the 7B layer's heads: 2048 query rows over
+    themselves (causal), rotary (half-split, base 10000), past 0, random q/k/v."""
+    S = 2048
+
+    def __init__(self):
+        import torch
+        from modelsharp_amd import native
+        S, H, KH, D = self.S, LayerRotation.H, LayerRotation.KH, LayerRotation.D
+        gen = torch.Generator(device="cpu").manual_seed(5)
+        self.q = torch.randn(1, S, H * D, generator=gen).cuda()
+        self.k = torch.randn(1, S, KH * D, generator=gen).cuda()
+        self.v = torch.randn(1, S, KH * D, generator=gen).cuda()
+        ang = torch.outer(torch.arange(S, dtype=torch.float64),
+                          1.0 / 10000 ** (torch.arange(D // 2, dtype=torch.float64) / (D // 2)))
+        self.cos, self.sin = torch.cos(ang).float().cuda(), torch.sin(ang).float().cuda()
+        self.pk, self.pv = torch.empty(1, KH, S, D, device="cuda"), torch.empty(1, KH, S, D, device="cuda")
+        self.o = torch.empty(1, S, H * D, device="cuda")
+        self.d = native.GqaDesc(batch=1, q_seq=S, kv_seq=S, num_heads=H, kv_num_heads=KH, head_dim=D, packed_qkv=0,
+                                past_seq=0, past_in_present=0, present_capacity=S, do_rotary=1, rotary_interleaved=0,
+                                cos_rows=S, cos_cols=D // 2, local_window_size=-1, scale=0.0, seqlens_len=0)
+        self.wsb = native.gqa_workspace_size(self.d)
+        self.ws = torch.empty(max(1, (self.wsb + 3) // 4), device="cuda")
+        self.flops = 2 * 2 * H * D * S * (S + 1) / 2   # q.k and p.v over the causal half
+
+    def launch(self, stream):
+        from modelsharp_amd import native
+        native.gqa(self.d, self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), None, None, None,
+                   self.cos.data_ptr(), self.sin.data_ptr(), self.o.data_ptr(), self.pk.data_ptr(), self.pv.data_ptr(),
+                   self.ws.data_ptr(), self.wsb, stream)
+
+
 def decoder_layer(args):
     """The 7B decoder layer at decode on the device: SkipSimplifiedLayerNormalization ->
     q/k/v (one grouped launch) -> GroupQueryAttention (28 query / 4 kv heads of 128, rotary,
@@ -604,27 +638,14 @@ def decoder_layer(args):
     del lay
     torch.cuda.empty_cache()
     # attention at prefill: 2048 query rows over themselves (causal), rotary, past 0
-    S, H, KH, D = 2048, LayerRotation.H, LayerRotation.KH, LayerRotation.D
-    gen = torch.Generator(device="cpu").manual_seed(5)
-    q = torch.randn(1, S, H * D, generator=gen).cuda()
-    k = torch.randn(1, S, KH * D, generator=gen).cuda()
-    v = torch.randn(1, S, KH * D, generator=gen).cuda()
-    ang = torch.outer(torch.arange(S, dtype=torch.float64), 1.0 / 10000 ** (torch.arange(D // 2, dtype=torch.float64) / (D // 2)))
-    cos, sin = torch.cos(ang).float().cuda(), torch.sin(ang).float().cuda()
-    pk, pv = torch.empty(1, KH, S, D, device="cuda"), torch.empty(1, KH, S, D, device="cuda")
-    o = torch.empty(1, S, H * D, device="cuda")
-    d = native.GqaDesc(batch=1, q_seq=S, kv_seq=S, num_heads=H, kv_num_heads=KH, head_dim=D, packed_qkv=0, past_seq=0,
-                       past_in_present=0, present_capacity=S, do_rotary=1, rotary_interleaved=0, cos_rows=S,
-                       cos_cols=D // 2, local_window_size=-1, scale=0.0, seqlens_len=0)
-    wsb = native.gqa_workspace_size(d)
-    ws = torch.empty(max(1, (wsb + 3) // 4), device="cuda")
-    gp = graph_of(lambda st: native.gqa(d, q.data_ptr(), k.data_ptr(), v.data_ptr(), None, None, None, cos.data_ptr(),
-                                        sin.data_ptr(), o.data_ptr(), pk.data_ptr(), pv.data_ptr(), ws.data_ptr(), wsb, st))
+    att = AttentionPrefill()
+    gp = graph_of(att.launch)
     msp = time_graph(gp, 5, 1)
-    flops = 2 * 2 * H * D * S * (S + 1) / 2   # q.k and p.v over the causal half
-    out["attention_prefill"] = {"q_seq": S, "past": 0, "us": round(msp * 1e3, 1),
-                                "TFLOPs": round(flops / (msp * 1e-3) / 1e12, 2)}
-    log(f"attention prefill S={S}: {msp * 1e3:.1f} us")
+    out["attention_prefill"] = {"q_seq": att.S, "past": 0, "us": round(msp * 1e3, 1),
+                                "TFLOPs": round(att.flops / (msp * 1e-3) / 1e12, 2)}
+    log(f"attention prefill S={att.S}: {msp * 1e3:.1f} us")
+    del gp, att
+    torch.cuda.empty_cache()
     return out
 
 
@@ -635,6 +656,23 @@ def profile_op(args) -> int:
     import torch
     from modelsharp_amd import workloads
     from modelsharp_amd import native
+    if args.op in ("decoder_layer", "attention_prefill"):
+        stream = torch.cuda.current_stream().cuda_stream
+        if args.op == "attention_prefill":
+            att = AttentionPrefill()
+            for _ in range(args.calls):
+                att.launch(stream)
+            what = f"GroupQueryAttention, {att.S} queries, past 0, 28/4 heads of 128 ({att.flops:.4g} flops each)"
+        else:
+            copies = 4
+            lay = LayerRotation(copies, 2047, seed=21)
+            for i in range(args.calls):
+                for n in LayerRotation.STAGES:
+                    lay.stage(i % copies, n, stream)
+            what = f"7B decoder layer steps at past 2047 ({copies} rotating copies), stages {LayerRotation.STAGES}"
+        torch.cuda.synchronize()
+        log(f"{args.calls} launches of {args.op}: {what}; kernel sources {kernel_source_digest()}")
+        return 0
     if args.op.startswith("prefill_"):
         ops = [next(o for o in workloads.LLAMA7B_PREFILL_OPS if o.name == args.op[len("prefill_"):])]
         M, kind = args.m, "rmsnorm"
