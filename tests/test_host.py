@@ -230,6 +230,49 @@ def test_tuning_knobs_validated_without_a_device():
     assert "invalid weights handle" in native.last_error()
 
 
+def test_host_entries_from_many_threads():
+    """The host entries a caller may reach from several threads at once without a device:
+    validation (its message in each thread's own last error), the global tuning knobs
+    (atomics), the live-handle registry's rejection of unknown handles (a mutex) and the
+    attention checks. ctypes drops the GIL around each foreign call, so the threads run in
+    the library together; this is also the workload the host library's ThreadSanitizer
+    build is run on (the csrc Makefile's tsan target)."""
+    import threading
+    lib = native.load()
+    junk = (ctypes.c_uint32 * 64)(*([0x4D534E42] * 64))
+    bogus = ctypes.c_void_p(ctypes.addressof(junk))
+    n_out = ctypes.c_int()
+    failures = []
+
+    def work(t):
+        try:
+            for i in range(300):
+                K = -(t * 1000 + i) - 1
+                st = lib.ms_hip_nbits_check(2, K, 4, 4, 0, 0, 0, 0, -1)
+                msg = native.last_error()
+                assert st == 1 and f"(got N=2, K={K})" in msg, msg
+                assert lib.ms_hip_set_tuning(3, (t + i) % 3) == native.MS_HIP_OK
+                assert lib.ms_hip_set_tuning(99, 0) == native.MS_HIP_ERR_INVALID
+                assert lib.ms_hip_nbits_weights_info(bogus, ctypes.byref(n_out), None, None, None, None) == \
+                    native.MS_HIP_ERR_INVALID
+                assert lib.ms_hip_nbits_set_tuning(bogus, 0, 0) == native.MS_HIP_ERR_INVALID
+                assert lib.ms_hip_gqa_check(None) != native.MS_HIP_OK
+                lib.ms_hip_available()
+                # the last error is still this thread's own after the other threads' calls
+                st = lib.ms_hip_nbits_check(2, 8, 3, 4, 0, 0, 0, 0, -1)
+                assert st == 1 and native.last_error() == "MatMulNBits supports bits=4 or bits=8; got 3."
+        except AssertionError as e:   # noqa: PERF203
+            failures.append((t, str(e)))
+
+    threads = [threading.Thread(target=work, args=(t,)) for t in range(8)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    lib.ms_hip_set_tuning(3, 0)
+    assert not failures, failures[:3]
+
+
 def test_unknown_handles_are_rejected_not_read():
     """A pointer that is not a live handle (never created, or destroyed) is rejected by
     every entry without being dereferenced."""
