@@ -530,19 +530,31 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_group_kernel(GqaArgs p, float
     }
 }
 
-// The splits of gqa_group_kernel meet here: one wave per (unit, 64 channels). Lane s reads
-// split s's maximum and sum; the maximum, the rescale factors and the normaliser come from
-// wave reductions; then each lane adds its channel over the splits with every split's
-// load issued together (fixed order, so deterministic).
+// The splits of gqa_group_kernel meet here: one wave per (unit, 64 channels). Each lane
+// issues the loads of its channel over every split and of split `lane`'s maximum and sum
+// together (one round trip to memory: the workspace was written by workgroups on other
+// XCDs); the maximum, the rescale factors and the normaliser come from wave reductions;
+// then each lane adds its channel over the splits in split order (deterministic).
 __global__ __launch_bounds__(64) void gqa_merge_kernel(GqaArgs p, const float* __restrict__ ws, int splits)
 {
     const int D = p.D, slices = (D + 63) / 64;
     const int unit = blockIdx.x / slices, d = (blockIdx.x % slices) * 64 + threadIdx.x;
     const int lane = threadIdx.x;
     const GqaUnit u = gqa_unit(p, unit);
-    const float* w = ws + (int64_t)unit * splits * (D + 2);
-    const float ml = lane < splits ? w[lane * (D + 2) + D] : -__builtin_inff();
-    const float ll = lane < splits ? w[lane * (D + 2) + D + 1] : 0.0f;
+    // The unit's splits * (D + 2) floats through a buffer resource: loads past them (split
+    // s >= splits, or a channel past D) return 0 without a branch.
+    const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(ws + (int64_t)unit * splits * (D + 2), splits * (D + 2) * 4);
+    const bool dv = d < D;
+    const int dof = dv ? d * 4 : kOOB;
+    float vals[kGqaMaxSplits];
+#pragma unroll
+    for (int s = 0; s < kGqaMaxSplits; ++s)
+        vals[s] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rw, dof, s * (D + 2) * 4, 0));
+    const float ml = lane < splits ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                                   rw, (lane * (D + 2) + D) * 4, 0, 0))
+                                   : -__builtin_inff();
+    const float ll = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                   rw, lane < splits ? (lane * (D + 2) + D + 1) * 4 : kOOB, 0, 0));
     float M = ll > 0.0f ? ml : -__builtin_inff();
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
@@ -551,10 +563,7 @@ __global__ __launch_bounds__(64) void gqa_merge_kernel(GqaArgs p, const float* _
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o);
     const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-    if (d >= D) return;
-    float vals[kGqaMaxSplits];
-#pragma unroll
-    for (int s = 0; s < kGqaMaxSplits; ++s) vals[s] = s < splits ? w[s * (D + 2) + d] : 0.0f;
+    if (!dv) return;
     float o = 0.0f;
 #pragma unroll
     for (int s = 0; s < kGqaMaxSplits; ++s)
