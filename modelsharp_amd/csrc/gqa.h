@@ -393,6 +393,9 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_group_kernel(GqaArgs p, float
     const int pos = rotary_pos(q_abs, p);
     float* const kb = p.pk + (int64_t)(b * p.kvH + g) * p.cap * D;
     float* const vb = p.pv + (int64_t)(b * p.kvH + g) * p.cap * D;
+    // this (batch, kv head)'s cached rows [0, past) (the host keeps past * D * 4 below 2^31)
+    const __amdgpu_buffer_rsrc_t rkc = buffer_rsrc(kb, p.past * D * 4);
+    const __amdgpu_buffer_rsrc_t rvc = buffer_rsrc(vb, p.past * D * 4);
     // The new rows [past, past + Skv) of this kv head: the first workgroup of each (batch, kv
     // head) writes them to the present cache (K rotated as gqa_append_kernel does); a chunk
     // that holds one of them builds it from the input row itself, so no workgroup reads a
@@ -416,37 +419,90 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_group_kernel(GqaArgs p, float
 #pragma unroll
     for (int i = 0; i < kGqaGroupMax / HPT; ++i) acc[i] = 0.0f;
 
+    // The group's query rows: their loads go first (with the cos / sin entries of their
+    // rotation), the first chunk's key and value loads after them, and the rotation is
+    // applied once those are in flight, so it waits for the query loads alone. The formula
+    // is rotated()'s: a c - b s or b c + a s, each product rounded.
+    constexpr int QPT = kGqaGroupMax * D / kGqaThreads;
+    const int rot = 2 * p.rot_half;
+    // the group's query rows (grp rows of D floats from this unit's query row)
+    const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(p.q + (int64_t)(b * p.Sq + qi) * p.q_stride + g * grp * D, grp * D * 4);
+    const __amdgpu_buffer_rsrc_t rcs = buffer_rsrc(p.do_rotary ? p.cos : p.q, p.do_rotary ? p.cache_rows * p.half * 4 : 0);
+    const __amdgpu_buffer_rsrc_t rsn = buffer_rsrc(p.do_rotary ? p.sin : p.q, p.do_rotary ? p.cache_rows * p.half * 4 : 0);
+    float qa[QPT], qb[QPT], qc[QPT], qn[QPT];
+    bool qrot[QPT], qfirst[QPT];
+#pragma unroll
+    for (int t = 0; t < QPT; ++t) {
+        const int i = tid + t * kGqaThreads;
+        const int r = i / D, d = i - r * D;
+        const bool valid = i < grp * D, rotating = p.do_rotary && d < rot;
+        int j = d, i0 = d, i1 = d;
+        if (rotating) {
+            if (p.interleaved) {
+                j = d >> 1;
+                i0 = 2 * j;
+                i1 = i0 + 1;
+            } else {
+                j = d < p.rot_half ? d : d - p.rot_half;
+                i0 = j;
+                i1 = j + p.rot_half;
+            }
+        }
+        qrot[t] = rotating;
+        qfirst[t] = d == i0;
+        const int row = r * D;
+        const int cs = rotating ? (pos * p.half + j) * 4 : kOOB;
+        qa[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rq, valid ? (row + i0) * 4 : kOOB, 0, 0));
+        qb[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rq, valid && rotating ? (row + i1) * 4 : kOOB, 0, 0));
+        qc[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rcs, valid ? cs : kOOB, 0, 0));
+        qn[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsn, valid ? cs : kOOB, 0, 0));
+    }
+
     constexpr int PER = kGqaChunk * (D / 4) / kGqaThreads;   // float4s of K (and of V) per thread
     static_assert(PER * kGqaThreads == kGqaChunk * (D / 4), "chunk shape");
-    for (int c0 = j0; c0 < j1; c0 += kGqaChunk) {
+    // A chunk's cached K and V rows into registers (every load in flight together,
+    // branch-free: rows past the chunk or not yet in the cache read zero).
+    float4 k4[PER], v4[PER];
+    auto load_chunk = [&](int c0) {
         const int n = min(kGqaChunk, j1 - c0);
-        // this chunk's K and V rows into registers first (every load in flight together) ...
-        float4 k4[PER], v4[PER];
 #pragma unroll
         for (int u = 0; u < PER; ++u) {
             const int i = tid + u * kGqaThreads;
             const int r = i / (D / 4), c4 = i - r * (D / 4);
             const int key = c0 + r;
-            k4[u] = v4[u] = float4{0.0f, 0.0f, 0.0f, 0.0f};
-            if (r < n && key < p.past) {
-                k4[u] = *reinterpret_cast<const float4*>(kb + (int64_t)key * D + 4 * c4);
-                v4[u] = *reinterpret_cast<const float4*>(vb + (int64_t)key * D + 4 * c4);
-            } else if (r < n) {   // a new row: from the input
-                const int sr = key - p.past;
-                const float* krow = p.k + (int64_t)(b * p.Skv + sr) * p.kv_stride + g * D;
-                const float* vrow = p.v + (int64_t)(b * p.Skv + sr) * p.kv_stride + g * D;
-                const int kp = rotary_pos(key, p);
-                k4[u] = float4{rotated(krow, 4 * c4, kp, p), rotated(krow, 4 * c4 + 1, kp, p),
-                               rotated(krow, 4 * c4 + 2, kp, p), rotated(krow, 4 * c4 + 3, kp, p)};
-                v4[u] = float4{vrow[4 * c4], vrow[4 * c4 + 1], vrow[4 * c4 + 2], vrow[4 * c4 + 3]};
-            }
+            const int off = r < n && key < p.past ? (key * D + 4 * c4) * 4 : kOOB;
+            k4[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rkc, off, 0, 0));
+            v4[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rvc, off, 0, 0));
         }
-        // ... then, on the first chunk, the group's rotated query rows, while they land
-        if (c0 == j0) {
-            for (int i = tid; i < grp * D; i += kGqaThreads) {
-                const int r = i / D, d = i - r * D;
-                const float* qrow = p.q + (int64_t)(b * p.Sq + qi) * p.q_stride + (g * grp + r) * D;
-                qs[i] = rotated(qrow, d, pos, p);
+    };
+    load_chunk(j0);
+    __builtin_amdgcn_sched_barrier(0);   // the first chunk's loads stay ahead of the rotation below
+    // the query rows, rotated: waits for the query loads alone
+#pragma unroll
+    for (int t = 0; t < QPT; ++t) {
+        const int i = tid + t * kGqaThreads;
+        if (i < grp * D)
+            qs[i] = !qrot[t] ? qa[t] : qfirst[t] ? qa[t] * qc[t] - qb[t] * qn[t] : qb[t] * qc[t] + qa[t] * qn[t];
+    }
+    for (int c0 = j0; c0 < j1; c0 += kGqaChunk) {
+        const int n = min(kGqaChunk, j1 - c0);
+        if (c0 != j0) load_chunk(c0);
+        // ... and a new row (at most Skv of them, at the end of the range) from the input
+        if (c0 + n > p.past) {
+#pragma unroll
+            for (int u = 0; u < PER; ++u) {
+                const int i = tid + u * kGqaThreads;
+                const int r = i / (D / 4), c4 = i - r * (D / 4);
+                const int key = c0 + r;
+                if (r < n && key >= p.past) {
+                    const int sr = key - p.past;
+                    const float* krow = p.k + (int64_t)(b * p.Skv + sr) * p.kv_stride + g * D;
+                    const float* vrow = p.v + (int64_t)(b * p.Skv + sr) * p.kv_stride + g * D;
+                    const int kp = rotary_pos(key, p);
+                    k4[u] = float4{rotated(krow, 4 * c4, kp, p), rotated(krow, 4 * c4 + 1, kp, p),
+                                   rotated(krow, 4 * c4 + 2, kp, p), rotated(krow, 4 * c4 + 3, kp, p)};
+                    v4[u] = float4{vrow[4 * c4], vrow[4 * c4 + 1], vrow[4 * c4 + 2], vrow[4 * c4 + 3]};
+                }
             }
         }
         __syncthreads();   // the previous chunk's readers are done with ks / vs / ps
