@@ -645,7 +645,7 @@ template <int D>
 __global__ __launch_bounds__(256, 2) void gqa_flash_kernel(GqaArgs p)
 {
     typedef float floatx4_t __attribute__((ext_vector_type(4)));
-    constexpr int KP = D + 4;   // padded rows: the 16-byte reads of 16 rows and the dword reads of V hit distinct banks
+    constexpr int KP = D + 4;   // padded rows: the 16-byte reads of 16 K rows, and of the 4 V rows of a step, spread over the banks
     constexpr int T = D / 16;   // k steps of four per 16-channel group
     extern __shared__ __attribute__((aligned(16))) float flash_lds[];
     float* const ks = flash_lds;
@@ -682,7 +682,8 @@ __global__ __launch_bounds__(256, 2) void gqa_flash_kernel(GqaArgs p)
     const float* kb = p.pk + (int64_t)(b * p.kvH + g) * p.cap * D;
     const float* vb = p.pv + (int64_t)(b * p.kvH + g) * p.cap * D;
 
-    float m_run = -__builtin_inff(), l_run = 0.0f;   // statistics of query r16 (in the 4 lanes of each c)
+    const float scale2 = p.scale * 1.44269504088896341f;   // scale * log2(e)
+    float m_run = -__builtin_inff(), l_run = 0.0f;   // statistics of query r16 (in the 4 lanes of each c), base 2
     floatx4_t acc_o[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) acc_o[t] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -736,7 +737,10 @@ __global__ __launch_bounds__(256, 2) void gqa_flash_kernel(GqaArgs p)
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt) st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[kt].w, qreg[t][3], st[kt], 0, 0, 0);
         }
-        // scale, mask (only chunks that cross a query's key range), chunk maximum of query r16
+        // scale, mask (only chunks that cross a query's key range), chunk maximum of query r16.
+        // Scores are kept in base 2 (times scale * log2(e)): the softmax is then
+        // 2^(s - max) with the hardware exp2 (v_exp_f32, 1 ulp), the same weights as
+        // e^(scale q.k - max) to about 1e-7 relative, well inside the 1e-5 bar.
         const bool full = __all(c0 >= kf_q && c0 + kFlashK - 1 <= kl_q);
         float cm = -__builtin_inff();
 #pragma unroll
@@ -745,7 +749,7 @@ __global__ __launch_bounds__(256, 2) void gqa_flash_kernel(GqaArgs p)
             for (int i = 0; i < 4; ++i) {
                 const int key = c0 + kt * 16 + 4 * c + i;
                 const bool ok = full || (key >= kf_q && key <= kl_q);
-                const float sc = ok ? st[kt][i] * p.scale : -__builtin_inff();
+                const float sc = ok ? st[kt][i] * scale2 : -__builtin_inff();
                 st[kt][i] = sc;
                 cm = fmaxf(cm, sc);
             }
@@ -753,13 +757,13 @@ __global__ __launch_bounds__(256, 2) void gqa_flash_kernel(GqaArgs p)
         cm = fmaxf(cm, __shfl_xor(cm, 32));
         const float m_new = fmaxf(m_run, cm);
         const bool none = m_new == -__builtin_inff();   // no key of this query so far
-        const float alpha = none ? 1.0f : expf(m_run - m_new);
+        const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
         float ls = 0.0f;
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float e = none ? 0.0f : expf(st[kt][i] - m_new);
+                const float e = none ? 0.0f : __builtin_amdgcn_exp2f(st[kt][i] - m_new);
                 st[kt][i] = e;
                 ls = ls + e;
             }
@@ -774,27 +778,37 @@ __global__ __launch_bounds__(256, 2) void gqa_flash_kernel(GqaArgs p)
 #pragma unroll
             for (int t = 0; t < T; ++t) acc_o[t][i] = acc_o[t][i] * ai;
         }
-        // O += P V: A = P (queries x keys, from st), B = V (keys x channels)
+        // O += P V: A = P (queries x keys, from st), B = V (keys x channels). Output tile t
+        // column r16 is channel T r16 + t, so a lane's B operands of one key row are T
+        // consecutive floats (16-byte reads).
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float* vrow = vs + (kt * 16 + 4 * c + i) * KP + r16;
+                const float* vrow = vs + (kt * 16 + 4 * c + i) * KP + T * r16;
+                float4 vv[T / 4];
 #pragma unroll
-                for (int t = 0; t < T; ++t)
-                    acc_o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(st[kt][i], vrow[16 * t], acc_o[t], 0, 0, 0);
+                for (int w = 0; w < T / 4; ++w) vv[w] = *reinterpret_cast<const float4*>(vrow + 4 * w);
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    const float4& v4 = vv[t >> 2];
+                    const float bv = (t & 3) == 0 ? v4.x : (t & 3) == 1 ? v4.y : (t & 3) == 2 ? v4.z : v4.w;
+                    acc_o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(st[kt][i], bv, acc_o[t], 0, 0, 0);
+                }
             }
     }
-    // out rows: queries 4c + i of the wave, channels 16t + r16
+    // out rows: queries 4c + i of the wave, channels T r16 + t (T consecutive floats per lane)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const float li = __shfl(l_run, 4 * c + i);
         const int qo = q0 + wave * 16 + 4 * c + i;
         if (qo < p.Sq) {
-            float* orow = p.out + (int64_t)(b * p.Sq + qo) * p.H * D + h * D;
+            float* orow = p.out + (int64_t)(b * p.Sq + qo) * p.H * D + h * D + T * r16;
             const float inv = li > 0.0f ? 1.0f / li : 0.0f;
 #pragma unroll
-            for (int t = 0; t < T; ++t) orow[16 * t + r16] = acc_o[t][i] * inv;
+            for (int w = 0; w < T / 4; ++w)
+                *reinterpret_cast<float4*>(orow + 4 * w) = float4{acc_o[4 * w][i] * inv, acc_o[4 * w + 1][i] * inv,
+                                                                  acc_o[4 * w + 2][i] * inv, acc_o[4 * w + 3][i] * inv};
         }
     }
 }
