@@ -564,10 +564,14 @@ class LayerRotation:
                                   stream)
         elif name == "silu_mul":
             native.silu_mul(self.gt.data_ptr(), self.up.data_ptr(), self.act.data_ptr(), self.INTER, stream)
+        elif name == "gate_up_silu":   # gate, up and SiLU-Mul in one launch
+            native.gemm_dev_swiglu(h[4], h[5], self.n2.data_ptr(), self.act.data_ptr(), 1, stream)
         elif name == "down":
             h[6].gemm_dev(self.act.data_ptr(), self.x[r].data_ptr(), 1, stream)
 
-    STAGES = ("norm1", "qkv", "attention", "o", "norm2", "gate_up", "silu_mul", "down")
+    STAGES = ("norm1", "qkv", "attention", "o", "norm2", "gate_up_silu", "down")
+    # the same step with gate+up and SiLU-Mul as two launches
+    UNFUSED = ("norm1", "qkv", "attention", "o", "norm2", "gate_up", "silu_mul", "down")
 
     def close(self):
         for row in self.h:
@@ -611,9 +615,9 @@ def decoder_layer(args):
     """The 7B decoder layer at decode on the device: SkipSimplifiedLayerNormalization ->
     q/k/v (one grouped launch) -> GroupQueryAttention (28 query / 4 kv heads of 128, rotary,
     past 2047 rows appended in place) -> o -> SkipSimplifiedLayerNormalization -> gate/up
-    (one grouped launch) -> SiLU*Mul -> down, device pointers throughout; rotating copies of
-    the layer (weights and KV cache) over >= 1 GiB. Then GroupQueryAttention at prefill
-    (2048 query rows, past 0)."""
+    and SiLU*Mul (one launch) -> down, device pointers throughout; rotating copies of the
+    layer (weights and KV cache) over >= 1 GiB; the same step with gate/up and SiLU*Mul as
+    two launches beside it. Then GroupQueryAttention at prefill (2048 query rows, past 0)."""
     import torch
     from modelsharp_amd import native, workloads
     past = 2047
@@ -623,16 +627,21 @@ def decoder_layer(args):
     g = graph_of(lambda st: [lay.stage(r, n, st) for r in range(copies) for n in LayerRotation.STAGES])
     ms = time_graph(g, max(4, math.ceil(200 / copies)), 2) / copies
     del g
+    g = graph_of(lambda st: [lay.stage(r, n, st) for r in range(copies) for n in LayerRotation.UNFUSED])
+    ms_unfused = time_graph(g, max(4, math.ceil(200 / copies)), 2) / copies
+    del g
     stages = {}
-    for n in LayerRotation.STAGES:
+    for n in dict.fromkeys(LayerRotation.STAGES + LayerRotation.UNFUSED):
         gs = graph_of(lambda st, n=n: [lay.stage(r, n, st) for r in range(copies)])
         stages[n] = round(time_graph(gs, max(4, math.ceil(200 / copies)), 2) / copies * 1e3, 3)
         del gs
     finite = bool(torch.isfinite(lay.x[0]).all())
-    log(f"decoder layer step (past {past}): {ms * 1e3:.2f} us; stages {stages}; finite output {finite}")
+    log(f"decoder layer step (past {past}): {ms * 1e3:.2f} us ({ms_unfused * 1e3:.2f} us with gate+up and "
+        f"SiLU-Mul apart); stages {stages}; finite output {finite}")
     out = {"workload": "7B decoder layer at decode, M=1, past 2047, device-resident (hidden 3584, 28/4 heads of "
                        "128, intermediate 18944, bs 32 zp)", "rotating_copies": copies,
-           "us_per_step": round(ms * 1e3, 3), "stage_us": stages,
+           "us_per_step": round(ms * 1e3, 3), "stages": list(LayerRotation.STAGES),
+           "us_per_step_gate_up_and_silu_apart": round(ms_unfused * 1e3, 3), "stage_us": stages,
            "bytes_per_step": per_copy, "GBs": round(per_copy / (ms * 1e-3) / 1e9, 1), "finite": finite}
     lay.close()
     del lay

@@ -198,6 +198,24 @@ int ms_hip_nbits_device_error(void* handle);
 int ms_hip_nbits_gemm_dev_batch(void* const* handles, const float* const* dA,
                                 float* const* dY, int count, int M, void* stream);
 
+/* The MLP's gate and up projections of one input and their SiLU-gated product in one
+ * call: H = (G * (1 / (1 + exp(-G)))) * U with G = A W_gate^T, U = A W_up^T, the
+ * product the reference computes with two MatMulNBits nodes and Sigmoid -> Mul -> Mul
+ * (MatMulNBitsKernel.cs:77-265, Activations/SigmoidKernel.cs:13-22, the elementwise Mul),
+ * with the same roundings as ms_hip_silu_mul. No single counterpart in the reference:
+ * for a decode step (M = 1, both 4-bit with the fast layouts, K and N equal) it is one
+ * launch whose workgroups compute the same rows of both projections and store only H,
+ * bit-identical to the grouped gate+up launch of ms_hip_nbits_gemm_dev_batch followed
+ * by ms_hip_silu_mul; otherwise it runs those steps, with U in the gate handle's
+ * workspace (which may grow: not under stream capture before a first eager call). The
+ * handles must share K, N and the device (MS_HIP_ERR_INVALID otherwise). */
+int ms_hip_nbits_gemm_dev_swiglu(void* gate_handle, void* up_handle, const float* dA, float* dH,
+                                 int M, void* stream);
+/* Whether ms_hip_nbits_gemm_dev_swiglu with these arguments is the single fused launch
+ * (*fused = 1, with its grid and block) or the three-step form (*fused = 0). */
+int ms_hip_nbits_swiglu_launch_info(void* gate_handle, void* up_handle, const float* dA, int M,
+                                    int* fused, int* grid, int* block);
+
 /* One-shot form with the exact signature semantics of ms_qgemm_nbits
  * (native/ms_kernels.h:42-44): uploads, computes, downloads, frees. */
 int ms_hip_qgemm_nbits(const float* a, const uint8_t* bq, const float* scales,

@@ -69,35 +69,45 @@ __device__ __forceinline__ T op_field(int oi, T v0, T v1, T v2, T v3)
     return oi == 0 ? v0 : oi == 1 ? v1 : oi == 2 ? v2 : v3;
 }
 
-template <int M, int G, int KW, int U, int L, int WAVES, int RL, int NB>
+// SW (SwiGLU): ops 0 and 1 are the gate and up projections of one input (same N); the first
+// half of the row-waves computes gate rows, the second half the same rows of up, and the
+// epilogue stores H = (g * (1 / (1 + exp(-g)))) * u into op 1's output (the SiLU-Mul of
+// silu_mul_kernel, with its roundings), so the gate and up rows never leave the workgroup.
+template <int M, int G, int KW, int U, int L, int WAVES, int RL, int NB, bool SW = false>
 __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
 {
     static_assert(NB >= 2 && NB <= 4, "two to four load batches in flight");
     constexpr int R = kWave / G;
     constexpr int WR = WAVES / KW;
-    constexpr int ROWS0 = R * WR;      // rows of one layer; a lane owns RL rows, ROWS0 apart
-    constexpr int ROWS = RL * ROWS0;
+    static_assert(!SW || WR % 2 == 0, "SwiGLU splits the row-waves between gate and up");
+    constexpr int WRO = SW ? WR / 2 : WR;   // row-waves per op
+    constexpr int ROWS0 = R * WRO;     // rows of one layer; a lane owns RL rows, ROWS0 apart
+    constexpr int ROWS = RL * ROWS0;   // rows per workgroup (of each op with SW)
     constexpr int SPAN = G * KW;
     constexpr int BSPAN = SPAN >> L;   // blocks per step
     static_assert((BSPAN << L) == SPAN && (BSPAN & 1) == 0, "a step covers an even number of whole blocks");
     static_assert(WR * KW == WAVES, "KW must divide WAVES");
     extern __shared__ float4 lds_a4[];  // [M][C][kChunkStride4]
-    __shared__ float red[KW > 1 ? KW : 1][ROWS][M];
+    __shared__ float red[KW > 1 ? KW : 1][(SW ? 2 : 1) * ROWS][M];
+    __shared__ float swx[SW ? ROWS : 1][M];   // SW: the gate rows, handed to the up waves
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int g = lane % G, r = lane / G;
     const int wk = wave % KW, wr = wave / KW;
-    const int rl = wr * R + r;
+    const int rl = (SW ? wr % WRO : wr) * R + r;
     const int bid = blockIdx.x;
-    const int oi = (p.nops > 1 && bid >= p.op[1].first) + (p.nops > 2 && bid >= p.op[2].first) +
-                   (p.nops > 3 && bid >= p.op[3].first);
+    // The op is uniform over a wave (per workgroup without SW, per wave with it): read
+    // through the first lane so its buffer descriptors stay scalar.
+    const int oi = SW ? __builtin_amdgcn_readfirstlane(wr / WRO)
+                      : (p.nops > 1 && bid >= p.op[1].first) + (p.nops > 2 && bid >= p.op[2].first) +
+                            (p.nops > 3 && bid >= p.op[3].first);
     const uint8_t* const ob = op_field(oi, p.op[0].b, p.op[1].b, p.op[2].b, p.op[3].b);
     const float* const osc = op_field(oi, p.op[0].scales, p.op[1].scales, p.op[2].scales, p.op[3].scales);
     const uint8_t* const ozp = op_field(oi, p.op[0].zp, p.op[1].zp, p.op[2].zp, p.op[3].zp);
     float* const oy = op_field(oi, p.op[0].y, p.op[1].y, p.op[2].y, p.op[3].y);
     const int N = op_field(oi, p.op[0].N, p.op[1].N, p.op[2].N, p.op[3].N);
-    const int first = op_field(oi, p.op[0].first, p.op[1].first, p.op[2].first, p.op[3].first);
+    const int first = SW ? 0 : op_field(oi, p.op[0].first, p.op[1].first, p.op[2].first, p.op[3].first);
     // Row slot rl + j * ROWS0 of this workgroup is row n0 + j * ROWS0; slots past N idle.
     const int n0 = (bid - first) * ROWS + rl;
     bool vrow[RL];
@@ -260,12 +270,13 @@ steps_done:
 #pragma unroll
         for (int m = 0; m < M; ++m) acc[j][m] = group_sum_to_last<G>(acc[j][m]);
     }
+    const int ro = SW ? oi * ROWS : 0;   // this op's rows in red
     if constexpr (KW > 1) {
         if (g == G - 1) {
 #pragma unroll
             for (int j = 0; j < RL; ++j) {
 #pragma unroll
-                for (int m = 0; m < M; ++m) red[wk][j * ROWS0 + rl][m] = acc[j][m];
+                for (int m = 0; m < M; ++m) red[wk][ro + j * ROWS0 + rl][m] = acc[j][m];
             }
         }
         __syncthreads();
@@ -274,13 +285,38 @@ steps_done:
             for (int j = 0; j < RL; ++j) {
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
-                    float s = red[0][j * ROWS0 + rl][m];
+                    float s = red[0][ro + j * ROWS0 + rl][m];
 #pragma unroll
-                    for (int w = 1; w < KW; ++w) s += red[w][j * ROWS0 + rl][m];
+                    for (int w = 1; w < KW; ++w) s += red[w][ro + j * ROWS0 + rl][m];
                     acc[j][m] = s;
                 }
             }
         }
+    }
+    if constexpr (SW) {
+        // the gate rows to LDS; the up waves then store (g * sigmoid(g)) * u
+        if (oi == 0 && wk == 0 && g == G - 1) {
+#pragma unroll
+            for (int j = 0; j < RL; ++j) {
+#pragma unroll
+                for (int m = 0; m < M; ++m) swx[j * ROWS0 + rl][m] = acc[j][m];
+            }
+        }
+        __syncthreads();
+        if (oi == 1 && wk == 0 && g == G - 1) {
+#pragma unroll
+            for (int j = 0; j < RL; ++j) {
+                if (vrow[j]) {
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        const float x = swx[j * ROWS0 + rl][m];
+                        const float sg = 1.0f / (1.0f + expf(-x));
+                        oy[(int64_t)m * N + n0 + j * ROWS0] = (x * sg) * acc[j][m];
+                    }
+                }
+            }
+        }
+        return;
     }
     if (wk == 0 && g == G - 1) {
 #pragma unroll

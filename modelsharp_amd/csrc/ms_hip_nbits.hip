@@ -507,6 +507,28 @@ const std::array<GemvFn, kNumGemvConfigs> kGemvTable[kGemvMaxM][2] = {
 };
 std::atomic<bool> g_gemv_lds_raised[kGemvMaxM][2][kNumGemvConfigs];
 
+// The SwiGLU form of gemv_w4 (gate and up of one input, their SiLU-Mul stored), M = 1:
+// [L slot][config], null for configs whose row-waves do not split in two.
+template <int L, size_t I>
+constexpr GemvFn gemv_sw_fn_at()
+{
+    constexpr GemvConfig c = kGemvConfigs[I];
+    if constexpr ((c.waves / c.KW) % 2 == 0)
+        return gemv_w4_kernel<1, c.G, c.KW, c.U, L, c.waves, c.RL, c.NB, true>;
+    else
+        return nullptr;
+}
+template <int L, size_t... I>
+constexpr std::array<GemvFn, sizeof...(I)> gemv_sw_row(std::index_sequence<I...>)
+{
+    return {gemv_sw_fn_at<L, I>()...};
+}
+const std::array<GemvFn, kNumGemvConfigs> kGemvSwTable[2] = {
+    gemv_sw_row<0>(std::make_index_sequence<kNumGemvConfigs>{}),
+    gemv_sw_row<2>(std::make_index_sequence<kNumGemvConfigs>{}),
+};
+std::atomic<bool> g_gemv_sw_lds_raised[2][kNumGemvConfigs];
+
 // Output rows of one gemv_w4 workgroup.
 constexpr int gemv_rows(const GemvConfig& c) { return (kWave / c.G) * (c.waves / c.KW) * c.RL; }
 
@@ -612,6 +634,57 @@ int launch_gemv_group(const GemvMember* mem, int n, const float* dA, int M, int 
     p.nb = w0.nb;
     p.zrb = w0.zrb;
     hipLaunchKernelGGL(fn, dim3(first), dim3(c.waves * kWave), lds, stream, p);
+    MS_HIP_CHECK(hipGetLastError());
+    return MS_HIP_OK;
+}
+
+bool gemv_groupable(const Weights& a, const Weights& b);
+
+// The fused SwiGLU launch: M = 1, gate and up groupable on gemv_w4 with the same N, and the
+// config the grouped launch of the two would take splits its row-waves in two. *ci
+// receives that config.
+bool swiglu_fused_config(const Weights& wg, const Weights& wu, const float* dA, int M, int* ci)
+{
+    if (M != 1 || !dA || (reinterpret_cast<uintptr_t>(dA) & 15) || !gemv_groupable(wg, wu) || wg.N != wu.N)
+        return false;
+    const int c = pick_gemv_config(wg, knobs_of(wg), 1, 2 * wg.N);
+    if (c < 0 || !kGemvSwTable[l_slot(wg)][c]) return false;
+    *ci = c;
+    return true;
+}
+
+int launch_gemv_swiglu(const Weights& wg, const Weights& wu, const float* dA, float* dH, int ci, hipStream_t stream)
+{
+    const GemvConfig& c = kGemvConfigs[ci];
+    const int ls = l_slot(wg);
+    GemvFn fn = kGemvSwTable[ls][ci];
+    const int rows = gemv_rows(c) / 2;   // of each projection per workgroup
+    const size_t lds = (size_t)(wg.K / 32) * kChunkStride4 * 16;
+    if (lds > 64 * 1024 && !g_gemv_sw_lds_raised[ls][ci].load()) {
+        MS_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        g_gemv_sw_lds_raised[ls][ci].store(true);
+    }
+    const int grid = (wg.N + rows - 1) / rows;
+    GemvParams p;
+    const Weights* mem[2] = {&wg, &wu};
+    for (int i = 0; i < kGemvMaxOps; ++i) {
+        const Weights& m = *mem[std::min(i, 1)];
+        p.op[i].b = m.d_b;
+        p.op[i].scales = m.d_scales;
+        p.op[i].zp = m.has_zp ? m.d_zp : nullptr;
+        p.op[i].y = dH;
+        p.op[i].N = m.N;
+        p.op[i].first = 0;
+    }
+    p.nops = 2;
+    p.a = dA;
+    p.row_bytes = (int)wg.row_bytes;
+    p.K = wg.K;
+    p.C = wg.K / 32;
+    p.nb = wg.nb;
+    p.zrb = wg.zrb;
+    hipLaunchKernelGGL(fn, dim3(grid), dim3(c.waves * kWave), lds, stream, p);
     MS_HIP_CHECK(hipGetLastError());
     return MS_HIP_OK;
 }
@@ -2096,6 +2169,61 @@ int ms_hip_nbits_gemm_dev_batch(void* const* handles, const float* const* dA, fl
         }
         i += n;
     }
+    return MS_HIP_OK;
+}
+
+int ms_hip_nbits_gemm_dev_swiglu(void* gate_handle, void* up_handle, const float* dA, float* dH, int M,
+                                 void* stream)
+{
+    if (int st = gate()) return st;
+    Weights* wg = from_handle(gate_handle);
+    Weights* wu = from_handle(up_handle);
+    if (!wg || !wu) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
+    if (M < 0) return fail(MS_HIP_ERR_INVALID, "[ms_hip] M must be non-negative; got %d", M);
+    if (wg->K != wu->K || wg->N != wu->N || wg->device != wu->device)
+        return fail(MS_HIP_ERR_INVALID,
+                    "[ms_hip] swiglu: the gate and up projections must share K, N and the device (got K=%d/%d, N=%d/%d)",
+                    wg->K, wu->K, wg->N, wu->N);
+    if (M == 0) return MS_HIP_OK;
+    if (!dA || !dH || (reinterpret_cast<uintptr_t>(dH) & 3))
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] swiglu: null or misaligned activations or output");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (int st = take_device_error(*wg, s)) return st;
+    if (int st = take_device_error(*wu, s)) return st;
+    int ci = -1;
+    if (swiglu_fused_config(*wg, *wu, dA, M, &ci)) return launch_gemv_swiglu(*wg, *wu, dA, dH, ci, s);
+    // Otherwise the three steps: gate into H, up into the gate handle's workspace, then the
+    // SiLU-Mul in place (the same roundings as the fused form).
+    if (int st = enqueue_gemm(*wg, dA, dH, M, s)) return st;
+    Ws ws;
+    const int got = ensure_ws(*wg, (size_t)M * wg->N * sizeof(float), 0, s, &ws);
+    if (got < 0) return fail(MS_HIP_ERR_HIP, "[ms_hip] swiglu: workspace allocation failed");
+    if (got == 0)
+        return fail(MS_HIP_ERR_UNSUPPORTED,
+                    "[ms_hip] swiglu: this call needs the gate handle's workspace to grow, which a captured stream "
+                    "cannot do; make the call once outside capture first");
+    float* dU = reinterpret_cast<float*>(ws.data);
+    if (int st = enqueue_gemm(*wu, dA, dU, M, s)) return st;
+    const int64_t n = (int64_t)M * wg->N;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 8192)), dim3(256), 0, s,
+                       dH, dU, dH, n);
+    MS_HIP_CHECK(hipGetLastError());
+    return MS_HIP_OK;
+}
+
+int ms_hip_nbits_swiglu_launch_info(void* gate_handle, void* up_handle, const float* dA, int M, int* fused,
+                                    int* grid, int* block)
+{
+    Weights* wg = from_handle(gate_handle);
+    Weights* wu = from_handle(up_handle);
+    if (!wg || !wu) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
+    if (M <= 0) return fail(MS_HIP_ERR_INVALID, "[ms_hip] M must be positive; got %d", M);
+    int ci = -1;
+    const bool f = wg->K == wu->K && swiglu_fused_config(*wg, *wu, dA, M, &ci);
+    const int rows = f ? gemv_rows(kGemvConfigs[ci]) / 2 : 1;
+    if (fused) *fused = f ? 1 : 0;
+    if (grid) *grid = f ? (wg->N + rows - 1) / rows : 0;
+    if (block) *block = f ? kGemvConfigs[ci].waves * kWave : 0;
     return MS_HIP_OK;
 }
 

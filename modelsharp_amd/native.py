@@ -94,6 +94,8 @@ _PROTOTYPES = {
     "ms_hip_nbits_debug_set_counters": (_c_int, [_vp, _c_int, _c_int]),
     "ms_hip_nbits_launch_info": (_c_int, [_vp, _c_int, _ip, _ip, _ip, _ip]),
     "ms_hip_nbits_batch_launch_info": (_c_int, [_vp, _vp, _c_int, _c_int, _ip, _ip, _ip, _ip, _ip]),
+    "ms_hip_nbits_gemm_dev_swiglu": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _vp]),
+    "ms_hip_nbits_swiglu_launch_info": (_c_int, [_vp, _vp, _vp, _c_int, _ip, _ip, _ip]),
 }
 
 _lock = threading.Lock()
@@ -336,6 +338,19 @@ def batch_launch_info(weights: list, dA: list[int], M: int) -> dict:
                                                  ctypes.byref(gr), ctypes.byref(bl)))
     return {"calls": c.value, "kernel": KERNEL_NAMES[k.value], "lanes_per_row": g.value, "grid": gr.value,
             "block": bl.value}
+
+
+def gemm_dev_swiglu(gate, up, dA: int, dH: int, M: int, stream: int | None = None) -> None:
+    """H = SiLU(A W_gate^T) * (A W_up^T) on device pointers (one launch at M = 1)."""
+    check(load().ms_hip_nbits_gemm_dev_swiglu(gate.handle, up.handle, _vp(dA), _vp(dH), int(M), _vp(stream or 0)))
+
+
+def swiglu_launch_info(gate, up, dA: int, M: int) -> dict:
+    """Whether gemm_dev_swiglu with these arguments is the single fused launch, and its shape."""
+    f, g, b = (ctypes.c_int() for _ in range(3))
+    check(load().ms_hip_nbits_swiglu_launch_info(gate.handle, up.handle, _vp(dA), int(M), ctypes.byref(f),
+                                                  ctypes.byref(g), ctypes.byref(b)))
+    return {"fused": bool(f.value), "grid": g.value, "block": b.value}
 
 
 def set_gemv_lanes(lanes: int) -> None:

@@ -100,6 +100,89 @@ def test_elementwise(gpu):
     assert torch.equal(y, y2)
 
 
+# ---- gate + up + SiLU-Mul in one call (ms_hip_nbits_gemm_dev_swiglu) --------------------
+SWIGLU_OPS = [workloads.Op("7b_gate", 3584, 18944, 32, True, 0.001, 0.01),      # the 7B layer's MLP
+              workloads.Op("qwen_gate", 896, 4864, 32, True, 0.002, 0.02),
+              workloads.Op("llama_bs128", 4096, 11008, 128, False),               # block size 128, no zp
+              workloads.Op("ragged", 1024, 1000, 32, True)]                       # N not a multiple of the tile
+
+
+def _swiglu_handles(op, seed):
+    wg = native.NBitsWeights(*workloads.make_weights(op, seed), op.N, op.K, op.bits, op.block_size)
+    wu = native.NBitsWeights(*workloads.make_weights(op, seed + 1), op.N, op.K, op.bits, op.block_size)
+    return wg, wu
+
+
+@pytest.mark.parametrize("op", SWIGLU_OPS, ids=lambda o: o.name)
+def test_swiglu_fused_decode_equals_grouped_then_silu(gpu, op):
+    """At M = 1 the fused launch (the same rows of gate and up in one workgroup, H stored
+    directly) is bit-identical to the grouped gate+up launch followed by ms_hip_silu_mul,
+    and within the GEMV bar of the oracle's gate and up composed with SiLU-Mul in float64."""
+    import torch
+    wg, wu = _swiglu_handles(op, 41)
+    a = workloads.make_activations(1, op.K, seed=42)
+    da = dev(a)
+    info = native.swiglu_launch_info(wg, wu, da.data_ptr(), 1)
+    log(f"swiglu {op.name} K={op.K} N={op.N}: {info}")
+    assert info["fused"]
+    h = torch.full((1, op.N), float("nan"), device="cuda")
+    native.gemm_dev_swiglu(wg, wu, da.data_ptr(), h.data_ptr(), 1)
+    g, u, h2 = (torch.empty((1, op.N), device="cuda") for _ in range(3))
+    native.gemm_dev_batch([wg, wu], [da.data_ptr()] * 2, [g.data_ptr(), u.data_ptr()], 1)
+    native.silu_mul(g.data_ptr(), u.data_ptr(), h2.data_ptr(), op.N)
+    torch.cuda.synchronize()
+    assert torch.equal(h, h2)
+    bg, sg, zg = workloads.make_weights(op, 41)
+    bu, su, zu = workloads.make_weights(op, 42)
+    gr = oracle.matmul_nbits(a, bg, sg, zg, op.N, op.K, op.bits, op.block_size).astype(np.float64)
+    ur = oracle.matmul_nbits(a, bu, su, zu, op.N, op.K, op.bits, op.block_size).astype(np.float64)
+    hr = gr / (1 + np.exp(-gr)) * ur
+    got = host(h).astype(np.float64)
+    rel = np.linalg.norm(got - hr) / np.linalg.norm(hr)
+    log(f"  relative Frobenius error against the oracle {rel:.2e}")
+    assert rel <= 1e-5
+    wg.close()
+    wu.close()
+
+
+@pytest.mark.parametrize("M", [0, 2, 4, 17, 130])
+def test_swiglu_other_forms_equal_separate_calls(gpu, M):
+    """Other M (and block size 64, which the decode GEMV does not take) run the three steps
+    (gate into H, up into the gate handle's workspace, SiLU-Mul in place): bit-identical to
+    the separate calls."""
+    import torch
+    for op in (workloads.Op("g32", 1024, 1000, 32, True), workloads.Op("g64", 1024, 600, 64, True)):
+        wg, wu = _swiglu_handles(op, 51 + M)
+        a = workloads.make_activations(max(M, 1), op.K, seed=M + 3, kind="rmsnorm")[:M]
+        da = dev(a) if M else torch.empty((0, op.K), device="cuda")
+        if M:
+            assert not native.swiglu_launch_info(wg, wu, da.data_ptr(), M)["fused"]
+        h = torch.full((M, op.N), float("nan"), device="cuda")
+        native.gemm_dev_swiglu(wg, wu, da.data_ptr(), h.data_ptr(), M)
+        if M:
+            g, u, h2 = (torch.empty((M, op.N), device="cuda") for _ in range(3))
+            wg.gemm_dev(da.data_ptr(), g.data_ptr(), M)
+            wu.gemm_dev(da.data_ptr(), u.data_ptr(), M)
+            native.silu_mul(g.data_ptr(), u.data_ptr(), h2.data_ptr(), M * op.N)
+            torch.cuda.synchronize()
+            assert torch.equal(h, h2), (op.name, M)
+        wg.close()
+        wu.close()
+
+
+def test_swiglu_rejects_mismatched_projections(gpu):
+    import torch
+    wg = native.NBitsWeights(*workloads.make_weights(workloads.Op("a", 512, 64, 32, True), 1), 64, 512, 4, 32)
+    wu = native.NBitsWeights(*workloads.make_weights(workloads.Op("b", 512, 96, 32, True), 2), 96, 512, 4, 32)
+    a = dev(workloads.make_activations(1, 512, seed=3))
+    h = torch.zeros((1, 96), device="cuda")
+    with pytest.raises(native.HipError) as e:
+        native.gemm_dev_swiglu(wg, wu, a.data_ptr(), h.data_ptr(), 1)
+    assert e.value.status == native.MS_HIP_ERR_INVALID and "share K, N" in e.value.message
+    wg.close()
+    wu.close()
+
+
 # ---- GroupQueryAttention ---------------------------------------------------------------------
 from test_oracle_decoder import GQA_CASES, make_case   # noqa: E402
 
