@@ -12,6 +12,8 @@ MatMulNBits to the next:
   Sigmoid, Mul, Add                 Activations/SigmoidKernel.cs, the elementwise Mul/Add
                                     (equal shapes: the residual stream and the MLP gate)
   SiluMul                           Sigmoid -> Mul -> Mul fused by fuse_silu_mul()
+  GateUpSiluMul                     MatMulNBits(x, gate), MatMulNBits(x, up) -> SiluMul, fused by
+                                    fuse_gate_up_silu()
 
 Activations are torch tensors on the device (host arrays are uploaded once per call);
 initializers (norm weights, rotary caches) are uploaded once and kept. Nothing here
@@ -244,6 +246,102 @@ def fuse_silu_mul(graph: ModelGraph) -> int:
     return fused
 
 
+def fuse_gate_up_silu(graph: ModelGraph) -> int:
+    """Rewrites MatMulNBits(x, W_gate) -> g, MatMulNBits(x, W_up) -> u, SiluMul(g, u) -> h
+    into one GateUpSiluMul(x, B_g, scales_g, zp_g, B_u, scales_u, zp_u) -> h node when g and
+    u feed nothing else and the two projections share their attributes and carry no
+    g_idx or bias inputs (run fuse_silu_mul first). Returns the number of patterns fused."""
+    uses: dict[str, int] = {}
+    for n in graph.nodes:
+        for i in n.inputs:
+            uses[i] = uses.get(i, 0) + 1
+    for o in graph.outputs:
+        uses[o] = uses.get(o, 0) + 1
+    producer = {o: n for n in graph.nodes for o in n.outputs}
+    fused = 0
+    drop: set[int] = set()
+    replace: dict[int, GraphNode] = {}
+
+    def plain(n):
+        return (n is not None and n.op_type == "MatMulNBits" and id(n) not in drop and len(n.outputs) == 1
+                and not any(n.inputs[4:]))
+
+    for sm in graph.nodes:
+        if sm.op_type != "SiluMul" or len(sm.inputs) != 2:
+            continue
+        gn, un = producer.get(sm.inputs[0]), producer.get(sm.inputs[1])
+        if not (plain(gn) and plain(un)) or gn is un or gn.inputs[0] != un.inputs[0]:
+            continue
+        if uses.get(sm.inputs[0], 0) != 1 or uses.get(sm.inputs[1], 0) != 1:
+            continue
+        keys = ("N", "K", "bits", "block_size")
+        if any(gn.attributes.get(k) != un.attributes.get(k) for k in keys):
+            continue
+        tri = lambda n: (list(n.inputs[1:4]) + ["", "", ""])[:3]
+        drop.update({id(gn), id(un)})
+        replace[id(sm)] = GraphNode("GateUpSiluMul", sm.name + "/gate_up_silu",
+                                    [gn.inputs[0]] + tri(gn) + tri(un), list(sm.outputs), dict(gn.attributes))
+        fused += 1
+    graph.nodes = [replace.get(id(n), n) for n in graph.nodes if id(n) not in drop]
+    return fused
+
+
+class HipGateUpSiluMulKernel(IKernel):
+    """GateUpSiluMul(x, gate triple, up triple) = SiluMul(MatMulNBits(x, gate), MatMulNBits(x,
+    up)) (the nodes fuse_gate_up_silu replaces): both projections validated as
+    MatMulNBits nodes (MatMulNBitsKernel.cs:79-161), then one ms_hip_nbits_gemm_dev_swiglu
+    call on device activations (one launch at M = 1, bit-identical to the three kernels);
+    other inputs (host arrays, fp16 activations, the W4A8 opt-in) run the three kernels."""
+    op_type = "GateUpSiluMul"
+
+    def __init__(self, matmul=None):
+        from .hip_kernel import HipMatMulNBitsKernel
+        self._mm = matmul if matmul is not None else HipMatMulNBitsKernel()
+        self._silu = HipSiluMulKernel()
+
+    def close(self):
+        self._mm.close()
+
+    def preload(self, graph: ModelGraph) -> int:
+        """Load-time upload of the fused nodes' two weight triples, as
+        HipMatMulNBitsKernel.preload does for MatMulNBits nodes (file-backed initializers
+        streamed from their slices). Returns the number of handles created."""
+        pseudo = []
+        for n in graph.nodes:
+            if n.op_type == self.op_type:
+                pseudo += [GraphNode("MatMulNBits", n.name + "/gate", [n.inputs[0]] + list(n.inputs[1:4]),
+                                     [n.name + "/g"], n.attributes),
+                           GraphNode("MatMulNBits", n.name + "/up", [n.inputs[0]] + list(n.inputs[4:7]),
+                                     [n.name + "/u"], n.attributes)]
+        g = ModelGraph(pseudo, graph.initializers)
+        g.sources = getattr(graph, "sources", {})
+        return self._mm.preload(g)
+
+    def execute(self, node, ctx):
+        x = node.inputs[0]
+        gnode = GraphNode("MatMulNBits", node.name + "/gate", [x] + list(node.inputs[1:4]), [node.name + "/g"],
+                          node.attributes)
+        unode = GraphNode("MatMulNBits", node.name + "/up", [x] + list(node.inputs[4:7]), [node.name + "/u"],
+                          node.attributes)
+        a, bg, sg, zg, N, K, bits, bs = self._mm._validate(gnode, ctx)
+        _, bu, su, zu, _, _, _, _ = self._mm._validate(unode, ctx)
+        torch = _torch()
+        if not isinstance(a, np.ndarray) and a.dtype == torch.float32 and not self._mm.w4a8:
+            wg = self._mm._weights(gnode, bg, sg, zg, N, K, bits, bs)
+            wu = self._mm._weights(unode, bu, su, zu, N, K, bits, bs)
+            lead = tuple(a.shape[:-1])
+            M = int(np.prod(lead)) if lead else 1
+            a2 = a.reshape(M, K).contiguous()
+            h = torch.empty(lead + (N,), dtype=torch.float32, device=a.device)
+            native.gemm_dev_swiglu(wg, wu, a2.data_ptr(), h.data_ptr(), M, _stream(a2))
+            ctx.set(node.outputs[0], h)
+            return
+        self._mm.execute(gnode, ctx)
+        self._mm.execute(unode, ctx)
+        self._silu.execute(GraphNode("SiluMul", node.name + "/silu_mul", [gnode.outputs[0], unode.outputs[0]],
+                                     list(node.outputs)), ctx)
+
+
 @dataclasses.dataclass
 class _Cache:
     k: object
@@ -392,6 +490,6 @@ def register_decoder_kernels(registry: KernelRegistry) -> KernelRegistry:
     wins, KernelRegistry.cs:20-24)."""
     for k in (HipSimplifiedLayerNormalizationKernel(), HipSkipSimplifiedLayerNormalizationKernel(),
               HipGroupQueryAttentionKernel(), HipAddKernel(), HipMulKernel(), HipSigmoidKernel(),
-              HipSiluMulKernel()):
+              HipSiluMulKernel(), HipGateUpSiluMulKernel()):
         registry.register(k)
     return registry

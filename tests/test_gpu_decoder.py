@@ -13,7 +13,8 @@ import pytest
 
 import oracle
 from modelsharp_amd import native, workloads
-from modelsharp_amd.decoder_kernels import (HipGroupQueryAttentionKernel, fuse_silu_mul, register_decoder_kernels)
+from modelsharp_amd.decoder_kernels import (HipGroupQueryAttentionKernel, fuse_gate_up_silu, fuse_silu_mul,
+                                            register_decoder_kernels)
 from modelsharp_amd.graph import Engine, GraphContext, GraphNode, KernelRegistry, ModelGraph
 from modelsharp_amd.hip_kernel import register_kernels
 
@@ -457,6 +458,7 @@ def test_decoder_layer_end_to_end(gpu, fused):
     g = layer_graph(hid, H, KH, D, inter, bs, seed=1)
     if fused:
         assert fuse_silu_mul(g) == 1 and [n.op_type for n in g.nodes].count("SiluMul") == 1
+        assert fuse_gate_up_silu(g) == 1 and [n.op_type for n in g.nodes].count("GateUpSiluMul") == 1
     reg = register_decoder_kernels(register_kernels(KernelRegistry()))
     eng = Engine(g, reg)
     r = np.random.default_rng(2)

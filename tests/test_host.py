@@ -392,6 +392,37 @@ def test_fuse_silu_mul_patterns():
     assert fuse_silu_mul(g) == 0
 
 
+def test_fuse_gate_up_silu_patterns():
+    from modelsharp_amd.decoder_kernels import fuse_gate_up_silu, fuse_silu_mul
+    at = {"N": 8, "K": 4, "bits": 4, "block_size": 32}
+    mk = lambda: ModelGraph(nodes=[   # noqa: E731
+        GraphNode("MatMulNBits", "gate", ["n", "Bg", "Sg", "Zg"], ["g"], dict(at)),
+        GraphNode("MatMulNBits", "up", ["n", "Bu", "Su"], ["u"], dict(at)),
+        GraphNode("Sigmoid", "sig", ["g"], ["s"]),
+        GraphNode("Mul", "m1", ["g", "s"], ["a"]),
+        GraphNode("Mul", "m2", ["a", "u"], ["h"]),
+        GraphNode("MatMulNBits", "down", ["h", "Bd", "Sd"], ["y"], dict(at)),
+    ], initializers={}, inputs=["n"], outputs=["y"])
+    g = mk()
+    assert fuse_silu_mul(g) == 1 and fuse_gate_up_silu(g) == 1
+    assert [(n.op_type, n.inputs, n.outputs) for n in g.nodes] == [
+        ("GateUpSiluMul", ["n", "Bg", "Sg", "Zg", "Bu", "Su", ""], ["h"]),
+        ("MatMulNBits", ["h", "Bd", "Sd"], ["y"])]
+    assert g.nodes[0].attributes == at
+    g = mk()
+    g.outputs.append("u")   # the up projection is used elsewhere: no fusion
+    assert fuse_silu_mul(g) == 1 and fuse_gate_up_silu(g) == 0
+    g = mk()
+    g.nodes[1].inputs[0] = "other"   # gate and up of different inputs
+    assert fuse_silu_mul(g) == 1 and fuse_gate_up_silu(g) == 0
+    g = mk()
+    g.nodes[1].attributes["N"] = 16   # different shapes
+    assert fuse_silu_mul(g) == 1 and fuse_gate_up_silu(g) == 0
+    g = mk()
+    g.nodes[0].inputs += ["g_idx"]   # a g_idx input is not folded
+    assert fuse_silu_mul(g) == 1 and fuse_gate_up_silu(g) == 0
+
+
 def test_gqa_kernel_validation_messages():
     from modelsharp_amd.decoder_kernels import HipGroupQueryAttentionKernel
     k = HipGroupQueryAttentionKernel()
