@@ -26,13 +26,14 @@ namespace msnb {
 
 constexpr int kNormThreads = 256;
 
-// Sum over the workgroup in a fixed order: wave sums by xor butterflies, then the four
-// wave sums in index order.
+// Sum over the workgroup in a fixed order: each wave's sum by a DPP scan (one VALU op per
+// level, the sum in lane 63), then the four wave sums in index order. The closing barrier
+// lets a caller reuse red.
 __device__ __forceinline__ float block_sum256(float v, float* red)
 {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    v = group_sum_to_last<64>(v);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) red[wave] = v;
+    if (lane == 63) red[wave] = v;
     __syncthreads();
     const float s = ((red[0] + red[1]) + red[2]) + red[3];
     __syncthreads();
@@ -75,10 +76,13 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* x, c
         const float4* x4 = reinterpret_cast<const float4*>(x + off);
         float4 t[kNormRegs];
         float ss = 0.0f;
+        // the scale is loaded with x, before the reduction's barrier (one round trip to memory)
+        float4 sc[kNormRegs];
 #pragma unroll
         for (int u = 0; u < kNormRegs; ++u) {
             const int i = threadIdx.x + u * kNormThreads;
             t[u] = i < n4 ? x4[i] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+            sc[u] = i < n4 ? reinterpret_cast<const float4*>(scale)[i] : float4{0.0f, 0.0f, 0.0f, 0.0f};
         }
 #pragma unroll
         for (int u = 0; u < kNormRegs; ++u) ss = f4sq(t[u], ss);
@@ -88,7 +92,7 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* x, c
 #pragma unroll
         for (int u = 0; u < kNormRegs; ++u) {
             const int i = threadIdx.x + u * kNormThreads;
-            if (i < n4) y4[i] = f4norm(t[u], inv, reinterpret_cast<const float4*>(scale)[i]);
+            if (i < n4) y4[i] = f4norm(t[u], inv, sc[u]);
         }
         return;
     }
@@ -117,13 +121,15 @@ __global__ __launch_bounds__(kNormThreads) void skip_rmsnorm_kernel(
         const int n4 = norm >> 2;
         const float4* a4 = reinterpret_cast<const float4*>(input + off);
         const float4* b4 = reinterpret_cast<const float4*>(skip + off);
-        float4 t[kNormRegs];
+        float4 t[kNormRegs], gm[kNormRegs];
         float ss = 0.0f;
+        // gamma is loaded with the inputs, before the reduction's barrier (one round trip)
 #pragma unroll
         for (int u = 0; u < kNormRegs; ++u) {
             const int i = threadIdx.x + u * kNormThreads;
             t[u] = i < n4 ? f4add(a4[i], b4[i]) : float4{0.0f, 0.0f, 0.0f, 0.0f};
             if (bias && i < n4) t[u] = f4add(t[u], reinterpret_cast<const float4*>(bias)[i]);
+            gm[u] = i < n4 ? reinterpret_cast<const float4*>(gamma)[i] : float4{0.0f, 0.0f, 0.0f, 0.0f};
         }
 #pragma unroll
         for (int u = 0; u < kNormRegs; ++u) ss = f4sq(t[u], ss);
@@ -140,7 +146,7 @@ __global__ __launch_bounds__(kNormThreads) void skip_rmsnorm_kernel(
         for (int u = 0; u < kNormRegs; ++u) {
             const int i = threadIdx.x + u * kNormThreads;
             if (i < n4) {
-                float4 v = f4norm(t[u], inv, reinterpret_cast<const float4*>(gamma)[i]);
+                float4 v = f4norm(t[u], inv, gm[u]);
                 if (beta) v = f4add(v, reinterpret_cast<const float4*>(beta)[i]);
                 reinterpret_cast<float4*>(out + off)[i] = v;
             }
