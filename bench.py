@@ -530,6 +530,7 @@ class LayerRotation:
         self.cos, self.sin = torch.cos(ang).float().cuda(), torch.sin(ang).float().cuda()
         self.x = [dev(1, HID) for _ in range(copies)]
         self.resid = [dev(1, HID) for _ in range(copies)]
+        self.resid2 = [torch.empty(1, HID, device="cuda") for _ in range(copies)]   # the fused norms' sums
         e = lambda n: torch.empty(1, n, device="cuda")   # noqa: E731
         self.n1, self.q, self.k, self.v, self.attn, self.o = e(HID), e(HID), e(KH * D), e(KH * D), e(HID), e(HID)
         self.n2, self.gt, self.up, self.act, self.y = e(HID), e(self.INTER), e(self.INTER), e(self.INTER), e(HID)
@@ -568,9 +569,21 @@ class LayerRotation:
             native.gemm_dev_swiglu(h[4], h[5], self.n2.data_ptr(), self.act.data_ptr(), 1, stream)
         elif name == "down":
             h[6].gemm_dev(self.act.data_ptr(), self.x[r].data_ptr(), 1, stream)
+        elif name == "norm1_qkv":   # SkipRMSNorm computed in the q/k/v launch's staging
+            native.gemm_dev_skipnorm(h[0:3], self.x[r].data_ptr(), self.resid[r].data_ptr(), self.g1[r].data_ptr(),
+                                     eps, self.n1.data_ptr(), self.resid2[r].data_ptr(),
+                                     [self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr()], 1, stream)
+        elif name == "norm2_gate_up_silu":   # SkipRMSNorm, gate, up and SiLU-Mul in one launch
+            native.gemm_dev_skipnorm_swiglu(h[4], h[5], self.o.data_ptr(), self.resid2[r].data_ptr(),
+                                            self.g2[r].data_ptr(), eps, self.n2.data_ptr(), self.resid[r].data_ptr(),
+                                            self.act.data_ptr(), 1, stream)
 
-    STAGES = ("norm1", "qkv", "attention", "o", "norm2", "gate_up_silu", "down")
-    # the same step with gate+up and SiLU-Mul as two launches
+    # the norms in the launches of the projections that read them (the residual stream
+    # alternates between two buffers: a fused norm's sum may not overwrite its skip input)
+    STAGES = ("norm1_qkv", "attention", "o", "norm2_gate_up_silu", "down")
+    # the norms as launches of their own
+    NORMS_APART = ("norm1", "qkv", "attention", "o", "norm2", "gate_up_silu", "down")
+    # and gate+up and SiLU-Mul as two launches too
     UNFUSED = ("norm1", "qkv", "attention", "o", "norm2", "gate_up", "silu_mul", "down")
 
     def close(self):
@@ -627,20 +640,25 @@ def decoder_layer(args):
     g = graph_of(lambda st: [lay.stage(r, n, st) for r in range(copies) for n in LayerRotation.STAGES])
     ms = time_graph(g, max(4, math.ceil(200 / copies)), 2) / copies
     del g
+    g = graph_of(lambda st: [lay.stage(r, n, st) for r in range(copies) for n in LayerRotation.NORMS_APART])
+    ms_norms = time_graph(g, max(4, math.ceil(200 / copies)), 2) / copies
+    del g
     g = graph_of(lambda st: [lay.stage(r, n, st) for r in range(copies) for n in LayerRotation.UNFUSED])
     ms_unfused = time_graph(g, max(4, math.ceil(200 / copies)), 2) / copies
     del g
     stages = {}
-    for n in dict.fromkeys(LayerRotation.STAGES + LayerRotation.UNFUSED):
+    for n in dict.fromkeys(LayerRotation.STAGES + LayerRotation.NORMS_APART + LayerRotation.UNFUSED):
         gs = graph_of(lambda st, n=n: [lay.stage(r, n, st) for r in range(copies)])
         stages[n] = round(time_graph(gs, max(4, math.ceil(200 / copies)), 2) / copies * 1e3, 3)
         del gs
     finite = bool(torch.isfinite(lay.x[0]).all())
-    log(f"decoder layer step (past {past}): {ms * 1e3:.2f} us ({ms_unfused * 1e3:.2f} us with gate+up and "
-        f"SiLU-Mul apart); stages {stages}; finite output {finite}")
+    log(f"decoder layer step (past {past}): {ms * 1e3:.2f} us ({ms_norms * 1e3:.2f} us with the norms as launches "
+        f"of their own, {ms_unfused * 1e3:.2f} us with gate+up and SiLU-Mul apart too); stages {stages}; "
+        f"finite output {finite}")
     out = {"workload": "7B decoder layer at decode, M=1, past 2047, device-resident (hidden 3584, 28/4 heads of "
                        "128, intermediate 18944, bs 32 zp)", "rotating_copies": copies,
            "us_per_step": round(ms * 1e3, 3), "stages": list(LayerRotation.STAGES),
+           "us_per_step_norms_apart": round(ms_norms * 1e3, 3),
            "us_per_step_gate_up_and_silu_apart": round(ms_unfused * 1e3, 3), "stage_us": stages,
            "bytes_per_step": per_copy, "GBs": round(per_copy / (ms * 1e-3) / 1e9, 1), "finite": finite}
     lay.close()

@@ -216,6 +216,33 @@ int ms_hip_nbits_gemm_dev_swiglu(void* gate_handle, void* up_handle, const float
 int ms_hip_nbits_swiglu_launch_info(void* gate_handle, void* up_handle, const float* dA, int M,
                                     int* fused, int* grid, int* block);
 
+/* SkipSimplifiedLayerNormalization without beta or bias followed by the projections that
+ * read its output, in one call (SkipSimplifiedLayerNormalizationKernel.cs:29-86, then
+ * MatMulNBitsKernel.cs:77-265): T = X + Skip (M rows of K, K the handles' common K),
+ * Norm = (T * inv) * gamma with inv = 1 / sqrt(mean(T^2) + eps) per row, Y_i = Norm W_i^T.
+ * dSum (may be null) receives T, dNorm the normed rows; neither may overlap dX or dSkip
+ * (MS_HIP_ERR_INVALID). No single counterpart in the reference. For a decode step (M = 1,
+ * up to four 4-bit projections that ms_hip_nbits_gemm_dev_batch would group, 16-byte
+ * aligned norm buffers) it is one launch: every workgroup computes the norm in its staging
+ * and scales its sums by inv (Y = inv * (T gamma) W^T, the decode tolerance of the batch
+ * call); otherwise ms_hip_skip_rmsnorm, then ms_hip_nbits_gemm_dev_batch on dNorm. */
+int ms_hip_nbits_gemm_dev_skipnorm(void* const* handles, int count, const float* dX,
+                                   const float* dSkip, const float* dGamma, float eps,
+                                   float* dNorm, float* dSum, float* const* dY, int M,
+                                   void* stream);
+/* The same norm followed by ms_hip_nbits_gemm_dev_swiglu on its output: one launch where
+ * the SwiGLU call's fused form applies, else the norm and that call. */
+int ms_hip_nbits_gemm_dev_skipnorm_swiglu(void* gate_handle, void* up_handle, const float* dX,
+                                          const float* dSkip, const float* dGamma, float eps,
+                                          float* dNorm, float* dSum, float* dH, int M,
+                                          void* stream);
+/* Whether the call above (swiglu = 0: ms_hip_nbits_gemm_dev_skipnorm with `count`
+ * handles; 1: the SwiGLU form, handles = {gate, up}) with these buffers is the fused
+ * launch (*fused = 1, with its grid and block) or the norm and the projections apart. */
+int ms_hip_nbits_skipnorm_launch_info(void* const* handles, int count, int swiglu, const float* dX,
+                                      const float* dSkip, const float* dGamma, const float* dNorm,
+                                      const float* dSum, int M, int* fused, int* grid, int* block);
+
 /* One-shot form with the exact signature semantics of ms_qgemm_nbits
  * (native/ms_kernels.h:42-44): uploads, computes, downloads, frees. */
 int ms_hip_qgemm_nbits(const float* a, const uint8_t* bq, const float* scales,

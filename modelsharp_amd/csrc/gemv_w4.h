@@ -59,6 +59,15 @@ struct GemvParams {
     int K;
     int C;                   // K / 32 chunks per row
     int nb, zrb;
+    // NORM launches (M = 1): A = SkipRMSNorm(nx + nskip) * ngamma, computed by every workgroup
+    // from nx, nskip and ngamma; workgroup 0 writes nx + nskip to nsum (when not null) and
+    // the normed activations to nout.
+    const float* nx;
+    const float* nskip;
+    const float* ngamma;
+    float* nsum;
+    float* nout;
+    float neps;
 };
 
 // Uniform choice among the op table's entries (selects on a wave-uniform index, so the
@@ -73,9 +82,24 @@ __device__ __forceinline__ T op_field(int oi, T v0, T v1, T v2, T v3)
 // half of the row-waves computes gate rows, the second half the same rows of up, and the
 // epilogue stores H = (g * (1 / (1 + exp(-g)))) * u into op 1's output (the SiLU-Mul of
 // silu_mul_kernel, with its roundings), so the gate and up rows never leave the workgroup.
-template <int M, int G, int KW, int U, int L, int WAVES, int RL, int NB, bool SW = false>
+//
+// NORM (M = 1): the activations are SkipSimplifiedLayerNormalization's output, computed in
+// the workgroup's staging instead of read: t = x + skip, then A = (t * inv) * gamma with
+// inv = 1 / sqrt(sum t^2 / K + eps). Each workgroup stages t * gamma (two threads per
+// chunk, 16 values each; the host checks 2 C <= threads) and its share of sum t^2, and
+// applies inv to its sums before they are stored: y = inv * sum_k W_k (t_k gamma_k), the
+// same dot product in another order. The staging loads are consumed before the weight
+// stream is issued, so the stream's registers are not held beside them (issuing the first
+// weight batch ahead of the staging measured no faster: the 7B q+k+v with its norm 7.9 ->
+// 8.5 us). The staging reads three vectors where gemv_w4 reads one, which every workgroup
+// pays in L2 bandwidth: the 7B gate+up+SiLU launch with its norm takes 22.6 us against 19.9
+// without (the norm's own launch 4.1 us). Workgroup 0 also
+// writes t (the residual stream) and (t * inv) * gamma; neither may overlap x or skip,
+// which the other workgroups are still reading (checked by the host).
+template <int M, int G, int KW, int U, int L, int WAVES, int RL, int NB, bool SW = false, bool NORM = false>
 __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
 {
+    static_assert(!NORM || M == 1, "the fused norm serves one row of activations");
     static_assert(NB >= 2 && NB <= 4, "two to four load batches in flight");
     constexpr int R = kWave / G;
     constexpr int WR = WAVES / KW;
@@ -90,6 +114,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
     extern __shared__ float4 lds_a4[];  // [M][C][kChunkStride4]
     __shared__ float red[KW > 1 ? KW : 1][(SW ? 2 : 1) * ROWS][M];
     __shared__ float swx[SW ? ROWS : 1][M];   // SW: the gate rows, handed to the up waves
+    __shared__ float nred[NORM ? WAVES : 1];  // NORM: the waves' sums of t^2
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -129,12 +154,27 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
     const int am = idx / C, ac = idx - am * C;
     const int aoff = idx < na ? (am * p.K + ac * 32) * 4 : kOOB;
     float4 av[8];
-    // The chunk's 16-byte offsets ride in the scalar offset, so kOOB itself is never
-    // added to in int arithmetic (the hardware adds them as unsigned 32-bit values, and
-    // kOOB + 112 still lies past every buffer).
+    float4 xv[4], kv[4], gv[4];   // NORM: half chunk idx of x, skip and gamma
+    if constexpr (NORM) {
+        // Half chunk idx (values 16 idx .. 16 idx + 15) of x, skip and gamma, consumed (below)
+        // before the weight stream is issued.
+        const int ho = idx < 2 * C ? idx * 64 : kOOB;
+        const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(p.nx, p.K * 4), rk = buffer_rsrc(p.nskip, p.K * 4),
+                                     rg = buffer_rsrc(p.ngamma, p.K * 4);
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-        av[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ra, aoff, 16 * j, 0));
+        for (int j = 0; j < 4; ++j) {
+            xv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rx, ho, 16 * j, 0));
+            kv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, ho, 16 * j, 0));
+            gv[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rg, ho, 16 * j, 0));
+        }
+    } else {
+        // The chunk's 16-byte offsets ride in the scalar offset, so kOOB itself is never
+        // added to in int arithmetic (the hardware adds them as unsigned 32-bit values, and
+        // kOOB + 112 still lies past every buffer).
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            av[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ra, aoff, 16 * j, 0));
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- 2. weight stream: NB batches of U steps in flight ----------------------------
@@ -178,17 +218,51 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_w4_kernel(GemvParams p)
     // refilled with the steps NB U further on as soon as it has been reduced, so between
     // (NB - 1) U and NB U steps per lane are always in flight.
     Batch bt[NB];
+    if constexpr (NORM) {
+        // t = x + skip, t * gamma staged, the thread's share of sum t^2 (in the order of
+        // skip_rmsnorm_kernel's f4sq); then the weight batches.
+        const bool hv = idx < 2 * C;
+        float ss = 0.0f;
 #pragma unroll
-    for (int b = 0; b < NB; ++b) load(bt[b], b * U);
+        for (int j = 0; j < 4; ++j) {
+            const float4 t = float4{xv[j].x + kv[j].x, xv[j].y + kv[j].y, xv[j].z + kv[j].z, xv[j].w + kv[j].w};
+            ss = ss + t.x * t.x;
+            ss = ss + t.y * t.y;
+            ss = ss + t.z * t.z;
+            ss = ss + t.w * t.w;
+            if (bid == 0 && hv && p.nsum) reinterpret_cast<float4*>(p.nsum)[4 * idx + j] = t;
+            if (hv)
+                lds_a4[(idx >> 1) * kChunkStride4 + (idx & 1) * 4 + j] =
+                    stage_odd16(float4{t.x * gv[j].x, t.y * gv[j].y, t.z * gv[j].z, t.w * gv[j].w});
+        }
+        ss = group_sum_to_last<64>(ss);
+        if ((idx & (kWave - 1)) == kWave - 1) nred[idx / kWave] = ss;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) load(bt[b], b * U);
+    } else {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) load(bt[b], b * U);
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- 3. stage A: odd k divided by 16 (exact), matching 16 (q - zp) of the dequant ----
-    if (idx < na) {
-        float4* dst = &lds_a4[idx * kChunkStride4];
+    if constexpr (!NORM) {
+        if (idx < na) {
+            float4* dst = &lds_a4[idx * kChunkStride4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dst[j] = stage_odd16(av[j]);
+            for (int j = 0; j < 8; ++j) dst[j] = stage_odd16(av[j]);
+        }
     }
     __syncthreads();
+    // NORM: inv from the waves' sums of t^2 in wave order (every thread, the same value)
+    float inv = 1.0f;
+    if constexpr (NORM) {
+        float sst = nred[0];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) sst = sst + nred[w];
+        inv = 1.0f / __builtin_sqrtf(sst / (float)p.K + p.neps);
+    }
 
     float acc[RL][M];
 #pragma unroll
@@ -299,7 +373,7 @@ steps_done:
 #pragma unroll
             for (int j = 0; j < RL; ++j) {
 #pragma unroll
-                for (int m = 0; m < M; ++m) swx[j * ROWS0 + rl][m] = acc[j][m];
+                for (int m = 0; m < M; ++m) swx[j * ROWS0 + rl][m] = NORM ? acc[j][m] * inv : acc[j][m];
             }
         }
         __syncthreads();
@@ -311,19 +385,35 @@ steps_done:
                     for (int m = 0; m < M; ++m) {
                         const float x = swx[j * ROWS0 + rl][m];
                         const float sg = 1.0f / (1.0f + expf(-x));
-                        oy[(int64_t)m * N + n0 + j * ROWS0] = (x * sg) * acc[j][m];
+                        const float u = NORM ? acc[j][m] * inv : acc[j][m];
+                        oy[(int64_t)m * N + n0 + j * ROWS0] = (x * sg) * u;
                     }
                 }
             }
         }
-        return;
-    }
-    if (wk == 0 && g == G - 1) {
+    } else if (wk == 0 && g == G - 1) {
 #pragma unroll
         for (int j = 0; j < RL; ++j) {
             if (vrow[j]) {
 #pragma unroll
-                for (int m = 0; m < M; ++m) oy[(int64_t)m * N + n0 + j * ROWS0] = acc[j][m];
+                for (int m = 0; m < M; ++m)
+                    oy[(int64_t)m * N + n0 + j * ROWS0] = NORM ? acc[j][m] * inv : acc[j][m];
+            }
+        }
+    }
+    // NORM: workgroup 0 writes the normed activations, (t * inv) * gamma (the roundings of
+    // skip_rmsnorm_kernel), from x, skip and gamma read again.
+    if constexpr (NORM) {
+        if (bid == 0 && idx < 2 * C) {
+            const float4* x4 = reinterpret_cast<const float4*>(p.nx) + 4 * idx;
+            const float4* k4 = reinterpret_cast<const float4*>(p.nskip) + 4 * idx;
+            const float4* g4 = reinterpret_cast<const float4*>(p.ngamma) + 4 * idx;
+            float4* o4 = reinterpret_cast<float4*>(p.nout) + 4 * idx;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 x = x4[j], k = k4[j], gm = g4[j];
+                const float4 t = float4{x.x + k.x, x.y + k.y, x.z + k.z, x.w + k.w};
+                o4[j] = float4{(t.x * inv) * gm.x, (t.y * inv) * gm.y, (t.z * inv) * gm.z, (t.w * inv) * gm.w};
             }
         }
     }

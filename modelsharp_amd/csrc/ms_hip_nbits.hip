@@ -529,6 +529,39 @@ const std::array<GemvFn, kNumGemvConfigs> kGemvSwTable[2] = {
 };
 std::atomic<bool> g_gemv_sw_lds_raised[2][kNumGemvConfigs];
 
+// The same two forms with the SkipRMSNorm prologue (NORM, M = 1): [L slot][config].
+template <int L, size_t I, bool SW>
+constexpr GemvFn gemv_norm_fn_at()
+{
+    constexpr GemvConfig c = kGemvConfigs[I];
+    if constexpr (SW && (c.waves / c.KW) % 2 != 0)
+        return nullptr;
+    else
+        return gemv_w4_kernel<1, c.G, c.KW, c.U, L, c.waves, c.RL, c.NB, SW, true>;
+}
+template <int L, bool SW, size_t... I>
+constexpr std::array<GemvFn, sizeof...(I)> gemv_norm_row(std::index_sequence<I...>)
+{
+    return {gemv_norm_fn_at<L, I, SW>()...};
+}
+const std::array<GemvFn, kNumGemvConfigs> kGemvNormTable[2][2] = {   // [SW][L slot]
+    {gemv_norm_row<0, false>(std::make_index_sequence<kNumGemvConfigs>{}),
+     gemv_norm_row<2, false>(std::make_index_sequence<kNumGemvConfigs>{})},
+    {gemv_norm_row<0, true>(std::make_index_sequence<kNumGemvConfigs>{}),
+     gemv_norm_row<2, true>(std::make_index_sequence<kNumGemvConfigs>{})},
+};
+std::atomic<bool> g_gemv_norm_lds_raised[2][2][kNumGemvConfigs];
+
+// The SkipRMSNorm that a NORM launch computes in its staging.
+struct NormArgs {
+    const float* x;
+    const float* skip;
+    const float* gamma;
+    float* sum;   // x + skip, or nullptr
+    float* out;   // the normed activations
+    float eps;
+};
+
 // Output rows of one gemv_w4 workgroup.
 constexpr int gemv_rows(const GemvConfig& c) { return (kWave / c.G) * (c.waves / c.KW) * c.RL; }
 
@@ -601,20 +634,36 @@ struct GemvMember {
     float* dY;
 };
 
-int launch_gemv_group(const GemvMember* mem, int n, const float* dA, int M, int ci, hipStream_t stream)
+void set_norm(GemvParams& p, const NormArgs* na)
+{
+    p.nx = na ? na->x : nullptr;
+    p.nskip = na ? na->skip : nullptr;
+    p.ngamma = na ? na->gamma : nullptr;
+    p.nsum = na ? na->sum : nullptr;
+    p.nout = na ? na->out : nullptr;
+    p.neps = na ? na->eps : 0.0f;
+}
+
+// A NORM launch stages two half chunks per thread: 2 C <= threads.
+bool norm_fits(const GemvConfig& c, int K) { return 2 * (K / 32) <= c.waves * kWave; }
+
+int launch_gemv_group(const GemvMember* mem, int n, const float* dA, int M, int ci, hipStream_t stream,
+                      const NormArgs* na = nullptr)
 {
     const Weights& w0 = *mem[0].w;
     const GemvConfig& c = kGemvConfigs[ci];
     const int ls = l_slot(w0);
-    GemvFn fn = kGemvTable[M - 1][ls][ci];
+    GemvFn fn = na ? kGemvNormTable[0][ls][ci] : kGemvTable[M - 1][ls][ci];
     const int rows = gemv_rows(c);
     const size_t lds = (size_t)M * (w0.K / 32) * kChunkStride4 * 16;
-    if (lds > 64 * 1024 && !g_gemv_lds_raised[M - 1][ls][ci].load()) {
+    std::atomic<bool>& raised = na ? g_gemv_norm_lds_raised[0][ls][ci] : g_gemv_lds_raised[M - 1][ls][ci];
+    if (lds > 64 * 1024 && !raised.load()) {
         MS_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        g_gemv_lds_raised[M - 1][ls][ci].store(true);
+        raised.store(true);
     }
     GemvParams p;
+    set_norm(p, na);
     int first = 0;
     for (int i = 0; i < kGemvMaxOps; ++i) {
         const GemvMember& m = mem[std::min(i, n - 1)];   // unused entries repeat the last member
@@ -653,20 +702,23 @@ bool swiglu_fused_config(const Weights& wg, const Weights& wu, const float* dA, 
     return true;
 }
 
-int launch_gemv_swiglu(const Weights& wg, const Weights& wu, const float* dA, float* dH, int ci, hipStream_t stream)
+int launch_gemv_swiglu(const Weights& wg, const Weights& wu, const float* dA, float* dH, int ci, hipStream_t stream,
+                       const NormArgs* na = nullptr)
 {
     const GemvConfig& c = kGemvConfigs[ci];
     const int ls = l_slot(wg);
-    GemvFn fn = kGemvSwTable[ls][ci];
+    GemvFn fn = na ? kGemvNormTable[1][ls][ci] : kGemvSwTable[ls][ci];
     const int rows = gemv_rows(c) / 2;   // of each projection per workgroup
     const size_t lds = (size_t)(wg.K / 32) * kChunkStride4 * 16;
-    if (lds > 64 * 1024 && !g_gemv_sw_lds_raised[ls][ci].load()) {
+    std::atomic<bool>& raised = na ? g_gemv_norm_lds_raised[1][ls][ci] : g_gemv_sw_lds_raised[ls][ci];
+    if (lds > 64 * 1024 && !raised.load()) {
         MS_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        g_gemv_sw_lds_raised[ls][ci].store(true);
+        raised.store(true);
     }
     const int grid = (wg.N + rows - 1) / rows;
     GemvParams p;
+    set_norm(p, na);
     const Weights* mem[2] = {&wg, &wu};
     for (int i = 0; i < kGemvMaxOps; ++i) {
         const Weights& m = *mem[std::min(i, 1)];
@@ -2223,6 +2275,175 @@ int ms_hip_nbits_swiglu_launch_info(void* gate_handle, void* up_handle, const fl
     const int rows = f ? gemv_rows(kGemvConfigs[ci]) / 2 : 1;
     if (fused) *fused = f ? 1 : 0;
     if (grid) *grid = f ? (wg->N + rows - 1) / rows : 0;
+    if (block) *block = f ? kGemvConfigs[ci].waves * kWave : 0;
+    return MS_HIP_OK;
+}
+
+// ---- SkipSimplifiedLayerNormalization fused into the projections that read its output ----
+namespace {
+
+bool ranges_overlap(const void* a, const void* b, size_t bytes)
+{
+    if (!a || !b) return false;
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return x < y + bytes && y < x + bytes;
+}
+
+// Validation shared by the two entries: the norm's buffers (M rows of K) and their overlaps.
+int skipnorm_check(const char* what, const float* dX, const float* dSkip, const float* dGamma, const float* dNorm,
+                   const float* dSum, int M, int K)
+{
+    if (!dX || !dSkip || !dGamma || !dNorm)
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] %s: null input, skip, gamma or normed output", what);
+    for (const void* q : {(const void*)dX, (const void*)dSkip, (const void*)dGamma, (const void*)dNorm,
+                          (const void*)dSum})
+        if (reinterpret_cast<uintptr_t>(q) & 3)
+            return fail(MS_HIP_ERR_INVALID, "[ms_hip] %s: buffers must be 4-byte aligned", what);
+    const size_t bytes = (size_t)M * K * sizeof(float);
+    for (const float* o : {dNorm, dSum})
+        for (const float* i : {dX, dSkip})
+            if (ranges_overlap(o, i, bytes))
+                return fail(MS_HIP_ERR_INVALID,
+                            "[ms_hip] %s: the normed output and the sum must not overlap the input or the skip", what);
+    if (ranges_overlap(dNorm, dSum, bytes))
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] %s: the normed output and the sum must not overlap", what);
+    return MS_HIP_OK;
+}
+
+bool aligned16_all(std::initializer_list<const void*> ps)
+{
+    for (const void* q : ps)
+        if (reinterpret_cast<uintptr_t>(q) & 15) return false;
+    return true;
+}
+
+// The fused launch of the batch form: M = 1, every handle groupable with the first (at most
+// kGemvMaxOps), a gemv_w4 config for their rows whose threads cover two per chunk, and
+// 16-byte aligned norm buffers. *ci receives the config.
+bool skipnorm_batch_fused(Weights* const* ws, int count, const float* dX, const float* dSkip, const float* dGamma,
+                          const float* dNorm, const float* dSum, int M, int* ci)
+{
+    if (M != 1 || count < 1 || count > kGemvMaxOps) return false;
+    if (!aligned16_all({dX, dSkip, dGamma, dNorm, dSum})) return false;
+    const Weights& w0 = *ws[0];
+    if (!gemv_groupable(w0, w0)) return false;
+    int ntot = 0;
+    for (int i = 0; i < count; ++i) {
+        if (!gemv_groupable(w0, *ws[i])) return false;
+        ntot += ws[i]->N;
+    }
+    const Knobs kn = knobs_of(w0);
+    if (kn.skinny() == 2) return false;
+    const int c = pick_gemv_config(w0, kn, 1, ntot);
+    if (c < 0 || !norm_fits(kGemvConfigs[c], w0.K) || !kGemvNormTable[0][l_slot(w0)][c]) return false;
+    *ci = c;
+    return true;
+}
+
+bool skipnorm_swiglu_fused(const Weights& wg, const Weights& wu, const float* dX, const float* dSkip,
+                           const float* dGamma, const float* dNorm, const float* dSum, int M, int* ci)
+{
+    int c = -1;
+    if (!aligned16_all({dX, dSkip, dGamma, dNorm, dSum}) || !swiglu_fused_config(wg, wu, dNorm, M, &c)) return false;
+    if (!norm_fits(kGemvConfigs[c], wg.K) || !kGemvNormTable[1][l_slot(wg)][c]) return false;
+    *ci = c;
+    return true;
+}
+
+}  // namespace
+
+int ms_hip_nbits_gemm_dev_skipnorm(void* const* handles, int count, const float* dX, const float* dSkip,
+                                   const float* dGamma, float eps, float* dNorm, float* dSum, float* const* dY, int M,
+                                   void* stream)
+{
+    if (int st = gate()) return st;
+    if (count <= 0 || !handles || !dY) return fail(MS_HIP_ERR_INVALID, "[ms_hip] skipnorm: invalid batch arguments");
+    std::vector<Weights*> ws((size_t)count);
+    for (int i = 0; i < count; ++i)
+        if (!(ws[i] = from_handle(handles[i])))
+            return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle at batch index %d", i);
+    if (M < 0) return fail(MS_HIP_ERR_INVALID, "[ms_hip] M must be non-negative; got %d", M);
+    const int K = ws[0]->K;
+    for (int i = 1; i < count; ++i)
+        if (ws[i]->K != K || ws[i]->device != ws[0]->device)
+            return fail(MS_HIP_ERR_INVALID, "[ms_hip] skipnorm: every projection must share K and the device");
+    if (M == 0) return MS_HIP_OK;
+    if (int st = skipnorm_check("skipnorm", dX, dSkip, dGamma, dNorm, dSum, M, K)) return st;
+    for (int i = 0; i < count; ++i)
+        if (!dY[i] || (reinterpret_cast<uintptr_t>(dY[i]) & 3))
+            return fail(MS_HIP_ERR_INVALID, "[ms_hip] null or misaligned output at batch index %d", i);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    for (int i = 0; i < count; ++i)
+        if (int st = take_device_error(*ws[i], s)) return st;
+    int ci = -1;
+    if (skipnorm_batch_fused(ws.data(), count, dX, dSkip, dGamma, dNorm, dSum, M, &ci)) {
+        GemvMember mem[kGemvMaxOps];
+        for (int i = 0; i < count; ++i) mem[i] = GemvMember{ws[i], dY[i]};
+        const NormArgs na{dX, dSkip, dGamma, dSum, dNorm, eps};
+        return launch_gemv_group(mem, count, dX, 1, ci, s, &na);
+    }
+    // Otherwise the norm, then the batch on its output.
+    if (int st = ms_hip_skip_rmsnorm(dX, dSkip, dGamma, nullptr, nullptr, dNorm, dSum, nullptr, M, K, eps, stream))
+        return st;
+    std::vector<const float*> dA((size_t)count, dNorm);
+    return ms_hip_nbits_gemm_dev_batch(handles, dA.data(), dY, count, M, stream);
+}
+
+int ms_hip_nbits_gemm_dev_skipnorm_swiglu(void* gate_handle, void* up_handle, const float* dX, const float* dSkip,
+                                          const float* dGamma, float eps, float* dNorm, float* dSum, float* dH, int M,
+                                          void* stream)
+{
+    if (int st = gate()) return st;
+    Weights* wg = from_handle(gate_handle);
+    Weights* wu = from_handle(up_handle);
+    if (!wg || !wu) return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle");
+    if (M < 0) return fail(MS_HIP_ERR_INVALID, "[ms_hip] M must be non-negative; got %d", M);
+    if (wg->K != wu->K || wg->N != wu->N || wg->device != wu->device)
+        return fail(MS_HIP_ERR_INVALID,
+                    "[ms_hip] swiglu: the gate and up projections must share K, N and the device (got K=%d/%d, N=%d/%d)",
+                    wg->K, wu->K, wg->N, wu->N);
+    if (M == 0) return MS_HIP_OK;
+    if (int st = skipnorm_check("skipnorm_swiglu", dX, dSkip, dGamma, dNorm, dSum, M, wg->K)) return st;
+    if (!dH || (reinterpret_cast<uintptr_t>(dH) & 3))
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] swiglu: null or misaligned activations or output");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (int st = take_device_error(*wg, s)) return st;
+    if (int st = take_device_error(*wu, s)) return st;
+    int ci = -1;
+    if (skipnorm_swiglu_fused(*wg, *wu, dX, dSkip, dGamma, dNorm, dSum, M, &ci)) {
+        const NormArgs na{dX, dSkip, dGamma, dSum, dNorm, eps};
+        return launch_gemv_swiglu(*wg, *wu, dX, dH, ci, s, &na);
+    }
+    if (int st = ms_hip_skip_rmsnorm(dX, dSkip, dGamma, nullptr, nullptr, dNorm, dSum, nullptr, M, wg->K, eps, stream))
+        return st;
+    return ms_hip_nbits_gemm_dev_swiglu(gate_handle, up_handle, dNorm, dH, M, stream);
+}
+
+int ms_hip_nbits_skipnorm_launch_info(void* const* handles, int count, int swiglu, const float* dX,
+                                      const float* dSkip, const float* dGamma, const float* dNorm, const float* dSum,
+                                      int M, int* fused, int* grid, int* block)
+{
+    if (count <= 0 || !handles || (swiglu && count != 2))
+        return fail(MS_HIP_ERR_INVALID, "[ms_hip] skipnorm: invalid batch arguments");
+    std::vector<Weights*> ws((size_t)count);
+    for (int i = 0; i < count; ++i)
+        if (!(ws[i] = from_handle(handles[i])))
+            return fail(MS_HIP_ERR_INVALID, "[ms_hip] invalid weights handle at batch index %d", i);
+    int ci = -1, gr = 0, rows = 1;
+    bool f;
+    if (swiglu) {
+        f = ws[0]->K == ws[1]->K && ws[0]->N == ws[1]->N &&
+            skipnorm_swiglu_fused(*ws[0], *ws[1], dX, dSkip, dGamma, dNorm, dSum, M, &ci);
+        if (f) gr = (ws[0]->N + gemv_rows(kGemvConfigs[ci]) / 2 - 1) / (gemv_rows(kGemvConfigs[ci]) / 2);
+    } else {
+        f = skipnorm_batch_fused(ws.data(), count, dX, dSkip, dGamma, dNorm, dSum, M, &ci);
+        if (f) {
+            rows = gemv_rows(kGemvConfigs[ci]);
+            for (int i = 0; i < count; ++i) gr += (ws[i]->N + rows - 1) / rows;
+        }
+    }
+    if (fused) *fused = f ? 1 : 0;
+    if (grid) *grid = f ? gr : 0;
     if (block) *block = f ? kGemvConfigs[ci].waves * kWave : 0;
     return MS_HIP_OK;
 }

@@ -14,6 +14,8 @@ MatMulNBits to the next:
   SiluMul                           Sigmoid -> Mul -> Mul fused by fuse_silu_mul()
   GateUpSiluMul                     MatMulNBits(x, gate), MatMulNBits(x, up) -> SiluMul, fused by
                                     fuse_gate_up_silu()
+  SkipNormMatMulNBits,              SkipSimplifiedLayerNormalization and the MatMulNBits (or the
+  SkipNormGateUpSiluMul             GateUpSiluMul) that read its output, fused by fuse_skipnorm()
 
 Activations are torch tensors on the device (host arrays are uploaded once per call);
 initializers (norm weights, rotary caches) are uploaded once and kept. Nothing here
@@ -342,6 +344,183 @@ class HipGateUpSiluMulKernel(IKernel):
                                      list(node.outputs)), ctx)
 
 
+def fuse_skipnorm(graph: ModelGraph) -> int:
+    """Rewrites a SkipSimplifiedLayerNormalization(x, skip, gamma) -> (n, mean, inv_std, t)
+    without beta or bias, whose normed output n feeds nothing but 1-4 MatMulNBits nodes on n
+    (sharing K, bits and block_size, no g_idx or bias inputs) or one GateUpSiluMul on n, and
+    whose mean and inv_std outputs are unused, into one node at the norm's place:
+    SkipNormMatMulNBits(x, skip, gamma, B_1, scales_1, zp_1, ...) -> (y_1, ..., t) with
+    attributes K, bits, block_size, Ns (each projection's N) and epsilon, or
+    SkipNormGateUpSiluMul(x, skip, gamma, gate triple, up triple) -> (h, t). The projections'
+    weights must be graph inputs, initializers or outputs of nodes before the norm. Run
+    fuse_gate_up_silu first. Returns the number of norms fused."""
+    consumers: dict[str, list[GraphNode]] = {}
+    for n in graph.nodes:
+        for i in n.inputs:
+            if i:
+                consumers.setdefault(i, []).append(n)
+    outs = set(graph.outputs)
+    available = set(graph.inputs) | set(graph.initializers) | {""}
+    fused = 0
+    drop: set[int] = set()
+    replace: dict[int, GraphNode] = {}
+    keys = ("K", "bits", "block_size")
+
+    def plain_mm(c, n):
+        return (c.op_type == "MatMulNBits" and len(c.outputs) == 1 and c.inputs[0] == n and n not in c.inputs[1:]
+                and not any(c.inputs[4:]))
+
+    def tri(c, lo):
+        return (list(c.inputs[lo:lo + 3]) + ["", "", ""])[:3]
+
+    for node in graph.nodes:
+        s = node
+        ok = (s.op_type == "SkipSimplifiedLayerNormalization" and len(s.inputs) >= 3 and not any(s.inputs[3:])
+              and s.outputs and s.outputs[0] and s.outputs[0] not in outs
+              and not any(o and (o in outs or consumers.get(o)) for o in s.outputs[1:3]))
+        cons = consumers.get(s.outputs[0], []) if ok else []
+        if ok and cons and not any(id(c) in drop for c in cons):
+            n = s.outputs[0]
+            t = s.outputs[3] if len(s.outputs) > 3 else ""
+            eps = s.attributes.get("epsilon", 1e-5)
+            fnode = None
+            if len(cons) == 1 and cons[0].op_type == "GateUpSiluMul" and cons[0].inputs[0] == n \
+                    and n not in cons[0].inputs[1:]:
+                c = cons[0]
+                w = tri(c, 1) + tri(c, 4)
+                if all(x in available for x in w):
+                    fnode = GraphNode("SkipNormGateUpSiluMul", s.name + "/skipnorm", list(s.inputs[:3]) + w,
+                                      [c.outputs[0], t], {**c.attributes, "epsilon": eps})
+            elif 1 <= len(cons) <= 4 and all(plain_mm(c, n) for c in cons) \
+                    and all(c.attributes.get(k) == cons[0].attributes.get(k) for c in cons for k in keys):
+                w = [x for c in cons for x in tri(c, 1)]
+                if all(x in available for x in w):
+                    at = {k: cons[0].attributes.get(k) for k in keys}
+                    at.update(Ns=[c.attributes.get("N") for c in cons], epsilon=eps)
+                    fnode = GraphNode("SkipNormMatMulNBits", s.name + "/skipnorm", list(s.inputs[:3]) + w,
+                                      [c.outputs[0] for c in cons] + [t], at)
+            if fnode is not None:
+                drop.update(id(c) for c in cons)
+                replace[id(s)] = fnode
+                fused += 1
+        available.update(o for o in node.outputs if o)
+    graph.nodes = [replace.get(id(n), n) for n in graph.nodes if id(n) not in drop]
+    return fused
+
+
+class _HipSkipNormFused(IKernel):
+    """The nodes fuse_skipnorm makes: SkipSimplifiedLayerNormalization
+    (SkipSimplifiedLayerNormalizationKernel.cs:29-86) and the projections of its output
+    (MatMulNBitsKernel.cs:79-161 validation), as one ms_hip_nbits_gemm_dev_skipnorm(_swiglu)
+    call on the device (one launch at M = 1); the W4A8 opt-in runs the nodes apart."""
+
+    def __init__(self, matmul=None):
+        from .hip_kernel import HipMatMulNBitsKernel
+        self._mm = matmul if matmul is not None else HipMatMulNBitsKernel()
+        self._norm = HipSkipSimplifiedLayerNormalizationKernel()
+        self._dev = _DeviceInputs()
+
+    def close(self):
+        self._mm.close()
+
+    def _projections(self, node: GraphNode, a: str) -> list[GraphNode]:
+        raise NotImplementedError
+
+    def preload(self, graph: ModelGraph) -> int:
+        """Load-time upload of the fused nodes' weight triples (HipMatMulNBitsKernel.preload)."""
+        pseudo = [p for n in graph.nodes if n.op_type == self.op_type for p in self._projections(n, n.inputs[0])]
+        g = ModelGraph(pseudo, graph.initializers)
+        g.sources = getattr(graph, "sources", {})
+        return self._mm.preload(g)
+
+    def _apart(self, node: GraphNode, ctx: GraphContext, normed: str) -> None:
+        raise NotImplementedError
+
+    def execute(self, node: GraphNode, ctx: GraphContext) -> None:
+        torch = _torch()
+        normed = node.name + "/normed"
+        t_name = node.outputs[-1]
+        if self._mm.w4a8:
+            self._norm.execute(GraphNode("SkipSimplifiedLayerNormalization", node.name + "/norm", list(node.inputs[:3]),
+                                         [normed, "", "", t_name], {"epsilon": _attr_float(node, "epsilon", 1e-5)}),
+                               ctx)
+            self._apart(node, ctx, normed)
+            return
+        x = self._dev.input(ctx, node.inputs[0])
+        skip = self._dev.input(ctx, node.inputs[1])
+        gamma = self._dev.input(ctx, node.inputs[2])
+        K = gamma.numel()
+        if skip.numel() != x.numel():
+            raise ModelSharpException("SkipSimplifiedLayerNormalization skip must have the input's shape.")
+        M = 0 if K == 0 else x.numel() // K
+        dnorm = torch.empty_like(x)
+        ctx.set(normed, dnorm)   # for the projections' validation (shapes), written by the call
+        dsum = torch.empty_like(x) if t_name else None
+        self._run(node, ctx, normed, x, skip, gamma, dnorm, dsum, M)
+        if t_name:
+            ctx.set(t_name, dsum)
+
+
+class HipSkipNormMatMulNBitsKernel(_HipSkipNormFused):
+    op_type = "SkipNormMatMulNBits"
+
+    def _projections(self, node, a):
+        at = node.attributes
+        return [GraphNode("MatMulNBits", f"{node.name}/mm{i}", [a] + list(node.inputs[3 + 3 * i:6 + 3 * i]),
+                          [node.outputs[i]], {"K": at["K"], "N": N, "bits": at["bits"],
+                                              "block_size": at["block_size"]})
+                for i, N in enumerate(at["Ns"])]
+
+    def _apart(self, node, ctx, normed):
+        for p in self._projections(node, normed):
+            self._mm.execute(p, ctx)
+
+    def _run(self, node, ctx, normed, x, skip, gamma, dnorm, dsum, M):
+        torch = _torch()
+        hs, ys = [], []
+        for p in self._projections(node, normed):
+            a, b, sc, zp, N, K, bits, bs = self._mm._validate(p, ctx)
+            hs.append(self._mm._weights(p, b, sc, zp, N, K, bits, bs))
+            ys.append(torch.empty(tuple(x.shape[:-1]) + (N,), dtype=torch.float32, device=x.device))
+        native.gemm_dev_skipnorm(hs, x.data_ptr(), skip.data_ptr(), gamma.data_ptr(),
+                                 _attr_float(node, "epsilon", 1e-5), dnorm.data_ptr(),
+                                 None if dsum is None else dsum.data_ptr(), [y.data_ptr() for y in ys], M, _stream(x))
+        for o, y in zip(node.outputs[:-1], ys):
+            ctx.set(o, y)
+
+
+class HipSkipNormGateUpSiluMulKernel(_HipSkipNormFused):
+    op_type = "SkipNormGateUpSiluMul"
+
+    def __init__(self, matmul=None):
+        super().__init__(matmul)
+        self._gus = HipGateUpSiluMulKernel(self._mm)
+
+    def _projections(self, node, a):
+        at = node.attributes
+        mk = lambda nm, lo: GraphNode("MatMulNBits", f"{node.name}/{nm}", [a] + list(node.inputs[lo:lo + 3]),   # noqa: E731
+                                      [f"{node.name}/{nm}_out"], {k: at[k] for k in ("K", "N", "bits", "block_size")})
+        return [mk("gate", 3), mk("up", 6)]
+
+    def _apart(self, node, ctx, normed):
+        self._gus.execute(GraphNode("GateUpSiluMul", node.name + "/gate_up_silu", [normed] + list(node.inputs[3:9]),
+                                    [node.outputs[0]], {k: v for k, v in node.attributes.items() if k != "epsilon"}),
+                          ctx)
+
+    def _run(self, node, ctx, normed, x, skip, gamma, dnorm, dsum, M):
+        torch = _torch()
+        gnode, unode = self._projections(node, normed)
+        _, bg, sg, zg, N, K, bits, bs = self._mm._validate(gnode, ctx)
+        _, bu, su, zu, _, _, _, _ = self._mm._validate(unode, ctx)
+        wg = self._mm._weights(gnode, bg, sg, zg, N, K, bits, bs)
+        wu = self._mm._weights(unode, bu, su, zu, N, K, bits, bs)
+        h = torch.empty(tuple(x.shape[:-1]) + (N,), dtype=torch.float32, device=x.device)
+        native.gemm_dev_skipnorm_swiglu(wg, wu, x.data_ptr(), skip.data_ptr(), gamma.data_ptr(),
+                                        _attr_float(node, "epsilon", 1e-5), dnorm.data_ptr(),
+                                        None if dsum is None else dsum.data_ptr(), h.data_ptr(), M, _stream(x))
+        ctx.set(node.outputs[0], h)
+
+
 @dataclasses.dataclass
 class _Cache:
     k: object
@@ -490,6 +669,7 @@ def register_decoder_kernels(registry: KernelRegistry) -> KernelRegistry:
     wins, KernelRegistry.cs:20-24)."""
     for k in (HipSimplifiedLayerNormalizationKernel(), HipSkipSimplifiedLayerNormalizationKernel(),
               HipGroupQueryAttentionKernel(), HipAddKernel(), HipMulKernel(), HipSigmoidKernel(),
-              HipSiluMulKernel(), HipGateUpSiluMulKernel()):
+              HipSiluMulKernel(), HipGateUpSiluMulKernel(), HipSkipNormMatMulNBitsKernel(),
+              HipSkipNormGateUpSiluMulKernel()):
         registry.register(k)
     return registry

@@ -96,6 +96,12 @@ _PROTOTYPES = {
     "ms_hip_nbits_batch_launch_info": (_c_int, [_vp, _vp, _c_int, _c_int, _ip, _ip, _ip, _ip, _ip]),
     "ms_hip_nbits_gemm_dev_swiglu": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _vp]),
     "ms_hip_nbits_swiglu_launch_info": (_c_int, [_vp, _vp, _vp, _c_int, _ip, _ip, _ip]),
+    "ms_hip_nbits_gemm_dev_skipnorm": (_c_int, [_vp, _c_int, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _c_int,
+                                                _vp]),
+    "ms_hip_nbits_gemm_dev_skipnorm_swiglu": (_c_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp,
+                                                       _c_int, _vp]),
+    "ms_hip_nbits_skipnorm_launch_info": (_c_int, [_vp, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _c_int, _ip, _ip,
+                                                   _ip]),
 }
 
 _lock = threading.Lock()
@@ -350,6 +356,37 @@ def swiglu_launch_info(gate, up, dA: int, M: int) -> dict:
     f, g, b = (ctypes.c_int() for _ in range(3))
     check(load().ms_hip_nbits_swiglu_launch_info(gate.handle, up.handle, _vp(dA), int(M), ctypes.byref(f),
                                                   ctypes.byref(g), ctypes.byref(b)))
+    return {"fused": bool(f.value), "grid": g.value, "block": b.value}
+
+
+def gemm_dev_skipnorm(weights: list, dX: int, dSkip: int, dGamma: int, eps: float, dNorm: int, dSum: int | None,
+                      dY: list[int], M: int, stream: int | None = None) -> None:
+    """SkipSimplifiedLayerNormalization (no beta or bias) of X + Skip, then each projection of
+    the normed rows: dNorm, dSum (optional) and dY[i] on device pointers (one launch at M = 1)."""
+    n = len(weights)
+    hs = (_vp * n)(*[w.handle for w in weights])
+    py = (_vp * n)(*dY)
+    check(load().ms_hip_nbits_gemm_dev_skipnorm(hs, n, _vp(dX), _vp(dSkip), _vp(dGamma), ctypes.c_float(eps),
+                                                 _vp(dNorm), _vp(dSum or 0), py, int(M), _vp(stream or 0)))
+
+
+def gemm_dev_skipnorm_swiglu(gate, up, dX: int, dSkip: int, dGamma: int, eps: float, dNorm: int, dSum: int | None,
+                             dH: int, M: int, stream: int | None = None) -> None:
+    """The same norm, then gemm_dev_swiglu on its output (one launch at M = 1)."""
+    check(load().ms_hip_nbits_gemm_dev_skipnorm_swiglu(gate.handle, up.handle, _vp(dX), _vp(dSkip), _vp(dGamma),
+                                                        ctypes.c_float(eps), _vp(dNorm), _vp(dSum or 0), _vp(dH),
+                                                        int(M), _vp(stream or 0)))
+
+
+def skipnorm_launch_info(weights: list, swiglu: bool, dX: int, dSkip: int, dGamma: int, dNorm: int,
+                         dSum: int | None, M: int) -> dict:
+    """Whether the fused norm call with these arguments is one launch, and its shape."""
+    n = len(weights)
+    hs = (_vp * n)(*[w.handle for w in weights])
+    f, g, b = (ctypes.c_int() for _ in range(3))
+    check(load().ms_hip_nbits_skipnorm_launch_info(hs, n, int(bool(swiglu)), _vp(dX), _vp(dSkip), _vp(dGamma),
+                                                    _vp(dNorm), _vp(dSum or 0), int(M), ctypes.byref(f),
+                                                    ctypes.byref(g), ctypes.byref(b)))
     return {"fused": bool(f.value), "grid": g.value, "block": b.value}
 
 

@@ -14,7 +14,7 @@ import pytest
 import oracle
 from modelsharp_amd import native, workloads
 from modelsharp_amd.decoder_kernels import (HipGroupQueryAttentionKernel, fuse_gate_up_silu, fuse_silu_mul,
-                                            register_decoder_kernels)
+                                            fuse_skipnorm, register_decoder_kernels)
 from modelsharp_amd.graph import Engine, GraphContext, GraphNode, KernelRegistry, ModelGraph
 from modelsharp_amd.hip_kernel import register_kernels
 
@@ -182,6 +182,125 @@ def test_swiglu_rejects_mismatched_projections(gpu):
     assert e.value.status == native.MS_HIP_ERR_INVALID and "share K, N" in e.value.message
     wg.close()
     wu.close()
+
+
+# ---- SkipSimplifiedLayerNormalization fused into its projections ----------------------------
+# (projection shapes, M): the 7B q/k/v of one normed input and the Qwen q/k/v (one grouped
+# launch each at M = 1), a lone projection, block size 128 without zero points, and M > 1
+# (the norm and the batch call apart).
+SKIPNORM_CASES = [([workloads.DECODE_7B[i] for i in (0, 1, 2)], 1),
+                  (workloads.QWEN05B_DECODE[:3], 1),
+                  ([workloads.Op("lone", 1024, 700, 32, True)], 1),
+                  ([workloads.Op("bs128", 4096, 1100, 128, False)], 1),
+                  ([workloads.Op("m3a", 1024, 300, 32, True), workloads.Op("m3b", 1024, 200, 32, True)], 3)]
+
+
+def _norm_inputs(M, K, seed):
+    r = np.random.default_rng(seed)
+    x = r.standard_normal((M, K)).astype(np.float32)
+    s = (r.standard_normal((M, K)) * 3).astype(np.float32)
+    g = r.uniform(0.5, 1.5, K).astype(np.float32)
+    return x, s, g
+
+
+def _check_norm_outputs(norm, sm, x, s, g, eps):
+    out_ref, _, sum_ref = oracle.skip_rmsnorm(x, s, g, None, None, eps)
+    assert np.array_equal(sm, sum_ref)
+    assert np.allclose(norm, out_ref, rtol=2e-6, atol=1e-7 * np.abs(out_ref).max())
+    return out_ref
+
+
+@pytest.mark.parametrize("ops,M", SKIPNORM_CASES, ids=lambda v: str(v) if isinstance(v, int) else v[0].name)
+def test_skipnorm_projections(gpu, ops, M):
+    """T = X + Skip and the normed rows as ms_hip_skip_rmsnorm writes them (T bit-exact, the
+    norm within its rtol), and each projection of the normed rows within the GEMV bar of the
+    oracle (norm, then matmul_nbits). At M = 1 it is one launch that computes the norm in
+    every workgroup's staging and scales the sums by inv; two calls agree bit for bit."""
+    import torch
+    K, eps = ops[0].K, 1e-6
+    x, s, g = _norm_inputs(M, K, seed=K + M)
+    hs, host_w = [], []
+    for i, op in enumerate(ops):
+        b, sc, z = workloads.make_weights(op, 60 + i)
+        host_w.append((b, sc, z))
+        hs.append(native.NBitsWeights(b, sc, z, op.N, op.K, op.bits, op.block_size))
+    dx, ds, dg = dev(x), dev(s), dev(g)
+    norm, sm = torch.empty_like(dx), torch.empty_like(dx)
+    info = native.skipnorm_launch_info(hs, False, dx.data_ptr(), ds.data_ptr(), dg.data_ptr(), norm.data_ptr(),
+                                       sm.data_ptr(), M)
+    log(f"skipnorm {[o.name for o in ops]} K={K} M={M}: {info}")
+    assert info["fused"] == (M == 1)
+    ys = [torch.full((M, op.N), float("nan"), device="cuda") for op in ops]
+    native.gemm_dev_skipnorm(hs, dx.data_ptr(), ds.data_ptr(), dg.data_ptr(), eps, norm.data_ptr(), sm.data_ptr(),
+                             [y.data_ptr() for y in ys], M)
+    first = [host(y) for y in ys]
+    out_ref = _check_norm_outputs(host(norm), host(sm), x, s, g, eps)
+    for (b, sc, z), op, y in zip(host_w, ops, first):
+        ref = oracle.matmul_nbits(out_ref, b, sc, z, op.N, op.K, op.bits, op.block_size)
+        rowmax = np.max(np.abs(ref), axis=-1, keepdims=True)
+        err = np.max(np.abs(y - ref) / rowmax)
+        log(f"  {op.name}: max row-relative err {err:.2e}")
+        assert err <= 1e-5
+    native.gemm_dev_skipnorm(hs, dx.data_ptr(), ds.data_ptr(), dg.data_ptr(), eps, norm.data_ptr(), None,
+                             [y.data_ptr() for y in ys], M)
+    for y, y1 in zip(ys, first):
+        assert np.array_equal(host(y), y1)
+    for h in hs:
+        h.close()
+
+
+@pytest.mark.parametrize("op", SWIGLU_OPS[:3], ids=lambda o: o.name)
+def test_skipnorm_swiglu(gpu, op):
+    """The norm, then gate, up and SiLU-Mul: one launch at M = 1, within the GEMV bar of the
+    unfused calls (ms_hip_skip_rmsnorm, then ms_hip_nbits_gemm_dev_swiglu) and of the
+    oracle in float64."""
+    import torch
+    eps = 1e-5
+    x, s, g = _norm_inputs(1, op.K, seed=op.N)
+    wg, wu = _swiglu_handles(op, 71)
+    dx, ds, dg = dev(x), dev(s), dev(g)
+    norm, sm = torch.empty_like(dx), torch.empty_like(dx)
+    info = native.skipnorm_launch_info([wg, wu], True, dx.data_ptr(), ds.data_ptr(), dg.data_ptr(), norm.data_ptr(),
+                                       sm.data_ptr(), 1)
+    log(f"skipnorm swiglu {op.name}: {info}")
+    assert info["fused"]
+    h = torch.full((1, op.N), float("nan"), device="cuda")
+    native.gemm_dev_skipnorm_swiglu(wg, wu, dx.data_ptr(), ds.data_ptr(), dg.data_ptr(), eps, norm.data_ptr(),
+                                    sm.data_ptr(), h.data_ptr(), 1)
+    out_ref = _check_norm_outputs(host(norm), host(sm), x, s, g, eps)
+    n2, h2 = torch.empty_like(dx), torch.empty_like(h)
+    native.skip_rmsnorm(dx.data_ptr(), ds.data_ptr(), dg.data_ptr(), None, None, n2.data_ptr(), None, None, 1, op.K,
+                        eps)
+    native.gemm_dev_swiglu(wg, wu, n2.data_ptr(), h2.data_ptr(), 1)
+    got, sep = host(h).astype(np.float64), host(h2).astype(np.float64)
+    bg, sg, zg = workloads.make_weights(op, 71)
+    bu, su, zu = workloads.make_weights(op, 72)
+    gr = oracle.matmul_nbits(out_ref, bg, sg, zg, op.N, op.K, op.bits, op.block_size).astype(np.float64)
+    ur = oracle.matmul_nbits(out_ref, bu, su, zu, op.N, op.K, op.bits, op.block_size).astype(np.float64)
+    hr = gr / (1 + np.exp(-gr)) * ur
+    for what, v in (("oracle", hr), ("unfused", sep)):
+        rel = np.linalg.norm(got - v) / np.linalg.norm(v)
+        log(f"  against the {what}: relative Frobenius {rel:.2e}")
+        assert rel <= 1e-5
+    wg.close()
+    wu.close()
+
+
+def test_skipnorm_rejects_outputs_over_inputs(gpu):
+    """The fused launch's workgroups read X and Skip while workgroup 0 writes the sum and the
+    normed rows, so those outputs may not overlap the inputs (the residual stream needs a
+    second buffer)."""
+    import torch
+    op = workloads.Op("a", 512, 64, 32, True)
+    w = native.NBitsWeights(*workloads.make_weights(op, 1), op.N, op.K, op.bits, op.block_size)
+    x, s, g = (dev(v) for v in _norm_inputs(1, op.K, seed=2))
+    norm, y = torch.empty_like(x), torch.empty((1, op.N), device="cuda")
+    for dnorm, dsum in ((norm, s), (x, None), (norm, norm)):
+        with pytest.raises(native.HipError) as e:
+            native.gemm_dev_skipnorm([w], x.data_ptr(), s.data_ptr(), g.data_ptr(), 1e-6, dnorm.data_ptr(),
+                                     None if dsum is None else dsum.data_ptr(), [y.data_ptr()], 1)
+        assert e.value.status == native.MS_HIP_ERR_INVALID and "overlap" in e.value.message
+    w.close()
 
 
 # ---- GroupQueryAttention ---------------------------------------------------------------------
@@ -452,13 +571,18 @@ def layer_oracle(g, x, resid, past_k, past_v, hid, H, KH, D, inter, bs):
 @pytest.mark.parametrize("fused", [False, True])
 def test_decoder_layer_end_to_end(gpu, fused):
     """Prefill of 5 tokens, then 3 decode steps, the whole layer on the device (no host
-    round trip between operators), against the oracle composed on the CPU."""
+    round trip between operators), against the oracle composed on the CPU; fused: SiLU-Mul,
+    gate/up and both norms folded into the launches of the projections (the norm computed
+    in the projection launch's staging at the decode steps, apart at the prefill)."""
     import torch
     hid, H, KH, D, inter, bs = 512, 8, 2, 64, 1024, 32
     g = layer_graph(hid, H, KH, D, inter, bs, seed=1)
     if fused:
         assert fuse_silu_mul(g) == 1 and [n.op_type for n in g.nodes].count("SiluMul") == 1
         assert fuse_gate_up_silu(g) == 1 and [n.op_type for n in g.nodes].count("GateUpSiluMul") == 1
+        assert fuse_skipnorm(g) == 2
+        ops = [n.op_type for n in g.nodes]
+        assert ops.count("SkipNormMatMulNBits") == 1 and ops.count("SkipNormGateUpSiluMul") == 1
     reg = register_decoder_kernels(register_kernels(KernelRegistry()))
     eng = Engine(g, reg)
     r = np.random.default_rng(2)

@@ -423,6 +423,55 @@ def test_fuse_gate_up_silu_patterns():
     assert fuse_silu_mul(g) == 1 and fuse_gate_up_silu(g) == 0
 
 
+def test_fuse_skipnorm_patterns():
+    from modelsharp_amd.decoder_kernels import fuse_gate_up_silu, fuse_silu_mul, fuse_skipnorm
+    at = {"K": 4, "bits": 4, "block_size": 32}
+    inits = {k: None for k in ("g1", "g2", "Bq", "Sq", "Zq", "Bk", "Sk", "Bg", "Sg", "Zg", "Bu", "Su", "Bd", "Sd")}
+    mk = lambda: ModelGraph(nodes=[   # noqa: E731
+        GraphNode("SkipSimplifiedLayerNormalization", "ln1", ["x", "r", "g1"], ["n1", "", "", "t1"], {"epsilon": 1e-6}),
+        GraphNode("MatMulNBits", "q", ["n1", "Bq", "Sq", "Zq"], ["q"], dict(at, N=8)),
+        GraphNode("MatMulNBits", "k", ["n1", "Bk", "Sk"], ["k"], dict(at, N=2)),
+        GraphNode("Add", "mix", ["q", "t1"], ["o"]),
+        GraphNode("SkipSimplifiedLayerNormalization", "ln2", ["o", "t1", "g2"], ["n2", "", "", "t2"]),
+        GraphNode("MatMulNBits", "gate", ["n2", "Bg", "Sg", "Zg"], ["g"], dict(at, N=8)),
+        GraphNode("MatMulNBits", "up", ["n2", "Bu", "Su"], ["u"], dict(at, N=8)),
+        GraphNode("Sigmoid", "sig", ["g"], ["s"]),
+        GraphNode("Mul", "m1", ["g", "s"], ["a"]),
+        GraphNode("Mul", "m2", ["a", "u"], ["h"]),
+        GraphNode("MatMulNBits", "down", ["h", "Bd", "Sd"], ["y"], dict(at, N=4)),
+    ], initializers=dict(inits), inputs=["x", "r"], outputs=["y", "k", "t2"])
+    g = mk()
+    assert fuse_silu_mul(g) == 1 and fuse_gate_up_silu(g) == 1 and fuse_skipnorm(g) == 2
+    assert [(n.op_type, n.inputs, n.outputs) for n in g.nodes] == [
+        ("SkipNormMatMulNBits", ["x", "r", "g1", "Bq", "Sq", "Zq", "Bk", "Sk", ""], ["q", "k", "t1"]),
+        ("Add", ["q", "t1"], ["o"]),
+        ("SkipNormGateUpSiluMul", ["o", "t1", "g2", "Bg", "Sg", "Zg", "Bu", "Su", ""], ["h", "t2"]),
+        ("MatMulNBits", ["h", "Bd", "Sd"], ["y"])]
+    assert g.nodes[0].attributes == dict(at, Ns=[8, 2], epsilon=1e-6)
+    assert g.nodes[2].attributes == dict(at, N=8, epsilon=1e-5)
+    g = mk()
+    g.outputs.append("n1")   # the normed output is used elsewhere: that norm stays
+    assert fuse_skipnorm(g) == 1 and g.nodes[0].op_type == "SkipSimplifiedLayerNormalization"
+    g = mk()
+    g.nodes[0].outputs[2] = "inv"
+    g.outputs.append("inv")   # inv_std is used: no fusion of that norm
+    assert fuse_skipnorm(g) == 1 and g.nodes[0].op_type == "SkipSimplifiedLayerNormalization"
+    g = mk()
+    g.nodes[0].inputs.append("beta")   # beta is not folded
+    assert fuse_skipnorm(g) == 1 and g.nodes[0].op_type == "SkipSimplifiedLayerNormalization"
+    g = mk()
+    g.nodes[2].attributes["K"] = 8   # projections of different shapes
+    assert fuse_skipnorm(g) == 1 and g.nodes[0].op_type == "SkipSimplifiedLayerNormalization"
+    g = mk()
+    del g.initializers["Bk"]   # a weight computed after the norm: not available at its place
+    g.nodes.insert(0, GraphNode("Add", "late", ["x", "x"], ["Bk"]))
+    g.nodes[0], g.nodes[1] = g.nodes[1], g.nodes[0]
+    assert fuse_skipnorm(g) == 1 and g.nodes[0].op_type == "SkipSimplifiedLayerNormalization"
+    g = mk()   # without the SiLU fusions, gate and up are two plain projections of n2
+    assert fuse_skipnorm(g) == 2 and g.nodes[2].op_type == "SkipNormMatMulNBits"
+    assert g.nodes[2].outputs == ["g", "u", "t2"]
+
+
 def test_gqa_kernel_validation_messages():
     from modelsharp_amd.decoder_kernels import HipGroupQueryAttentionKernel
     k = HipGroupQueryAttentionKernel()
