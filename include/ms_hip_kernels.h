@@ -220,8 +220,9 @@ int ms_hip_nbits_swiglu_launch_info(void* gate_handle, void* up_handle, const fl
  * read its output, in one call (SkipSimplifiedLayerNormalizationKernel.cs:29-86, then
  * MatMulNBitsKernel.cs:77-265): T = X + Skip (M rows of K, K the handles' common K),
  * Norm = (T * inv) * gamma with inv = 1 / sqrt(mean(T^2) + eps) per row, Y_i = Norm W_i^T.
- * dSum (may be null) receives T, dNorm the normed rows; neither may overlap dX or dSkip
- * (MS_HIP_ERR_INVALID). No single counterpart in the reference. For a decode step (M = 1,
+ * dSum (may be null) receives T, dNorm the normed rows; neither may overlap dX or dSkip,
+ * nor may an output dY[i] overlap any of the four (MS_HIP_ERR_INVALID). No single
+ * counterpart in the reference. For a decode step (M = 1,
  * up to four 4-bit projections that ms_hip_nbits_gemm_dev_batch would group, 16-byte
  * aligned norm buffers) it is one launch: every workgroup computes the norm in its staging
  * and scales its sums by inv (Y = inv * (T gamma) W^T, the decode tolerance of the batch

@@ -2310,6 +2310,22 @@ int skipnorm_check(const char* what, const float* dX, const float* dSkip, const 
     return MS_HIP_OK;
 }
 
+// A projection's output (M rows of N) may not overlap the norm's buffers (M rows of K):
+// workgroups still reading X or Skip, or the normed rows, while others store Y.
+int skipnorm_check_out(const char* what, const float* dY, int N, const float* dX, const float* dSkip,
+                       const float* dNorm, const float* dSum, int M, int K)
+{
+    const uintptr_t y = reinterpret_cast<uintptr_t>(dY), ye = y + (size_t)M * N * sizeof(float);
+    for (const float* q : {dX, dSkip, dNorm, dSum}) {
+        if (!q) continue;
+        const uintptr_t a = reinterpret_cast<uintptr_t>(q), ae = a + (size_t)M * K * sizeof(float);
+        if (y < ae && a < ye)
+            return fail(MS_HIP_ERR_INVALID, "[ms_hip] %s: an output must not overlap the input, skip, normed rows or sum",
+                        what);
+    }
+    return MS_HIP_OK;
+}
+
 bool aligned16_all(std::initializer_list<const void*> ps)
 {
     for (const void* q : ps)
@@ -2369,9 +2385,11 @@ int ms_hip_nbits_gemm_dev_skipnorm(void* const* handles, int count, const float*
             return fail(MS_HIP_ERR_INVALID, "[ms_hip] skipnorm: every projection must share K and the device");
     if (M == 0) return MS_HIP_OK;
     if (int st = skipnorm_check("skipnorm", dX, dSkip, dGamma, dNorm, dSum, M, K)) return st;
-    for (int i = 0; i < count; ++i)
+    for (int i = 0; i < count; ++i) {
         if (!dY[i] || (reinterpret_cast<uintptr_t>(dY[i]) & 3))
             return fail(MS_HIP_ERR_INVALID, "[ms_hip] null or misaligned output at batch index %d", i);
+        if (int st = skipnorm_check_out("skipnorm", dY[i], ws[i]->N, dX, dSkip, dNorm, dSum, M, K)) return st;
+    }
     const hipStream_t s = static_cast<hipStream_t>(stream);
     for (int i = 0; i < count; ++i)
         if (int st = take_device_error(*ws[i], s)) return st;
@@ -2406,6 +2424,7 @@ int ms_hip_nbits_gemm_dev_skipnorm_swiglu(void* gate_handle, void* up_handle, co
     if (int st = skipnorm_check("skipnorm_swiglu", dX, dSkip, dGamma, dNorm, dSum, M, wg->K)) return st;
     if (!dH || (reinterpret_cast<uintptr_t>(dH) & 3))
         return fail(MS_HIP_ERR_INVALID, "[ms_hip] swiglu: null or misaligned activations or output");
+    if (int st = skipnorm_check_out("skipnorm_swiglu", dH, wg->N, dX, dSkip, dNorm, dSum, M, wg->K)) return st;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (int st = take_device_error(*wg, s)) return st;
     if (int st = take_device_error(*wu, s)) return st;

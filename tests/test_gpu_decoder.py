@@ -295,10 +295,10 @@ def test_skipnorm_rejects_outputs_over_inputs(gpu):
     w = native.NBitsWeights(*workloads.make_weights(op, 1), op.N, op.K, op.bits, op.block_size)
     x, s, g = (dev(v) for v in _norm_inputs(1, op.K, seed=2))
     norm, y = torch.empty_like(x), torch.empty((1, op.N), device="cuda")
-    for dnorm, dsum in ((norm, s), (x, None), (norm, norm)):
+    for dnorm, dsum, dy in ((norm, s, y), (x, None, y), (norm, norm, y), (norm, None, x), (norm, None, norm)):
         with pytest.raises(native.HipError) as e:
             native.gemm_dev_skipnorm([w], x.data_ptr(), s.data_ptr(), g.data_ptr(), 1e-6, dnorm.data_ptr(),
-                                     None if dsum is None else dsum.data_ptr(), [y.data_ptr()], 1)
+                                     None if dsum is None else dsum.data_ptr(), [dy.data_ptr()], 1)
         assert e.value.status == native.MS_HIP_ERR_INVALID and "overlap" in e.value.message
     w.close()
 
