@@ -175,26 +175,37 @@ def cpu_description() -> dict:
     return {"model": model, "isa": isa, "threads_available": os.cpu_count()}
 
 
-def _time_calls(fn, budget_s):
-    """Calls fn() at least once and until budget_s has passed; returns (calls, seconds)."""
+def _median_call(fn, budget_s, reps=5):
+    """Seconds per call of fn(): `reps` repetitions, each calling fn at least once and until
+    budget_s / reps has passed; returns (median, min, max) of the repetitions' per-call times."""
     fn()   # warm
-    calls, t0 = 0, time.perf_counter()
-    while True:
-        fn()
-        calls += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            return calls, el
+    per = []
+    for _ in range(reps):
+        calls, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            calls += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s / reps:
+                break
+        per.append(el / calls)
+    return statistics.median(per), min(per), max(per)
 
 
 def cpu_baseline(budget_s):
     """The oracle (kind "port": a C restatement of MatMulNBitsKernel.Execute's default
     path, column-parallel over N as MatMulParallel.For) on every workload, on all the
-    host's cores and on one thread, each for a bounded sample of about budget_s / 10."""
+    host's cores and on one thread: each figure the median of 5 repetitions of a bounded
+    sample (the budget shared over the figures)."""
     import oracle
     from modelsharp_amd import workloads
     nthreads = oracle.threads()
-    per = max(0.2, budget_s / 10.0)
+    nfig = 2 * (3 + len(workloads.LLAMA7B_SMALLM_M) + 3 * len(workloads.LLAMA7B_PREFILL_OPS))
+    per = max(0.25, budget_s / nfig)
+
+    def timed(fn):
+        med, lo, hi = _median_call(fn, per)
+        return {"ms_per_call": round(med * 1e3, 3), "ms_min": round(lo * 1e3, 3), "ms_max": round(hi * 1e3, 3)}
 
     def decode_set(name, ops, M, seed, bs_note):
         host = [workloads.make_weights(op, seed + i) for i, op in enumerate(ops)]
@@ -207,31 +218,34 @@ def cpu_baseline(budget_s):
         row = {"workload": name, "sample": f"{'+'.join(op.name for op in ops)} at M={M}, {bs_note}",
                "bytes_per_call": nbytes}
         for nt, key in ((nthreads, "all_cores"), (1, "one_thread")):
-            calls, el = _time_calls(lambda: run(nt), per)
-            row[key] = {"threads": nt, "ms_per_call": round(el / calls * 1e3, 3),
-                        "GBs": round(nbytes * calls / el / 1e9, 3)}
+            t = timed(lambda: run(nt))
+            row[key] = {"threads": nt, **t, "GBs": round(nbytes / (t["ms_per_call"] * 1e-3) / 1e9, 3)}
         return row
 
     rows = []
     rows.append(decode_set("qwen05b_up", [workloads.QWEN05B_UP], 1, 100, "K=896 N=4864 bs=32 zp"))
     rows.append(decode_set("qwen05b_decode", workloads.QWEN05B_DECODE, 1, 200, "8 projections, bs=32 zp"))
     rows.append(decode_set("7b_decode", workloads.DECODE_7B, 1, 300, "7 projections, bs=32 zp"))
-    for M in (1, 16):
+    for M in workloads.LLAMA7B_SMALLM_M:
         rows.append(decode_set(f"llama7b_smallm_M{M}", workloads.LLAMA7B_SMALLM_OPS, M, 400,
                                "bs=128, no zp"))
-    # prefill: M=2048 on a sample of output columns (the full call is ~10^2 s of CPU work)
-    op = workloads.LLAMA7B_PREFILL_OPS[0]
-    b, s, z = workloads.make_weights(op, 500)
-    a = workloads.make_activations(2048, op.K, 501, kind="rmsnorm")
-    prow = {"workload": "llama7b_prefill_M2048", "sample": f"M=2048 K={op.K}, bs=32 zp, output columns sampled"}
-    for nt, key, cols in ((nthreads, "all_cores", 512), (1, "one_thread", 32)):
-        bc, sc = b[:cols], s.reshape(op.N, -1)[:cols]
-        zc = None if z is None else z[:cols]
-        calls, el = _time_calls(lambda: oracle.matmul_nbits(a, bc, sc, zc, cols, op.K, 4, 32, nthreads=nt), per)
-        fl = 2.0 * 2048 * cols * op.K
-        prow[key] = {"threads": nt, "columns": cols, "ms_per_call": round(el / calls * 1e3, 3),
-                     "GFLOPs": round(fl * calls / el / 1e9, 3)}
-    rows.append(prow)
+    # prefill: a sample of output columns (a full M=2048 call is ~10^2 s of CPU work); the
+    # columns are independent, so GFLOP/s over a sample is the call's rate
+    for i, op in enumerate(workloads.LLAMA7B_PREFILL_OPS):
+        b, s, z = workloads.make_weights(op, 500 + i)
+        for M in (128, 512, 2048):
+            a = workloads.make_activations(M, op.K, 501 + i, kind="rmsnorm")
+            prow = {"workload": f"llama7b_prefill_K{op.K}_N{op.N}_M{M}",
+                    "sample": f"M={M} K={op.K} N={op.N}, bs=32 zp, output columns sampled"}
+            for nt, key in ((nthreads, "all_cores"), (1, "one_thread")):
+                cols = max(8, min(op.N, (128 if nt > 1 else 8) * 2048 // M))
+                bc, sc = b[:cols], s.reshape(op.N, -1)[:cols]
+                zc = None if z is None else z[:cols]
+                t = timed(lambda: oracle.matmul_nbits(a, bc, sc, zc, cols, op.K, 4, 32, nthreads=nt))
+                fl = 2.0 * M * cols * op.K
+                prow[key] = {"threads": nt, "columns": cols, **t,
+                             "GFLOPs": round(fl / (t["ms_per_call"] * 1e-3) / 1e9, 3)}
+            rows.append(prow)
 
     head = next(r for r in rows if r["workload"] == "7b_decode")
     out = {"value": head["all_cores"]["GBs"], "unit": "GB/s", "cores": nthreads, "kind": "port",
@@ -245,8 +259,8 @@ def cpu_baseline(budget_s):
         gate = next(o for o in workloads.DECODE_7B if o.name == "gate")
         b, s, z = workloads.make_weights(gate, 600)
         a = workloads.make_activations(1, gate.K, 601)
-        calls, el = _time_calls(lambda: oracle.ref_qgemm_nbits(a, b, s, z, 1, gate.N, gate.K, 4, 32), per)
-        out["reference_native_gate_GBs"] = round(workloads.algorithmic_bytes(gate, 1) * calls / el / 1e9, 3)
+        med, _, _ = _median_call(lambda: oracle.ref_qgemm_nbits(a, b, s, z, 1, gate.N, gate.K, 4, 32), per)
+        out["reference_native_gate_GBs"] = round(workloads.algorithmic_bytes(gate, 1) / med / 1e9, 3)
     return out
 
 
