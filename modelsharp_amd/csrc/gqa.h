@@ -368,7 +368,8 @@ template <int D>
 __global__ __launch_bounds__(kGqaThreads) void gqa_group_kernel(GqaArgs p, float* __restrict__ ws, int splits)
 {
     constexpr int KP = D + 4;            // padded K row: float4 reads of 16 different rows hit distinct banks
-    constexpr int HPT = kGqaThreads / D; // heads per pass of the P.V loop
+    constexpr int C4 = D / 4;            // P.V: 4-channel groups of a row
+    static_assert(kGqaThreads / C4 >= kGqaGroupMax, "one P.V pass covers every head of the group");
     __shared__ __attribute__((aligned(16))) float qs[kGqaGroupMax * D];
     __shared__ __attribute__((aligned(16))) float ks[kGqaChunk * KP];
     __shared__ __attribute__((aligned(16))) float vs[kGqaChunk * D];
@@ -399,8 +400,12 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_group_kernel(GqaArgs p, float
     // The new rows [past, past + Skv) of this kv head: the first workgroup of each (batch, kv
     // head) writes them to the present cache (K rotated as gqa_append_kernel does); a chunk
     // that holds one of them builds it from the input row itself, so no workgroup reads a
-    // cache row another one writes.
-    if (qi == 0 && sp == 0) {
+    // cache row another one writes. Up to kGqaGroupMax rows (every decode step) their loads
+    // go out with the query rows' below and the stores follow once those have landed, so
+    // the writing workgroup pays no round trip of its own; more rows take this loop first.
+    const bool nwrite = qi == 0 && sp == 0 && p.Skv > 0;
+    const bool nfast = p.Skv <= kGqaGroupMax;
+    if (nwrite && !nfast) {
         for (int i = tid; i < p.Skv * D; i += kGqaThreads) {
             const int sr = i / D, d = i - sr * D;
             const float* krow = p.k + (int64_t)(b * p.Skv + sr) * p.kv_stride + g * D;
@@ -410,14 +415,12 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_group_kernel(GqaArgs p, float
         }
     }
 
-    // score phase: thread (h = tid / 32, j = tid % 32); P.V phase: thread (d = tid % D, heads
-    // tid / D, tid / D + HPT, ...)
+    // score phase: thread (h = tid / 32, j = tid % 32); P.V phase: thread (head vh = tid / C4,
+    // channels 4 vc .. 4 vc + 3 with vc = tid % C4), one 16-byte read of V per key
     const int sh = tid >> 5, sj = tid & 31;
     float m_run = -__builtin_inff(), l_run = 0.0f;   // per head, held by the 32 lanes of head sh
-    const int dd = tid % D, h0 = tid / D;
-    float acc[kGqaGroupMax / HPT];
-#pragma unroll
-    for (int i = 0; i < kGqaGroupMax / HPT; ++i) acc[i] = 0.0f;
+    const int vc = tid % C4, vh = tid / C4;
+    float4 acc = float4{0.0f, 0.0f, 0.0f, 0.0f};
 
     // The group's query rows: their loads go first (with the cos / sin entries of their
     // rotation), the first chunk's key and value loads after them, and the rotation is
@@ -457,6 +460,42 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_group_kernel(GqaArgs p, float
         qc[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rcs, valid ? cs : kOOB, 0, 0));
         qn[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsn, valid ? cs : kOOB, 0, 0));
     }
+    // The new K and V rows (nwrite && nfast: Skv * D <= QPT * kGqaThreads elements), loaded
+    // the same way: element i = tid + t * kGqaThreads is channel d of new row sr, rotated at
+    // position past + sr.
+    const bool nload = nwrite && nfast;
+    const int64_t nbase = (int64_t)b * p.Skv * p.kv_stride + g * D;
+    const int nbytes = nload ? ((p.Skv - 1) * p.kv_stride + D) * 4 : 0;
+    const __amdgpu_buffer_rsrc_t rnk = buffer_rsrc(p.k + nbase, nbytes), rnv = buffer_rsrc(p.v + nbase, nbytes);
+    float na[QPT], nb[QPT], nc[QPT], nn[QPT], nv[QPT];
+    bool nrot[QPT], nfirst[QPT];
+#pragma unroll
+    for (int t = 0; t < QPT; ++t) {
+        const int i = tid + t * kGqaThreads;
+        const int sr = i / D, d = i - sr * D;
+        const bool valid = nload && i < p.Skv * D, rotating = p.do_rotary && d < rot;
+        int j = d, i0 = d, i1 = d;
+        if (rotating) {
+            if (p.interleaved) {
+                j = d >> 1;
+                i0 = 2 * j;
+                i1 = i0 + 1;
+            } else {
+                j = d < p.rot_half ? d : d - p.rot_half;
+                i0 = j;
+                i1 = j + p.rot_half;
+            }
+        }
+        nrot[t] = rotating;
+        nfirst[t] = d == i0;
+        const int row = sr * p.kv_stride;
+        const int cs = rotating ? (rotary_pos(p.past + sr, p) * p.half + j) * 4 : kOOB;
+        na[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rnk, valid ? (row + i0) * 4 : kOOB, 0, 0));
+        nb[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rnk, valid && rotating ? (row + i1) * 4 : kOOB, 0, 0));
+        nc[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rcs, valid ? cs : kOOB, 0, 0));
+        nn[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsn, valid ? cs : kOOB, 0, 0));
+        nv[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rnv, valid ? (row + d) * 4 : kOOB, 0, 0));
+    }
 
     constexpr int PER = kGqaChunk * (D / 4) / kGqaThreads;   // float4s of K (and of V) per thread
     static_assert(PER * kGqaThreads == kGqaChunk * (D / 4), "chunk shape");
@@ -483,6 +522,18 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_group_kernel(GqaArgs p, float
         const int i = tid + t * kGqaThreads;
         if (i < grp * D)
             qs[i] = !qrot[t] ? qa[t] : qfirst[t] ? qa[t] * qc[t] - qb[t] * qn[t] : qb[t] * qc[t] + qa[t] * qn[t];
+    }
+    // the new rows to the present cache (row past + sr, channel d: offset past * D + i)
+    if (nload) {
+#pragma unroll
+        for (int t = 0; t < QPT; ++t) {
+            const int i = tid + t * kGqaThreads;
+            if (i < p.Skv * D) {
+                kb[(int64_t)p.past * D + i] =
+                    !nrot[t] ? na[t] : nfirst[t] ? na[t] * nc[t] - nb[t] * nn[t] : nb[t] * nc[t] + na[t] * nn[t];
+                vb[(int64_t)p.past * D + i] = nv[t];
+            }
+        }
     }
     for (int c0 = j0; c0 < j1; c0 += kGqaChunk) {
         const int n = min(kGqaChunk, j1 - c0);
@@ -547,15 +598,20 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_group_kernel(GqaArgs p, float
             if (sj == 0) alpha[sh] = a;
         }
         __syncthreads();
-#pragma unroll
-        for (int i = 0; i < kGqaGroupMax / HPT; ++i) {
-            const int h = h0 + i * HPT;
-            if (h < grp) {
-                float o = acc[i] * alpha[h];
-                const float* ph = ps + h * kGqaChunk;
-                for (int j = 0; j < n; ++j) o = __builtin_fmaf(ph[j], vs[j * D + dd], o);
-                acc[i] = o;
+        if (vh < grp) {
+            // per channel: o = acc * alpha, then o = fma(p_j, v_j, o) in key order
+            const float a = alpha[vh];
+            float4 o = float4{acc.x * a, acc.y * a, acc.z * a, acc.w * a};
+            const float* ph = ps + vh * kGqaChunk;
+            for (int j = 0; j < n; ++j) {
+                const float pj = ph[j];
+                const float4 v = *reinterpret_cast<const float4*>(vs + j * D + 4 * vc);
+                o.x = __builtin_fmaf(pj, v.x, o.x);
+                o.y = __builtin_fmaf(pj, v.y, o.y);
+                o.z = __builtin_fmaf(pj, v.z, o.z);
+                o.w = __builtin_fmaf(pj, v.w, o.w);
             }
+            acc = o;
         }
     }
     // the per-head (max, sum) live in the score lanes: hand them to the P.V threads via LDS
@@ -565,22 +621,26 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_group_kernel(GqaArgs p, float
         ps[sh * kGqaChunk + 1] = l_run;
     }
     __syncthreads();
-#pragma unroll
-    for (int i = 0; i < kGqaGroupMax / HPT; ++i) {
-        const int h = h0 + i * HPT;
-        if (h < grp) {
-            const int hh = g * grp + h;
-            const int64_t unit = ((int64_t)b * p.H + hh) * p.Sq + qi;
-            const float mh = ps[h * kGqaChunk], lh = ps[h * kGqaChunk + 1];
-            if (splits == 1) {
-                p.out[(int64_t)(b * p.Sq + qi) * p.H * D + hh * D + dd] = lh > 0.0f ? acc[i] * (1.0f / lh) : 0.0f;
-            } else {
-                float* w = ws + (unit * splits + sp) * (D + 2);
-                w[dd] = acc[i];
-                if (dd == 0) {
-                    w[D] = mh;
-                    w[D + 1] = lh;
-                }
+    if (vh < grp) {
+        const int hh = g * grp + vh;
+        const int64_t unit = ((int64_t)b * p.H + hh) * p.Sq + qi;
+        const float mh = ps[vh * kGqaChunk], lh = ps[vh * kGqaChunk + 1];
+        if (splits == 1) {
+            const float r = lh > 0.0f ? 1.0f / lh : 0.0f;
+            float* o = p.out + (int64_t)(b * p.Sq + qi) * p.H * D + hh * D + 4 * vc;
+            o[0] = lh > 0.0f ? acc.x * r : 0.0f;
+            o[1] = lh > 0.0f ? acc.y * r : 0.0f;
+            o[2] = lh > 0.0f ? acc.z * r : 0.0f;
+            o[3] = lh > 0.0f ? acc.w * r : 0.0f;
+        } else {
+            float* w = ws + (unit * splits + sp) * (D + 2);
+            w[4 * vc] = acc.x;
+            w[4 * vc + 1] = acc.y;
+            w[4 * vc + 2] = acc.z;
+            w[4 * vc + 3] = acc.w;
+            if (vc == 0) {
+                w[D] = mh;
+                w[D + 1] = lh;
             }
         }
     }
