@@ -649,8 +649,11 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_group_kernel(GqaArgs p, float
 // The splits of gqa_group_kernel meet here: one wave per (unit, 64 channels). Each lane
 // issues the loads of its channel over every split and of split `lane`'s maximum and sum
 // together (one round trip to memory: the workspace was written by workgroups on other
-// XCDs); the maximum, the rescale factors and the normaliser come from wave reductions;
-// then each lane adds its channel over the splits in split order (deterministic).
+// XCDs); the maximum and the normaliser come from DPP reductions, and each lane then adds
+// its channel over the splits in split order (deterministic), split s's rescale factor
+// read from lane s with v_readlane. Splits past `splits` load zeros (value and factor), so
+// the sum runs over all kGqaMaxSplits without a branch: a ds_bpermute per split, each
+// behind a branch and its own wait, had made the merge a chain of 64 LDS round trips.
 __global__ __launch_bounds__(64) void gqa_merge_kernel(GqaArgs p, const float* __restrict__ ws, int splits)
 {
     const int D = p.D, slices = (D + 63) / 64;
@@ -671,20 +674,16 @@ __global__ __launch_bounds__(64) void gqa_merge_kernel(GqaArgs p, const float* _
                                    : -__builtin_inff();
     const float ll = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                                    rw, lane < splits ? (lane * (D + 2) + D + 1) * 4 : kOOB, 0, 0));
-    float M = ll > 0.0f ? ml : -__builtin_inff();
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
-    const float f = ll > 0.0f ? expf(ml - M) : 0.0f;
-    float lsum = ll * f;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o);
+    static_assert(kGqaMaxSplits == kWave, "split s's maximum and sum sit in lane s");
+    const float mr = row16_max_all(ll > 0.0f ? ml : -__builtin_inff());
+    const float M = fmaxf(fmaxf(lane_value(mr, 0), lane_value(mr, 16)), fmaxf(lane_value(mr, 32), lane_value(mr, 48)));
+    const float f = ll > 0.0f ? expf(ml - M) : 0.0f;   // 0 for splits past `splits` (ll loads 0)
+    const float lsum = lane_value(group_sum_to_last<64>(ll * f), 63);
     const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-    if (!dv) return;
-    float o = 0.0f;
+    float o = 0.0f;   // every lane runs the sum (lane s must be active when its factor is read)
 #pragma unroll
-    for (int s = 0; s < kGqaMaxSplits; ++s)
-        if (s < splits) o = __builtin_fmaf(vals[s], __shfl(f, s), o);
-    p.out[(int64_t)(u.b * p.Sq + u.qi) * p.H * D + u.h * D + d] = o * inv;
+    for (int s = 0; s < kGqaMaxSplits; ++s) o = __builtin_fmaf(vals[s], lane_value(f, s), o);
+    if (dv) p.out[(int64_t)(u.b * p.Sq + u.qi) * p.H * D + u.h * D + d] = o * inv;
 }
 
 // Prefill (more than 8 queries), head_dim D in {64, 128}: flash attention on the fp32 matrix

@@ -127,6 +127,11 @@ __device__ __forceinline__ float dpp_read(float x)
 {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
 }
+// x of lane l (a wave-uniform index), in every lane: v_readlane into a scalar register.
+__device__ __forceinline__ float lane_value(float x, int l)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+}
 __device__ __forceinline__ float row16_max_all(float x)
 {
     x = fmaxf(x, dpp_read<0xB1>(x));    // quad_perm [1,0,3,2]
