@@ -583,15 +583,11 @@ __global__ __launch_bounds__(kGqaThreads) void gqa_group_kernel(GqaArgs p, float
                 }
                 sc = ((d0 + d1) + (d2 + d3)) * p.scale;
             }
-            float cm = sc;
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) cm = fmaxf(cm, __shfl_xor(cm, o, 32));
+            const float cm = half_max_all(sc);   // the 32 score lanes of head sh
             const float m_new = fmaxf(m_run, cm);   // finite: the chunk holds at least one key
             const float a = expf(m_run - m_new);    // 0 on the first chunk
             const float e = sj < n ? expf(sc - m_new) : 0.0f;
-            float cs = e;
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) cs += __shfl_xor(cs, o, 32);
+            const float cs = half_sum_all(e);
             l_run = l_run * a + cs;
             m_run = m_new;
             ps[sh * kGqaChunk + sj] = e;

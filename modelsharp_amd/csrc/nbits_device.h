@@ -141,6 +141,19 @@ __device__ __forceinline__ float row16_max_all(float x)
     return x;
 }
 
+// Maximum of x over each aligned 32-lane half of the wave, in every lane of the half:
+// row16_max_all, then the other row of the half by v_permlane16_swap (with x on both
+// sides, the first result holds rows 0 and 2 in rows 1 and 3, the second rows 1 and 3 in
+// rows 0 and 2).
+__device__ __forceinline__ float half_max_all(float x)
+{
+    x = row16_max_all(x);
+    const int xi = __builtin_bit_cast(int, x);
+    const auto sw = __builtin_amdgcn_permlane16_swap(xi, xi, false, false);
+    const int other = ((threadIdx.x >> 4) & 1) ? sw[0] : sw[1];
+    return fmaxf(x, __builtin_bit_cast(float, other));
+}
+
 // Sum of x over each aligned group of G lanes (G = 16, 32 or 64), left in the group's last
 // lane (the other lanes hold partial sums): an inclusive scan inside each 16-lane row
 // (row_shr 1, 2, 4, 8), then row_bcast:15 into rows 1 and 3 and row_bcast:31 into rows 2
@@ -157,6 +170,15 @@ __device__ __forceinline__ float group_sum_to_last(float x)
     if constexpr (G >= 32) x = dpp_add<0x142, 0xA>(x);   // row_bcast:15 -> rows 1, 3
     if constexpr (G == 64) x = dpp_add<0x143, 0xC>(x);   // row_bcast:31 -> rows 2, 3
     return x;
+}
+
+// Sum of x over each aligned 32-lane half of the wave, in every lane of the half (fixed
+// order: the scan of group_sum_to_last, then the halves' last lanes read back).
+__device__ __forceinline__ float half_sum_all(float x)
+{
+    x = group_sum_to_last<32>(x);
+    const float lo = lane_value(x, 31), hi = lane_value(x, 63);
+    return (threadIdx.x & 32) ? hi : lo;
 }
 
 // Cross-workgroup hand-off through data written and read with agent-scope atomic
