@@ -808,8 +808,8 @@ __global__ __launch_bounds__(256, 2) void gqa_flash_kernel(GqaArgs p)
                 st[kt][i] = sc;
                 cm = fmaxf(cm, sc);
             }
-        cm = fmaxf(cm, __shfl_xor(cm, 16));
-        cm = fmaxf(cm, __shfl_xor(cm, 32));
+        cm = fmaxf(cm, xor16_value(cm));   // the query's 4 lanes (rows c) of the wave
+        cm = fmaxf(cm, xor32_value(cm));
         const float m_new = fmaxf(m_run, cm);
         const bool none = m_new == -__builtin_inff();   // no key of this query so far
         const float alpha = none ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
@@ -822,8 +822,8 @@ __global__ __launch_bounds__(256, 2) void gqa_flash_kernel(GqaArgs p)
                 st[kt][i] = e;
                 ls = ls + e;
             }
-        ls = ls + __shfl_xor(ls, 16);
-        ls = ls + __shfl_xor(ls, 32);
+        ls = ls + xor16_value(ls);
+        ls = ls + xor32_value(ls);
         l_run = l_run * alpha + ls;
         m_run = m_new;
         // rescale O rows (queries 4c + i of the wave) by their alpha

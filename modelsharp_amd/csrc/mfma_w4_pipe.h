@@ -123,8 +123,8 @@ __device__ __forceinline__ int row_exponent(float mx)
 __device__ __forceinline__ float block256_max(float x, float* red4)
 {
     x = row16_max_all(x);
-    x = fmaxf(x, __shfl_xor(x, 16));
-    x = fmaxf(x, __shfl_xor(x, 32));
+    x = fmaxf(x, xor16_value(x));
+    x = fmaxf(x, xor32_value(x));
     const int wave = threadIdx.x / kWave;
     if ((threadIdx.x & (kWave - 1)) == 0) red4[wave] = x;
     __syncthreads();
@@ -449,7 +449,7 @@ template <bool B8>
 __global__ __launch_bounds__(256) void mfma_w4_pipe_kernel(PipeParams p)
 {
     using L = PipeLds<B8>;
-    constexpr int BM = kPipeBM, BN = kPipeBN, FM = 4, FN = 4;
+    constexpr int BN = kPipeBN, FM = 4, FN = 4;
     constexpr int A_ST = L::A_ST, CG = L::CG, SG = L::SG, ZG = L::ZG;
     constexpr int OFF_A = L::OFF_A, OFF_C = L::OFF_C, OFF_S = L::OFF_S, OFF_Z = L::OFF_Z, OFF_B = L::OFF_B,
                   OFF_E = L::OFF_E;

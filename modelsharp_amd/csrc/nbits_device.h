@@ -141,17 +141,29 @@ __device__ __forceinline__ float row16_max_all(float x)
     return x;
 }
 
-// Maximum of x over each aligned 32-lane half of the wave, in every lane of the half:
-// row16_max_all, then the other row of the half by v_permlane16_swap (with x on both
-// sides, the first result holds rows 0 and 2 in rows 1 and 3, the second rows 1 and 3 in
-// rows 0 and 2).
+// x of lane l ^ 16 (the same position in the other 16-lane row of the half) by
+// v_permlane16_swap: with x on both sides, the first result holds rows 0 and 2 in rows 1
+// and 3, the second rows 1 and 3 in rows 0 and 2. A VALU op, where ds_bpermute is an LDS
+// round trip.
+__device__ __forceinline__ float xor16_value(float x)
+{
+    const int xi = __builtin_bit_cast(int, x);
+    const auto sw = __builtin_amdgcn_permlane16_swap(xi, xi, false, false);
+    return __builtin_bit_cast(float, (threadIdx.x & 16) ? sw[0] : sw[1]);
+}
+// x of lane l ^ 32 (the other half of the wave) by v_permlane32_swap: the first result
+// holds the lower half in the upper, the second the upper half in the lower.
+__device__ __forceinline__ float xor32_value(float x)
+{
+    const int xi = __builtin_bit_cast(int, x);
+    const auto sw = __builtin_amdgcn_permlane32_swap(xi, xi, false, false);
+    return __builtin_bit_cast(float, (threadIdx.x & 32) ? sw[0] : sw[1]);
+}
+// Maximum of x over each aligned 32-lane half of the wave, in every lane of the half.
 __device__ __forceinline__ float half_max_all(float x)
 {
     x = row16_max_all(x);
-    const int xi = __builtin_bit_cast(int, x);
-    const auto sw = __builtin_amdgcn_permlane16_swap(xi, xi, false, false);
-    const int other = ((threadIdx.x >> 4) & 1) ? sw[0] : sw[1];
-    return fmaxf(x, __builtin_bit_cast(float, other));
+    return fmaxf(x, xor16_value(x));
 }
 
 // Sum of x over each aligned group of G lanes (G = 16, 32 or 64), left in the group's last
