@@ -1,7 +1,7 @@
 """CPU oracle of the MatMulNBits operator — TEST INFRASTRUCTURE.
 
 Loaded only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
-leg, as the checker or as the timed CPU baseline; the product never imports
+leg, to check the device's results or as the timed CPU baseline; the product never imports
 it. liboracle_nbits.so is the C restatement of the reference's managed kernel
 and of its native W4A8 kernel (ms_nbits_oracle.c, citations there);
 _ref/libms_ref_qgemm.so and _ref/libms_ref_w4a8.so, when present, are the

@@ -2,8 +2,8 @@
  * ms_nbits_oracle.h — CPU oracle for the MatMulNBits operator.
  *
  * TEST INFRASTRUCTURE. Only tests/, __graft_entry__.smoke() and bench.py's
- * cpu_baseline leg load this library, and only as the checker or as the timed
- * CPU baseline. The product library (modelsharp_amd/csrc) never links it.
+ * cpu_baseline leg load this library, and only to check the device's results or
+ * as the timed CPU baseline. The product library (modelsharp_amd/csrc) never links it.
  *
  * Every function restates one piece of the reference's managed kernel; the
  * file:line citation is on each declaration (paths are relative to the

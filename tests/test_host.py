@@ -134,7 +134,7 @@ def test_context_semantics():
 
 def test_workload_costs_match_published_table():
     from modelsharp_amd import workloads as W
-    # BASELINE table rows (bytes, flops)
+    # the workload table's rows (algorithmic bytes, flops)
     assert W.algorithmic_bytes(W.QWEN05B_UP, 1) == 2_814_976
     assert W.flops(W.QWEN05B_UP, 1) == 8_716_288
     gate = next(o for o in W.DECODE_7B if o.name == "gate")
