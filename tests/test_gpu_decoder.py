@@ -354,6 +354,8 @@ GROUPED_CASES = [
     dict(seed=107, B=1, Sq=3, H=6, KH=2, D=128, past=33, cos_cols=24),               # partial rotary span
     dict(seed=108, B=1, Sq=2, H=2, KH=2, D=64, past=90, cos_rows=64),                # positions past the cache
     dict(seed=109, B=1, Sq=1, H=14, KH=2, D=128, past=5000, rotary=False, cos_rows=8),
+    dict(seed=110, B=1, Sq=2, H=8, KH=2, D=128, past=40, kv_seq=12, cos_rows=64),   # more than 8 new rows
+    dict(seed=111, B=2, Sq=4, H=4, KH=2, D=64, past=30, kv_seq=2, cos_rows=64),     # fewer new rows than queries
 ]
 
 
@@ -377,6 +379,7 @@ FLASH_CASES = [
     dict(seed=207, B=1, Sq=65, H=6, KH=2, D=128, past=0, cos_cols=24, cos_rows=80),  # partial rotary span
     dict(seed=208, B=1, Sq=20, H=2, KH=2, D=64, past=90, cos_rows=64),               # positions past the cache
     dict(seed=209, B=1, Sq=129, H=14, KH=2, D=128, past=700, rotary=False, cos_rows=8),
+    dict(seed=210, B=1, Sq=20, H=4, KH=2, D=64, past=10, kv_seq=28, cos_rows=64),    # more new keys than queries
 ]
 
 

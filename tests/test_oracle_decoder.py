@@ -137,10 +137,13 @@ def gqa_f64(d, q, k, v, pk, pv, seqlens, cos, sin):
 
 
 def make_case(seed, B, Sq, H, KH, D, past, packed=False, rotary=True, interleaved=False, window=-1, seqlens=None,
-              cos_rows=64, cos_cols=None):
+              cos_rows=64, cos_cols=None, kv_seq=None):
+    # kv_seq: new key/value rows, Sq unless given (the reference takes key.Shape[1],
+    # GroupQueryAttentionKernel.cs:131; packed QKV shares the query length, :104)
+    Skv = Sq if kv_seq is None else kv_seq
     r = rng(seed)
-    d = oracle.GqaDesc(batch=B, q_seq=Sq, kv_seq=Sq, num_heads=H, kv_num_heads=KH, head_dim=D,
-                       packed_qkv=int(packed), past_seq=past, past_in_present=0, present_capacity=past + Sq,
+    d = oracle.GqaDesc(batch=B, q_seq=Sq, kv_seq=Skv, num_heads=H, kv_num_heads=KH, head_dim=D,
+                       packed_qkv=int(packed), past_seq=past, past_in_present=0, present_capacity=past + Skv,
                        do_rotary=int(rotary), rotary_interleaved=int(interleaved), cos_rows=cos_rows,
                        cos_cols=cos_cols if cos_cols is not None else D // 2, local_window_size=window, scale=0.0,
                        seqlens_len=0 if seqlens is None else len(seqlens))
@@ -149,8 +152,8 @@ def make_case(seed, B, Sq, H, KH, D, past, packed=False, rotary=True, interleave
         k = v = None
     else:
         q = r.standard_normal((B, Sq, H * D)).astype(np.float32)
-        k = r.standard_normal((B, Sq, KH * D)).astype(np.float32)
-        v = r.standard_normal((B, Sq, KH * D)).astype(np.float32)
+        k = r.standard_normal((B, Skv, KH * D)).astype(np.float32)
+        v = r.standard_normal((B, Skv, KH * D)).astype(np.float32)
     pk = r.standard_normal((B, KH, past, D)).astype(np.float32) if past else None
     pv = r.standard_normal((B, KH, past, D)).astype(np.float32) if past else None
     ang = np.outer(np.arange(cos_rows), 1.0 / 10000 ** (np.arange(d.cos_cols) / d.cos_cols))
@@ -169,6 +172,8 @@ GQA_CASES = [
     dict(seed=7, B=1, Sq=3, H=2, KH=1, D=20, past=2, cos_cols=6),                # partial rotary span
     dict(seed=8, B=1, Sq=2, H=2, KH=2, D=8, past=70, cos_rows=64),               # position past the cache
     dict(seed=9, B=1, Sq=3, H=4, KH=2, D=16, past=4, rotary=False),
+    dict(seed=10, B=1, Sq=2, H=4, KH=2, D=16, past=5, kv_seq=6),                 # more new keys than queries
+    dict(seed=12, B=2, Sq=4, H=4, KH=2, D=16, past=3, kv_seq=2),                 # fewer new keys than queries
 ]
 
 
